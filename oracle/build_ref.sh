@@ -1,0 +1,29 @@
+#!/bin/sh
+# Builds the reference's myl7/fss v0.7.1 DCF (vendored in the reference tree
+# at third_party/myl7_fss, source files used unmodified and in place) into
+# oracle/_ref/, one library per output group, plus oracle/ref_shim.cpp.
+# Compile definitions follow the reference's myl7_core target
+# (CMakeLists.txt:84-93): kBlocks=8, kLambda=16, OpenSSL libcrypto, OpenMP.
+# Outputs go only to oracle/_ref/ (git-ignored).  Without the reference tree
+# this script does nothing and exits 0.
+set -eu
+HERE=$(cd "$(dirname "$0")" && pwd)
+REF=${SUF_REFERENCE_ROOT:-/root/reference}
+M="$REF/third_party/myl7_fss"
+if [ ! -f "$M/src/dcf.c" ]; then
+  echo "build_ref: reference tree not found at $REF; nothing built"
+  exit 0
+fi
+OUT="$HERE/_ref"
+mkdir -p "$OUT/obj"
+CFLAGS="-O2 -fPIC -fopenmp -DkBlocks=8 -DkLambda=16 -I$M/include"
+gcc $CFLAGS -c "$M/src/dcf.c" -o "$OUT/obj/dcf.o"
+gcc $CFLAGS -c "$M/src/prg/aes128_mmo.c" -o "$OUT/obj/aes128_mmo.o"
+g++ -std=c++17 -fno-gnu-unique $CFLAGS -I"$REF/include" -c "$HERE/ref_shim.cpp" -o "$OUT/obj/ref_shim.o"
+for grp in bytes u128_le; do
+  gcc $CFLAGS -c "$M/src/group/$grp.c" -o "$OUT/obj/group_$grp.o"
+  g++ -shared -fopenmp -Wl,-Bsymbolic -o "$OUT/libmyl7ref_$grp.so.tmp" "$OUT/obj/dcf.o" "$OUT/obj/aes128_mmo.o" \
+    "$OUT/obj/group_$grp.o" "$OUT/obj/ref_shim.o" -lcrypto
+  mv "$OUT/libmyl7ref_$grp.so.tmp" "$OUT/libmyl7ref_$grp.so"
+done
+echo "build_ref: built $OUT/libmyl7ref_bytes.so $OUT/libmyl7ref_u128_le.so"

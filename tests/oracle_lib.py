@@ -1,0 +1,216 @@
+"""ctypes bindings for the CPU oracle (oracle/_build/liboracle.so) and, when it
+was built, the reference's own myl7 DCF (oracle/_ref/libmyl7ref_*.so).
+
+Test infrastructure only: the product package never imports this module.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+ORACLE_SO = os.path.join(ORACLE_DIR, "_build", "liboracle.so")
+REF_DIR = os.path.join(ORACLE_DIR, "_ref")
+
+u8p = ctypes.POINTER(ctypes.c_uint8)
+u64p = ctypes.POINTER(ctypes.c_uint64)
+i32p = ctypes.POINTER(ctypes.c_int)
+c_sz = ctypes.c_size_t
+
+GROUP_XOR = 0
+GROUP_ADD = 1
+PRG_STATE_BYTES = 128  # kBlocks (8) x lambda (16)
+
+
+def ptr(a, t=u8p):
+    if a is None:
+        return None
+    return a.ctypes.data_as(t)
+
+
+def _load_oracle():
+    if not os.path.exists(ORACLE_SO):
+        subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
+    lib = ctypes.CDLL(ORACLE_SO)
+    lib.orc_myl7_key_bytes.restype = c_sz
+    lib.orc_packed_key_bytes.restype = c_sz
+    lib.orc_lut_key_bytes.restype = c_sz
+    lib.orc_mt64_next.restype = ctypes.c_uint64
+    lib.orc_beaver_scale.restype = ctypes.c_uint64
+    lib.orc_beaver_scale.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int64, ctypes.c_int]
+    lib.orc_myl7_gen.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_uint64,
+                                 u8p, ctypes.c_int, u8p, u8p, u8p]
+    lib.orc_myl7_eval.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, u8p,
+                                  ctypes.c_uint64, u8p]
+    lib.orc_myl7_eval_many_bit.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, c_sz,
+                                           u8p, u64p, c_sz, u8p, ctypes.c_int]
+    lib.orc_seed_from_id.argtypes = [ctypes.c_uint64, ctypes.c_uint64, u8p]
+    lib.orc_mt64_fill.argtypes = [ctypes.c_uint64, u64p, c_sz]
+    lib.orc_aes128_ctr.argtypes = [u8p, ctypes.c_uint64, ctypes.c_uint64, c_sz, u8p]
+    lib.orc_packed_build_key.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_int, u64p,
+                                         ctypes.c_int, u8p, u8p]
+    lib.orc_packed_eval.argtypes = [u8p, c_sz, ctypes.c_int, u64p, c_sz, u64p]
+    lib.orc_lut_build_key.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
+                                      u64p, ctypes.c_int, u64p, u8p, u8p]
+    lib.orc_lut_eval.argtypes = [u8p, c_sz, ctypes.c_int, u64p, c_sz, u64p]
+    lib.orc_trunc_postproc.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64,
+                                       ctypes.c_uint64, u64p, u64p, c_sz, ctypes.c_int, u64p,
+                                       c_sz, ctypes.c_int, ctypes.c_int, ctypes.c_int, u64p, c_sz]
+    lib.orc_beaver_matmul.argtypes = [ctypes.c_int, u64p, u64p, u64p, u64p, u64p, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int64, ctypes.c_int, u64p,
+                                      ctypes.c_int]
+    lib.orc_add_rout_aos.argtypes = [u64p, c_sz, ctypes.c_int, u64p, ctypes.c_int]
+    return lib
+
+
+LIB = _load_oracle()
+
+
+class Prg:
+    """myl7 PRG state: eight AES-128 keys taken from a 128-byte state."""
+
+    def __init__(self, state: bytes):
+        assert len(state) == PRG_STATE_BYTES
+        self.state = bytes(state)
+        self.buf = ctypes.create_string_buffer(8 * 176)
+        st = np.frombuffer(self.state, dtype=np.uint8).copy()
+        LIB.orc_prg_init(self.buf, ptr(st), PRG_STATE_BYTES)
+
+
+def mt64(seed, n):
+    out = np.empty(n, dtype=np.uint64)
+    LIB.orc_mt64_fill(seed, ptr(out, u64p), n)
+    return out
+
+
+def mt64_bytes(seed, n):
+    """n bytes, each the low byte of one mt19937_64 output."""
+    return (mt64(seed, n) & np.uint64(0xFF)).astype(np.uint8)
+
+
+def aes_expand(key: bytes) -> np.ndarray:
+    rk = np.zeros(176, dtype=np.uint8)
+    k = np.frombuffer(bytes(key), dtype=np.uint8).copy()
+    LIB.orc_aes128_expand(ptr(k), ptr(rk))
+    return rk
+
+
+def aes_encrypt(key: bytes, block: bytes) -> bytes:
+    rk = aes_expand(key)
+    b = np.frombuffer(bytes(block), dtype=np.uint8).copy()
+    out = np.zeros(16, dtype=np.uint8)
+    LIB.orc_aes128_encrypt(ptr(rk), ptr(b), ptr(out))
+    return out.tobytes()
+
+
+def myl7_key_bytes(in_bits, payload_len):
+    return LIB.orc_myl7_key_bytes(in_bits, payload_len)
+
+
+def myl7_gen(prg, group, in_bits, alpha, payload: bytes, seeds: np.ndarray):
+    kb = myl7_key_bytes(in_bits, len(payload))
+    k0 = np.zeros(kb, dtype=np.uint8)
+    k1 = np.zeros(kb, dtype=np.uint8)
+    p = np.frombuffer(bytes(payload), dtype=np.uint8).copy()
+    rc = LIB.orc_myl7_gen(prg.buf, group, in_bits, int(alpha) & (2**64 - 1), ptr(p), len(payload),
+                          ptr(np.ascontiguousarray(seeds, dtype=np.uint8)), ptr(k0), ptr(k1))
+    assert rc == 0
+    return k0, k1
+
+
+def myl7_gen_batch(prg, group, in_bits, alphas, payload: bytes, seeds: np.ndarray):
+    """seeds: [n][chunks*32] bytes. Returns (keys0 [n][kb], keys1 [n][kb])."""
+    n = len(alphas)
+    kb = myl7_key_bytes(in_bits, len(payload))
+    k0 = np.zeros((n, kb), dtype=np.uint8)
+    k1 = np.zeros((n, kb), dtype=np.uint8)
+    for i in range(n):
+        a, b = myl7_gen(prg, group, in_bits, int(alphas[i]), payload, seeds[i])
+        k0[i] = a
+        k1[i] = b
+    return k0, k1
+
+
+def myl7_eval(prg, group, in_bits, key: np.ndarray, x, payload_len):
+    out = np.zeros(max(payload_len, 1), dtype=np.uint8)
+    rc = LIB.orc_myl7_eval(prg.buf, group, in_bits, ptr(np.ascontiguousarray(key)),
+                           int(x) & (2**64 - 1), ptr(out))
+    assert rc == 0
+    return out[:payload_len]
+
+
+def myl7_eval_many_bit(prg, group, in_bits, keys: np.ndarray, xs: np.ndarray, threads=1):
+    n = xs.shape[0]
+    out = np.zeros(n, dtype=np.uint8)
+    keys = np.ascontiguousarray(keys)
+    rc = LIB.orc_myl7_eval_many_bit(prg.buf, group, in_bits, keys.shape[1], ptr(keys),
+                                    ptr(np.ascontiguousarray(xs, dtype=np.uint64), u64p), n,
+                                    ptr(out), threads)
+    assert rc == 0
+    return out
+
+
+def seed_from_id(i, tweak):
+    s = np.zeros(16, dtype=np.uint8)
+    LIB.orc_seed_from_id(i, tweak, ptr(s))
+    return s
+
+
+def packed_key(party, nonce, in_bits, thr, seed):
+    thr = np.ascontiguousarray(thr, dtype=np.uint64)
+    blob = np.zeros(LIB.orc_packed_key_bytes(len(thr)), dtype=np.uint8)
+    LIB.orc_packed_build_key(party, nonce, in_bits, ptr(thr, u64p), len(thr), ptr(seed), ptr(blob))
+    return blob
+
+
+def packed_eval(keys, key_bytes, broadcast, xs, out_words):
+    xs = np.ascontiguousarray(xs, dtype=np.uint64)
+    out = np.zeros(len(xs) * out_words, dtype=np.uint64)
+    LIB.orc_packed_eval(ptr(np.ascontiguousarray(keys)), key_bytes, int(broadcast),
+                        ptr(xs, u64p), len(xs), ptr(out, u64p))
+    return out.reshape(len(xs), out_words)
+
+
+def lut_key(party, nonce, in_bits, out_words, cuts, payload, seed):
+    cuts = np.ascontiguousarray(cuts, dtype=np.uint64)
+    payload = np.ascontiguousarray(payload, dtype=np.uint64).ravel()
+    intervals = len(cuts) - 1
+    blob = np.zeros(LIB.orc_lut_key_bytes(intervals, out_words), dtype=np.uint8)
+    LIB.orc_lut_build_key(party, nonce, in_bits, out_words, ptr(cuts, u64p), intervals,
+                          ptr(payload, u64p), ptr(seed), ptr(blob))
+    return blob
+
+
+def lut_eval(keys, key_bytes, broadcast, xs, out_words):
+    xs = np.ascontiguousarray(xs, dtype=np.uint64)
+    out = np.zeros(len(xs) * out_words, dtype=np.uint64)
+    LIB.orc_lut_eval(ptr(np.ascontiguousarray(keys)), key_bytes, int(broadcast),
+                     ptr(xs, u64p), len(xs), ptr(out, u64p))
+    return out.reshape(len(xs), out_words)
+
+
+# ---------------- reference build (oracle/_ref) ----------------
+def ref_available(group=GROUP_XOR):
+    return os.path.exists(_ref_path(group))
+
+
+def _ref_path(group):
+    name = "libmyl7ref_bytes.so" if group == GROUP_XOR else "libmyl7ref_u128_le.so"
+    return os.path.join(REF_DIR, name)
+
+
+_REF = {}
+
+
+def ref_lib(group=GROUP_XOR):
+    if group not in _REF:
+        lib = ctypes.CDLL(_ref_path(group), mode=ctypes.RTLD_LOCAL)
+        lib.ref_adapter_eval.argtypes = [ctypes.c_int, u8p, c_sz, ctypes.c_uint64, u8p, c_sz]
+        lib.ref_adapter_eval_many.argtypes = [ctypes.c_int, c_sz, u8p, u64p, c_sz, ctypes.c_int,
+                                              u8p]
+        lib.ref_adapter_gen.argtypes = [ctypes.c_int, ctypes.c_uint64, u8p, c_sz, u8p, u8p, c_sz]
+        _REF[group] = lib
+    return _REF[group]
