@@ -1,0 +1,230 @@
+"""Benchmark: 64-bit DCF evaluations per second, 2 parties, N = 2^20, on one
+MI355X.
+
+Workload (one step): both parties evaluate their N myl7-format DCF keys
+(lambda = 16 bytes, AES-128-MMO PRG, XOR output group, 1-byte payload,
+2152 bytes per key) at the public masked inputs xhat_i = x_i + r_in_i, i.e.
+2N key evaluations whose XOR reconstructs 1[xhat_i < r_in_i].  Keys and
+inputs are resident in HBM before timing starts; keygen runs once on the
+device beforehand and is reported separately.
+
+Synthetic inputs (std::mt19937_64 throughout): r_in = mt(1) words;
+x = round(N(0,1) * 2^12) by Box-Muller on mt(2); PRG state = low bytes of
+mt(3); DCF seeds = bytes of mt(4) words; alpha_i = r_in_i, beta = 0x01.
+
+Prints one JSON line.  --gpus above 1 is refused (single-GPU build).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "64-bit DCF evals/sec (2 parties, N=2^20) + secure layer latency ms, 1 MI355X"
+HBM_PEAK_GBPS = 8000.0
+VALU_PEAK_GOPS = 256 * 64 * 2.4  # 256 CUs x 64 lanes x 2.4 GHz, 32-bit integer ops
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--n", type=int, default=1 << 20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_baseline(keys0, keys1, xhat, gpu_bits0, gpu_bits1, seconds):
+    """The reference's own myl7 batch evaluation (oracle/_ref, built from the
+    reference sources), single thread as in Myl7FssBackend::eval_dcf_many_u64
+    (include/proto/myl7_fss_backend.hpp:73-100), on a bounded sample."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as ol
+
+    state = ol.mt64_bytes(3, 128)
+    chunk = 1024
+    kb = keys0.shape[1]
+    if ol.ref_available():
+        ref = ol.ref_lib(ol.GROUP_XOR)
+        ref.ref_prg_init(ol.ptr(state), 128)
+        kind = "reference"
+
+        def run(keys, xs, out):
+            return ref.ref_adapter_eval_many(64, kb, ol.ptr(keys), ol.ptr(xs, ol.u64p), len(xs),
+                                             1, ol.ptr(out))
+    else:
+        prg = ol.Prg(state.tobytes())
+        kind = "port"
+
+        def run(keys, xs, out):
+            out[:] = ol.myl7_eval_many_bit(prg, 0, 64, keys, xs)
+            return 0
+
+    done = 0
+    mismatches = 0
+    t0 = time.perf_counter()
+    i = 0
+    n = keys0.shape[0]
+    while True:
+        lo = (i * chunk) % n
+        hi = lo + chunk
+        for keys, gb in ((keys0, gpu_bits0), (keys1, gpu_bits1)):
+            out = np.zeros(chunk, dtype=np.uint8)
+            k = np.ascontiguousarray(keys[lo:hi])
+            x = np.ascontiguousarray(xhat[lo:hi])
+            assert run(k, x, out) == 0
+            mismatches += int(np.count_nonzero(out != gb[lo:hi]))
+            done += chunk
+        i += 1
+        if time.perf_counter() - t0 >= seconds or i * chunk >= n:
+            break
+    dt = time.perf_counter() - t0
+    return {
+        "value": done / dt,
+        "unit": "evals/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": "%d DCF evals (%d keys per party, both parties) of the same N=2^20 "
+                  "batch, serial myl7 dcf_eval via OpenSSL EVP AES as the reference "
+                  "batch loop does; shares compared with the GPU: %d mismatches"
+                  % (done, done // 2, mismatches),
+        "mismatches": mismatches,
+    }
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print("bench.py: this build runs on one GPU only (got --gpus %d); "
+              "multi-GPU sharding is described in DESIGN.md, not implemented" % a.gpus)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from suf_amd import native, pfss
+
+    native.call("sufhip_init", 0)
+    n = a.n
+    state = bytes((pfss.host_mt19937_64(3, 128) & np.uint64(0xFF)).astype(np.uint8))
+    r_in = pfss.host_mt19937_64(1, n)
+    x = pfss.host_normal_fixed(2, 1.0, 0.0, 12, n)
+    xhat = (x + r_in).astype(np.uint64)
+    seeds = pfss.host_mt19937_64(4, 4 * n).view(np.uint8).reshape(n, 32)
+
+    def d(arr):
+        arr = np.ascontiguousarray(arr)
+        if arr.dtype == np.uint64:
+            arr = arr.view(np.int64)
+        return torch.from_numpy(arr.copy()).cuda()
+
+    d_alpha, d_xhat, d_seeds = d(r_in), d(xhat), d(seeds)
+    d_beta = d(np.array([1], dtype=np.uint8))
+    kb = pfss.dcf_key_bytes(64, 1)
+
+    # Keygen (dealer), once, on the device.
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    k0, k1 = pfss.dcf_gen(native.GROUP_XOR, 64, state, d_alpha, d_beta, d_seeds)
+    e1.record()
+    torch.cuda.synchronize()
+    keygen_ms = e0.elapsed_time(e1)
+
+    out0 = torch.empty(n, dtype=torch.uint8, device="cuda")
+    out1 = torch.empty(n, dtype=torch.uint8, device="cuda")
+
+    def step(evs=None):
+        if evs is not None:
+            evs[0].record()
+        pfss.dcf_eval(native.GROUP_XOR, 64, 1, state, k0, d_xhat, native.DCF_OUT_BIT, out=out0)
+        if evs is not None:
+            evs[1].record()
+        pfss.dcf_eval(native.GROUP_XOR, 64, 1, state, k1, d_xhat, native.DCF_OUT_BIT, out=out1)
+        if evs is not None:
+            evs[2].record()
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(a.steps)]
+    t_start, t_stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    for s in range(a.steps):
+        step(evs[s])
+    t_stop.record()
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_stop)
+    launch_ms = [e[0].elapsed_time(e[1]) for e in evs] + [e[1].elapsed_time(e[2]) for e in evs]
+    kern_ms = float(np.mean(launch_ms))
+
+    # Reconstruct and check (outside the timed region).
+    rec = (out0 ^ out1).cpu().numpy()
+    ok = bool(np.array_equal(rec, (xhat < r_in).astype(np.uint8)))
+
+    evals = 2 * n * a.steps
+    value = evals / (total_ms / 1e3)
+    key_bytes_per_launch = n * (kb + 8 + 1)
+    achieved_gbps = key_bytes_per_launch / (kern_ms / 1e3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "evals/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": total_ms / a.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {
+            "workload": "dcf_batch: N=2^20 myl7 DCF keys per party over Z_2^64, 2 parties",
+            "N": n, "in_bits": 64, "lambda_bytes": 16, "group": "xor", "payload_bytes": 1,
+            "key_bytes": kb, "out": "1 byte per eval (share byte 0 & 1)",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved_gbps,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": achieved_gbps / HBM_PEAK_GBPS,
+            "traffic": None,
+            "kernel": "dcf_eval_bit_kernel",
+            "kernel_ms": kern_ms,
+            "bytes_per_launch": key_bytes_per_launch,
+            "note": "key bytes streamed per launch / launch time; the kernel is bound by "
+                    "VALU+LDS AES work, see roofline_valu",
+        },
+        "roofline_valu": {
+            "bound": "valu",
+            "aes_blocks_per_launch": n * 64 * 2,
+            "aes_blocks_per_s": n * 64 * 2 / (kern_ms / 1e3),
+            "peak_gops": VALU_PEAK_GOPS,
+        },
+        "keygen_ms": keygen_ms,
+        "secure_layer_ms": None,
+        "check": "ok" if ok else "MISMATCH",
+    }
+    if not a.no_cpu:
+        sample = 1 << 14
+        g0 = out0[:sample].cpu().numpy()
+        g1 = out1[:sample].cpu().numpy()
+        line["cpu_baseline"] = cpu_baseline(k0[:sample].cpu().numpy(), k1[:sample].cpu().numpy(),
+                                            xhat[:sample], g0, g1, a.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    if not ok:
+        sys.exit(1)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,149 @@
+/*
+ * suf_hip.h -- C ABI of libsuf_hip.so, the MI355X (gfx950) PFSS execution
+ * backend for SUF.
+ *
+ * This header replaces the reference's GPU boundary:
+ *   - cuda/pfss_cuda_api.hpp:6-24 (a 4-function C API whose bodies are stubs,
+ *     cuda/pfss_kernels.cu:814-830) -> the sufhip_dcf_* / sufhip_packed_lt_* /
+ *     sufhip_interval_lut_* evaluators below;
+ *   - the device entry points of proto::PfssGpuStagedEval
+ *     (include/proto/backend_gpu.hpp:157-210), whose CUDA bodies live in
+ *     cuda/pfss_backend_gpu.cu:523-1378;
+ *   - the extern "C" launcher set of include/runtime/cuda_primitives.hpp:13-236.
+ *
+ * Conventions (all entry points):
+ *   - Plain pointers and sizes; no HIP or torch types.  `stream` is a
+ *     hipStream_t passed as void* (NULL = the default stream).
+ *   - Pointers named d_* are device pointers; all other pointers are host.
+ *   - Every function returns SUFHIP_OK (0) or a negative status; the message
+ *     of the last failure on the calling thread is sufhip_last_error().
+ *     The reference launchers return void and silently do nothing for n == 0;
+ *     here n == 0 is also a successful no-op.
+ *   - Work is enqueued asynchronously on `stream` unless stated otherwise.
+ *   - Ring arithmetic is over Z_2^64 (unsigned wrap-around).
+ */
+#ifndef SUF_HIP_H
+#define SUF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SUFHIP_OK 0
+#define SUFHIP_ERR_INVALID (-1) /* bad argument: size, null pointer, tag */
+#define SUFHIP_ERR_HIP (-2)     /* HIP runtime error (launch, copy, sync) */
+#define SUFHIP_ERR_NOMEM (-3)   /* device allocation failed */
+
+#define SUFHIP_ABI_VERSION 1
+
+/* DCF output groups (myl7/fss v0.7.1 src/group/): */
+#define SUFHIP_GROUP_XOR 0 /* bytes.c: XOR of 16-byte blocks (the group SUF links) */
+#define SUFHIP_GROUP_ADD 1 /* u128_le.c: addition mod 2^127 of little-endian blocks */
+
+/* DCF output modes for sufhip_dcf_eval: */
+#define SUFHIP_DCF_OUT_BIT 0    /* 1 byte per element: share byte 0 & 1
+                                   (Myl7FssBackend::eval_dcf_many_u64,
+                                   include/proto/myl7_fss_backend.hpp:73-100) */
+#define SUFHIP_DCF_OUT_BYTES 1  /* out_bytes bytes per element: the first
+                                   out_bytes bytes of the payload share
+                                   (PfssBackendBatch::eval_dcf_many_u64 with
+                                   outs_flat [N][out_bytes]) */
+#define SUFHIP_DCF_OUT_PACKED 2 /* one bit per element: bit (i % 64) of u64
+                                   word i / 64 is share byte 0 & 1 of element i */
+
+/* ---------------------------------------------------------------------- */
+/* Library and runtime plumbing (lets C++ host code manage device memory   */
+/* and streams without including HIP headers).                             */
+/* ---------------------------------------------------------------------- */
+int sufhip_abi_version(void);
+const char* sufhip_last_error(void);
+/* Selects the device for the calling thread and loads the kernels. */
+int sufhip_init(int device);
+int sufhip_device_count(int* count);
+int sufhip_stream_create(void** stream);
+int sufhip_stream_destroy(void* stream);
+int sufhip_stream_synchronize(void* stream);
+int sufhip_malloc(void** d_ptr, size_t bytes);
+int sufhip_free(void* d_ptr);
+int sufhip_host_alloc(void** h_ptr, size_t bytes); /* pinned host memory */
+int sufhip_host_free(void* h_ptr);
+int sufhip_memcpy_h2d(void* d_dst, const void* src, size_t bytes, void* stream);
+int sufhip_memcpy_d2h(void* dst, const void* d_src, size_t bytes, void* stream);
+int sufhip_memcpy_d2d(void* d_dst, const void* d_src, size_t bytes, void* stream);
+
+/* Timed region helpers: records an event pair around nothing; the caller
+ * records `start` and `stop` on the stream and reads the elapsed ms. */
+int sufhip_event_create(void** ev);
+int sufhip_event_destroy(void* ev);
+int sufhip_event_record(void* ev, void* stream);
+int sufhip_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* ---------------------------------------------------------------------- */
+/* AES-128 and the myl7 PRG                                                 */
+/* ---------------------------------------------------------------------- */
+/* AES-128-CTR keystream: block i = AES_k(le64(ctr_lo + i) || le64(ctr_hi)).
+ * Replaces the aes128_ctr_kernel launch of src/demo/test_cuda_prg.cpp:93
+ * (kernel cuda/pfss_kernels.cu:169-184).  round_keys: 176 bytes (FIPS-197
+ * key schedule); d_out: [blocks][16]. */
+int sufhip_aes128_ctr(uint8_t* d_out, const uint8_t* round_keys, uint64_t ctr_lo,
+                      uint64_t ctr_hi, size_t blocks, void* stream);
+
+/* myl7 PRG (third_party/myl7_fss/src/prg/aes128_mmo.c:41-52) on n seeds:
+ * d_out[i][16 j .. 16 j + 16) = AES_{K_j}(seed_i) xor seed_i, j < out_blocks
+ * (out_blocks <= 8), K_j = prg_state[16 j .. 16 j + 16). */
+int sufhip_prg_mmo(const uint8_t* prg_state, const uint8_t* d_seeds, size_t n, int out_blocks,
+                   uint8_t* d_out, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* DCF in the myl7 adapter key format                                       */
+/* (include/proto/myl7_fss_backend.hpp:131-213):                            */
+/*   [in_bits u8][num_chunks u8][party u8][0][payload_len u32 LE]           */
+/*   then per 16-byte payload chunk: [seed 16][cw 33 x in_bits][cw_np1 16]  */
+/* Keys are flat [N][key_bytes]; `key_broadcast` = 1 means one key for all  */
+/* N points (PfssGpuStagedEval::*_broadcast, backend_gpu.hpp:166-175).      */
+/* prg_state is the 128-byte myl7 PRG state (prg_init, aes128_mmo.c:16-31). */
+/* ---------------------------------------------------------------------- */
+size_t sufhip_dcf_key_bytes(int in_bits, int payload_len);
+
+/* Dealer: N comparison keys f_i(x) = payload_i * 1[x < alpha_i] on in_bits
+ * bits (myl7 dcf_gen, third_party/myl7_fss/src/dcf.c:42-142, via
+ * Myl7FssBackend::gen_dcf, myl7_fss_backend.hpp:134-213).
+ * d_alpha [N] u64; d_payload [payload_len] (payload_broadcast = 1) or
+ * [N][payload_len]; d_seeds [N][num_chunks][2][16] (party-0 then party-1
+ * seed of each chunk).  Writes d_keys0, d_keys1 [N][key_bytes]. */
+int sufhip_dcf_gen(int group, int in_bits, const uint8_t* prg_state, const uint64_t* d_alpha,
+                   const uint8_t* d_payload, int payload_len, int payload_broadcast,
+                   const uint8_t* d_seeds, size_t n, uint8_t* d_keys0, uint8_t* d_keys1,
+                   void* stream);
+
+/* Evaluator: one party's shares at N points (myl7 dcf_eval, dcf.c:146-193;
+ * Myl7FssBackend::eval_dcf / eval_dcf_many_u64, myl7_fss_backend.hpp:73-100,
+ * 215-256; PfssGpuStagedEval::eval_dcf_many_u64_device[_broadcast],
+ * backend_gpu.hpp:159-175).  The party is read from each key's header.
+ * key_bytes must equal sufhip_dcf_key_bytes(in_bits, payload_len).
+ * out_mode SUFHIP_DCF_OUT_BIT: d_out [N] bytes; SUFHIP_DCF_OUT_BYTES:
+ * d_out [N][out_bytes], 1 <= out_bytes <= payload_len;
+ * SUFHIP_DCF_OUT_PACKED: d_out [ceil(N/64)] u64 words. */
+int sufhip_dcf_eval(int group, int in_bits, int payload_len, const uint8_t* prg_state,
+                    const uint8_t* d_keys, size_t key_bytes, int key_broadcast,
+                    const uint64_t* d_xs, size_t n, int out_mode, int out_bytes, void* d_out,
+                    void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Host-side helpers for seeded synthetic inputs                            */
+/* ---------------------------------------------------------------------- */
+/* out[i] = the i-th output of std::mt19937_64(seed). */
+int sufhip_host_mt19937_64(uint64_t seed, uint64_t* out, size_t n);
+/* out[i] = llround(clip(sigma * z_i, -clip, clip) * 2^frac_bits) as a
+ * two's-complement u64, z_i standard normal by Box-Muller on
+ * std::mt19937_64(seed) words (clip <= 0 disables clipping). */
+int sufhip_host_normal_fixed(uint64_t seed, double sigma, double clip, int frac_bits,
+                             uint64_t* out, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SUF_HIP_H */

@@ -1,0 +1,235 @@
+// AES-128 encryption for CDNA4 with the round table resident in LDS.
+//
+// State words are little-endian 32-bit columns (word c = bytes 4c..4c+3 of
+// the block), so blocks, keys and round keys load straight from memory.  One
+// 1 KB table T(x) = {2s, s, s, 3s} (s = SubBytes(x), bytes in row order) is
+// enough: the other three columns of the classic four-table form are byte
+// rotations of it, and the final round's S-box bytes are read out of T.
+//
+// Bank conflicts: a wave's 64 lookups per step use data-dependent indices.
+// The table is replicated kCopies times in LDS, copy c holding entry e at
+// word e * kCopies + c, and lane l always reads copy l % kCopies, so lanes
+// with distinct (l % kCopies) never share a bank whatever the indices are.
+// The S-box itself is derived at compile time from its FIPS-197 definition
+// (inverse in GF(2^8) then the affine map with 0x63).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace sufhip {
+
+struct SboxTable {
+  uint8_t v[256];
+};
+
+constexpr uint8_t gf_mul_c(uint8_t a, uint8_t b) {
+  uint8_t r = 0;
+  for (int i = 0; i < 8; ++i) {
+    if (b & 1) r = static_cast<uint8_t>(r ^ a);
+    a = static_cast<uint8_t>((a << 1) ^ ((a & 0x80) ? 0x1b : 0));
+    b = static_cast<uint8_t>(b >> 1);
+  }
+  return r;
+}
+
+constexpr SboxTable make_sbox() {
+  SboxTable t{};
+  for (int x = 0; x < 256; ++x) {
+    uint8_t inv = 0;
+    if (x != 0) {
+      // x^254 = x^-1
+      uint8_t r = 1, base = static_cast<uint8_t>(x);
+      int e = 254;
+      while (e) {
+        if (e & 1) r = gf_mul_c(r, base);
+        base = gf_mul_c(base, base);
+        e >>= 1;
+      }
+      inv = r;
+    }
+    uint8_t s = 0x63;
+    for (int i = 0; i < 8; ++i) {
+      int bit = ((inv >> i) ^ (inv >> ((i + 4) & 7)) ^ (inv >> ((i + 5) & 7)) ^
+                 (inv >> ((i + 6) & 7)) ^ (inv >> ((i + 7) & 7))) & 1;
+      s = static_cast<uint8_t>(s ^ (bit << i));
+    }
+    t.v[x] = s;
+  }
+  return t;
+}
+
+struct TTable {
+  uint32_t v[256];
+};
+
+constexpr TTable make_ttable() {
+  TTable t{};
+  SboxTable s = make_sbox();
+  for (int x = 0; x < 256; ++x) {
+    uint32_t v = s.v[x];
+    uint32_t v2 = gf_mul_c(static_cast<uint8_t>(v), 2);
+    uint32_t v3 = v2 ^ v;
+    t.v[x] = v2 | (v << 8) | (v << 16) | (v3 << 24);
+  }
+  return t;
+}
+
+inline constexpr SboxTable kSboxHost = make_sbox();
+inline constexpr TTable kTHost = make_ttable();
+
+// Per-translation-unit device copy of T (no relocatable device code).
+static __device__ const TTable kTDev = make_ttable();
+
+// Round keys of one AES-128 key as 44 little-endian words (kernel argument).
+struct RoundKeys {
+  uint32_t w[44];
+};
+
+// The myl7 PRG keys K_0..K_7 (prg_init, third_party/myl7_fss/src/prg/
+// aes128_mmo.c:16-31 with kBlocks = 8), expanded; passed by value.
+constexpr int kPrgMaxBlocks = 8;
+struct PrgKeys {
+  uint32_t rk[kPrgMaxBlocks][44];
+};
+
+// Host-side key expansion (FIPS-197 5.2) producing 44 little-endian words.
+inline void aes128_expand_words(const uint8_t key[16], uint32_t rk[44]) {
+  uint8_t b[176];
+  for (int i = 0; i < 16; ++i) b[i] = key[i];
+  uint8_t rcon = 1;
+  for (int w = 4; w < 44; ++w) {
+    uint8_t t0 = b[4 * (w - 1)], t1 = b[4 * (w - 1) + 1], t2 = b[4 * (w - 1) + 2],
+            t3 = b[4 * (w - 1) + 3];
+    if (w % 4 == 0) {
+      uint8_t r0 = t0;
+      t0 = static_cast<uint8_t>(kSboxHost.v[t1] ^ rcon);
+      t1 = kSboxHost.v[t2];
+      t2 = kSboxHost.v[t3];
+      t3 = kSboxHost.v[r0];
+      rcon = gf_mul_c(rcon, 2);
+    }
+    b[4 * w] = static_cast<uint8_t>(b[4 * (w - 4)] ^ t0);
+    b[4 * w + 1] = static_cast<uint8_t>(b[4 * (w - 4) + 1] ^ t1);
+    b[4 * w + 2] = static_cast<uint8_t>(b[4 * (w - 4) + 2] ^ t2);
+    b[4 * w + 3] = static_cast<uint8_t>(b[4 * (w - 4) + 3] ^ t3);
+  }
+  for (int w = 0; w < 44; ++w)
+    rk[w] = uint32_t(b[4 * w]) | uint32_t(b[4 * w + 1]) << 8 | uint32_t(b[4 * w + 2]) << 16 |
+            uint32_t(b[4 * w + 3]) << 24;
+}
+
+inline void expand_prg_keys(const uint8_t* state, int blocks, PrgKeys* k) {
+  for (int j = 0; j < kPrgMaxBlocks; ++j)
+    for (int w = 0; w < 44; ++w) k->rk[j][w] = 0;
+  for (int j = 0; j < blocks && j < kPrgMaxBlocks; ++j) aes128_expand_words(state + 16 * j, k->rk[j]);
+}
+
+__device__ __forceinline__ uint32_t rotl32(uint32_t x, int r) {
+  return __builtin_amdgcn_alignbit(x, x, 32 - r);
+}
+
+// LDS-resident T table, kCopies-way replicated.  `lane_word` is this lane's
+// copy index (lane % kCopies).
+template <int kCopies>
+struct AesLds {
+  static constexpr int kWords = 256 * kCopies;
+  const uint32_t* tab;  // LDS
+  uint32_t lane_word;
+
+  __device__ __forceinline__ uint32_t T(uint32_t byte) const {
+    return tab[byte * kCopies + lane_word];
+  }
+  __device__ __forceinline__ uint32_t b0(uint32_t w) const { return T(w & 0xffu); }
+  __device__ __forceinline__ uint32_t b1(uint32_t w) const { return T((w >> 8) & 0xffu); }
+  __device__ __forceinline__ uint32_t b2(uint32_t w) const { return T((w >> 16) & 0xffu); }
+  __device__ __forceinline__ uint32_t b3(uint32_t w) const { return T(w >> 24); }
+
+  // One full middle round: SubBytes, ShiftRows, MixColumns, AddRoundKey.
+  __device__ __forceinline__ void round(uint32_t& s0, uint32_t& s1, uint32_t& s2, uint32_t& s3,
+                                        uint32_t k0, uint32_t k1, uint32_t k2,
+                                        uint32_t k3) const {
+    uint32_t t0 = b0(s0) ^ rotl32(b1(s1), 8) ^ rotl32(b2(s2), 16) ^ rotl32(b3(s3), 24) ^ k0;
+    uint32_t t1 = b0(s1) ^ rotl32(b1(s2), 8) ^ rotl32(b2(s3), 16) ^ rotl32(b3(s0), 24) ^ k1;
+    uint32_t t2 = b0(s2) ^ rotl32(b1(s3), 8) ^ rotl32(b2(s0), 16) ^ rotl32(b3(s1), 24) ^ k2;
+    uint32_t t3 = b0(s3) ^ rotl32(b1(s0), 8) ^ rotl32(b2(s1), 16) ^ rotl32(b3(s2), 24) ^ k3;
+    s0 = t0;
+    s1 = t1;
+    s2 = t2;
+    s3 = t3;
+  }
+
+  // Final-round column c from state words (a = s_c, b = s_{c+1}, ...).
+  __device__ __forceinline__ uint32_t last_col(uint32_t a, uint32_t b, uint32_t c,
+                                               uint32_t d) const {
+    return ((b0(a) >> 8) & 0xffu) | (b1(b) & 0xff00u) | (b2(c) & 0xff0000u) |
+           ((b3(d) << 8) & 0xff000000u);
+  }
+
+  // Full AES-128 encryption of (s0..s3); rk points at the 11 round keys
+  // (uint4 per round, usually in LDS).
+  __device__ __forceinline__ void encrypt(uint32_t& s0, uint32_t& s1, uint32_t& s2, uint32_t& s3,
+                                          const uint4* rk) const {
+    uint4 k = rk[0];
+    s0 ^= k.x;
+    s1 ^= k.y;
+    s2 ^= k.z;
+    s3 ^= k.w;
+#pragma unroll
+    for (int r = 1; r < 10; ++r) {
+      k = rk[r];
+      round(s0, s1, s2, s3, k.x, k.y, k.z, k.w);
+    }
+    k = rk[10];
+    uint32_t o0 = last_col(s0, s1, s2, s3) ^ k.x;
+    uint32_t o1 = last_col(s1, s2, s3, s0) ^ k.y;
+    uint32_t o2 = last_col(s2, s3, s0, s1) ^ k.z;
+    uint32_t o3 = last_col(s3, s0, s1, s2) ^ k.w;
+    s0 = o0;
+    s1 = o1;
+    s2 = o2;
+    s3 = o3;
+  }
+
+  // Only byte 0 of the ciphertext: rounds 1-8 in full, column 0 of round 9,
+  // one S-box lookup in round 10.
+  __device__ __forceinline__ uint32_t encrypt_byte0(uint32_t s0, uint32_t s1, uint32_t s2,
+                                                    uint32_t s3, const uint4* rk) const {
+    uint4 k = rk[0];
+    s0 ^= k.x;
+    s1 ^= k.y;
+    s2 ^= k.z;
+    s3 ^= k.w;
+#pragma unroll
+    for (int r = 1; r < 9; ++r) {
+      k = rk[r];
+      round(s0, s1, s2, s3, k.x, k.y, k.z, k.w);
+    }
+    const uint32_t k9 = reinterpret_cast<const uint32_t*>(rk)[36];
+    const uint32_t k10 = reinterpret_cast<const uint32_t*>(rk)[40];
+    uint32_t c0 = b0(s0) ^ rotl32(b1(s1), 8) ^ rotl32(b2(s2), 16) ^ rotl32(b3(s3), 24) ^ k9;
+    return ((b0(c0) >> 8) ^ k10) & 0xffu;
+  }
+};
+
+// Copies `nkeys` expanded keys (44 words each) from a kernel argument into
+// LDS as uint4 rounds.  Must be followed by __syncthreads().
+__device__ __forceinline__ void fill_round_keys(uint4* lds, const uint32_t (*rk)[44], int nkeys) {
+  for (int i = threadIdx.x; i < nkeys * 11; i += blockDim.x) {
+    const uint32_t* k = rk[i / 11] + 4 * (i % 11);
+    lds[i] = make_uint4(k[0], k[1], k[2], k[3]);
+  }
+}
+
+// Cooperative fill of the replicated table from the constant T table in
+// global memory (`tsrc`, 256 words).  Must be followed by __syncthreads().
+template <int kCopies>
+__device__ __forceinline__ void fill_ttable(uint32_t* lds, const uint32_t* tsrc) {
+  const int nthreads = blockDim.x;
+  for (int i = threadIdx.x; i < 256 * kCopies; i += nthreads) {
+    lds[i] = tsrc[i / kCopies];
+  }
+}
+
+}  // namespace sufhip

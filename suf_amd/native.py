@@ -1,0 +1,100 @@
+"""ctypes binding of libsuf_hip.so (the C ABI declared in include/suf_hip.h).
+
+The library is loaded from suf_amd/lib/libsuf_hip.so, built in-tree by
+`python -m suf_amd.build`.  There is no fallback: if the library is missing
+or fails to load, every entry point raises.
+"""
+import ctypes
+import os
+import re
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+LIB_PATH = os.path.join(PKG, "lib", "libsuf_hip.so")
+HEADER = os.path.join(ROOT, "include", "suf_hip.h")
+
+OK = 0
+GROUP_XOR = 0
+GROUP_ADD = 1
+DCF_OUT_BIT = 0
+DCF_OUT_BYTES = 1
+DCF_OUT_PACKED = 2
+
+c_int = ctypes.c_int
+c_sz = ctypes.c_size_t
+c_u64 = ctypes.c_uint64
+c_i64 = ctypes.c_int64
+c_dbl = ctypes.c_double
+c_vp = ctypes.c_void_p
+c_float = ctypes.c_float
+
+# argtypes for every exported function; pointers travel as integers (void*).
+_SIGS = {
+    "sufhip_abi_version": (c_int, []),
+    "sufhip_last_error": (ctypes.c_char_p, []),
+    "sufhip_init": (c_int, [c_int]),
+    "sufhip_device_count": (c_int, [c_vp]),
+    "sufhip_stream_create": (c_int, [c_vp]),
+    "sufhip_stream_destroy": (c_int, [c_vp]),
+    "sufhip_stream_synchronize": (c_int, [c_vp]),
+    "sufhip_malloc": (c_int, [c_vp, c_sz]),
+    "sufhip_free": (c_int, [c_vp]),
+    "sufhip_host_alloc": (c_int, [c_vp, c_sz]),
+    "sufhip_host_free": (c_int, [c_vp]),
+    "sufhip_memcpy_h2d": (c_int, [c_vp, c_vp, c_sz, c_vp]),
+    "sufhip_memcpy_d2h": (c_int, [c_vp, c_vp, c_sz, c_vp]),
+    "sufhip_memcpy_d2d": (c_int, [c_vp, c_vp, c_sz, c_vp]),
+    "sufhip_event_create": (c_int, [c_vp]),
+    "sufhip_event_destroy": (c_int, [c_vp]),
+    "sufhip_event_record": (c_int, [c_vp, c_vp]),
+    "sufhip_event_elapsed_ms": (c_int, [c_vp, c_vp, c_vp]),
+    "sufhip_aes128_ctr": (c_int, [c_vp, c_vp, c_u64, c_u64, c_sz, c_vp]),
+    "sufhip_prg_mmo": (c_int, [c_vp, c_vp, c_sz, c_int, c_vp, c_vp]),
+    "sufhip_dcf_key_bytes": (c_sz, [c_int, c_int]),
+    "sufhip_dcf_gen": (c_int, [c_int, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_vp, c_sz, c_vp,
+                               c_vp, c_vp]),
+    "sufhip_dcf_eval": (c_int, [c_int, c_int, c_int, c_vp, c_vp, c_sz, c_int, c_vp, c_sz, c_int,
+                                c_int, c_vp, c_vp]),
+    "sufhip_host_mt19937_64": (c_int, [c_u64, c_vp, c_sz]),
+    "sufhip_host_normal_fixed": (c_int, [c_u64, c_dbl, c_dbl, c_int, c_vp, c_sz]),
+}
+
+_lib = None
+
+
+class SufHipError(RuntimeError):
+    pass
+
+
+def header_symbols():
+    """Names of every function declared in include/suf_hip.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sufhip_[a-z0-9_]+)\s*\(", text)))
+
+
+def load(path=LIB_PATH):
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise SufHipError("libsuf_hip.so not built: run `python -m suf_amd.build` (%s)" % path)
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc, what=""):
+    if rc != OK:
+        msg = load().sufhip_last_error().decode(errors="replace")
+        raise SufHipError("%s failed (status %d): %s" % (what or "sufhip call", rc, msg))
+
+
+def call(name, *args):
+    rc = getattr(load(), name)(*args)
+    check(rc, name)
+    return rc
