@@ -222,6 +222,125 @@ __device__ __forceinline__ void fill_round_keys(uint4* lds, const uint32_t (*rk)
   }
 }
 
+// ---------------------------------------------------------------------------
+// Two-table variant for the DCF hot loop.
+//
+// LDS holds T0 = T and T2 = rotl16(T), each replicated 64 ways (64 KB each;
+// T2 starts at byte 65536).  Entry e, copy c of table j sits at byte address
+// j * 65536 + e * 256 + c * 4, so a lookup address is assembled with one
+// v_perm_b32 from the state word (byte k -> address byte 1) and a per-lane
+// register holding c * 4 in byte 0 and j in byte 2.  With
+// T1 = rotl8(T0) and T3 = rotl8(T2), an output column is
+//   T0[a] ^ T2[c] ^ rotl8(T0[b] ^ T2[d] ^ rotr8(k)),
+// i.e. one rotate per column once round keys 1..9 are stored pre-rotated by
+// rotr8 (AesLds2Keys).  The final round reads S-box bytes straight out of
+// T0 (bytes 1, 2) and T2 (bytes 0, 3).  Every lane reads only its own copy,
+// so the 64 lanes of a wave touch 64 distinct banks.
+struct AesLds2 {
+  static constexpr int kCopies = 64;
+  static constexpr int kWordsPerTable = 256 * kCopies;
+  static constexpr int kBytes = 2 * kWordsPerTable * 4;
+  const uint32_t* lds;  // base of the two tables
+  uint32_t lane_t0;     // lane * 4
+  uint32_t lane_t2;     // lane * 4 | 0x10000
+
+  __device__ __forceinline__ static uint32_t sel(int k) {
+    // byte0 <- src1 byte0, byte1 <- src0 byte k, byte2 <- src1 byte2, byte3 <- 0
+    return 0x0c020000u | uint32_t(4 + k) << 8;
+  }
+  __device__ __forceinline__ uint32_t ld(uint32_t byte_addr) const {
+    return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(lds) + byte_addr);
+  }
+  template <int k>
+  __device__ __forceinline__ uint32_t t0(uint32_t w) const {
+    return ld(__builtin_amdgcn_perm(w, lane_t0, sel(k)));
+  }
+  template <int k>
+  __device__ __forceinline__ uint32_t t2(uint32_t w) const {
+    return ld(__builtin_amdgcn_perm(w, lane_t2, sel(k)));
+  }
+  __device__ __forceinline__ static uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+  }
+  // Column from (a = s_c, b = s_{c+1}, c = s_{c+2}, d = s_{c+3}) and the
+  // rotr8-rotated round key word kr.
+  __device__ __forceinline__ uint32_t col(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                          uint32_t kr) const {
+    const uint32_t inner = xor3(t0<1>(b), t2<3>(d), kr);
+    return xor3(t0<0>(a), t2<2>(c), rotl32(inner, 8));
+  }
+  __device__ __forceinline__ void round(uint32_t& s0, uint32_t& s1, uint32_t& s2, uint32_t& s3,
+                                        const uint4 k) const {
+    const uint32_t n0 = col(s0, s1, s2, s3, k.x);
+    const uint32_t n1 = col(s1, s2, s3, s0, k.y);
+    const uint32_t n2 = col(s2, s3, s0, s1, k.z);
+    const uint32_t n3 = col(s3, s0, s1, s2, k.w);
+    s0 = n0;
+    s1 = n1;
+    s2 = n2;
+    s3 = n3;
+  }
+  __device__ __forceinline__ uint32_t last_col(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                               uint32_t k) const {
+    const uint32_t lo = __builtin_amdgcn_perm(t0<1>(b), t2<0>(a), 0x0c0c0500u);   // bytes 0,1
+    const uint32_t hi = __builtin_amdgcn_perm(t2<3>(d), t0<2>(c), 0x07020c0cu);   // bytes 2,3
+    return (lo | hi) ^ k;
+  }
+  // rk: 11 rounds as uint4; rounds 1..9 pre-rotated (AesLds2Keys layout).
+  __device__ __forceinline__ void encrypt(uint32_t& s0, uint32_t& s1, uint32_t& s2, uint32_t& s3,
+                                          const uint4* rk) const {
+    uint4 k = rk[0];
+    s0 ^= k.x;
+    s1 ^= k.y;
+    s2 ^= k.z;
+    s3 ^= k.w;
+#pragma unroll
+    for (int r = 1; r < 10; ++r) round(s0, s1, s2, s3, rk[r]);
+    k = rk[10];
+    const uint32_t o0 = last_col(s0, s1, s2, s3, k.x);
+    const uint32_t o1 = last_col(s1, s2, s3, s0, k.y);
+    const uint32_t o2 = last_col(s2, s3, s0, s1, k.z);
+    const uint32_t o3 = last_col(s3, s0, s1, s2, k.w);
+    s0 = o0;
+    s1 = o1;
+    s2 = o2;
+    s3 = o3;
+  }
+  // Byte 0 of the ciphertext only.
+  __device__ __forceinline__ uint32_t encrypt_byte0(uint32_t s0, uint32_t s1, uint32_t s2,
+                                                    uint32_t s3, const uint4* rk) const {
+    uint4 k = rk[0];
+    s0 ^= k.x;
+    s1 ^= k.y;
+    s2 ^= k.z;
+    s3 ^= k.w;
+#pragma unroll
+    for (int r = 1; r < 9; ++r) round(s0, s1, s2, s3, rk[r]);
+    const uint32_t k9 = rk[9].x;
+    const uint32_t k10 = rk[10].x;
+    const uint32_t c0 = col(s0, s1, s2, s3, k9);
+    return (t2<0>(c0) ^ k10) & 0xffu;
+  }
+};
+
+// Fills both replicated tables (AesLds2 layout).  Follow with __syncthreads().
+__device__ __forceinline__ void fill_ttable2(uint32_t* lds, const uint32_t* tsrc) {
+  for (int i = threadIdx.x; i < AesLds2::kWordsPerTable; i += blockDim.x) {
+    const uint32_t v = tsrc[i / AesLds2::kCopies];
+    lds[i] = v;
+    lds[AesLds2::kWordsPerTable + i] = rotl32(v, 16);
+  }
+}
+
+// Host: round keys in the AesLds2 layout (rounds 1..9 rotated right by 8).
+inline void aes2_key_layout(const uint32_t rk[44], uint32_t out[44]) {
+  for (int w = 0; w < 44; ++w) {
+    const int r = w / 4;
+    const uint32_t v = rk[w];
+    out[w] = (r >= 1 && r <= 9) ? ((v >> 8) | (v << 24)) : v;
+  }
+}
+
 // Cooperative fill of the replicated table from the constant T table in
 // global memory (`tsrc`, 256 words).  Must be followed by __syncthreads().
 template <int kCopies>

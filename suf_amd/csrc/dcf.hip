@@ -25,8 +25,12 @@
 namespace sufhip {
 namespace {
 
-constexpr int kEvalBlock = 256;
-constexpr int kDcfCopies = 64;  // T-table replication (64 KB of LDS)
+// One workgroup per CU: the two replicated AES tables take 128 KB of the
+// CU's 160 KB LDS.  Kernels loop over the batch in grid strides.
+#ifndef SUFHIP_DCF_BLOCK
+#define SUFHIP_DCF_BLOCK 512
+#endif
+constexpr int kDcfBlock = SUFHIP_DCF_BLOCK;
 
 struct Prg4 {
   uint32_t rk[4][44];  // K_0..K_3: DCF uses PRG output blocks 0..3
@@ -140,8 +144,7 @@ __device__ __forceinline__ void load16(const uint8_t* p, bool more, uint32_t (&w
 }
 
 // Bit-mode walk of one chunk: returns share byte 0 & 1.
-template <int kCopies>
-__device__ __forceinline__ uint32_t walk_bit(const AesLds<kCopies>& aes, const uint4* rkl,
+__device__ __forceinline__ uint32_t walk_bit(const AesLds2& aes, const uint4* rkl,
                                              const uint8_t* chunk, int in_bits, uint64_t x,
                                              uint32_t party) {
   uint32_t seed[4];
@@ -153,9 +156,9 @@ __device__ __forceinline__ uint32_t walk_bit(const AesLds<kCopies>& aes, const u
   for (int i = 0; i < in_bits; ++i, cw += 33) {
     const uint32_t xi = uint32_t(x >> (in_bits - 1 - i)) & 1u;
     const CwBit c = load_cw_bit(cw);
-    const uint4* ks = rkl + 22 * xi;  // K_{2 x_i}: next seed
-    const uint4* kv = ks + 11;         // K_{2 x_i + 1}: value block
     uint32_t a0 = s0, a1 = s1, a2 = s2, a3 = s3;
+const uint4* ks = rkl + 22 * xi;  // K_{2 x_i}: next seed
+    const uint4* kv = ks + 11;         // K_{2 x_i + 1}: value block
     aes.encrypt(a0, a1, a2, a3, ks);
     const uint32_t vb = (aes.encrypt_byte0(s0, s1, s2, s3, kv) ^ s0) & 1u;
     a0 ^= s0;
@@ -183,8 +186,8 @@ __device__ __forceinline__ uint32_t walk_bit(const AesLds<kCopies>& aes, const u
 }
 
 // Full-block walk of one chunk (any group): returns the 16-byte share.
-template <int kGroup, int kCopies>
-__device__ __forceinline__ U128 walk_full(const AesLds<kCopies>& aes, const uint4* rkl,
+template <int kGroup>
+__device__ __forceinline__ U128 walk_full(const AesLds2& aes, const uint4* rkl,
                                           const uint8_t* chunk, int in_bits, uint64_t x,
                                           uint32_t party, bool more_after) {
   uint32_t seed[4];
@@ -233,56 +236,60 @@ __device__ __forceinline__ U128 walk_full(const AesLds<kCopies>& aes, const uint
   return gadd<kGroup>(v, s);
 }
 
-template <int kMode, int kCopies>
-__global__ void __launch_bounds__(kEvalBlock) dcf_eval_bit_kernel(DcfEvalArgs a) {
-  __shared__ uint32_t lds[256 * kCopies];
-  __shared__ uint4 rkl[4 * 11];
-  fill_ttable<kCopies>(lds, kTDev.v);
-  fill_round_keys(rkl, a.prg.rk, 4);
-  __syncthreads();
-  const AesLds<kCopies> aes{lds, threadIdx.x % kCopies};
-  const size_t e = size_t(blockIdx.x) * kEvalBlock + threadIdx.x;
-  uint32_t bit = 0;
-  if (e < a.n) {
+// Stages the replicated tables and the K_0..K_3 round keys in LDS.
+#define SUFHIP_DCF_LDS_SETUP(PRG)                                  \
+  __shared__ uint32_t tabs[2 * AesLds2::kWordsPerTable];           \
+  __shared__ uint4 rkl[4 * 11];                                    \
+  fill_ttable2(tabs, kTDev.v);                                     \
+  fill_round_keys(rkl, (PRG).rk, 4);                               \
+  __syncthreads();                                                 \
+  const uint32_t lane4 = (threadIdx.x & 63u) * 4u;                 \
+  const AesLds2 aes{tabs, lane4, lane4 | 0x10000u}
+
+template <int kMode>
+__global__ void __launch_bounds__(kDcfBlock) dcf_eval_bit_kernel(DcfEvalArgs a) {
+  SUFHIP_DCF_LDS_SETUP(a.prg);
+  const size_t stride = size_t(gridDim.x) * kDcfBlock;
+  for (size_t base = size_t(blockIdx.x) * kDcfBlock; base < a.n; base += stride) {
+    const size_t e = base + threadIdx.x;
+    uint32_t bit = 0;
+    if (e < a.n) {
+      const uint8_t* key = a.broadcast ? a.keys : a.keys + e * a.key_bytes;
+      const uint32_t party = key[2] & 1u;
+      uint64_t x = a.xs[e];
+      if (a.in_bits < 64) x &= (uint64_t(1) << a.in_bits) - 1;
+      bit = walk_bit(aes, rkl, key + 8, a.in_bits, x, party);
+    }
+    if constexpr (kMode == SUFHIP_DCF_OUT_BIT) {
+      if (e < a.n) static_cast<uint8_t*>(a.out)[e] = uint8_t(bit);
+    } else {
+      // Waves cover 64 consecutive elements starting at a multiple of 64.
+      const uint64_t word = __ballot(bit != 0);
+      if ((threadIdx.x & 63) == 0 && e < a.n) static_cast<uint64_t*>(a.out)[e >> 6] = word;
+    }
+  }
+}
+
+template <int kGroup>
+__global__ void __launch_bounds__(kDcfBlock) dcf_eval_bytes_kernel(DcfEvalArgs a) {
+  SUFHIP_DCF_LDS_SETUP(a.prg);
+  const size_t stride = size_t(gridDim.x) * kDcfBlock;
+  const size_t chunk_bytes = 32 + 33 * size_t(a.in_bits);
+  for (size_t e = size_t(blockIdx.x) * kDcfBlock + threadIdx.x; e < a.n; e += stride) {
     const uint8_t* key = a.broadcast ? a.keys : a.keys + e * a.key_bytes;
     const uint32_t party = key[2] & 1u;
     uint64_t x = a.xs[e];
     if (a.in_bits < 64) x &= (uint64_t(1) << a.in_bits) - 1;
-    bit = walk_bit<kCopies>(aes, rkl, key + 8, a.in_bits, x, party);
-  }
-  if constexpr (kMode == SUFHIP_DCF_OUT_BIT) {
-    if (e < a.n) static_cast<uint8_t*>(a.out)[e] = uint8_t(bit);
-  } else {
-    const uint64_t word = __ballot(bit != 0);
-    if ((threadIdx.x & 63) == 0 && e < a.n) static_cast<uint64_t*>(a.out)[e >> 6] = word;
-  }
-}
-
-template <int kGroup, int kCopies>
-__global__ void __launch_bounds__(kEvalBlock) dcf_eval_bytes_kernel(DcfEvalArgs a) {
-  __shared__ uint32_t lds[256 * kCopies];
-  __shared__ uint4 rkl[4 * 11];
-  fill_ttable<kCopies>(lds, kTDev.v);
-  fill_round_keys(rkl, a.prg.rk, 4);
-  __syncthreads();
-  const AesLds<kCopies> aes{lds, threadIdx.x % kCopies};
-  const size_t e = size_t(blockIdx.x) * kEvalBlock + threadIdx.x;
-  if (e >= a.n) return;
-  const uint8_t* key = a.broadcast ? a.keys : a.keys + e * a.key_bytes;
-  const uint32_t party = key[2] & 1u;
-  uint64_t x = a.xs[e];
-  if (a.in_bits < 64) x &= (uint64_t(1) << a.in_bits) - 1;
-  const size_t chunk_bytes = 32 + 33 * size_t(a.in_bits);
-  uint8_t* out = static_cast<uint8_t*>(a.out) + e * size_t(a.out_bytes);
-  for (int c = 0; c < a.chunks; ++c) {
-    const bool more = (c + 1) * chunk_bytes + 8 < a.key_bytes;
-    U128 r = walk_full<kGroup, kCopies>(aes, rkl, key + 8 + c * chunk_bytes, a.in_bits, x,
-                                        party, more);
-    const int base = 16 * c;
-    const int take = a.out_bytes - base < 16 ? a.out_bytes - base : 16;
-    for (int b = 0; b < take; ++b) {
-      const uint64_t word = b < 8 ? r.lo : r.hi;
-      out[base + b] = uint8_t(word >> (8 * (b & 7)));
+    uint8_t* out = static_cast<uint8_t*>(a.out) + e * size_t(a.out_bytes);
+    for (int c = 0; c < a.chunks; ++c) {
+      const bool more = (c + 1) * chunk_bytes + 8 < a.key_bytes;
+      U128 r = walk_full<kGroup>(aes, rkl, key + 8 + c * chunk_bytes, a.in_bits, x, party, more);
+      const int base = 16 * c;
+      const int take = a.out_bytes - base < 16 ? a.out_bytes - base : 16;
+      for (int b = 0; b < take; ++b) {
+        const uint64_t word = b < 8 ? r.lo : r.hi;
+        out[base + b] = uint8_t(word >> (8 * (b & 7)));
+      }
     }
   }
 }
@@ -347,12 +354,12 @@ struct DcfGenArgs {
   int chunks;
 };
 
-template <int kCopies>
-__device__ __forceinline__ void prg4(const AesLds<kCopies>& aes, const uint4* rkl, const U128& s,
+__device__ __forceinline__ void prg4(const AesLds2& aes, const uint4* rkl, const U128& s,
                                      U128 (&o)[4]) {
   const uint32_t w0 = uint32_t(s.lo), w1 = uint32_t(s.lo >> 32), w2 = uint32_t(s.hi),
                  w3 = uint32_t(s.hi >> 32);
-#pragma unroll
+  // One block at a time keeps the dealer kernel inside the register budget.
+#pragma unroll 1
   for (int j = 0; j < 4; ++j) {
     uint32_t a0 = w0, a1 = w1, a2 = w2, a3 = w3;
     aes.encrypt(a0, a1, a2, a3, rkl + 11 * j);
@@ -367,18 +374,9 @@ __device__ __forceinline__ void put128(ByteWriter& w, U128 v) {
   w.put32(uint32_t(v.hi >> 32));
 }
 
-// myl7 dcf_gen (third_party/myl7_fss/src/dcf.c:42-142) for kLtAlpha, one key
-// pair per lane, written in the adapter layout (myl7_fss_backend.hpp:156-210).
-template <int kGroup, int kCopies>
-__global__ void __launch_bounds__(kEvalBlock) dcf_gen_kernel(DcfGenArgs a) {
-  __shared__ uint32_t lds[256 * kCopies];
-  __shared__ uint4 rkl[4 * 11];
-  fill_ttable<kCopies>(lds, kTDev.v);
-  fill_round_keys(rkl, a.prg.rk, 4);
-  __syncthreads();
-  const AesLds<kCopies> aes{lds, threadIdx.x % kCopies};
-  const size_t e = size_t(blockIdx.x) * kEvalBlock + threadIdx.x;
-  if (e >= a.n) return;
+template <int kGroup>
+__device__ __forceinline__ void gen_one(const AesLds2& aes, const uint4* rkl, const DcfGenArgs& a,
+                                        size_t e) {
   const int nb = a.in_bits;
   uint64_t alpha = a.alpha[e];
   if (nb < 64) alpha &= (uint64_t(1) << nb) - 1;
@@ -416,8 +414,8 @@ __global__ void __launch_bounds__(kEvalBlock) dcf_gen_kernel(DcfGenArgs a) {
     U128 v{0, 0};
     for (int i = 0; i < nb; ++i) {
       U128 e0[4], e1[4];
-      prg4<kCopies>(aes, rkl, s0, e0);
-      prg4<kCopies>(aes, rkl, s1, e1);
+      prg4(aes, rkl, s0, e0);
+      prg4(aes, rkl, s1, e1);
       const uint32_t t0l = uint32_t(e0[0].hi >> 63), t0r = uint32_t(e0[2].hi >> 63);
       const uint32_t t1l = uint32_t(e1[0].hi >> 63), t1r = uint32_t(e1[2].hi >> 63);
 #pragma unroll
@@ -463,8 +461,35 @@ __global__ void __launch_bounds__(kEvalBlock) dcf_gen_kernel(DcfGenArgs a) {
   w1.flush();
 }
 
+// myl7 dcf_gen (third_party/myl7_fss/src/dcf.c:42-142) for kLtAlpha, one key
+// pair per lane, written in the adapter layout (myl7_fss_backend.hpp:156-210).
+template <int kGroup>
+__global__ void __launch_bounds__(kDcfBlock) dcf_gen_kernel(DcfGenArgs a) {
+  SUFHIP_DCF_LDS_SETUP(a.prg);
+  const size_t stride = size_t(gridDim.x) * kDcfBlock;
+  for (size_t e = size_t(blockIdx.x) * kDcfBlock + threadIdx.x; e < a.n; e += stride)
+    gen_one<kGroup>(aes, rkl, a, e);
+}
+
+// K_0..K_3 expanded and laid out for AesLds2 (rounds 1..9 rotated).
 void fill_prg4(const uint8_t* state, Prg4* p) {
-  for (int j = 0; j < 4; ++j) aes128_expand_words(state + 16 * j, p->rk[j]);
+  for (int j = 0; j < 4; ++j) {
+    uint32_t rk[44];
+    aes128_expand_words(state + 16 * j, rk);
+    aes2_key_layout(rk, p->rk[j]);
+  }
+}
+
+// Grid for the grid-stride DCF kernels: one workgroup per CU (LDS-limited),
+// never more workgroups than the batch needs.
+int dcf_grid(size_t n, unsigned int* grid) {
+  int dev = 0, cus = 0;
+  SUFHIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
+  SUFHIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+               "hipDeviceGetAttribute(CU count)");
+  const size_t need = (n + kDcfBlock - 1) / kDcfBlock;
+  *grid = static_cast<unsigned int>(need < size_t(cus) ? need : size_t(cus));
+  return SUFHIP_OK;
 }
 
 constexpr size_t kMaxElems = size_t(1) << 38;
@@ -509,12 +534,13 @@ int sufhip_dcf_gen(int group, int in_bits, const uint8_t* prg_state, const uint6
   a.payload_len = payload_len;
   a.in_bits = in_bits;
   a.chunks = (payload_len + 15) / 16;
-  const dim3 grid(grid_for(n, kEvalBlock));
+  unsigned int g = 0;
+  if (int rc = dcf_grid(n, &g)) return rc;
   if (group == SUFHIP_GROUP_XOR)
-    hipLaunchKernelGGL((dcf_gen_kernel<SUFHIP_GROUP_XOR, kDcfCopies>), grid, dim3(kEvalBlock), 0,
+    hipLaunchKernelGGL((dcf_gen_kernel<SUFHIP_GROUP_XOR>), dim3(g), dim3(kDcfBlock), 0,
                        as_stream(stream), a);
   else
-    hipLaunchKernelGGL((dcf_gen_kernel<SUFHIP_GROUP_ADD, kDcfCopies>), grid, dim3(kEvalBlock), 0,
+    hipLaunchKernelGGL((dcf_gen_kernel<SUFHIP_GROUP_ADD>), dim3(g), dim3(kDcfBlock), 0,
                        as_stream(stream), a);
   return check_launch("dcf_gen_kernel");
 }
@@ -550,24 +576,22 @@ int sufhip_dcf_eval(int group, int in_bits, int payload_len, const uint8_t* prg_
   a.in_bits = in_bits;
   a.chunks = 1;
   a.out_bytes = out_mode == SUFHIP_DCF_OUT_BYTES ? out_bytes : 1;
-  const dim3 grid(grid_for(n, kEvalBlock));
+  unsigned int g = 0;
+  if (int rc = dcf_grid(n, &g)) return rc;
+  const dim3 grid(g), block(kDcfBlock);
   hipStream_t s = as_stream(stream);
   if (out_mode == SUFHIP_DCF_OUT_BIT) {
-    hipLaunchKernelGGL((dcf_eval_bit_kernel<SUFHIP_DCF_OUT_BIT, kDcfCopies>), grid,
-                       dim3(kEvalBlock), 0, s, a);
+    hipLaunchKernelGGL((dcf_eval_bit_kernel<SUFHIP_DCF_OUT_BIT>), grid, block, 0, s, a);
   } else if (out_mode == SUFHIP_DCF_OUT_PACKED) {
     SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_out) & 7) == 0,
                    "sufhip_dcf_eval: packed output must be 8-byte aligned");
-    hipLaunchKernelGGL((dcf_eval_bit_kernel<SUFHIP_DCF_OUT_PACKED, kDcfCopies>), grid,
-                       dim3(kEvalBlock), 0, s, a);
+    hipLaunchKernelGGL((dcf_eval_bit_kernel<SUFHIP_DCF_OUT_PACKED>), grid, block, 0, s, a);
   } else {
     a.chunks = (out_bytes + 15) / 16;
     if (group == SUFHIP_GROUP_XOR)
-      hipLaunchKernelGGL((dcf_eval_bytes_kernel<SUFHIP_GROUP_XOR, kDcfCopies>), grid,
-                         dim3(kEvalBlock), 0, s, a);
+      hipLaunchKernelGGL((dcf_eval_bytes_kernel<SUFHIP_GROUP_XOR>), grid, block, 0, s, a);
     else
-      hipLaunchKernelGGL((dcf_eval_bytes_kernel<SUFHIP_GROUP_ADD, kDcfCopies>), grid,
-                         dim3(kEvalBlock), 0, s, a);
+      hipLaunchKernelGGL((dcf_eval_bytes_kernel<SUFHIP_GROUP_ADD>), grid, block, 0, s, a);
   }
   return check_launch("dcf_eval kernel");
 }
