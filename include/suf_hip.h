@@ -133,6 +133,79 @@ int sufhip_dcf_eval(int group, int in_bits, int payload_len, const uint8_t* prg_
                     void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* Ring postprocessing, Beaver products, row reductions and open packing.   */
+/* Each replaces the launcher of the same name in                          */
+/* include/runtime/cuda_primitives.hpp (line numbers below) with the same   */
+/* argument list, a status return, and the kernel formula of               */
+/* cuda/cuda_primitives.cu.                                                 */
+/* ---------------------------------------------------------------------- */
+/* launch_beaver_mul_kernel (:15-25): out = c + d*b + e*a (+ d*e if party 0).
+ * d_x, d_y are accepted for signature parity and not read. */
+int sufhip_beaver_mul(int party, const uint64_t* d_x, const uint64_t* d_y, const uint64_t* d_a,
+                      const uint64_t* d_b, const uint64_t* d_c, const uint64_t* d_d_open,
+                      const uint64_t* d_e_open, uint64_t* d_out, size_t n, void* stream);
+/* launch_beaver_mul_aos_kernel (:29-35): triples are {u64 a, b, c} per element. */
+int sufhip_beaver_mul_aos(int party, const void* d_triples, const uint64_t* d_d_open,
+                          const uint64_t* d_e_open, uint64_t* d_out, size_t n, void* stream);
+/* launch_trunc_shift_kernel (:39-43): out = x >> frac_bits. */
+int sufhip_trunc_shift(const uint64_t* d_in, uint64_t* d_out, int frac_bits, size_t n,
+                       void* stream);
+/* launch_trunc_postproc_kernel (:48-64): faithful TR/ARS (kind_gapars = 0) or
+ * GapARS (1) output share from the PFSS base word, carry/sign/wrap bool words
+ * and the public xhat (formulas of include/gates/postproc_hooks.hpp:172-373).
+ * A bool index is used only when 0 <= idx < bool_stride and d_bools != NULL. */
+int sufhip_trunc_postproc(int party, int kind_gapars, int frac_bits, uint64_t r_hi_share,
+                          uint64_t m_share, const uint64_t* d_hatx_public, const uint64_t* d_arith,
+                          size_t arith_stride, int arith_idx, const uint64_t* d_bools,
+                          size_t bool_stride, int carry_idx, int sign_idx, int wrap_idx,
+                          uint64_t* d_out, size_t n, void* stream);
+/* launch_horner_cubic_kernel (:68-75): ((c3 x + c2) x + c1) x + c0. */
+int sufhip_horner_cubic(const uint64_t* d_x, const uint64_t* d_c0, const uint64_t* d_c1,
+                        const uint64_t* d_c2, const uint64_t* d_c3, uint64_t* d_out, size_t n,
+                        void* stream);
+/* launch_add_rout_aos_kernel (:79-84): out[i*out_words + j] += r_out[j] for
+ * j < r_out_words; r_out is a host array.  Up to 64 words (the reference
+ * launcher silently does nothing above 8; here that is an error above 64). */
+int sufhip_add_rout_aos(uint64_t* d_out, size_t elems, int out_words, const uint64_t* r_out,
+                        size_t r_out_words, void* stream);
+/* launch_row_broadcast_mul_kernel (:91-102). */
+int sufhip_row_broadcast_mul(int party, const uint64_t* d_A, const uint64_t* d_B_rows,
+                             const uint64_t* d_C, const uint64_t* d_d_open,
+                             const uint64_t* d_e_open_rows, int rows, int cols,
+                             const int* d_valid_lens, uint64_t* d_out, size_t n, void* stream);
+/* launch_row_sum_kernel (:106-111); valid_lens (optional) are clamped to cols. */
+int sufhip_row_sum(const uint64_t* d_mat, int rows, int cols, const int* d_valid_lens,
+                   uint64_t* d_out_rows, void* stream);
+/* launch_row_sum_ragged_kernel (:117-121). */
+int sufhip_row_sum_ragged(const uint64_t* d_vals, const int* d_row_offsets, int rows,
+                          uint64_t* d_out_rows, void* stream);
+/* launch_row_mean_kernel (:169-174): sum >> log2(L) for power-of-two L, else
+ * the u64 sum divided by L as a plain integer (the reference's formula). */
+int sufhip_row_mean(const uint64_t* d_mat, int rows, int cols, const int* d_valid_lens,
+                    uint64_t* d_out_rows, void* stream);
+/* launch_row_variance_kernel (:179-185): sum over active columns of (x - mean)^2. */
+int sufhip_row_variance(const uint64_t* d_mat, const uint64_t* d_mean, int rows, int cols,
+                        const int* d_valid_lens, uint64_t* d_out_rows, void* stream);
+/* launch_unpack_eff_bits_kernel (:189-193) / launch_pack_eff_bits_kernel
+ * (:197-201): LSB-first bitstream of eff_bits-wide values in u64 words;
+ * the packed buffer holds ceil(n * eff_bits / 64) words. */
+int sufhip_unpack_eff_bits(const uint64_t* d_packed, int eff_bits, uint64_t* d_out, size_t n,
+                           void* stream);
+int sufhip_pack_eff_bits(const uint64_t* d_in, int eff_bits, uint64_t* d_packed, size_t n,
+                         void* stream);
+/* launch_open_add_to_signed_kernel (:206-212), launch_unpack_add_to_signed_kernel
+ * (:217-224), launch_unpack_add_mod_kernel (:229-236). */
+int sufhip_open_add_to_signed(const uint64_t* d_local_share, const uint64_t* d_remote_share,
+                              uint64_t* d_out_signed, size_t n, int ring_bits, uint64_t ring_mask,
+                              void* stream);
+int sufhip_unpack_add_to_signed(const uint64_t* d_local_share, const uint64_t* d_packed_remote,
+                                int eff_bits, uint64_t* d_out_signed, size_t n, int ring_bits,
+                                uint64_t ring_mask, void* stream);
+int sufhip_unpack_add_mod(const uint64_t* d_local_share, const uint64_t* d_packed_remote,
+                          int eff_bits, uint64_t* d_out_mod, size_t n, int ring_bits,
+                          uint64_t ring_mask, void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* Host-side helpers for seeded synthetic inputs                            */
 /* ---------------------------------------------------------------------- */
 /* out[i] = the i-th output of std::mt19937_64(seed). */

@@ -120,6 +120,10 @@ void orc_beaver_matmul(int party, const uint64_t* D, const uint64_t* E, const ui
                        const uint64_t* B, const uint64_t* C, int batches, int M, int K,
                        int N, int w_transposed, int has_scale, int64_t mul_const,
                        int mul_shift, uint64_t* out, int threads);
+void orc_row_mean(const uint64_t* mat, int rows, int cols, const int* valid_lens,
+                  uint64_t* out);
+void orc_open_add(const uint64_t* local, const uint64_t* remote, int eff_bits, uint64_t* out,
+                  size_t n, int ring_bits, uint64_t ring_mask, int sign_extend);
 void orc_pack_eff_bits(const uint64_t* in, int eff_bits, uint64_t* packed, size_t n);
 void orc_unpack_eff_bits(const uint64_t* packed, int eff_bits, uint64_t* out, size_t n);
 

@@ -64,13 +64,15 @@ void orc_horner_cubic(const uint64_t* x, const uint64_t* c0, const uint64_t* c1,
   }
 }
 
-/* cuda/cuda_primitives.cu:271-301 with the launcher's clamp of r_out_words to 8 (:824-850). */
+/* cuda/cuda_primitives.cu:271-301; word j of each element gains r_out[j] for
+ * j < r_out_words.  (The reference launcher, :824-850, does nothing at all when
+ * out_words or r_out_words exceeds 8; this oracle states the kernel formula.) */
 void orc_add_rout_aos(uint64_t* out, size_t elems, int out_words, const uint64_t* r_out,
                       int r_out_words) {
   if (out_words <= 0) return;
-  int rw = r_out_words < 8 ? r_out_words : 8;
   for (size_t i = 0; i < elems; i++)
-    for (int j = 0; j < out_words && j < rw; j++) out[i * (size_t)out_words + (size_t)j] += r_out[j];
+    for (int j = 0; j < out_words && j < r_out_words; j++)
+      out[i * (size_t)out_words + (size_t)j] += r_out[j];
 }
 
 /* cuda/cuda_primitives.cu:303-336 */
@@ -193,5 +195,65 @@ void orc_unpack_eff_bits(const uint64_t* packed, int eff_bits, uint64_t* out, si
     uint64_t lo = packed[w], hi = w + 1 < words ? packed[w + 1] : 0;
     uint64_t v = off == 0 ? lo : (lo >> off) | (hi << (64 - off));
     out[i] = v & m;
+  }
+}
+
+/* cuda/cuda_primitives.cu:630-670 (row_mean_kernel): the row sum shifted right
+ * by log2(L) when L is a power of two, else the u64 sum divided by L as a plain
+ * unsigned integer (the reference's formula; not a ring operation). */
+void orc_row_mean(const uint64_t* mat, int rows, int cols, const int* valid_lens,
+                  uint64_t* out) {
+  for (int r = 0; r < rows; r++) {
+    int L = valid_lens ? valid_lens[r] : cols;
+    if (L <= 0) {
+      out[r] = 0;
+      continue;
+    }
+    uint64_t acc = 0;
+    for (int c = 0; c < L; c++) acc += mat[(size_t)r * (size_t)cols + (size_t)c];
+    if ((L & (L - 1)) == 0) {
+      int sh = 0;
+      while ((1 << sh) != L && sh < 63) ++sh;
+      out[r] = acc >> sh;
+    } else {
+      out[r] = acc / (uint64_t)(unsigned)L;
+    }
+  }
+}
+
+static uint64_t ring_sign(uint64_t v, int ring_bits, uint64_t ring_mask) {
+  if (ring_bits >= 64) return v;
+  v &= ring_mask;
+  if (v & (1ULL << (ring_bits - 1))) v |= ~ring_mask;
+  return v;
+}
+
+/* cuda/cuda_primitives.cu:26-112: open = local + remote (remote optionally
+ * eff_bits-packed), then either sign-extended from ring_bits (to_signed) or
+ * masked to the ring (mod). */
+void orc_open_add(const uint64_t* local, const uint64_t* remote, int eff_bits, uint64_t* out,
+                  size_t n, int ring_bits, uint64_t ring_mask, int sign_extend) {
+  if (ring_bits <= 0) ring_bits = 1;
+  if (ring_bits > 64) ring_bits = 64;
+  if (eff_bits <= 0) eff_bits = 1;
+  if (eff_bits > 64) eff_bits = 64;
+  size_t words = (size_t)(((unsigned __int128)n * (unsigned)eff_bits + 63) / 64);
+  uint64_t m = eff_bits >= 64 ? ~0ULL : (1ULL << eff_bits) - 1;
+  for (size_t i = 0; i < n; i++) {
+    uint64_t r;
+    if (eff_bits >= 64) {
+      r = remote[i];
+    } else {
+      size_t bit = i * (size_t)eff_bits, w = bit >> 6;
+      int off = (int)(bit & 63);
+      uint64_t lo = w < words ? remote[w] : 0, hi = w + 1 < words ? remote[w + 1] : 0;
+      r = (off == 0 ? lo : (lo >> off) | (hi << (64 - off))) & m;
+    }
+    uint64_t v = local[i] + r;
+    if (sign_extend) {
+      out[i] = ring_sign(v, ring_bits, ring_mask);
+    } else {
+      out[i] = ring_bits < 64 ? v & ring_mask : v;
+    }
   }
 }

@@ -55,6 +55,25 @@ _SIGS = {
                                c_vp, c_vp]),
     "sufhip_dcf_eval": (c_int, [c_int, c_int, c_int, c_vp, c_vp, c_sz, c_int, c_vp, c_sz, c_int,
                                 c_int, c_vp, c_vp]),
+    "sufhip_beaver_mul": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_sz,
+                                  c_vp]),
+    "sufhip_beaver_mul_aos": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "sufhip_trunc_shift": (c_int, [c_vp, c_vp, c_int, c_sz, c_vp]),
+    "sufhip_trunc_postproc": (c_int, [c_int, c_int, c_int, c_u64, c_u64, c_vp, c_vp, c_sz, c_int,
+                                      c_vp, c_sz, c_int, c_int, c_int, c_vp, c_sz, c_vp]),
+    "sufhip_horner_cubic": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "sufhip_add_rout_aos": (c_int, [c_vp, c_sz, c_int, c_vp, c_sz, c_vp]),
+    "sufhip_row_broadcast_mul": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_vp,
+                                         c_vp, c_sz, c_vp]),
+    "sufhip_row_sum": (c_int, [c_vp, c_int, c_int, c_vp, c_vp, c_vp]),
+    "sufhip_row_sum_ragged": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp]),
+    "sufhip_row_mean": (c_int, [c_vp, c_int, c_int, c_vp, c_vp, c_vp]),
+    "sufhip_row_variance": (c_int, [c_vp, c_vp, c_int, c_int, c_vp, c_vp, c_vp]),
+    "sufhip_unpack_eff_bits": (c_int, [c_vp, c_int, c_vp, c_sz, c_vp]),
+    "sufhip_pack_eff_bits": (c_int, [c_vp, c_int, c_vp, c_sz, c_vp]),
+    "sufhip_open_add_to_signed": (c_int, [c_vp, c_vp, c_vp, c_sz, c_int, c_u64, c_vp]),
+    "sufhip_unpack_add_to_signed": (c_int, [c_vp, c_vp, c_int, c_vp, c_sz, c_int, c_u64, c_vp]),
+    "sufhip_unpack_add_mod": (c_int, [c_vp, c_vp, c_int, c_vp, c_sz, c_int, c_u64, c_vp]),
     "sufhip_host_mt19937_64": (c_int, [c_u64, c_vp, c_sz]),
     "sufhip_host_normal_fixed": (c_int, [c_u64, c_dbl, c_dbl, c_int, c_vp, c_sz]),
 }

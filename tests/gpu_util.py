@@ -27,3 +27,18 @@ def say(msg):
     """Names the case before a GPU step (so a fault report identifies it)."""
     sys.stdout.write("[gpu-case] %s\n" % msg)
     sys.stdout.flush()
+
+
+class Pins:
+    """Keeps device tensors alive for the duration of a test step:
+    p(arr) uploads arr and returns its device address."""
+
+    def __init__(self):
+        self.held = []
+
+    def __call__(self, a):
+        if a is None:
+            return None
+        t = a if isinstance(a, torch.Tensor) else dev(a)
+        self.held.append(t)
+        return t.data_ptr()

@@ -63,6 +63,8 @@ def _load_oracle():
                                       ctypes.c_int, ctypes.c_int64, ctypes.c_int, u64p,
                                       ctypes.c_int]
     lib.orc_add_rout_aos.argtypes = [u64p, c_sz, ctypes.c_int, u64p, ctypes.c_int]
+    lib.orc_open_add.argtypes = [u64p, u64p, ctypes.c_int, u64p, c_sz, ctypes.c_int,
+                                 ctypes.c_uint64, ctypes.c_int]
     return lib
 
 
@@ -214,3 +216,106 @@ def ref_lib(group=GROUP_XOR):
         lib.ref_adapter_gen.argtypes = [ctypes.c_int, ctypes.c_uint64, u8p, c_sz, u8p, u8p, c_sz]
         _REF[group] = lib
     return _REF[group]
+
+
+# ---------------- ring postprocessing ----------------
+def _u64(a):
+    return np.ascontiguousarray(a, dtype=np.uint64)
+
+
+def beaver_mul(party, a, b, c, d, e):
+    out = np.zeros(len(a), dtype=np.uint64)
+    LIB.orc_beaver_mul(party, *(ptr(_u64(v), u64p) for v in (a, b, c, d, e)), ptr(out, u64p),
+                       c_sz(len(a)))
+    return out
+
+
+def trunc_postproc(party, gapars, f, r_hi, m, hatx, arith, arith_stride, arith_idx, bools,
+                   bool_stride, carry_idx, sign_idx, wrap_idx, n):
+    out = np.zeros(n, dtype=np.uint64)
+    LIB.orc_trunc_postproc(party, gapars, f, int(r_hi), int(m),
+                           ptr(_u64(hatx), u64p) if hatx is not None else None,
+                           ptr(_u64(arith), u64p), arith_stride, arith_idx,
+                           ptr(_u64(bools), u64p) if bools is not None else None, bool_stride,
+                           carry_idx, sign_idx, wrap_idx, ptr(out, u64p), n)
+    return out
+
+
+def horner(x, c0, c1, c2, c3):
+    out = np.zeros(len(x), dtype=np.uint64)
+    LIB.orc_horner_cubic(*(ptr(_u64(v), u64p) for v in (x, c0, c1, c2, c3)), ptr(out, u64p),
+                         c_sz(len(x)))
+    return out
+
+
+def add_rout_aos(out, elems, out_words, r_out):
+    out = _u64(out).copy()
+    r = _u64(r_out)
+    LIB.orc_add_rout_aos(ptr(out, u64p), elems, out_words, ptr(r, u64p), len(r))
+    return out
+
+
+def row_broadcast_mul(party, A, B_rows, C, d, e_rows, rows, cols, valid_lens=None):
+    out = np.zeros(rows * cols, dtype=np.uint64)
+    vl = np.ascontiguousarray(valid_lens, dtype=np.int32) if valid_lens is not None else None
+    LIB.orc_row_broadcast_mul(party, *(ptr(_u64(v), u64p) for v in (A, B_rows, C, d, e_rows)),
+                              rows, cols, ptr(vl, i32p) if vl is not None else None,
+                              ptr(out, u64p))
+    return out
+
+
+def _rows_call(fn, mat, rows, cols, valid_lens, *extra):
+    out = np.zeros(rows, dtype=np.uint64)
+    vl = np.ascontiguousarray(valid_lens, dtype=np.int32) if valid_lens is not None else None
+    args = [ptr(_u64(mat), u64p)] + [ptr(_u64(e), u64p) for e in extra]
+    fn(*args, rows, cols, ptr(vl, i32p) if vl is not None else None, ptr(out, u64p))
+    return out
+
+
+def row_sum(mat, rows, cols, valid_lens=None):
+    return _rows_call(LIB.orc_row_sum, mat, rows, cols, valid_lens)
+
+
+def row_mean(mat, rows, cols, valid_lens=None):
+    return _rows_call(LIB.orc_row_mean, mat, rows, cols, valid_lens)
+
+
+def row_variance(mat, mean, rows, cols, valid_lens=None):
+    return _rows_call(LIB.orc_row_variance, mat, rows, cols, valid_lens, mean)
+
+
+def row_sum_ragged(vals, offs):
+    rows = len(offs) - 1
+    out = np.zeros(rows, dtype=np.uint64)
+    o = np.ascontiguousarray(offs, dtype=np.int32)
+    LIB.orc_row_sum_ragged(ptr(_u64(vals), u64p), ptr(o, i32p), rows, ptr(out, u64p))
+    return out
+
+
+def pack_eff_bits(vals, eff_bits):
+    n = len(vals)
+    words = (n * eff_bits + 63) // 64
+    out = np.zeros(max(words, 1), dtype=np.uint64)
+    LIB.orc_pack_eff_bits(ptr(_u64(vals), u64p), eff_bits, ptr(out, u64p), c_sz(n))
+    return out[:words]
+
+
+def unpack_eff_bits(packed, eff_bits, n):
+    out = np.zeros(n, dtype=np.uint64)
+    LIB.orc_unpack_eff_bits(ptr(_u64(packed), u64p), eff_bits, ptr(out, u64p), c_sz(n))
+    return out
+
+
+def open_add(local, remote, eff_bits, n, ring_bits, ring_mask, sign_extend):
+    out = np.zeros(n, dtype=np.uint64)
+    LIB.orc_open_add(ptr(_u64(local), u64p), ptr(_u64(remote), u64p), eff_bits, ptr(out, u64p),
+                     c_sz(n), ring_bits, ctypes.c_uint64(ring_mask), sign_extend)
+    return out
+
+
+def beaver_matmul(party, D, E, A, B, C, batches, M, K, N, w_t=0, has_scale=0, mul_const=0,
+                  mul_shift=0, threads=8):
+    out = np.zeros(batches * M * N, dtype=np.uint64)
+    LIB.orc_beaver_matmul(party, *(ptr(_u64(v), u64p) for v in (D, E, A, B, C)), batches, M, K, N,
+                          w_t, has_scale, mul_const, mul_shift, ptr(out, u64p), threads)
+    return out
