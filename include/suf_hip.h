@@ -133,6 +133,42 @@ int sufhip_dcf_eval(int group, int in_bits, int payload_len, const uint8_t* prg_
                     void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* Interval LUT and packed compare in the reference GPU blob formats        */
+/* (cuda/pfss_backend_gpu.cu:75-94, 189-288), evaluated with the kernel     */
+/* counter convention of cuda/pfss_kernels.cu:240-719.  They replace        */
+/* GpuPfssBackend::eval_interval_lut_many_device[_broadcast] and            */
+/* eval_packed_lt_many_device[_broadcast] (PfssGpuStagedEval,               */
+/* include/proto/backend_gpu.hpp:176-201) and PfssIntervalLutExt::          */
+/* eval_interval_lut_many_u64 / PackedLtBackend::eval_packed_lt_many        */
+/* (pfss_interval_lut_ext.hpp:17-27, packed_backend.hpp:15-23).             */
+/* Keys are device blobs: [N][key_bytes] or one blob (key_broadcast = 1),   */
+/* 8-byte aligned; key_bytes must equal the *_key_bytes() of the stated     */
+/* geometry.  Outputs are u64 [N][out_words].                               */
+/* ---------------------------------------------------------------------- */
+/* seed_from_id (cuda/pfss_backend_gpu.cu:189-194): 16 bytes, byte i = low
+ * byte of the i-th output of std::mt19937_64(id ^ tweak * 0x9e3779b97f4a7c15). */
+void sufhip_seed_from_id(uint64_t id, uint64_t tweak, uint8_t* seed16);
+size_t sufhip_interval_lut_key_bytes(int intervals, int out_words);
+/* Host: one party's LUT blob (build_interval_key, pfss_backend_gpu.cu:223-255).
+ * cuts [intervals + 1], payload [intervals][out_words]. */
+int sufhip_interval_lut_build_key(int party, uint64_t nonce, int in_bits, int out_words,
+                                  const uint64_t* cuts, int intervals, const uint64_t* payload,
+                                  const uint8_t* seed16, uint8_t* blob);
+int sufhip_interval_lut_eval(const uint8_t* d_keys, size_t key_bytes, int key_broadcast,
+                             int intervals, int out_words, const uint64_t* d_xs, size_t n,
+                             uint64_t* d_out, void* stream);
+size_t sufhip_packed_lt_key_bytes(int num_thr);
+/* Host: one party's packed-compare blob (build_packed_cmp_key,
+ * pfss_backend_gpu.cu:257-288); thresholds are stored masked to in_bits and
+ * the sorted flag is derived. */
+int sufhip_packed_lt_build_key(int party, uint64_t nonce, int in_bits, const uint64_t* thresholds,
+                               int num_thr, const uint8_t* seed16, uint8_t* blob);
+/* out_words must be ceil(num_thr / 64). */
+int sufhip_packed_lt_eval(const uint8_t* d_keys, size_t key_bytes, int key_broadcast, int num_thr,
+                          int out_words, const uint64_t* d_xs, size_t n, uint64_t* d_out,
+                          void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* Ring postprocessing, Beaver products, row reductions and open packing.   */
 /* Each replaces the launcher of the same name in                          */
 /* include/runtime/cuda_primitives.hpp (line numbers below) with the same   */

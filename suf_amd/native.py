@@ -55,6 +55,15 @@ _SIGS = {
                                c_vp, c_vp]),
     "sufhip_dcf_eval": (c_int, [c_int, c_int, c_int, c_vp, c_vp, c_sz, c_int, c_vp, c_sz, c_int,
                                 c_int, c_vp, c_vp]),
+    "sufhip_seed_from_id": (None, [c_u64, c_u64, c_vp]),
+    "sufhip_interval_lut_key_bytes": (c_sz, [c_int, c_int]),
+    "sufhip_interval_lut_build_key": (c_int, [c_int, c_u64, c_int, c_int, c_vp, c_int, c_vp, c_vp,
+                                              c_vp]),
+    "sufhip_interval_lut_eval": (c_int, [c_vp, c_sz, c_int, c_int, c_int, c_vp, c_sz, c_vp,
+                                         c_vp]),
+    "sufhip_packed_lt_key_bytes": (c_sz, [c_int]),
+    "sufhip_packed_lt_build_key": (c_int, [c_int, c_u64, c_int, c_vp, c_int, c_vp, c_vp]),
+    "sufhip_packed_lt_eval": (c_int, [c_vp, c_sz, c_int, c_int, c_int, c_vp, c_sz, c_vp, c_vp]),
     "sufhip_beaver_mul": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_sz,
                                   c_vp]),
     "sufhip_beaver_mul_aos": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]),
