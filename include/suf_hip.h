@@ -215,6 +215,22 @@ int sufhip_row_sum(const uint64_t* d_mat, int rows, int cols, const int* d_valid
 /* launch_row_sum_ragged_kernel (:117-121). */
 int sufhip_row_sum_ragged(const uint64_t* d_vals, const int* d_row_offsets, int rows,
                           uint64_t* d_out_rows, void* stream);
+/* launch_beaver_matmul2d_kernel (:133-147): out = C + D*B + A*E (+ D*E for
+ * party 0) mod 2^64; A, D [M x K]; B, E [K x N] (or [N x K] when
+ * w_transposed); C, out [M x N]; optional (out * mul_const) >> mul_shift on the
+ * signed 128-bit product when has_scale. */
+int sufhip_beaver_matmul2d(int party, const uint64_t* d_D_open, const uint64_t* d_E_open,
+                           const uint64_t* d_A_tri_share, const uint64_t* d_B_tri_share,
+                           const uint64_t* d_C_tri_share, int M, int K, int N, int w_transposed,
+                           int has_scale, int64_t mul_const, int mul_shift, uint64_t* d_out,
+                           void* stream);
+/* launch_beaver_matmul2d_batched_kernel (:151-166): D [batches][M x K],
+ * E [batches][K x N]; the same A, B, C for every batch; out [batches][M x N]. */
+int sufhip_beaver_matmul2d_batched(int party, const uint64_t* d_D_open, const uint64_t* d_E_open,
+                                   const uint64_t* d_A_tri_share, const uint64_t* d_B_tri_share,
+                                   const uint64_t* d_C_tri_share, int batches, int M, int K, int N,
+                                   int w_transposed, int has_scale, int64_t mul_const,
+                                   int mul_shift, uint64_t* d_out, void* stream);
 /* launch_row_mean_kernel (:169-174): sum >> log2(L) for power-of-two L, else
  * the u64 sum divided by L as a plain integer (the reference's formula). */
 int sufhip_row_mean(const uint64_t* d_mat, int rows, int cols, const int* d_valid_lens,

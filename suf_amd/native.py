@@ -74,6 +74,11 @@ _SIGS = {
     "sufhip_add_rout_aos": (c_int, [c_vp, c_sz, c_int, c_vp, c_sz, c_vp]),
     "sufhip_row_broadcast_mul": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_vp,
                                          c_vp, c_sz, c_vp]),
+    "sufhip_beaver_matmul2d": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int,
+                                       c_int, c_int, c_i64, c_int, c_vp, c_vp]),
+    "sufhip_beaver_matmul2d_batched": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int,
+                                               c_int, c_int, c_int, c_int, c_i64, c_int, c_vp,
+                                               c_vp]),
     "sufhip_row_sum": (c_int, [c_vp, c_int, c_int, c_vp, c_vp, c_vp]),
     "sufhip_row_sum_ragged": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp]),
     "sufhip_row_mean": (c_int, [c_vp, c_int, c_int, c_vp, c_vp, c_vp]),
