@@ -93,12 +93,41 @@ def build(if_stale=False, jobs=None):
     return LIB
 
 
+HOST_SRC = os.path.join(PKG, "host")
+CPP_TESTS = os.path.join(ROOT, "tests", "cpp")
+CPP_TEST_OUT = os.path.join(CPP_TESTS, "_build")
+
+
+def build_host_tests():
+    """Compiles the C++ proto-interface backend (suf_amd/host) into each C++
+    test driver under tests/cpp, linked against libsuf_hip.so (g++, no HIP
+    headers: the backend reaches the GPU only through the C ABI)."""
+    os.makedirs(CPP_TEST_OUT, exist_ok=True)
+    host = sorted(glob.glob(os.path.join(HOST_SRC, "*.cpp")))
+    outs = []
+    for t in sorted(glob.glob(os.path.join(CPP_TESTS, "*.cpp"))):
+        exe = os.path.join(CPP_TEST_OUT, os.path.splitext(os.path.basename(t))[0])
+        rel = os.path.relpath(LIBDIR, CPP_TEST_OUT)
+        cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-Wextra", "-pthread",
+               "-I" + os.path.join(ROOT, "include"), t] + host + [
+               "-L" + LIBDIR, "-lsuf_hip", "-Wl,-rpath,$ORIGIN/" + rel,
+               "-Wl,-rpath-link,/opt/rocm/lib", "-o", exe + ".tmp"]
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+        if r.returncode != 0:
+            raise RuntimeError("g++ failed for %s:\n%s" % (os.path.basename(t), r.stdout))
+        os.replace(exe + ".tmp", exe)
+        outs.append(exe)
+    return outs
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--if-stale", action="store_true")
     ap.add_argument("-j", type=int, default=None)
     a = ap.parse_args()
     print(build(if_stale=a.if_stale, jobs=a.j))
+    for exe in build_host_tests():
+        print(exe)
 
 
 if __name__ == "__main__":

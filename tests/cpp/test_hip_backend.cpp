@@ -1,0 +1,237 @@
+// Two-party test of HipPfssBackend through the SUF proto interfaces, in the
+// style of the reference's in-process tests (src/demo/test_pfss_gpu.cpp,
+// test_cuda_packed_pfss.cpp): a dealer instance generates keys, one instance
+// per party evaluates on its own thread, and the shares must reconstruct the
+// closed forms (1[x < alpha], the LUT row, the threshold bitmask).
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <random>
+#include <stdexcept>
+#include <thread>
+#include <vector>
+
+#include "suf_hip.h"
+#include "suf_hip/hip_pfss_backend.hpp"
+
+using suf_hip::HipPfssBackend;
+
+static int g_fail = 0;
+#define CHECK(cond, ...)                   \
+  do {                                     \
+    if (!(cond)) {                         \
+      std::fprintf(stderr, __VA_ARGS__);   \
+      std::fprintf(stderr, "\n");          \
+      ++g_fail;                            \
+      return;                              \
+    }                                      \
+  } while (0)
+
+// Runs f(party, backend) for both parties concurrently.
+static void two_parties(const std::function<void(int, HipPfssBackend&)>& f) {
+  HipPfssBackend b0, b1;
+  std::thread t0([&] { f(0, b0); });
+  std::thread t1([&] { f(1, b1); });
+  t0.join();
+  t1.join();
+}
+
+static std::vector<uint8_t> flatten(const proto::FssKey& k, size_t n) {
+  std::vector<uint8_t> v(k.bytes.size() * n);
+  for (size_t i = 0; i < n; ++i) std::memcpy(v.data() + i * k.bytes.size(), k.bytes.data(), k.bytes.size());
+  return v;
+}
+
+static void test_dcf(int in_bits, size_t payload_len) {
+  HipPfssBackend::Params dp;
+  dp.seed = 99 + payload_len;
+  HipPfssBackend dealer(dp);
+  std::mt19937_64 rng(in_bits * 131 + payload_len);
+  const uint64_t mask = in_bits == 64 ? ~0ull : ((1ull << in_bits) - 1);
+  const size_t nkeys = 40, per = 5, n = nkeys * per;
+  std::vector<uint8_t> payload(payload_len, 0);
+  payload[0] = 1;  // XorBytes {1} or pack_u64_le(1) (AddU64)
+  std::vector<proto::DcfKeyPair> keys;
+  std::vector<uint64_t> alphas, xs;
+  for (size_t k = 0; k < nkeys; ++k) {
+    uint64_t a = rng() & mask;
+    alphas.push_back(a);
+    keys.push_back(dealer.gen_dcf(in_bits, dealer.u64_to_bits_msb(a, in_bits), payload));
+    for (size_t d = 0; d < per; ++d) xs.push_back((a + d - 2) & mask);
+  }
+  const size_t kb = keys[0].k0.bytes.size();
+  const int ob = payload_len == 1 ? 1 : 8;
+  std::vector<uint8_t> outs[2], single[2];
+  two_parties([&](int p, HipPfssBackend& be) {
+    std::vector<uint8_t> flat(kb * n);
+    for (size_t i = 0; i < n; ++i) {
+      const auto& k = p ? keys[i / per].k1 : keys[i / per].k0;
+      std::memcpy(flat.data() + i * kb, k.bytes.data(), kb);
+    }
+    outs[p].assign(n * ob, 0);
+    be.eval_dcf_many_u64(in_bits, kb, flat.data(), xs, ob, outs[p].data());
+    const auto& k0 = p ? keys[0].k1 : keys[0].k0;
+    single[p] = be.eval_dcf(in_bits, k0, be.u64_to_bits_msb(xs[0], in_bits));
+  });
+  for (size_t i = 0; i < n; ++i) {
+    const uint64_t lt = xs[i] < alphas[i / per];
+    uint64_t rec;
+    if (payload_len == 1) {
+      rec = (outs[0][i] ^ outs[1][i]) & 1;
+    } else {
+      uint64_t a, b;
+      std::memcpy(&a, &outs[0][i * 8], 8);
+      std::memcpy(&b, &outs[1][i * 8], 8);
+      rec = a + b;
+    }
+    CHECK(rec == lt, "dcf in_bits=%d plen=%zu i=%zu rec=%llu exp=%llu", in_bits, payload_len, i,
+          (unsigned long long)rec, (unsigned long long)lt);
+  }
+  CHECK(single[0].size() == payload_len, "eval_dcf returns payload_len bytes");
+}
+
+static void test_dcf_device_broadcast() {
+  HipPfssBackend dealer;
+  const uint64_t alpha = 0x8000000000001234ull;
+  auto kp = dealer.gen_dcf(64, dealer.u64_to_bits_msb(alpha, 64), std::vector<uint8_t>{1});
+  const size_t n = 10000;
+  std::vector<uint64_t> xs(n);
+  std::mt19937_64 rng(5);
+  for (auto& x : xs) x = rng();
+  xs[0] = alpha - 1;
+  xs[1] = alpha;
+  std::vector<uint8_t> outs[2];
+  two_parties([&](int p, HipPfssBackend& be) {
+    void* d = nullptr;
+    if (sufhip_malloc(&d, n * 8) || sufhip_memcpy_h2d(d, xs.data(), n * 8, nullptr) ||
+        sufhip_stream_synchronize(nullptr))
+      throw std::runtime_error("staging xs");
+    const auto& k = p ? kp.k1 : kp.k0;
+    outs[p].assign(n, 0);
+    be.eval_dcf_many_u64_device_broadcast(64, k.bytes.size(), k.bytes.data(),
+                                          static_cast<const uint64_t*>(d), n, 1, outs[p].data());
+    // device-only call keeps the result in last_device_bools()
+    be.eval_dcf_many_u64_device_broadcast(64, k.bytes.size(), k.bytes.data(),
+                                          static_cast<const uint64_t*>(d), n, 1, nullptr);
+    std::vector<uint8_t> dev(n);
+    if (sufhip_memcpy_d2h(dev.data(), be.last_device_bools(), n, nullptr) ||
+        sufhip_stream_synchronize(nullptr))
+      throw std::runtime_error("reading last_device_bools");
+    if (dev != outs[p]) throw std::runtime_error("last_device_bools differs from host output");
+    sufhip_free(d);
+  });
+  for (size_t i = 0; i < n; ++i)
+    CHECK(uint64_t((outs[0][i] ^ outs[1][i]) & 1) == uint64_t(xs[i] < alpha), "bcast dcf i=%zu", i);
+}
+
+static void test_lut() {
+  HipPfssBackend dealer;
+  proto::IntervalLutDesc desc;
+  desc.in_bits = 6;
+  desc.out_words = 2;
+  desc.cutpoints = {0, 20, 40, 64};
+  desc.payload_flat = {100, 200, 300, 400, 500, 600};
+  auto kp = dealer.gen_interval_lut(desc);
+  std::vector<uint64_t> xs = {0, 25, 50, 19, 20, 63};
+  std::vector<uint64_t> outs[2], bouts[2];
+  two_parties([&](int p, HipPfssBackend& be) {
+    const auto& k = p ? kp.k1 : kp.k0;
+    auto flat = flatten(k, xs.size());
+    outs[p].assign(xs.size() * 2, 0);
+    be.eval_interval_lut_many_u64(k.bytes.size(), flat.data(), xs, 2, outs[p].data());
+    void* d = nullptr;
+    if (sufhip_malloc(&d, xs.size() * 8) ||
+        sufhip_memcpy_h2d(d, xs.data(), xs.size() * 8, nullptr) ||
+        sufhip_stream_synchronize(nullptr))
+      throw std::runtime_error("staging xs");
+    bouts[p].assign(xs.size() * 2, 0);
+    be.eval_interval_lut_many_device_broadcast(k.bytes.size(), k.bytes.data(),
+                                               static_cast<const uint64_t*>(d), xs.size(), 2,
+                                               bouts[p].data());
+    sufhip_free(d);
+  });
+  for (size_t i = 0; i < xs.size(); ++i) {
+    const size_t iv = xs[i] < 20 ? 0 : (xs[i] < 40 ? 1 : 2);
+    for (int w = 0; w < 2; ++w) {
+      CHECK(outs[0][i * 2 + w] + outs[1][i * 2 + w] == desc.payload_flat[iv * 2 + w], "lut i=%zu", i);
+      CHECK(bouts[0][i * 2 + w] + bouts[1][i * 2 + w] == desc.payload_flat[iv * 2 + w],
+            "lut bcast i=%zu", i);
+    }
+  }
+}
+
+static void test_packed() {
+  HipPfssBackend dealer;
+  std::vector<uint64_t> thr = {5, 12, 33, 48, 60};
+  auto kp = dealer.gen_packed_lt(6, thr);
+  std::vector<uint64_t> xs = {0, 15, 63, 33, 4};
+  std::vector<uint64_t> outs[2];
+  two_parties([&](int p, HipPfssBackend& be) {
+    const auto& k = p ? kp.k1 : kp.k0;
+    auto flat = flatten(k, xs.size());
+    outs[p].assign(xs.size(), 0);
+    be.eval_packed_lt_many(k.bytes.size(), flat.data(), xs, 6, 1, outs[p].data());
+  });
+  for (size_t i = 0; i < xs.size(); ++i) {
+    uint64_t exp = 0;
+    for (size_t j = 0; j < thr.size(); ++j) exp |= uint64_t(xs[i] < thr[j]) << j;
+    CHECK((outs[0][i] ^ outs[1][i]) == exp, "packed i=%zu", i);
+  }
+}
+
+static void test_errors() {
+  HipPfssBackend be;
+  bool threw = false;
+  try {
+    be.gen_dcf(65, std::vector<uint8_t>(65, 0), std::vector<uint8_t>{1});
+  } catch (const std::runtime_error&) {
+    threw = true;
+  }
+  CHECK(threw, "gen_dcf(in_bits=65) must throw");
+  threw = false;
+  try {
+    std::vector<uint8_t> junk(100, 0);
+    be.eval_dcf_many_u64(64, junk.size(), junk.data(), std::vector<uint64_t>{1}, 1, junk.data());
+  } catch (const std::runtime_error&) {
+    threw = true;
+  }
+  CHECK(threw, "eval on a malformed key must throw");
+}
+
+static void test_factory() {
+  setenv("SUF_PFSS_BACKEND", "HIP", 1);
+  auto be = suf_hip::make_hip_backend_from_env();
+  CHECK(be != nullptr, "SUF_PFSS_BACKEND=hip must select the HIP backend");
+  CHECK(dynamic_cast<proto::PfssGpuStagedEval*>(be.get()) != nullptr, "staged-eval capability");
+  CHECK(dynamic_cast<proto::PackedLtBackend*>(be.get()) != nullptr, "packed capability");
+  setenv("SUF_PFSS_BACKEND", "cpu", 1);
+  CHECK(suf_hip::make_hip_backend_from_env() == nullptr, "other kinds are not ours");
+}
+
+int main() {
+  uint8_t state[128];
+  std::mt19937_64 g(3);
+  for (auto& b : state) b = uint8_t(g() & 0xFF);
+  HipPfssBackend::set_prg_state(state);
+  try {
+    test_dcf(64, 1);
+    test_dcf(64, 8);
+    test_dcf(12, 8);
+    test_dcf(16, 1);
+    test_dcf_device_broadcast();
+    test_lut();
+    test_packed();
+    test_errors();
+    test_factory();
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "exception: %s\n", e.what());
+    return 2;
+  }
+  if (g_fail) {
+    std::fprintf(stderr, "%d check(s) failed\n", g_fail);
+    return 1;
+  }
+  std::printf("hip backend two-party test passed\n");
+  return 0;
+}
