@@ -25,6 +25,11 @@ sys.path.insert(0, ROOT)
 
 METRIC = "64-bit DCF evals/sec (2 parties, N=2^20) + secure layer latency ms, 1 MI355X"
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per dcf_eval_bit_kernel launch at N = 2^20, measured with
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch) and scaled by the
+# counters' reading for a 256 MiB device copy (FETCH x2.0, WRITE x1.0); the
+# commands and raw values are in profiles/dcf_eval_bit_kernel__dcf_batch_n2p20.md.
+MEASURED_TRAFFIC_BYTES = 1258342 * 1024 * 2.0 + 1110.5 * 1024 * 1.0
 VALU_PEAK_GOPS = 256 * 64 * 2.4  # 256 CUs x 64 lanes x 2.4 GHz, 32-bit integer ops
 
 
@@ -216,7 +221,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved_gbps / HBM_PEAK_GBPS,
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC_BYTES if n == 1 << 20 else None,
             "kernel": "dcf_eval_bit_kernel",
             "kernel_ms": kern_ms,
             "bytes_per_launch": key_bytes_per_launch,
