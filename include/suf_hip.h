@@ -133,6 +133,49 @@ int sufhip_dcf_eval(int group, int in_bits, int payload_len, const uint8_t* prg_
                     void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* Truncation gate (one instance, scalar input mask r), both halves of SUF's */
+/* trunc pipeline: keygen composite_gen_trunc_gate                           */
+/* (include/gates/composite_fss.hpp:645-833) and the online evaluation that  */
+/* SUF runs as composite_eval_batch_backend's AddU64 branch                  */
+/* (composite_fss.hpp:1385-1638) followed by the trunc postproc hook         */
+/* (include/gates/postproc_hooks.hpp:172-373; launch_trunc_postproc_kernel,  */
+/* include/runtime/cuda_primitives.hpp:47-63).                               */
+/* Keys are device blobs (8-byte aligned): a 64-byte header (tag "STG1",     */
+/* kind, frac_bits, party, key flags, shares of r_in, r_hi, r_out, the       */
+/* carry / sign rotation bits and GapARS's m) followed by the f-bit carry    */
+/* DCF key and, for TR / ARS, the 64-bit wrap (and ARS sign) DCF keys, all   */
+/* in the myl7 adapter format with an 8-byte additive payload.               */
+/* ---------------------------------------------------------------------- */
+#define SUFHIP_TRUNC_TR 0     /* GateKind::FaithfulTR  */
+#define SUFHIP_TRUNC_ARS 1    /* GateKind::FaithfulARS */
+#define SUFHIP_TRUNC_GAPARS 2 /* GateKind::GapARS      */
+#define SUFHIP_TRUNC_RAND_WORDS 19
+
+/* 0 for an unknown kind or frac_bits outside [1, 62]. */
+size_t sufhip_trunc_key_bytes(int kind, int frac_bits);
+
+/* Dealer: both parties' keys for one gate.  rnd: SUFHIP_TRUNC_RAND_WORDS
+ * host u64 words at fixed positions: 0 r | 1 r_in split | 2 r_out split |
+ * 3 carry-rotation split | 4 sign-rotation split | 5 r_hi split | 6 m split |
+ * 7..10, 11..14, 15..18 seeds of the carry, wrap and sign DCF keys (party-0
+ * seed = words 0,1 LE; party-1 seed = words 2,3).  A split of v gives party 0
+ * the word s and party 1 v - s.  Writes d_key0, d_key1
+ * [sufhip_trunc_key_bytes(kind, frac_bits)]. */
+int sufhip_trunc_gen(int kind, int frac_bits, const uint8_t* prg_state, const uint64_t* rnd,
+                     uint8_t* d_key0, uint8_t* d_key1, void* stream);
+
+/* Device workspace sufhip_trunc_eval needs for N points (0 = none). */
+size_t sufhip_trunc_work_bytes(int frac_bits, size_t n);
+
+/* One party: d_y[i] = this party's share of trunc(x_i) given the public
+ * d_xhat[i] = x_i + r.  kind / frac_bits must be the ones the key was made
+ * with; the party is read from the key.  d_work: >= sufhip_trunc_work_bytes
+ * bytes, 16-byte aligned, clobbered. */
+int sufhip_trunc_eval(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,
+                      size_t key_bytes, const uint64_t* d_xhat, size_t n, uint64_t* d_y,
+                      void* d_work, size_t work_bytes, void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* Interval LUT and packed compare in the reference GPU blob formats        */
 /* (cuda/pfss_backend_gpu.cu:75-94, 189-288), evaluated with the kernel     */
 /* counter convention of cuda/pfss_kernels.cu:240-719.  They replace        */

@@ -18,6 +18,10 @@
  *     std::mt19937_64 (10000th output of the default seed).
  *   - trunc / Beaver / Horner / row reductions: __int128 closed forms
  *     (x >> f, X*W mod 2^64, ...) in tests/test_oracle_*.py.
+ *   - truncation gate (gates.c): two-party reconstruction equals x >> f
+ *     (TR), the arithmetic shift (ARS) and the gap shift (GapARS) over
+ *     random and edge-case inputs and masks; DCF keys via the pinned myl7
+ *     functions above.
  */
 #ifndef SUF_ORACLE_H
 #define SUF_ORACLE_H
@@ -126,6 +130,17 @@ void orc_open_add(const uint64_t* local, const uint64_t* remote, int eff_bits, u
                   size_t n, int ring_bits, uint64_t ring_mask, int sign_extend);
 void orc_pack_eff_bits(const uint64_t* in, int eff_bits, uint64_t* packed, size_t n);
 void orc_unpack_eff_bits(const uint64_t* packed, int eff_bits, uint64_t* out, size_t n);
+
+/* ---------------- truncation gate (oracle/gates.c) ---------------- */
+#define ORC_TRUNC_TR 0     /* GateKind::FaithfulTR  */
+#define ORC_TRUNC_ARS 1    /* GateKind::FaithfulARS */
+#define ORC_TRUNC_GAPARS 2 /* GateKind::GapARS      */
+#define ORC_TRUNC_RAND_WORDS 19
+size_t orc_trunc_key_bytes(int kind, int frac_bits);
+int orc_trunc_gen(const orc_prg_state* p, int kind, int frac_bits, const uint64_t* rnd,
+                  uint8_t* key0, uint8_t* key1);
+int orc_trunc_eval(const orc_prg_state* p, int kind, int frac_bits, const uint8_t* key,
+                   const uint64_t* xhat, size_t n, uint64_t* y);
 
 #ifdef __cplusplus
 }

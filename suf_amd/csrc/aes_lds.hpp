@@ -223,51 +223,38 @@ __device__ __forceinline__ void fill_round_keys(uint4* lds, const uint32_t (*rk)
 }
 
 // ---------------------------------------------------------------------------
-// Two-table variant for the DCF hot loop.
-//
-// LDS holds T0 = T and T2 = rotl16(T), each replicated 64 ways (64 KB each;
-// T2 starts at byte 65536).  Entry e, copy c of table j sits at byte address
-// j * 65536 + e * 256 + c * 4, so a lookup address is assembled with one
-// v_perm_b32 from the state word (byte k -> address byte 1) and a per-lane
-// register holding c * 4 in byte 0 and j in byte 2.  With
-// T1 = rotl8(T0) and T3 = rotl8(T2), an output column is
-//   T0[a] ^ T2[c] ^ rotl8(T0[b] ^ T2[d] ^ rotr8(k)),
-// i.e. one rotate per column once round keys 1..9 are stored pre-rotated by
-// rotr8 (AesLds2Keys).  The final round reads S-box bytes straight out of
-// T0 (bytes 1, 2) and T2 (bytes 0, 3).  Every lane reads only its own copy,
-// so the 64 lanes of a wave touch 64 distinct banks.
-struct AesLds2 {
-  static constexpr int kCopies = 64;
-  static constexpr int kWordsPerTable = 256 * kCopies;
-  static constexpr int kBytes = 2 * kWordsPerTable * 4;
-  const uint32_t* lds;  // base of the two tables
-  uint32_t lane_t0;     // lane * 4
-  uint32_t lane_t2;     // lane * 4 | 0x10000
+// Four-table variant: T0..T3 = rotl(8j)(T), each replicated 32 ways.  LDS
+// banks serve a wave64 read as two 32-lane halves, so lane l reading copy
+// l % 32 is conflict-free.  Two tables share each 64 KB half:
+//   byte address = (j >> 1) * 65536 + e * 256 + (j & 1) * 128 + c * 4,
+// so a lookup is still one v_perm_b32 from the state word and a per-lane
+// base, and a column is T0[a] ^ T1[b] ^ T2[c] ^ T3[d] ^ k -- two 3-input
+// XORs, no rotates, round keys in plain FIPS-197 order.
+struct AesLds4 {
+  static constexpr int kCopies = 32;
+  static constexpr int kWords = 4 * 256 * kCopies;  // 128 KB
+  const uint32_t* lds;
+  uint32_t base[4];  // per-lane address byte 0 / byte 2 for T0..T3
 
+  __device__ __forceinline__ static AesLds4 make(const uint32_t* lds) {
+    const uint32_t c4 = (threadIdx.x & 31u) * 4u;
+    return AesLds4{lds, {c4, c4 | 128u, c4 | 0x10000u, c4 | 0x10080u}};
+  }
   __device__ __forceinline__ static uint32_t sel(int k) {
     // byte0 <- src1 byte0, byte1 <- src0 byte k, byte2 <- src1 byte2, byte3 <- 0
     return 0x0c020000u | uint32_t(4 + k) << 8;
   }
-  __device__ __forceinline__ uint32_t ld(uint32_t byte_addr) const {
-    return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(lds) + byte_addr);
-  }
-  template <int k>
-  __device__ __forceinline__ uint32_t t0(uint32_t w) const {
-    return ld(__builtin_amdgcn_perm(w, lane_t0, sel(k)));
-  }
-  template <int k>
-  __device__ __forceinline__ uint32_t t2(uint32_t w) const {
-    return ld(__builtin_amdgcn_perm(w, lane_t2, sel(k)));
+  template <int j, int k>
+  __device__ __forceinline__ uint32_t t(uint32_t w) const {
+    const uint32_t addr = __builtin_amdgcn_perm(w, base[j], sel(k));
+    return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(lds) + addr);
   }
   __device__ __forceinline__ static uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
     return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
   }
-  // Column from (a = s_c, b = s_{c+1}, c = s_{c+2}, d = s_{c+3}) and the
-  // rotr8-rotated round key word kr.
   __device__ __forceinline__ uint32_t col(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
-                                          uint32_t kr) const {
-    const uint32_t inner = xor3(t0<1>(b), t2<3>(d), kr);
-    return xor3(t0<0>(a), t2<2>(c), rotl32(inner, 8));
+                                          uint32_t k) const {
+    return xor3(xor3(t<0, 0>(a), t<1, 1>(b), t<2, 2>(c)), t<3, 3>(d), k);
   }
   __device__ __forceinline__ void round(uint32_t& s0, uint32_t& s1, uint32_t& s2, uint32_t& s3,
                                         const uint4 k) const {
@@ -280,13 +267,14 @@ struct AesLds2 {
     s2 = n2;
     s3 = n3;
   }
+  // Final round: S(x) is byte 0 of T3[x], byte 1 of T0[x], byte 2 of T0[x]
+  // and byte 3 of T1[x].
   __device__ __forceinline__ uint32_t last_col(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
                                                uint32_t k) const {
-    const uint32_t lo = __builtin_amdgcn_perm(t0<1>(b), t2<0>(a), 0x0c0c0500u);   // bytes 0,1
-    const uint32_t hi = __builtin_amdgcn_perm(t2<3>(d), t0<2>(c), 0x07020c0cu);   // bytes 2,3
+    const uint32_t lo = __builtin_amdgcn_perm(t<0, 1>(b), t<3, 0>(a), 0x0c0c0500u);  // bytes 0,1
+    const uint32_t hi = __builtin_amdgcn_perm(t<1, 3>(d), t<0, 2>(c), 0x07020c0cu);  // bytes 2,3
     return (lo | hi) ^ k;
   }
-  // rk: 11 rounds as uint4; rounds 1..9 pre-rotated (AesLds2Keys layout).
   __device__ __forceinline__ void encrypt(uint32_t& s0, uint32_t& s1, uint32_t& s2, uint32_t& s3,
                                           const uint4* rk) const {
     uint4 k = rk[0];
@@ -306,7 +294,6 @@ struct AesLds2 {
     s2 = o2;
     s3 = o3;
   }
-  // Byte 0 of the ciphertext only.
   __device__ __forceinline__ uint32_t encrypt_byte0(uint32_t s0, uint32_t s1, uint32_t s2,
                                                     uint32_t s3, const uint4* rk) const {
     uint4 k = rk[0];
@@ -316,30 +303,38 @@ struct AesLds2 {
     s3 ^= k.w;
 #pragma unroll
     for (int r = 1; r < 9; ++r) round(s0, s1, s2, s3, rk[r]);
-    const uint32_t k9 = rk[9].x;
-    const uint32_t k10 = rk[10].x;
-    const uint32_t c0 = col(s0, s1, s2, s3, k9);
-    return (t2<0>(c0) ^ k10) & 0xffu;
+    const uint32_t c0 = col(s0, s1, s2, s3, rk[9].x);
+    return (t<3, 0>(c0) ^ rk[10].x) & 0xffu;
+  }
+  // Ciphertext words 0 and 1 only (the final round skips columns 2 and 3).
+  __device__ __forceinline__ void encrypt_lo2(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t s3,
+                                              const uint4* rk, uint32_t& o0,
+                                              uint32_t& o1) const {
+    uint4 k = rk[0];
+    s0 ^= k.x;
+    s1 ^= k.y;
+    s2 ^= k.z;
+    s3 ^= k.w;
+#pragma unroll
+    for (int r = 1; r < 10; ++r) round(s0, s1, s2, s3, rk[r]);
+    k = rk[10];
+    o0 = last_col(s0, s1, s2, s3, k.x);
+    o1 = last_col(s1, s2, s3, s0, k.y);
+  }
+  // Cooperative fill; follow with __syncthreads().
+  __device__ __forceinline__ static void fill(uint32_t* lds, const uint32_t* tsrc) {
+    for (int i = threadIdx.x; i < kWords; i += blockDim.x) {
+      const int half = i >> 14;           // 16384 words per 64 KB half
+      const int e = (i >> 6) & 255;
+      const int j = 2 * half + ((i >> 5) & 1);
+      const uint32_t v = tsrc[e];
+      lds[i] = j == 0 ? v : rotl32(v, 8 * j);
+    }
+  }
+  static void key_layout(const uint32_t rk[44], uint32_t out[44]) {
+    for (int w = 0; w < 44; ++w) out[w] = rk[w];
   }
 };
-
-// Fills both replicated tables (AesLds2 layout).  Follow with __syncthreads().
-__device__ __forceinline__ void fill_ttable2(uint32_t* lds, const uint32_t* tsrc) {
-  for (int i = threadIdx.x; i < AesLds2::kWordsPerTable; i += blockDim.x) {
-    const uint32_t v = tsrc[i / AesLds2::kCopies];
-    lds[i] = v;
-    lds[AesLds2::kWordsPerTable + i] = rotl32(v, 16);
-  }
-}
-
-// Host: round keys in the AesLds2 layout (rounds 1..9 rotated right by 8).
-inline void aes2_key_layout(const uint32_t rk[44], uint32_t out[44]) {
-  for (int w = 0; w < 44; ++w) {
-    const int r = w / 4;
-    const uint32_t v = rk[w];
-    out[w] = (r >= 1 && r <= 9) ? ((v >> 8) | (v << 24)) : v;
-  }
-}
 
 // Cooperative fill of the replicated table from the constant T table in
 // global memory (`tsrc`, 256 words).  Must be followed by __syncthreads().

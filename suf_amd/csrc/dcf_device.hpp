@@ -1,0 +1,498 @@
+// Device building blocks of the myl7/fss v0.7.1 DCF shared by the batch
+// kernels (dcf.hip) and the truncation gate (trunc_gate.hip): AES tables,
+// correction-word loaders, the tree walks and the per-lane key writer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "aes_lds.hpp"
+#include "sufhip_internal.hpp"
+
+namespace sufhip {
+namespace {
+
+
+// One workgroup per CU: the four replicated AES tables take 128 KB of the
+// CU's 160 KB LDS.  Kernels loop over the batch in grid strides.
+#ifndef SUFHIP_DCF_BLOCK
+#define SUFHIP_DCF_BLOCK 512
+#endif
+constexpr int kDcfBlock = SUFHIP_DCF_BLOCK;
+
+// AES tables for every DCF kernel: four rotated T tables, 32 copies each.
+using DcfAes = AesLds4;
+
+struct Prg4 {
+  uint32_t rk[4][44];  // K_0..K_3: DCF uses PRG output blocks 0..3
+};
+
+struct U128 {
+  uint64_t lo, hi;
+};
+
+__device__ __forceinline__ U128 mk(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+  return U128{uint64_t(w0) | uint64_t(w1) << 32, uint64_t(w2) | uint64_t(w3) << 32};
+}
+
+constexpr uint64_t kMsbClear = 0x7fffffffffffffffull;
+
+template <int kGroup>
+__device__ __forceinline__ U128 gadd(U128 a, U128 b) {
+  if constexpr (kGroup == SUFHIP_GROUP_XOR) {
+    return U128{a.lo ^ b.lo, a.hi ^ b.hi};
+  } else {
+    uint64_t lo = a.lo + b.lo;
+    uint64_t hi = a.hi + b.hi + (lo < a.lo ? 1 : 0);
+    return U128{lo, hi & kMsbClear};
+  }
+}
+
+template <int kGroup>
+__device__ __forceinline__ U128 gneg(U128 a) {
+  if constexpr (kGroup == SUFHIP_GROUP_XOR) {
+    return a;
+  } else {
+    uint64_t lo = 0 - a.lo;
+    uint64_t hi = ~a.hi + (lo == 0 ? 1 : 0);
+    return U128{lo, hi & kMsbClear};
+  }
+}
+
+// Per-level correction word fields needed by the bit modes:
+// s_cw (16 bytes), v_cw byte 0, and the t byte (tl << 1 | tr).
+struct CwBit {
+  uint32_t s[4];
+  uint32_t v0;
+  uint32_t tb;
+};
+
+__device__ __forceinline__ CwBit load_cw_bit(const uint8_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+  const uint32_t sh = uint32_t(a & 3);
+  // Bytes [0, 17) and byte 32 of the record; words 0..4 and 8 of the aligned
+  // window always lie inside the record (it is 33 bytes, sh <= 3).
+  uint32_t r0 = q[0], r1 = q[1], r2 = q[2], r3 = q[3], r4 = q[4], r8 = q[8];
+  CwBit c;
+  c.s[0] = __builtin_amdgcn_alignbyte(r1, r0, sh);
+  c.s[1] = __builtin_amdgcn_alignbyte(r2, r1, sh);
+  c.s[2] = __builtin_amdgcn_alignbyte(r3, r2, sh);
+  c.s[3] = __builtin_amdgcn_alignbyte(r4, r3, sh);
+  c.v0 = (r4 >> (8 * sh)) & 0xffu;
+  c.tb = (r8 >> (8 * sh)) & 0xffu;
+  return c;
+}
+
+struct CwFull {
+  uint32_t s[4];
+  uint32_t v[4];
+  uint32_t tb;
+};
+
+__device__ __forceinline__ CwFull load_cw_full(const uint8_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+  const uint32_t sh = uint32_t(a & 3);
+  uint32_t r[9];
+#pragma unroll
+  for (int j = 0; j < 9; ++j) r[j] = q[j];
+  CwFull c;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    c.s[j] = __builtin_amdgcn_alignbyte(r[j + 1], r[j], sh);
+    c.v[j] = __builtin_amdgcn_alignbyte(r[j + 5], r[j + 4], sh);
+  }
+  c.tb = (r[8] >> (8 * sh)) & 0xffu;
+  return c;
+}
+
+// Reads 16 bytes at p.  When p + 16 is the end of the key (`more` false) and
+// p is not 4-byte aligned, the last sh bytes come from byte loads so that no
+// word past the key is touched.
+__device__ __forceinline__ void load16(const uint8_t* p, bool more, uint32_t (&w)[4]) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+  const uint32_t sh = uint32_t(a & 3);
+  uint32_t r0 = q[0], r1 = q[1], r2 = q[2], r3 = q[3];
+  uint32_t r4 = 0;
+  if (sh != 0) {
+    if (more) {
+      r4 = q[4];
+    } else {
+      const uint8_t* tail = reinterpret_cast<const uint8_t*>(q + 4);
+      for (uint32_t k = 0; k < sh; ++k) r4 |= uint32_t(tail[k]) << (8 * k);
+    }
+  }
+  w[0] = __builtin_amdgcn_alignbyte(r1, r0, sh);
+  w[1] = __builtin_amdgcn_alignbyte(r2, r1, sh);
+  w[2] = __builtin_amdgcn_alignbyte(r3, r2, sh);
+  w[3] = __builtin_amdgcn_alignbyte(r4, r3, sh);
+}
+
+// Bit-mode walk of one chunk: returns share byte 0 & 1.
+__device__ __forceinline__ uint32_t walk_bit(const DcfAes& aes, const uint4* rkl,
+                                             const uint8_t* chunk, int in_bits, uint64_t x,
+                                             uint32_t party) {
+  uint32_t seed[4];
+  load16(chunk, true, seed);
+  uint32_t s0 = seed[0], s1 = seed[1], s2 = seed[2], s3 = seed[3] & 0x7fffffffu;
+  uint32_t t = party;
+  uint32_t v = 0;
+  const uint8_t* cw = chunk + 16;
+  for (int i = 0; i < in_bits; ++i, cw += 33) {
+    const uint32_t xi = uint32_t(x >> (in_bits - 1 - i)) & 1u;
+    const CwBit c = load_cw_bit(cw);
+    uint32_t a0 = s0, a1 = s1, a2 = s2, a3 = s3;
+const uint4* ks = rkl + 22 * xi;  // K_{2 x_i}: next seed
+    const uint4* kv = ks + 11;         // K_{2 x_i + 1}: value block
+    aes.encrypt(a0, a1, a2, a3, ks);
+    const uint32_t vb = (aes.encrypt_byte0(s0, s1, s2, s3, kv) ^ s0) & 1u;
+    a0 ^= s0;
+    a1 ^= s1;
+    a2 ^= s2;
+    a3 ^= s3;
+    uint32_t tn = a3 >> 31;
+    a3 &= 0x7fffffffu;
+    const uint32_t tmask = 0u - t;
+    a0 ^= c.s[0] & tmask;
+    a1 ^= c.s[1] & tmask;
+    a2 ^= c.s[2] & tmask;
+    a3 ^= c.s[3] & tmask;
+    tn ^= ((xi ? c.tb : (c.tb >> 1)) & 1u) & t;
+    v ^= vb ^ (c.v0 & t & 1u);
+    s0 = a0;
+    s1 = a1;
+    s2 = a2;
+    s3 = a3;
+    t = tn;
+  }
+  uint32_t np1[4];
+  load16(cw, false, np1);
+  return (v ^ s0 ^ (np1[0] & t)) & 1u;
+}
+
+// Full-block walk of one chunk (any group): returns the 16-byte share.
+template <int kGroup>
+__device__ __forceinline__ U128 walk_full(const DcfAes& aes, const uint4* rkl,
+                                          const uint8_t* chunk, int in_bits, uint64_t x,
+                                          uint32_t party, bool more_after) {
+  uint32_t seed[4];
+  load16(chunk, true, seed);
+  uint32_t s0 = seed[0], s1 = seed[1], s2 = seed[2], s3 = seed[3] & 0x7fffffffu;
+  uint32_t t = party;
+  U128 v{0, 0};
+  const uint8_t* cw = chunk + 16;
+  for (int i = 0; i < in_bits; ++i, cw += 33) {
+    const uint32_t xi = uint32_t(x >> (in_bits - 1 - i)) & 1u;
+    const CwFull c = load_cw_full(cw);
+    const uint4* ks = rkl + 22 * xi;
+    const uint4* kv = ks + 11;
+    uint32_t a0 = s0, a1 = s1, a2 = s2, a3 = s3;
+    uint32_t b0 = s0, b1 = s1, b2 = s2, b3 = s3;
+    aes.encrypt(a0, a1, a2, a3, ks);
+    aes.encrypt(b0, b1, b2, b3, kv);
+    a0 ^= s0;
+    a1 ^= s1;
+    a2 ^= s2;
+    a3 ^= s3;
+    U128 vd = mk(b0 ^ s0, b1 ^ s1, b2 ^ s2, (b3 ^ s3) & 0x7fffffffu);
+    uint32_t tn = a3 >> 31;
+    a3 &= 0x7fffffffu;
+    if (t) {
+      a0 ^= c.s[0];
+      a1 ^= c.s[1];
+      a2 ^= c.s[2];
+      a3 ^= c.s[3];
+      tn ^= (xi ? c.tb : (c.tb >> 1)) & 1u;
+      vd = gadd<kGroup>(vd, mk(c.v[0], c.v[1], c.v[2], c.v[3]));
+    }
+    if (party) vd = gneg<kGroup>(vd);
+    v = gadd<kGroup>(v, vd);
+    s0 = a0;
+    s1 = a1;
+    s2 = a2;
+    s3 = a3;
+    t = tn;
+  }
+  uint32_t np1[4];
+  load16(cw, more_after, np1);
+  U128 s = mk(s0, s1, s2, s3);
+  if (t) s = gadd<kGroup>(s, mk(np1[0], np1[1], np1[2], np1[3]));
+  if (party) s = gneg<kGroup>(s);
+  return gadd<kGroup>(v, s);
+}
+
+// Additive-group walk that keeps only the low 64 bits of the 16-byte
+// value: + mod 2^127 and negation never carry from bit 63 upward into the
+// low word, so the low 8 bytes of the share are exact.  Used for DCF keys
+// with an 8-byte payload (SUF's AddU64 predicates).
+struct Add64State {
+  uint32_t s0, s1, s2, s3;  // seed, MSB cleared
+  uint32_t t;
+  uint64_t v;  // accumulated value, low 64 bits
+};
+
+// Correction word fields for the low-64 walk: s_cw, v_cw bytes 0..7, t byte.
+struct CwAdd64 {
+  uint32_t s[4];
+  uint64_t v;
+  uint32_t tb;
+};
+
+__device__ __forceinline__ CwAdd64 load_cw_add64(const uint8_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+  const uint32_t sh = uint32_t(a & 3);
+  // Words 0..6 and 8 of the aligned window: bytes [0, 24) and byte 32 of
+  // the 33-byte record (word 8 may reach into the next record or cw_np1,
+  // both inside the key).
+  const uint32_t r0 = q[0], r1 = q[1], r2 = q[2], r3 = q[3], r4 = q[4], r5 = q[5], r6 = q[6],
+                 r8 = q[8];
+  CwAdd64 c;
+  c.s[0] = __builtin_amdgcn_alignbyte(r1, r0, sh);
+  c.s[1] = __builtin_amdgcn_alignbyte(r2, r1, sh);
+  c.s[2] = __builtin_amdgcn_alignbyte(r3, r2, sh);
+  c.s[3] = __builtin_amdgcn_alignbyte(r4, r3, sh);
+  c.v = uint64_t(__builtin_amdgcn_alignbyte(r5, r4, sh)) |
+        uint64_t(__builtin_amdgcn_alignbyte(r6, r5, sh)) << 32;
+  c.tb = (r8 >> (8 * sh)) & 0xffu;
+  return c;
+}
+
+// State at the root of one chunk (chunk = key + 8: seed, CWs, cw_np1).
+__device__ __forceinline__ Add64State add64_root(const uint8_t* chunk, uint32_t party) {
+  uint32_t seed[4];
+  load16(chunk, true, seed);
+  return Add64State{seed[0], seed[1], seed[2], seed[3] & 0x7fffffffu, party, 0};
+}
+
+// Levels [from, to) of an in_bits-level walk at x (only bits in_bits-1-i used).
+__device__ __forceinline__ void add64_walk(const DcfAes& aes, const uint4* rkl,
+                                           const uint8_t* chunk, int in_bits, int from, int to,
+                                           uint64_t x, uint32_t party, Add64State& st) {
+  const uint8_t* cw = chunk + 16 + 33 * from;
+  for (int i = from; i < to; ++i, cw += 33) {
+    const uint32_t xi = uint32_t(x >> (in_bits - 1 - i)) & 1u;
+    const CwAdd64 c = load_cw_add64(cw);
+    const uint4* ks = rkl + 22 * xi;
+    const uint4* kv = ks + 11;
+    uint32_t a0 = st.s0, a1 = st.s1, a2 = st.s2, a3 = st.s3;
+    uint32_t b0, b1;
+    aes.encrypt(a0, a1, a2, a3, ks);
+    aes.encrypt_lo2(st.s0, st.s1, st.s2, st.s3, kv, b0, b1);
+    uint64_t vd = uint64_t(b0 ^ st.s0) | uint64_t(b1 ^ st.s1) << 32;
+    a0 ^= st.s0;
+    a1 ^= st.s1;
+    a2 ^= st.s2;
+    a3 ^= st.s3;
+    uint32_t tn = a3 >> 31;
+    a3 &= 0x7fffffffu;
+    if (st.t) {
+      a0 ^= c.s[0];
+      a1 ^= c.s[1];
+      a2 ^= c.s[2];
+      a3 ^= c.s[3];
+      tn ^= (xi ? c.tb : (c.tb >> 1)) & 1u;
+      vd += c.v;
+    }
+    st.v += party ? 0 - vd : vd;
+    st.s0 = a0;
+    st.s1 = a1;
+    st.s2 = a2;
+    st.s3 = a3;
+    st.t = tn;
+  }
+}
+
+// Share after the last level: v + (-1)^party (s + t * cw_np1), low 64 bits.
+__device__ __forceinline__ uint64_t add64_finish(const uint8_t* chunk, int in_bits,
+                                                 uint32_t party, const Add64State& st) {
+  uint32_t np1[4];
+  load16(chunk + 16 + 33 * in_bits, false, np1);
+  uint64_t s = uint64_t(st.s0) | uint64_t(st.s1) << 32;
+  if (st.t) s += uint64_t(np1[0]) | uint64_t(np1[1]) << 32;
+  return st.v + (party ? 0 - s : s);
+}
+
+// Stages the replicated tables and the K_0..K_3 round keys in LDS.
+#define SUFHIP_DCF_LDS_SETUP(PRG)                                  \
+  __shared__ uint32_t tabs[DcfAes::kWords];                        \
+  __shared__ uint4 rkl[4 * 11];                                    \
+  DcfAes::fill(tabs, kTDev.v);                                     \
+  fill_round_keys(rkl, (PRG).rk, 4);                               \
+  __syncthreads();                                                 \
+  const DcfAes aes = DcfAes::make(tabs)
+
+// Sequential little-endian byte writer: stores aligned dwords where it can
+// and single bytes at unaligned edges, so lanes writing neighbouring keys
+// never touch each other's bytes.
+struct ByteWriter {
+  uint8_t* p;
+  uint64_t acc;
+  int n;
+  __device__ __forceinline__ void drain() {
+    while (n > 0) {
+      if ((reinterpret_cast<uintptr_t>(p) & 3) == 0) {
+        if (n < 4) break;
+        *reinterpret_cast<uint32_t*>(p) = uint32_t(acc);
+        p += 4;
+        acc >>= 32;
+        n -= 4;
+      } else {
+        *p = uint8_t(acc);
+        ++p;
+        acc >>= 8;
+        --n;
+      }
+    }
+  }
+  __device__ __forceinline__ void put8(uint32_t b) {
+    acc |= uint64_t(b & 0xffu) << (8 * n);
+    ++n;
+    drain();
+  }
+  __device__ __forceinline__ void put32(uint32_t w) {
+    acc |= uint64_t(w) << (8 * n);
+    n += 4;
+    drain();
+  }
+  __device__ __forceinline__ void flush() {
+    while (n > 0) {
+      *p = uint8_t(acc);
+      ++p;
+      acc >>= 8;
+      --n;
+    }
+  }
+};
+
+__device__ __forceinline__ void prg4(const DcfAes& aes, const uint4* rkl, const U128& s,
+                                     U128 (&o)[4]) {
+  const uint32_t w0 = uint32_t(s.lo), w1 = uint32_t(s.lo >> 32), w2 = uint32_t(s.hi),
+                 w3 = uint32_t(s.hi >> 32);
+  // One block at a time keeps the dealer kernel inside the register budget.
+#pragma unroll 1
+  for (int j = 0; j < 4; ++j) {
+    uint32_t a0 = w0, a1 = w1, a2 = w2, a3 = w3;
+    aes.encrypt(a0, a1, a2, a3, rkl + 11 * j);
+    o[j] = mk(a0 ^ w0, a1 ^ w1, a2 ^ w2, a3 ^ w3);
+  }
+}
+
+__device__ __forceinline__ void put128(ByteWriter& w, U128 v) {
+  w.put32(uint32_t(v.lo));
+  w.put32(uint32_t(v.lo >> 32));
+  w.put32(uint32_t(v.hi));
+  w.put32(uint32_t(v.hi >> 32));
+}
+
+// One DCF key pair for f(x) = beta * 1[x < alpha] (myl7 dcf_gen,
+// third_party/myl7_fss/src/dcf.c:42-142), written in the adapter layout
+// (include/proto/myl7_fss_backend.hpp:156-210).  seeds: [chunks][32]
+// (party-0 seed, party-1 seed).
+template <int kGroup>
+__device__ __forceinline__ void gen_key(const DcfAes& aes, const uint4* rkl, int nb, int chunks,
+                                        int payload_len, uint64_t alpha, const uint8_t* pay,
+                                        const uint8_t* seeds, uint8_t* out0, uint8_t* out1) {
+  if (nb < 64) alpha &= (uint64_t(1) << nb) - 1;
+  ByteWriter w0{out0, 0, 0};
+  ByteWriter w1{out1, 0, 0};
+  const uint32_t plen = uint32_t(payload_len);
+  w0.put32(uint32_t(nb) | uint32_t(chunks) << 8 | 0u << 16);
+  w1.put32(uint32_t(nb) | uint32_t(chunks) << 8 | 1u << 16);
+  w0.put32(plen);
+  w1.put32(plen);
+  for (int c = 0; c < chunks; ++c) {
+    uint8_t beta_b[16];
+    for (int b = 0; b < 16; ++b) {
+      const int idx = 16 * c + b;
+      beta_b[b] = idx < payload_len ? pay[idx] : 0;
+    }
+    U128 beta{0, 0};
+    for (int b = 0; b < 8; ++b) beta.lo |= uint64_t(beta_b[b]) << (8 * b);
+    for (int b = 0; b < 8; ++b) beta.hi |= uint64_t(beta_b[8 + b]) << (8 * b);
+    beta.hi &= kMsbClear;
+    const uint8_t* sp = seeds + size_t(c) * 32;
+    uint32_t sw[8];
+    for (int j = 0; j < 8; ++j) {
+      sw[j] = uint32_t(sp[4 * j]) | uint32_t(sp[4 * j + 1]) << 8 | uint32_t(sp[4 * j + 2]) << 16 |
+              uint32_t(sp[4 * j + 3]) << 24;
+    }
+    for (int j = 0; j < 4; ++j) w0.put32(sw[j]);
+    for (int j = 0; j < 4; ++j) w1.put32(sw[4 + j]);
+    U128 s0 = mk(sw[0], sw[1], sw[2], sw[3]);
+    U128 s1 = mk(sw[4], sw[5], sw[6], sw[7]);
+    s0.hi &= kMsbClear;
+    s1.hi &= kMsbClear;
+    uint32_t t0 = 0, t1 = 1;
+    U128 v{0, 0};
+    for (int i = 0; i < nb; ++i) {
+      U128 e0[4], e1[4];
+      prg4(aes, rkl, s0, e0);
+      prg4(aes, rkl, s1, e1);
+      const uint32_t t0l = uint32_t(e0[0].hi >> 63), t0r = uint32_t(e0[2].hi >> 63);
+      const uint32_t t1l = uint32_t(e1[0].hi >> 63), t1r = uint32_t(e1[2].hi >> 63);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        e0[j].hi &= kMsbClear;
+        e1[j].hi &= kMsbClear;
+      }
+      const uint32_t ai = uint32_t(alpha >> (nb - 1 - i)) & 1u;
+      // lose = side alpha does not take, keep = side it takes
+      const U128 s0_lose = ai ? e0[0] : e0[2], s1_lose = ai ? e1[0] : e1[2];
+      const U128 v0_lose = ai ? e0[1] : e0[3], v1_lose = ai ? e1[1] : e1[3];
+      const U128 s0_keep = ai ? e0[2] : e0[0], s1_keep = ai ? e1[2] : e1[0];
+      const U128 v0_keep = ai ? e0[3] : e0[1], v1_keep = ai ? e1[3] : e1[1];
+      const U128 s_cw{s0_lose.lo ^ s1_lose.lo, s0_lose.hi ^ s1_lose.hi};
+      U128 v_cw = gadd<kGroup>(v1_lose, gneg<kGroup>(v0_lose));
+      v_cw = gadd<kGroup>(v_cw, gneg<kGroup>(v));
+      if (t1) v_cw = gneg<kGroup>(v_cw);
+      if (ai) v_cw = gadd<kGroup>(v_cw, t1 ? gneg<kGroup>(beta) : beta);
+      v = gadd<kGroup>(v, gneg<kGroup>(v1_keep));
+      v = gadd<kGroup>(v, v0_keep);
+      v = gadd<kGroup>(v, t1 ? gneg<kGroup>(v_cw) : v_cw);
+      const uint32_t tl_cw = t0l ^ t1l ^ ai ^ 1u;
+      const uint32_t tr_cw = t0r ^ t1r ^ ai;
+      put128(w0, s_cw);
+      put128(w1, s_cw);
+      put128(w0, v_cw);
+      put128(w1, v_cw);
+      w0.put8(tl_cw << 1 | tr_cw);
+      w1.put8(tl_cw << 1 | tr_cw);
+      const uint32_t t0k = ai ? t0r : t0l, t1k = ai ? t1r : t1l, tcwk = ai ? tr_cw : tl_cw;
+      s0 = t0 ? U128{s0_keep.lo ^ s_cw.lo, s0_keep.hi ^ s_cw.hi} : s0_keep;
+      s1 = t1 ? U128{s1_keep.lo ^ s_cw.lo, s1_keep.hi ^ s_cw.hi} : s1_keep;
+      t0 = t0 ? (t0k ^ tcwk) : t0k;
+      t1 = t1 ? (t1k ^ tcwk) : t1k;
+    }
+    U128 last = gadd<kGroup>(s1, gneg<kGroup>(s0));
+    last = gadd<kGroup>(last, gneg<kGroup>(v));
+    if (t1) last = gneg<kGroup>(last);
+    put128(w0, last);
+    put128(w1, last);
+  }
+  w0.flush();
+  w1.flush();
+}
+
+// K_0..K_3 expanded (FIPS-197 word order).
+void fill_prg4(const uint8_t* state, Prg4* p) {
+  for (int j = 0; j < 4; ++j) {
+    aes128_expand_words(state + 16 * j, p->rk[j]);
+  }
+}
+
+// Grid for the grid-stride DCF kernels: one workgroup per CU (LDS-limited),
+// never more workgroups than the batch needs.
+int dcf_grid(size_t n, unsigned int* grid) {
+  int dev = 0, cus = 0;
+  SUFHIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
+  SUFHIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+               "hipDeviceGetAttribute(CU count)");
+  const size_t need = (n + kDcfBlock - 1) / kDcfBlock;
+  *grid = static_cast<unsigned int>(need < size_t(cus) ? need : size_t(cus));
+  return SUFHIP_OK;
+}
+
+}  // namespace
+}  // namespace sufhip

@@ -1,0 +1,358 @@
+// Truncation gate on one GPU: dealer keygen and the online evaluation that
+// SUF splits over composite_eval_batch_backend's AddU64 branch
+// (include/gates/composite_fss.hpp:1385-1638) and the trunc postproc hook
+// (include/gates/postproc_hooks.hpp:172-373), fused into one pass per party.
+//
+// Keygen follows composite_gen_trunc_gate (composite_fss.hpp:645-833): the
+// gate's predicates after the mask rewrite (include/suf/mask_rewrite.hpp,
+// src/compiler/suf_to_pfss.cpp:443-455), for x^ = x + r public and
+// r_low = r mod 2^f, are
+//   carry = 1[x^_low < r_low]           one f-bit DCF (none if r_low == 0)
+//   wrap  = 1[x^ < r]                   TR, ARS: one 64-bit DCF
+//   sign  = (wrap - 1[x^ < r + 2^63]) + 1[r < 2^63]           ARS
+// with 8-byte additive payloads (SUF's AddU64 semantics).  The rewrite's
+// second carry query, 1[x^_low < 0], is identically 0 and is not keyed.
+//
+// Evaluation of the carry DCF uses a prefix frontier: the walk state after
+// the first d levels depends only on the top d bits of x^_low, so for a
+// broadcast key and a large batch the 2^d frontier states are computed once
+// (one lane each) and every element continues from its prefix.  With d = f
+// the frontier holds the final share of every point of the domain and an
+// element's carry is a single table read.  The results are the same bytes a
+// full walk produces.
+#include <hip/hip_runtime.h>
+
+#include "dcf_device.hpp"
+#include "suf_hip.h"
+
+namespace sufhip {
+namespace {
+
+constexpr uint32_t kTag = 0x31475453u;  // "STG1"
+constexpr int kHdrBytes = 64;
+constexpr int kMaxFrontierBits = 16;
+
+__host__ __device__ constexpr size_t pad8(size_t v) { return (v + 7) & ~size_t(7); }
+
+size_t dcf_bytes(int in_bits) { return sufhip_dcf_key_bytes(in_bits, 8); }
+
+int frontier_bits(int f, size_t n) {
+  int lg = 0;
+  while (lg < 63 && (size_t(1) << (lg + 1)) <= n) ++lg;
+  int d = f < kMaxFrontierBits ? f : kMaxFrontierBits;
+  const int cap = lg - 4;
+  if (cap < d) d = cap < 0 ? 0 : cap;
+  return d;
+}
+
+struct TruncGenArgs {
+  Prg4 prg;
+  uint8_t* key0;
+  uint8_t* key1;
+  uint64_t hdr[2][8];
+  uint64_t alpha[3];
+  uint64_t seeds[3][4];
+  uint32_t off[3];
+  int bits[3];
+  int flags;
+  uint32_t total;
+};
+
+// One workgroup: zero both blobs, write the headers, then lanes 0..2 each
+// generate one DCF key pair.
+__global__ void __launch_bounds__(kDcfBlock) trunc_gen_kernel(TruncGenArgs a) {
+  SUFHIP_DCF_LDS_SETUP(a.prg);
+  __shared__ uint8_t one8[8];
+  __shared__ uint8_t seeds[3][32];
+  if (threadIdx.x < 8) one8[threadIdx.x] = threadIdx.x == 0 ? 1 : 0;
+  if (threadIdx.x < 96) {
+    const int j = threadIdx.x / 32, b = threadIdx.x % 32;
+    seeds[j][b] = uint8_t(a.seeds[j][b / 8] >> (8 * (b % 8)));
+  }
+  for (uint32_t i = threadIdx.x; i < a.total / 8; i += blockDim.x) {
+    const uint64_t v0 = i < 8 ? a.hdr[0][i] : 0;
+    const uint64_t v1 = i < 8 ? a.hdr[1][i] : 0;
+    reinterpret_cast<uint64_t*>(a.key0)[i] = v0;
+    reinterpret_cast<uint64_t*>(a.key1)[i] = v1;
+  }
+  __syncthreads();
+  const int j = threadIdx.x;
+  if (j < 3 && (a.flags >> j) & 1)
+    gen_key<SUFHIP_GROUP_ADD>(aes, rkl, a.bits[j], 1, 8, a.alpha[j], one8, seeds[j],
+                              a.key0 + a.off[j], a.key1 + a.off[j]);
+}
+
+// Frontier node v: {s0, s1, s2, s3} and {v_lo, v_hi, t, 0}.  With d == f the
+// node's value word holds the final share at point v.
+struct FrontierArgs {
+  Prg4 prg;
+  const uint8_t* key;
+  uint4* nodes;
+  int f;
+  int d;
+};
+
+__global__ void __launch_bounds__(kDcfBlock) trunc_frontier_kernel(FrontierArgs a) {
+  SUFHIP_DCF_LDS_SETUP(a.prg);
+  const uint32_t v = blockIdx.x * kDcfBlock + threadIdx.x;
+  if (v >= (1u << a.d) || !(a.key[7] & 1)) return;
+  const uint32_t party = a.key[6] & 1u;
+  const uint8_t* chunk = a.key + kHdrBytes + 8;
+  const uint64_t x = uint64_t(v) << (a.f - a.d);
+  Add64State st = add64_root(chunk, party);
+  add64_walk(aes, rkl, chunk, a.f, 0, a.d, x, party, st);
+  if (a.d == a.f) {
+    const uint64_t out = add64_finish(chunk, a.f, party, st);
+    a.nodes[2 * v + 1] = make_uint4(uint32_t(out), uint32_t(out >> 32), 0, 0);
+  } else {
+    a.nodes[2 * v] = make_uint4(st.s0, st.s1, st.s2, st.s3);
+    a.nodes[2 * v + 1] = make_uint4(uint32_t(st.v), uint32_t(st.v >> 32), st.t, 0);
+  }
+}
+
+struct TruncEvalArgs {
+  Prg4 prg;
+  const uint8_t* key;
+  const uint64_t* xhat;
+  uint64_t* y;
+  const uint4* nodes;
+  size_t n;
+  int f;
+  int d;
+};
+
+struct Hdr {
+  uint32_t party, flags;
+  uint64_t r_hi, base, cw, sw, m;
+  uint32_t ckb, ukb;
+};
+
+__device__ __forceinline__ Hdr read_hdr(const uint8_t* key) {
+  const uint64_t* w = reinterpret_cast<const uint64_t*>(key);
+  const uint64_t h0 = w[0];
+  Hdr h;
+  h.party = uint32_t(h0 >> 48) & 1u;
+  h.flags = uint32_t(h0 >> 56);
+  h.r_hi = w[2];
+  h.base = w[3];
+  h.cw = w[4];
+  h.sw = w[5];
+  h.m = w[6];
+  h.ckb = uint32_t(w[7]);
+  h.ukb = uint32_t(w[7] >> 32);
+  return h;
+}
+
+template <int kKind>
+__device__ __forceinline__ uint64_t postproc(const Hdr& h, int f, uint64_t x, uint64_t carry,
+                                             uint64_t wrap, uint64_t sign) {
+  if constexpr (kKind == SUFHIP_TRUNC_GAPARS) {
+    const uint64_t hb = x + (uint64_t(1) << 62);
+    uint64_t y = h.base + (h.party == 0 ? hb >> f : 0) - h.r_hi - carry;
+    if ((hb >> 63) == 0) y += h.m;
+    if (h.party == 0) y -= uint64_t(1) << (62 - f);
+    return y;
+  } else {
+    uint64_t y = h.base + (h.party == 0 ? x >> f : 0) - h.r_hi - carry +
+                 wrap * (uint64_t(1) << (64 - f));
+    if constexpr (kKind == SUFHIP_TRUNC_ARS) y += sign * (~uint64_t(0) << (64 - f));
+    return y;
+  }
+}
+
+// carry share = NOT(RotXor(a, 0, w)) = [p0] - w + a.
+__device__ __forceinline__ uint64_t carry_from(const Hdr& h, uint64_t a) {
+  return (h.party == 0 ? 1 : 0) - h.cw + a;
+}
+
+// Every DCF walk the element needs runs here (frontier continuation, 64-bit
+// wrap / sign keys).
+template <int kKind>
+__global__ void __launch_bounds__(kDcfBlock) trunc_eval_aes_kernel(TruncEvalArgs a) {
+  SUFHIP_DCF_LDS_SETUP(a.prg);
+  const Hdr h = read_hdr(a.key);
+  const uint8_t* carry_chunk = a.key + kHdrBytes + 8;
+  const uint8_t* wrap_chunk = a.key + kHdrBytes + pad8(h.ckb) + 8;
+  const uint8_t* sign_chunk = wrap_chunk + pad8(h.ukb);
+  const uint64_t low = (uint64_t(1) << a.f) - 1;
+  const size_t stride = size_t(gridDim.x) * kDcfBlock;
+  for (size_t e = size_t(blockIdx.x) * kDcfBlock + threadIdx.x; e < a.n; e += stride) {
+    const uint64_t x = a.xhat[e];
+    uint64_t carry = 0, wrap = 0, sign = 0;
+    if (h.flags & 1) {
+      const uint64_t xl = x & low;
+      uint64_t share;
+      if (a.d == a.f) {
+        const uint4 q = a.nodes[2 * xl + 1];
+        share = uint64_t(q.x) | uint64_t(q.y) << 32;
+      } else {
+        Add64State st;
+        if (a.d > 0) {
+          const size_t v = size_t(xl >> (a.f - a.d));
+          const uint4 s = a.nodes[2 * v], q = a.nodes[2 * v + 1];
+          st = Add64State{s.x, s.y, s.z, s.w, q.z, uint64_t(q.x) | uint64_t(q.y) << 32};
+        } else {
+          st = add64_root(carry_chunk, h.party);
+        }
+        add64_walk(aes, rkl, carry_chunk, a.f, a.d, a.f, xl, h.party, st);
+        share = add64_finish(carry_chunk, a.f, h.party, st);
+      }
+      carry = carry_from(h, share);
+    }
+    if constexpr (kKind != SUFHIP_TRUNC_GAPARS) {
+      Add64State st = add64_root(wrap_chunk, h.party);
+      add64_walk(aes, rkl, wrap_chunk, 64, 0, 64, x, h.party, st);
+      wrap = add64_finish(wrap_chunk, 64, h.party, st);
+    }
+    if constexpr (kKind == SUFHIP_TRUNC_ARS) {
+      Add64State st = add64_root(sign_chunk, h.party);
+      add64_walk(aes, rkl, sign_chunk, 64, 0, 64, x, h.party, st);
+      sign = (wrap - add64_finish(sign_chunk, 64, h.party, st)) + h.sw;
+    }
+    a.y[e] = postproc<kKind>(h, a.f, x, carry, wrap, sign);
+  }
+}
+
+// GapARS with the full-domain table (or no carry key): one table read per
+// element, HBM-bound.
+__global__ void __launch_bounds__(256) trunc_eval_table_kernel(TruncEvalArgs a) {
+  const Hdr h = read_hdr(a.key);
+  const uint64_t low = (uint64_t(1) << a.f) - 1;
+  const size_t stride = size_t(gridDim.x) * 256;
+  for (size_t e = size_t(blockIdx.x) * 256 + threadIdx.x; e < a.n; e += stride) {
+    const uint64_t x = a.xhat[e];
+    uint64_t carry = 0;
+    if (h.flags & 1) {
+      const uint4 q = a.nodes[2 * (x & low) + 1];
+      carry = carry_from(h, uint64_t(q.x) | uint64_t(q.y) << 32);
+    }
+    a.y[e] = postproc<SUFHIP_TRUNC_GAPARS>(h, a.f, x, carry, 0, 0);
+  }
+}
+
+bool valid_kind(int kind) {
+  return kind == SUFHIP_TRUNC_TR || kind == SUFHIP_TRUNC_ARS || kind == SUFHIP_TRUNC_GAPARS;
+}
+
+constexpr size_t kMaxElems = size_t(1) << 38;
+
+}  // namespace
+}  // namespace sufhip
+
+using namespace sufhip;
+
+extern "C" {
+
+size_t sufhip_trunc_key_bytes(int kind, int frac_bits) {
+  if (!valid_kind(kind) || frac_bits < 1 || frac_bits > 62) return 0;
+  size_t b = kHdrBytes + pad8(dcf_bytes(frac_bits));
+  if (kind != SUFHIP_TRUNC_GAPARS) b += pad8(dcf_bytes(64));
+  if (kind == SUFHIP_TRUNC_ARS) b += pad8(dcf_bytes(64));
+  return b;
+}
+
+int sufhip_trunc_gen(int kind, int frac_bits, const uint8_t* prg_state, const uint64_t* rnd,
+                     uint8_t* d_key0, uint8_t* d_key1, void* stream) {
+  SUFHIP_REQUIRE(valid_kind(kind), "sufhip_trunc_gen: unknown kind");
+  SUFHIP_REQUIRE(frac_bits >= 1 && frac_bits <= 62, "sufhip_trunc_gen: frac_bits out of [1, 62]");
+  SUFHIP_REQUIRE(prg_state && rnd && d_key0 && d_key1, "sufhip_trunc_gen: null pointer");
+  SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_key0) & 7) == 0 &&
+                     (reinterpret_cast<uintptr_t>(d_key1) & 7) == 0,
+                 "sufhip_trunc_gen: keys must be 8-byte aligned");
+  const int f = frac_bits;
+  const uint64_t r = rnd[0];
+  const uint64_t r_low = r & ((uint64_t(1) << f) - 1);
+  const uint64_t r_hi = r >> f;
+  const uint64_t m = (kind == SUFHIP_TRUNC_GAPARS && (r >> 63)) ? uint64_t(1) << (64 - f) : 0;
+  const uint64_t sign_w = r < (uint64_t(1) << 63) ? 1 : 0;
+  const int has_carry = r_low != 0;
+  const int has_wrap = kind != SUFHIP_TRUNC_GAPARS;
+  const int has_sign = kind == SUFHIP_TRUNC_ARS;
+  const uint32_t ckb = uint32_t(dcf_bytes(f)), ukb = uint32_t(dcf_bytes(64));
+  TruncGenArgs a{};
+  fill_prg4(prg_state, &a.prg);
+  a.key0 = d_key0;
+  a.key1 = d_key1;
+  a.flags = has_carry | has_wrap << 1 | has_sign << 2;
+  for (int p = 0; p < 2; ++p) {
+    auto split = [&](uint64_t v, uint64_t s) { return p == 0 ? s : v - s; };
+    a.hdr[p][0] = uint64_t(kTag) | uint64_t(kind) << 32 | uint64_t(f) << 40 |
+                  uint64_t(p) << 48 | uint64_t(a.flags) << 56;
+    a.hdr[p][1] = split(r, rnd[1]);
+    a.hdr[p][2] = split(r_hi, rnd[5]);
+    a.hdr[p][3] = split(0, rnd[2]);
+    a.hdr[p][4] = has_carry ? split(1, rnd[3]) : 0;
+    a.hdr[p][5] = has_sign ? split(sign_w, rnd[4]) : 0;
+    a.hdr[p][6] = kind == SUFHIP_TRUNC_GAPARS ? split(m, rnd[6]) : 0;
+    a.hdr[p][7] = uint64_t(ckb) | uint64_t(ukb) << 32;
+  }
+  a.alpha[0] = r_low;
+  a.alpha[1] = r;
+  a.alpha[2] = r + (uint64_t(1) << 63);
+  a.bits[0] = f;
+  a.bits[1] = 64;
+  a.bits[2] = 64;
+  a.off[0] = kHdrBytes;
+  a.off[1] = uint32_t(kHdrBytes + pad8(ckb));
+  a.off[2] = uint32_t(a.off[1] + pad8(ukb));
+  for (int j = 0; j < 3; ++j)
+    for (int w = 0; w < 4; ++w) a.seeds[j][w] = rnd[7 + 4 * j + w];
+  a.total = uint32_t(sufhip_trunc_key_bytes(kind, f));
+  hipLaunchKernelGGL(trunc_gen_kernel, dim3(1), dim3(kDcfBlock), 0, as_stream(stream), a);
+  return check_launch("trunc_gen_kernel");
+}
+
+size_t sufhip_trunc_work_bytes(int frac_bits, size_t n) {
+  if (frac_bits < 1 || frac_bits > 62) return 0;
+  const int d = frontier_bits(frac_bits, n);
+  return d > 0 ? size_t(32) << d : 0;
+}
+
+int sufhip_trunc_eval(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,
+                      size_t key_bytes, const uint64_t* d_xhat, size_t n, uint64_t* d_y,
+                      void* d_work, size_t work_bytes, void* stream) {
+  SUFHIP_REQUIRE(valid_kind(kind), "sufhip_trunc_eval: unknown kind");
+  SUFHIP_REQUIRE(frac_bits >= 1 && frac_bits <= 62, "sufhip_trunc_eval: frac_bits out of [1, 62]");
+  SUFHIP_REQUIRE(key_bytes == sufhip_trunc_key_bytes(kind, frac_bits),
+                 "sufhip_trunc_eval: key_bytes does not match (kind, frac_bits)");
+  if (n == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(n < kMaxElems, "sufhip_trunc_eval: n too large");
+  SUFHIP_REQUIRE(prg_state && d_key && d_xhat && d_y, "sufhip_trunc_eval: null pointer");
+  SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_key) & 7) == 0,
+                 "sufhip_trunc_eval: key must be 8-byte aligned");
+  const int d = frontier_bits(frac_bits, n);
+  const size_t need = sufhip_trunc_work_bytes(frac_bits, n);
+  SUFHIP_REQUIRE(work_bytes >= need && (need == 0 || d_work),
+                 "sufhip_trunc_eval: workspace smaller than sufhip_trunc_work_bytes()");
+  SUFHIP_REQUIRE(need == 0 || (reinterpret_cast<uintptr_t>(d_work) & 15) == 0,
+                 "sufhip_trunc_eval: workspace must be 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  Prg4 prg;
+  fill_prg4(prg_state, &prg);
+  if (d > 0) {
+    FrontierArgs fa{prg, d_key, static_cast<uint4*>(d_work), frac_bits, d};
+    const unsigned int blocks = ((1u << d) + kDcfBlock - 1) / kDcfBlock;
+    hipLaunchKernelGGL(trunc_frontier_kernel, dim3(blocks), dim3(kDcfBlock), 0, s, fa);
+    if (int rc = check_launch("trunc_frontier_kernel")) return rc;
+  }
+  TruncEvalArgs a{prg, d_key, d_xhat, d_y, static_cast<const uint4*>(d_work), n, frac_bits, d};
+  if (kind == SUFHIP_TRUNC_GAPARS && d == frac_bits) {
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(trunc_eval_table_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, a);
+    return check_launch("trunc_eval_table_kernel");
+  }
+  unsigned int g = 0;
+  if (int rc = dcf_grid(n, &g)) return rc;
+  if (kind == SUFHIP_TRUNC_GAPARS)
+    hipLaunchKernelGGL(trunc_eval_aes_kernel<SUFHIP_TRUNC_GAPARS>, dim3(g), dim3(kDcfBlock), 0,
+                       s, a);
+  else if (kind == SUFHIP_TRUNC_TR)
+    hipLaunchKernelGGL(trunc_eval_aes_kernel<SUFHIP_TRUNC_TR>, dim3(g), dim3(kDcfBlock), 0, s, a);
+  else
+    hipLaunchKernelGGL(trunc_eval_aes_kernel<SUFHIP_TRUNC_ARS>, dim3(g), dim3(kDcfBlock), 0, s,
+                       a);
+  return check_launch("trunc_eval_aes_kernel");
+}
+
+}  // extern "C"

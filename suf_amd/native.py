@@ -19,6 +19,10 @@ GROUP_ADD = 1
 DCF_OUT_BIT = 0
 DCF_OUT_BYTES = 1
 DCF_OUT_PACKED = 2
+TRUNC_TR = 0
+TRUNC_ARS = 1
+TRUNC_GAPARS = 2
+TRUNC_RAND_WORDS = 19
 
 c_int = ctypes.c_int
 c_sz = ctypes.c_size_t
@@ -55,6 +59,11 @@ _SIGS = {
                                c_vp, c_vp]),
     "sufhip_dcf_eval": (c_int, [c_int, c_int, c_int, c_vp, c_vp, c_sz, c_int, c_vp, c_sz, c_int,
                                 c_int, c_vp, c_vp]),
+    "sufhip_trunc_key_bytes": (c_sz, [c_int, c_int]),
+    "sufhip_trunc_gen": (c_int, [c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "sufhip_trunc_work_bytes": (c_sz, [c_int, c_sz]),
+    "sufhip_trunc_eval": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp, c_sz,
+                                  c_vp]),
     "sufhip_seed_from_id": (None, [c_u64, c_u64, c_vp]),
     "sufhip_interval_lut_key_bytes": (c_sz, [c_int, c_int]),
     "sufhip_interval_lut_build_key": (c_int, [c_int, c_u64, c_int, c_int, c_vp, c_int, c_vp, c_vp,

@@ -71,6 +71,42 @@ def dcf_eval(group, in_bits, payload_len, prg_state, keys, xs, out_mode=native.D
     return out
 
 
+def trunc_key_bytes(kind, frac_bits):
+    return native.load().sufhip_trunc_key_bytes(kind, frac_bits)
+
+
+def trunc_gen(kind, frac_bits, prg_state, rnd, device="cuda"):
+    """Dealer keys of one truncation gate.  rnd: 19 host u64 words (numpy).
+    Returns (key0, key1): uint8[key_bytes] device tensors (8-byte aligned)."""
+    import numpy as np
+
+    rnd = np.ascontiguousarray(rnd, dtype=np.uint64)
+    if rnd.size != native.TRUNC_RAND_WORDS:
+        raise ValueError("rnd must hold %d words" % native.TRUNC_RAND_WORDS)
+    kb = trunc_key_bytes(kind, frac_bits)
+    if kb == 0:
+        raise native.SufHipError("trunc_gen: bad (kind, frac_bits)")
+    k0 = torch.empty(kb // 8, dtype=torch.int64, device=device).view(torch.uint8)
+    k1 = torch.empty(kb // 8, dtype=torch.int64, device=device).view(torch.uint8)
+    native.call("sufhip_trunc_gen", kind, frac_bits, _state_buf(prg_state), rnd.ctypes.data,
+                _ptr(k0), _ptr(k1), _stream())
+    return k0, k1
+
+
+def trunc_eval(kind, frac_bits, prg_state, key, xhat, out=None, work=None):
+    """One party's truncated shares given the public masked inputs xhat (int64[N])."""
+    n = xhat.numel()
+    if out is None:
+        out = torch.empty(n, dtype=torch.int64, device=xhat.device)
+    wb = native.load().sufhip_trunc_work_bytes(frac_bits, n)
+    if work is None and wb:
+        work = torch.empty((wb + 7) // 8, dtype=torch.int64, device=xhat.device)
+    native.call("sufhip_trunc_eval", kind, frac_bits, _state_buf(prg_state), _ptr(key),
+                key.numel(), _ptr(xhat), n, _ptr(out), _ptr(work),
+                work.numel() * 8 if work is not None else 0, _stream())
+    return out
+
+
 def aes128_ctr(round_keys, ctr_lo, ctr_hi, blocks, device="cuda"):
     out = torch.empty(blocks * 16, dtype=torch.uint8, device=device)
     rk = native.ctypes.create_string_buffer(bytes(round_keys), 176)

@@ -65,6 +65,11 @@ def _load_oracle():
     lib.orc_add_rout_aos.argtypes = [u64p, c_sz, ctypes.c_int, u64p, ctypes.c_int]
     lib.orc_open_add.argtypes = [u64p, u64p, ctypes.c_int, u64p, c_sz, ctypes.c_int,
                                  ctypes.c_uint64, ctypes.c_int]
+    lib.orc_trunc_key_bytes.restype = c_sz
+    lib.orc_trunc_key_bytes.argtypes = [ctypes.c_int, ctypes.c_int]
+    lib.orc_trunc_gen.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, u64p, u8p, u8p]
+    lib.orc_trunc_eval.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, u8p, u64p, c_sz,
+                                   u64p]
     return lib
 
 
@@ -319,3 +324,30 @@ def beaver_matmul(party, D, E, A, B, C, batches, M, K, N, w_t=0, has_scale=0, mu
     LIB.orc_beaver_matmul(party, *(ptr(_u64(v), u64p) for v in (D, E, A, B, C)), batches, M, K, N,
                           w_t, has_scale, mul_const, mul_shift, ptr(out, u64p), threads)
     return out
+
+
+TRUNC_TR, TRUNC_ARS, TRUNC_GAPARS = 0, 1, 2
+TRUNC_RAND_WORDS = 19
+
+
+def trunc_key_bytes(kind, f):
+    return LIB.orc_trunc_key_bytes(kind, f)
+
+
+def trunc_gen(prg, kind, f, rnd):
+    rnd = _u64(rnd)
+    assert rnd.size == TRUNC_RAND_WORDS
+    kb = trunc_key_bytes(kind, f)
+    k0 = np.zeros(kb, dtype=np.uint8)
+    k1 = np.zeros(kb, dtype=np.uint8)
+    assert LIB.orc_trunc_gen(prg.buf, kind, f, ptr(rnd, u64p), ptr(k0), ptr(k1)) == 0
+    return k0, k1
+
+
+def trunc_eval(prg, kind, f, key, xhat):
+    xhat = _u64(xhat)
+    y = np.zeros(xhat.size, dtype=np.uint64)
+    key = np.ascontiguousarray(key, dtype=np.uint8)
+    assert LIB.orc_trunc_eval(prg.buf, kind, f, ptr(key), ptr(xhat, u64p), c_sz(xhat.size),
+                              ptr(y, u64p)) == 0
+    return y

@@ -34,6 +34,25 @@ def test_key_bytes_match_oracle(in_bits, plen):
     assert native.load().sufhip_dcf_key_bytes(in_bits, plen) == ol.myl7_key_bytes(in_bits, plen)
 
 
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("f", [1, 12, 24, 62])
+def test_trunc_key_bytes_match_oracle(kind, f):
+    lib = native.load()
+    assert lib.sufhip_trunc_key_bytes(kind, f) == ol.trunc_key_bytes(kind, f) > 0
+    assert lib.sufhip_trunc_key_bytes(kind, 0) == 0 == lib.sufhip_trunc_key_bytes(kind, 63)
+    assert lib.sufhip_trunc_key_bytes(3, f) == 0
+
+
+def test_trunc_workspace_sizes():
+    lib = native.load()
+    # Frontier depth min(f, 16, floor(log2 n) - 4), 32 bytes per node.
+    assert lib.sufhip_trunc_work_bytes(12, 1 << 20) == 32 << 12
+    assert lib.sufhip_trunc_work_bytes(24, 1 << 20) == 32 << 16
+    assert lib.sufhip_trunc_work_bytes(24, 3000) == 32 << 7
+    assert lib.sufhip_trunc_work_bytes(12, 31) == 0
+    assert lib.sufhip_trunc_work_bytes(12, 0) == 0
+
+
 def test_key_bytes_rejects_bad_geometry():
     lib = native.load()
     assert lib.sufhip_dcf_key_bytes(0, 1) == 0
