@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--n", type=int, default=1 << 20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gates", action="store_true",
+                    help="skip the spline-gate pipeline timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device-to-device copy kernel 5 times "
                          "(reference point for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -57,6 +59,42 @@ def calibrate_copy():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"calibrate_copy_bytes": n, "launches": 5}), flush=True)
+
+
+def bench_spline(steps, warmup, n=1 << 20, frac_bits=12):
+    """The spline gate (interval LUT + three Beaver products + GapARS by f and
+    2f) for both parties on N = 2^20 inputs x = clip(3 N(0,1), +-8) in Q12
+    (Box-Muller on mt(5)); coefficients from mt(6); dealer randomness mt(7).
+    Returns ms per gate evaluation (both parties) and the reconstruction check."""
+    import numpy as np
+    import torch
+
+    from suf_amd import pfss, spline
+
+    state = bytes((pfss.host_mt19937_64(3, 128) & np.uint64(0xFF)).astype(np.uint8))
+    alpha, coeffs = spline.spline_spec(frac_bits, seed=6)
+    x = pfss.host_normal_fixed(5, 3.0, 8.0, frac_bits, n)
+    x0 = pfss.host_mt19937_64(8, n)
+    x1 = (x - x0).astype(np.uint64)
+    gate = spline.SplineGate(n, alpha, coeffs, state, frac_bits, seed=7)
+    xd = [torch.from_numpy(v.view(np.int64).copy()).cuda() for v in (x0, x1)]
+    out = [torch.empty(n, dtype=torch.int64, device="cuda") for _ in range(2)]
+    for _ in range(warmup):
+        gate.eval2(xd, out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        gate.eval2(xd, out)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    rec = (out[0].cpu().numpy().view(np.uint64) + out[1].cpu().numpy().view(np.uint64))
+    ok = bool(np.array_equal(rec.astype(np.uint64),
+                             spline.spline_eval_ref(alpha, coeffs, x, frac_bits)))
+    return {"ms": ms, "n": n, "frac_bits": frac_bits, "intervals": int(gate.intervals),
+            "trunc": "GapARS f=%d and 2f=%d" % (frac_bits, 2 * frac_bits),
+            "steps": steps, "check": "ok" if ok else "MISMATCH"}
 
 
 def cpu_baseline(keys0, keys1, xhat, gpu_bits0, gpu_bits1, seconds):
@@ -238,6 +276,9 @@ def main():
         "secure_layer_ms": None,
         "check": "ok" if ok else "MISMATCH",
     }
+    if not a.no_gates:
+        line["spline_gate"] = bench_spline(max(a.steps // 2, 1), 2)
+        ok = ok and line["spline_gate"]["check"] == "ok"
     if not a.no_cpu:
         sample = 1 << 14
         g0 = out0[:sample].cpu().numpy()

@@ -176,6 +176,51 @@ int sufhip_trunc_eval(int kind, int frac_bits, const uint8_t* prg_state, const u
                       void* d_work, size_t work_bytes, void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* Two-party steps with both parties on one GPU (SUF's local channel: an    */
+/* open is an exchange of masked shares and an add).  Each call does both   */
+/* parties' local work of one round plus the open.  They stand in for the   */
+/* host loops of MulTask / TruncTask / CubicPolyTask                        */
+/* (include/runtime/phase_tasks.hpp:198-402, 2962-3061) when SUF runs both  */
+/* parties in one process; they have no launcher in cuda_primitives.hpp.   */
+/* ---------------------------------------------------------------------- */
+/* d_xhat[i] = (d_x0[i] + r0) + (d_x1[i] + r1): the masked open of a gate input. */
+int sufhip_open2_masked(const uint64_t* d_x0, const uint64_t* d_x1, uint64_t r0, uint64_t r1,
+                        size_t n, uint64_t* d_xhat, void* stream);
+
+/* One Beaver product for both parties.  Per element i and party p:
+ *   u_p = u[p][i*u_stride + u_off] (+ u_add[p][i*u_add_stride + u_add_off] << u_add_shift)
+ *   v_p = v[p][i];   (a_p, b_p, c_p) = triples[p][3i], [3i+1], [3i+2]
+ *   d = (u_0 - a_0) + (u_1 - a_1),  e = (v_0 - b_0) + (v_1 - b_1)        (the open)
+ *   z_p = c_p + d*b_p + e*a_p + [p == 0] d*e
+ *         (+ z_add[p][i*z_add_stride + z_add_off] << z_add_shift)
+ * zhat == NULL: z[p][i] = z_p.  Otherwise only the masked open of the
+ * product is written: zhat[i] = z_0 + z_1 + open_mask[0] + open_mask[1].
+ * u_add / z_add: both parties' pointers or neither. */
+typedef struct sufhip_mul2_args {
+  const uint64_t* u[2];
+  size_t u_stride;
+  size_t u_off;
+  const uint64_t* u_add[2];
+  size_t u_add_stride;
+  size_t u_add_off;
+  int u_add_shift;
+  const uint64_t* v[2];
+  const uint64_t* triples[2];
+  const uint64_t* z_add[2];
+  size_t z_add_stride;
+  size_t z_add_off;
+  int z_add_shift;
+  uint64_t* z[2];
+  uint64_t* zhat;
+  uint64_t open_mask[2];
+} sufhip_mul2_args;
+int sufhip_mul2(const sufhip_mul2_args* args, size_t n, void* stream);
+
+/* d_out[i] = d_y[i] + (d_add[i*add_stride + add_off] << shift) (one party). */
+int sufhip_add_shifted(const uint64_t* d_y, const uint64_t* d_add, size_t add_stride,
+                       size_t add_off, int shift, size_t n, uint64_t* d_out, void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* Interval LUT and packed compare in the reference GPU blob formats        */
 /* (cuda/pfss_backend_gpu.cu:75-94, 189-288), evaluated with the kernel     */
 /* counter convention of cuda/pfss_kernels.cu:240-719.  They replace        */

@@ -1,0 +1,139 @@
+// Two-party step kernels for gate pipelines whose two parties share one GPU
+// (the reference's local channel: both parties in one process, each "open"
+// an exchange of masked shares followed by an add).  Each kernel does the
+// local work of both parties for one protocol round plus the open, in one
+// pass over HBM:
+//   open2_masked  x^ = (x_0 + r_0) + (x_1 + r_1)          (a gate's masked open)
+//   mul2          Beaver product of MulTask (include/runtime/phase_tasks.hpp:
+//                 198-402) with the d/e open inline, optional pre-add on the
+//                 left factor and post-add on the product (the affine steps
+//                 of CubicPolyTask, phase_tasks.hpp:2962-3061), and optional
+//                 masked open of the product for the next gate
+//   add_shifted   y + (a << s), strided a (coefficient words of an AoS row)
+// All arithmetic is mod 2^64; per party the Beaver step is exactly
+// z_p = c_p + d*b_p + e*a_p + [p == 0] d*e (beaver_mul_kernel,
+// cuda/cuda_primitives.cu:114-139).
+#include <hip/hip_runtime.h>
+
+#include "suf_hip.h"
+#include "sufhip_internal.hpp"
+
+namespace sufhip {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr size_t kMaxElems = size_t(1) << 40;
+
+unsigned int ew_grid(size_t n) {
+  size_t g = (n + kBlock - 1) / kBlock;
+  return unsigned(g > 8192 ? 8192 : g);
+}
+
+__global__ void __launch_bounds__(kBlock)
+    open2_masked_kernel(const uint64_t* x0, const uint64_t* x1, uint64_t r, size_t n,
+                        uint64_t* xhat) {
+  const size_t stride = size_t(gridDim.x) * kBlock;
+  for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+    xhat[i] = x0[i] + x1[i] + r;
+}
+
+__global__ void __launch_bounds__(kBlock) mul2_kernel(sufhip_mul2_args a, size_t n) {
+  const size_t stride = size_t(gridDim.x) * kBlock;
+  const bool has_uadd = a.u_add[0] != nullptr;
+  const bool has_zadd = a.z_add[0] != nullptr;
+  const bool open = a.zhat != nullptr;
+  const uint64_t mask = a.open_mask[0] + a.open_mask[1];
+  for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+    uint64_t u0 = a.u[0][i * a.u_stride + a.u_off];
+    uint64_t u1 = a.u[1][i * a.u_stride + a.u_off];
+    if (has_uadd) {
+      u0 += a.u_add[0][i * a.u_add_stride + a.u_add_off] << a.u_add_shift;
+      u1 += a.u_add[1][i * a.u_add_stride + a.u_add_off] << a.u_add_shift;
+    }
+    const uint64_t v0 = a.v[0][i], v1 = a.v[1][i];
+    const uint64_t* t0 = a.triples[0] + 3 * i;
+    const uint64_t* t1 = a.triples[1] + 3 * i;
+    const uint64_t a0 = t0[0], b0 = t0[1], c0 = t0[2];
+    const uint64_t a1 = t1[0], b1 = t1[1], c1 = t1[2];
+    // The open: each party's masked shares, summed.
+    const uint64_t d = (u0 - a0) + (u1 - a1);
+    const uint64_t e = (v0 - b0) + (v1 - b1);
+    uint64_t z0 = c0 + d * b0 + e * a0 + d * e;
+    uint64_t z1 = c1 + d * b1 + e * a1;
+    if (has_zadd) {
+      z0 += a.z_add[0][i * a.z_add_stride + a.z_add_off] << a.z_add_shift;
+      z1 += a.z_add[1][i * a.z_add_stride + a.z_add_off] << a.z_add_shift;
+    }
+    if (open) {
+      a.zhat[i] = z0 + z1 + mask;
+    } else {
+      a.z[0][i] = z0;
+      a.z[1][i] = z1;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kBlock)
+    add_shifted_kernel(const uint64_t* y, const uint64_t* add, size_t stride_a, size_t off,
+                       int shift, size_t n, uint64_t* out) {
+  const size_t stride = size_t(gridDim.x) * kBlock;
+  for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+    out[i] = y[i] + (add[i * stride_a + off] << shift);
+}
+
+}  // namespace
+}  // namespace sufhip
+
+using namespace sufhip;
+
+extern "C" {
+
+int sufhip_open2_masked(const uint64_t* d_x0, const uint64_t* d_x1, uint64_t r0, uint64_t r1,
+                        size_t n, uint64_t* d_xhat, void* stream) {
+  if (n == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(n < kMaxElems, "sufhip_open2_masked: n too large");
+  SUFHIP_REQUIRE(d_x0 && d_x1 && d_xhat, "sufhip_open2_masked: null pointer");
+  hipLaunchKernelGGL(open2_masked_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream),
+                     d_x0, d_x1, r0 + r1, n, d_xhat);
+  return check_launch("open2_masked_kernel");
+}
+
+int sufhip_mul2(const sufhip_mul2_args* args, size_t n, void* stream) {
+  SUFHIP_REQUIRE(args != nullptr, "sufhip_mul2: null args");
+  if (n == 0) return SUFHIP_OK;
+  const sufhip_mul2_args& a = *args;
+  SUFHIP_REQUIRE(n < kMaxElems, "sufhip_mul2: n too large");
+  SUFHIP_REQUIRE(a.u[0] && a.u[1] && a.v[0] && a.v[1] && a.triples[0] && a.triples[1],
+                 "sufhip_mul2: null factor or triple pointer");
+  SUFHIP_REQUIRE(a.u_stride >= 1 && a.u_off < a.u_stride, "sufhip_mul2: bad u stride/offset");
+  SUFHIP_REQUIRE((a.u_add[0] == nullptr) == (a.u_add[1] == nullptr),
+                 "sufhip_mul2: u_add must be given for both parties or neither");
+  if (a.u_add[0])
+    SUFHIP_REQUIRE(a.u_add_stride >= 1 && a.u_add_off < a.u_add_stride && a.u_add_shift >= 0 &&
+                       a.u_add_shift < 64,
+                   "sufhip_mul2: bad u_add stride/offset/shift");
+  SUFHIP_REQUIRE((a.z_add[0] == nullptr) == (a.z_add[1] == nullptr),
+                 "sufhip_mul2: z_add must be given for both parties or neither");
+  if (a.z_add[0])
+    SUFHIP_REQUIRE(a.z_add_stride >= 1 && a.z_add_off < a.z_add_stride && a.z_add_shift >= 0 &&
+                       a.z_add_shift < 64,
+                   "sufhip_mul2: bad z_add stride/offset/shift");
+  SUFHIP_REQUIRE(a.zhat != nullptr || (a.z[0] && a.z[1]),
+                 "sufhip_mul2: need zhat (open) or both z outputs");
+  hipLaunchKernelGGL(mul2_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream), a, n);
+  return check_launch("mul2_kernel");
+}
+
+int sufhip_add_shifted(const uint64_t* d_y, const uint64_t* d_add, size_t add_stride,
+                       size_t add_off, int shift, size_t n, uint64_t* d_out, void* stream) {
+  if (n == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(n < kMaxElems, "sufhip_add_shifted: n too large");
+  SUFHIP_REQUIRE(d_y && d_add && d_out, "sufhip_add_shifted: null pointer");
+  SUFHIP_REQUIRE(add_stride >= 1 && add_off < add_stride && shift >= 0 && shift < 64,
+                 "sufhip_add_shifted: bad stride/offset/shift");
+  hipLaunchKernelGGL(add_shifted_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream),
+                     d_y, d_add, add_stride, add_off, shift, n, d_out);
+  return check_launch("add_shifted_kernel");
+}
+
+}  // extern "C"

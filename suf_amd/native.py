@@ -64,6 +64,9 @@ _SIGS = {
     "sufhip_trunc_work_bytes": (c_sz, [c_int, c_sz]),
     "sufhip_trunc_eval": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp, c_sz,
                                   c_vp]),
+    "sufhip_open2_masked": (c_int, [c_vp, c_vp, c_u64, c_u64, c_sz, c_vp, c_vp]),
+    "sufhip_mul2": (c_int, [c_vp, c_sz, c_vp]),
+    "sufhip_add_shifted": (c_int, [c_vp, c_vp, c_sz, c_sz, c_int, c_sz, c_vp, c_vp]),
     "sufhip_seed_from_id": (None, [c_u64, c_u64, c_vp]),
     "sufhip_interval_lut_key_bytes": (c_sz, [c_int, c_int]),
     "sufhip_interval_lut_build_key": (c_int, [c_int, c_u64, c_int, c_int, c_vp, c_int, c_vp, c_vp,
@@ -102,6 +105,17 @@ _SIGS = {
 }
 
 _lib = None
+
+
+class Mul2Args(ctypes.Structure):
+    """sufhip_mul2_args (include/suf_hip.h)."""
+    _fields_ = [
+        ("u", c_vp * 2), ("u_stride", c_sz), ("u_off", c_sz),
+        ("u_add", c_vp * 2), ("u_add_stride", c_sz), ("u_add_off", c_sz), ("u_add_shift", c_int),
+        ("v", c_vp * 2), ("triples", c_vp * 2),
+        ("z_add", c_vp * 2), ("z_add_stride", c_sz), ("z_add_off", c_sz), ("z_add_shift", c_int),
+        ("z", c_vp * 2), ("zhat", c_vp), ("open_mask", c_u64 * 2),
+    ]
 
 
 class SufHipError(RuntimeError):

@@ -1,0 +1,200 @@
+"""Piecewise-cubic spline gate (SiLU / GeLU shape) for two parties on one GPU.
+
+Protocol, as SUF runs it for SiLU/GeLU-style gates:
+  * coefficients: an interval LUT over the public x^ = x + r_in returns
+    additive shares of the piece's (c0, c1, c2, c3)
+    (composite_eval_batch_backend fast path, include/gates/composite_fss.hpp:
+    1248-1330; intervals rotated by r_in and split at the wrap,
+    src/compiler/suf_to_pfss.cpp:506-523);
+  * Horner with two truncations (CubicPolyTask, include/runtime/
+    phase_tasks.hpp:2962-3061):
+        m1 = c3 * x; u = m1 + c2 << f; p = u * x; p2 = trunc_f(p);
+        q = p2 + c1 << f; r = q * x; y = trunc_2f(r) + c0
+    with three Beaver products and two GapARS truncation gates.
+The output mask r_out of spline gates is 0 (include/gates/silu_composite.hpp:
+92), so the LUT's coefficient shares are used directly.
+
+Every step runs in libsuf_hip.so: open2_masked, interval_lut_eval, mul2,
+trunc_eval, add_shifted.  The dealer builds keys with the library's key
+builders and host std::mt19937_64 streams.
+"""
+import numpy as np
+import torch
+
+from . import native, pfss
+
+M64 = (1 << 64) - 1
+LUT_TWEAK = 7  # seed_from_id tweak of interval LUT keys (cuda/pfss_backend_gpu.cu:508-515)
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t):
+    return t.data_ptr() if t is not None else None
+
+
+def spline_spec(frac_bits=12, seed=6, coeff_bits=15):
+    """18 pieces over the ring in unsigned order: [k, k+1) for k = 0..7, the
+    positive tail [8, 2^63), the negative tail [-2^63, -8), and [-k, -k+1) for
+    k = 8..1 (units of 2^frac_bits).  Coefficients c0..c3 are signed Q(frac)
+    words drawn from std::mt19937_64(seed): (w mod 2^coeff_bits) - 2^(coeff_bits-1).
+    Returns (alpha [18] u64 ascending, coeffs int64 [18, 4])."""
+    one = 1 << frac_bits
+    alpha = [k * one for k in range(9)] + [1 << 63] + [(1 << 64) - k * one for k in range(8, 0, -1)]
+    w = pfss.host_mt19937_64(seed, 4 * len(alpha))
+    half = 1 << (coeff_bits - 1)
+    c = (w % np.uint64(1 << coeff_bits)).astype(np.int64) - half
+    return np.array(alpha, dtype=np.uint64), c.reshape(len(alpha), 4)
+
+
+def spline_eval_ref(alpha, coeffs, x, frac_bits):
+    """Plain fixed-point evaluation of the spline at x (u64 ring values): the
+    closed form of CubicPolyTask's reference path (phase_tasks.hpp:2933-2945)
+    with exact arithmetic shifts, in int64 numpy.  Raises if an intermediate
+    could leave (-2^62, 2^62) for these inputs."""
+    x = np.asarray(x, dtype=np.uint64)
+    piece = np.searchsorted(alpha, x, side="right") - 1
+    c = coeffs[piece]
+    xs = x.view(np.int64)
+    f = frac_bits
+    cx = int(np.abs(coeffs).max())
+    xm = int(np.abs(xs).max()) if xs.size else 0
+    u_max = cx * xm + (cx << f)
+    q_max = ((u_max * xm) >> f) + 1 + (cx << f)
+    if max(u_max * xm, q_max * xm) >= 1 << 62:
+        raise ValueError("spline_eval_ref: inputs outside the exact int64 range")
+    u = c[:, 3] * xs + (c[:, 2] << f)
+    p2 = (u * xs) >> f
+    q = p2 + (c[:, 1] << f)
+    y = ((q * xs) >> (2 * f)) + c[:, 0]
+    return y.view(np.uint64)
+
+
+def rotated_lut(alpha, coeffs, r_in):
+    """Interval LUT geometry over x^ = x + r_in: cutpoints [k + 1] (the last is
+    the 2^64 sentinel 0) and payload [k][4] words (c0..c3)."""
+    ivs = []
+    bounds = [int(a) for a in alpha] + [1 << 64]
+    for i in range(len(alpha)):
+        s = (bounds[i] + r_in) & M64
+        e = (bounds[i + 1] + r_in) & M64
+        pay = [int(v) & M64 for v in coeffs[i]]
+        if s < e:
+            ivs.append((s, e, pay))
+        else:
+            ivs.append((s, 0, pay))
+            if e != 0:
+                ivs.append((0, e, pay))
+    ivs.sort(key=lambda t: t[0])
+    cuts = [ivs[0][0]] + [hi for _, hi, _ in ivs]
+    payload = [w for _, _, pay in ivs for w in pay]
+    return np.array(cuts, dtype=np.uint64), np.array(payload, dtype=np.uint64), len(ivs)
+
+
+def _split(v, s):
+    return s & M64, (v - s) & M64
+
+
+class SplineGate:
+    """Dealer material for one spline gate instance over n elements, both
+    parties, resident on the GPU.  Randomness: std::mt19937_64(seed) words
+    for r_in, the Beaver triples and the truncation keys."""
+
+    def __init__(self, n, alpha, coeffs, prg_state, frac_bits=12, seed=7, nonce=1,
+                 device="cuda"):
+        self.n = n
+        self.f = frac_bits
+        self.prg_state = bytes(prg_state)
+        lib = native.load()
+        head = pfss.host_mt19937_64(seed, 2 + 2 * native.TRUNC_RAND_WORDS)
+        r_in = int(head[0])
+        self.rin = _split(r_in, int(head[1]))
+        cuts, payload, k = rotated_lut(alpha, coeffs, r_in)
+        self.intervals = k
+        kb = lib.sufhip_interval_lut_key_bytes(k, 4)
+        seed16 = native.ctypes.create_string_buffer(16)
+        lib.sufhip_seed_from_id(nonce, LUT_TWEAK, seed16)
+        self.lut_key_bytes = kb
+        self.lut = []
+        for party in (0, 1):
+            blob = np.zeros(kb, dtype=np.uint8)
+            native.call("sufhip_interval_lut_build_key", party, nonce, 64, 4, cuts.ctypes.data, k,
+                        payload.ctypes.data, seed16, blob.ctypes.data)
+            self.lut.append(torch.from_numpy(blob.view(np.int64).copy()).to(device).view(torch.uint8))
+        # Beaver triples: a, b uniform, c = a*b; party 0 holds the drawn share.
+        w = pfss.host_mt19937_64(seed + 1000, 3 * 5 * n).reshape(3, 5, n)
+        self.triples = []
+        for j in range(3):
+            a, b, a0, b0, c0 = w[j]
+            c = a * b
+            t0 = np.stack([a0, b0, c0], axis=1)
+            t1 = np.stack([a - a0, b - b0, c - c0], axis=1)
+            self.triples.append(tuple(torch.from_numpy(t.view(np.int64).copy()).to(device)
+                                      for t in (t0, t1)))
+        # Truncation gates: GapARS by f (after the 2nd product) and 2f (after the 3rd).
+        self.trunc = []
+        for j, fb in enumerate((frac_bits, 2 * frac_bits)):
+            rnd = head[2 + j * native.TRUNC_RAND_WORDS: 2 + (j + 1) * native.TRUNC_RAND_WORDS]
+            k0, k1 = pfss.trunc_gen(native.TRUNC_GAPARS, fb, self.prg_state, rnd, device)
+            r = int(rnd[0])
+            self.trunc.append({"f": fb, "keys": (k0, k1), "rin": _split(r, int(rnd[1]))})
+        wb = max(lib.sufhip_trunc_work_bytes(t["f"], n) for t in self.trunc)
+        self.work = torch.empty(max(1, (wb + 15) // 8), dtype=torch.int64, device=device)
+        self.work_bytes = wb
+        # Scratch for the online phase.
+        self.xhat = torch.empty(n, dtype=torch.int64, device=device)
+        self.coef = [torch.empty((n, 4), dtype=torch.int64, device=device) for _ in range(2)]
+        self.u = [torch.empty(n, dtype=torch.int64, device=device) for _ in range(2)]
+        self.y = [torch.empty(n, dtype=torch.int64, device=device) for _ in range(2)]
+
+    def _mul2(self, u, v, tri, u_stride=1, u_off=0, u_add=None, u_add_stride=1, u_add_off=0,
+              u_add_shift=0, z_add=None, z_add_stride=1, z_add_off=0, z_add_shift=0, z=None,
+              zhat=None, open_mask=(0, 0)):
+        a = native.Mul2Args()
+        a.u[0], a.u[1] = _p(u[0]), _p(u[1])
+        a.u_stride, a.u_off = u_stride, u_off
+        if u_add is not None:
+            a.u_add[0], a.u_add[1] = _p(u_add[0]), _p(u_add[1])
+            a.u_add_stride, a.u_add_off, a.u_add_shift = u_add_stride, u_add_off, u_add_shift
+        a.v[0], a.v[1] = _p(v[0]), _p(v[1])
+        a.triples[0], a.triples[1] = _p(tri[0]), _p(tri[1])
+        if z_add is not None:
+            a.z_add[0], a.z_add[1] = _p(z_add[0]), _p(z_add[1])
+            a.z_add_stride, a.z_add_off, a.z_add_shift = z_add_stride, z_add_off, z_add_shift
+        if z is not None:
+            a.z[0], a.z[1] = _p(z[0]), _p(z[1])
+        a.zhat = _p(zhat)
+        a.open_mask[0], a.open_mask[1] = open_mask[0], open_mask[1]
+        native.call("sufhip_mul2", native.ctypes.byref(a), self.n, _stream())
+
+    def _trunc(self, t, xhat, out):
+        for p in (0, 1):
+            native.call("sufhip_trunc_eval", native.TRUNC_GAPARS, t["f"],
+                        pfss._state_buf(self.prg_state), _p(t["keys"][p]), t["keys"][p].numel(),
+                        _p(xhat), self.n, _p(out[p]), _p(self.work), self.work_bytes, _stream())
+
+    def eval2(self, x, out):
+        """x, out: pairs of int64[n] device tensors (party 0, party 1 shares)."""
+        n, f, s = self.n, self.f, _stream()
+        native.call("sufhip_open2_masked", _p(x[0]), _p(x[1]), self.rin[0], self.rin[1], n,
+                    _p(self.xhat), s)
+        for p in (0, 1):
+            native.call("sufhip_interval_lut_eval", _p(self.lut[p]), self.lut_key_bytes, 1,
+                        self.intervals, 4, _p(self.xhat), n, _p(self.coef[p]), s)
+        # u = c3 * x + c2 << f
+        self._mul2(self.coef, x, self.triples[0], u_stride=4, u_off=3, z_add=self.coef,
+                   z_add_stride=4, z_add_off=2, z_add_shift=f, z=self.u)
+        # p^ = u * x + r_t1 (opened)
+        t1, t2 = self.trunc
+        self._mul2(self.u, x, self.triples[1], zhat=self.xhat, open_mask=t1["rin"])
+        self._trunc(t1, self.xhat, self.y)
+        # r^ = (p2 + c1 << f) * x + r_t2 (opened)
+        self._mul2(self.y, x, self.triples[2], u_add=self.coef, u_add_stride=4, u_add_off=1,
+                   u_add_shift=f, zhat=self.xhat, open_mask=t2["rin"])
+        self._trunc(t2, self.xhat, self.y)
+        for p in (0, 1):
+            native.call("sufhip_add_shifted", _p(self.y[p]), _p(self.coef[p]), 4, 0, 0, n,
+                        _p(out[p]), s)
+        return out
