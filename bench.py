@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gates", action="store_true",
-                    help="skip the spline-gate pipeline timing")
+                    help="skip the spline-gate and Beaver matmul pipeline timings")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device-to-device copy kernel 5 times "
                          "(reference point for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -94,6 +94,46 @@ def bench_spline(steps, warmup, n=1 << 20, frac_bits=12):
                              spline.spline_eval_ref(alpha, coeffs, x, frac_bits)))
     return {"ms": ms, "n": n, "frac_bits": frac_bits, "intervals": int(gate.intervals),
             "trunc": "GapARS f=%d and 2f=%d" % (frac_bits, 2 * frac_bits),
+            "steps": steps, "check": "ok" if ok else "MISMATCH"}
+
+
+def bench_matmul(steps, warmup, M=128, K=768, N=3072, frac_bits=12):
+    """Beaver matmul + GapARS truncation for both parties: X [128 x 768] =
+    round(N(0,1) 2^12) (mt(8)), W [768 x 3072] = round(N(0,0.02) 2^12) (mt(9)),
+    both additively shared (mt(108), mt(109)); triples and truncation key from
+    mt(10), mt(11).  Returns ms per evaluation and the reconstruction check."""
+    import numpy as np
+    import torch
+
+    from suf_amd import matmul_gate, pfss
+
+    state = bytes((pfss.host_mt19937_64(3, 128) & np.uint64(0xFF)).astype(np.uint8))
+    X = pfss.host_normal_fixed(8, 1.0, 0.0, frac_bits, M * K)
+    W = pfss.host_normal_fixed(9, 0.02, 0.0, frac_bits, K * N)
+    X0, W0 = pfss.host_mt19937_64(108, M * K), pfss.host_mt19937_64(109, K * N)
+    dev = lambda v: torch.from_numpy(np.ascontiguousarray(v).view(np.int64).copy()).cuda()
+    Xd = [dev(X0), dev((X - X0).astype(np.uint64))]
+    Wd = [dev(W0), dev((W - W0).astype(np.uint64))]
+    g = matmul_gate.BeaverMatmulTrunc(M, K, N, state, frac_bits, seed=10)
+    out = [torch.empty(M * N, dtype=torch.int64, device="cuda") for _ in range(2)]
+    for _ in range(warmup):
+        g.eval2(Xd, Wd, out)
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for s in range(steps):
+        g.eval2(Xd, Wd, out, events=ev[s])
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    mm_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    prod = X.view(np.int64).reshape(M, K) @ W.view(np.int64).reshape(K, N)
+    rec = (out[0].cpu().numpy().view(np.uint64) + out[1].cpu().numpy().view(np.uint64))
+    ok = bool(np.array_equal(rec.astype(np.uint64), (prod >> frac_bits).view(np.uint64).ravel()))
+    macs = 2 * 2 * M * K * N  # both parties, [D | A] x [B' ; E] is a 2K-deep product
+    return {"ms": ms, "shape": [M, K, N], "matmul_ms": mm_ms, "u64_macs": macs,
+            "u64_mac_per_s": macs / (mm_ms / 1e3), "trunc": "GapARS f=%d" % frac_bits,
             "steps": steps, "check": "ok" if ok else "MISMATCH"}
 
 
@@ -278,7 +318,9 @@ def main():
     }
     if not a.no_gates:
         line["spline_gate"] = bench_spline(max(a.steps // 2, 1), 2)
+        line["beaver_matmul_trunc"] = bench_matmul(max(a.steps // 2, 1), 2)
         ok = ok and line["spline_gate"]["check"] == "ok"
+        ok = ok and line["beaver_matmul_trunc"]["check"] == "ok"
     if not a.no_cpu:
         sample = 1 << 14
         g0 = out0[:sample].cpu().numpy()

@@ -170,10 +170,21 @@ size_t sufhip_trunc_work_bytes(int frac_bits, size_t n);
 /* One party: d_y[i] = this party's share of trunc(x_i) given the public
  * d_xhat[i] = x_i + r.  kind / frac_bits must be the ones the key was made
  * with; the party is read from the key.  d_work: >= sufhip_trunc_work_bytes
- * bytes, 16-byte aligned, clobbered. */
+ * bytes, 16-byte aligned, clobbered.  Equals sufhip_trunc_prepare followed
+ * by sufhip_trunc_finish on the same stream. */
 int sufhip_trunc_eval(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,
                       size_t key_bytes, const uint64_t* d_xhat, size_t n, uint64_t* d_y,
                       void* d_work, size_t work_bytes, void* stream);
+/* The two halves of sufhip_trunc_eval.  prepare reads only the key (it fills
+ * d_work with the carry DCF's prefix frontier for a batch of n points), so a
+ * caller may run it before the inputs exist, e.g. on another stream while
+ * earlier rounds execute; finish needs the same n, key and d_work. */
+int sufhip_trunc_prepare(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,
+                         size_t key_bytes, size_t n, void* d_work, size_t work_bytes,
+                         void* stream);
+int sufhip_trunc_finish(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,
+                        size_t key_bytes, const uint64_t* d_xhat, size_t n, uint64_t* d_y,
+                        const void* d_work, size_t work_bytes, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Two-party steps with both parties on one GPU (SUF's local channel: an    */
@@ -186,6 +197,11 @@ int sufhip_trunc_eval(int kind, int frac_bits, const uint8_t* prg_state, const u
 /* d_xhat[i] = (d_x0[i] + r0) + (d_x1[i] + r1): the masked open of a gate input. */
 int sufhip_open2_masked(const uint64_t* d_x0, const uint64_t* d_x1, uint64_t r0, uint64_t r1,
                         size_t n, uint64_t* d_xhat, void* stream);
+
+/* d_open[i] = (d_x0[i] - d_a0[i]) + (d_x1[i] - d_a1[i]): a Beaver open (the
+ * D = X - A and E = W - B of a matmul, attention_block.cpp:452-900). */
+int sufhip_open2_diff(const uint64_t* d_x0, const uint64_t* d_x1, const uint64_t* d_a0,
+                      const uint64_t* d_a1, size_t n, uint64_t* d_open, void* stream);
 
 /* One Beaver product for both parties.  Per element i and party p:
  *   u_p = u[p][i*u_stride + u_off] (+ u_add[p][i*u_add_stride + u_add_off] << u_add_shift)

@@ -321,14 +321,24 @@ struct AesLds4 {
     o0 = last_col(s0, s1, s2, s3, k.x);
     o1 = last_col(s1, s2, s3, s0, k.y);
   }
-  // Cooperative fill; follow with __syncthreads().
-  __device__ __forceinline__ static void fill(uint32_t* lds, const uint32_t* tsrc) {
-    for (int i = threadIdx.x; i < kWords; i += blockDim.x) {
-      const int half = i >> 14;           // 16384 words per 64 KB half
+  // Cooperative fill; follow with __syncthreads().  T is first staged in
+  // LDS (`stage`, 256 words) so that the replication loop reads LDS, not
+  // global memory: the fill then costs a few microseconds even for kernels
+  // with little other work.
+  __device__ __forceinline__ static void fill(uint32_t* lds, uint32_t* stage,
+                                              const uint32_t* tsrc) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) stage[i] = tsrc[i];
+    __syncthreads();
+    // 16-byte stores: words 4q..4q+3 are four copies of one (table, entry).
+    uint4* dst = reinterpret_cast<uint4*>(lds);
+#pragma unroll 4
+    for (int q = threadIdx.x; q < kWords / 4; q += blockDim.x) {
+      const int i = 4 * q;
+      const int half = i >> 14;  // 16384 words per 64 KB half
       const int e = (i >> 6) & 255;
       const int j = 2 * half + ((i >> 5) & 1);
-      const uint32_t v = tsrc[e];
-      lds[i] = j == 0 ? v : rotl32(v, 8 * j);
+      const uint32_t v = rotl32(stage[e], 8 * j);
+      dst[q] = make_uint4(v, v, v, v);
     }
   }
   static void key_layout(const uint32_t rk[44], uint32_t out[44]) {

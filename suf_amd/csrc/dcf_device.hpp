@@ -316,9 +316,10 @@ __device__ __forceinline__ uint64_t add64_finish(const uint8_t* chunk, int in_bi
 
 // Stages the replicated tables and the K_0..K_3 round keys in LDS.
 #define SUFHIP_DCF_LDS_SETUP(PRG)                                  \
-  __shared__ uint32_t tabs[DcfAes::kWords];                        \
+  __shared__ __align__(16) uint32_t tabs[DcfAes::kWords];          \
+  __shared__ uint32_t tstage[256];                                 \
   __shared__ uint4 rkl[4 * 11];                                    \
-  DcfAes::fill(tabs, kTDev.v);                                     \
+  DcfAes::fill(tabs, tstage, kTDev.v);                             \
   fill_round_keys(rkl, (PRG).rk, 4);                               \
   __syncthreads();                                                 \
   const DcfAes aes = DcfAes::make(tabs)

@@ -16,11 +16,16 @@
 // Evaluation of the carry DCF uses a prefix frontier: the walk state after
 // the first d levels depends only on the top d bits of x^_low, so for a
 // broadcast key and a large batch the 2^d frontier states are computed once
-// (one lane each) and every element continues from its prefix.  With d = f
-// the frontier holds the final share of every point of the domain and an
-// element's carry is a single table read.  The results are the same bytes a
-// full walk produces.
+// and every element continues from its prefix.  The first k0 = min(d, 12)
+// levels are walked one node per lane; deeper levels are expanded
+// breadth-first, one child per lane (2 AES per node).  d = min(f,
+// floor(log2 N) - 1, 22) balances the 2^(d+1) expansions against the N (f - d)
+// per-element levels.  With d = f the frontier holds the final share of every
+// point of the domain and an element's carry is a single table read.  The
+// results are the same bytes a full walk produces.
 #include <hip/hip_runtime.h>
+
+#include <string>
 
 #include "dcf_device.hpp"
 #include "suf_hip.h"
@@ -30,7 +35,8 @@ namespace {
 
 constexpr uint32_t kTag = 0x31475453u;  // "STG1"
 constexpr int kHdrBytes = 64;
-constexpr int kMaxFrontierBits = 16;
+constexpr int kMaxFrontierBits = 22;
+constexpr int kWalkFrontierBits = 12;
 
 __host__ __device__ constexpr size_t pad8(size_t v) { return (v + 7) & ~size_t(7); }
 
@@ -39,10 +45,19 @@ size_t dcf_bytes(int in_bits) { return sufhip_dcf_key_bytes(in_bits, 8); }
 int frontier_bits(int f, size_t n) {
   int lg = 0;
   while (lg < 63 && (size_t(1) << (lg + 1)) <= n) ++lg;
+  if (lg < 5) return 0;
   int d = f < kMaxFrontierBits ? f : kMaxFrontierBits;
-  const int cap = lg - 4;
-  if (cap < d) d = cap < 0 ? 0 : cap;
-  return d;
+  return d < lg - 1 ? d : lg - 1;
+}
+
+// Nodes of the walked level (k0) and of the final level (d) in the workspace:
+// level d always lands in the first 2^d slots, the level before it in the
+// 2^(d-1) slots after them.
+int walk_bits(int d) { return d < kWalkFrontierBits ? d : kWalkFrontierBits; }
+
+size_t frontier_nodes(int d) {
+  if (d == 0) return 0;
+  return (size_t(1) << d) + (d > walk_bits(d) ? size_t(1) << (d - 1) : 0);
 }
 
 struct TruncGenArgs {
@@ -94,7 +109,7 @@ struct FrontierArgs {
 
 __global__ void __launch_bounds__(kDcfBlock) trunc_frontier_kernel(FrontierArgs a) {
   SUFHIP_DCF_LDS_SETUP(a.prg);
-  const uint32_t v = blockIdx.x * kDcfBlock + threadIdx.x;
+  const uint32_t v = blockIdx.x * blockDim.x + threadIdx.x;
   if (v >= (1u << a.d) || !(a.key[7] & 1)) return;
   const uint32_t party = a.key[6] & 1u;
   const uint8_t* chunk = a.key + kHdrBytes + 8;
@@ -107,6 +122,40 @@ __global__ void __launch_bounds__(kDcfBlock) trunc_frontier_kernel(FrontierArgs 
   } else {
     a.nodes[2 * v] = make_uint4(st.s0, st.s1, st.s2, st.s3);
     a.nodes[2 * v + 1] = make_uint4(uint32_t(st.v), uint32_t(st.v >> 32), st.t, 0);
+  }
+}
+
+// One breadth-first level: nodes at depth `level` (in) -> depth level + 1
+// (out), one child per lane.  When level + 1 == f the children are final
+// shares.
+struct ExpandArgs {
+  Prg4 prg;
+  const uint8_t* key;
+  const uint4* in;
+  uint4* out;
+  int f;
+  int level;
+};
+
+__global__ void __launch_bounds__(kDcfBlock) trunc_expand_kernel(ExpandArgs a) {
+  SUFHIP_DCF_LDS_SETUP(a.prg);
+  if (!(a.key[7] & 1)) return;
+  const uint32_t party = a.key[6] & 1u;
+  const uint8_t* chunk = a.key + kHdrBytes + 8;
+  const uint32_t count = 2u << a.level;
+  for (uint32_t c = blockIdx.x * blockDim.x + threadIdx.x; c < count;
+       c += gridDim.x * blockDim.x) {
+    const uint4 s = a.in[2 * (c >> 1)], q = a.in[2 * (c >> 1) + 1];
+    Add64State st{s.x, s.y, s.z, s.w, q.z, uint64_t(q.x) | uint64_t(q.y) << 32};
+    const uint64_t x = uint64_t(c & 1u) << (a.f - 1 - a.level);
+    add64_walk(aes, rkl, chunk, a.f, a.level, a.level + 1, x, party, st);
+    if (a.level + 1 == a.f) {
+      const uint64_t out = add64_finish(chunk, a.f, party, st);
+      a.out[2 * c + 1] = make_uint4(uint32_t(out), uint32_t(out >> 32), 0, 0);
+    } else {
+      a.out[2 * c] = make_uint4(st.s0, st.s1, st.s2, st.s3);
+      a.out[2 * c + 1] = make_uint4(uint32_t(st.v), uint32_t(st.v >> 32), st.t, 0);
+    }
   }
 }
 
@@ -230,6 +279,22 @@ __global__ void __launch_bounds__(256) trunc_eval_table_kernel(TruncEvalArgs a) 
   }
 }
 
+// Launch shape for the frontier kernels: spread `count` lanes over all CUs
+// (one workgroup per CU, the AES tables fill its LDS), 64..512 lanes each.
+int spread_grid(size_t count, unsigned int* grid, unsigned int* block) {
+  int dev = 0, cus = 0;
+  SUFHIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
+  SUFHIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+               "hipDeviceGetAttribute(CU count)");
+  size_t per = (count + size_t(cus) - 1) / size_t(cus);
+  per = (per + 63) / 64 * 64;
+  const size_t b = per < 64 ? 64 : (per > size_t(kDcfBlock) ? size_t(kDcfBlock) : per);
+  const size_t g = (count + b - 1) / b;
+  *block = unsigned(b);
+  *grid = unsigned(g < size_t(cus) ? g : size_t(cus));
+  return SUFHIP_OK;
+}
+
 bool valid_kind(int kind) {
   return kind == SUFHIP_TRUNC_TR || kind == SUFHIP_TRUNC_ARS || kind == SUFHIP_TRUNC_GAPARS;
 }
@@ -304,37 +369,75 @@ int sufhip_trunc_gen(int kind, int frac_bits, const uint8_t* prg_state, const ui
 
 size_t sufhip_trunc_work_bytes(int frac_bits, size_t n) {
   if (frac_bits < 1 || frac_bits > 62) return 0;
-  const int d = frontier_bits(frac_bits, n);
-  return d > 0 ? size_t(32) << d : 0;
+  return frontier_nodes(frontier_bits(frac_bits, n)) * 32;
 }
 
-int sufhip_trunc_eval(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,
-                      size_t key_bytes, const uint64_t* d_xhat, size_t n, uint64_t* d_y,
-                      void* d_work, size_t work_bytes, void* stream) {
-  SUFHIP_REQUIRE(valid_kind(kind), "sufhip_trunc_eval: unknown kind");
-  SUFHIP_REQUIRE(frac_bits >= 1 && frac_bits <= 62, "sufhip_trunc_eval: frac_bits out of [1, 62]");
+// Shared argument checks of the evaluation entry points.
+static int trunc_check(const char* fn, int kind, int frac_bits, const uint8_t* prg_state,
+                       const uint8_t* d_key, size_t key_bytes, size_t n, const void* d_work,
+                       size_t work_bytes) {
+  SUFHIP_REQUIRE(valid_kind(kind), std::string(fn) + ": unknown kind");
+  SUFHIP_REQUIRE(frac_bits >= 1 && frac_bits <= 62, std::string(fn) + ": frac_bits out of [1, 62]");
   SUFHIP_REQUIRE(key_bytes == sufhip_trunc_key_bytes(kind, frac_bits),
-                 "sufhip_trunc_eval: key_bytes does not match (kind, frac_bits)");
-  if (n == 0) return SUFHIP_OK;
-  SUFHIP_REQUIRE(n < kMaxElems, "sufhip_trunc_eval: n too large");
-  SUFHIP_REQUIRE(prg_state && d_key && d_xhat && d_y, "sufhip_trunc_eval: null pointer");
+                 std::string(fn) + ": key_bytes does not match (kind, frac_bits)");
+  SUFHIP_REQUIRE(n < kMaxElems, std::string(fn) + ": n too large");
+  SUFHIP_REQUIRE(prg_state && d_key, std::string(fn) + ": null pointer");
   SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_key) & 7) == 0,
-                 "sufhip_trunc_eval: key must be 8-byte aligned");
-  const int d = frontier_bits(frac_bits, n);
+                 std::string(fn) + ": key must be 8-byte aligned");
   const size_t need = sufhip_trunc_work_bytes(frac_bits, n);
   SUFHIP_REQUIRE(work_bytes >= need && (need == 0 || d_work),
-                 "sufhip_trunc_eval: workspace smaller than sufhip_trunc_work_bytes()");
+                 std::string(fn) + ": workspace smaller than sufhip_trunc_work_bytes()");
   SUFHIP_REQUIRE(need == 0 || (reinterpret_cast<uintptr_t>(d_work) & 15) == 0,
-                 "sufhip_trunc_eval: workspace must be 16-byte aligned");
+                 std::string(fn) + ": workspace must be 16-byte aligned");
+  return SUFHIP_OK;
+}
+
+int sufhip_trunc_prepare(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,
+                         size_t key_bytes, size_t n, void* d_work, size_t work_bytes,
+                         void* stream) {
+  if (int rc = trunc_check("sufhip_trunc_prepare", kind, frac_bits, prg_state, d_key, key_bytes,
+                           n, d_work, work_bytes))
+    return rc;
+  const int d = frontier_bits(frac_bits, n);
+  if (n == 0 || d == 0) return SUFHIP_OK;
   hipStream_t s = as_stream(stream);
   Prg4 prg;
   fill_prg4(prg_state, &prg);
-  if (d > 0) {
-    FrontierArgs fa{prg, d_key, static_cast<uint4*>(d_work), frac_bits, d};
-    const unsigned int blocks = ((1u << d) + kDcfBlock - 1) / kDcfBlock;
-    hipLaunchKernelGGL(trunc_frontier_kernel, dim3(blocks), dim3(kDcfBlock), 0, s, fa);
-    if (int rc = check_launch("trunc_frontier_kernel")) return rc;
+  // Walk to depth k0, then expand level by level, alternating between the
+  // two workspace regions so that depth d ends in the first one.
+  uint4* lvl[2] = {static_cast<uint4*>(d_work), static_cast<uint4*>(d_work) + 2 * (size_t(1) << d)};
+  const int k0 = walk_bits(d);
+  int cur = (d - k0) & 1;
+  FrontierArgs fa{prg, d_key, lvl[cur], frac_bits, k0};
+  unsigned int g = 0, b = 0;
+  if (int rc = spread_grid(size_t(1) << k0, &g, &b)) return rc;
+  // The walk kernel is one lane per node (no stride loop): cover all nodes.
+  g = unsigned(((size_t(1) << k0) + b - 1) / b);
+  hipLaunchKernelGGL(trunc_frontier_kernel, dim3(g), dim3(b), 0, s, fa);
+  if (int rc = check_launch("trunc_frontier_kernel")) return rc;
+  for (int level = k0; level < d; ++level) {
+    ExpandArgs ea{prg, d_key, lvl[cur], lvl[cur ^ 1], frac_bits, level};
+    unsigned int eg = 0, eb = 0;
+    if (int rc = spread_grid(size_t(2) << level, &eg, &eb)) return rc;
+    hipLaunchKernelGGL(trunc_expand_kernel, dim3(eg), dim3(eb), 0, s, ea);
+    if (int rc = check_launch("trunc_expand_kernel")) return rc;
+    cur ^= 1;
   }
+  return SUFHIP_OK;
+}
+
+int sufhip_trunc_finish(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,
+                        size_t key_bytes, const uint64_t* d_xhat, size_t n, uint64_t* d_y,
+                        const void* d_work, size_t work_bytes, void* stream) {
+  if (int rc = trunc_check("sufhip_trunc_finish", kind, frac_bits, prg_state, d_key, key_bytes,
+                           n, d_work, work_bytes))
+    return rc;
+  if (n == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(d_xhat && d_y, "sufhip_trunc_finish: null pointer");
+  const int d = frontier_bits(frac_bits, n);
+  hipStream_t s = as_stream(stream);
+  Prg4 prg;
+  fill_prg4(prg_state, &prg);
   TruncEvalArgs a{prg, d_key, d_xhat, d_y, static_cast<const uint4*>(d_work), n, frac_bits, d};
   if (kind == SUFHIP_TRUNC_GAPARS && d == frac_bits) {
     size_t blocks = (n + 255) / 256;
@@ -353,6 +456,21 @@ int sufhip_trunc_eval(int kind, int frac_bits, const uint8_t* prg_state, const u
     hipLaunchKernelGGL(trunc_eval_aes_kernel<SUFHIP_TRUNC_ARS>, dim3(g), dim3(kDcfBlock), 0, s,
                        a);
   return check_launch("trunc_eval_aes_kernel");
+}
+
+int sufhip_trunc_eval(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,
+                      size_t key_bytes, const uint64_t* d_xhat, size_t n, uint64_t* d_y,
+                      void* d_work, size_t work_bytes, void* stream) {
+  if (int rc = trunc_check("sufhip_trunc_eval", kind, frac_bits, prg_state, d_key, key_bytes, n,
+                           d_work, work_bytes))
+    return rc;
+  if (n == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(d_xhat && d_y, "sufhip_trunc_eval: null pointer");
+  if (int rc = sufhip_trunc_prepare(kind, frac_bits, prg_state, d_key, key_bytes, n, d_work,
+                                    work_bytes, stream))
+    return rc;
+  return sufhip_trunc_finish(kind, frac_bits, prg_state, d_key, key_bytes, d_xhat, n, d_y, d_work,
+                             work_bytes, stream);
 }
 
 }  // extern "C"

@@ -4,6 +4,8 @@
 // local work of both parties for one protocol round plus the open, in one
 // pass over HBM:
 //   open2_masked  x^ = (x_0 + r_0) + (x_1 + r_1)          (a gate's masked open)
+//   open2_diff    d = (x_0 - a_0) + (x_1 - a_1)            (a Beaver open, e.g. D, E
+//                 of the Beaver matmul)
 //   mul2          Beaver product of MulTask (include/runtime/phase_tasks.hpp:
 //                 198-402) with the d/e open inline, optional pre-add on the
 //                 left factor and post-add on the product (the affine steps
@@ -35,6 +37,14 @@ __global__ void __launch_bounds__(kBlock)
   const size_t stride = size_t(gridDim.x) * kBlock;
   for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
     xhat[i] = x0[i] + x1[i] + r;
+}
+
+__global__ void __launch_bounds__(kBlock)
+    open2_diff_kernel(const uint64_t* x0, const uint64_t* x1, const uint64_t* a0,
+                      const uint64_t* a1, size_t n, uint64_t* d) {
+  const size_t stride = size_t(gridDim.x) * kBlock;
+  for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+    d[i] = (x0[i] - a0[i]) + (x1[i] - a1[i]);
 }
 
 __global__ void __launch_bounds__(kBlock) mul2_kernel(sufhip_mul2_args a, size_t n) {
@@ -96,6 +106,16 @@ int sufhip_open2_masked(const uint64_t* d_x0, const uint64_t* d_x1, uint64_t r0,
   hipLaunchKernelGGL(open2_masked_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream),
                      d_x0, d_x1, r0 + r1, n, d_xhat);
   return check_launch("open2_masked_kernel");
+}
+
+int sufhip_open2_diff(const uint64_t* d_x0, const uint64_t* d_x1, const uint64_t* d_a0,
+                      const uint64_t* d_a1, size_t n, uint64_t* d_open, void* stream) {
+  if (n == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(n < kMaxElems, "sufhip_open2_diff: n too large");
+  SUFHIP_REQUIRE(d_x0 && d_x1 && d_a0 && d_a1 && d_open, "sufhip_open2_diff: null pointer");
+  hipLaunchKernelGGL(open2_diff_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream),
+                     d_x0, d_x1, d_a0, d_a1, n, d_open);
+  return check_launch("open2_diff_kernel");
 }
 
 int sufhip_mul2(const sufhip_mul2_args* args, size_t n, void* stream) {

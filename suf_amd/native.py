@@ -64,7 +64,11 @@ _SIGS = {
     "sufhip_trunc_work_bytes": (c_sz, [c_int, c_sz]),
     "sufhip_trunc_eval": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp, c_sz,
                                   c_vp]),
+    "sufhip_trunc_prepare": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_sz, c_vp, c_sz, c_vp]),
+    "sufhip_trunc_finish": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp, c_sz,
+                                    c_vp]),
     "sufhip_open2_masked": (c_int, [c_vp, c_vp, c_u64, c_u64, c_sz, c_vp, c_vp]),
+    "sufhip_open2_diff": (c_int, [c_vp, c_vp, c_vp, c_vp, c_sz, c_vp, c_vp]),
     "sufhip_mul2": (c_int, [c_vp, c_sz, c_vp]),
     "sufhip_add_shifted": (c_int, [c_vp, c_vp, c_sz, c_sz, c_int, c_sz, c_vp, c_vp]),
     "sufhip_seed_from_id": (None, [c_u64, c_u64, c_vp]),

@@ -15,7 +15,8 @@ The output mask r_out of spline gates is 0 (include/gates/silu_composite.hpp:
 92), so the LUT's coefficient shares are used directly.
 
 Every step runs in libsuf_hip.so: open2_masked, interval_lut_eval, mul2,
-trunc_eval, add_shifted.  The dealer builds keys with the library's key
+trunc_prepare / trunc_finish, add_shifted.  The truncations' key-only
+precomputation runs on side streams, overlapped with the first rounds.  The dealer builds keys with the library's key
 builders and host std::mt19937_64 streams.
 """
 import numpy as np
@@ -140,9 +141,14 @@ class SplineGate:
             k0, k1 = pfss.trunc_gen(native.TRUNC_GAPARS, fb, self.prg_state, rnd, device)
             r = int(rnd[0])
             self.trunc.append({"f": fb, "keys": (k0, k1), "rin": _split(r, int(rnd[1]))})
-        wb = max(lib.sufhip_trunc_work_bytes(t["f"], n) for t in self.trunc)
-        self.work = torch.empty(max(1, (wb + 15) // 8), dtype=torch.int64, device=device)
-        self.work_bytes = wb
+        # Per (truncation, party) workspace for the key-only frontier, which
+        # eval2 computes on one side stream per party while the LUT and the
+        # first two products run.
+        for t in self.trunc:
+            t["work_bytes"] = lib.sufhip_trunc_work_bytes(t["f"], n)
+            t["work"] = [torch.empty(max(2, (t["work_bytes"] + 15) // 8), dtype=torch.int64,
+                                     device=device) for _ in range(2)]
+        self.side = [torch.cuda.Stream(device=device) for _ in range(2)]
         # Scratch for the online phase.
         self.xhat = torch.empty(n, dtype=torch.int64, device=device)
         self.coef = [torch.empty((n, 4), dtype=torch.int64, device=device) for _ in range(2)]
@@ -169,15 +175,35 @@ class SplineGate:
         a.open_mask[0], a.open_mask[1] = open_mask[0], open_mask[1]
         native.call("sufhip_mul2", native.ctypes.byref(a), self.n, _stream())
 
+    def _prepare(self):
+        """Key-only halves of both truncations, one side stream per party."""
+        start = torch.cuda.Event()
+        start.record()
+        done = []
+        for p in (0, 1):
+            side = self.side[p]
+            side.wait_event(start)
+            for t in self.trunc:
+                native.call("sufhip_trunc_prepare", native.TRUNC_GAPARS, t["f"],
+                            pfss._state_buf(self.prg_state), _p(t["keys"][p]),
+                            t["keys"][p].numel(), self.n, _p(t["work"][p]), t["work_bytes"],
+                            side.cuda_stream)
+            ev = torch.cuda.Event()
+            ev.record(side)
+            done.append(ev)
+        return done
+
     def _trunc(self, t, xhat, out):
         for p in (0, 1):
-            native.call("sufhip_trunc_eval", native.TRUNC_GAPARS, t["f"],
+            native.call("sufhip_trunc_finish", native.TRUNC_GAPARS, t["f"],
                         pfss._state_buf(self.prg_state), _p(t["keys"][p]), t["keys"][p].numel(),
-                        _p(xhat), self.n, _p(out[p]), _p(self.work), self.work_bytes, _stream())
+                        _p(xhat), self.n, _p(out[p]), _p(t["work"][p]), t["work_bytes"],
+                        _stream())
 
     def eval2(self, x, out):
         """x, out: pairs of int64[n] device tensors (party 0, party 1 shares)."""
         n, f, s = self.n, self.f, _stream()
+        prepared = self._prepare()
         native.call("sufhip_open2_masked", _p(x[0]), _p(x[1]), self.rin[0], self.rin[1], n,
                     _p(self.xhat), s)
         for p in (0, 1):
@@ -189,6 +215,8 @@ class SplineGate:
         # p^ = u * x + r_t1 (opened)
         t1, t2 = self.trunc
         self._mul2(self.u, x, self.triples[1], zhat=self.xhat, open_mask=t1["rin"])
+        for ev in prepared:
+            torch.cuda.current_stream().wait_event(ev)
         self._trunc(t1, self.xhat, self.y)
         # r^ = (p2 + c1 << f) * x + r_t2 (opened)
         self._mul2(self.y, x, self.triples[2], u_add=self.coef, u_add_stride=4, u_add_off=1,

@@ -45,10 +45,12 @@ def test_trunc_key_bytes_match_oracle(kind, f):
 
 def test_trunc_workspace_sizes():
     lib = native.load()
-    # Frontier depth min(f, 16, floor(log2 n) - 4), 32 bytes per node.
+    # Frontier depth d = min(f, floor(log2 n) - 1, 22), none below n = 32;
+    # 32 bytes per node, 2^d nodes plus 2^(d-1) when levels beyond 12 are expanded.
     assert lib.sufhip_trunc_work_bytes(12, 1 << 20) == 32 << 12
-    assert lib.sufhip_trunc_work_bytes(24, 1 << 20) == 32 << 16
-    assert lib.sufhip_trunc_work_bytes(24, 3000) == 32 << 7
+    assert lib.sufhip_trunc_work_bytes(24, 1 << 20) == 32 * ((1 << 19) + (1 << 18))
+    assert lib.sufhip_trunc_work_bytes(24, 3000) == 32 << 10
+    assert lib.sufhip_trunc_work_bytes(40, 1 << 30) == 32 * ((1 << 22) + (1 << 21))
     assert lib.sufhip_trunc_work_bytes(12, 31) == 0
     assert lib.sufhip_trunc_work_bytes(12, 0) == 0
 

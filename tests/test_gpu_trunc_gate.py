@@ -76,10 +76,12 @@ def _run(kind, f, n, r, seed, oracle_sample):
 
 
 @pytest.mark.parametrize("kind,f,n", [
-    (ol.TRUNC_GAPARS, 12, 1 << 16),   # full-domain table (frontier d = f = 12)
-    (ol.TRUNC_GAPARS, 24, 1 << 16),   # prefix frontier d = 12 < f, 12 levels per element
+    (ol.TRUNC_GAPARS, 12, 1 << 16),   # full-domain table, walked (d = f = 12)
+    (ol.TRUNC_GAPARS, 24, 1 << 16),   # d = 15: walk 12 + 3 expanded levels, 9 per element
+    (ol.TRUNC_GAPARS, 24, 1 << 15),   # d = 14: an even number of expanded levels
+    (ol.TRUNC_GAPARS, 14, 1 << 16),   # d = f = 14: the last expanded level is final
     (ol.TRUNC_GAPARS, 12, 20),        # no frontier (d = 0)
-    (ol.TRUNC_GAPARS, 30, 3000),      # d = 7
+    (ol.TRUNC_GAPARS, 30, 3000),      # d = 10, walked only
     (ol.TRUNC_GAPARS, 1, 1000),       # f = 1: table of 2 entries
     (ol.TRUNC_TR, 12, 2000),          # carry frontier + 64-bit wrap key
     (ol.TRUNC_ARS, 7, 300),           # carry, wrap and sign keys
