@@ -328,6 +328,19 @@ int sufhip_beaver_matmul2d(int party, const uint64_t* d_D_open, const uint64_t* 
                            const uint64_t* d_C_tri_share, int M, int K, int N, int w_transposed,
                            int has_scale, int64_t mul_const, int mul_shift, uint64_t* d_out,
                            void* stream);
+/* The same product as sufhip_beaver_matmul2d (w_transposed = 0, no scale) on
+ * the int8 matrix cores: operands split into balanced base-256 digits and
+ * the 36 digit-plane GEMMs with i + j < 8 accumulated exactly in int32
+ * (v_mfma_i32_32x32x32_i8), recombined mod 2^64.  Requires M % 32 == 0,
+ * N % 64 == 0, K % 32 == 0 and K <= 8191 (work_bytes() is 0 otherwise).
+ * d_work: 16-byte aligned device scratch of
+ * sufhip_beaver_matmul2d_mfma_work_bytes(M, K, N) bytes (the digit planes,
+ * 16 (M + N) K bytes, plus k-slice partial sums for small grids), clobbered. */
+size_t sufhip_beaver_matmul2d_mfma_work_bytes(int M, int K, int N);
+int sufhip_beaver_matmul2d_mfma(int party, const uint64_t* d_D_open, const uint64_t* d_E_open,
+                                const uint64_t* d_A_tri_share, const uint64_t* d_B_tri_share,
+                                const uint64_t* d_C_tri_share, int M, int K, int N,
+                                uint64_t* d_out, void* d_work, size_t work_bytes, void* stream);
 /* launch_beaver_matmul2d_batched_kernel (:151-166): D [batches][M x K],
  * E [batches][K x N]; the same A, B, C for every batch; out [batches][M x N]. */
 int sufhip_beaver_matmul2d_batched(int party, const uint64_t* d_D_open, const uint64_t* d_E_open,

@@ -6,7 +6,9 @@ Protocol (the matmul tasks of src/nn/attention_block.cpp:452-900 and the CPU
 form src/nn/matmul_beaver.cpp:139-161, then SUF's AutoTrunc lowered to
 GapARS):
   D = open(X - A), E = open(W - B)
-  Z_p = C_p + D*B_p + A_p*E (+ D*E for party 0)      (launch_beaver_matmul2d)
+  Z_p = C_p + D*B_p + A_p*E (+ D*E for party 0)      (launch_beaver_matmul2d;
+                                                     int8-limb MFMA form when the
+                                                     shape allows)
   Y_p = trunc_f(open(Z + r))                         (truncation gate)
 Every step runs in libsuf_hip.so; the dealer's triple product C = A*B is
 computed by the same matmul kernel (party 0 form with C = 0, D = A, E = B).
@@ -31,16 +33,26 @@ def _dev(a):
     return torch.from_numpy(np.ascontiguousarray(a).view(np.int64).copy()).cuda()
 
 
-def _matmul(party, D, E, A, B, C, M, K, N, out):
-    native.call("sufhip_beaver_matmul2d", party, _p(D), _p(E), _p(A), _p(B), _p(C), M, K, N, 0, 0,
-                0, 0, _p(out), _stream())
+def _matmul(party, D, E, A, B, C, M, K, N, out, work=None):
+    """The int8-limb matrix-core product when the shape allows it and a
+    workspace is given, else the VALU kernel (same result bits)."""
+    if work is not None:
+        native.call("sufhip_beaver_matmul2d_mfma", party, _p(D), _p(E), _p(A), _p(B), _p(C), M, K,
+                    N, _p(out), _p(work), work.numel() * 8, _stream())
+    else:
+        native.call("sufhip_beaver_matmul2d", party, _p(D), _p(E), _p(A), _p(B), _p(C), M, K, N, 0,
+                    0, 0, 0, _p(out), _stream())
+
+
+def mfma_ok(M, K, N):
+    return M % 32 == 0 and N % 64 == 0 and K % 32 == 0 and K <= 8191
 
 
 class BeaverMatmulTrunc:
     """Dealer material (triples, truncation keys) for Y = trunc_f(X W), both
     parties.  Randomness: std::mt19937_64(seed) streams."""
 
-    def __init__(self, M, K, N, prg_state, frac_bits=12, seed=10):
+    def __init__(self, M, K, N, prg_state, frac_bits=12, seed=10, use_mfma=True):
         self.M, self.K, self.N, self.f = M, K, N, frac_bits
         self.prg_state = bytes(prg_state)
         lib = native.load()
@@ -73,6 +85,10 @@ class BeaverMatmulTrunc:
         self.E = torch.empty(K * N, dtype=torch.int64, device="cuda")
         self.Z = [torch.empty(M * N, dtype=torch.int64, device="cuda") for _ in range(2)]
         self.zhat = torch.empty(M * N, dtype=torch.int64, device="cuda")
+        self.mm_work = None
+        if use_mfma and mfma_ok(M, K, N):
+            wb = lib.sufhip_beaver_matmul2d_mfma_work_bytes(M, K, N)
+            self.mm_work = torch.empty((wb + 7) // 8, dtype=torch.int64, device="cuda")
 
     def eval2(self, X, W, out, events=None):
         """X, W, out: pairs of device int64 tensors (party shares).  events:
@@ -96,7 +112,8 @@ class BeaverMatmulTrunc:
         if events:
             events[0].record()
         for p in (0, 1):
-            _matmul(p, self.D, self.E, self.A[p], self.B[p], self.C[p], M, K, N, self.Z[p])
+            _matmul(p, self.D, self.E, self.A[p], self.B[p], self.C[p], M, K, N, self.Z[p],
+                    self.mm_work)
         if events:
             events[1].record()
         native.call("sufhip_open2_masked", _p(self.Z[0]), _p(self.Z[1]), self.rin[0], self.rin[1],

@@ -67,6 +67,9 @@ _SIGS = {
     "sufhip_trunc_prepare": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_sz, c_vp, c_sz, c_vp]),
     "sufhip_trunc_finish": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp, c_sz,
                                     c_vp]),
+    "sufhip_beaver_matmul2d_mfma_work_bytes": (c_sz, [c_int, c_int, c_int]),
+    "sufhip_beaver_matmul2d_mfma": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int,
+                                            c_vp, c_vp, c_sz, c_vp]),
     "sufhip_open2_masked": (c_int, [c_vp, c_vp, c_u64, c_u64, c_sz, c_vp, c_vp]),
     "sufhip_open2_diff": (c_int, [c_vp, c_vp, c_vp, c_vp, c_sz, c_vp, c_vp]),
     "sufhip_mul2": (c_int, [c_vp, c_sz, c_vp]),

@@ -76,3 +76,40 @@ def test_config3_shape_reconstructs_xw():
     z = outs[0] + outs[1]
     xw = ol.beaver_matmul(1, zeros_d, W, X, zeros_e, np.zeros(M * N, np.uint64), 1, M, K, N)
     assert np.array_equal(z, xw)
+
+
+@pytest.mark.parametrize("M,K,N", [(32, 32, 64), (64, 96, 128), (128, 768, 3072), (96, 3072, 64)])
+def test_mfma_limb_matmul_matches_valu_and_oracle(M, K, N):
+    say("mfma limb matmul %dx%dx%d" % (M, K, N))
+    P = Pins()
+    rng = np.random.default_rng(M + 7 * K + 13 * N)
+    D = rng_u64(rng, M * K)
+    E = rng_u64(rng, K * N)
+    A = rng_u64(rng, M * K)
+    B = rng_u64(rng, K * N)
+    C = rng_u64(rng, M * N)
+    # Digit edge cases: all-ones (every digit -1 with borrows), 2^63, 0x80 bytes.
+    D[:8] = [2**64 - 1, 2**63, 0x8080808080808080, 0x7F7F7F7F7F7F7F7F, 1, 0, 0xFF, 2**63 - 1]
+    E[:8] = [2**64 - 1, 0x8080808080808080, 2**63, 3, 0, 2**64 - 1, 0x80, 0xFFFFFFFF00000000]
+    lib = native.load()
+    wb = lib.sufhip_beaver_matmul2d_mfma_work_bytes(M, K, N)
+    work = torch.empty((wb + 7) // 8, dtype=torch.int64, device="cuda")
+    for party in (0, 1):
+        out = torch.empty(M * N, dtype=torch.int64, device="cuda")
+        ref = torch.empty(M * N, dtype=torch.int64, device="cuda")
+        native.call("sufhip_beaver_matmul2d_mfma", party, P(D), P(E), P(A), P(B), P(C), M, K, N,
+                    out.data_ptr(), work.data_ptr(), wb, None)
+        native.call("sufhip_beaver_matmul2d", party, P(D), P(E), P(A), P(B), P(C), M, K, N, 0, 0,
+                    0, 0, ref.data_ptr(), None)
+        torch.cuda.synchronize()
+        got = u64(out)
+        assert np.array_equal(got, u64(ref)), party
+        if M * N * K <= 64 * 96 * 128:
+            assert np.array_equal(got, ol.beaver_matmul(party, D, E, A, B, C, 1, M, K, N))
+
+
+def test_mfma_limb_matmul_rejects_bad_shapes():
+    lib = native.load()
+    for M, K, N in [(33, 32, 64), (32, 31, 64), (32, 32, 96), (32, 8192, 64)]:
+        rc = lib.sufhip_beaver_matmul2d_mfma(0, 1, 1, 1, 1, 1, M, K, N, 1, 16, 1 << 30, None)
+        assert rc == -1  # SUFHIP_ERR_INVALID, before any device work
