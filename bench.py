@@ -61,7 +61,7 @@ def calibrate_copy():
     print(json.dumps({"calibrate_copy_bytes": n, "launches": 5}), flush=True)
 
 
-def bench_spline(steps, warmup, n=1 << 20, frac_bits=12):
+def bench_spline(steps, warmup, n=1 << 20, frac_bits=12, cpu_seconds=0.0):
     """The spline gate (interval LUT + three Beaver products + GapARS by f and
     2f) for both parties on N = 2^20 inputs x = clip(3 N(0,1), +-8) in Q12
     (Box-Muller on mt(5)); coefficients from mt(6); dealer randomness mt(7).
@@ -92,12 +92,73 @@ def bench_spline(steps, warmup, n=1 << 20, frac_bits=12):
     rec = (out[0].cpu().numpy().view(np.uint64) + out[1].cpu().numpy().view(np.uint64))
     ok = bool(np.array_equal(rec.astype(np.uint64),
                              spline.spline_eval_ref(alpha, coeffs, x, frac_bits)))
-    return {"ms": ms, "n": n, "frac_bits": frac_bits, "intervals": int(gate.intervals),
-            "trunc": "GapARS f=%d and 2f=%d" % (frac_bits, 2 * frac_bits),
-            "steps": steps, "check": "ok" if ok else "MISMATCH"}
+    res = {"ms": ms, "n": n, "frac_bits": frac_bits, "intervals": int(gate.intervals),
+           "trunc": "GapARS f=%d and 2f=%d" % (frac_bits, 2 * frac_bits),
+           "steps": steps, "check": "ok" if ok else "MISMATCH"}
+    if cpu_seconds > 0:
+        res["cpu_baseline"] = cpu_spline_baseline(gate, state, x0, x1,
+                                                  [out[0].cpu().numpy(), out[1].cpu().numpy()],
+                                                  cpu_seconds)
+    return res
 
 
-def bench_matmul(steps, warmup, M=128, K=768, N=3072, frac_bits=12):
+def cpu_spline_baseline(gate, state, x0, x1, gpu_out, seconds):
+    """The same two-party spline gate on the host with the oracle's plain-C
+    restatement of each step (interval LUT, Beaver products, truncation gate
+    with its DCF walks), one thread, on consecutive 1024-element chunks of the
+    batch until the time budget is used; shares compared with the GPU's."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as ol
+
+    prg = ol.Prg(state)
+    f = gate.f
+    lut = [gate.lut[p].cpu().numpy() for p in (0, 1)]
+    tri = [[t.cpu().numpy().view(np.uint64).reshape(-1, 3) for t in pair] for pair in gate.triples]
+    tk = [[k.cpu().numpy() for k in t["keys"]] for t in gate.trunc]
+    rin = sum(gate.rin) & ((1 << 64) - 1)
+    t_rin = [sum(t["rin"]) & ((1 << 64) - 1) for t in gate.trunc]
+    sh = np.uint64(f)
+    chunk, done, mism = 1024, 0, 0
+    t0 = time.perf_counter()
+    while done + chunk <= x0.size:
+        sl = slice(done, done + chunk)
+        a0, a1 = x0[sl], x1[sl]
+        xhat = (a0 + a1 + np.uint64(rin)).astype(np.uint64)
+        C = [ol.lut_eval(lut[p], gate.lut_key_bytes, 1, xhat, 4, idx0=done).reshape(chunk, 4)
+             for p in (0, 1)]
+
+        def mul(u, v, t):
+            t = [t[0][sl], t[1][sl]]
+            d = (u[0] - t[0][:, 0]) + (u[1] - t[1][:, 0])
+            e = (v[0] - t[0][:, 1]) + (v[1] - t[1][:, 1])
+            return [ol.beaver_mul(p, t[p][:, 0], t[p][:, 1], t[p][:, 2], d, e) for p in (0, 1)]
+
+        u = mul([C[0][:, 3], C[1][:, 3]], [a0, a1], tri[0])
+        u = [u[p] + (C[p][:, 2] << sh) for p in (0, 1)]
+        pz = mul(u, [a0, a1], tri[1])
+        phat = (pz[0] + pz[1] + np.uint64(t_rin[0])).astype(np.uint64)
+        y = [ol.trunc_eval(prg, ol.TRUNC_GAPARS, f, tk[0][p], phat) for p in (0, 1)]
+        q = [y[p] + (C[p][:, 1] << sh) for p in (0, 1)]
+        rz = mul(q, [a0, a1], tri[2])
+        rhat = (rz[0] + rz[1] + np.uint64(t_rin[1])).astype(np.uint64)
+        y2 = [ol.trunc_eval(prg, ol.TRUNC_GAPARS, 2 * f, tk[1][p], rhat) for p in (0, 1)]
+        for p in (0, 1):
+            mism += int(np.count_nonzero((y2[p] + C[p][:, 0]).astype(np.uint64) !=
+                                         gpu_out[p][sl].view(np.uint64)))
+        done += chunk
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": done / dt, "unit": "gate elements/s (both parties)", "cores": 1,
+            "kind": "port", "ms_per_2p20": (1 << 20) / (done / dt) * 1e3,
+            "sample": "%d of the 2^20 elements (oracle C restatement of LUT, Beaver and "
+                      "truncation-gate steps, one thread); shares compared with the GPU: "
+                      "%d mismatches" % (done, mism), "mismatches": mism}
+
+
+def bench_matmul(steps, warmup, M=128, K=768, N=3072, frac_bits=12, cpu_seconds=0.0):
     """Beaver matmul + GapARS truncation for both parties: X [128 x 768] =
     round(N(0,1) 2^12) (mt(8)), W [768 x 3072] = round(N(0,0.02) 2^12) (mt(9)),
     both additively shared (mt(108), mt(109)); triples and truncation key from
@@ -132,9 +193,59 @@ def bench_matmul(steps, warmup, M=128, K=768, N=3072, frac_bits=12):
     rec = (out[0].cpu().numpy().view(np.uint64) + out[1].cpu().numpy().view(np.uint64))
     ok = bool(np.array_equal(rec.astype(np.uint64), (prod >> frac_bits).view(np.uint64).ravel()))
     macs = 2 * 2 * M * K * N  # both parties, [D | A] x [B' ; E] is a 2K-deep product
-    return {"ms": ms, "shape": [M, K, N], "matmul_ms": mm_ms, "u64_macs": macs,
-            "u64_mac_per_s": macs / (mm_ms / 1e3), "trunc": "GapARS f=%d" % frac_bits,
-            "steps": steps, "check": "ok" if ok else "MISMATCH"}
+    res = {"ms": ms, "shape": [M, K, N], "matmul_ms": mm_ms, "u64_macs": macs,
+           "u64_mac_per_s": macs / (mm_ms / 1e3), "trunc": "GapARS f=%d" % frac_bits,
+           "matmul_kernel": "int8-limb MFMA" if g.mm_work is not None else "u64 VALU",
+           "steps": steps, "check": "ok" if ok else "MISMATCH"}
+    if cpu_seconds > 0:
+        res["cpu_baseline"] = cpu_matmul_baseline(g, state, Xd, Wd, out, cpu_seconds)
+    return res
+
+
+def cpu_matmul_baseline(g, state, Xd, Wd, out, seconds):
+    """Beaver matmul + truncation on the host: the oracle's OpenMP u64 matmul
+    (src/nn/matmul_beaver.cpp:139-161 semantics) for both parties and the
+    oracle truncation gate, on the first rows of the product (8 rows at a
+    time) until the time budget is used; outputs compared with the GPU's."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as ol
+
+    threads = min(os.cpu_count() or 1, 16)
+    M, K, N, f = g.M, g.K, g.N, g.f
+    h = lambda t: t.cpu().numpy().view(np.uint64)
+    X = [h(Xd[0]).reshape(M, K), h(Xd[1]).reshape(M, K)]
+    W = [h(Wd[0]), h(Wd[1])]
+    A = [h(a).reshape(M, K) for a in g.A]
+    B = [h(b) for b in g.B]
+    C = [h(c).reshape(M, N) for c in g.C]
+    keys = [k.cpu().numpy() for k in g.keys]
+    gpu = [h(o).reshape(M, N) for o in out]
+    prg = ol.Prg(state)
+    E = ((W[0] - B[0]) + (W[1] - B[1])).astype(np.uint64)
+    rin = sum(g.rin) & ((1 << 64) - 1)
+    rows, mism = 0, 0
+    t0 = time.perf_counter()
+    while rows + 8 <= M:
+        r = slice(rows, rows + 8)
+        D = ((X[0][r] - A[0][r]) + (X[1][r] - A[1][r])).astype(np.uint64)
+        Z = [ol.beaver_matmul(p, D, E, A[p][r], B[p], C[p][r], 1, 8, K, N, threads=threads)
+             for p in (0, 1)]
+        zhat = (Z[0] + Z[1] + np.uint64(rin)).astype(np.uint64)
+        for p in (0, 1):
+            y = ol.trunc_eval(prg, ol.TRUNC_GAPARS, f, keys[p], zhat)
+            mism += int(np.count_nonzero(y != gpu[p][r].ravel()))
+        rows += 8
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    macs = 2 * 2 * rows * K * N
+    return {"value": macs / dt, "unit": "u64 MAC/s (both parties, with truncation)",
+            "cores": threads, "kind": "port", "ms_full_shape": dt * M / rows * 1e3,
+            "sample": "%d of the %d output rows (oracle C matmul, OpenMP %d threads, then the "
+                      "oracle truncation gate); outputs compared with the GPU: %d mismatches"
+                      % (rows, M, threads, mism), "mismatches": mism}
 
 
 def cpu_baseline(keys0, keys1, xhat, gpu_bits0, gpu_bits1, seconds):
@@ -317,8 +428,9 @@ def main():
         "check": "ok" if ok else "MISMATCH",
     }
     if not a.no_gates:
-        line["spline_gate"] = bench_spline(max(a.steps // 2, 1), 2)
-        line["beaver_matmul_trunc"] = bench_matmul(max(a.steps // 2, 1), 2)
+        gate_cpu = 0.0 if a.no_cpu else a.cpu_seconds / 2
+        line["spline_gate"] = bench_spline(max(a.steps // 2, 1), 2, cpu_seconds=gate_cpu)
+        line["beaver_matmul_trunc"] = bench_matmul(max(a.steps // 2, 1), 2, cpu_seconds=gate_cpu)
         ok = ok and line["spline_gate"]["check"] == "ok"
         ok = ok and line["beaver_matmul_trunc"]["check"] == "ok"
     if not a.no_cpu:

@@ -130,8 +130,16 @@ void orc_lut_build_key(int party, uint64_t nonce, int in_bits, int out_words,
 
 void orc_lut_eval(const uint8_t* keys, size_t key_bytes, int broadcast,
                   const uint64_t* xs, size_t n, uint64_t* out) {
-  for (size_t idx = 0; idx < n; idx++) {
-    const uint8_t* k = broadcast ? keys : keys + idx * key_bytes;
+  orc_lut_eval_at(keys, key_bytes, broadcast, xs, n, 0, out);
+}
+
+/* Elements idx0 .. idx0 + n - 1 of a batch: the keystream counter uses the
+ * element's index in the whole batch. */
+void orc_lut_eval_at(const uint8_t* keys, size_t key_bytes, int broadcast,
+                     const uint64_t* xs, size_t n, size_t idx0, uint64_t* out) {
+  for (size_t i = 0; i < n; i++) {
+    const size_t idx = idx0 + i;
+    const uint8_t* k = broadcast ? keys : keys + i * key_bytes;
     int in_bits = ld16(k), out_words = ld16(k + 2);
     int intervals = (int)ld32(k + 4), party = k[8];
     uint64_t nonce = ld64(k + 16);
@@ -139,7 +147,7 @@ void orc_lut_eval(const uint8_t* keys, size_t key_bytes, int broadcast,
     const uint8_t* cuts = k + ORC_LUT_HDR;
     const uint8_t* pay = cuts + 8 * (size_t)(intervals + 1);
     uint64_t m = mask_bits(in_bits);
-    uint64_t x = xs[idx] & m;
+    uint64_t x = xs[i] & m;
     int iv = intervals - 1;
     if (intervals > 1) {
       int lo = 0, hi = intervals;
@@ -159,7 +167,7 @@ void orc_lut_eval(const uint8_t* keys, size_t key_bytes, int broadcast,
       keystream(rk, ctr, &ks[0], &ks[1]);
       for (int h = 0; h < 2 && w + h < out_words; h++) {
         uint64_t r = ld64(row + 8 * (size_t)(w + h));
-        out[idx * (size_t)out_words + (size_t)(w + h)] = party == 0 ? ks[h] : r - ks[h];
+        out[i * (size_t)out_words + (size_t)(w + h)] = party == 0 ? ks[h] : r - ks[h];
       }
     }
   }

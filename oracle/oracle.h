@@ -97,6 +97,10 @@ void orc_lut_build_key(int party, uint64_t nonce, int in_bits, int out_words,
                        const uint8_t seed[16], uint8_t* blob);
 void orc_lut_eval(const uint8_t* keys, size_t key_bytes, int broadcast,
                   const uint64_t* xs, size_t n, uint64_t* out);
+/* The same for elements idx0 .. idx0 + n - 1 of a larger batch (the keystream
+ * counter depends on the element index). */
+void orc_lut_eval_at(const uint8_t* keys, size_t key_bytes, int broadcast,
+                     const uint64_t* xs, size_t n, size_t idx0, uint64_t* out);
 
 /* ---------------- ring postprocessing (cuda/cuda_primitives.cu) ---------------- */
 void orc_beaver_mul(int party, const uint64_t* a, const uint64_t* b, const uint64_t* c,

@@ -55,6 +55,7 @@ def _load_oracle():
     lib.orc_lut_build_key.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
                                       u64p, ctypes.c_int, u64p, u8p, u8p]
     lib.orc_lut_eval.argtypes = [u8p, c_sz, ctypes.c_int, u64p, c_sz, u64p]
+    lib.orc_lut_eval_at.argtypes = [u8p, c_sz, ctypes.c_int, u64p, c_sz, c_sz, u64p]
     lib.orc_trunc_postproc.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64,
                                        ctypes.c_uint64, u64p, u64p, c_sz, ctypes.c_int, u64p,
                                        c_sz, ctypes.c_int, ctypes.c_int, ctypes.c_int, u64p, c_sz]
@@ -191,11 +192,12 @@ def lut_key(party, nonce, in_bits, out_words, cuts, payload, seed):
     return blob
 
 
-def lut_eval(keys, key_bytes, broadcast, xs, out_words):
+def lut_eval(keys, key_bytes, broadcast, xs, out_words, idx0=0):
+    """idx0: index of xs[0] in the batch (the keystream counter uses it)."""
     xs = np.ascontiguousarray(xs, dtype=np.uint64)
     out = np.zeros(len(xs) * out_words, dtype=np.uint64)
-    LIB.orc_lut_eval(ptr(np.ascontiguousarray(keys)), key_bytes, int(broadcast),
-                     ptr(xs, u64p), len(xs), ptr(out, u64p))
+    LIB.orc_lut_eval_at(ptr(np.ascontiguousarray(keys)), key_bytes, int(broadcast),
+                        ptr(xs, u64p), len(xs), idx0, ptr(out, u64p))
     return out.reshape(len(xs), out_words)
 
 

@@ -194,3 +194,15 @@ def test_gpu_packed_matches_oracle(num_thr, sorted_thr, broadcast):
                     out.data_ptr(), torch.cuda.current_stream().cuda_stream)
         exp = ol.packed_eval(keys, kb, int(broadcast), xs, ow)
         assert np.array_equal(u64(out).reshape(n, ow), exp), party
+
+
+def test_oracle_lut_eval_at_matches_the_batch_slice():
+    rng = np.random.default_rng(9)
+    cuts = np.sort(rng.integers(0, 1 << 20, 9, dtype=np.uint64))
+    payload = rng.integers(0, 1 << 63, 8 * 3, dtype=np.uint64)
+    blob = ol.lut_key(0, 5, 20, 3, cuts, payload, ol.seed_from_id(5, 7))
+    xs = rng.integers(0, 1 << 20, 300, dtype=np.uint64)
+    whole = ol.lut_eval(blob, blob.size, 1, xs, 3)
+    part = ol.lut_eval(blob, blob.size, 1, xs[100:250], 3, idx0=100)
+    assert np.array_equal(whole[100:250], part)
+    assert not np.array_equal(ol.lut_eval(blob, blob.size, 1, xs[100:250], 3), part)
