@@ -236,6 +236,95 @@ int sufhip_mul2(const sufhip_mul2_args* args, size_t n, void* stream);
 int sufhip_add_shifted(const uint64_t* d_y, const uint64_t* d_add, size_t add_stride,
                        size_t add_off, int shift, size_t n, uint64_t* d_out, void* stream);
 
+/* Generalised operands for the row-wise tasks of SUF's softmax and LayerNorm
+ * (SoftmaxBlockTask, include/nn/softmax_block_task.hpp:33-450; LayerNormTask,
+ * RecipTask, RsqrtTask, MulRowBroadcastTask, include/runtime/phase_tasks.hpp:
+ * 1383-2668, 3140-3653), whose factors are affine in stored shares: x - mu[row],
+ * 2 - xy, 1.5 - h/2, t + c0, inv[row].
+ *
+ * A term reads, for element i and party p, p[p][j * stride + off] with
+ * j = index ? index[i] : i (index: int32, e.g. the row of element i), shifted
+ * left by `shift` and subtracted when `negate` is set.  An absent term has
+ * p[0] == p[1] == NULL; a present one needs both.  j is clamped to
+ * [0, len), so no index value reads outside the arrays; without an index,
+ * len must be >= n. */
+typedef struct sufhip_term2 {
+  const uint64_t* p[2];
+  const int32_t* index;
+  size_t len;    /* rows j the arrays hold (j is clamped below len) */
+  size_t stride; /* >= 1 */
+  size_t off;    /* < stride */
+  int shift;     /* 0..63 */
+  int negate;
+} sufhip_term2;
+
+/* Per element and party: t[0] + t[1] + [p == 0] party0_const, i.e. the
+ * shared value sum_terms + party0_const (a public constant is added to party
+ * 0's share only). */
+typedef struct sufhip_operand2 {
+  sufhip_term2 t[2];
+  uint64_t party0_const;
+} sufhip_operand2;
+
+/* Evaluates an operand for both parties: d_out0 / d_out1 (either may be NULL)
+ * receive the shares, and d_xhat (may be NULL) the masked open
+ * xhat[i] = x_0 + x_1 + mask of a gate input (mask = r_0 + r_1). */
+int sufhip_lin2(const sufhip_operand2* x, size_t n, uint64_t* d_out0, uint64_t* d_out1,
+                uint64_t* d_xhat, uint64_t mask, void* stream);
+
+/* Beaver product for both parties with general operands (MulTask and
+ * MulRowBroadcastTask, phase_tasks.hpp:198-402, 1810-2185; beaver_mul_kernel
+ * and row_broadcast_mul_kernel, cuda/cuda_primitives.cu:114-139, 303-336):
+ *   d = open(u - a), e = open(v - b),
+ *   z_p = c_p + d*b_p + e*a_p + [p == 0] d*e + z_add_p.
+ * a, b, c are the triple shares as terms (shift 0, not negated; an index on b
+ * gives the row-broadcast triple of MulRowBroadcastTask, whose e is then one
+ * value per row).  z_add's terms may be absent.  zhat == NULL: z[p][i] = z_p;
+ * otherwise only zhat[i] = z_0 + z_1 + open_mask is written (the masked open
+ * of the product for the next truncation gate). */
+typedef struct sufhip_mul2x_args {
+  sufhip_operand2 u;
+  sufhip_operand2 v;
+  sufhip_term2 a;
+  sufhip_term2 b;
+  sufhip_term2 c;
+  sufhip_operand2 z_add;
+  uint64_t* z[2];
+  uint64_t* zhat;
+  uint64_t open_mask;
+} sufhip_mul2x_args;
+int sufhip_mul2x(const sufhip_mul2x_args* args, size_t n, void* stream);
+
+/* Row sums for both parties (launch_row_sum_kernel / launch_row_sum_ragged_kernel,
+ * cuda_primitives.cu:339-389, run for both parties, followed by the public
+ * scaling of LayerNormTask's mean and variance, phase_tasks.hpp:2293-2470):
+ *   s_p[r] = mul_const * sum_{i in row r} x_p[i]  (mod 2^64)
+ * Row r covers elements [d_row_offsets[r], d_row_offsets[r+1]) when
+ * d_row_offsets (int32 [rows + 1], non-decreasing) is given, else
+ * [r * cols, (r + 1) * cols).  d_sum0 / d_sum1 / d_hat may each be NULL;
+ * d_hat[r] = s_0[r] + s_1[r] + mask (masked open of the scaled sum). */
+int sufhip_row_sum2(const sufhip_operand2* x, int rows, int cols, const int32_t* d_row_offsets,
+                    uint64_t mul_const, uint64_t* d_sum0, uint64_t* d_sum1, uint64_t* d_hat,
+                    uint64_t mask, void* stream);
+
+/* One pairwise-max round of RowMaxDiffTask (include/nn/row_maxdiff_task.hpp:
+ * 49-150), max(a, b) = b + ReLU(a - b), for both parties.  For output slot j:
+ *   src_b[j] < 0: next_p[j] = cur_p[src_a[j]] (odd element carried);
+ *   else: d_p = cur_p[src_a[j]] - cur_p[src_b[j]], xhat = d_0 + d_1 + mask,
+ *         (q0_p, q1_p) = interval LUT share of party p at xhat (element index
+ *         j of the batch, out_words = 2, the ReLU SUF's coefficients shifted
+ *         to the public xhat: q0 + q1 xhat = ReLU(d)),
+ *         next_p[j] = cur_p[src_b[j]] + q0_p + q1_p * xhat.
+ * d_lut0 / d_lut1: the parties' broadcast interval-LUT blobs (format of
+ * sufhip_interval_lut_build_key; intervals <= 64, key_bytes =
+ * sufhip_interval_lut_key_bytes(intervals, 2)).  Source indices outside
+ * [0, n_in) yield 0 instead of a read. */
+int sufhip_relu_max_round2(const uint64_t* d_cur0, const uint64_t* d_cur1, size_t n_in,
+                           const int32_t* d_src_a, const int32_t* d_src_b, size_t n_out,
+                           const uint8_t* d_lut0, const uint8_t* d_lut1, size_t key_bytes,
+                           int intervals, uint64_t mask, uint64_t* d_next0, uint64_t* d_next1,
+                           void* stream);
+
 /* ---------------------------------------------------------------------- */
 /* Interval LUT and packed compare in the reference GPU blob formats        */
 /* (cuda/pfss_backend_gpu.cu:75-94, 189-288), evaluated with the kernel     */

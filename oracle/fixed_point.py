@@ -1,0 +1,154 @@
+"""Closed forms of SUF's softmax and LayerNorm task chains over Z_2^64.
+
+TEST INFRASTRUCTURE ONLY: the checker.  Only tests/, __graft_entry__.smoke()
+and the cpu_baseline leg of bench.py import this module; the product never
+does.
+
+What a two-party run of each task chain must reconstruct to, as plain
+fixed-point arithmetic on int64 numpy arrays.  Every truncation of the secure
+chain is an exact arithmetic shift (floor division by 2^k; GapARS and
+faithful ARS both reconstruct to it while |x| < 2^62), so the chains reduce
+to these formulas.  Products are checked against 2^62 before they are
+formed: an input outside that range raises instead of wrapping.
+
+  cubic_task      CubicPolyTask (include/runtime/phase_tasks.hpp:2933-3061)
+  recip_task      RecipTask (phase_tasks.hpp:3190-3540; NR step of
+                  ref_reciprocal_fixed, include/gates/reciprocal_gate.hpp:96-109)
+  rsqrt_task      RsqrtTask (phase_tasks.hpp:1415-1640) with the init
+                  c0 + (c1 x >> f) and the NR step of ref_rsqrt_fixed
+                  (include/gates/rsqrt_gate.hpp:100-117)
+  row_max_diff    RowMaxDiffTask (include/nn/row_maxdiff_task.hpp:49-165)
+  softmax_block   SoftmaxBlockTask (include/nn/softmax_block_task.hpp:97-450)
+  layernorm       LayerNormTask (phase_tasks.hpp:2232-2610) without gamma/beta,
+                  as transformer_layer_forward runs it
+                  (src/nn/transformer_layer.cpp:626-760)
+
+Pinning (tests/test_oracle_fixed_point.py): each formula against the real
+function it approximates (exp, 1/x, 1/sqrt, softmax, layer norm in float64)
+within the table's stated accuracy, against brute force (row max, piece
+selection at every boundary), and against hand-computed values.
+"""
+import numpy as np
+
+LIM = float(1 << 62)
+
+
+def _i64(a):
+    return np.asarray(a).astype(np.uint64).view(np.int64)
+
+
+def _u64(a):
+    return np.asarray(a, dtype=np.int64).view(np.uint64)
+
+
+def _check(a, b, what):
+    m = np.abs(a.astype(np.float64)) * np.abs(b.astype(np.float64))
+    if m.size and float(m.max()) >= LIM * (1 - 1e-9):
+        raise ValueError("%s: product outside the exact range (|a b| >= 2^62)" % what)
+
+
+def mul_shift(a, b, s, what="mul_shift"):
+    """floor(a * b / 2^s) for int64 arrays (the reconstruction of a Beaver
+    product followed by an exact truncation by s)."""
+    a = np.asarray(a, dtype=np.int64)
+    b = np.asarray(b, dtype=np.int64)
+    _check(a, b, what)
+    return (a * b) >> s
+
+
+def piece_index(alpha, x):
+    """Piece of each u64 input: the last alpha_i <= x (alpha[0] = 0)."""
+    return np.searchsorted(np.asarray(alpha, dtype=np.uint64), _u64(_i64(x)), side="right") - 1
+
+
+def cubic_task(alpha, coeffs, x, f):
+    """y = trunc_2f((trunc_f((c3 x + c2 2^f) x) + c1 2^f) x) + c0."""
+    x = _i64(x)
+    c = np.asarray(coeffs, dtype=np.int64)[piece_index(alpha, x)]
+    u = c[:, 3] * x + (c[:, 2] << f)
+    _check(c[:, 3], x, "cubic c3 x")
+    p2 = mul_shift(u, x, f, "cubic u x")
+    q = p2 + (c[:, 1] << f)
+    return mul_shift(q, x, 2 * f, "cubic q x") + c[:, 0]
+
+
+def affine_init(alpha, coeffs, x, f):
+    """c0 + trunc_f(c1 x) for the piece of x (the init of RecipTask / RsqrtTask)."""
+    x = _i64(x)
+    c = np.asarray(coeffs, dtype=np.int64)[piece_index(alpha, x)]
+    return c[:, 0] + mul_shift(c[:, 1], x, f, "init c1 x")
+
+
+def recip_task(alpha, coeffs, x, f, iters=1):
+    """NR for 1/x: xy = trunc_f(y x); y = trunc_f(y (2^(f+1) - xy))."""
+    x = _i64(x)
+    y = affine_init(alpha, coeffs, x, f)
+    two = np.int64(2 << f)
+    for _ in range(iters):
+        xy = mul_shift(y, x, f, "recip y x")
+        y = mul_shift(y, two - xy, f, "recip y (2 - xy)")
+    return y
+
+
+def rsqrt_task(alpha, coeffs, x, f, iters=1):
+    """NR for 1/sqrt(x): y2 = trunc_f(y y); h = trunc_f(x y2) >> 1
+    (= trunc_(f+1)(x y2)); y = trunc_f(y (1.5 2^f - h))."""
+    x = _i64(x)
+    y = affine_init(alpha, coeffs, x, f)
+    onept5 = np.int64(3 << (f - 1))
+    for _ in range(iters):
+        y2 = mul_shift(y, y, f, "rsqrt y y")
+        h = mul_shift(x, y2, f + 1, "rsqrt x y2")
+        y = mul_shift(y, onept5 - h, f, "rsqrt y inner")
+    return y
+
+
+def row_max_diff(x, offsets):
+    """delta_i = max(row) - x_i over each row [offsets[r], offsets[r+1])."""
+    x = _i64(x)
+    out = np.zeros_like(x)
+    for r in range(len(offsets) - 1):
+        b, e = int(offsets[r]), int(offsets[r + 1])
+        if e > b:
+            out[b:e] = x[b:e].max() - x[b:e]
+    return out
+
+
+def row_sums(x, offsets):
+    x = _i64(x)
+    return np.array([int(x[int(offsets[r]):int(offsets[r + 1])].sum())
+                     for r in range(len(offsets) - 1)], dtype=np.int64)
+
+
+def row_of(offsets):
+    offsets = np.asarray(offsets)
+    return np.repeat(np.arange(len(offsets) - 1), np.diff(offsets))
+
+
+def softmax_block(scores, offsets, nexp, recip, f, recip_iters=1):
+    """Packed ragged rows of Q(f) scores -> Q(f) probabilities.
+    nexp = (alpha, coeffs[4]); recip = (alpha, coeffs[2]).
+    Returns (prob, dict of the intermediate stages)."""
+    delta = row_max_diff(scores, offsets)
+    e = cubic_task(nexp[0], nexp[1], delta, f)
+    s = row_sums(e, offsets)
+    inv = recip_task(recip[0], recip[1], s, f, recip_iters)
+    prob = mul_shift(e, inv[row_of(offsets)], f, "softmax e inv")
+    return prob, {"delta": delta, "exp": e, "sum": s, "inv": inv}
+
+
+def layernorm(x, rows, cols, f, inv_len, eps_q, rsqrt, rsqrt_iters=1):
+    """Row-major [rows x cols] Q(f) -> Q(f):
+    mu = trunc_f(sum x * invL); d = x - mu; var = trunc_2f(sum d^2 * invL);
+    r = rsqrt(var + eps); y = trunc_f(d r)."""
+    x = _i64(x).reshape(rows, cols)
+    s = x.sum(axis=1)
+    mu = mul_shift(s, np.full(rows, inv_len, dtype=np.int64), f, "ln sum invL")
+    d = x - mu[:, None]
+    _check(d, d, "ln d d")
+    sq = (d * d).sum(axis=1)
+    var = mul_shift(sq, np.full(rows, inv_len, dtype=np.int64), 2 * f, "ln sq invL")
+    v = var + np.int64(eps_q)
+    r = rsqrt_task(rsqrt[0], rsqrt[1], v, f, rsqrt_iters)
+    y = mul_shift(d, np.broadcast_to(r[:, None], d.shape), f, "ln d r")
+    return y.reshape(-1), {"mu": mu, "var": var, "rsqrt": r}

@@ -261,6 +261,72 @@ __global__ void __launch_bounds__(kLutBlock) packed_keyed_kernel(PackedArgs a, i
   }
 }
 
+// One pairwise-max round of RowMaxDiffTask for both parties: each party's
+// broadcast LUT (ReLU coefficients at the public xhat, 2 words) staged in LDS.
+constexpr int kReluMaxIntervals = 64;
+
+struct ReluRoundArgs {
+  const uint64_t* cur[2];
+  const int32_t* src_a;
+  const int32_t* src_b;
+  const uint8_t* lut[2];
+  uint64_t* next[2];
+  size_t n_in;
+  size_t n_out;
+  uint64_t mask;
+  int intervals;
+};
+
+__global__ void __launch_bounds__(kLutBlock) relu_max_round2_kernel(ReluRoundArgs a) {
+  __shared__ uint32_t tab[256 * kLutCopies];
+  __shared__ uint4 rk[2][11];
+  __shared__ uint64_t cuts[2][kReluMaxIntervals];
+  __shared__ uint64_t pay[2][2 * kReluMaxIntervals];
+  fill_ttable<kLutCopies>(tab, kTDev.v);
+  const int nint = a.intervals;
+  for (int p = 0; p < 2; ++p) {
+    const uint8_t* k = a.lut[p];
+    const uint32_t* rkg = reinterpret_cast<const uint32_t*>(k + 40);
+    for (int i = threadIdx.x; i < 11; i += blockDim.x)
+      rk[p][i] = make_uint4(rkg[4 * i], rkg[4 * i + 1], rkg[4 * i + 2], rkg[4 * i + 3]);
+    const uint64_t* cg = reinterpret_cast<const uint64_t*>(k + kLutHdr);
+    const uint64_t* pg = cg + (nint + 1);
+    for (int i = threadIdx.x; i < nint; i += blockDim.x) cuts[p][i] = cg[i];
+    for (int i = threadIdx.x; i < 2 * nint; i += blockDim.x) pay[p][i] = pg[i];
+  }
+  __syncthreads();
+  const AesLds<kLutCopies> aes{tab, threadIdx.x % kLutCopies};
+  uint64_t m[2], nonce[2];
+  int party[2];
+  for (int p = 0; p < 2; ++p) {
+    m[p] = mask_bits(*reinterpret_cast<const uint16_t*>(a.lut[p]));
+    party[p] = a.lut[p][8];
+    nonce[p] = ld64(a.lut[p] + 16);
+  }
+  for (size_t j = size_t(blockIdx.x) * kLutBlock + threadIdx.x; j < a.n_out;
+       j += size_t(gridDim.x) * kLutBlock) {
+    const int32_t ia = a.src_a[j], ib = a.src_b[j];
+    const bool va = ia >= 0 && size_t(ia) < a.n_in;
+    if (ib < 0) {
+      a.next[0][j] = va ? a.cur[0][ia] : 0;
+      a.next[1][j] = va ? a.cur[1][ia] : 0;
+      continue;
+    }
+    const bool vb = size_t(ib) < a.n_in;
+    const uint64_t xa0 = va ? a.cur[0][ia] : 0, xa1 = va ? a.cur[1][ia] : 0;
+    const uint64_t xb0 = vb ? a.cur[0][ib] : 0, xb1 = vb ? a.cur[1][ib] : 0;
+    const uint64_t xhat = (xa0 - xb0) + (xa1 - xb1) + a.mask;
+    uint64_t q[2][2];
+    for (int p = 0; p < 2; ++p) {
+      const uint64_t x = xhat & m[p];
+      const int iv = interval_of(x, nint, m[p], [&](int i) { return cuts[p][i]; });
+      write_masked_row(aes, rk[p], nonce[p], j, iv, 2, party[p], pay[p] + 2 * iv, q[p]);
+    }
+    a.next[0][j] = xb0 + q[0][0] + q[0][1] * xhat;
+    a.next[1][j] = xb1 + q[1][0] + q[1][1] * xhat;
+  }
+}
+
 unsigned int lut_grid(size_t n) {
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess)
@@ -383,6 +449,29 @@ int sufhip_packed_lt_eval(const uint8_t* d_keys, size_t key_bytes, int key_broad
                        key_broadcast ? 1 : 0);
   }
   return check_launch("packed_lt kernel");
+}
+
+int sufhip_relu_max_round2(const uint64_t* d_cur0, const uint64_t* d_cur1, size_t n_in,
+                           const int32_t* d_src_a, const int32_t* d_src_b, size_t n_out,
+                           const uint8_t* d_lut0, const uint8_t* d_lut1, size_t key_bytes,
+                           int intervals, uint64_t mask, uint64_t* d_next0, uint64_t* d_next1,
+                           void* stream) {
+  SUFHIP_REQUIRE(intervals >= 1 && intervals <= kReluMaxIntervals,
+                 "sufhip_relu_max_round2: intervals must be in [1, 64]");
+  SUFHIP_REQUIRE(key_bytes == sufhip_interval_lut_key_bytes(intervals, 2),
+                 "sufhip_relu_max_round2: key_bytes does not match (intervals, 2)");
+  if (n_out == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(n_in > 0 && n_in < (size_t(1) << 31), "sufhip_relu_max_round2: bad n_in");
+  SUFHIP_REQUIRE(d_cur0 && d_cur1 && d_src_a && d_src_b && d_lut0 && d_lut1 && d_next0 && d_next1,
+                 "sufhip_relu_max_round2: null pointer");
+  SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_lut0) & 7) == 0 &&
+                     (reinterpret_cast<uintptr_t>(d_lut1) & 7) == 0,
+                 "sufhip_relu_max_round2: keys must be 8-byte aligned");
+  ReluRoundArgs a{{d_cur0, d_cur1}, d_src_a, d_src_b, {d_lut0, d_lut1}, {d_next0, d_next1},
+                  n_in, n_out, mask, intervals};
+  hipLaunchKernelGGL(relu_max_round2_kernel, dim3(lut_grid(n_out)), dim3(kLutBlock), 0,
+                     as_stream(stream), a);
+  return check_launch("relu_max_round2_kernel");
 }
 
 }  // extern "C"

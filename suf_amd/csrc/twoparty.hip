@@ -12,10 +12,22 @@
 //                 of CubicPolyTask, phase_tasks.hpp:2962-3061), and optional
 //                 masked open of the product for the next gate
 //   add_shifted   y + (a << s), strided a (coefficient words of an AoS row)
+//   lin2          a general operand (sum of up to two strided / row-indexed,
+//                 shifted, signed terms plus a public constant on party 0's
+//                 share) for both parties, and/or its masked open
+//   mul2x         the Beaver product of two general operands, with the
+//                 row-broadcast triple of MulRowBroadcastTask (phase_tasks.hpp:
+//                 1810-2185) when b is row-indexed
+//   row_sum2      per-row sums of a general operand for both parties, scaled
+//                 by a public constant, and/or their masked open (the mean /
+//                 variance / softmax-denominator steps of LayerNormTask and
+//                 SoftmaxBlockTask)
 // All arithmetic is mod 2^64; per party the Beaver step is exactly
 // z_p = c_p + d*b_p + e*a_p + [p == 0] d*e (beaver_mul_kernel,
 // cuda/cuda_primitives.cu:114-139).
 #include <hip/hip_runtime.h>
+
+#include <string>
 
 #include "suf_hip.h"
 #include "sufhip_internal.hpp"
@@ -91,6 +103,120 @@ __global__ void __launch_bounds__(kBlock)
     out[i] = y[i] + (add[i * stride_a + off] << shift);
 }
 
+__device__ __forceinline__ uint64_t term_at(const sufhip_term2& t, int p, size_t i) {
+  // Clamped to the arrays' rows whether or not the row comes from an index.
+  size_t j = i;
+  if (t.index) {
+    const int32_t r = t.index[i];
+    j = r < 0 ? 0 : size_t(r);
+  }
+  if (j >= t.len) j = t.len - 1;
+  const uint64_t v = t.p[p][j * t.stride + t.off] << t.shift;
+  return t.negate ? uint64_t(0) - v : v;
+}
+
+__device__ __forceinline__ uint64_t operand_at(const sufhip_operand2& o, int p, size_t i) {
+  uint64_t v = p == 0 ? o.party0_const : 0;
+  if (o.t[0].p[0]) v += term_at(o.t[0], p, i);
+  if (o.t[1].p[0]) v += term_at(o.t[1], p, i);
+  return v;
+}
+
+__global__ void __launch_bounds__(kBlock)
+    lin2_kernel(sufhip_operand2 x, size_t n, uint64_t* out0, uint64_t* out1, uint64_t* xhat,
+                uint64_t mask) {
+  const size_t stride = size_t(gridDim.x) * kBlock;
+  for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+    const uint64_t x0 = operand_at(x, 0, i), x1 = operand_at(x, 1, i);
+    if (out0) out0[i] = x0;
+    if (out1) out1[i] = x1;
+    if (xhat) xhat[i] = x0 + x1 + mask;
+  }
+}
+
+__global__ void __launch_bounds__(kBlock) mul2x_kernel(sufhip_mul2x_args a, size_t n) {
+  const size_t stride = size_t(gridDim.x) * kBlock;
+  const bool open = a.zhat != nullptr;
+  for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+    const uint64_t u0 = operand_at(a.u, 0, i), u1 = operand_at(a.u, 1, i);
+    const uint64_t v0 = operand_at(a.v, 0, i), v1 = operand_at(a.v, 1, i);
+    const uint64_t a0 = term_at(a.a, 0, i), a1 = term_at(a.a, 1, i);
+    const uint64_t b0 = term_at(a.b, 0, i), b1 = term_at(a.b, 1, i);
+    const uint64_t c0 = term_at(a.c, 0, i), c1 = term_at(a.c, 1, i);
+    // The open: each party's masked shares, summed.
+    const uint64_t d = (u0 - a0) + (u1 - a1);
+    const uint64_t e = (v0 - b0) + (v1 - b1);
+    const uint64_t z0 = c0 + d * b0 + e * a0 + d * e + operand_at(a.z_add, 0, i);
+    const uint64_t z1 = c1 + d * b1 + e * a1 + operand_at(a.z_add, 1, i);
+    if (open) {
+      a.zhat[i] = z0 + z1 + a.open_mask;
+    } else {
+      a.z[0][i] = z0;
+      a.z[1][i] = z1;
+    }
+  }
+}
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t lo = __shfl_xor(uint32_t(v), off, 64);
+    const uint32_t hi = __shfl_xor(uint32_t(v >> 32), off, 64);
+    v += uint64_t(lo) | uint64_t(hi) << 32;
+  }
+  return v;
+}
+
+// One wave per row, four rows per workgroup.
+__global__ void __launch_bounds__(kBlock)
+    row_sum2_kernel(sufhip_operand2 x, int rows, int cols, const int32_t* offs,
+                    uint64_t mul_const, uint64_t* sum0, uint64_t* sum1, uint64_t* hat,
+                    uint64_t mask) {
+  const int lane = threadIdx.x & 63;
+  for (int r = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6); r < rows;
+       r += gridDim.x * (kBlock / 64)) {
+    const size_t b = offs ? size_t(offs[r]) : size_t(r) * size_t(cols);
+    const size_t e = offs ? size_t(offs[r + 1]) : b + size_t(cols);
+    uint64_t s0 = 0, s1 = 0;
+    for (size_t i = b + lane; i < e; i += 64) {
+      s0 += operand_at(x, 0, i);
+      s1 += operand_at(x, 1, i);
+    }
+    s0 = wave_sum_u64(s0) * mul_const;
+    s1 = wave_sum_u64(s1) * mul_const;
+    if (lane == 0) {
+      if (sum0) sum0[r] = s0;
+      if (sum1) sum1[r] = s1;
+      if (hat) hat[r] = s0 + s1 + mask;
+    }
+  }
+}
+
+// Host-side checks of the generalised operands (see sufhip_term2 in suf_hip.h).
+int check_term(const sufhip_term2& t, size_t n, bool allow_shift, const char* what) {
+  if (!t.p[0] && !t.p[1]) return SUFHIP_OK;
+  if (!t.p[0] || !t.p[1]) {
+    set_error(std::string(what) + ": a term needs both parties' pointers or neither");
+    return SUFHIP_ERR_INVALID;
+  }
+  if (t.stride < 1 || t.off >= t.stride || t.shift < 0 || t.shift > 63 ||
+      (!allow_shift && (t.shift != 0 || t.negate))) {
+    set_error(std::string(what) + ": bad term stride/offset/shift/negate");
+    return SUFHIP_ERR_INVALID;
+  }
+  if (t.len == 0 || (!t.index && t.len < n)) {
+    set_error(std::string(what) + ": term len smaller than the element count");
+    return SUFHIP_ERR_INVALID;
+  }
+  return SUFHIP_OK;
+}
+
+int check_operand(const sufhip_operand2& o, size_t n, const char* what) {
+  for (int k = 0; k < 2; ++k)
+    if (int rc = check_term(o.t[k], n, true, what)) return rc;
+  return SUFHIP_OK;
+}
+
 }  // namespace
 }  // namespace sufhip
 
@@ -154,6 +280,54 @@ int sufhip_add_shifted(const uint64_t* d_y, const uint64_t* d_add, size_t add_st
   hipLaunchKernelGGL(add_shifted_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream),
                      d_y, d_add, add_stride, add_off, shift, n, d_out);
   return check_launch("add_shifted_kernel");
+}
+
+int sufhip_lin2(const sufhip_operand2* x, size_t n, uint64_t* d_out0, uint64_t* d_out1,
+                uint64_t* d_xhat, uint64_t mask, void* stream) {
+  SUFHIP_REQUIRE(x != nullptr, "sufhip_lin2: null operand");
+  if (n == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(n < kMaxElems, "sufhip_lin2: n too large");
+  SUFHIP_REQUIRE(d_out0 || d_out1 || d_xhat, "sufhip_lin2: no output");
+  if (int rc = check_operand(*x, n, "sufhip_lin2")) return rc;
+  hipLaunchKernelGGL(lin2_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream), *x, n,
+                     d_out0, d_out1, d_xhat, mask);
+  return check_launch("lin2_kernel");
+}
+
+int sufhip_mul2x(const sufhip_mul2x_args* args, size_t n, void* stream) {
+  SUFHIP_REQUIRE(args != nullptr, "sufhip_mul2x: null args");
+  if (n == 0) return SUFHIP_OK;
+  const sufhip_mul2x_args& a = *args;
+  SUFHIP_REQUIRE(n < kMaxElems, "sufhip_mul2x: n too large");
+  if (int rc = check_operand(a.u, n, "sufhip_mul2x u")) return rc;
+  if (int rc = check_operand(a.v, n, "sufhip_mul2x v")) return rc;
+  if (int rc = check_operand(a.z_add, n, "sufhip_mul2x z_add")) return rc;
+  SUFHIP_REQUIRE(a.a.p[0] && a.b.p[0] && a.c.p[0], "sufhip_mul2x: triple shares missing");
+  if (int rc = check_term(a.a, n, false, "sufhip_mul2x a")) return rc;
+  if (int rc = check_term(a.b, n, false, "sufhip_mul2x b")) return rc;
+  if (int rc = check_term(a.c, n, false, "sufhip_mul2x c")) return rc;
+  SUFHIP_REQUIRE(a.zhat != nullptr || (a.z[0] && a.z[1]),
+                 "sufhip_mul2x: need zhat (open) or both z outputs");
+  hipLaunchKernelGGL(mul2x_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream), a, n);
+  return check_launch("mul2x_kernel");
+}
+
+int sufhip_row_sum2(const sufhip_operand2* x, int rows, int cols, const int32_t* d_row_offsets,
+                    uint64_t mul_const, uint64_t* d_sum0, uint64_t* d_sum1, uint64_t* d_hat,
+                    uint64_t mask, void* stream) {
+  SUFHIP_REQUIRE(x != nullptr, "sufhip_row_sum2: null operand");
+  SUFHIP_REQUIRE(rows >= 0 && (d_row_offsets || cols >= 0), "sufhip_row_sum2: bad shape");
+  if (rows == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(d_sum0 || d_sum1 || d_hat, "sufhip_row_sum2: no output");
+  // Without offsets every element index is < rows * cols; with offsets the
+  // caller's offsets bound them (indexed terms clamp on the device).
+  const size_t n = d_row_offsets ? 0 : size_t(rows) * size_t(cols);
+  if (int rc = check_operand(*x, n, "sufhip_row_sum2")) return rc;
+  size_t g = (size_t(rows) + kBlock / 64 - 1) / (kBlock / 64);
+  if (g > 8192) g = 8192;
+  hipLaunchKernelGGL(row_sum2_kernel, dim3(unsigned(g)), dim3(kBlock), 0, as_stream(stream), *x,
+                     rows, cols, d_row_offsets, mul_const, d_sum0, d_sum1, d_hat, mask);
+  return check_launch("row_sum2_kernel");
 }
 
 }  // extern "C"

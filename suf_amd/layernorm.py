@@ -1,0 +1,133 @@
+"""SUF's LayerNorm for two parties on one GPU.
+
+Task chain (LayerNormTask, include/runtime/phase_tasks.hpp:2186-2668, with
+RsqrtTask, :1383-1700, as transformer_layer_forward builds it,
+src/nn/transformer_layer.cpp:626-760: no gamma/beta, eps = 1/1024,
+invL = llround(2^f / cols), one NR iteration):
+
+  mean     mu = trunc_f(invL * sum x)           (row sums, local; one open)
+  var      d = x - mu[row]; q = d * d (Beaver); var = trunc_2f(invL * sum q)
+  rsqrt    v = var + eps; LUT (c0, c1) at v^; y = c0 + trunc_f(c1 v);
+           y2 = trunc_f(y y); h = trunc_(f+1)(v y2); y = trunc_f(y (1.5 - h))
+  norm     out = trunc_f(d * y[row])            (row-broadcast Beaver)
+
+RsqrtTask's reference code forms its init from the opened x^ and the clear
+mask, and halves x y2 by a local shift of a share; here the init is a Beaver
+product with a truncation and the halving is folded into the truncation by
+f + 1, which reconstructs to the same floor((x y2 >> f) / 2) of
+ref_rsqrt_fixed (include/gates/rsqrt_gate.hpp:100-117).  Every truncation is
+a GapARS gate with its own key.  Randomness: suf_amd.tasks.Dealer(seed).
+"""
+import numpy as np
+import torch
+
+from . import tables
+from .tasks import (CoeffLut, Dealer, Triples, Trunc, dev_i32, lin2, mul2x, operand, pair,
+                    row_sum2, term)
+
+
+class Rsqrt:
+    """RsqrtTask over n values given as an operand v (both parties) and its
+    masked open vhat = v + lut.mask."""
+
+    def __init__(self, n, dealer, prg_state, frac_bits=12, table=None, iters=1, device="cuda"):
+        self.n, self.f, self.iters = n, frac_bits, iters
+        alpha, coeffs = table if table is not None else tables.rsqrt_table(frac_bits)
+        self.table = (alpha, coeffs)
+        self.lut = CoeffLut(dealer, alpha, coeffs, device)
+        self.tri = [Triples(dealer, n, device=device) for _ in range(1 + 3 * iters)]
+        fs = [frac_bits] + [frac_bits, frac_bits + 1, frac_bits] * iters
+        self.tr = [Trunc(dealer, f, n, prg_state, device=device) for f in fs]
+        self.coef = pair(n, device, 2)
+        self.zhat = torch.empty(n, dtype=torch.int64, device=device)
+        self.t = pair(n, device)
+        self.y2 = pair(n, device)
+        self.h = pair(n, device)
+        self.y = pair(n, device)
+
+    def truncs(self):
+        return self.tr
+
+    def eval2(self, v, vhat, out=None):
+        n, f = self.n, self.f
+        out = self.y if out is None else out
+        self.lut.eval2(vhat, n, self.coef)
+        mul2x(operand(term(self.coef, stride=2, off=1)), v, self.tri[0], n, zhat=self.zhat,
+              open_mask=self.tr[0].mask)
+        self.tr[0].finish(self.zhat, self.t)
+        y = operand(term(self.t), term(self.coef, stride=2, off=0))
+        for it in range(self.iters):
+            ta, tb, tc = self.tr[1 + 3 * it: 4 + 3 * it]
+            ka, kb, kc = self.tri[1 + 3 * it: 4 + 3 * it]
+            mul2x(y, y, ka, n, zhat=self.zhat, open_mask=ta.mask)
+            ta.finish(self.zhat, self.y2)
+            mul2x(v, operand(term(self.y2)), kb, n, zhat=self.zhat, open_mask=tb.mask)
+            tb.finish(self.zhat, self.h)
+            inner = operand(term(self.h, neg=True), const=3 << (f - 1))
+            mul2x(y, inner, kc, n, zhat=self.zhat, open_mask=tc.mask)
+            tc.finish(self.zhat, out)
+            y = operand(term(out))
+        if self.iters == 0:
+            lin2(y, n, out=out)
+        return out
+
+
+class LayerNormBlock:
+    """LayerNorm over a row-major [rows x cols] Q(f) matrix, both parties."""
+
+    def __init__(self, rows, cols, prg_state, frac_bits=12, seed=12, eps=1.0 / 1024.0,
+                 rsqrt_iters=1, table=None, device="cuda"):
+        self.rows, self.cols, self.f = rows, cols, frac_bits
+        self.n = rows * cols
+        self.prg_state = bytes(prg_state)
+        self.inv_len = tables.inv_len_qf(cols, frac_bits)
+        self.eps_q = tables.eps_qf(eps, frac_bits)
+        dealer = Dealer(seed)
+        row = np.repeat(np.arange(rows), cols)
+        self.row_index = dev_i32(row, device)
+        self.tr_mean = Trunc(dealer, frac_bits, rows, self.prg_state, device=device)
+        self.tri_sq = Triples(dealer, self.n, device=device)
+        self.tr_var = Trunc(dealer, 2 * frac_bits, rows, self.prg_state, device=device)
+        self.rsqrt = Rsqrt(rows, dealer, self.prg_state, frac_bits, table, rsqrt_iters, device)
+        self.tri_norm = Triples(dealer, self.n, row_of=row, device=device)
+        self.tr_norm = Trunc(dealer, frac_bits, self.n, self.prg_state, device=device)
+        self.side = torch.cuda.Stream(device=device)
+        self.mu = pair(rows, device)
+        self.sq = pair(self.n, device)
+        self.var = pair(rows, device)
+        self.rowhat = torch.empty(rows, dtype=torch.int64, device=device)
+        self.zhat = torch.empty(self.n, dtype=torch.int64, device=device)
+
+    def truncs(self):
+        return [self.tr_mean, self.tr_var] + self.rsqrt.truncs() + [self.tr_norm]
+
+    def _prepare(self):
+        start = torch.cuda.Event()
+        start.record()
+        self.side.wait_event(start)
+        for t in self.truncs():
+            t.prepare(self.side)
+        done = torch.cuda.Event()
+        done.record(self.side)
+        return done
+
+    def eval2(self, x, out):
+        """x, out: pairs of int64 [rows * cols] device tensors."""
+        rows, cols, n = self.rows, self.cols, self.n
+        prepared = self._prepare()
+        row_sum2(operand(term(x)), rows, cols, mul_const=self.inv_len, hat=self.rowhat,
+                 mask=self.tr_mean.mask)
+        torch.cuda.current_stream().wait_event(prepared)
+        self.tr_mean.finish(self.rowhat, self.mu)
+        diff = operand(term(x), term(self.mu, index=self.row_index, neg=True, length=rows))
+        mul2x(diff, diff, self.tri_sq, n, z=self.sq)
+        row_sum2(operand(term(self.sq)), rows, cols, mul_const=self.inv_len, hat=self.rowhat,
+                 mask=self.tr_var.mask)
+        self.tr_var.finish(self.rowhat, self.var)
+        v = operand(term(self.var), const=self.eps_q)
+        lin2(v, rows, xhat=self.rowhat, mask=self.rsqrt.lut.mask)
+        rs = self.rsqrt.eval2(v, self.rowhat)
+        mul2x(diff, operand(term(rs, index=self.row_index, length=rows)), self.tri_norm, n,
+              zhat=self.zhat, open_mask=self.tr_norm.mask)
+        self.tr_norm.finish(self.zhat, out)
+        return out

@@ -74,6 +74,11 @@ _SIGS = {
     "sufhip_open2_diff": (c_int, [c_vp, c_vp, c_vp, c_vp, c_sz, c_vp, c_vp]),
     "sufhip_mul2": (c_int, [c_vp, c_sz, c_vp]),
     "sufhip_add_shifted": (c_int, [c_vp, c_vp, c_sz, c_sz, c_int, c_sz, c_vp, c_vp]),
+    "sufhip_lin2": (c_int, [c_vp, c_sz, c_vp, c_vp, c_vp, c_u64, c_vp]),
+    "sufhip_mul2x": (c_int, [c_vp, c_sz, c_vp]),
+    "sufhip_row_sum2": (c_int, [c_vp, c_int, c_int, c_vp, c_u64, c_vp, c_vp, c_vp, c_u64, c_vp]),
+    "sufhip_relu_max_round2": (c_int, [c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_int,
+                                       c_u64, c_vp, c_vp, c_vp]),
     "sufhip_seed_from_id": (None, [c_u64, c_u64, c_vp]),
     "sufhip_interval_lut_key_bytes": (c_sz, [c_int, c_int]),
     "sufhip_interval_lut_build_key": (c_int, [c_int, c_u64, c_int, c_int, c_vp, c_int, c_vp, c_vp,
@@ -123,6 +128,23 @@ class Mul2Args(ctypes.Structure):
         ("z_add", c_vp * 2), ("z_add_stride", c_sz), ("z_add_off", c_sz), ("z_add_shift", c_int),
         ("z", c_vp * 2), ("zhat", c_vp), ("open_mask", c_u64 * 2),
     ]
+
+
+class Term2(ctypes.Structure):
+    """sufhip_term2 (include/suf_hip.h)."""
+    _fields_ = [("p", c_vp * 2), ("index", c_vp), ("len", c_sz), ("stride", c_sz),
+                ("off", c_sz), ("shift", c_int), ("negate", c_int)]
+
+
+class Operand2(ctypes.Structure):
+    """sufhip_operand2 (include/suf_hip.h)."""
+    _fields_ = [("t", Term2 * 2), ("party0_const", c_u64)]
+
+
+class Mul2xArgs(ctypes.Structure):
+    """sufhip_mul2x_args (include/suf_hip.h)."""
+    _fields_ = [("u", Operand2), ("v", Operand2), ("a", Term2), ("b", Term2), ("c", Term2),
+                ("z_add", Operand2), ("z", c_vp * 2), ("zhat", c_vp), ("open_mask", c_u64)]
 
 
 class SufHipError(RuntimeError):

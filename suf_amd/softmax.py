@@ -1,0 +1,201 @@
+"""SUF's softmax block for two parties on one GPU.
+
+Task chain (SoftmaxBlockTask, include/nn/softmax_block_task.hpp:97-450, fed
+by RowMaxDiffTask, include/nn/row_maxdiff_task.hpp:49-165, as
+attention_forward runs them, src/nn/attention_block.cpp:1240-1760), over
+packed ragged rows (row r holds elements [offsets[r], offsets[r+1])):
+
+  RowMaxDiff   pairwise max tree, max(a, b) = b + ReLU(a - b), one ReLU
+               gate per round (interval LUT of ReLU's public-x^
+               coefficients), then delta = max(row) - x
+  nExp         CubicPolyTask on delta with the exp(-t) spline table
+               (suf_amd/spline.SplineGate)
+  row sum      s = sum of exp over the row (local), opened with the
+               reciprocal's mask
+  Recip        RecipTask: affine-init LUT (c0, c1), y = c0 + trunc_f(c1 s),
+               NR y <- trunc_f(y (2 - trunc_f(y s)))
+  normalise    MulRowBroadcastTask e * inv(row), then trunc_f
+
+Every truncation is a GapARS gate with its own key (the reference shares one
+trunc key among a task's truncations; reconstruction is the same exact
+shift).  Randomness: suf_amd.tasks.Dealer(seed).
+"""
+import numpy as np
+import torch
+
+from . import native, spline, tables
+from .tasks import (RELU_ALPHA, CoeffLut, Dealer, Triples, Trunc, dev_i32, lin2, mul2x,
+                    operand, pair, relu_coeffs_for, row_sum2, stream_ptr, term)
+
+
+def causal_offsets(heads, seq):
+    """Row offsets of `heads` causal [seq x seq] score blocks, packed: row r
+    of each head keeps its first r + 1 columns."""
+    lens = np.tile(np.arange(1, seq + 1), heads)
+    return np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+
+
+def max_tree_plan(offsets):
+    """Rounds of the pairwise max over packed rows (RowMaxDiffTask's
+    RoundPrep, row_maxdiff_task.hpp:60-125): per round the source indices of
+    each next-level slot (src_b = -1 for a carried odd element), and the
+    final position of each row's max."""
+    offsets = np.asarray(offsets, dtype=np.int64)
+    lens = np.diff(offsets)
+    cur_off = offsets.copy()
+    cur_len = lens.copy()
+    rounds = []
+    while np.any(cur_len > 1):
+        nxt_len = (cur_len + 1) // 2
+        nxt_off = np.concatenate([[0], np.cumsum(nxt_len)])
+        src_a = np.empty(int(nxt_off[-1]), dtype=np.int32)
+        src_b = np.empty(int(nxt_off[-1]), dtype=np.int32)
+        for r in range(len(cur_len)):
+            L, b, o = int(cur_len[r]), int(cur_off[r]), int(nxt_off[r])
+            pairs = L // 2
+            src_a[o:o + pairs] = b + 2 * np.arange(pairs)
+            src_b[o:o + pairs] = b + 2 * np.arange(pairs) + 1
+            if L & 1:
+                src_a[o + pairs] = b + L - 1
+                src_b[o + pairs] = -1
+        rounds.append((src_a, src_b, int(cur_off[-1])))
+        cur_off, cur_len = nxt_off, nxt_len
+    # Row r's max sits at cur_off[r] of the last level (rows are non-empty).
+    return rounds, cur_off[:-1].astype(np.int64)
+
+
+class RowMaxDiff:
+    """delta = max(row) - x for packed ragged rows, both parties."""
+
+    def __init__(self, offsets, dealer, device="cuda"):
+        self.offsets = np.asarray(offsets, dtype=np.int64)
+        if np.any(np.diff(self.offsets) < 1):
+            raise ValueError("RowMaxDiff: every row needs at least one element")
+        self.n = int(self.offsets[-1])
+        self.rows = len(self.offsets) - 1
+        rounds, max_pos = max_tree_plan(self.offsets)
+        self.rounds = []
+        for src_a, src_b, n_in in rounds:
+            lut = CoeffLut(dealer, RELU_ALPHA, [[0, 0], [0, 0]], device,
+                           coeffs_for_rin=relu_coeffs_for)
+            self.rounds.append({"a": dev_i32(src_a, device), "b": dev_i32(src_b, device),
+                                "n_in": n_in, "n_out": len(src_a), "lut": lut,
+                                "out": pair(len(src_a), device),
+                                "src": (src_a, src_b)})
+        row = np.repeat(np.arange(self.rows), np.diff(self.offsets))
+        self.max_index = dev_i32(max_pos[row], device)
+        self.max_len = self.rows
+
+    def eval2(self, x, delta):
+        """x, delta: pairs of int64 [n] device tensors."""
+        cur = x
+        for rd in self.rounds:
+            lut = rd["lut"]
+            native.call("sufhip_relu_max_round2", cur[0].data_ptr(), cur[1].data_ptr(),
+                        rd["n_in"], rd["a"].data_ptr(), rd["b"].data_ptr(), rd["n_out"],
+                        lut.keys[0].data_ptr(), lut.keys[1].data_ptr(), lut.key_bytes,
+                        lut.intervals, lut.mask, rd["out"][0].data_ptr(),
+                        rd["out"][1].data_ptr(), stream_ptr())
+            cur = rd["out"]
+        lin2(operand(term(cur, index=self.max_index, length=cur[0].numel()),
+                     term(x, neg=True)), self.n, out=delta)
+        return delta
+
+
+class Recip:
+    """RecipTask over n values whose shares x and masked open
+    xhat = x + lut.mask the caller provides."""
+
+    def __init__(self, n, dealer, prg_state, frac_bits=12, table=None, iters=1, device="cuda"):
+        self.n, self.f, self.iters = n, frac_bits, iters
+        alpha, coeffs = table if table is not None else tables.recip_table(frac_bits)
+        self.table = (alpha, coeffs)
+        self.lut = CoeffLut(dealer, alpha, coeffs, device)
+        self.tri = [Triples(dealer, n, device=device) for _ in range(1 + 2 * iters)]
+        self.tr = [Trunc(dealer, frac_bits, n, prg_state, device=device)
+                   for _ in range(1 + 2 * iters)]
+        self.coef = pair(n, device, 2)
+        self.zhat = torch.empty(n, dtype=torch.int64, device=device)
+        self.t = pair(n, device)
+        self.xy = pair(n, device)
+        self.y = pair(n, device)
+
+    def truncs(self):
+        return self.tr
+
+    def eval2(self, x, xhat, out=None):
+        n, f = self.n, self.f
+        out = self.y if out is None else out
+        self.lut.eval2(xhat, n, self.coef)
+        xs = operand(term(x))
+        mul2x(operand(term(self.coef, stride=2, off=1)), xs, self.tri[0], n, zhat=self.zhat,
+              open_mask=self.tr[0].mask)
+        self.tr[0].finish(self.zhat, self.t)
+        y = operand(term(self.t), term(self.coef, stride=2, off=0))
+        for it in range(self.iters):
+            t1, t2 = self.tr[1 + 2 * it], self.tr[2 + 2 * it]
+            mul2x(y, xs, self.tri[1 + 2 * it], n, zhat=self.zhat, open_mask=t1.mask)
+            t1.finish(self.zhat, self.xy)
+            two_minus = operand(term(self.xy, neg=True), const=2 << f)
+            mul2x(y, two_minus, self.tri[2 + 2 * it], n, zhat=self.zhat, open_mask=t2.mask)
+            t2.finish(self.zhat, out)
+            y = operand(term(out))
+        if self.iters == 0:
+            lin2(y, n, out=out)
+        return out
+
+
+class SoftmaxBlock:
+    """Probabilities of packed ragged Q(f) score rows, both parties."""
+
+    def __init__(self, offsets, prg_state, frac_bits=12, seed=11, recip_iters=1, nexp=None,
+                 recip=None, device="cuda"):
+        self.offsets = np.asarray(offsets, dtype=np.int64)
+        self.n = int(self.offsets[-1])
+        self.rows = len(self.offsets) - 1
+        self.f = frac_bits
+        self.prg_state = bytes(prg_state)
+        dealer = Dealer(seed)
+        self.rowmax = RowMaxDiff(self.offsets, dealer, device)
+        self.nexp_table = nexp if nexp is not None else tables.nexp_table(frac_bits)
+        self.nexp = spline.SplineGate(self.n, self.nexp_table[0], self.nexp_table[1],
+                                      self.prg_state, frac_bits, seed=dealer.word() >> 1,
+                                      nonce=dealer.word())
+        self.recip = Recip(self.rows, dealer, self.prg_state, frac_bits, recip, recip_iters,
+                           device)
+        row = np.repeat(np.arange(self.rows), np.diff(self.offsets))
+        self.row_index = dev_i32(row, device)
+        self.tri = Triples(dealer, self.n, row_of=row, device=device)
+        self.tr = Trunc(dealer, frac_bits, self.n, self.prg_state, device=device)
+        self.offs_dev = dev_i32(self.offsets, device)
+        self.side = torch.cuda.Stream(device=device)
+        self.delta = pair(self.n, device)
+        self.e = pair(self.n, device)
+        self.s = pair(self.rows, device)
+        self.shat = torch.empty(self.rows, dtype=torch.int64, device=device)
+        self.zhat = torch.empty(self.n, dtype=torch.int64, device=device)
+
+    def _prepare(self):
+        """Key-only halves of the block's own truncations on a side stream."""
+        start = torch.cuda.Event()
+        start.record()
+        self.side.wait_event(start)
+        for t in self.recip.truncs() + [self.tr]:
+            t.prepare(self.side)
+        done = torch.cuda.Event()
+        done.record(self.side)
+        return done
+
+    def eval2(self, x, out):
+        """x, out: pairs of int64 [n] device tensors (packed rows)."""
+        prepared = self._prepare()
+        self.rowmax.eval2(x, self.delta)
+        self.nexp.eval2(self.delta, self.e)
+        row_sum2(operand(term(self.e)), self.rows, offsets=self.offs_dev, sums=self.s,
+                 hat=self.shat, mask=self.recip.lut.mask)
+        torch.cuda.current_stream().wait_event(prepared)
+        inv = self.recip.eval2(self.s, self.shat)
+        mul2x(operand(term(self.e)), operand(term(inv, index=self.row_index)), self.tri, self.n,
+              zhat=self.zhat, open_mask=self.tr.mask)
+        self.tr.finish(self.zhat, out)
+        return out

@@ -1,0 +1,245 @@
+"""Building blocks of SUF's task chains for two parties on one GPU.
+
+The reference runs each gate as a PhaseTask per party over a local channel
+(include/runtime/phase_tasks.hpp).  Here both parties live in one process on
+one GPU, so every protocol round is one launch that does both parties' local
+work and the open (libsuf_hip.so two-party kernels); these classes hold the
+dealer material of one gate instance and issue those launches on torch's
+current stream.
+
+  Dealer       seeded std::mt19937_64 streams for one block's randomness
+  Triples      Beaver triples, elementwise or row-broadcast
+               (RowBroadcastTripleProvider, phase_tasks.hpp:1701-1712)
+  Trunc        one truncation gate (TruncTask, phase_tasks.hpp:403-1166):
+               both parties' keys, the key-only prepare and the finish
+  CoeffLut     one coefficient interval LUT over a public masked input (the
+               composite interval-LUT fast path, include/gates/composite_fss.hpp:
+               1248-1384), rotated by the gate's r_in
+  term/operand the generalised operands of sufhip_lin2 / sufhip_mul2x
+"""
+import numpy as np
+import torch
+
+from . import native, pfss
+
+M64 = (1 << 64) - 1
+LUT_TWEAK = 7  # seed_from_id tweak of interval LUT keys (cuda/pfss_backend_gpu.cu:508-515)
+
+
+def stream_ptr():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def dev(a, device="cuda"):
+    """Host u64 / int64 numpy array -> device int64 tensor (same bits)."""
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int64).copy()).to(device)
+
+
+def dev_i32(a, device="cuda"):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32).copy()).to(device)
+
+
+def split(v, s):
+    """Additive split of v with party 0's share s."""
+    return s & M64, (v - s) & M64
+
+
+class Dealer:
+    """Randomness of one block: draw k uses the first words of
+    std::mt19937_64(seed * 0x9e3779b97f4a7c15 + k)."""
+
+    def __init__(self, seed):
+        self.seed = int(seed)
+        self.k = 0
+
+    def words(self, n):
+        self.k += 1
+        return pfss.host_mt19937_64((self.seed * 0x9E3779B97F4A7C15 + self.k) & M64, n)
+
+    def word(self):
+        return int(self.words(1)[0])
+
+
+def term(pair, index=None, stride=1, off=0, shift=0, neg=False, length=None):
+    """sufhip_term2 over a pair of device tensors (party 0, party 1)."""
+    t = native.Term2()
+    if pair is None:
+        return t
+    t.p[0], t.p[1] = pair[0].data_ptr(), pair[1].data_ptr()
+    t.index = index.data_ptr() if index is not None else None
+    t.len = length if length is not None else pair[0].numel() // stride
+    t.stride, t.off, t.shift, t.negate = stride, off, shift, 1 if neg else 0
+    return t
+
+
+def operand(*terms, const=0):
+    """sufhip_operand2: up to two terms plus a public constant (party 0)."""
+    if len(terms) > 2:
+        raise ValueError("an operand holds at most two terms")
+    o = native.Operand2()
+    for k, t in enumerate(terms):
+        o.t[k] = t
+    o.party0_const = const & M64
+    return o
+
+
+def lin2(x, n, out=None, xhat=None, mask=0):
+    native.call("sufhip_lin2", native.ctypes.byref(x), n,
+                ptr(out[0]) if out is not None else None,
+                ptr(out[1]) if out is not None else None, ptr(xhat), mask & M64, stream_ptr())
+
+
+def mul2x(u, v, tri, n, z=None, zhat=None, open_mask=0, z_add=None):
+    """Beaver product of two operands with triple `tri` (a Triples); writes
+    the shares to z (pair) or the masked open of the product to zhat."""
+    a = native.Mul2xArgs()
+    a.u, a.v = u, v
+    a.a, a.b, a.c = tri.terms()
+    if z_add is not None:
+        a.z_add = z_add
+    if z is not None:
+        a.z[0], a.z[1] = ptr(z[0]), ptr(z[1])
+    a.zhat = ptr(zhat)
+    a.open_mask = open_mask & M64
+    native.call("sufhip_mul2x", native.ctypes.byref(a), n, stream_ptr())
+
+
+def row_sum2(x, rows, cols=0, offsets=None, mul_const=1, sums=None, hat=None, mask=0):
+    native.call("sufhip_row_sum2", native.ctypes.byref(x), rows, cols, ptr(offsets),
+                mul_const & M64, ptr(sums[0]) if sums is not None else None,
+                ptr(sums[1]) if sums is not None else None, ptr(hat), mask & M64, stream_ptr())
+
+
+class Triples:
+    """Beaver triples for n products.  a, c per element; b per element, or
+    per row when row_of (host int array: the row of each element) is given,
+    with c_i = a_i * b_row(i) (the row-broadcast triple).  Party 0 holds the
+    drawn shares, party 1 the differences."""
+
+    def __init__(self, dealer, n, row_of=None, device="cuda"):
+        self.n = n
+        nb = n if row_of is None else int(np.max(row_of)) + 1 if len(row_of) else 1
+        a = dealer.words(n)
+        b = dealer.words(nb)
+        c = a * (b if row_of is None else b[np.asarray(row_of)])
+        a0, b0, c0 = dealer.words(n), dealer.words(nb), dealer.words(n)
+        self.a = (dev(a0, device), dev(a - a0, device))
+        self.b = (dev(b0, device), dev(b - b0, device))
+        self.c = (dev(c0, device), dev(c - c0, device))
+        self.row_index = None if row_of is None else dev_i32(row_of, device)
+        self.host = {"a": a, "b": b, "c": c, "a0": a0, "b0": b0, "c0": c0}
+
+    def terms(self):
+        return term(self.a), term(self.b, index=self.row_index), term(self.c)
+
+    def shares(self, p):
+        """Host copies of party p's (a, b, c) shares (tests)."""
+        h = self.host
+        if p == 0:
+            return h["a0"], h["b0"], h["c0"]
+        return ((h["a"] - h["a0"]).astype(np.uint64), (h["b"] - h["b0"]).astype(np.uint64),
+                (h["c"] - h["c0"]).astype(np.uint64))
+
+
+class Trunc:
+    """One truncation gate (scalar mask r) over n elements, both parties."""
+
+    def __init__(self, dealer, frac_bits, n, prg_state, kind=native.TRUNC_GAPARS,
+                 device="cuda"):
+        self.kind, self.f, self.n = kind, frac_bits, n
+        self.prg_state = bytes(prg_state)
+        self.rnd = dealer.words(native.TRUNC_RAND_WORDS)
+        self.mask = int(self.rnd[0])  # r = r_0 + r_1: the open's mask
+        self.keys = pfss.trunc_gen(kind, frac_bits, self.prg_state, self.rnd, device)
+        self.work_bytes = native.load().sufhip_trunc_work_bytes(frac_bits, n)
+        self.work = [torch.empty(max(2, (self.work_bytes + 15) // 8), dtype=torch.int64,
+                                 device=device) for _ in range(2)]
+        self._state = pfss._state_buf(self.prg_state)
+
+    def prepare(self, stream=None):
+        """Key-only half (both parties) on `stream` (default: current)."""
+        s = stream.cuda_stream if stream is not None else stream_ptr()
+        for p in (0, 1):
+            native.call("sufhip_trunc_prepare", self.kind, self.f, self._state, ptr(self.keys[p]),
+                        self.keys[p].numel(), self.n, ptr(self.work[p]), self.work_bytes, s)
+
+    def finish(self, xhat, out):
+        for p in (0, 1):
+            native.call("sufhip_trunc_finish", self.kind, self.f, self._state, ptr(self.keys[p]),
+                        self.keys[p].numel(), ptr(xhat), self.n, ptr(out[p]), ptr(self.work[p]),
+                        self.work_bytes, stream_ptr())
+
+
+def rotated_lut(alpha, coeffs, r_in):
+    """Interval LUT geometry over x^ = x + r_in for pieces [alpha_i,
+    alpha_{i+1}) (the last to 2^64) with coefficient rows `coeffs`: cutpoints
+    [k + 1] (the last is the 2^64 sentinel 0) and payload [k][words]
+    (rotation and wrap split as src/compiler/suf_to_pfss.cpp:506-523)."""
+    ivs = []
+    bounds = [int(a) for a in alpha] + [1 << 64]
+    for i in range(len(alpha)):
+        s = (bounds[i] + r_in) & M64
+        e = (bounds[i + 1] + r_in) & M64
+        pay = [int(v) & M64 for v in coeffs[i]]
+        if s < e:
+            ivs.append((s, e, pay))
+        else:
+            ivs.append((s, 0, pay))
+            if e != 0:
+                ivs.append((0, e, pay))
+    ivs.sort(key=lambda t: t[0])
+    cuts = [ivs[0][0]] + [hi for _, hi, _ in ivs]
+    payload = [w for _, _, pay in ivs for w in pay]
+    return np.array(cuts, dtype=np.uint64), np.array(payload, dtype=np.uint64), len(ivs)
+
+
+class CoeffLut:
+    """Both parties' broadcast interval-LUT keys returning the coefficient
+    row of x's piece at the public x^ = x + r_in.  mask = r_in."""
+
+    def __init__(self, dealer, alpha, coeffs, device="cuda", coeffs_for_rin=None):
+        self.words = int(np.asarray(coeffs).shape[1])
+        r_in = dealer.word()
+        self.mask = r_in
+        rows = coeffs_for_rin(r_in) if coeffs_for_rin is not None else coeffs
+        cuts, payload, k = rotated_lut(alpha, rows, r_in)
+        self.intervals = k
+        lib = native.load()
+        self.key_bytes = lib.sufhip_interval_lut_key_bytes(k, self.words)
+        self.nonce = dealer.word()
+        seed16 = native.ctypes.create_string_buffer(16)
+        lib.sufhip_seed_from_id(self.nonce, LUT_TWEAK, seed16)
+        self.blobs = []
+        self.keys = []
+        for party in (0, 1):
+            blob = np.zeros(self.key_bytes, dtype=np.uint8)
+            native.call("sufhip_interval_lut_build_key", party, self.nonce, 64, self.words,
+                        cuts.ctypes.data, k, payload.ctypes.data, seed16, blob.ctypes.data)
+            self.blobs.append(blob)
+            self.keys.append(torch.from_numpy(blob.view(np.int64).copy()).to(device)
+                             .view(torch.uint8))
+
+    def eval2(self, xhat, n, out):
+        """out: pair of int64 [n * words] tensors (AoS rows)."""
+        for p in (0, 1):
+            native.call("sufhip_interval_lut_eval", ptr(self.keys[p]), self.key_bytes, 1,
+                        self.intervals, self.words, ptr(xhat), n, ptr(out[p]), stream_ptr())
+
+
+def relu_coeffs_for(r_in):
+    """ReLU (make_relu_value_suf_u64, include/gates/relu_gate.hpp:9-44) as
+    public-x^ coefficients: x = x^ - r_in on [0, 2^63) -> (-r_in, 1), 0 on
+    [2^63, 2^64) -> (0, 0) (shift_coeffs_to_public_hatx,
+    src/compiler/suf_to_pfss.cpp:193-243)."""
+    return [[(-r_in) & M64, 1], [0, 0]]
+
+
+RELU_ALPHA = np.array([0, 1 << 63], dtype=np.uint64)
+
+
+def pair(n, device="cuda", width=1):
+    return tuple(torch.empty(n * width, dtype=torch.int64, device=device) for _ in range(2))

@@ -1,0 +1,243 @@
+"""Softmax block (RowMaxDiff + nExp + row sum + Recip + normalise) and
+LayerNorm (mean, variance, Rsqrt, normalise) for two parties on one GPU.
+
+Share level: each stage's shares equal the composition of the CPU oracle's
+protocol steps (interval LUT, Beaver, truncation gate) on the same dealer
+material (tests/twoparty_oracle.py).  Reconstruction: equals the fixed-point
+closed forms of oracle/fixed_point.py, at small shapes and at the full
+config shapes (12 x 128 causal score rows; 128 x 768).
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as ol
+import twoparty_oracle as tp
+from gpu_util import dev, say, u64
+from suf_amd import layernorm, native, pfss, softmax, tables
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                "oracle"))
+import fixed_point as fp  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+STATE = ol.mt64_bytes(3, ol.PRG_STATE_BYTES).tobytes()
+F = 12
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    native.call("sufhip_init", 0)
+
+
+def _share(x, seed):
+    x = np.asarray(x).astype(np.uint64)
+    x0 = pfss.host_mt19937_64(seed, x.size)
+    return x0, (x - x0).astype(np.uint64)
+
+
+def _pair_dev(x0, x1):
+    return dev(x0), dev(x1)
+
+
+def _scores(offsets, seed, sigma=2.0):
+    return pfss.host_normal_fixed(seed, sigma, 0.0, F, int(offsets[-1]))
+
+
+def _recon(p):
+    return (u64(p[0]) + u64(p[1])).astype(np.uint64)
+
+
+def test_max_tree_plan_covers_rows():
+    offs = np.array([0, 1, 4, 11, 11 + 64], dtype=np.int64)
+    rounds, max_pos = softmax.max_tree_plan(offs)
+    assert len(rounds) == 6 and len(max_pos) == 4
+
+
+@pytest.mark.parametrize("offsets", [
+    np.array([0, 1, 3, 6, 13, 13 + 128, 13 + 128 + 65], dtype=np.int64),
+    softmax.causal_offsets(2, 16),
+])
+def test_row_max_diff_shares(offsets):
+    x = _scores(offsets, 21)
+    x[0] = np.uint64(1 << 63)  # most negative value in its own row
+    x0, x1 = _share(x, 22)
+    say("row max diff n=%d rows=%d" % (offsets[-1], len(offsets) - 1))
+    rm = softmax.RowMaxDiff(offsets, softmax.Dealer(5))
+    delta = tuple(torch.empty(int(offsets[-1]), dtype=torch.int64, device="cuda")
+                  for _ in range(2))
+    rm.eval2(_pair_dev(x0, x1), delta)
+    g = [u64(delta[0]), u64(delta[1])]
+    o = tp.relu_rounds2(rm, [x0, x1])
+    assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
+    want = fp.row_max_diff(x, offsets).view(np.uint64)
+    assert np.array_equal((g[0] + g[1]).astype(np.uint64), want)
+
+
+def test_recip_shares_and_closed_form():
+    n = 300
+    s = (np.arange(n, dtype=np.int64) * 1499 + 4096) % (200 << F)
+    s[:5] = [0, 1, 4096, (64 << F) - 1, 1024 << F]
+    s = s.astype(np.uint64)
+    s0, s1 = _share(s, 31)
+    say("recip n=%d" % n)
+    d = softmax.Dealer(9)
+    rc = softmax.Recip(n, d, STATE, F)
+    t = torch.cuda.current_stream()
+    for tr in rc.truncs():
+        tr.prepare()
+    shat = dev((s + np.uint64(rc.lut.mask)).astype(np.uint64))
+    out = rc.eval2(_pair_dev(s0, s1), shat)
+    t.synchronize()
+    g = [u64(out[0]), u64(out[1])]
+    prg = ol.Prg(STATE)
+    o = tp.recip2(prg, rc, [s0, s1], u64(shat))
+    assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
+    want = fp.recip_task(rc.table[0], rc.table[1], s, F).view(np.uint64)
+    assert np.array_equal((g[0] + g[1]).astype(np.uint64), want)
+
+
+def test_rsqrt_shares_and_closed_form():
+    n = 200
+    v = (np.arange(n, dtype=np.int64) * 331 + 1) % (20 << F)
+    v[:4] = [0, 3, 4, 16 << F]
+    v = v.astype(np.uint64)
+    v0, v1 = _share(v, 41)
+    say("rsqrt n=%d" % n)
+    rs = layernorm.Rsqrt(n, softmax.Dealer(10), STATE, F)
+    for tr in rs.truncs():
+        tr.prepare()
+    vp = _pair_dev(v0, v1)
+    vhat = dev((v + np.uint64(rs.lut.mask)).astype(np.uint64))
+    from suf_amd.tasks import operand, term
+    out = rs.eval2(operand(term(vp)), vhat)
+    g = [u64(out[0]), u64(out[1])]
+    prg = ol.Prg(STATE)
+    o = tp.rsqrt2(prg, rs, [v0, v1], u64(vhat))
+    assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
+    want = fp.rsqrt_task(rs.table[0], rs.table[1], v, F).view(np.uint64)
+    assert np.array_equal((g[0] + g[1]).astype(np.uint64), want)
+
+
+def _softmax_oracle(sm, x0, x1):
+    """Shares of every stage of SoftmaxBlock on the CPU oracle."""
+    prg = ol.Prg(STATE)
+    offs = sm.offsets
+    row = fp.row_of(offs)
+    delta = tp.relu_rounds2(sm.rowmax, [x0, x1])
+    return delta, row, prg
+
+
+@pytest.mark.parametrize("heads,seq", [(1, 8), (2, 33)])
+def test_softmax_block_small(heads, seq):
+    offs = softmax.causal_offsets(heads, seq)
+    n = int(offs[-1])
+    x = _scores(offs, 50 + seq)
+    x0, x1 = _share(x, 51)
+    say("softmax block heads=%d seq=%d n=%d" % (heads, seq, n))
+    sm = softmax.SoftmaxBlock(offs, STATE, F, seed=13)
+    out = tuple(torch.empty(n, dtype=torch.int64, device="cuda") for _ in range(2))
+    sm.eval2(_pair_dev(x0, x1), out)
+    prob, st = fp.softmax_block(x, offs, sm.nexp_table, sm.recip.table, F)
+    assert np.array_equal(_recon(sm.delta), st["delta"].view(np.uint64))
+    assert np.array_equal(_recon(sm.e), st["exp"].view(np.uint64))
+    assert np.array_equal(_recon(sm.s), st["sum"].view(np.uint64))
+    assert np.array_equal(_recon(out), prob.view(np.uint64))
+    # Share level for the stages after the nExp gate (its own chain is
+    # checked share-for-share in test_gpu_spline.py).
+    prg = ol.Prg(STATE)
+    e = [u64(sm.e[0]), u64(sm.e[1])]
+    s = [u64(sm.s[0]), u64(sm.s[1])]
+    assert np.array_equal(s[0], ol.row_sum_ragged(e[0], offs.astype(np.int32)))
+    inv = tp.recip2(prg, sm.recip, s, u64(sm.shat))
+    row = fp.row_of(offs)
+    o = tp.beaver_trunc2(prg, e, inv, sm.tri, sm.tr, row_of=row)
+    g = [u64(out[0]), u64(out[1])]
+    assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
+
+
+def test_softmax_block_config_shape_twice():
+    offs = softmax.causal_offsets(12, 128)
+    n = int(offs[-1])
+    assert n == 99072
+    x = _scores(offs, 11)
+    x0, x1 = _share(x, 111)
+    say("softmax block config shape n=%d" % n)
+    sm = softmax.SoftmaxBlock(offs, STATE, F, seed=11)
+    prob, st = fp.softmax_block(x, offs, sm.nexp_table, sm.recip.table, F)
+    xin = _pair_dev(x0, x1)
+    out = tuple(torch.empty(n, dtype=torch.int64, device="cuda") for _ in range(2))
+    for _ in range(2):  # scratch and keys are reused across calls
+        sm.eval2(xin, out)
+        assert np.array_equal(_recon(out), prob.view(np.uint64))
+
+
+def test_layernorm_small_shares():
+    rows, cols = 4, 96
+    x = pfss.host_normal_fixed(60, 1.0, 0.0, F, rows * cols)
+    x[:cols] = x[:cols] * np.uint64(3)  # a wider row
+    x0, x1 = _share(x, 61)
+    say("layernorm %dx%d" % (rows, cols))
+    ln = layernorm.LayerNormBlock(rows, cols, STATE, F, seed=14)
+    out = tuple(torch.empty(rows * cols, dtype=torch.int64, device="cuda") for _ in range(2))
+    ln.eval2(_pair_dev(x0, x1), out)
+    y, st = fp.layernorm(x, rows, cols, F, ln.inv_len, ln.eps_q, ln.rsqrt.table)
+    assert np.array_equal(_recon(ln.mu), st["mu"].view(np.uint64))
+    assert np.array_equal(_recon(ln.var), st["var"].view(np.uint64))
+    assert np.array_equal(_recon(out), y.view(np.uint64))
+    # Share level: the whole chain on the oracle.
+    prg = ol.Prg(STATE)
+    row = np.repeat(np.arange(rows), cols)
+    xs = [x0, x1]
+    sums = [ol.row_sum(xs[p], rows, cols) * np.uint64(ln.inv_len) for p in (0, 1)]
+    mu = tp.trunc2(prg, ln.tr_mean, tp.open2(sums, ln.tr_mean.mask))
+    diff = [(xs[p] - mu[p][row]).astype(np.uint64) for p in (0, 1)]
+    sq = tp.beaver2(diff, diff, ln.tri_sq)
+    vs = [ol.row_sum(sq[p], rows, cols) * np.uint64(ln.inv_len) for p in (0, 1)]
+    var = tp.trunc2(prg, ln.tr_var, tp.open2(vs, ln.tr_var.mask))
+    v = tp.const2(var, ln.eps_q)
+    rs = tp.rsqrt2(prg, ln.rsqrt, v, tp.open2(v, ln.rsqrt.lut.mask))
+    o = tp.beaver_trunc2(prg, diff, rs, ln.tri_norm, ln.tr_norm, row_of=row)
+    g = [u64(out[0]), u64(out[1])]
+    assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
+
+
+def test_layernorm_config_shape_twice():
+    rows, cols = 128, 768
+    x = pfss.host_normal_fixed(12, 1.0, 0.0, F, rows * cols)
+    x0, x1 = _share(x, 121)
+    say("layernorm config shape %dx%d" % (rows, cols))
+    ln = layernorm.LayerNormBlock(rows, cols, STATE, F, seed=12)
+    y, _ = fp.layernorm(x, rows, cols, F, ln.inv_len, ln.eps_q, ln.rsqrt.table)
+    xin = _pair_dev(x0, x1)
+    out = tuple(torch.empty(rows * cols, dtype=torch.int64, device="cuda") for _ in range(2))
+    for _ in range(2):
+        ln.eval2(xin, out)
+        assert np.array_equal(_recon(out), y.view(np.uint64))
+
+
+def test_lin2_and_row_sum2_bounds():
+    """Row-indexed terms clamp their index; invalid operand descriptions are
+    rejected on the host."""
+    from suf_amd.tasks import lin2, operand, term
+    n = 64
+    a = (dev(np.arange(n, dtype=np.int64)), dev(np.arange(n, dtype=np.int64) * 2))
+    idx = dev(np.array([0, 1, 2, 1000, -5] + [3] * (n - 5), dtype=np.int32))
+    rowv = (dev(np.array([10, 20, 30, 40], dtype=np.int64)),
+            dev(np.array([1, 2, 3, 4], dtype=np.int64)))
+    out = tuple(torch.empty(n, dtype=torch.int64, device="cuda") for _ in range(2))
+    say("lin2 clamp")
+    lin2(operand(term(a), term(rowv, index=idx, shift=1, neg=True), const=7), n, out=out)
+    g0 = u64(out[0]).astype(np.int64)
+    ii = np.clip(np.array([0, 1, 2, 1000, -5] + [3] * (n - 5)), 0, 3)
+    assert np.array_equal(g0, np.arange(n) - 2 * np.array([10, 20, 30, 40])[ii] + 7)
+    bad = term(a)
+    bad.len = n - 1
+    with pytest.raises(native.SufHipError):
+        lin2(operand(bad), n, out=out)
+    with pytest.raises(native.SufHipError):
+        lin2(operand(term(a, stride=2, off=2)), n, out=out)

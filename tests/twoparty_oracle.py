@@ -1,0 +1,115 @@
+"""Two-party protocol steps composed from the CPU oracle (test infrastructure):
+the share-level expectation for the GPU task chains, step by step, from the
+same dealer material (keys and triples copied back from the device objects).
+
+Each helper returns both parties' shares as host u64 arrays.
+"""
+import numpy as np
+
+import oracle_lib as ol
+from gpu_util import host
+
+M64 = (1 << 64) - 1
+
+
+def u(a):
+    return np.asarray(a).astype(np.uint64) if np.asarray(a).dtype != np.uint64 else np.asarray(a)
+
+
+def lut2(lut, xhat):
+    """Both parties' coefficient rows [n][words] of a tasks.CoeffLut."""
+    n = xhat.size
+    return [ol.lut_eval(lut.blobs[p], lut.key_bytes, 1, u(xhat), lut.words).reshape(n, lut.words)
+            for p in (0, 1)]
+
+
+def beaver2(x, y, tri, row_of=None):
+    """z_p of the Beaver product of shares x = (x0, x1), y = (y0, y1) with a
+    tasks.Triples (row-broadcast when row_of is given: y and b per row)."""
+    sh = [tri.shares(p) for p in (0, 1)]
+    a = [sh[p][0] for p in (0, 1)]
+    b = [sh[p][1] if row_of is None else sh[p][1][row_of] for p in (0, 1)]
+    c = [sh[p][2] for p in (0, 1)]
+    yy = [u(y[p]) if row_of is None else u(y[p])[row_of] for p in (0, 1)]
+    d = ((u(x[0]) - a[0]) + (u(x[1]) - a[1])).astype(np.uint64)
+    e = ((yy[0] - b[0]) + (yy[1] - b[1])).astype(np.uint64)
+    return [ol.beaver_mul(p, a[p], b[p], c[p], d, e) for p in (0, 1)]
+
+
+def open2(z, mask):
+    return (u(z[0]) + u(z[1]) + np.uint64(mask & M64)).astype(np.uint64)
+
+
+def trunc2(prg, tr, zhat):
+    """Both parties' outputs of a tasks.Trunc at the masked open zhat."""
+    return [ol.trunc_eval(prg, tr.kind, tr.f, host(tr.keys[p]), u(zhat)) for p in (0, 1)]
+
+
+def beaver_trunc2(prg, x, y, tri, tr, row_of=None):
+    z = beaver2(x, y, tri, row_of)
+    return trunc2(prg, tr, open2(z, tr.mask))
+
+
+def add2(x, y):
+    return [(u(x[p]) + u(y[p])).astype(np.uint64) for p in (0, 1)]
+
+
+def const2(x, c):
+    """x + c with the public constant on party 0's share."""
+    return [(u(x[0]) + np.uint64(c & M64)).astype(np.uint64), u(x[1])]
+
+
+def neg2(x):
+    return [(np.uint64(0) - u(x[p])).astype(np.uint64) for p in (0, 1)]
+
+
+def recon(x):
+    return (u(x[0]) + u(x[1])).astype(np.uint64)
+
+
+def recip2(prg, rc, x, xhat):
+    """softmax.Recip on shares x with masked open xhat."""
+    f = rc.f
+    coef = lut2(rc.lut, xhat)
+    t = beaver_trunc2(prg, [coef[0][:, 1], coef[1][:, 1]], x, rc.tri[0], rc.tr[0])
+    y = add2(t, [coef[0][:, 0], coef[1][:, 0]])
+    for it in range(rc.iters):
+        xy = beaver_trunc2(prg, y, x, rc.tri[1 + 2 * it], rc.tr[1 + 2 * it])
+        y = beaver_trunc2(prg, y, const2(neg2(xy), 2 << f), rc.tri[2 + 2 * it],
+                          rc.tr[2 + 2 * it])
+    return y
+
+
+def rsqrt2(prg, rs, v, vhat):
+    """layernorm.Rsqrt on shares v with masked open vhat."""
+    f = rs.f
+    coef = lut2(rs.lut, vhat)
+    t = beaver_trunc2(prg, [coef[0][:, 1], coef[1][:, 1]], v, rs.tri[0], rs.tr[0])
+    y = add2(t, [coef[0][:, 0], coef[1][:, 0]])
+    for it in range(rs.iters):
+        ta, tb, tc = rs.tr[1 + 3 * it: 4 + 3 * it]
+        ka, kb, kc = rs.tri[1 + 3 * it: 4 + 3 * it]
+        y2 = beaver_trunc2(prg, y, y, ka, ta)
+        h = beaver_trunc2(prg, v, y2, kb, tb)
+        y = beaver_trunc2(prg, y, const2(neg2(h), 3 << (f - 1)), kc, tc)
+    return y
+
+
+def relu_rounds2(rm, x):
+    """softmax.RowMaxDiff on shares x: delta shares."""
+    cur = [u(x[0]), u(x[1])]
+    for rd in rm.rounds:
+        src_a, src_b = rd["src"]
+        pair = src_b >= 0
+        bb = np.where(pair, src_b, 0)
+        xa = [cur[p][src_a] for p in (0, 1)]
+        xb = [cur[p][bb] for p in (0, 1)]
+        xhat = ((xa[0] - xb[0]) + (xa[1] - xb[1]) + np.uint64(rd["lut"].mask)).astype(np.uint64)
+        q = lut2(rd["lut"], xhat)
+        nxt = []
+        for p in (0, 1):
+            v = (xb[p] + q[p][:, 0] + q[p][:, 1] * xhat).astype(np.uint64)
+            nxt.append(np.where(pair, v, xa[p]).astype(np.uint64))
+        cur = nxt
+    mi = host(rm.max_index).astype(np.int64)
+    return [(cur[p][mi] - u(x[p])).astype(np.uint64) for p in (0, 1)]
