@@ -248,6 +248,96 @@ def cpu_matmul_baseline(g, state, Xd, Wd, out, seconds):
                       % (rows, M, threads, mism), "mismatches": mism}
 
 
+def bench_softmax_ln(steps, warmup, frac_bits=12, cpu=True):
+    """Softmax over 12 heads x 128 x 128 causal score rows (scores
+    round(N(0,2) 2^12), mt(11)) followed by LayerNorm over 128 x 768
+    (round(N(0,1) 2^12), mt(12)), both parties; shares from mt(111), mt(121);
+    dealer material from suf_amd.tasks.Dealer(11), Dealer(12).  Returns ms
+    per block (softmax + LayerNorm) and each part."""
+    import numpy as np
+    import torch
+
+    from suf_amd import layernorm, pfss, softmax
+
+    state = bytes((pfss.host_mt19937_64(3, 128) & np.uint64(0xFF)).astype(np.uint8))
+    offs = softmax.causal_offsets(12, 128)
+    n_sm = int(offs[-1])
+    rows, cols = 128, 768
+    sc = pfss.host_normal_fixed(11, 2.0, 0.0, frac_bits, n_sm)
+    xl = pfss.host_normal_fixed(12, 1.0, 0.0, frac_bits, rows * cols)
+    dev = lambda v: torch.from_numpy(np.ascontiguousarray(v).view(np.int64).copy()).cuda()
+
+    def shares(v, seed):
+        v0 = pfss.host_mt19937_64(seed, v.size)
+        return v0, (v - v0).astype(np.uint64)
+
+    s0, s1 = shares(sc, 111)
+    l0, l1 = shares(xl, 121)
+    sin, lin = (dev(s0), dev(s1)), (dev(l0), dev(l1))
+    sm = softmax.SoftmaxBlock(offs, state, frac_bits, seed=11)
+    ln = layernorm.LayerNormBlock(rows, cols, state, frac_bits, seed=12)
+    sout = tuple(torch.empty(n_sm, dtype=torch.int64, device="cuda") for _ in range(2))
+    lout = tuple(torch.empty(rows * cols, dtype=torch.int64, device="cuda") for _ in range(2))
+    for _ in range(warmup):
+        sm.eval2(sin, sout)
+        ln.eval2(lin, lout)
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for s in range(steps):
+        ev[s][0].record()
+        sm.eval2(sin, sout)
+        ev[s][1].record()
+        ln.eval2(lin, lout)
+        ev[s][2].record()
+    torch.cuda.synchronize()
+    sm_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]))
+    ln_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
+    res = {"ms": sm_ms + ln_ms, "softmax_ms": sm_ms, "layernorm_ms": ln_ms,
+           "softmax_shape": "12 heads x 128 causal rows (%d scores)" % n_sm,
+           "layernorm_shape": [rows, cols], "frac_bits": frac_bits, "steps": steps,
+           "check": "not run (--no-cpu)"}
+    if cpu:
+        res.update(cpu_softmax_ln_baseline(state, sm, ln, (s0, s1), (l0, l1), sc, xl, sout, lout,
+                                           frac_bits))
+    return res
+
+
+def cpu_softmax_ln_baseline(state, sm, ln, sx, lx, sc, xl, sout, lout, f):
+    """The same two-party softmax and LayerNorm chains on the host, composed
+    from the oracle's plain-C steps (interval LUT, Beaver, truncation gate with
+    its DCF walks), one thread, over the whole batch; shares compared with the
+    GPU's, and the reconstruction checked against the fixed-point closed form."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import fixed_point as fp
+    import oracle_lib as ol
+    import twoparty_oracle as tp
+
+    h = lambda t: t.cpu().numpy().view(np.uint64)
+    t0 = time.perf_counter()
+    prob, _ = tp.softmax2(ol.Prg(state), sm, list(sx))
+    t1 = time.perf_counter()
+    y = tp.layernorm2(ol.Prg(state), ln, list(lx))
+    t2 = time.perf_counter()
+    mism = sum(int(np.count_nonzero(prob[p] != h(sout[p]))) for p in (0, 1))
+    mism += sum(int(np.count_nonzero(y[p] != h(lout[p]))) for p in (0, 1))
+    want_p, _ = fp.softmax_block(sc, sm.offsets, sm.nexp_table, sm.recip.table, f)
+    want_y, _ = fp.layernorm(xl, ln.rows, ln.cols, f, ln.inv_len, ln.eps_q, ln.rsqrt.table)
+    rec_ok = (np.array_equal((h(sout[0]) + h(sout[1])).astype(np.uint64), want_p.view(np.uint64))
+              and np.array_equal((h(lout[0]) + h(lout[1])).astype(np.uint64),
+                                 want_y.view(np.uint64)))
+    return {"check": "ok" if rec_ok and mism == 0 else "MISMATCH",
+            "cpu_baseline": {"value": (t2 - t0) * 1e3, "unit": "ms per block (both parties)",
+                             "softmax_ms": (t1 - t0) * 1e3, "layernorm_ms": (t2 - t1) * 1e3,
+                             "cores": 1, "kind": "port",
+                             "sample": "the whole block (oracle C restatement of the LUT, "
+                                       "Beaver and truncation-gate steps, one thread); shares "
+                                       "compared with the GPU: %d mismatches" % mism,
+                             "mismatches": mism}}
+
+
 def cpu_baseline(keys0, keys1, xhat, gpu_bits0, gpu_bits1, seconds):
     """The reference's own myl7 batch evaluation (oracle/_ref, built from the
     reference sources), single thread as in Myl7FssBackend::eval_dcf_many_u64
@@ -431,8 +521,10 @@ def main():
         gate_cpu = 0.0 if a.no_cpu else a.cpu_seconds / 2
         line["spline_gate"] = bench_spline(max(a.steps // 2, 1), 2, cpu_seconds=gate_cpu)
         line["beaver_matmul_trunc"] = bench_matmul(max(a.steps // 2, 1), 2, cpu_seconds=gate_cpu)
+        line["softmax_layernorm"] = bench_softmax_ln(max(a.steps // 2, 1), 2, cpu=not a.no_cpu)
         ok = ok and line["spline_gate"]["check"] == "ok"
         ok = ok and line["beaver_matmul_trunc"]["check"] == "ok"
+        ok = ok and line["softmax_layernorm"]["check"] in ("ok", "not run (--no-cpu)")
     if not a.no_cpu:
         sample = 1 << 14
         g0 = out0[:sample].cpu().numpy()

@@ -243,8 +243,9 @@ int sufhip_add_shifted(const uint64_t* d_y, const uint64_t* d_add, size_t add_st
  * 2 - xy, 1.5 - h/2, t + c0, inv[row].
  *
  * A term reads, for element i and party p, p[p][j * stride + off] with
- * j = index ? index[i] : i (index: int32, e.g. the row of element i), shifted
- * left by `shift` and subtracted when `negate` is set.  An absent term has
+ * j = index ? index[i] : i (index: int32, e.g. the row of element i),
+ * multiplies it by the public `mul` (mod 2^64), shifts it left by `shift` and
+ * subtracts it when `negate` is set.  An absent term has
  * p[0] == p[1] == NULL; a present one needs both.  j is clamped to
  * [0, len), so no index value reads outside the arrays; without an index,
  * len must be >= n. */
@@ -256,6 +257,7 @@ typedef struct sufhip_term2 {
   size_t off;    /* < stride */
   int shift;     /* 0..63 */
   int negate;
+  uint64_t mul;  /* public multiplier applied before the shift (0 acts as 1) */
 } sufhip_term2;
 
 /* Per element and party: t[0] + t[1] + [p == 0] party0_const, i.e. the
@@ -437,6 +439,43 @@ int sufhip_beaver_matmul2d_batched(int party, const uint64_t* d_D_open, const ui
                                    const uint64_t* d_C_tri_share, int batches, int M, int K, int N,
                                    int w_transposed, int has_scale, int64_t mul_const,
                                    int mul_shift, uint64_t* d_out, void* stream);
+/* Two-party batched Beaver product with one triple per batch instance (the
+ * per-head QK^T and PV products of attention_forward,
+ * src/nn/attention_block.cpp:1590-1850, as BatchedMatmul2DTask runs them; the
+ * reference's batched launcher reuses one triple for every batch,
+ * cuda_primitives.hpp:149-150): for batch b and party p,
+ *   out_p[b] = C_p[b] + D[b] * B_p[b] + A_p[b] * E[b] (+ D[b] * E[b] for p = 0)
+ * with D [b][M x K], E [b][K x N], A_p [b][M x K], B_p [b][K x N],
+ * C_p and out_p [b][M x N], row-major, mod 2^64. */
+int sufhip_beaver_matmul2_batched(const uint64_t* d_D_open, const uint64_t* d_E_open,
+                                  const uint64_t* d_A0, const uint64_t* d_A1,
+                                  const uint64_t* d_B0, const uint64_t* d_B1,
+                                  const uint64_t* d_C0, const uint64_t* d_C1, int batches, int M,
+                                  int K, int N, uint64_t* d_out0, uint64_t* d_out1,
+                                  void* stream);
+
+/* Share x public weight for both parties (nn::matmul_publicW_gpu,
+ * src/nn/matmul_gpu.cu:388-720; CPU form src/nn/matmul_publicW.cpp:17-36):
+ * Y_p = X_p * W mod 2^64, X_p [M x K] u64 shares, W [K x N] public int64, on
+ * the int8 matrix cores with W in `digits` balanced base-256 digit planes.
+ * sufhip_public_w_digits: host helper, the digits the weights need (1..8).
+ * sufhip_public_w_prepare: W's planes [digits][N][K] (done once per weight;
+ * d_planes of sufhip_public_w_planes_bytes bytes, 16-byte aligned).
+ * sufhip_matmul_public2: M, K, N multiples of 32, digits in 1..4 with
+ * digits * K < 2^17 (exact int32 accumulation); writes the shares
+ * (d_out0 and d_out1) and/or the masked open d_zhat = Y_0 + Y_1 + mask that
+ * the following truncation gate consumes.  d_work: 16-byte aligned, of
+ * sufhip_matmul_public2_work_bytes(M, K, N) bytes (0 for a bad shape). */
+int sufhip_public_w_digits(const int64_t* w, size_t n);
+size_t sufhip_public_w_planes_bytes(int K, int N, int digits);
+int sufhip_public_w_prepare(const int64_t* d_W, int K, int N, int digits, int8_t* d_planes,
+                            void* stream);
+size_t sufhip_matmul_public2_work_bytes(int M, int K, int N);
+int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int K, int N,
+                          const int8_t* d_planes, int digits, uint64_t* d_out0, uint64_t* d_out1,
+                          uint64_t* d_zhat, uint64_t mask, void* d_work, size_t work_bytes,
+                          void* stream);
+
 /* launch_row_mean_kernel (:169-174): sum >> log2(L) for power-of-two L, else
  * the u64 sum divided by L as a plain integer (the reference's formula). */
 int sufhip_row_mean(const uint64_t* d_mat, int rows, int cols, const int* d_valid_lens,

@@ -22,9 +22,16 @@ formed: an input outside that range raises instead of wrapping.
   layernorm       LayerNormTask (phase_tasks.hpp:2232-2610) without gamma/beta,
                   as transformer_layer_forward runs it
                   (src/nn/transformer_layer.cpp:626-760)
+  attention       attention_forward's causal prefill (src/nn/attention_block.cpp:
+                  1500-1900): per-head Q K^T scaled by inv_sqrt and truncated by
+                  2f, softmax over the causal rows, P V truncated by f
+  transformer_layer  transformer_layer_forward (transformer_layer.cpp:435-830)
+                  with mlp_forward (src/nn/mlp_block.cpp:378-767): LN, QKV,
+                  attention, Wout, residual, LN, W1, GeLU cubic, W2, residual
 
 Pinning (tests/test_oracle_fixed_point.py): each formula against the real
-function it approximates (exp, 1/x, 1/sqrt, softmax, layer norm in float64)
+function it approximates (exp, 1/x, 1/sqrt, softmax, layer norm, a float64
+GPT-2 layer with the same weights)
 within the table's stated accuracy, against brute force (row max, piece
 selection at every boundary), and against hand-computed values.
 """
@@ -152,3 +159,63 @@ def layernorm(x, rows, cols, f, inv_len, eps_q, rsqrt, rsqrt_iters=1):
     r = rsqrt_task(rsqrt[0], rsqrt[1], v, f, rsqrt_iters)
     y = mul_shift(d, np.broadcast_to(r[:, None], d.shape), f, "ln d r")
     return y.reshape(-1), {"mu": mu, "var": var, "rsqrt": r}
+
+
+def matmul_shift(X, W, s, what="matmul"):
+    """floor(X W / 2^s) for int64 matrices, exact (checked against 2^62)."""
+    X = np.asarray(X, dtype=np.int64)
+    W = np.asarray(W, dtype=np.int64)
+    k = X.shape[-1]
+    bound = float(np.abs(X).max(initial=0)) * float(np.abs(W).max(initial=0)) * k
+    if bound >= LIM * (1 - 1e-9):
+        raise ValueError("%s: product outside the exact range" % what)
+    return np.matmul(X, W) >> s
+
+
+def causal_offsets(heads, seq):
+    lens = np.tile(np.arange(1, seq + 1), heads)
+    return np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+
+
+def attention(qkv, seq, d, heads, f, nexp, recip):
+    """Causal attention on Q(f) QKV rows [seq x 3d] -> context [seq x d]."""
+    dh = d // heads
+    qkv = _i64(qkv).reshape(seq, 3 * d)
+    inv_sqrt = max(int(np.floor(abs((1.0 / np.sqrt(dh)) * (1 << f)) + 0.5)), 1)
+    offs = causal_offsets(heads, seq)
+    scores = []
+    for h in range(heads):
+        Q = qkv[:, h * dh:(h + 1) * dh]
+        K = qkv[:, d + h * dh:d + (h + 1) * dh]
+        S = matmul_shift(Q, K.T, 0, "attention Q K^T")
+        S = mul_shift(S, np.full(S.shape, inv_sqrt, dtype=np.int64), 2 * f, "attention scale")
+        for r in range(seq):
+            scores.append(S[r, :r + 1])
+    scores = np.concatenate(scores)
+    prob, st = softmax_block(scores, offs, nexp, recip, f)
+    ctx = np.zeros((seq, d), dtype=np.int64)
+    for h in range(heads):
+        P = np.zeros((seq, seq), dtype=np.int64)
+        for r in range(seq):
+            b = int(offs[h * seq + r])
+            P[r, :r + 1] = prob[b:b + r + 1]
+        V = qkv[:, 2 * d + h * dh:2 * d + (h + 1) * dh]
+        ctx[:, h * dh:(h + 1) * dh] = matmul_shift(P, V, f, "attention P V")
+    return ctx.reshape(-1), {"scores": scores, "prob": prob, **st}
+
+
+def transformer_layer(x, W, seq, d, heads, ffn, f, tabs, inv_len, eps_q):
+    """x [seq x d] Q(f) -> layer output; W: dict of int64 Wqkv [d x 3d],
+    Wout [d x d], W1 [d x ffn], W2 [ffn x d]; tabs: dict of (alpha, coeffs)
+    for "nexp", "recip", "rsqrt", "gelu"."""
+    x = _i64(x).reshape(seq, d)
+    h1, _ = layernorm(x, seq, d, f, inv_len, eps_q, tabs["rsqrt"])
+    qkv = matmul_shift(h1.reshape(seq, d), W["Wqkv"], f, "qkv")
+    ctx, st = attention(qkv, seq, d, heads, f, tabs["nexp"], tabs["recip"])
+    r1 = matmul_shift(ctx.reshape(seq, d), W["Wout"], f, "out proj") + x
+    h2, _ = layernorm(r1, seq, d, f, inv_len, eps_q, tabs["rsqrt"])
+    u = matmul_shift(h2.reshape(seq, d), W["W1"], f, "w1")
+    g = cubic_task(tabs["gelu"][0], tabs["gelu"][1], u.reshape(-1), f).reshape(seq, ffn)
+    out = matmul_shift(g, W["W2"], f, "w2") + r1
+    return out.reshape(-1), {"h1": h1, "qkv": qkv.reshape(-1), "ctx": ctx, "r1": r1.reshape(-1),
+                             "h2": h2, "u": u.reshape(-1), "g": g.reshape(-1), **st}

@@ -14,7 +14,8 @@
 // transposed ([k][m], so a lane's two rows are one 16-byte LDS read) and the
 // RHS tile ([k][n], a lane's four columns are two 16-byte reads), with B + E
 // folded in while staging.  Batched launches put the batch in grid.z and
-// reuse the same A, B, C for every batch instance (cuda_primitives.hpp:149-150).
+// reuse the same A, B, C for every batch instance (cuda_primitives.hpp:149-150);
+// the two-party form puts (batch, party) in grid.z with one triple per batch.
 #include <hip/hip_runtime.h>
 
 #include "sufhip_internal.hpp"
@@ -37,6 +38,14 @@ struct MmArgs {
   int has_scale;
   int64_t mul_const;
   int mul_shift;
+  // Two-party form: grid.z = 2 * batch + party; each party's triple shares
+  // and output, one triple per batch instance ([b][M][K], [b][K][N],
+  // [b][M][N]).  A, B, C, out and party above are unused then.
+  int two_party;
+  const uint64_t* A2[2];
+  const uint64_t* B2[2];
+  const uint64_t* C2[2];
+  uint64_t* out2[2];
 };
 
 __device__ __forceinline__ uint64_t scaled(uint64_t acc, const MmArgs& a) {
@@ -59,11 +68,18 @@ __global__ void __launch_bounds__(kMmThreads) beaver_matmul_kernel(MmArgs a) {
   const int tid = threadIdx.x;
   const int tx = tid & 15, ty = tid >> 4;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const size_t b = blockIdx.z;
   const int M = a.M, K = a.K, N = a.N;
+  const int party = a.two_party ? int(blockIdx.z & 1) : a.party;
+  const size_t b = a.two_party ? blockIdx.z >> 1 : blockIdx.z;
   const uint64_t* D = a.D + b * size_t(M) * K;
   const uint64_t* E = a.E + b * size_t(K) * N;
-  const bool p0 = a.party == 0;
+  // Triple shares and output of this (batch, party): shared by every batch
+  // in the one-party form (cuda_primitives.hpp:149-150), per batch otherwise.
+  const uint64_t* TA = a.two_party ? a.A2[party] + b * size_t(M) * K : a.A;
+  const uint64_t* TB = a.two_party ? a.B2[party] + b * size_t(K) * N : a.B;
+  const uint64_t* TC = a.two_party ? a.C2[party] + b * size_t(M) * N : a.C;
+  uint64_t* OUT = a.two_party ? a.out2[party] + b * size_t(M) * N : a.out + b * size_t(M) * N;
+  const bool p0 = party == 0;
 
   uint64_t acc[2][4];
   uint32_t hi[2][4];
@@ -84,7 +100,7 @@ __global__ void __launch_bounds__(kMmThreads) beaver_matmul_kernel(MmArgs a) {
       const int mm = idx >> 4, kk = idx & 15;
       const int gm = m0 + mm, gk = k0 + kk;
       uint64_t v = 0;
-      if (gm < M && gk < K2) v = gk < K ? D[size_t(gm) * K + gk] : a.A[size_t(gm) * K + (gk - K)];
+      if (gm < M && gk < K2) v = gk < K ? D[size_t(gm) * K + gk] : TA[size_t(gm) * K + (gk - K)];
       sL[kk][mm] = v;
     }
     // RHS tile: 16 k x 64 n = 1024 values, 4 per lane.  k < K: B (+E for party 0), else E.
@@ -105,7 +121,7 @@ __global__ void __launch_bounds__(kMmThreads) beaver_matmul_kernel(MmArgs a) {
         const int kr = gk < K ? gk : gk - K;
         const size_t off = kTrans ? size_t(gn) * K + kr : size_t(kr) * N + gn;
         if (gk < K) {
-          v = a.B[off];
+          v = TB[off];
           if (p0) v += E[off];
         } else {
           v = E[off];
@@ -143,8 +159,8 @@ __global__ void __launch_bounds__(kMmThreads) beaver_matmul_kernel(MmArgs a) {
       const int gn = n0 + 4 * tx + j;
       if (gn >= N) continue;
       const size_t o = size_t(gm) * N + gn;
-      const uint64_t v = a.C[o] + acc[i][j] + (uint64_t(hi[i][j]) << 32);
-      a.out[b * size_t(M) * N + o] = scaled(v, a);
+      const uint64_t v = TC[o] + acc[i][j] + (uint64_t(hi[i][j]) << 32);
+      OUT[o] = scaled(v, a);
     }
   }
 }
@@ -156,13 +172,29 @@ int launch(int party, const uint64_t* D, const uint64_t* E, const uint64_t* A, c
   SUFHIP_REQUIRE(D && E && A && B && C && out, "sufhip_beaver_matmul2d: null pointer");
   SUFHIP_REQUIRE(batches <= 65535, "sufhip_beaver_matmul2d: at most 65535 batches");
   SUFHIP_REQUIRE(size_t(K) * 2 < (size_t(1) << 31), "sufhip_beaver_matmul2d: K too large");
-  MmArgs a{D, E, A, B, C, out, M, K, N, party, has_scale, mul_const, mul_shift};
+  MmArgs a{D, E, A, B, C, out, M, K, N, party, has_scale, mul_const, mul_shift, 0,
+           {nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}};
   const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, batches), block(kMmThreads);
   if (w_transposed)
     hipLaunchKernelGGL(beaver_matmul_kernel<true>, grid, block, 0, as_stream(stream), a);
   else
     hipLaunchKernelGGL(beaver_matmul_kernel<false>, grid, block, 0, as_stream(stream), a);
   return check_launch("beaver_matmul_kernel");
+}
+
+int launch2(const uint64_t* D, const uint64_t* E, const uint64_t* A0, const uint64_t* A1,
+            const uint64_t* B0, const uint64_t* B1, const uint64_t* C0, const uint64_t* C1,
+            int batches, int M, int K, int N, uint64_t* out0, uint64_t* out1, void* stream) {
+  if (batches <= 0 || M <= 0 || K <= 0 || N <= 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(D && E && A0 && A1 && B0 && B1 && C0 && C1 && out0 && out1,
+                 "sufhip_beaver_matmul2_batched: null pointer");
+  SUFHIP_REQUIRE(batches <= 32767, "sufhip_beaver_matmul2_batched: at most 32767 batches");
+  SUFHIP_REQUIRE(size_t(K) * 2 < (size_t(1) << 31), "sufhip_beaver_matmul2_batched: K too large");
+  MmArgs a{D, E, nullptr, nullptr, nullptr, nullptr, M, K, N, 0, 0, 0, 0, 1,
+           {A0, A1}, {B0, B1}, {C0, C1}, {out0, out1}};
+  const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, 2 * batches), block(kMmThreads);
+  hipLaunchKernelGGL(beaver_matmul_kernel<false>, grid, block, 0, as_stream(stream), a);
+  return check_launch("beaver_matmul_kernel (two-party)");
 }
 
 }  // namespace
@@ -188,6 +220,16 @@ int sufhip_beaver_matmul2d_batched(int party, const uint64_t* d_D_open, const ui
                                    int mul_shift, uint64_t* d_out, void* stream) {
   return launch(party, d_D_open, d_E_open, d_A_tri_share, d_B_tri_share, d_C_tri_share, batches, M,
                 K, N, w_transposed, has_scale, mul_const, mul_shift, d_out, stream);
+}
+
+int sufhip_beaver_matmul2_batched(const uint64_t* d_D_open, const uint64_t* d_E_open,
+                                   const uint64_t* d_A0, const uint64_t* d_A1,
+                                   const uint64_t* d_B0, const uint64_t* d_B1,
+                                   const uint64_t* d_C0, const uint64_t* d_C1, int batches, int M,
+                                   int K, int N, uint64_t* d_out0, uint64_t* d_out1,
+                                   void* stream) {
+  return launch2(d_D_open, d_E_open, d_A0, d_A1, d_B0, d_B1, d_C0, d_C1, batches, M, K, N, d_out0,
+                 d_out1, stream);
 }
 
 }  // extern "C"

@@ -111,7 +111,9 @@ __device__ __forceinline__ uint64_t term_at(const sufhip_term2& t, int p, size_t
     j = r < 0 ? 0 : size_t(r);
   }
   if (j >= t.len) j = t.len - 1;
-  const uint64_t v = t.p[p][j * t.stride + t.off] << t.shift;
+  uint64_t v = t.p[p][j * t.stride + t.off];
+  if (t.mul) v *= t.mul;
+  v <<= t.shift;
   return t.negate ? uint64_t(0) - v : v;
 }
 
@@ -200,8 +202,8 @@ int check_term(const sufhip_term2& t, size_t n, bool allow_shift, const char* wh
     return SUFHIP_ERR_INVALID;
   }
   if (t.stride < 1 || t.off >= t.stride || t.shift < 0 || t.shift > 63 ||
-      (!allow_shift && (t.shift != 0 || t.negate))) {
-    set_error(std::string(what) + ": bad term stride/offset/shift/negate");
+      (!allow_shift && (t.shift != 0 || t.negate || t.mul > 1))) {
+    set_error(std::string(what) + ": bad term stride/offset/shift/negate/mul");
     return SUFHIP_ERR_INVALID;
   }
   if (t.len == 0 || (!t.index && t.len < n)) {

@@ -1,0 +1,276 @@
+"""A GPT-2-shaped secure transformer layer for two parties on one GPU.
+
+transformer_layer_forward (src/nn/transformer_layer.cpp:435-830) with
+attention_forward (src/nn/attention_block.cpp:931-1900, causal prefill) and
+mlp_forward (src/nn/mlp_block.cpp:378-767):
+
+  h1  = LayerNorm(x)
+  qkv = trunc_f(h1 Wqkv)                      public weights, MFMA digit GEMM
+  s   = trunc_2f(inv_sqrt * Q_h K_h^T)        Beaver per head, causal rows packed
+  p   = Softmax(s)                            suf_amd.softmax.SoftmaxBlock
+  c   = trunc_f(P_h V_h), heads merged        Beaver per head
+  r1  = trunc_f(c Wout) + x
+  h2  = LayerNorm(r1)
+  u   = trunc_f(h2 W1); g = GeLU(u)           spline gate (CubicPolyTask)
+  out = trunc_f(g W2) + r1
+
+Every truncation is a GapARS gate with its own key; every Beaver product has
+its own triple (one per head for the attention products; the reference
+reuses one triple for all heads and one trunc key per task).  The score
+scale inv_sqrt = llround(2^f / sqrt(d_head)) is a public factor folded into
+the truncation's open (the reference applies (acc * inv_sqrt) >> f to each
+share in the matmul epilogue, cuda_primitives.cu:391-417, which
+reconstructs to the same value up to a carry of one unit before the
+truncation).  No biases (the reference layer passes none).
+"""
+import math
+
+import numpy as np
+import torch
+
+from . import native, spline, tables
+from .layernorm import LayerNormBlock
+from .softmax import SoftmaxBlock, causal_offsets
+from .tasks import Dealer, Trunc, dev, dev_i32, lin2, operand, pair, ptr, stream_ptr, term
+
+M64 = (1 << 64) - 1
+
+
+class PublicMatmulTrunc:
+    """Y = trunc_f(X W) for both parties; W public int64 [K x N] (host)."""
+
+    def __init__(self, M, K, N, W, dealer, prg_state, frac_bits=12, device="cuda"):
+        lib = native.load()
+        self.M, self.K, self.N, self.f = M, K, N, frac_bits
+        W = np.ascontiguousarray(W, dtype=np.int64).reshape(K, N)
+        self.W = W
+        self.digits = lib.sufhip_public_w_digits(W.ctypes.data, W.size)
+        pb = lib.sufhip_public_w_planes_bytes(K, N, self.digits)
+        if pb == 0:
+            raise native.SufHipError("PublicMatmulTrunc: unsupported shape %r" % ((M, K, N),))
+        self.planes = torch.empty((pb + 15) // 16 * 2, dtype=torch.int64, device=device)
+        dW = dev(W, device)
+        native.call("sufhip_public_w_prepare", ptr(dW), K, N, self.digits, ptr(self.planes),
+                    stream_ptr())
+        torch.cuda.current_stream().synchronize()
+        wb = lib.sufhip_matmul_public2_work_bytes(M, K, N)
+        self.work = torch.empty((wb + 15) // 16 * 2, dtype=torch.int64, device=device)
+        self.work_bytes = self.work.numel() * 8
+        self.tr = Trunc(dealer, frac_bits, M * N, prg_state, device=device)
+        self.zhat = torch.empty(M * N, dtype=torch.int64, device=device)
+
+    def truncs(self):
+        return [self.tr]
+
+    def product2(self, X, out=None, zhat=None, mask=0):
+        native.call("sufhip_matmul_public2", ptr(X[0]), ptr(X[1]), self.M, self.K, self.N,
+                    ptr(self.planes), self.digits,
+                    ptr(out[0]) if out is not None else None,
+                    ptr(out[1]) if out is not None else None, ptr(zhat), mask & M64,
+                    ptr(self.work), self.work_bytes, stream_ptr())
+
+    def eval2(self, X, out):
+        self.product2(X, zhat=self.zhat, mask=self.tr.mask)
+        self.tr.finish(self.zhat, out)
+        return out
+
+
+class BatchedTriples:
+    """Beaver matrix triples per batch: A [b][M x K], B [b][K x N] uniform,
+    C = A B mod 2^64; party 0 holds the drawn shares."""
+
+    def __init__(self, dealer, batches, M, K, N, device="cuda"):
+        A = dealer.words(batches * M * K).reshape(batches, M, K)
+        B = dealer.words(batches * K * N).reshape(batches, K, N)
+        C = np.matmul(A, B)  # uint64: exact mod 2^64
+        A0 = dealer.words(A.size).reshape(A.shape)
+        B0 = dealer.words(B.size).reshape(B.shape)
+        C0 = dealer.words(C.size).reshape(C.shape)
+        self.A = (dev(A0, device), dev(A - A0, device))
+        self.B = (dev(B0, device), dev(B - B0, device))
+        self.C = (dev(C0, device), dev(C - C0, device))
+        self.host = (A, B, C, A0, B0, C0)
+
+
+def _beaver_batched(D, E, tri, batches, M, K, N, out):
+    native.call("sufhip_beaver_matmul2_batched", ptr(D), ptr(E), ptr(tri.A[0]), ptr(tri.A[1]),
+                ptr(tri.B[0]), ptr(tri.B[1]), ptr(tri.C[0]), ptr(tri.C[1]), batches, M, K, N,
+                ptr(out[0]), ptr(out[1]), stream_ptr())
+
+
+def attention_maps(seq, d, heads):
+    """Index maps (int32) between the layouts of the attention core:
+    gq/gk/gv gather Q_h [seq x dh], K_h^T [dh x seq], V_h [seq x dh] from the
+    [seq x 3d] QKV rows; gs gathers the packed causal scores from the dense
+    [heads][seq][seq] products; gp gathers dense P_h from the packed
+    probabilities (masked entries read the zero slot n_packed); gc merges the
+    heads' [heads][seq][dh] context into [seq x d]."""
+    dh = d // heads
+    h = np.arange(heads)[:, None, None]
+    m = np.arange(seq)[None, :, None]
+    k = np.arange(dh)[None, None, :]
+    gq = m * 3 * d + h * dh + k                                   # [h][m][k]
+    kk = np.arange(dh)[None, :, None]
+    nn_ = np.arange(seq)[None, None, :]
+    gk = nn_ * 3 * d + d + h * dh + kk                            # [h][k][n]
+    ks = np.arange(seq)[None, :, None]
+    nd = np.arange(dh)[None, None, :]
+    gv = ks * 3 * d + 2 * d + h * dh + nd                         # [h][k][n]
+    offs = causal_offsets(heads, seq)
+    n_packed = int(offs[-1])
+    rows = np.repeat(np.arange(heads * seq), np.tile(np.arange(1, seq + 1), heads))
+    col = np.arange(n_packed) - offs[:-1][rows]
+    gs = (rows // seq) * seq * seq + (rows % seq) * seq + col      # packed -> dense index
+    r = np.arange(seq)[None, :, None]
+    c = np.arange(seq)[None, None, :]
+    row_id = h * seq + r
+    gp = np.where(c <= r, offs[:-1][row_id] + c, n_packed)       # [h][m][k]
+    t = np.arange(seq)[:, None]
+    j = np.arange(d)[None, :]
+    gc = (j // dh) * seq * dh + t * dh + (j % dh)                 # [t][j]
+    return {"gq": gq.ravel(), "gk": gk.ravel(), "gv": gv.ravel(), "gs": gs.ravel(),
+            "gp": gp.ravel(), "gc": gc.ravel(), "offsets": offs, "n_packed": n_packed}
+
+
+class AttentionCore:
+    """Causal multi-head attention on opened-nothing QKV shares [seq x 3d]:
+    per-head Beaver QK^T, scaled truncation into packed causal rows, the
+    softmax block, per-head Beaver PV, truncation into [seq x d]."""
+
+    def __init__(self, seq, d, heads, dealer, prg_state, frac_bits=12, device="cuda"):
+        self.seq, self.d, self.heads, self.f = seq, d, heads, frac_bits
+        self.dh = dh = d // heads
+        inv_sqrt = tables.llround((1.0 / math.sqrt(dh)) * math.ldexp(1.0, frac_bits))
+        self.inv_sqrt = max(inv_sqrt, 1)
+        mp = attention_maps(seq, d, heads)
+        self.offsets, self.n = mp["offsets"], mp["n_packed"]
+        self.maps = {k: dev_i32(mp[k], device) for k in ("gq", "gk", "gv", "gs", "gp", "gc")}
+        self.tri_qk = BatchedTriples(dealer, heads, seq, dh, seq, device)
+        self.tri_pv = BatchedTriples(dealer, heads, seq, seq, dh, device)
+        self.tr_s = Trunc(dealer, 2 * frac_bits, self.n, prg_state, device=device)
+        self.tr_c = Trunc(dealer, frac_bits, seq * d, prg_state, device=device)
+        self.softmax = SoftmaxBlock(self.offsets, prg_state, frac_bits, seed=dealer.word() >> 1,
+                                    device=device)
+        hsd = heads * seq * dh
+        self.D = torch.empty(hsd, dtype=torch.int64, device=device)
+        self.E = torch.empty(hsd, dtype=torch.int64, device=device)
+        self.D2 = torch.empty(heads * seq * seq, dtype=torch.int64, device=device)
+        self.S = pair(heads * seq * seq, device)
+        self.Z = pair(hsd, device)
+        self.scores = pair(self.n, device)
+        self.prob = pair(self.n + 1, device)  # slot n stays 0: the masked entries of P
+        for t in self.prob:
+            t[self.n:].zero_()
+        self.zs = torch.empty(self.n, dtype=torch.int64, device=device)
+        self.zc = torch.empty(seq * d, dtype=torch.int64, device=device)
+
+    def truncs(self):
+        return [self.tr_s, self.tr_c]
+
+    def eval2(self, qkv, out):
+        seq, d, h, dh, mp = self.seq, self.d, self.heads, self.dh, self.maps
+        # D = open(Q_h - A), E = open(K_h^T - B), then the per-head products.
+        lin2(operand(term(qkv, index=mp["gq"]), term(self.tri_qk.A, neg=True)), h * seq * dh,
+             xhat=self.D)
+        lin2(operand(term(qkv, index=mp["gk"]), term(self.tri_qk.B, neg=True)), h * seq * dh,
+             xhat=self.E)
+        _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S)
+        # Masked open of inv_sqrt * S at the packed causal positions, truncation by 2f.
+        lin2(operand(term(self.S, index=mp["gs"], mul=self.inv_sqrt)), self.n, xhat=self.zs,
+             mask=self.tr_s.mask)
+        self.tr_s.finish(self.zs, self.scores)
+        self.softmax.eval2(self.scores, self.prob)
+        lin2(operand(term(self.prob, index=mp["gp"]), term(self.tri_pv.A, neg=True)),
+             h * seq * seq, xhat=self.D2)
+        lin2(operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True)), h * seq * dh,
+             xhat=self.E)
+        _beaver_batched(self.D2, self.E, self.tri_pv, h, seq, seq, dh, self.Z)
+        lin2(operand(term(self.Z, index=mp["gc"])), seq * d, xhat=self.zc, mask=self.tr_c.mask)
+        self.tr_c.finish(self.zc, out)
+        return out
+
+
+def synthetic_weights(d=768, ffn=3072, frac_bits=12, seed=13):
+    """round(N(0, 0.02) 2^f) weights (Box-Muller on std::mt19937_64): Wqkv
+    from mt(seed), Wout mt(100 seed + 1), W1 mt(100 seed + 2), W2 mt(100 seed + 3)."""
+    from . import pfss
+
+    def w(s, k, n):
+        return pfss.host_normal_fixed(s, 0.02, 0.0, frac_bits, k * n).view(np.int64).reshape(k, n)
+
+    return {"Wqkv": w(seed, d, 3 * d), "Wout": w(100 * seed + 1, d, d),
+            "W1": w(100 * seed + 2, d, ffn), "W2": w(100 * seed + 3, ffn, d)}
+
+
+class TransformerLayer:
+    """One GPT-2-shaped layer over x [seq x d] Q(f) shares, both parties."""
+
+    def __init__(self, prg_state, weights, seq=128, d=768, heads=12, ffn=3072, frac_bits=12,
+                 seed=13, device="cuda"):
+        self.seq, self.d, self.heads, self.ffn, self.f = seq, d, heads, ffn, frac_bits
+        self.prg_state = bytes(prg_state)
+        dealer = Dealer(seed)
+        sub = lambda: dealer.word() >> 1  # noqa: E731
+        self.ln1 = LayerNormBlock(seq, d, self.prg_state, frac_bits, seed=sub(), device=device)
+        self.qkv = PublicMatmulTrunc(seq, d, 3 * d, weights["Wqkv"], dealer, self.prg_state,
+                                     frac_bits, device)
+        self.attn = AttentionCore(seq, d, heads, dealer, self.prg_state, frac_bits, device)
+        self.proj = PublicMatmulTrunc(seq, d, d, weights["Wout"], dealer, self.prg_state,
+                                      frac_bits, device)
+        self.ln2 = LayerNormBlock(seq, d, self.prg_state, frac_bits, seed=sub(), device=device)
+        self.w1 = PublicMatmulTrunc(seq, d, ffn, weights["W1"], dealer, self.prg_state,
+                                    frac_bits, device)
+        self.gelu_table = tables.gelu_table(frac_bits)
+        self.gelu = spline.SplineGate(seq * ffn, self.gelu_table[0], self.gelu_table[1],
+                                      self.prg_state, frac_bits, seed=sub(), nonce=dealer.word())
+        self.w2 = PublicMatmulTrunc(seq, ffn, d, weights["W2"], dealer, self.prg_state,
+                                    frac_bits, device)
+        self.side = torch.cuda.Stream(device=device)
+        n = seq * d
+        self.h1, self.qkvs, self.ctx, self.a = pair(n), pair(3 * n), pair(n), pair(n)
+        self.r1, self.h2, self.u, self.g, self.m = pair(n), pair(n), pair(seq * ffn), \
+            pair(seq * ffn), pair(n)
+
+    def truncs(self):
+        return (self.qkv.truncs() + self.attn.truncs() + self.proj.truncs() + self.w1.truncs()
+                + self.w2.truncs())
+
+    def eval2(self, x, out, marks=None):
+        """x, out: pairs of int64 [seq * d] device tensors.  marks: optional
+        list of torch events recorded after each stage (profiling)."""
+        start = torch.cuda.Event()
+        start.record()
+        self.side.wait_event(start)
+        for t in self.truncs():
+            t.prepare(self.side)
+        prepared = torch.cuda.Event()
+        prepared.record(self.side)
+
+        def mark():
+            if marks is not None:
+                ev = torch.cuda.Event(enable_timing=True)
+                ev.record()
+                marks.append(ev)
+
+        n = self.seq * self.d
+        mark()
+        self.ln1.eval2(x, self.h1)
+        mark()
+        torch.cuda.current_stream().wait_event(prepared)
+        self.qkv.eval2(self.h1, self.qkvs)
+        mark()
+        self.attn.eval2(self.qkvs, self.ctx)
+        mark()
+        self.proj.eval2(self.ctx, self.a)
+        lin2(operand(term(self.a), term(x)), n, out=self.r1)
+        mark()
+        self.ln2.eval2(self.r1, self.h2)
+        mark()
+        self.w1.eval2(self.h2, self.u)
+        mark()
+        self.gelu.eval2(self.u, self.g)
+        mark()
+        self.w2.eval2(self.g, self.m)
+        lin2(operand(term(self.m), term(self.r1)), n, out=out)
+        mark()
+        return out

@@ -75,6 +75,14 @@ _SIGS = {
     "sufhip_mul2": (c_int, [c_vp, c_sz, c_vp]),
     "sufhip_add_shifted": (c_int, [c_vp, c_vp, c_sz, c_sz, c_int, c_sz, c_vp, c_vp]),
     "sufhip_lin2": (c_int, [c_vp, c_sz, c_vp, c_vp, c_vp, c_u64, c_vp]),
+    "sufhip_beaver_matmul2_batched": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                              c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp]),
+    "sufhip_public_w_digits": (c_int, [c_vp, c_sz]),
+    "sufhip_public_w_planes_bytes": (c_sz, [c_int, c_int, c_int]),
+    "sufhip_public_w_prepare": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp]),
+    "sufhip_matmul_public2_work_bytes": (c_sz, [c_int, c_int, c_int]),
+    "sufhip_matmul_public2": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_vp,
+                                      c_vp, c_u64, c_vp, c_sz, c_vp]),
     "sufhip_mul2x": (c_int, [c_vp, c_sz, c_vp]),
     "sufhip_row_sum2": (c_int, [c_vp, c_int, c_int, c_vp, c_u64, c_vp, c_vp, c_vp, c_u64, c_vp]),
     "sufhip_relu_max_round2": (c_int, [c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_int,
@@ -133,7 +141,7 @@ class Mul2Args(ctypes.Structure):
 class Term2(ctypes.Structure):
     """sufhip_term2 (include/suf_hip.h)."""
     _fields_ = [("p", c_vp * 2), ("index", c_vp), ("len", c_sz), ("stride", c_sz),
-                ("off", c_sz), ("shift", c_int), ("negate", c_int)]
+                ("off", c_sz), ("shift", c_int), ("negate", c_int), ("mul", c_u64)]
 
 
 class Operand2(ctypes.Structure):

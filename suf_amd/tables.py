@@ -14,6 +14,8 @@ interval LUT of the gate carries.
                recip_piecewise_affine_init.hpp:11-66) through the same
                expansion (RecipTask reads words 0 and 1,
                include/runtime/phase_tasks.hpp:3314-3326): 2 words.
+  gelu_table   make_gelu_spline_spec (include/gates/tables/gelu_spline_table.hpp:
+               57-92) through build_silu_suf_from_piecewise: 4 words.
   rsqrt_table  make_rsqrt_affine_init_spec (include/gates/tables/
                rsqrt_piecewise_affine_init.hpp:11-83) through
                build_rsqrt_affine_eval_suf (src/nn/transformer_layer.cpp:
@@ -85,6 +87,86 @@ def _finish(pieces, words):
     for i, (_, _, cs) in enumerate(pieces):
         c[i, :len(cs[:words])] = cs[:words]
     return alpha, c
+
+
+def append_interval_signed(ivs, start_signed, end_signed, offset, coeffs):
+    """append_interval_signed (include/gates/piecewise_poly.hpp:254-269): a
+    signed [start, end) as u64 intervals, split at the wrap, the upper part
+    ending at the ~0 surrogate of 2^64."""
+    L, U = start_signed & M64, end_signed & M64
+
+    def push(a, b):
+        if a != b:
+            ivs.append((a, b, offset, list(coeffs)))
+
+    if L < U:
+        push(L, U)
+    else:
+        push(0, U)
+        push(L, M64)
+
+
+def suf_from_piecewise(ivs, frac_bits, words=4):
+    """build_silu_suf_from_piecewise (include/suf/suf_silu_builders.hpp:79-186):
+    intervals sorted by start, a zero piece before the first when it starts
+    above 0 and in every gap, overlaps trimmed, coefficients expanded to
+    x-form cubics.  Returns (alpha, coeffs[words])."""
+    pieces = []
+    cur = 0
+    seeded = False
+    zero = [0] * words
+    for start, end, off, cs in sorted(ivs, key=lambda t: t[0]):
+        if end <= start:
+            continue
+        if not seeded:
+            if start > 0:
+                pieces.append((0, 0, zero))
+            cur = start
+            seeded = True
+        if start < cur:
+            start = cur
+        if end <= start:
+            continue
+        if start > cur:
+            pieces.append((cur, 0, zero))
+            cur = start
+        pieces.append((start, off, expand_to_x_coeffs(off, cs, 3, frac_bits)))
+        cur = end
+    if not pieces:
+        pieces = [(0, 0, zero)]
+    return _finish(pieces, words)
+
+
+def _gelu(x):
+    return 0.5 * x * (1.0 + math.erf(x * 0.70710678118654752440))
+
+
+def _gelu_deriv(x):
+    phi = 0.39894228040143267794 * math.exp(-0.5 * x * x)
+    return 0.5 * (1.0 + math.erf(x * 0.70710678118654752440)) + x * phi
+
+
+def gelu_table(frac_bits=12, segments=16):
+    """make_gelu_spline_spec (include/gates/tables/gelu_spline_table.hpp:57-92):
+    0 below -8, Hermite cubics of x Phi(x) on `segments` pieces of [-8, 8),
+    y = x above 8; through build_silu_suf_from_piecewise: (alpha, coeffs[4])."""
+    lo, hi = -8.0, 8.0
+    step = (hi - lo) / segments
+    ivs = []
+    append_interval_signed(ivs, INT64_MIN, _enc(lo, frac_bits), 0, [0])
+    for i in range(segments):
+        start = lo + step * i
+        end = hi if i == segments - 1 else start + step
+        sf, ef = _enc(start, frac_bits), _enc(end, frac_bits)
+        h = end - start
+        y0, y1 = _gelu(start), _gelu(end)
+        m0, m1 = _gelu_deriv(start), _gelu_deriv(end)
+        c2 = (3.0 * (y1 - y0) - (2.0 * m0 + m1) * h) / (h * h)
+        c3 = (2.0 * (y0 - y1) + (m0 + m1) * h) / (h * h * h)
+        pack = [_enc(y0, frac_bits), _enc(m0, frac_bits), _enc(c2, frac_bits), _enc(c3, frac_bits)]
+        append_interval_signed(ivs, sf, ef, sf, pack)
+    append_interval_signed(ivs, _enc(hi, frac_bits), INT64_MAX, 0, [0, 1 << frac_bits])
+    return suf_from_piecewise(ivs, frac_bits, 4)
 
 
 def nexp_table(frac_bits=12, segments=16):

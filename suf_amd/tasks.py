@@ -64,7 +64,7 @@ class Dealer:
         return int(self.words(1)[0])
 
 
-def term(pair, index=None, stride=1, off=0, shift=0, neg=False, length=None):
+def term(pair, index=None, stride=1, off=0, shift=0, neg=False, length=None, mul=1):
     """sufhip_term2 over a pair of device tensors (party 0, party 1)."""
     t = native.Term2()
     if pair is None:
@@ -73,6 +73,7 @@ def term(pair, index=None, stride=1, off=0, shift=0, neg=False, length=None):
     t.index = index.data_ptr() if index is not None else None
     t.len = length if length is not None else pair[0].numel() // stride
     t.stride, t.off, t.shift, t.negate = stride, off, shift, 1 if neg else 0
+    t.mul = mul & M64
     return t
 
 

@@ -1,0 +1,168 @@
+"""GPT-2-shaped secure transformer layer for two parties on one GPU, and its
+new building blocks.
+
+  * public-weight GEMM (int8 digit MFMA): each party's share equals
+    X_p W mod 2^64 (numpy uint64 matmul wraps mod 2^64), the masked open
+    equals their sum plus the mask, over 1-3 weight digits and sliced /
+    unsliced grids;
+  * two-party batched Beaver matmul: each party's share equals the oracle's
+    beaver_matmul (orc_beaver_matmul) per batch, and reconstructs to X W;
+  * attention core and the whole layer: reconstruction equals the closed
+    form of oracle/fixed_point.py (small shapes and the config shape
+    128 x 768, 12 heads, FFN 3072).
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as ol
+from gpu_util import dev, say, u64
+from suf_amd import layer, native, pfss, tables
+from suf_amd.tasks import Dealer
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                "oracle"))
+import fixed_point as fp  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+STATE = ol.mt64_bytes(3, ol.PRG_STATE_BYTES).tobytes()
+F = 12
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    native.call("sufhip_init", 0)
+
+
+def _tabs():
+    return {"nexp": tables.nexp_table(F), "recip": tables.recip_table(F),
+            "rsqrt": tables.rsqrt_table(F), "gelu": tables.gelu_table(F)}
+
+
+def _pair(x, seed):
+    x = np.asarray(x).astype(np.uint64)
+    x0 = pfss.host_mt19937_64(seed, x.size)
+    return x0, (x - x0).astype(np.uint64)
+
+
+@pytest.mark.parametrize("M,K,N,wmax", [(32, 64, 96, 100), (64, 96, 64, 30000),
+                                        (128, 768, 2304, 400), (32, 32, 32, 1 << 20),
+                                        (128, 3072, 768, 500)])
+def test_public_matmul_shares(M, K, N, wmax):
+    rng = np.random.default_rng(M + K + N)
+    W = rng.integers(-wmax, wmax + 1, size=(K, N)).astype(np.int64)
+    W[0, 0], W[-1, -1] = wmax, -wmax
+    X0 = pfss.host_mt19937_64(M * 7 + 1, M * K).reshape(M, K)
+    X1 = pfss.host_mt19937_64(M * 7 + 2, M * K).reshape(M, K)
+    say("public matmul %dx%dx%d wmax=%d" % (M, K, N, wmax))
+    pm = layer.PublicMatmulTrunc(M, K, N, W, Dealer(3), STATE, F)
+    out = tuple(torch.empty(M * N, dtype=torch.int64, device="cuda") for _ in range(2))
+    zhat = torch.empty(M * N, dtype=torch.int64, device="cuda")
+    mask = 0x1234567890ABCDEF
+    xd = (dev(X0), dev(X1))
+    pm.product2(xd, out=out)
+    pm.product2(xd, zhat=zhat, mask=mask)
+    Wu = W.view(np.uint64)
+    want = [np.matmul(X0, Wu).ravel(), np.matmul(X1, Wu).ravel()]
+    assert np.array_equal(u64(out[0]), want[0]) and np.array_equal(u64(out[1]), want[1])
+    assert np.array_equal(u64(zhat), (want[0] + want[1] + np.uint64(mask)).astype(np.uint64))
+
+
+def test_public_matmul_trunc_reconstructs():
+    M, K, N = 64, 128, 96
+    X = pfss.host_normal_fixed(71, 1.0, 0.0, F, M * K)
+    W = pfss.host_normal_fixed(72, 0.05, 0.0, F, K * N).view(np.int64).reshape(K, N)
+    x0, x1 = _pair(X, 73)
+    say("public matmul + trunc %dx%dx%d" % (M, K, N))
+    pm = layer.PublicMatmulTrunc(M, K, N, W, Dealer(4), STATE, F)
+    pm.tr.prepare()
+    out = tuple(torch.empty(M * N, dtype=torch.int64, device="cuda") for _ in range(2))
+    pm.eval2((dev(x0), dev(x1)), out)
+    rec = (u64(out[0]) + u64(out[1])).astype(np.uint64)
+    want = fp.matmul_shift(X.view(np.int64).reshape(M, K), W, F).ravel().view(np.uint64)
+    assert np.array_equal(rec, want)
+
+
+def test_beaver_matmul2_batched_vs_oracle():
+    b, M, K, N = 3, 32, 64, 48
+    X = pfss.host_normal_fixed(81, 1.0, 0.0, F, b * M * K).reshape(b, M, K)
+    Y = pfss.host_normal_fixed(82, 1.0, 0.0, F, b * K * N).reshape(b, K, N)
+    say("beaver matmul2 batched b=%d %dx%dx%d" % (b, M, K, N))
+    tri = layer.BatchedTriples(Dealer(5), b, M, K, N)
+    A, B, C, A0, B0, C0 = tri.host
+    A1, B1, C1 = A - A0, B - B0, C - C0
+    x0 = pfss.host_mt19937_64(83, X.size).reshape(X.shape)
+    y0 = pfss.host_mt19937_64(84, Y.size).reshape(Y.shape)
+    D = ((x0 - A0) + (X - x0 - A1)).astype(np.uint64)
+    E = ((y0 - B0) + (Y - y0 - B1)).astype(np.uint64)
+    out = tuple(torch.empty(b * M * N, dtype=torch.int64, device="cuda") for _ in range(2))
+    layer._beaver_batched(dev(D), dev(E), tri, b, M, K, N, out)
+    g = [u64(out[0]).reshape(b, M, N), u64(out[1]).reshape(b, M, N)]
+    for i in range(b):
+        for p, (Ap, Bp, Cp) in enumerate(((A0, B0, C0), (A1, B1, C1))):
+            o = ol.beaver_matmul(p, D[i], E[i], Ap[i], Bp[i], Cp[i], 1, M, K, N)
+            assert np.array_equal(g[p][i].ravel(), np.asarray(o).ravel())
+    rec = (g[0] + g[1]).astype(np.uint64)
+    assert np.array_equal(rec, np.matmul(X, Y))
+
+
+def _layer_case(seq, d, heads, ffn, seed):
+    W = layer.synthetic_weights(d, ffn, F, seed)
+    x = pfss.host_normal_fixed(seed + 1, 1.0, 0.0, F, seq * d)
+    return W, x
+
+
+@pytest.mark.parametrize("seq,d,heads", [(32, 64, 2), (64, 128, 4)])
+def test_attention_core_reconstructs(seq, d, heads):
+    qkv = pfss.host_normal_fixed(90 + seq, 1.0, 0.0, F, seq * 3 * d)
+    q0, q1 = _pair(qkv, 91)
+    say("attention core seq=%d d=%d heads=%d" % (seq, d, heads))
+    at = layer.AttentionCore(seq, d, heads, Dealer(6), STATE, F)
+    for t in at.truncs():
+        t.prepare()
+    out = tuple(torch.empty(seq * d, dtype=torch.int64, device="cuda") for _ in range(2))
+    at.eval2((dev(q0), dev(q1)), out)
+    tabs = _tabs()
+    want, st = fp.attention(qkv, seq, d, heads, F, tabs["nexp"], tabs["recip"])
+    sc = (u64(at.scores[0]) + u64(at.scores[1])).astype(np.uint64)
+    assert np.array_equal(sc, st["scores"].view(np.uint64))
+    rec = (u64(out[0]) + u64(out[1])).astype(np.uint64)
+    assert np.array_equal(rec, want.view(np.uint64))
+
+
+def test_layer_small_reconstructs():
+    seq, d, heads, ffn = 32, 64, 2, 128
+    W, x = _layer_case(seq, d, heads, ffn, 21)
+    x0, x1 = _pair(x, 22)
+    say("transformer layer small seq=%d d=%d heads=%d ffn=%d" % (seq, d, heads, ffn))
+    ly = layer.TransformerLayer(STATE, W, seq, d, heads, ffn, F, seed=23)
+    out = tuple(torch.empty(seq * d, dtype=torch.int64, device="cuda") for _ in range(2))
+    ly.eval2((dev(x0), dev(x1)), out)
+    want, st = fp.transformer_layer(x, W, seq, d, heads, ffn, F, _tabs(),
+                                    tables.inv_len_qf(d), tables.eps_qf())
+    for name, t in (("h1", ly.h1), ("qkv", ly.qkvs), ("ctx", ly.ctx), ("r1", ly.r1),
+                    ("h2", ly.h2), ("u", ly.u), ("g", ly.g)):
+        rec = (u64(t[0]) + u64(t[1])).astype(np.uint64)
+        assert np.array_equal(rec, st[name].view(np.uint64).ravel()), name
+    rec = (u64(out[0]) + u64(out[1])).astype(np.uint64)
+    assert np.array_equal(rec, want.view(np.uint64))
+
+
+def test_layer_config_shape_twice():
+    seq, d, heads, ffn = 128, 768, 12, 3072
+    W, x = _layer_case(seq, d, heads, ffn, 13)
+    x0, x1 = _pair(x, 141)
+    say("transformer layer config shape")
+    ly = layer.TransformerLayer(STATE, W, seq, d, heads, ffn, F, seed=13)
+    want, _ = fp.transformer_layer(x, W, seq, d, heads, ffn, F, _tabs(),
+                                   tables.inv_len_qf(d), tables.eps_qf())
+    xin = (dev(x0), dev(x1))
+    out = tuple(torch.empty(seq * d, dtype=torch.int64, device="cuda") for _ in range(2))
+    for _ in range(2):
+        ly.eval2(xin, out)
+        rec = (u64(out[0]) + u64(out[1])).astype(np.uint64)
+        assert np.array_equal(rec, want.view(np.uint64))

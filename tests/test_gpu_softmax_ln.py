@@ -123,15 +123,6 @@ def test_rsqrt_shares_and_closed_form():
     assert np.array_equal((g[0] + g[1]).astype(np.uint64), want)
 
 
-def _softmax_oracle(sm, x0, x1):
-    """Shares of every stage of SoftmaxBlock on the CPU oracle."""
-    prg = ol.Prg(STATE)
-    offs = sm.offsets
-    row = fp.row_of(offs)
-    delta = tp.relu_rounds2(sm.rowmax, [x0, x1])
-    return delta, row, prg
-
-
 @pytest.mark.parametrize("heads,seq", [(1, 8), (2, 33)])
 def test_softmax_block_small(heads, seq):
     offs = softmax.causal_offsets(heads, seq)
@@ -147,15 +138,10 @@ def test_softmax_block_small(heads, seq):
     assert np.array_equal(_recon(sm.e), st["exp"].view(np.uint64))
     assert np.array_equal(_recon(sm.s), st["sum"].view(np.uint64))
     assert np.array_equal(_recon(out), prob.view(np.uint64))
-    # Share level for the stages after the nExp gate (its own chain is
-    # checked share-for-share in test_gpu_spline.py).
-    prg = ol.Prg(STATE)
-    e = [u64(sm.e[0]), u64(sm.e[1])]
-    s = [u64(sm.s[0]), u64(sm.s[1])]
-    assert np.array_equal(s[0], ol.row_sum_ragged(e[0], offs.astype(np.int32)))
-    inv = tp.recip2(prg, sm.recip, s, u64(sm.shat))
-    row = fp.row_of(offs)
-    o = tp.beaver_trunc2(prg, e, inv, sm.tri, sm.tr, row_of=row)
+    # Share level: the whole chain on the oracle.
+    o, st2 = tp.softmax2(ol.Prg(STATE), sm, [x0, x1])
+    for k, dv in (("delta", sm.delta), ("exp", sm.e), ("sum", sm.s)):
+        assert np.array_equal(u64(dv[0]), st2[k][0]) and np.array_equal(u64(dv[1]), st2[k][1])
     g = [u64(out[0]), u64(out[1])]
     assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
 
@@ -190,18 +176,7 @@ def test_layernorm_small_shares():
     assert np.array_equal(_recon(ln.var), st["var"].view(np.uint64))
     assert np.array_equal(_recon(out), y.view(np.uint64))
     # Share level: the whole chain on the oracle.
-    prg = ol.Prg(STATE)
-    row = np.repeat(np.arange(rows), cols)
-    xs = [x0, x1]
-    sums = [ol.row_sum(xs[p], rows, cols) * np.uint64(ln.inv_len) for p in (0, 1)]
-    mu = tp.trunc2(prg, ln.tr_mean, tp.open2(sums, ln.tr_mean.mask))
-    diff = [(xs[p] - mu[p][row]).astype(np.uint64) for p in (0, 1)]
-    sq = tp.beaver2(diff, diff, ln.tri_sq)
-    vs = [ol.row_sum(sq[p], rows, cols) * np.uint64(ln.inv_len) for p in (0, 1)]
-    var = tp.trunc2(prg, ln.tr_var, tp.open2(vs, ln.tr_var.mask))
-    v = tp.const2(var, ln.eps_q)
-    rs = tp.rsqrt2(prg, ln.rsqrt, v, tp.open2(v, ln.rsqrt.lut.mask))
-    o = tp.beaver_trunc2(prg, diff, rs, ln.tri_norm, ln.tr_norm, row_of=row)
+    o = tp.layernorm2(ol.Prg(STATE), ln, [x0, x1])
     g = [u64(out[0]), u64(out[1])]
     assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
 

@@ -8,6 +8,7 @@ import pytest
 import torch
 
 import oracle_lib as ol
+import twoparty_oracle as tp
 from gpu_util import dev, host, say, u64
 from suf_amd import native, pfss, spline
 
@@ -29,31 +30,7 @@ def _shares(x, seed):
 
 def _oracle_pipeline(gate, x0, x1):
     """Both parties' outputs, step by step on the CPU oracle."""
-    prg = ol.Prg(STATE)
-    n = x0.size
-    rin = sum(gate.rin) & spline.M64
-    xhat = (x0 + x1 + np.uint64(rin)).astype(np.uint64)
-    C = [ol.lut_eval(host(gate.lut[p]), gate.lut_key_bytes, 1, xhat, 4).reshape(n, 4)
-         for p in (0, 1)]
-    tri = [[u64(t).reshape(n, 3) for t in pair] for pair in gate.triples]
-
-    def mul(u, v, t):
-        d = (u[0] - t[0][:, 0]) + (u[1] - t[1][:, 0])
-        e = (v[0] - t[0][:, 1]) + (v[1] - t[1][:, 1])
-        return [ol.beaver_mul(p, t[p][:, 0], t[p][:, 1], t[p][:, 2], d, e) for p in (0, 1)]
-
-    sh = np.uint64(F)
-    u = mul([C[0][:, 3], C[1][:, 3]], [x0, x1], tri[0])
-    u = [u[p] + (C[p][:, 2] << sh) for p in (0, 1)]
-    pz = mul(u, [x0, x1], tri[1])
-    t1, t2 = gate.trunc
-    phat = (pz[0] + pz[1] + np.uint64(sum(t1["rin"]) & spline.M64)).astype(np.uint64)
-    y = [ol.trunc_eval(prg, ol.TRUNC_GAPARS, t1["f"], host(t1["keys"][p]), phat) for p in (0, 1)]
-    q = [y[p] + (C[p][:, 1] << sh) for p in (0, 1)]
-    rz = mul(q, [x0, x1], tri[2])
-    rhat = (rz[0] + rz[1] + np.uint64(sum(t2["rin"]) & spline.M64)).astype(np.uint64)
-    y2 = [ol.trunc_eval(prg, ol.TRUNC_GAPARS, t2["f"], host(t2["keys"][p]), rhat) for p in (0, 1)]
-    return [(y2[p] + C[p][:, 0]).astype(np.uint64) for p in (0, 1)]
+    return tp.spline2(ol.Prg(STATE), gate, [x0, x1])
 
 
 @pytest.mark.parametrize("n,seed", [(3000, 7), (777, 8)])

@@ -113,3 +113,67 @@ def relu_rounds2(rm, x):
         cur = nxt
     mi = host(rm.max_index).astype(np.int64)
     return [(cur[p][mi] - u(x[p])).astype(np.uint64) for p in (0, 1)]
+
+
+def spline2(prg, gate, x, idx0=0, sl=None):
+    """spline.SplineGate (CubicPolyTask) on shares x = (x0, x1): both
+    parties' outputs.  sl: a slice of the gate's batch (x holds that slice;
+    idx0 = its first element index, the LUT keystream counter uses it)."""
+    x0, x1 = u(x[0]), u(x[1])
+    n = x0.size
+    sl = sl if sl is not None else slice(0, n)
+    f = gate.f
+    rin = sum(gate.rin) & M64
+    xhat = (x0 + x1 + np.uint64(rin)).astype(np.uint64)
+    lut = [host(gate.lut[p]) for p in (0, 1)]
+    C = [ol.lut_eval(lut[p], gate.lut_key_bytes, 1, xhat, 4, idx0=idx0).reshape(n, 4)
+         for p in (0, 1)]
+    tri = [[host(t).view(np.uint64).reshape(-1, 3)[sl] for t in pr] for pr in gate.triples]
+
+    def mul(a, b, t):
+        d = (a[0] - t[0][:, 0]) + (a[1] - t[1][:, 0])
+        e = (b[0] - t[0][:, 1]) + (b[1] - t[1][:, 1])
+        return [ol.beaver_mul(p, t[p][:, 0], t[p][:, 1], t[p][:, 2], d, e) for p in (0, 1)]
+
+    sh = np.uint64(f)
+    m1 = mul([C[0][:, 3], C[1][:, 3]], [x0, x1], tri[0])
+    m1 = [m1[p] + (C[p][:, 2] << sh) for p in (0, 1)]
+    pz = mul(m1, [x0, x1], tri[1])
+    t1, t2 = gate.trunc
+    phat = (pz[0] + pz[1] + np.uint64(sum(t1["rin"]) & M64)).astype(np.uint64)
+    y = [ol.trunc_eval(prg, ol.TRUNC_GAPARS, t1["f"], host(t1["keys"][p]), phat) for p in (0, 1)]
+    q = [y[p] + (C[p][:, 1] << sh) for p in (0, 1)]
+    rz = mul(q, [x0, x1], tri[2])
+    rhat = (rz[0] + rz[1] + np.uint64(sum(t2["rin"]) & M64)).astype(np.uint64)
+    y2 = [ol.trunc_eval(prg, ol.TRUNC_GAPARS, t2["f"], host(t2["keys"][p]), rhat) for p in (0, 1)]
+    return [(y2[p] + C[p][:, 0]).astype(np.uint64) for p in (0, 1)]
+
+
+def softmax2(prg, sm, x):
+    """softmax.SoftmaxBlock on shares x: (prob shares, stage shares)."""
+    offs = sm.offsets
+    row = np.repeat(np.arange(len(offs) - 1), np.diff(offs))
+    delta = relu_rounds2(sm.rowmax, x)
+    e = spline2(prg, sm.nexp, delta)
+    s = [ol.row_sum_ragged(e[p], offs.astype(np.int32)) for p in (0, 1)]
+    inv = recip2(prg, sm.recip, s, open2(s, sm.recip.lut.mask))
+    prob = beaver_trunc2(prg, e, inv, sm.tri, sm.tr, row_of=row)
+    return prob, {"delta": delta, "exp": e, "sum": s, "inv": inv}
+
+
+def layernorm2(prg, ln, x):
+    """layernorm.LayerNormBlock on shares x: output shares."""
+    rows, cols = ln.rows, ln.cols
+    row = np.repeat(np.arange(rows), cols)
+    xs = [u(x[0]), u(x[1])]
+    sums = [(ol.row_sum(xs[p], rows, cols) * np.uint64(ln.inv_len)).astype(np.uint64)
+            for p in (0, 1)]
+    mu = trunc2(prg, ln.tr_mean, open2(sums, ln.tr_mean.mask))
+    diff = [(xs[p] - mu[p][row]).astype(np.uint64) for p in (0, 1)]
+    sq = beaver2(diff, diff, ln.tri_sq)
+    vs = [(ol.row_sum(sq[p], rows, cols) * np.uint64(ln.inv_len)).astype(np.uint64)
+          for p in (0, 1)]
+    var = trunc2(prg, ln.tr_var, open2(vs, ln.tr_var.mask))
+    v = const2(var, ln.eps_q)
+    rs = rsqrt2(prg, ln.rsqrt, v, open2(v, ln.rsqrt.lut.mask))
+    return beaver_trunc2(prg, diff, rs, ln.tri_norm, ln.tr_norm, row_of=row)
