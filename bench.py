@@ -116,9 +116,9 @@ def cpu_spline_baseline(gate, state, x0, x1, gpu_out, seconds):
     f = gate.f
     lut = [gate.lut[p].cpu().numpy() for p in (0, 1)]
     tri = [[t.cpu().numpy().view(np.uint64).reshape(-1, 3) for t in pair] for pair in gate.triples]
-    tk = [[k.cpu().numpy() for k in t["keys"]] for t in gate.trunc]
+    tk = [[k.cpu().numpy() for k in t.keys] for t in gate.trunc]
     rin = sum(gate.rin) & ((1 << 64) - 1)
-    t_rin = [sum(t["rin"]) & ((1 << 64) - 1) for t in gate.trunc]
+    t_rin = [t.mask for t in gate.trunc]
     sh = np.uint64(f)
     chunk, done, mism = 1024, 0, 0
     t0 = time.perf_counter()
@@ -338,6 +338,80 @@ def cpu_softmax_ln_baseline(state, sm, ln, sx, lx, sc, xl, sout, lout, f):
                              "mismatches": mism}}
 
 
+def bench_layer(steps, warmup, frac_bits=12, cpu=True):
+    """One GPT-2-small-shaped secure layer (hidden 768, 12 heads, seq 128, FFN
+    3072, GeLU) for both parties: weights round(N(0,0.02) 2^12) (mt(13) and
+    derived seeds), input x = round(N(0,1) 2^12) (mt(14)) shared with mt(141);
+    dealer material from suf_amd.tasks.Dealer(13).  Times the whole layer as
+    one HIP graph replay (and eagerly, with a per-stage breakdown)."""
+    import numpy as np
+    import torch
+
+    from suf_amd import layer, pfss, tasks
+
+    seq, d, heads, ffn = 128, 768, 12, 3072
+    state = bytes((pfss.host_mt19937_64(3, 128) & np.uint64(0xFF)).astype(np.uint8))
+    W = layer.synthetic_weights(d, ffn, frac_bits, 13)
+    x = pfss.host_normal_fixed(14, 1.0, 0.0, frac_bits, seq * d)
+    x0 = pfss.host_mt19937_64(141, seq * d)
+    dev = lambda v: torch.from_numpy(np.ascontiguousarray(v).view(np.int64).copy()).cuda()
+    xin = (dev(x0), dev((x - x0).astype(np.uint64)))
+    ly = layer.TransformerLayer(state, W, seq, d, heads, ffn, frac_bits, seed=13)
+    out = tuple(torch.empty(seq * d, dtype=torch.int64, device="cuda") for _ in range(2))
+    for _ in range(warmup):
+        ly.eval2(xin, out)
+    torch.cuda.synchronize()
+    stages = ["ln1", "qkv", "attention", "out_proj+residual", "ln2", "w1", "gelu",
+              "w2+residual"]
+    marks_all = []
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        m = []
+        ly.eval2(xin, out, marks=m)
+        marks_all.append(m)
+    e1.record()
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / steps
+    per_stage = {stages[i]: float(np.mean([m[i].elapsed_time(m[i + 1]) for m in marks_all]))
+                 for i in range(len(stages))}
+    eager_out = [out[0].cpu().numpy().copy(), out[1].cpu().numpy().copy()]
+    g = tasks.capture(lambda: ly.eval2(xin, out))
+    torch.cuda.synchronize()
+    replay_ok = True
+    for _ in range(2):  # replays agree with the eager result
+        g.replay()
+        torch.cuda.synchronize()
+        replay_ok = replay_ok and all(np.array_equal(out[p].cpu().numpy(), eager_out[p])
+                                      for p in (0, 1))
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    graph_ms = e0.elapsed_time(e1) / steps
+    res = {"ms": graph_ms, "eager_ms": eager_ms, "stages_eager_ms": per_stage,
+           "shape": {"seq": seq, "hidden": d, "heads": heads, "ffn": ffn}, "frac_bits": frac_bits,
+           "ring": "Z_2^64", "steps": steps, "graph_replays_match_eager": replay_ok,
+           "check": "not run (--no-cpu)" if replay_ok else "MISMATCH"}
+    if cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import fixed_point as fp
+        from suf_amd import tables
+
+        tabs = {"nexp": tables.nexp_table(frac_bits), "recip": tables.recip_table(frac_bits),
+                "rsqrt": tables.rsqrt_table(frac_bits), "gelu": tables.gelu_table(frac_bits)}
+        t0 = time.perf_counter()
+        want, _ = fp.transformer_layer(x, W, seq, d, heads, ffn, frac_bits, tabs,
+                                       tables.inv_len_qf(d), tables.eps_qf())
+        dt = time.perf_counter() - t0
+        rec = (eager_out[0].view(np.uint64) + eager_out[1].view(np.uint64)).astype(np.uint64)
+        ok = replay_ok and bool(np.array_equal(rec, want.view(np.uint64)))
+        res["check"] = "ok" if ok else "MISMATCH"
+        res["closed_form_cpu_ms"] = dt * 1e3
+    return res
+
+
 def cpu_baseline(keys0, keys1, xhat, gpu_bits0, gpu_bits1, seconds):
     """The reference's own myl7 batch evaluation (oracle/_ref, built from the
     reference sources), single thread as in Myl7FssBackend::eval_dcf_many_u64
@@ -522,9 +596,12 @@ def main():
         line["spline_gate"] = bench_spline(max(a.steps // 2, 1), 2, cpu_seconds=gate_cpu)
         line["beaver_matmul_trunc"] = bench_matmul(max(a.steps // 2, 1), 2, cpu_seconds=gate_cpu)
         line["softmax_layernorm"] = bench_softmax_ln(max(a.steps // 2, 1), 2, cpu=not a.no_cpu)
+        line["secure_layer"] = bench_layer(max(a.steps // 2, 1), 2, cpu=not a.no_cpu)
+        line["secure_layer_ms"] = line["secure_layer"]["ms"]
         ok = ok and line["spline_gate"]["check"] == "ok"
         ok = ok and line["beaver_matmul_trunc"]["check"] == "ok"
         ok = ok and line["softmax_layernorm"]["check"] in ("ok", "not run (--no-cpu)")
+        ok = ok and line["secure_layer"]["check"] in ("ok", "not run (--no-cpu)")
     if not a.no_cpu:
         sample = 1 << 14
         g0 = out0[:sample].cpu().numpy()

@@ -186,6 +186,46 @@ int sufhip_trunc_finish(int kind, int frac_bits, const uint8_t* prg_state, const
                         size_t key_bytes, const uint64_t* d_xhat, size_t n, uint64_t* d_y,
                         const void* d_work, size_t work_bytes, void* stream);
 
+/* Both parties' finish in one launch (keys d_key0 / d_key1 of the same gate,
+ * each with the workspace its prepare filled); the same shares as two
+ * sufhip_trunc_finish calls. */
+int sufhip_trunc_finish2(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key0,
+                         const uint8_t* d_key1, size_t key_bytes, const uint64_t* d_xhat, size_t n,
+                         uint64_t* d_y0, uint64_t* d_y1, const void* d_work0,
+                         const void* d_work1, size_t work_bytes, void* stream);
+
+/* The key-only halves of many gates (any kinds, widths and batch sizes) in
+ * one walk launch plus one launch per level expanded beyond depth 12; each
+ * job's workspace ends as sufhip_trunc_prepare would leave it.  For
+ * frac_bits <= 14 the workspace holds the full-domain table of the carry
+ * share, so the finish is one table read per element. */
+typedef struct sufhip_trunc_job {
+  int kind;
+  int frac_bits;
+  const uint8_t* d_key;
+  size_t key_bytes;
+  size_t n;
+  void* d_work;
+  size_t work_bytes;
+} sufhip_trunc_job;
+int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int count,
+                               void* stream);
+
+/* A truncation folded into the launch that produces its masked open: for a
+ * GapARS gate with frac_bits <= 14 whose keys were prepared (full-domain
+ * tables), y[p][i] receives party p's truncated share at the open value
+ * instead of the open being written.  key / table: both parties' key blobs
+ * (8-byte aligned) and prepared workspaces (16-byte aligned) of
+ * work_bytes >= sufhip_trunc_work_bytes(frac_bits, n) each.  A key that is
+ * not a GapARS key for frac_bits yields zeros. */
+typedef struct sufhip_trunc_epilogue {
+  const uint8_t* key[2];
+  const void* table[2];
+  size_t work_bytes;
+  int frac_bits;
+  uint64_t* y[2];
+} sufhip_trunc_epilogue;
+
 /* ---------------------------------------------------------------------- */
 /* Two-party steps with both parties on one GPU (SUF's local channel: an    */
 /* open is an exchange of masked shares and an add).  Each call does both   */
@@ -270,9 +310,12 @@ typedef struct sufhip_operand2 {
 
 /* Evaluates an operand for both parties: d_out0 / d_out1 (either may be NULL)
  * receive the shares, and d_xhat (may be NULL) the masked open
- * xhat[i] = x_0 + x_1 + mask of a gate input (mask = r_0 + r_1). */
+ * xhat[i] = x_0 + x_1 + mask of a gate input (mask = r_0 + r_1).  With
+ * `trunc` (may be NULL) the open feeds that truncation gate, whose outputs
+ * are written instead of d_xhat. */
 int sufhip_lin2(const sufhip_operand2* x, size_t n, uint64_t* d_out0, uint64_t* d_out1,
-                uint64_t* d_xhat, uint64_t mask, void* stream);
+                uint64_t* d_xhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,
+                void* stream);
 
 /* Beaver product for both parties with general operands (MulTask and
  * MulRowBroadcastTask, phase_tasks.hpp:198-402, 1810-2185; beaver_mul_kernel
@@ -283,7 +326,8 @@ int sufhip_lin2(const sufhip_operand2* x, size_t n, uint64_t* d_out0, uint64_t* 
  * gives the row-broadcast triple of MulRowBroadcastTask, whose e is then one
  * value per row).  z_add's terms may be absent.  zhat == NULL: z[p][i] = z_p;
  * otherwise only zhat[i] = z_0 + z_1 + open_mask is written (the masked open
- * of the product for the next truncation gate). */
+ * of the product for the next truncation gate); with `trunc` that gate's
+ * outputs are written instead. */
 typedef struct sufhip_mul2x_args {
   sufhip_operand2 u;
   sufhip_operand2 v;
@@ -294,6 +338,7 @@ typedef struct sufhip_mul2x_args {
   uint64_t* z[2];
   uint64_t* zhat;
   uint64_t open_mask;
+  const sufhip_trunc_epilogue* trunc; /* the open feeds this gate (replaces zhat) */
 } sufhip_mul2x_args;
 int sufhip_mul2x(const sufhip_mul2x_args* args, size_t n, void* stream);
 
@@ -304,10 +349,11 @@ int sufhip_mul2x(const sufhip_mul2x_args* args, size_t n, void* stream);
  * Row r covers elements [d_row_offsets[r], d_row_offsets[r+1]) when
  * d_row_offsets (int32 [rows + 1], non-decreasing) is given, else
  * [r * cols, (r + 1) * cols).  d_sum0 / d_sum1 / d_hat may each be NULL;
- * d_hat[r] = s_0[r] + s_1[r] + mask (masked open of the scaled sum). */
+ * d_hat[r] = s_0[r] + s_1[r] + mask (masked open of the scaled sum); with
+ * `trunc` the truncation gate's outputs are written instead of d_hat. */
 int sufhip_row_sum2(const sufhip_operand2* x, int rows, int cols, const int32_t* d_row_offsets,
                     uint64_t mul_const, uint64_t* d_sum0, uint64_t* d_sum1, uint64_t* d_hat,
-                    uint64_t mask, void* stream);
+                    uint64_t mask, const sufhip_trunc_epilogue* trunc, void* stream);
 
 /* One pairwise-max round of RowMaxDiffTask (include/nn/row_maxdiff_task.hpp:
  * 49-150), max(a, b) = b + ReLU(a - b), for both parties.  For output slot j:
@@ -464,7 +510,8 @@ int sufhip_beaver_matmul2_batched(const uint64_t* d_D_open, const uint64_t* d_E_
  * sufhip_matmul_public2: M, K, N multiples of 32, digits in 1..4 with
  * digits * K < 2^17 (exact int32 accumulation); writes the shares
  * (d_out0 and d_out1) and/or the masked open d_zhat = Y_0 + Y_1 + mask that
- * the following truncation gate consumes.  d_work: 16-byte aligned, of
+ * the following truncation gate consumes (with `trunc`: that gate's outputs
+ * instead of d_zhat).  d_work: 16-byte aligned, of
  * sufhip_matmul_public2_work_bytes(M, K, N) bytes (0 for a bad shape). */
 int sufhip_public_w_digits(const int64_t* w, size_t n);
 size_t sufhip_public_w_planes_bytes(int K, int N, int digits);
@@ -473,8 +520,8 @@ int sufhip_public_w_prepare(const int64_t* d_W, int K, int N, int digits, int8_t
 size_t sufhip_matmul_public2_work_bytes(int M, int K, int N);
 int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int K, int N,
                           const int8_t* d_planes, int digits, uint64_t* d_out0, uint64_t* d_out1,
-                          uint64_t* d_zhat, uint64_t mask, void* d_work, size_t work_bytes,
-                          void* stream);
+                          uint64_t* d_zhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,
+                          void* d_work, size_t work_bytes, void* stream);
 
 /* launch_row_mean_kernel (:169-174): sum >> log2(L) for power-of-two L, else
  * the u64 sum divided by L as a plain integer (the reference's formula). */

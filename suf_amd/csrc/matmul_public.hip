@@ -25,6 +25,7 @@
 
 #include "suf_hip.h"
 #include "sufhip_internal.hpp"
+#include "trunc_device.hpp"
 
 namespace sufhip {
 namespace {
@@ -106,6 +107,7 @@ struct PubArgs {
   uint64_t* zhat;    // masked open (or NULL)
   uint64_t mask;
   uint64_t* part;    // [slices][2][M][N] when gridDim.z > 1
+  TruncEpi epi;      // the open feeds this truncation gate (replaces zhat)
 };
 
 // One wave per 32 x 32 tile and k-slice; grid = (N / 32, M / 32, slices).
@@ -169,11 +171,11 @@ __global__ void __launch_bounds__(64) public_mfma_kernel(PubArgs a) {
       tot[r] += v;
     }
   }
-  if (gridDim.z == 1 && a.zhat) {
+  if (gridDim.z == 1 && (a.zhat || a.epi.on)) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-      a.zhat[size_t(row) * N + col] = tot[r] + a.mask;
+      put_open(a.epi, a.zhat, size_t(row) * N + col, tot[r] + a.mask);
     }
   }
 }
@@ -181,7 +183,7 @@ __global__ void __launch_bounds__(64) public_mfma_kernel(PubArgs a) {
 // Slices -> shares and/or the masked open.
 __global__ void __launch_bounds__(256)
     public_reduce_kernel(const uint64_t* part, int slices, size_t mn, uint64_t* out0,
-                         uint64_t* out1, uint64_t* zhat, uint64_t mask) {
+                         uint64_t* out1, uint64_t* zhat, uint64_t mask, TruncEpi epi) {
   for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < mn; i += size_t(gridDim.x) * 256) {
     uint64_t v0 = 0, v1 = 0;
     for (int z = 0; z < slices; ++z) {
@@ -190,7 +192,7 @@ __global__ void __launch_bounds__(256)
     }
     if (out0) out0[i] = v0;
     if (out1) out1[i] = v1;
-    if (zhat) zhat[i] = v0 + v1 + mask;
+    put_open(epi, zhat, i, v0 + v1 + mask);
   }
 }
 
@@ -261,8 +263,8 @@ size_t sufhip_matmul_public2_work_bytes(int M, int K, int N) {
 
 int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int K, int N,
                           const int8_t* d_planes, int digits, uint64_t* d_out0, uint64_t* d_out1,
-                          uint64_t* d_zhat, uint64_t mask, void* d_work, size_t work_bytes,
-                          void* stream) {
+                          uint64_t* d_zhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,
+                          void* d_work, size_t work_bytes, void* stream) {
   SUFHIP_REQUIRE(shape_ok(M, K, N),
                  "sufhip_matmul_public2: needs M, K, N multiples of 32 and K < 65536");
   SUFHIP_REQUIRE(digits >= 1 && digits <= 4 && size_t(digits) * K < (size_t(1) << 17),
@@ -270,7 +272,9 @@ int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int
   SUFHIP_REQUIRE(d_X0 && d_X1 && d_planes && d_work, "sufhip_matmul_public2: null pointer");
   SUFHIP_REQUIRE((d_out0 == nullptr) == (d_out1 == nullptr),
                  "sufhip_matmul_public2: give both share outputs or neither");
-  SUFHIP_REQUIRE(d_out0 || d_zhat, "sufhip_matmul_public2: no output");
+  SUFHIP_REQUIRE(d_out0 || d_zhat || trunc, "sufhip_matmul_public2: no output");
+  TruncEpi epi;
+  if (int rc = make_epi(trunc, size_t(M) * N, "sufhip_matmul_public2", &epi)) return rc;
   SUFHIP_REQUIRE(work_bytes >= sufhip_matmul_public2_work_bytes(M, K, N),
                  "sufhip_matmul_public2: workspace too small");
   SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_work) & 15) == 0 &&
@@ -285,7 +289,7 @@ int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int
   if (int rc = check_launch("split_x2_kernel")) return rc;
   const int sl = pub_slices(M, K, N);
   uint64_t* part = reinterpret_cast<uint64_t*>(Lp + size_t(kPlanes) * 2 * M * K);
-  PubArgs a{Lp, d_planes, M, K, N, {d_out0, d_out1}, d_zhat, mask, part};
+  PubArgs a{Lp, d_planes, M, K, N, {d_out0, d_out1}, d_zhat, mask, part, epi};
   const dim3 grid(N / 32, M / 32, sl);
   switch (digits) {
     case 1: hipLaunchKernelGGL(public_mfma_kernel<1>, grid, dim3(64), 0, s, a); break;
@@ -299,7 +303,7 @@ int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int
   size_t g = (mn + 255) / 256;
   if (g > 4096) g = 4096;
   hipLaunchKernelGGL(public_reduce_kernel, dim3(unsigned(g)), dim3(256), 0, s, part, sl, mn,
-                     d_out0, d_out1, d_zhat, mask);
+                     d_out0, d_out1, d_zhat, mask, epi);
   return check_launch("public_reduce_kernel");
 }
 

@@ -1,0 +1,136 @@
+// Device-side pieces of the truncation gate shared by the gate's own kernels
+// (trunc_gate.hip) and the two-party kernels whose masked open feeds a
+// truncation (twoparty.hip, matmul_public.hip): the key header, the
+// postproc formulas (trunc_postproc_kernel, cuda/cuda_primitives.cu:179-252;
+// include/gates/postproc_hooks.hpp:172-373) and the GapARS evaluation from a
+// prepared full-domain carry table.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "suf_hip.h"
+#include "sufhip_internal.hpp"
+
+namespace sufhip {
+
+constexpr uint32_t kTruncTag = 0x31475453u;  // "STG1"
+constexpr int kTruncHdrBytes = 64;
+// Carry keys up to this many bits are prepared as full-domain tables (one
+// read per element at evaluation).
+constexpr int kTruncTableBits = 14;
+
+struct TruncHdr {
+  uint32_t tag, kind, f, party, flags;
+  uint64_t r_hi, base, cw, sw, m;
+  uint32_t ckb, ukb;
+};
+
+// Header word 0: tag | kind << 32 | f << 40 | party << 48 | flags << 56.
+__device__ __forceinline__ TruncHdr read_trunc_hdr(const uint8_t* key) {
+  const uint64_t* w = reinterpret_cast<const uint64_t*>(key);
+  const uint64_t h0 = w[0];
+  TruncHdr h;
+  h.tag = uint32_t(h0);
+  h.kind = uint32_t(h0 >> 32) & 0xffu;
+  h.f = uint32_t(h0 >> 40) & 0xffu;
+  h.party = uint32_t(h0 >> 48) & 1u;
+  h.flags = uint32_t(h0 >> 56);
+  h.r_hi = w[2];
+  h.base = w[3];
+  h.cw = w[4];
+  h.sw = w[5];
+  h.m = w[6];
+  h.ckb = uint32_t(w[7]);
+  h.ukb = uint32_t(w[7] >> 32);
+  return h;
+}
+
+template <int kKind>
+__device__ __forceinline__ uint64_t trunc_postproc(const TruncHdr& h, int f, uint64_t x,
+                                                   uint64_t carry, uint64_t wrap, uint64_t sign) {
+  if constexpr (kKind == SUFHIP_TRUNC_GAPARS) {
+    const uint64_t hb = x + (uint64_t(1) << 62);
+    uint64_t y = h.base + (h.party == 0 ? hb >> f : 0) - h.r_hi - carry;
+    if ((hb >> 63) == 0) y += h.m;
+    if (h.party == 0) y -= uint64_t(1) << (62 - f);
+    return y;
+  } else {
+    uint64_t y = h.base + (h.party == 0 ? x >> f : 0) - h.r_hi - carry +
+                 wrap * (uint64_t(1) << (64 - f));
+    if constexpr (kKind == SUFHIP_TRUNC_ARS) y += sign * (~uint64_t(0) << (64 - f));
+    return y;
+  }
+}
+
+// carry share = NOT(RotXor(a, 0, w)) = [p0] - w + a.
+__device__ __forceinline__ uint64_t trunc_carry_from(const TruncHdr& h, uint64_t a) {
+  return (h.party == 0 ? 1 : 0) - h.cw + a;
+}
+
+// One party's GapARS output at the public xhat from the key and its prepared
+// full-domain table (node v's value word holds the carry DCF's share at v).
+// A key that is not a GapARS key for f bits yields 0; the table read stays
+// inside its 2^f nodes either way.
+__device__ __forceinline__ uint64_t trunc_table_eval(const uint8_t* key, const uint4* table,
+                                                     int f, uint64_t xhat) {
+  const TruncHdr h = read_trunc_hdr(key);
+  if (h.tag != kTruncTag || h.kind != SUFHIP_TRUNC_GAPARS || int(h.f) != f) return 0;
+  uint64_t carry = 0;
+  if (h.flags & 1) {
+    const uint4 q = table[2 * (xhat & ((uint64_t(1) << f) - 1)) + 1];
+    carry = trunc_carry_from(h, uint64_t(q.x) | uint64_t(q.y) << 32);
+  }
+  return trunc_postproc<SUFHIP_TRUNC_GAPARS>(h, f, xhat, carry, 0, 0);
+}
+
+// A truncation gate folded into the launch that produces its masked open.
+struct TruncEpi {
+  const uint8_t* key[2];
+  const uint4* table[2];
+  uint64_t* y[2];
+  int f;
+  int on;
+};
+
+// Writes the open value v of element i: the gate's two output shares when
+// the epilogue is on, else the open itself (if requested).
+__device__ __forceinline__ void put_open(const TruncEpi& e, uint64_t* hat, size_t i, uint64_t v) {
+  if (e.on) {
+    e.y[0][i] = trunc_table_eval(e.key[0], e.table[0], e.f, v);
+    e.y[1][i] = trunc_table_eval(e.key[1], e.table[1], e.f, v);
+  } else if (hat) {
+    hat[i] = v;
+  }
+}
+
+// Validates an epilogue for n elements and converts it (NULL -> off).
+inline int make_epi(const sufhip_trunc_epilogue* t, size_t n, const char* what, TruncEpi* out) {
+  *out = TruncEpi{{nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}, 0, 0};
+  if (!t) return SUFHIP_OK;
+  const bool ok = t->frac_bits >= 1 && t->frac_bits <= kTruncTableBits && t->key[0] &&
+                  t->key[1] && t->table[0] && t->table[1] && t->y[0] && t->y[1] &&
+                  (reinterpret_cast<uintptr_t>(t->key[0]) & 7) == 0 &&
+                  (reinterpret_cast<uintptr_t>(t->key[1]) & 7) == 0 &&
+                  (reinterpret_cast<uintptr_t>(t->table[0]) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(t->table[1]) & 15) == 0;
+  if (!ok) {
+    set_error(std::string(what) + ": truncation epilogue needs frac_bits in [1, 14], both keys, "
+              "tables and outputs, aligned");
+    return SUFHIP_ERR_INVALID;
+  }
+  if (t->work_bytes < sufhip_trunc_work_bytes(t->frac_bits, n > 0 ? n : 1)) {
+    set_error(std::string(what) + ": truncation epilogue table smaller than its work bytes");
+    return SUFHIP_ERR_INVALID;
+  }
+  *out = TruncEpi{{t->key[0], t->key[1]},
+                  {static_cast<const uint4*>(t->table[0]), static_cast<const uint4*>(t->table[1])},
+                  {t->y[0], t->y[1]},
+                  t->frac_bits,
+                  1};
+  return SUFHIP_OK;
+}
+
+}  // namespace sufhip

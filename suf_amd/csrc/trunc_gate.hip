@@ -18,23 +18,29 @@
 // broadcast key and a large batch the 2^d frontier states are computed once
 // and every element continues from its prefix.  The first k0 = min(d, 12)
 // levels are walked one node per lane; deeper levels are expanded
-// breadth-first, one child per lane (2 AES per node).  d = min(f,
-// floor(log2 N) - 1, 22) balances the 2^(d+1) expansions against the N (f - d)
-// per-element levels.  With d = f the frontier holds the final share of every
-// point of the domain and an element's carry is a single table read.  The
-// results are the same bytes a full walk produces.
+// breadth-first, one child per lane (2 AES per node).  For f <= 14, d = f:
+// the frontier holds the final share of every point of the domain and an
+// element's carry is a single table read (the key-only work, 2^f walks, is
+// off the critical path: it needs no input).  Above, d = min(f, max(floor(
+// log2 N) - 1, 12), 22) balances the 2^(d+1) expansions against the N (f - d)
+// per-element levels, never leaving more than f - 12 levels per element.  The
+// results are the same bytes a full walk produces.  sufhip_trunc_prepare_batch
+// runs the key-only halves of many gates in one walk launch plus one launch
+// per expanded level; sufhip_trunc_finish2 evaluates both parties' keys in
+// one launch.
 #include <hip/hip_runtime.h>
 
 #include <string>
 
 #include "dcf_device.hpp"
 #include "suf_hip.h"
+#include "trunc_device.hpp"
 
 namespace sufhip {
 namespace {
 
-constexpr uint32_t kTag = 0x31475453u;  // "STG1"
-constexpr int kHdrBytes = 64;
+constexpr uint32_t kTag = kTruncTag;
+constexpr int kHdrBytes = kTruncHdrBytes;
 constexpr int kMaxFrontierBits = 22;
 constexpr int kWalkFrontierBits = 12;
 
@@ -43,11 +49,13 @@ __host__ __device__ constexpr size_t pad8(size_t v) { return (v + 7) & ~size_t(7
 size_t dcf_bytes(int in_bits) { return sufhip_dcf_key_bytes(in_bits, 8); }
 
 int frontier_bits(int f, size_t n) {
+  if (n == 0) return 0;
+  if (f <= kTruncTableBits) return f;
   int lg = 0;
   while (lg < 63 && (size_t(1) << (lg + 1)) <= n) ++lg;
-  if (lg < 5) return 0;
-  int d = f < kMaxFrontierBits ? f : kMaxFrontierBits;
-  return d < lg - 1 ? d : lg - 1;
+  int d = lg - 1 > kWalkFrontierBits ? lg - 1 : kWalkFrontierBits;
+  if (d > kMaxFrontierBits) d = kMaxFrontierBits;
+  return d < f ? d : f;
 }
 
 // Nodes of the walked level (k0) and of the final level (d) in the workspace:
@@ -159,59 +167,30 @@ __global__ void __launch_bounds__(kDcfBlock) trunc_expand_kernel(ExpandArgs a) {
   }
 }
 
+// One launch evaluates one or both parties: grid.y selects the party slot.
 struct TruncEvalArgs {
   Prg4 prg;
-  const uint8_t* key;
+  const uint8_t* keys[2];
   const uint64_t* xhat;
-  uint64_t* y;
-  const uint4* nodes;
+  uint64_t* ys[2];
+  const uint4* tables[2];
   size_t n;
   int f;
   int d;
 };
 
-struct Hdr {
-  uint32_t party, flags;
-  uint64_t r_hi, base, cw, sw, m;
-  uint32_t ckb, ukb;
-};
+using Hdr = TruncHdr;
 
-__device__ __forceinline__ Hdr read_hdr(const uint8_t* key) {
-  const uint64_t* w = reinterpret_cast<const uint64_t*>(key);
-  const uint64_t h0 = w[0];
-  Hdr h;
-  h.party = uint32_t(h0 >> 48) & 1u;
-  h.flags = uint32_t(h0 >> 56);
-  h.r_hi = w[2];
-  h.base = w[3];
-  h.cw = w[4];
-  h.sw = w[5];
-  h.m = w[6];
-  h.ckb = uint32_t(w[7]);
-  h.ukb = uint32_t(w[7] >> 32);
-  return h;
-}
+__device__ __forceinline__ Hdr read_hdr(const uint8_t* key) { return read_trunc_hdr(key); }
 
 template <int kKind>
 __device__ __forceinline__ uint64_t postproc(const Hdr& h, int f, uint64_t x, uint64_t carry,
                                              uint64_t wrap, uint64_t sign) {
-  if constexpr (kKind == SUFHIP_TRUNC_GAPARS) {
-    const uint64_t hb = x + (uint64_t(1) << 62);
-    uint64_t y = h.base + (h.party == 0 ? hb >> f : 0) - h.r_hi - carry;
-    if ((hb >> 63) == 0) y += h.m;
-    if (h.party == 0) y -= uint64_t(1) << (62 - f);
-    return y;
-  } else {
-    uint64_t y = h.base + (h.party == 0 ? x >> f : 0) - h.r_hi - carry +
-                 wrap * (uint64_t(1) << (64 - f));
-    if constexpr (kKind == SUFHIP_TRUNC_ARS) y += sign * (~uint64_t(0) << (64 - f));
-    return y;
-  }
+  return trunc_postproc<kKind>(h, f, x, carry, wrap, sign);
 }
 
-// carry share = NOT(RotXor(a, 0, w)) = [p0] - w + a.
 __device__ __forceinline__ uint64_t carry_from(const Hdr& h, uint64_t a) {
-  return (h.party == 0 ? 1 : 0) - h.cw + a;
+  return trunc_carry_from(h, a);
 }
 
 // Every DCF walk the element needs runs here (frontier continuation, 64-bit
@@ -219,9 +198,12 @@ __device__ __forceinline__ uint64_t carry_from(const Hdr& h, uint64_t a) {
 template <int kKind>
 __global__ void __launch_bounds__(kDcfBlock) trunc_eval_aes_kernel(TruncEvalArgs a) {
   SUFHIP_DCF_LDS_SETUP(a.prg);
-  const Hdr h = read_hdr(a.key);
-  const uint8_t* carry_chunk = a.key + kHdrBytes + 8;
-  const uint8_t* wrap_chunk = a.key + kHdrBytes + pad8(h.ckb) + 8;
+  const uint8_t* key = a.keys[blockIdx.y];
+  const uint4* nodes = a.tables[blockIdx.y];
+  uint64_t* y = a.ys[blockIdx.y];
+  const Hdr h = read_hdr(key);
+  const uint8_t* carry_chunk = key + kHdrBytes + 8;
+  const uint8_t* wrap_chunk = key + kHdrBytes + pad8(h.ckb) + 8;
   const uint8_t* sign_chunk = wrap_chunk + pad8(h.ukb);
   const uint64_t low = (uint64_t(1) << a.f) - 1;
   const size_t stride = size_t(gridDim.x) * kDcfBlock;
@@ -232,13 +214,13 @@ __global__ void __launch_bounds__(kDcfBlock) trunc_eval_aes_kernel(TruncEvalArgs
       const uint64_t xl = x & low;
       uint64_t share;
       if (a.d == a.f) {
-        const uint4 q = a.nodes[2 * xl + 1];
+        const uint4 q = nodes[2 * xl + 1];
         share = uint64_t(q.x) | uint64_t(q.y) << 32;
       } else {
         Add64State st;
         if (a.d > 0) {
           const size_t v = size_t(xl >> (a.f - a.d));
-          const uint4 s = a.nodes[2 * v], q = a.nodes[2 * v + 1];
+          const uint4 s = nodes[2 * v], q = nodes[2 * v + 1];
           st = Add64State{s.x, s.y, s.z, s.w, q.z, uint64_t(q.x) | uint64_t(q.y) << 32};
         } else {
           st = add64_root(carry_chunk, h.party);
@@ -258,37 +240,115 @@ __global__ void __launch_bounds__(kDcfBlock) trunc_eval_aes_kernel(TruncEvalArgs
       add64_walk(aes, rkl, sign_chunk, 64, 0, 64, x, h.party, st);
       sign = (wrap - add64_finish(sign_chunk, 64, h.party, st)) + h.sw;
     }
-    a.y[e] = postproc<kKind>(h, a.f, x, carry, wrap, sign);
+    y[e] = postproc<kKind>(h, a.f, x, carry, wrap, sign);
   }
 }
 
 // GapARS with the full-domain table (or no carry key): one table read per
 // element, HBM-bound.
 __global__ void __launch_bounds__(256) trunc_eval_table_kernel(TruncEvalArgs a) {
-  const Hdr h = read_hdr(a.key);
+  const uint8_t* key = a.keys[blockIdx.y];
+  const uint4* nodes = a.tables[blockIdx.y];
+  uint64_t* y = a.ys[blockIdx.y];
+  const Hdr h = read_hdr(key);
   const uint64_t low = (uint64_t(1) << a.f) - 1;
   const size_t stride = size_t(gridDim.x) * 256;
   for (size_t e = size_t(blockIdx.x) * 256 + threadIdx.x; e < a.n; e += stride) {
     const uint64_t x = a.xhat[e];
     uint64_t carry = 0;
     if (h.flags & 1) {
-      const uint4 q = a.nodes[2 * (x & low) + 1];
+      const uint4 q = nodes[2 * (x & low) + 1];
       carry = carry_from(h, uint64_t(q.x) | uint64_t(q.y) << 32);
     }
-    a.y[e] = postproc<SUFHIP_TRUNC_GAPARS>(h, a.f, x, carry, 0, 0);
+    y[e] = postproc<SUFHIP_TRUNC_GAPARS>(h, a.f, x, carry, 0, 0);
+  }
+}
+
+// Key-only halves of several gates at once: the walk to depth min(d, 12) of
+// every job in one launch (lanes [begin[j], begin[j+1]) belong to job j),
+// then per level one launch expanding every job that goes deeper.
+constexpr int kBatchJobs = 24;
+
+struct BatchLevelArgs {
+  Prg4 prg;
+  int count;
+  int level;  // expansion: the common input depth; walk: unused
+  uint32_t begin[kBatchJobs + 1];
+  const uint8_t* key[kBatchJobs];
+  const uint4* in[kBatchJobs];
+  uint4* out[kBatchJobs];
+  int f[kBatchJobs];
+  int d[kBatchJobs];  // walk: depth walked
+};
+
+__device__ __forceinline__ int batch_job(const BatchLevelArgs& a, uint32_t g) {
+  int j = 0;
+  while (j + 1 < a.count && g >= a.begin[j + 1]) ++j;
+  return j;
+}
+
+__global__ void __launch_bounds__(kDcfBlock) trunc_batch_walk_kernel(BatchLevelArgs a) {
+  SUFHIP_DCF_LDS_SETUP(a.prg);
+  const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= a.begin[a.count]) return;
+  const int j = batch_job(a, g);
+  const uint8_t* key = a.key[j];
+  const uint32_t v = g - a.begin[j];
+  if (!(key[7] & 1)) return;
+  const uint32_t party = key[6] & 1u;
+  const uint8_t* chunk = key + kHdrBytes + 8;
+  const int f = a.f[j], d = a.d[j];
+  const uint64_t x = uint64_t(v) << (f - d);
+  Add64State st = add64_root(chunk, party);
+  add64_walk(aes, rkl, chunk, f, 0, d, x, party, st);
+  uint4* nodes = a.out[j];
+  if (d == f) {
+    const uint64_t out = add64_finish(chunk, f, party, st);
+    nodes[2 * v + 1] = make_uint4(uint32_t(out), uint32_t(out >> 32), 0, 0);
+  } else {
+    nodes[2 * v] = make_uint4(st.s0, st.s1, st.s2, st.s3);
+    nodes[2 * v + 1] = make_uint4(uint32_t(st.v), uint32_t(st.v >> 32), st.t, 0);
+  }
+}
+
+__global__ void __launch_bounds__(kDcfBlock) trunc_batch_expand_kernel(BatchLevelArgs a) {
+  SUFHIP_DCF_LDS_SETUP(a.prg);
+  const uint32_t total = a.begin[a.count];
+  for (uint32_t g = blockIdx.x * blockDim.x + threadIdx.x; g < total;
+       g += gridDim.x * blockDim.x) {
+    const int j = batch_job(a, g);
+    const uint8_t* key = a.key[j];
+    if (!(key[7] & 1)) continue;
+    const uint32_t party = key[6] & 1u;
+    const uint8_t* chunk = key + kHdrBytes + 8;
+    const int f = a.f[j], level = a.level;
+    const uint32_t c = g - a.begin[j];
+    const uint4 s = a.in[j][2 * (c >> 1)], q = a.in[j][2 * (c >> 1) + 1];
+    Add64State st{s.x, s.y, s.z, s.w, q.z, uint64_t(q.x) | uint64_t(q.y) << 32};
+    const uint64_t x = uint64_t(c & 1u) << (f - 1 - level);
+    add64_walk(aes, rkl, chunk, f, level, level + 1, x, party, st);
+    if (level + 1 == f) {
+      const uint64_t out = add64_finish(chunk, f, party, st);
+      a.out[j][2 * c + 1] = make_uint4(uint32_t(out), uint32_t(out >> 32), 0, 0);
+    } else {
+      a.out[j][2 * c] = make_uint4(st.s0, st.s1, st.s2, st.s3);
+      a.out[j][2 * c + 1] = make_uint4(uint32_t(st.v), uint32_t(st.v >> 32), st.t, 0);
+    }
   }
 }
 
 // Launch shape for the frontier kernels: spread `count` lanes over all CUs
-// (one workgroup per CU, the AES tables fill its LDS), 64..512 lanes each.
+// (one workgroup per CU, the AES tables fill its LDS), 256..512 lanes each.
 int spread_grid(size_t count, unsigned int* grid, unsigned int* block) {
   int dev = 0, cus = 0;
   SUFHIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
   SUFHIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
                "hipDeviceGetAttribute(CU count)");
+  // At least 256 lanes per workgroup: every lane helps fill the LDS tables,
+  // which dominates small launches.
   size_t per = (count + size_t(cus) - 1) / size_t(cus);
   per = (per + 63) / 64 * 64;
-  const size_t b = per < 64 ? 64 : (per > size_t(kDcfBlock) ? size_t(kDcfBlock) : per);
+  const size_t b = per < 256 ? 256 : (per > size_t(kDcfBlock) ? size_t(kDcfBlock) : per);
   const size_t g = (count + b - 1) / b;
   *block = unsigned(b);
   *grid = unsigned(g < size_t(cus) ? g : size_t(cus));
@@ -300,6 +360,29 @@ bool valid_kind(int kind) {
 }
 
 constexpr size_t kMaxElems = size_t(1) << 38;
+
+// Finish for `parties` (1 or 2) key slots: the table kernel for GapARS with
+// a full-domain table, else the DCF-walk kernel.
+int launch_finish(int kind, const TruncEvalArgs& a, int parties, hipStream_t s) {
+  if (kind == SUFHIP_TRUNC_GAPARS && a.d == a.f) {
+    size_t blocks = (a.n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(trunc_eval_table_kernel, dim3(unsigned(blocks), parties), dim3(256), 0, s,
+                       a);
+    return check_launch("trunc_eval_table_kernel");
+  }
+  unsigned int g = 0;
+  if (int rc = dcf_grid(a.n, &g)) return rc;
+  const dim3 grid(g, parties);
+  if (kind == SUFHIP_TRUNC_GAPARS)
+    hipLaunchKernelGGL(trunc_eval_aes_kernel<SUFHIP_TRUNC_GAPARS>, grid, dim3(kDcfBlock), 0, s,
+                       a);
+  else if (kind == SUFHIP_TRUNC_TR)
+    hipLaunchKernelGGL(trunc_eval_aes_kernel<SUFHIP_TRUNC_TR>, grid, dim3(kDcfBlock), 0, s, a);
+  else
+    hipLaunchKernelGGL(trunc_eval_aes_kernel<SUFHIP_TRUNC_ARS>, grid, dim3(kDcfBlock), 0, s, a);
+  return check_launch("trunc_eval_aes_kernel");
+}
 
 }  // namespace
 }  // namespace sufhip
@@ -438,24 +521,103 @@ int sufhip_trunc_finish(int kind, int frac_bits, const uint8_t* prg_state, const
   hipStream_t s = as_stream(stream);
   Prg4 prg;
   fill_prg4(prg_state, &prg);
-  TruncEvalArgs a{prg, d_key, d_xhat, d_y, static_cast<const uint4*>(d_work), n, frac_bits, d};
-  if (kind == SUFHIP_TRUNC_GAPARS && d == frac_bits) {
-    size_t blocks = (n + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(trunc_eval_table_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, a);
-    return check_launch("trunc_eval_table_kernel");
+  const uint4* tab = static_cast<const uint4*>(d_work);
+  TruncEvalArgs a{prg, {d_key, d_key}, d_xhat, {d_y, d_y}, {tab, tab}, n, frac_bits, d};
+  return launch_finish(kind, a, 1, s);
+}
+
+int sufhip_trunc_finish2(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key0,
+                         const uint8_t* d_key1, size_t key_bytes, const uint64_t* d_xhat, size_t n,
+                         uint64_t* d_y0, uint64_t* d_y1, const void* d_work0,
+                         const void* d_work1, size_t work_bytes, void* stream) {
+  if (int rc = trunc_check("sufhip_trunc_finish2", kind, frac_bits, prg_state, d_key0, key_bytes,
+                           n, d_work0, work_bytes))
+    return rc;
+  if (int rc = trunc_check("sufhip_trunc_finish2", kind, frac_bits, prg_state, d_key1, key_bytes,
+                           n, d_work1, work_bytes))
+    return rc;
+  if (n == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(d_xhat && d_y0 && d_y1, "sufhip_trunc_finish2: null pointer");
+  Prg4 prg;
+  fill_prg4(prg_state, &prg);
+  TruncEvalArgs a{prg,
+                  {d_key0, d_key1},
+                  d_xhat,
+                  {d_y0, d_y1},
+                  {static_cast<const uint4*>(d_work0), static_cast<const uint4*>(d_work1)},
+                  n,
+                  frac_bits,
+                  frontier_bits(frac_bits, n)};
+  return launch_finish(kind, a, 2, as_stream(stream));
+}
+
+int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int count,
+                               void* stream) {
+  SUFHIP_REQUIRE(count >= 0 && (count == 0 || jobs), "sufhip_trunc_prepare_batch: bad jobs");
+  SUFHIP_REQUIRE(prg_state, "sufhip_trunc_prepare_batch: null prg_state");
+  hipStream_t s = as_stream(stream);
+  Prg4 prg;
+  fill_prg4(prg_state, &prg);
+  for (int base = 0; base < count; base += kBatchJobs) {
+    const int m = count - base < kBatchJobs ? count - base : kBatchJobs;
+    // Per job: its depth d, walked depth k0 and the two workspace regions,
+    // alternated so that depth d ends in the first (as sufhip_trunc_prepare).
+    int d[kBatchJobs], cur[kBatchJobs];
+    uint4* lvl[kBatchJobs][2];
+    int maxd = 0;
+    for (int i = 0; i < m; ++i) {
+      const sufhip_trunc_job& jb = jobs[base + i];
+      if (int rc = trunc_check("sufhip_trunc_prepare_batch", jb.kind, jb.frac_bits, prg_state,
+                               jb.d_key, jb.key_bytes, jb.n, jb.d_work, jb.work_bytes))
+        return rc;
+      d[i] = frontier_bits(jb.frac_bits, jb.n);
+      const int k0 = walk_bits(d[i]);
+      lvl[i][0] = static_cast<uint4*>(jb.d_work);
+      lvl[i][1] = d[i] > 0 ? lvl[i][0] + 2 * (size_t(1) << d[i]) : nullptr;
+      cur[i] = (d[i] - k0) & 1;
+      if (d[i] > maxd) maxd = d[i];
+    }
+    BatchLevelArgs wa{};
+    wa.prg = prg;
+    wa.begin[0] = 0;
+    for (int i = 0; i < m; ++i) {
+      const sufhip_trunc_job& jb = jobs[base + i];
+      const int k0 = walk_bits(d[i]);
+      wa.key[wa.count] = jb.d_key;
+      wa.out[wa.count] = lvl[i][cur[i]];
+      wa.f[wa.count] = jb.frac_bits;
+      wa.d[wa.count] = k0;
+      wa.begin[wa.count + 1] = wa.begin[wa.count] + (d[i] > 0 ? (1u << k0) : 0u);
+      ++wa.count;
+    }
+    if (wa.begin[wa.count] > 0) {
+      const unsigned b = kDcfBlock;
+      const unsigned g = (wa.begin[wa.count] + b - 1) / b;
+      hipLaunchKernelGGL(trunc_batch_walk_kernel, dim3(g), dim3(b), 0, s, wa);
+      if (int rc = check_launch("trunc_batch_walk_kernel")) return rc;
+    }
+    for (int level = kWalkFrontierBits; level < maxd; ++level) {
+      BatchLevelArgs ea{};
+      ea.prg = prg;
+      ea.level = level;
+      ea.begin[0] = 0;
+      for (int i = 0; i < m; ++i) {
+        if (d[i] <= level) continue;
+        ea.key[ea.count] = jobs[base + i].d_key;
+        ea.in[ea.count] = lvl[i][cur[i]];
+        ea.out[ea.count] = lvl[i][cur[i] ^ 1];
+        ea.f[ea.count] = jobs[base + i].frac_bits;
+        ea.begin[ea.count + 1] = ea.begin[ea.count] + (2u << level);
+        ++ea.count;
+        cur[i] ^= 1;
+      }
+      unsigned int eg = 0, eb = 0;
+      if (int rc = spread_grid(ea.begin[ea.count], &eg, &eb)) return rc;
+      hipLaunchKernelGGL(trunc_batch_expand_kernel, dim3(eg), dim3(eb), 0, s, ea);
+      if (int rc = check_launch("trunc_batch_expand_kernel")) return rc;
+    }
   }
-  unsigned int g = 0;
-  if (int rc = dcf_grid(n, &g)) return rc;
-  if (kind == SUFHIP_TRUNC_GAPARS)
-    hipLaunchKernelGGL(trunc_eval_aes_kernel<SUFHIP_TRUNC_GAPARS>, dim3(g), dim3(kDcfBlock), 0,
-                       s, a);
-  else if (kind == SUFHIP_TRUNC_TR)
-    hipLaunchKernelGGL(trunc_eval_aes_kernel<SUFHIP_TRUNC_TR>, dim3(g), dim3(kDcfBlock), 0, s, a);
-  else
-    hipLaunchKernelGGL(trunc_eval_aes_kernel<SUFHIP_TRUNC_ARS>, dim3(g), dim3(kDcfBlock), 0, s,
-                       a);
-  return check_launch("trunc_eval_aes_kernel");
+  return SUFHIP_OK;
 }
 
 int sufhip_trunc_eval(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,

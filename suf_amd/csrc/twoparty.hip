@@ -31,6 +31,7 @@
 
 #include "suf_hip.h"
 #include "sufhip_internal.hpp"
+#include "trunc_device.hpp"
 
 namespace sufhip {
 namespace {
@@ -126,19 +127,19 @@ __device__ __forceinline__ uint64_t operand_at(const sufhip_operand2& o, int p, 
 
 __global__ void __launch_bounds__(kBlock)
     lin2_kernel(sufhip_operand2 x, size_t n, uint64_t* out0, uint64_t* out1, uint64_t* xhat,
-                uint64_t mask) {
+                uint64_t mask, TruncEpi epi) {
   const size_t stride = size_t(gridDim.x) * kBlock;
   for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
     const uint64_t x0 = operand_at(x, 0, i), x1 = operand_at(x, 1, i);
     if (out0) out0[i] = x0;
     if (out1) out1[i] = x1;
-    if (xhat) xhat[i] = x0 + x1 + mask;
+    put_open(epi, xhat, i, x0 + x1 + mask);
   }
 }
 
-__global__ void __launch_bounds__(kBlock) mul2x_kernel(sufhip_mul2x_args a, size_t n) {
+__global__ void __launch_bounds__(kBlock) mul2x_kernel(sufhip_mul2x_args a, size_t n, TruncEpi epi) {
   const size_t stride = size_t(gridDim.x) * kBlock;
-  const bool open = a.zhat != nullptr;
+  const bool open = a.zhat != nullptr || epi.on;
   for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
     const uint64_t u0 = operand_at(a.u, 0, i), u1 = operand_at(a.u, 1, i);
     const uint64_t v0 = operand_at(a.v, 0, i), v1 = operand_at(a.v, 1, i);
@@ -151,7 +152,7 @@ __global__ void __launch_bounds__(kBlock) mul2x_kernel(sufhip_mul2x_args a, size
     const uint64_t z0 = c0 + d * b0 + e * a0 + d * e + operand_at(a.z_add, 0, i);
     const uint64_t z1 = c1 + d * b1 + e * a1 + operand_at(a.z_add, 1, i);
     if (open) {
-      a.zhat[i] = z0 + z1 + a.open_mask;
+      put_open(epi, a.zhat, i, z0 + z1 + a.open_mask);
     } else {
       a.z[0][i] = z0;
       a.z[1][i] = z1;
@@ -173,7 +174,7 @@ __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 __global__ void __launch_bounds__(kBlock)
     row_sum2_kernel(sufhip_operand2 x, int rows, int cols, const int32_t* offs,
                     uint64_t mul_const, uint64_t* sum0, uint64_t* sum1, uint64_t* hat,
-                    uint64_t mask) {
+                    uint64_t mask, TruncEpi epi) {
   const int lane = threadIdx.x & 63;
   for (int r = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6); r < rows;
        r += gridDim.x * (kBlock / 64)) {
@@ -189,7 +190,7 @@ __global__ void __launch_bounds__(kBlock)
     if (lane == 0) {
       if (sum0) sum0[r] = s0;
       if (sum1) sum1[r] = s1;
-      if (hat) hat[r] = s0 + s1 + mask;
+      put_open(epi, hat, size_t(r), s0 + s1 + mask);
     }
   }
 }
@@ -285,14 +286,17 @@ int sufhip_add_shifted(const uint64_t* d_y, const uint64_t* d_add, size_t add_st
 }
 
 int sufhip_lin2(const sufhip_operand2* x, size_t n, uint64_t* d_out0, uint64_t* d_out1,
-                uint64_t* d_xhat, uint64_t mask, void* stream) {
+                uint64_t* d_xhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,
+                void* stream) {
   SUFHIP_REQUIRE(x != nullptr, "sufhip_lin2: null operand");
   if (n == 0) return SUFHIP_OK;
   SUFHIP_REQUIRE(n < kMaxElems, "sufhip_lin2: n too large");
-  SUFHIP_REQUIRE(d_out0 || d_out1 || d_xhat, "sufhip_lin2: no output");
+  SUFHIP_REQUIRE(d_out0 || d_out1 || d_xhat || trunc, "sufhip_lin2: no output");
   if (int rc = check_operand(*x, n, "sufhip_lin2")) return rc;
+  TruncEpi epi;
+  if (int rc = make_epi(trunc, n, "sufhip_lin2", &epi)) return rc;
   hipLaunchKernelGGL(lin2_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream), *x, n,
-                     d_out0, d_out1, d_xhat, mask);
+                     d_out0, d_out1, d_xhat, mask, epi);
   return check_launch("lin2_kernel");
 }
 
@@ -308,19 +312,24 @@ int sufhip_mul2x(const sufhip_mul2x_args* args, size_t n, void* stream) {
   if (int rc = check_term(a.a, n, false, "sufhip_mul2x a")) return rc;
   if (int rc = check_term(a.b, n, false, "sufhip_mul2x b")) return rc;
   if (int rc = check_term(a.c, n, false, "sufhip_mul2x c")) return rc;
-  SUFHIP_REQUIRE(a.zhat != nullptr || (a.z[0] && a.z[1]),
-                 "sufhip_mul2x: need zhat (open) or both z outputs");
-  hipLaunchKernelGGL(mul2x_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream), a, n);
+  SUFHIP_REQUIRE(a.zhat != nullptr || a.trunc != nullptr || (a.z[0] && a.z[1]),
+                 "sufhip_mul2x: need zhat (open), a truncation epilogue or both z outputs");
+  TruncEpi epi;
+  if (int rc = make_epi(a.trunc, n, "sufhip_mul2x", &epi)) return rc;
+  hipLaunchKernelGGL(mul2x_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream), a, n,
+                     epi);
   return check_launch("mul2x_kernel");
 }
 
 int sufhip_row_sum2(const sufhip_operand2* x, int rows, int cols, const int32_t* d_row_offsets,
                     uint64_t mul_const, uint64_t* d_sum0, uint64_t* d_sum1, uint64_t* d_hat,
-                    uint64_t mask, void* stream) {
+                    uint64_t mask, const sufhip_trunc_epilogue* trunc, void* stream) {
   SUFHIP_REQUIRE(x != nullptr, "sufhip_row_sum2: null operand");
   SUFHIP_REQUIRE(rows >= 0 && (d_row_offsets || cols >= 0), "sufhip_row_sum2: bad shape");
   if (rows == 0) return SUFHIP_OK;
-  SUFHIP_REQUIRE(d_sum0 || d_sum1 || d_hat, "sufhip_row_sum2: no output");
+  SUFHIP_REQUIRE(d_sum0 || d_sum1 || d_hat || trunc, "sufhip_row_sum2: no output");
+  TruncEpi epi;
+  if (int rc = make_epi(trunc, size_t(rows), "sufhip_row_sum2", &epi)) return rc;
   // Without offsets every element index is < rows * cols; with offsets the
   // caller's offsets bound them (indexed terms clamp on the device).
   const size_t n = d_row_offsets ? 0 : size_t(rows) * size_t(cols);
@@ -328,7 +337,7 @@ int sufhip_row_sum2(const sufhip_operand2* x, int rows, int cols, const int32_t*
   size_t g = (size_t(rows) + kBlock / 64 - 1) / (kBlock / 64);
   if (g > 8192) g = 8192;
   hipLaunchKernelGGL(row_sum2_kernel, dim3(unsigned(g)), dim3(kBlock), 0, as_stream(stream), *x,
-                     rows, cols, d_row_offsets, mul_const, d_sum0, d_sum1, d_hat, mask);
+                     rows, cols, d_row_offsets, mul_const, d_sum0, d_sum1, d_hat, mask, epi);
   return check_launch("row_sum2_kernel");
 }
 

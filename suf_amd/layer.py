@@ -31,7 +31,8 @@ import torch
 from . import native, spline, tables
 from .layernorm import LayerNormBlock
 from .softmax import SoftmaxBlock, causal_offsets
-from .tasks import Dealer, Trunc, dev, dev_i32, lin2, operand, pair, ptr, stream_ptr, term
+from .tasks import (Dealer, Prepared, Trunc, dev, dev_i32, lin2, operand, pair, ptr, stream_ptr,
+                    term)
 
 M64 = (1 << 64) - 1
 
@@ -62,16 +63,21 @@ class PublicMatmulTrunc:
     def truncs(self):
         return [self.tr]
 
-    def product2(self, X, out=None, zhat=None, mask=0):
+    def product2(self, X, out=None, zhat=None, mask=0, trunc=None):
         native.call("sufhip_matmul_public2", ptr(X[0]), ptr(X[1]), self.M, self.K, self.N,
                     ptr(self.planes), self.digits,
                     ptr(out[0]) if out is not None else None,
                     ptr(out[1]) if out is not None else None, ptr(zhat), mask & M64,
+                    native.ctypes.byref(trunc) if trunc is not None else None,
                     ptr(self.work), self.work_bytes, stream_ptr())
 
     def eval2(self, X, out):
-        self.product2(X, zhat=self.zhat, mask=self.tr.mask)
-        self.tr.finish(self.zhat, out)
+        """Its truncation must have been prepared."""
+        if self.tr.has_table():
+            self.product2(X, mask=self.tr.mask, trunc=self.tr.epilogue(out))
+        else:
+            self.product2(X, zhat=self.zhat, mask=self.tr.mask)
+            self.tr.finish(self.zhat, out)
         return out
 
 
@@ -161,14 +167,17 @@ class AttentionCore:
         self.prob = pair(self.n + 1, device)  # slot n stays 0: the masked entries of P
         for t in self.prob:
             t[self.n:].zero_()
-        self.zs = torch.empty(self.n, dtype=torch.int64, device=device)
-        self.zc = torch.empty(seq * d, dtype=torch.int64, device=device)
+        self.side = torch.cuda.Stream(device=device)
 
     def truncs(self):
-        return [self.tr_s, self.tr_c]
+        return [self.tr_s, self.tr_c] + self.softmax.truncs()
 
-    def eval2(self, qkv, out):
+    def eval2(self, qkv, out, prep=None):
+        """prep: (tasks.Prepared, batch) holding the key-only halves of
+        truncs(), or None to issue them here."""
         seq, d, h, dh, mp = self.seq, self.d, self.heads, self.dh, self.maps
+        if prep is None:
+            prep = (Prepared(self.side, [self.truncs()]), 0)
         # D = open(Q_h - A), E = open(K_h^T - B), then the per-head products.
         lin2(operand(term(qkv, index=mp["gq"]), term(self.tri_qk.A, neg=True)), h * seq * dh,
              xhat=self.D)
@@ -176,17 +185,16 @@ class AttentionCore:
              xhat=self.E)
         _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S)
         # Masked open of inv_sqrt * S at the packed causal positions, truncation by 2f.
-        lin2(operand(term(self.S, index=mp["gs"], mul=self.inv_sqrt)), self.n, xhat=self.zs,
-             mask=self.tr_s.mask)
-        self.tr_s.finish(self.zs, self.scores)
-        self.softmax.eval2(self.scores, self.prob)
+        prep[0].wait(prep[1])
+        lin2(operand(term(self.S, index=mp["gs"], mul=self.inv_sqrt)), self.n,
+             into=(self.tr_s, self.scores))
+        self.softmax.eval2(self.scores, self.prob, prep=prep)
         lin2(operand(term(self.prob, index=mp["gp"]), term(self.tri_pv.A, neg=True)),
              h * seq * seq, xhat=self.D2)
         lin2(operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True)), h * seq * dh,
              xhat=self.E)
         _beaver_batched(self.D2, self.E, self.tri_pv, h, seq, seq, dh, self.Z)
-        lin2(operand(term(self.Z, index=mp["gc"])), seq * d, xhat=self.zc, mask=self.tr_c.mask)
-        self.tr_c.finish(self.zc, out)
+        lin2(operand(term(self.Z, index=mp["gc"])), seq * d, into=(self.tr_c, out))
         return out
 
 
@@ -231,20 +239,19 @@ class TransformerLayer:
         self.r1, self.h2, self.u, self.g, self.m = pair(n), pair(n), pair(seq * ffn), \
             pair(seq * ffn), pair(n)
 
-    def truncs(self):
-        return (self.qkv.truncs() + self.attn.truncs() + self.proj.truncs() + self.w1.truncs()
-                + self.w2.truncs())
+    def stage_truncs(self):
+        """The layer's truncation gates in four batches, in order of need."""
+        return [self.ln1.truncs(),
+                self.qkv.truncs() + self.attn.truncs(),
+                self.proj.truncs() + self.ln2.truncs(),
+                self.w1.truncs() + self.gelu.truncs() + self.w2.truncs()]
 
     def eval2(self, x, out, marks=None):
         """x, out: pairs of int64 [seq * d] device tensors.  marks: optional
-        list of torch events recorded after each stage (profiling)."""
-        start = torch.cuda.Event()
-        start.record()
-        self.side.wait_event(start)
-        for t in self.truncs():
-            t.prepare(self.side)
-        prepared = torch.cuda.Event()
-        prepared.record(self.side)
+        list of torch events recorded after each stage (profiling).  The
+        key-only halves of all truncation gates run on a side stream in four
+        batches, each ahead of the stage that needs it."""
+        prep = Prepared(self.side, self.stage_truncs())
 
         def mark():
             if marks is not None:
@@ -254,21 +261,23 @@ class TransformerLayer:
 
         n = self.seq * self.d
         mark()
-        self.ln1.eval2(x, self.h1)
+        self.ln1.eval2(x, self.h1, prep=(prep, 0))
         mark()
-        torch.cuda.current_stream().wait_event(prepared)
+        prep.wait(1)
         self.qkv.eval2(self.h1, self.qkvs)
         mark()
-        self.attn.eval2(self.qkvs, self.ctx)
+        self.attn.eval2(self.qkvs, self.ctx, prep=(prep, 1))
         mark()
+        prep.wait(2)
         self.proj.eval2(self.ctx, self.a)
         lin2(operand(term(self.a), term(x)), n, out=self.r1)
         mark()
-        self.ln2.eval2(self.r1, self.h2)
+        self.ln2.eval2(self.r1, self.h2, prep=(prep, 2))
         mark()
+        prep.wait(3)
         self.w1.eval2(self.h2, self.u)
         mark()
-        self.gelu.eval2(self.u, self.g)
+        self.gelu.eval2(self.u, self.g, prep=(prep, 3))
         mark()
         self.w2.eval2(self.g, self.m)
         lin2(operand(term(self.m), term(self.r1)), n, out=out)

@@ -16,14 +16,15 @@ mask, and halves x y2 by a local shift of a share; here the init is a Beaver
 product with a truncation and the halving is folded into the truncation by
 f + 1, which reconstructs to the same floor((x y2 >> f) / 2) of
 ref_rsqrt_fixed (include/gates/rsqrt_gate.hpp:100-117).  Every truncation is
-a GapARS gate with its own key.  Randomness: suf_amd.tasks.Dealer(seed).
+a GapARS gate with its own key; those up to 14 bits are folded into the launch
+producing their masked open.  Randomness: suf_amd.tasks.Dealer(seed).
 """
 import numpy as np
 import torch
 
 from . import tables
-from .tasks import (CoeffLut, Dealer, Triples, Trunc, dev_i32, lin2, mul2x, operand, pair,
-                    row_sum2, term)
+from .tasks import (CoeffLut, Dealer, Prepared, Triples, Trunc, dev_i32, lin2, mul2x, operand,
+                    pair, row_sum2, term)
 
 
 class Rsqrt:
@@ -39,7 +40,6 @@ class Rsqrt:
         fs = [frac_bits] + [frac_bits, frac_bits + 1, frac_bits] * iters
         self.tr = [Trunc(dealer, f, n, prg_state, device=device) for f in fs]
         self.coef = pair(n, device, 2)
-        self.zhat = torch.empty(n, dtype=torch.int64, device=device)
         self.t = pair(n, device)
         self.y2 = pair(n, device)
         self.h = pair(n, device)
@@ -49,23 +49,21 @@ class Rsqrt:
         return self.tr
 
     def eval2(self, v, vhat, out=None):
+        """v: operand of the values; vhat: their masked open with lut.mask.
+        The gate's truncations must have been prepared."""
         n, f = self.n, self.f
         out = self.y if out is None else out
         self.lut.eval2(vhat, n, self.coef)
-        mul2x(operand(term(self.coef, stride=2, off=1)), v, self.tri[0], n, zhat=self.zhat,
-              open_mask=self.tr[0].mask)
-        self.tr[0].finish(self.zhat, self.t)
+        mul2x(operand(term(self.coef, stride=2, off=1)), v, self.tri[0], n,
+              into=(self.tr[0], self.t))
         y = operand(term(self.t), term(self.coef, stride=2, off=0))
         for it in range(self.iters):
             ta, tb, tc = self.tr[1 + 3 * it: 4 + 3 * it]
             ka, kb, kc = self.tri[1 + 3 * it: 4 + 3 * it]
-            mul2x(y, y, ka, n, zhat=self.zhat, open_mask=ta.mask)
-            ta.finish(self.zhat, self.y2)
-            mul2x(v, operand(term(self.y2)), kb, n, zhat=self.zhat, open_mask=tb.mask)
-            tb.finish(self.zhat, self.h)
+            mul2x(y, y, ka, n, into=(ta, self.y2))
+            mul2x(v, operand(term(self.y2)), kb, n, into=(tb, self.h))
             inner = operand(term(self.h, neg=True), const=3 << (f - 1))
-            mul2x(y, inner, kc, n, zhat=self.zhat, open_mask=tc.mask)
-            tc.finish(self.zhat, out)
+            mul2x(y, inner, kc, n, into=(tc, out))
             y = operand(term(out))
         if self.iters == 0:
             lin2(y, n, out=out)
@@ -96,38 +94,27 @@ class LayerNormBlock:
         self.sq = pair(self.n, device)
         self.var = pair(rows, device)
         self.rowhat = torch.empty(rows, dtype=torch.int64, device=device)
-        self.zhat = torch.empty(self.n, dtype=torch.int64, device=device)
 
     def truncs(self):
         return [self.tr_mean, self.tr_var] + self.rsqrt.truncs() + [self.tr_norm]
 
-    def _prepare(self):
-        start = torch.cuda.Event()
-        start.record()
-        self.side.wait_event(start)
-        for t in self.truncs():
-            t.prepare(self.side)
-        done = torch.cuda.Event()
-        done.record(self.side)
-        return done
-
-    def eval2(self, x, out):
-        """x, out: pairs of int64 [rows * cols] device tensors."""
+    def eval2(self, x, out, prep=None):
+        """x, out: pairs of int64 [rows * cols] device tensors.  prep:
+        (tasks.Prepared, batch) holding this block's key-only halves, or None
+        to issue them here on the block's side stream."""
         rows, cols, n = self.rows, self.cols, self.n
-        prepared = self._prepare()
-        row_sum2(operand(term(x)), rows, cols, mul_const=self.inv_len, hat=self.rowhat,
-                 mask=self.tr_mean.mask)
-        torch.cuda.current_stream().wait_event(prepared)
-        self.tr_mean.finish(self.rowhat, self.mu)
+        if prep is None:
+            prep = (Prepared(self.side, [self.truncs()]), 0)
+        prep[0].wait(prep[1])
+        row_sum2(operand(term(x)), rows, cols, mul_const=self.inv_len,
+                 into=(self.tr_mean, self.mu))
         diff = operand(term(x), term(self.mu, index=self.row_index, neg=True, length=rows))
         mul2x(diff, diff, self.tri_sq, n, z=self.sq)
-        row_sum2(operand(term(self.sq)), rows, cols, mul_const=self.inv_len, hat=self.rowhat,
-                 mask=self.tr_var.mask)
-        self.tr_var.finish(self.rowhat, self.var)
+        row_sum2(operand(term(self.sq)), rows, cols, mul_const=self.inv_len,
+                 into=(self.tr_var, self.var))
         v = operand(term(self.var), const=self.eps_q)
         lin2(v, rows, xhat=self.rowhat, mask=self.rsqrt.lut.mask)
         rs = self.rsqrt.eval2(v, self.rowhat)
         mul2x(diff, operand(term(rs, index=self.row_index, length=rows)), self.tri_norm, n,
-              zhat=self.zhat, open_mask=self.tr_norm.mask)
-        self.tr_norm.finish(self.zhat, out)
+              into=(self.tr_norm, out))
         return out

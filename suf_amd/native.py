@@ -74,7 +74,7 @@ _SIGS = {
     "sufhip_open2_diff": (c_int, [c_vp, c_vp, c_vp, c_vp, c_sz, c_vp, c_vp]),
     "sufhip_mul2": (c_int, [c_vp, c_sz, c_vp]),
     "sufhip_add_shifted": (c_int, [c_vp, c_vp, c_sz, c_sz, c_int, c_sz, c_vp, c_vp]),
-    "sufhip_lin2": (c_int, [c_vp, c_sz, c_vp, c_vp, c_vp, c_u64, c_vp]),
+    "sufhip_lin2": (c_int, [c_vp, c_sz, c_vp, c_vp, c_vp, c_u64, c_vp, c_vp]),
     "sufhip_beaver_matmul2_batched": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                               c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp]),
     "sufhip_public_w_digits": (c_int, [c_vp, c_sz]),
@@ -82,9 +82,13 @@ _SIGS = {
     "sufhip_public_w_prepare": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp]),
     "sufhip_matmul_public2_work_bytes": (c_sz, [c_int, c_int, c_int]),
     "sufhip_matmul_public2": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_vp,
-                                      c_vp, c_u64, c_vp, c_sz, c_vp]),
+                                      c_vp, c_u64, c_vp, c_vp, c_sz, c_vp]),
+    "sufhip_trunc_finish2": (c_int, [c_int, c_int, c_vp, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp,
+                                     c_vp, c_vp, c_sz, c_vp]),
+    "sufhip_trunc_prepare_batch": (c_int, [c_vp, c_vp, c_int, c_vp]),
     "sufhip_mul2x": (c_int, [c_vp, c_sz, c_vp]),
-    "sufhip_row_sum2": (c_int, [c_vp, c_int, c_int, c_vp, c_u64, c_vp, c_vp, c_vp, c_u64, c_vp]),
+    "sufhip_row_sum2": (c_int, [c_vp, c_int, c_int, c_vp, c_u64, c_vp, c_vp, c_vp, c_u64, c_vp,
+                                c_vp]),
     "sufhip_relu_max_round2": (c_int, [c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_int,
                                        c_u64, c_vp, c_vp, c_vp]),
     "sufhip_seed_from_id": (None, [c_u64, c_u64, c_vp]),
@@ -152,7 +156,20 @@ class Operand2(ctypes.Structure):
 class Mul2xArgs(ctypes.Structure):
     """sufhip_mul2x_args (include/suf_hip.h)."""
     _fields_ = [("u", Operand2), ("v", Operand2), ("a", Term2), ("b", Term2), ("c", Term2),
-                ("z_add", Operand2), ("z", c_vp * 2), ("zhat", c_vp), ("open_mask", c_u64)]
+                ("z_add", Operand2), ("z", c_vp * 2), ("zhat", c_vp), ("open_mask", c_u64),
+                ("trunc", c_vp)]
+
+
+class TruncEpilogue(ctypes.Structure):
+    """sufhip_trunc_epilogue (include/suf_hip.h)."""
+    _fields_ = [("key", c_vp * 2), ("table", c_vp * 2), ("work_bytes", c_sz),
+                ("frac_bits", c_int), ("y", c_vp * 2)]
+
+
+class TruncJob(ctypes.Structure):
+    """sufhip_trunc_job (include/suf_hip.h)."""
+    _fields_ = [("kind", c_int), ("frac_bits", c_int), ("d_key", c_vp), ("key_bytes", c_sz),
+                ("n", c_sz), ("d_work", c_vp), ("work_bytes", c_sz)]
 
 
 class SufHipError(RuntimeError):

@@ -18,14 +18,16 @@ packed ragged rows (row r holds elements [offsets[r], offsets[r+1])):
 
 Every truncation is a GapARS gate with its own key (the reference shares one
 trunc key among a task's truncations; reconstruction is the same exact
-shift).  Randomness: suf_amd.tasks.Dealer(seed).
+shift); those by f are folded into the launch of the product they truncate
+(a table read, the key-only half prepared on a side stream beforehand).
+Randomness: suf_amd.tasks.Dealer(seed).
 """
 import numpy as np
 import torch
 
 from . import native, spline, tables
-from .tasks import (RELU_ALPHA, CoeffLut, Dealer, Triples, Trunc, dev_i32, lin2, mul2x,
-                    operand, pair, relu_coeffs_for, row_sum2, stream_ptr, term)
+from .tasks import (RELU_ALPHA, CoeffLut, Dealer, Prepared, Triples, Trunc, dev_i32, lin2,
+                    mul2x, operand, pair, relu_coeffs_for, row_sum2, stream_ptr, term)
 
 
 def causal_offsets(heads, seq):
@@ -124,21 +126,20 @@ class Recip:
         return self.tr
 
     def eval2(self, x, xhat, out=None):
+        """x: shares of the values; xhat: their masked open with lut.mask.
+        The gate's truncations must have been prepared."""
         n, f = self.n, self.f
         out = self.y if out is None else out
         self.lut.eval2(xhat, n, self.coef)
         xs = operand(term(x))
-        mul2x(operand(term(self.coef, stride=2, off=1)), xs, self.tri[0], n, zhat=self.zhat,
-              open_mask=self.tr[0].mask)
-        self.tr[0].finish(self.zhat, self.t)
+        mul2x(operand(term(self.coef, stride=2, off=1)), xs, self.tri[0], n,
+              into=(self.tr[0], self.t))
         y = operand(term(self.t), term(self.coef, stride=2, off=0))
         for it in range(self.iters):
             t1, t2 = self.tr[1 + 2 * it], self.tr[2 + 2 * it]
-            mul2x(y, xs, self.tri[1 + 2 * it], n, zhat=self.zhat, open_mask=t1.mask)
-            t1.finish(self.zhat, self.xy)
+            mul2x(y, xs, self.tri[1 + 2 * it], n, into=(t1, self.xy))
             two_minus = operand(term(self.xy, neg=True), const=2 << f)
-            mul2x(y, two_minus, self.tri[2 + 2 * it], n, zhat=self.zhat, open_mask=t2.mask)
-            t2.finish(self.zhat, out)
+            mul2x(y, two_minus, self.tri[2 + 2 * it], n, into=(t2, out))
             y = operand(term(out))
         if self.iters == 0:
             lin2(y, n, out=out)
@@ -173,29 +174,21 @@ class SoftmaxBlock:
         self.e = pair(self.n, device)
         self.s = pair(self.rows, device)
         self.shat = torch.empty(self.rows, dtype=torch.int64, device=device)
-        self.zhat = torch.empty(self.n, dtype=torch.int64, device=device)
 
-    def _prepare(self):
-        """Key-only halves of the block's own truncations on a side stream."""
-        start = torch.cuda.Event()
-        start.record()
-        self.side.wait_event(start)
-        for t in self.recip.truncs() + [self.tr]:
-            t.prepare(self.side)
-        done = torch.cuda.Event()
-        done.record(self.side)
-        return done
+    def truncs(self):
+        return self.nexp.truncs() + self.recip.truncs() + [self.tr]
 
-    def eval2(self, x, out):
-        """x, out: pairs of int64 [n] device tensors (packed rows)."""
-        prepared = self._prepare()
+    def eval2(self, x, out, prep=None):
+        """x, out: pairs of int64 [n] device tensors (packed rows).  prep:
+        (tasks.Prepared, batch) holding this block's key-only halves, or None
+        to issue them here on the block's side stream."""
+        if prep is None:
+            prep = (Prepared(self.side, [self.truncs()]), 0)
         self.rowmax.eval2(x, self.delta)
-        self.nexp.eval2(self.delta, self.e)
+        self.nexp.eval2(self.delta, self.e, prep=prep)
         row_sum2(operand(term(self.e)), self.rows, offsets=self.offs_dev, sums=self.s,
                  hat=self.shat, mask=self.recip.lut.mask)
-        torch.cuda.current_stream().wait_event(prepared)
         inv = self.recip.eval2(self.s, self.shat)
         mul2x(operand(term(self.e)), operand(term(inv, index=self.row_index)), self.tri, self.n,
-              zhat=self.zhat, open_mask=self.tr.mask)
-        self.tr.finish(self.zhat, out)
+              into=(self.tr, out))
         return out

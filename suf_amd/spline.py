@@ -14,15 +14,18 @@ Protocol, as SUF runs it for SiLU/GeLU-style gates:
 The output mask r_out of spline gates is 0 (include/gates/silu_composite.hpp:
 92), so the LUT's coefficient shares are used directly.
 
-Every step runs in libsuf_hip.so: open2_masked, interval_lut_eval, mul2,
-trunc_prepare / trunc_finish, add_shifted.  The truncations' key-only
-precomputation runs on side streams, overlapped with the first rounds.  The dealer builds keys with the library's key
-builders and host std::mt19937_64 streams.
+Every step runs in libsuf_hip.so: open2_masked, interval_lut_eval, mul2x
+(the first truncation folded into the product's launch as a table lookup),
+trunc_finish2 for the 2f truncation, lin2.  The truncations' key-only
+precomputation runs on a side stream, overlapped with the first rounds.  The
+dealer builds keys with the library's key builders and host std::mt19937_64
+streams.
 """
 import numpy as np
 import torch
 
 from . import native, pfss
+from .tasks import AosTriples, Prepared, Trunc, lin2, mul2x, operand, term
 
 M64 = (1 << 64) - 1
 LUT_TWEAK = 7  # seed_from_id tweak of interval LUT keys (cuda/pfss_backend_gpu.cu:508-515)
@@ -138,91 +141,41 @@ class SplineGate:
         self.trunc = []
         for j, fb in enumerate((frac_bits, 2 * frac_bits)):
             rnd = head[2 + j * native.TRUNC_RAND_WORDS: 2 + (j + 1) * native.TRUNC_RAND_WORDS]
-            k0, k1 = pfss.trunc_gen(native.TRUNC_GAPARS, fb, self.prg_state, rnd, device)
-            r = int(rnd[0])
-            self.trunc.append({"f": fb, "keys": (k0, k1), "rin": _split(r, int(rnd[1]))})
-        # Per (truncation, party) workspace for the key-only frontier, which
-        # eval2 computes on one side stream per party while the LUT and the
-        # first two products run.
-        for t in self.trunc:
-            t["work_bytes"] = lib.sufhip_trunc_work_bytes(t["f"], n)
-            t["work"] = [torch.empty(max(2, (t["work_bytes"] + 15) // 8), dtype=torch.int64,
-                                     device=device) for _ in range(2)]
-        self.side = [torch.cuda.Stream(device=device) for _ in range(2)]
+            self.trunc.append(Trunc(None, fb, n, self.prg_state, rnd=rnd, device=device))
+        self.side = torch.cuda.Stream(device=device)
         # Scratch for the online phase.
         self.xhat = torch.empty(n, dtype=torch.int64, device=device)
         self.coef = [torch.empty((n, 4), dtype=torch.int64, device=device) for _ in range(2)]
         self.u = [torch.empty(n, dtype=torch.int64, device=device) for _ in range(2)]
         self.y = [torch.empty(n, dtype=torch.int64, device=device) for _ in range(2)]
+        self.y2 = [torch.empty(n, dtype=torch.int64, device=device) for _ in range(2)]
+        self.tri = [AosTriples(t) for t in self.triples]
 
-    def _mul2(self, u, v, tri, u_stride=1, u_off=0, u_add=None, u_add_stride=1, u_add_off=0,
-              u_add_shift=0, z_add=None, z_add_stride=1, z_add_off=0, z_add_shift=0, z=None,
-              zhat=None, open_mask=(0, 0)):
-        a = native.Mul2Args()
-        a.u[0], a.u[1] = _p(u[0]), _p(u[1])
-        a.u_stride, a.u_off = u_stride, u_off
-        if u_add is not None:
-            a.u_add[0], a.u_add[1] = _p(u_add[0]), _p(u_add[1])
-            a.u_add_stride, a.u_add_off, a.u_add_shift = u_add_stride, u_add_off, u_add_shift
-        a.v[0], a.v[1] = _p(v[0]), _p(v[1])
-        a.triples[0], a.triples[1] = _p(tri[0]), _p(tri[1])
-        if z_add is not None:
-            a.z_add[0], a.z_add[1] = _p(z_add[0]), _p(z_add[1])
-            a.z_add_stride, a.z_add_off, a.z_add_shift = z_add_stride, z_add_off, z_add_shift
-        if z is not None:
-            a.z[0], a.z[1] = _p(z[0]), _p(z[1])
-        a.zhat = _p(zhat)
-        a.open_mask[0], a.open_mask[1] = open_mask[0], open_mask[1]
-        native.call("sufhip_mul2", native.ctypes.byref(a), self.n, _stream())
+    def truncs(self):
+        return list(self.trunc)
 
-    def _prepare(self):
-        """Key-only halves of both truncations, one side stream per party."""
-        start = torch.cuda.Event()
-        start.record()
-        done = []
-        for p in (0, 1):
-            side = self.side[p]
-            side.wait_event(start)
-            for t in self.trunc:
-                native.call("sufhip_trunc_prepare", native.TRUNC_GAPARS, t["f"],
-                            pfss._state_buf(self.prg_state), _p(t["keys"][p]),
-                            t["keys"][p].numel(), self.n, _p(t["work"][p]), t["work_bytes"],
-                            side.cuda_stream)
-            ev = torch.cuda.Event()
-            ev.record(side)
-            done.append(ev)
-        return done
-
-    def _trunc(self, t, xhat, out):
-        for p in (0, 1):
-            native.call("sufhip_trunc_finish", native.TRUNC_GAPARS, t["f"],
-                        pfss._state_buf(self.prg_state), _p(t["keys"][p]), t["keys"][p].numel(),
-                        _p(xhat), self.n, _p(out[p]), _p(t["work"][p]), t["work_bytes"],
-                        _stream())
-
-    def eval2(self, x, out):
-        """x, out: pairs of int64[n] device tensors (party 0, party 1 shares)."""
-        n, f, s = self.n, self.f, _stream()
-        prepared = self._prepare()
+    def eval2(self, x, out, prep=None):
+        """x, out: pairs of int64[n] device tensors (party 0, party 1 shares).
+        prep: (tasks.Prepared, batch) holding this gate's key-only halves, or
+        None to issue them here on the gate's side stream."""
+        n, f, s = self.n, self.f, torch.cuda.current_stream().cuda_stream
+        if prep is None:
+            prep = (Prepared(self.side, [self.truncs()]), 0)
         native.call("sufhip_open2_masked", _p(x[0]), _p(x[1]), self.rin[0], self.rin[1], n,
                     _p(self.xhat), s)
         for p in (0, 1):
             native.call("sufhip_interval_lut_eval", _p(self.lut[p]), self.lut_key_bytes, 1,
                         self.intervals, 4, _p(self.xhat), n, _p(self.coef[p]), s)
+        xs = operand(term(x))
         # u = c3 * x + c2 << f
-        self._mul2(self.coef, x, self.triples[0], u_stride=4, u_off=3, z_add=self.coef,
-                   z_add_stride=4, z_add_off=2, z_add_shift=f, z=self.u)
-        # p^ = u * x + r_t1 (opened)
+        mul2x(operand(term(self.coef, stride=4, off=3)), xs, self.tri[0], n, z=self.u,
+              z_add=operand(term(self.coef, stride=4, off=2, shift=f)))
+        prep[0].wait(prep[1])
         t1, t2 = self.trunc
-        self._mul2(self.u, x, self.triples[1], zhat=self.xhat, open_mask=t1["rin"])
-        for ev in prepared:
-            torch.cuda.current_stream().wait_event(ev)
-        self._trunc(t1, self.xhat, self.y)
-        # r^ = (p2 + c1 << f) * x + r_t2 (opened)
-        self._mul2(self.y, x, self.triples[2], u_add=self.coef, u_add_stride=4, u_add_off=1,
-                   u_add_shift=f, zhat=self.xhat, open_mask=t2["rin"])
-        self._trunc(t2, self.xhat, self.y)
-        for p in (0, 1):
-            native.call("sufhip_add_shifted", _p(self.y[p]), _p(self.coef[p]), 4, 0, 0, n,
-                        _p(out[p]), s)
+        # y = trunc_f(u * x)
+        mul2x(operand(term(self.u)), xs, self.tri[1], n, into=(t1, self.y))
+        # y2 = trunc_2f((y + c1 << f) * x); out = y2 + c0
+        mul2x(operand(term(self.y), term(self.coef, stride=4, off=1, shift=f)), xs, self.tri[2],
+              n, into=(t2, self.y2))
+        lin2(operand(term(self.y2), term(self.coef, stride=4, off=0)), n, out=out)
         return out

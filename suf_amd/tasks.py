@@ -88,15 +88,39 @@ def operand(*terms, const=0):
     return o
 
 
-def lin2(x, n, out=None, xhat=None, mask=0):
+def _open_target(into, xhat, mask):
+    """into = (Trunc, out pair): the open feeds that truncation gate.
+    Returns (epilogue struct or None, open buffer, mask, finish-afterwards)."""
+    if into is None:
+        return None, xhat, mask, None
+    tr, y = into
+    if tr.has_table():
+        return tr.epilogue(y), None, tr.mask, None
+    return None, tr.zhat_buf(), tr.mask, (tr, y)
+
+
+def _after(fin):
+    if fin is not None:
+        tr, y = fin
+        tr.finish(tr.zhat_buf(), y)
+
+
+def lin2(x, n, out=None, xhat=None, mask=0, into=None):
+    """Operand shares (out) and/or their masked open (xhat), or with
+    into = (Trunc, y) the open truncated into y."""
+    epi, hat, mask, fin = _open_target(into, xhat, mask)
     native.call("sufhip_lin2", native.ctypes.byref(x), n,
                 ptr(out[0]) if out is not None else None,
-                ptr(out[1]) if out is not None else None, ptr(xhat), mask & M64, stream_ptr())
+                ptr(out[1]) if out is not None else None, ptr(hat), mask & M64,
+                native.ctypes.byref(epi) if epi is not None else None, stream_ptr())
+    _after(fin)
 
 
-def mul2x(u, v, tri, n, z=None, zhat=None, open_mask=0, z_add=None):
+def mul2x(u, v, tri, n, z=None, zhat=None, open_mask=0, z_add=None, into=None):
     """Beaver product of two operands with triple `tri` (a Triples); writes
-    the shares to z (pair) or the masked open of the product to zhat."""
+    the shares to z (pair), the masked open of the product to zhat, or with
+    into = (Trunc, y) the open truncated into y."""
+    epi, hat, mask, fin = _open_target(into, zhat, open_mask)
     a = native.Mul2xArgs()
     a.u, a.v = u, v
     a.a, a.b, a.c = tri.terms()
@@ -104,15 +128,22 @@ def mul2x(u, v, tri, n, z=None, zhat=None, open_mask=0, z_add=None):
         a.z_add = z_add
     if z is not None:
         a.z[0], a.z[1] = ptr(z[0]), ptr(z[1])
-    a.zhat = ptr(zhat)
-    a.open_mask = open_mask & M64
+    a.zhat = ptr(hat)
+    a.open_mask = mask & M64
+    a.trunc = native.ctypes.cast(native.ctypes.pointer(epi), native.c_vp) if epi is not None \
+        else None
     native.call("sufhip_mul2x", native.ctypes.byref(a), n, stream_ptr())
+    _after(fin)
 
 
-def row_sum2(x, rows, cols=0, offsets=None, mul_const=1, sums=None, hat=None, mask=0):
+def row_sum2(x, rows, cols=0, offsets=None, mul_const=1, sums=None, hat=None, mask=0,
+             into=None):
+    epi, hat, mask, fin = _open_target(into, hat, mask)
     native.call("sufhip_row_sum2", native.ctypes.byref(x), rows, cols, ptr(offsets),
                 mul_const & M64, ptr(sums[0]) if sums is not None else None,
-                ptr(sums[1]) if sums is not None else None, ptr(hat), mask & M64, stream_ptr())
+                ptr(sums[1]) if sums is not None else None, ptr(hat), mask & M64,
+                native.ctypes.byref(epi) if epi is not None else None, stream_ptr())
+    _after(fin)
 
 
 class Triples:
@@ -146,33 +177,100 @@ class Triples:
                 (h["c"] - h["c0"]).astype(np.uint64))
 
 
+TABLE_BITS = 14  # carry keys this wide are prepared as full-domain tables
+
+
 class Trunc:
     """One truncation gate (scalar mask r) over n elements, both parties."""
 
     def __init__(self, dealer, frac_bits, n, prg_state, kind=native.TRUNC_GAPARS,
-                 device="cuda"):
+                 device="cuda", rnd=None):
         self.kind, self.f, self.n = kind, frac_bits, n
+        self.device = device
         self.prg_state = bytes(prg_state)
-        self.rnd = dealer.words(native.TRUNC_RAND_WORDS)
+        self.rnd = np.ascontiguousarray(rnd, dtype=np.uint64) if rnd is not None else \
+            dealer.words(native.TRUNC_RAND_WORDS)
         self.mask = int(self.rnd[0])  # r = r_0 + r_1: the open's mask
         self.keys = pfss.trunc_gen(kind, frac_bits, self.prg_state, self.rnd, device)
         self.work_bytes = native.load().sufhip_trunc_work_bytes(frac_bits, n)
         self.work = [torch.empty(max(2, (self.work_bytes + 15) // 8), dtype=torch.int64,
                                  device=device) for _ in range(2)]
         self._state = pfss._state_buf(self.prg_state)
+        self._zhat = None
+
+    def has_table(self):
+        """The finish is one table read that other launches can fold in."""
+        return self.kind == native.TRUNC_GAPARS and self.f <= TABLE_BITS
+
+    def zhat_buf(self):
+        if self._zhat is None:
+            self._zhat = torch.empty(self.n, dtype=torch.int64, device=self.device)
+        return self._zhat
+
+    def jobs(self):
+        """sufhip_trunc_job of both parties' keys (key-only half)."""
+        out = []
+        for p in (0, 1):
+            j = native.TruncJob()
+            j.kind, j.frac_bits = self.kind, self.f
+            j.d_key, j.key_bytes = ptr(self.keys[p]), self.keys[p].numel()
+            j.n, j.d_work, j.work_bytes = self.n, ptr(self.work[p]), self.work_bytes
+            out.append(j)
+        return out
+
+    def epilogue(self, y):
+        e = native.TruncEpilogue()
+        e.key[0], e.key[1] = ptr(self.keys[0]), ptr(self.keys[1])
+        e.table[0], e.table[1] = ptr(self.work[0]), ptr(self.work[1])
+        e.work_bytes = self.work_bytes
+        e.frac_bits = self.f
+        e.y[0], e.y[1] = ptr(y[0]), ptr(y[1])
+        return e
 
     def prepare(self, stream=None):
         """Key-only half (both parties) on `stream` (default: current)."""
-        s = stream.cuda_stream if stream is not None else stream_ptr()
-        for p in (0, 1):
-            native.call("sufhip_trunc_prepare", self.kind, self.f, self._state, ptr(self.keys[p]),
-                        self.keys[p].numel(), self.n, ptr(self.work[p]), self.work_bytes, s)
+        prepare_batch([self], stream)
 
     def finish(self, xhat, out):
-        for p in (0, 1):
-            native.call("sufhip_trunc_finish", self.kind, self.f, self._state, ptr(self.keys[p]),
-                        self.keys[p].numel(), ptr(xhat), self.n, ptr(out[p]), ptr(self.work[p]),
-                        self.work_bytes, stream_ptr())
+        """Both parties' outputs at the masked open xhat (one launch)."""
+        native.call("sufhip_trunc_finish2", self.kind, self.f, self._state, ptr(self.keys[0]),
+                    ptr(self.keys[1]), self.keys[0].numel(), ptr(xhat), self.n, ptr(out[0]),
+                    ptr(out[1]), ptr(self.work[0]), ptr(self.work[1]), self.work_bytes,
+                    stream_ptr())
+
+
+def prepare_batch(truncs, stream=None):
+    """The key-only halves of many truncation gates (same PRG state) in one
+    batched launch sequence on `stream` (default: current)."""
+    if not truncs:
+        return
+    state = truncs[0].prg_state
+    if any(t.prg_state != state for t in truncs):
+        raise ValueError("prepare_batch: gates with different PRG states")
+    jobs = [j for t in truncs for j in t.jobs()]
+    arr = (native.TruncJob * len(jobs))(*jobs)
+    s = stream.cuda_stream if stream is not None else stream_ptr()
+    native.call("sufhip_trunc_prepare_batch", truncs[0]._state, arr, len(jobs), s)
+
+
+class Prepared:
+    """Key-only halves of a block's truncation gates issued on a side stream
+    (in batches, in order of need); wait(k) makes the current stream wait for
+    batch k."""
+
+    def __init__(self, side, batches):
+        start = torch.cuda.Event()
+        start.record()
+        side.wait_event(start)
+        self.events = []
+        for b in batches:
+            prepare_batch(b, side)
+            ev = torch.cuda.Event()
+            ev.record(side)
+            self.events.append(ev)
+
+    def wait(self, k=0):
+        torch.cuda.current_stream().wait_event(self.events[k])
 
 
 def rotated_lut(alpha, coeffs, r_in):
@@ -244,3 +342,34 @@ RELU_ALPHA = np.array([0, 1 << 63], dtype=np.uint64)
 
 def pair(n, device="cuda", width=1):
     return tuple(torch.empty(n * width, dtype=torch.int64, device=device) for _ in range(2))
+
+
+def capture(fn, warmup=1):
+    """Records fn() (launches on torch's current stream, side streams joined
+    by events) into a HIP graph; replay() then reissues the whole chain with
+    one launch.  fn must allocate nothing and clear no memory with memset
+    (every entry point of libsuf_hip.so qualifies).  Runs fn `warmup` times
+    eagerly first."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(warmup):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+class AosTriples:
+    """Elementwise triples stored as {a, b, c} per element (the AoS layout of
+    launch_beaver_mul_aos_kernel, include/runtime/cuda_primitives.hpp:29-35):
+    pair of int64 [n * 3] tensors."""
+
+    def __init__(self, pair_aos):
+        self.t = pair_aos
+
+    def terms(self):
+        return (term(self.t, stride=3, off=0), term(self.t, stride=3, off=1),
+                term(self.t, stride=3, off=2))

@@ -45,13 +45,16 @@ def test_trunc_key_bytes_match_oracle(kind, f):
 
 def test_trunc_workspace_sizes():
     lib = native.load()
-    # Frontier depth d = min(f, floor(log2 n) - 1, 22), none below n = 32;
-    # 32 bytes per node, 2^d nodes plus 2^(d-1) when levels beyond 12 are expanded.
+    # Frontier depth: d = f for f <= 14 (full-domain table), else
+    # d = min(f, max(floor(log2 n) - 1, 12), 22); 32 bytes per node, 2^d nodes
+    # plus 2^(d-1) when levels beyond 12 are expanded; nothing for n = 0.
     assert lib.sufhip_trunc_work_bytes(12, 1 << 20) == 32 << 12
+    assert lib.sufhip_trunc_work_bytes(12, 31) == 32 << 12
+    assert lib.sufhip_trunc_work_bytes(13, 128) == 32 * ((1 << 13) + (1 << 12))
     assert lib.sufhip_trunc_work_bytes(24, 1 << 20) == 32 * ((1 << 19) + (1 << 18))
-    assert lib.sufhip_trunc_work_bytes(24, 3000) == 32 << 10
+    assert lib.sufhip_trunc_work_bytes(24, 3000) == 32 << 12
+    assert lib.sufhip_trunc_work_bytes(24, 128) == 32 << 12
     assert lib.sufhip_trunc_work_bytes(40, 1 << 30) == 32 * ((1 << 22) + (1 << 21))
-    assert lib.sufhip_trunc_work_bytes(12, 31) == 0
     assert lib.sufhip_trunc_work_bytes(12, 0) == 0
 
 

@@ -140,12 +140,10 @@ def spline2(prg, gate, x, idx0=0, sl=None):
     m1 = [m1[p] + (C[p][:, 2] << sh) for p in (0, 1)]
     pz = mul(m1, [x0, x1], tri[1])
     t1, t2 = gate.trunc
-    phat = (pz[0] + pz[1] + np.uint64(sum(t1["rin"]) & M64)).astype(np.uint64)
-    y = [ol.trunc_eval(prg, ol.TRUNC_GAPARS, t1["f"], host(t1["keys"][p]), phat) for p in (0, 1)]
+    y = trunc2(prg, t1, open2(pz, t1.mask))
     q = [y[p] + (C[p][:, 1] << sh) for p in (0, 1)]
     rz = mul(q, [x0, x1], tri[2])
-    rhat = (rz[0] + rz[1] + np.uint64(sum(t2["rin"]) & M64)).astype(np.uint64)
-    y2 = [ol.trunc_eval(prg, ol.TRUNC_GAPARS, t2["f"], host(t2["keys"][p]), rhat) for p in (0, 1)]
+    y2 = trunc2(prg, t2, open2(rz, t2.mask))
     return [(y2[p] + C[p][:, 0]).astype(np.uint64) for p in (0, 1)]
 
 
