@@ -355,6 +355,17 @@ int sufhip_row_sum2(const sufhip_operand2* x, int rows, int cols, const int32_t*
                     uint64_t mul_const, uint64_t* d_sum0, uint64_t* d_sum1, uint64_t* d_hat,
                     uint64_t mask, const sufhip_trunc_epilogue* trunc, void* stream);
 
+/* Both parties' broadcast interval-LUT keys of one gate in one launch (the
+ * coefficient LUT of a composite gate evaluated by both parties), at the
+ * masked open xhat = x_0 + x_1 + mask of the operand x, or at d_xhat when x
+ * is NULL.  Same shares as sufhip_interval_lut_eval with each key; for small
+ * gates (intervals <= 64, intervals * out_words <= 512).  d_out0 / d_out1:
+ * [n][out_words]. */
+int sufhip_interval_lut_eval2(const uint8_t* d_key0, const uint8_t* d_key1, size_t key_bytes,
+                              int intervals, int out_words, const sufhip_operand2* x,
+                              const uint64_t* d_xhat, uint64_t mask, size_t n, uint64_t* d_out0,
+                              uint64_t* d_out1, void* stream);
+
 /* One pairwise-max round of RowMaxDiffTask (include/nn/row_maxdiff_task.hpp:
  * 49-150), max(a, b) = b + ReLU(a - b), for both parties.  For output slot j:
  *   src_b[j] < 0: next_p[j] = cur_p[src_a[j]] (odd element carried);

@@ -25,6 +25,7 @@
 #include <random>
 
 #include "aes_lds.hpp"
+#include "operand_device.hpp"
 #include "sufhip_internal.hpp"
 
 namespace sufhip {
@@ -327,6 +328,62 @@ __global__ void __launch_bounds__(kLutBlock) relu_max_round2_kernel(ReluRoundArg
   }
 }
 
+// Both parties' broadcast keys of one small gate in one launch, each staged
+// in LDS, at the masked open of an operand (or a given open).
+constexpr int kLut2Intervals = 64;
+constexpr int kLut2Payload = 512;
+
+struct Lut2Args {
+  const uint8_t* key[2];
+  sufhip_operand2 x;
+  const uint64_t* xhat;  // used when x has no terms
+  uint64_t mask;
+  uint64_t* out[2];
+  size_t n;
+  int intervals;
+  int out_words;
+  int has_x;
+};
+
+__global__ void __launch_bounds__(kLutBlock) lut_bcast2_kernel(Lut2Args a) {
+  __shared__ uint32_t tab[256 * kLutCopies];
+  __shared__ uint4 rk[2][11];
+  __shared__ uint64_t cuts[2][kLut2Intervals];
+  __shared__ uint64_t pay[2][kLut2Payload];
+  fill_ttable<kLutCopies>(tab, kTDev.v);
+  const int nint = a.intervals, ow = a.out_words;
+  for (int p = 0; p < 2; ++p) {
+    const uint8_t* k = a.key[p];
+    const uint32_t* rkg = reinterpret_cast<const uint32_t*>(k + 40);
+    for (int i = threadIdx.x; i < 11; i += blockDim.x)
+      rk[p][i] = make_uint4(rkg[4 * i], rkg[4 * i + 1], rkg[4 * i + 2], rkg[4 * i + 3]);
+    const uint64_t* cg = reinterpret_cast<const uint64_t*>(k + kLutHdr);
+    const uint64_t* pg = cg + (nint + 1);
+    for (int i = threadIdx.x; i < nint; i += blockDim.x) cuts[p][i] = cg[i];
+    for (int i = threadIdx.x; i < nint * ow; i += blockDim.x) pay[p][i] = pg[i];
+  }
+  __syncthreads();
+  const AesLds<kLutCopies> aes{tab, threadIdx.x % kLutCopies};
+  uint64_t m[2], nonce[2];
+  int party[2];
+  for (int p = 0; p < 2; ++p) {
+    m[p] = mask_bits(*reinterpret_cast<const uint16_t*>(a.key[p]));
+    party[p] = a.key[p][8];
+    nonce[p] = ld64(a.key[p] + 16);
+  }
+  for (size_t e = size_t(blockIdx.x) * kLutBlock + threadIdx.x; e < a.n;
+       e += size_t(gridDim.x) * kLutBlock) {
+    const uint64_t xh = a.has_x ? operand_at(a.x, 0, e) + operand_at(a.x, 1, e) + a.mask
+                                : a.xhat[e];
+    for (int p = 0; p < 2; ++p) {
+      const uint64_t x = xh & m[p];
+      const int iv = interval_of(x, nint, m[p], [&](int i) { return cuts[p][i]; });
+      write_masked_row(aes, rk[p], nonce[p], e, iv, ow, party[p], pay[p] + size_t(iv) * ow,
+                       a.out[p] + e * size_t(ow));
+    }
+  }
+}
+
 unsigned int lut_grid(size_t n) {
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess)
@@ -449,6 +506,42 @@ int sufhip_packed_lt_eval(const uint8_t* d_keys, size_t key_bytes, int key_broad
                        key_broadcast ? 1 : 0);
   }
   return check_launch("packed_lt kernel");
+}
+
+int sufhip_interval_lut_eval2(const uint8_t* d_key0, const uint8_t* d_key1, size_t key_bytes,
+                              int intervals, int out_words, const sufhip_operand2* x,
+                              const uint64_t* d_xhat, uint64_t mask, size_t n, uint64_t* d_out0,
+                              uint64_t* d_out1, void* stream) {
+  SUFHIP_REQUIRE(intervals >= 1 && intervals <= kLut2Intervals && out_words >= 1 &&
+                     intervals * out_words <= kLut2Payload,
+                 "sufhip_interval_lut_eval2: needs intervals <= 64 and intervals * out_words "
+                 "<= 512");
+  SUFHIP_REQUIRE(key_bytes == sufhip_interval_lut_key_bytes(intervals, out_words),
+                 "sufhip_interval_lut_eval2: key_bytes does not match (intervals, out_words)");
+  if (n == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(d_key0 && d_key1 && d_out0 && d_out1 && (x || d_xhat),
+                 "sufhip_interval_lut_eval2: null pointer");
+  SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_key0) & 7) == 0 &&
+                     (reinterpret_cast<uintptr_t>(d_key1) & 7) == 0,
+                 "sufhip_interval_lut_eval2: keys must be 8-byte aligned");
+  Lut2Args a{};
+  a.key[0] = d_key0;
+  a.key[1] = d_key1;
+  if (x) {
+    if (int rc = check_operand(*x, n, "sufhip_interval_lut_eval2")) return rc;
+    a.x = *x;
+    a.has_x = 1;
+  }
+  a.xhat = d_xhat;
+  a.mask = mask;
+  a.out[0] = d_out0;
+  a.out[1] = d_out1;
+  a.n = n;
+  a.intervals = intervals;
+  a.out_words = out_words;
+  hipLaunchKernelGGL(lut_bcast2_kernel, dim3(lut_grid(n)), dim3(kLutBlock), 0, as_stream(stream),
+                     a);
+  return check_launch("lut_bcast2_kernel");
 }
 
 int sufhip_relu_max_round2(const uint64_t* d_cur0, const uint64_t* d_cur1, size_t n_in,

@@ -31,6 +31,7 @@
 
 #include "suf_hip.h"
 #include "sufhip_internal.hpp"
+#include "operand_device.hpp"
 #include "trunc_device.hpp"
 
 namespace sufhip {
@@ -104,27 +105,6 @@ __global__ void __launch_bounds__(kBlock)
     out[i] = y[i] + (add[i * stride_a + off] << shift);
 }
 
-__device__ __forceinline__ uint64_t term_at(const sufhip_term2& t, int p, size_t i) {
-  // Clamped to the arrays' rows whether or not the row comes from an index.
-  size_t j = i;
-  if (t.index) {
-    const int32_t r = t.index[i];
-    j = r < 0 ? 0 : size_t(r);
-  }
-  if (j >= t.len) j = t.len - 1;
-  uint64_t v = t.p[p][j * t.stride + t.off];
-  if (t.mul) v *= t.mul;
-  v <<= t.shift;
-  return t.negate ? uint64_t(0) - v : v;
-}
-
-__device__ __forceinline__ uint64_t operand_at(const sufhip_operand2& o, int p, size_t i) {
-  uint64_t v = p == 0 ? o.party0_const : 0;
-  if (o.t[0].p[0]) v += term_at(o.t[0], p, i);
-  if (o.t[1].p[0]) v += term_at(o.t[1], p, i);
-  return v;
-}
-
 __global__ void __launch_bounds__(kBlock)
     lin2_kernel(sufhip_operand2 x, size_t n, uint64_t* out0, uint64_t* out1, uint64_t* xhat,
                 uint64_t mask, TruncEpi epi) {
@@ -193,31 +173,6 @@ __global__ void __launch_bounds__(kBlock)
       put_open(epi, hat, size_t(r), s0 + s1 + mask);
     }
   }
-}
-
-// Host-side checks of the generalised operands (see sufhip_term2 in suf_hip.h).
-int check_term(const sufhip_term2& t, size_t n, bool allow_shift, const char* what) {
-  if (!t.p[0] && !t.p[1]) return SUFHIP_OK;
-  if (!t.p[0] || !t.p[1]) {
-    set_error(std::string(what) + ": a term needs both parties' pointers or neither");
-    return SUFHIP_ERR_INVALID;
-  }
-  if (t.stride < 1 || t.off >= t.stride || t.shift < 0 || t.shift > 63 ||
-      (!allow_shift && (t.shift != 0 || t.negate || t.mul > 1))) {
-    set_error(std::string(what) + ": bad term stride/offset/shift/negate/mul");
-    return SUFHIP_ERR_INVALID;
-  }
-  if (t.len == 0 || (!t.index && t.len < n)) {
-    set_error(std::string(what) + ": term len smaller than the element count");
-    return SUFHIP_ERR_INVALID;
-  }
-  return SUFHIP_OK;
-}
-
-int check_operand(const sufhip_operand2& o, size_t n, const char* what) {
-  for (int k = 0; k < 2; ++k)
-    if (int rc = check_term(o.t[k], n, true, what)) return rc;
-  return SUFHIP_OK;
 }
 
 }  // namespace

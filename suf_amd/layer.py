@@ -7,6 +7,7 @@ mlp_forward (src/nn/mlp_block.cpp:378-767):
   h1  = LayerNorm(x)
   qkv = trunc_f(h1 Wqkv)                      public weights, MFMA digit GEMM
   s   = trunc_2f(inv_sqrt * Q_h K_h^T)        Beaver per head, causal rows packed
+                                              (2f as two f-bit truncations)
   p   = Softmax(s)                            suf_amd.softmax.SoftmaxBlock
   c   = trunc_f(P_h V_h), heads merged        Beaver per head
   r1  = trunc_f(c Wout) + x
@@ -153,7 +154,9 @@ class AttentionCore:
         self.maps = {k: dev_i32(mp[k], device) for k in ("gq", "gk", "gv", "gs", "gp", "gc")}
         self.tri_qk = BatchedTriples(dealer, heads, seq, dh, seq, device)
         self.tri_pv = BatchedTriples(dealer, heads, seq, seq, dh, device)
-        self.tr_s = Trunc(dealer, 2 * frac_bits, self.n, prg_state, device=device)
+        # The scores' truncation by 2f as two f-bit table gates (same floor).
+        self.tr_s = [Trunc(dealer, frac_bits, self.n, prg_state, device=device)
+                     for _ in range(2)]
         self.tr_c = Trunc(dealer, frac_bits, seq * d, prg_state, device=device)
         self.softmax = SoftmaxBlock(self.offsets, prg_state, frac_bits, seed=dealer.word() >> 1,
                                     device=device)
@@ -163,6 +166,7 @@ class AttentionCore:
         self.D2 = torch.empty(heads * seq * seq, dtype=torch.int64, device=device)
         self.S = pair(heads * seq * seq, device)
         self.Z = pair(hsd, device)
+        self.sa = pair(self.n, device)
         self.scores = pair(self.n, device)
         self.prob = pair(self.n + 1, device)  # slot n stays 0: the masked entries of P
         for t in self.prob:
@@ -170,7 +174,7 @@ class AttentionCore:
         self.side = torch.cuda.Stream(device=device)
 
     def truncs(self):
-        return [self.tr_s, self.tr_c] + self.softmax.truncs()
+        return self.tr_s + [self.tr_c] + self.softmax.truncs()
 
     def eval2(self, qkv, out, prep=None):
         """prep: (tasks.Prepared, batch) holding the key-only halves of
@@ -187,7 +191,8 @@ class AttentionCore:
         # Masked open of inv_sqrt * S at the packed causal positions, truncation by 2f.
         prep[0].wait(prep[1])
         lin2(operand(term(self.S, index=mp["gs"], mul=self.inv_sqrt)), self.n,
-             into=(self.tr_s, self.scores))
+             into=(self.tr_s[0], self.sa))
+        lin2(operand(term(self.sa)), self.n, into=(self.tr_s[1], self.scores))
         self.softmax.eval2(self.scores, self.prob, prep=prep)
         lin2(operand(term(self.prob, index=mp["gp"]), term(self.tri_pv.A, neg=True)),
              h * seq * seq, xhat=self.D2)

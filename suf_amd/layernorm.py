@@ -6,7 +6,8 @@ src/nn/transformer_layer.cpp:626-760: no gamma/beta, eps = 1/1024,
 invL = llround(2^f / cols), one NR iteration):
 
   mean     mu = trunc_f(invL * sum x)           (row sums, local; one open)
-  var      d = x - mu[row]; q = d * d (Beaver); var = trunc_2f(invL * sum q)
+  var      d = x - mu[row]; q = d * d (Beaver); var = trunc_2f(invL * sum q),
+           as trunc_f(trunc_f(.)) (the same floor, two f-bit table gates)
   rsqrt    v = var + eps; LUT (c0, c1) at v^; y = c0 + trunc_f(c1 v);
            y2 = trunc_f(y y); h = trunc_(f+1)(v y2); y = trunc_f(y (1.5 - h))
   norm     out = trunc_f(d * y[row])            (row-broadcast Beaver)
@@ -48,12 +49,13 @@ class Rsqrt:
     def truncs(self):
         return self.tr
 
-    def eval2(self, v, vhat, out=None):
-        """v: operand of the values; vhat: their masked open with lut.mask.
-        The gate's truncations must have been prepared."""
+    def eval2(self, v, vhat=None, out=None):
+        """v: operand of the values; vhat: their masked open with lut.mask, or
+        None to open them inside the LUT launch.  The gate's truncations must
+        have been prepared."""
         n, f = self.n, self.f
         out = self.y if out is None else out
-        self.lut.eval2(vhat, n, self.coef)
+        self.lut.eval2(vhat, n, self.coef, x=v if vhat is None else None)
         mul2x(operand(term(self.coef, stride=2, off=1)), v, self.tri[0], n,
               into=(self.tr[0], self.t))
         y = operand(term(self.t), term(self.coef, stride=2, off=0))
@@ -85,18 +87,20 @@ class LayerNormBlock:
         self.row_index = dev_i32(row, device)
         self.tr_mean = Trunc(dealer, frac_bits, rows, self.prg_state, device=device)
         self.tri_sq = Triples(dealer, self.n, device=device)
-        self.tr_var = Trunc(dealer, 2 * frac_bits, rows, self.prg_state, device=device)
+        self.tr_var = [Trunc(dealer, frac_bits, rows, self.prg_state, device=device)
+                       for _ in range(2)]
         self.rsqrt = Rsqrt(rows, dealer, self.prg_state, frac_bits, table, rsqrt_iters, device)
         self.tri_norm = Triples(dealer, self.n, row_of=row, device=device)
         self.tr_norm = Trunc(dealer, frac_bits, self.n, self.prg_state, device=device)
         self.side = torch.cuda.Stream(device=device)
         self.mu = pair(rows, device)
         self.sq = pair(self.n, device)
+        self.va = pair(rows, device)
         self.var = pair(rows, device)
         self.rowhat = torch.empty(rows, dtype=torch.int64, device=device)
 
     def truncs(self):
-        return [self.tr_mean, self.tr_var] + self.rsqrt.truncs() + [self.tr_norm]
+        return [self.tr_mean] + self.tr_var + self.rsqrt.truncs() + [self.tr_norm]
 
     def eval2(self, x, out, prep=None):
         """x, out: pairs of int64 [rows * cols] device tensors.  prep:
@@ -111,10 +115,10 @@ class LayerNormBlock:
         diff = operand(term(x), term(self.mu, index=self.row_index, neg=True, length=rows))
         mul2x(diff, diff, self.tri_sq, n, z=self.sq)
         row_sum2(operand(term(self.sq)), rows, cols, mul_const=self.inv_len,
-                 into=(self.tr_var, self.var))
+                 into=(self.tr_var[0], self.va))
+        lin2(operand(term(self.va)), rows, into=(self.tr_var[1], self.var))
         v = operand(term(self.var), const=self.eps_q)
-        lin2(v, rows, xhat=self.rowhat, mask=self.rsqrt.lut.mask)
-        rs = self.rsqrt.eval2(v, self.rowhat)
+        rs = self.rsqrt.eval2(v)
         mul2x(diff, operand(term(rs, index=self.row_index, length=rows)), self.tri_norm, n,
               into=(self.tr_norm, out))
         return out

@@ -89,6 +89,8 @@ _SIGS = {
     "sufhip_mul2x": (c_int, [c_vp, c_sz, c_vp]),
     "sufhip_row_sum2": (c_int, [c_vp, c_int, c_int, c_vp, c_u64, c_vp, c_vp, c_vp, c_u64, c_vp,
                                 c_vp]),
+    "sufhip_interval_lut_eval2": (c_int, [c_vp, c_vp, c_sz, c_int, c_int, c_vp, c_vp, c_u64,
+                                          c_sz, c_vp, c_vp, c_vp]),
     "sufhip_relu_max_round2": (c_int, [c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_int,
                                        c_u64, c_vp, c_vp, c_vp]),
     "sufhip_seed_from_id": (None, [c_u64, c_u64, c_vp]),

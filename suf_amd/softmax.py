@@ -125,13 +125,14 @@ class Recip:
     def truncs(self):
         return self.tr
 
-    def eval2(self, x, xhat, out=None):
-        """x: shares of the values; xhat: their masked open with lut.mask.
-        The gate's truncations must have been prepared."""
+    def eval2(self, x, xhat=None, out=None):
+        """x: shares of the values; xhat: their masked open with lut.mask, or
+        None to open them inside the LUT launch.  The gate's truncations must
+        have been prepared."""
         n, f = self.n, self.f
         out = self.y if out is None else out
-        self.lut.eval2(xhat, n, self.coef)
         xs = operand(term(x))
+        self.lut.eval2(xhat, n, self.coef, x=xs if xhat is None else None)
         mul2x(operand(term(self.coef, stride=2, off=1)), xs, self.tri[0], n,
               into=(self.tr[0], self.t))
         y = operand(term(self.t), term(self.coef, stride=2, off=0))
@@ -186,9 +187,8 @@ class SoftmaxBlock:
             prep = (Prepared(self.side, [self.truncs()]), 0)
         self.rowmax.eval2(x, self.delta)
         self.nexp.eval2(self.delta, self.e, prep=prep)
-        row_sum2(operand(term(self.e)), self.rows, offsets=self.offs_dev, sums=self.s,
-                 hat=self.shat, mask=self.recip.lut.mask)
-        inv = self.recip.eval2(self.s, self.shat)
+        row_sum2(operand(term(self.e)), self.rows, offsets=self.offs_dev, sums=self.s)
+        inv = self.recip.eval2(self.s)
         mul2x(operand(term(self.e)), operand(term(inv, index=self.row_index)), self.tri, self.n,
               into=(self.tr, out))
         return out

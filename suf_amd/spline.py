@@ -10,14 +10,18 @@ Protocol, as SUF runs it for SiLU/GeLU-style gates:
     phase_tasks.hpp:2962-3061):
         m1 = c3 * x; u = m1 + c2 << f; p = u * x; p2 = trunc_f(p);
         q = p2 + c1 << f; r = q * x; y = trunc_2f(r) + c0
-    with three Beaver products and two GapARS truncation gates.
+    with three Beaver products and GapARS truncation gates.  trunc_2f(r) + c0
+    is evaluated as trunc_f(trunc_f(r) + c0 << f): floor(floor(r / 2^f) /
+    2^f) = floor(r / 2^2f) and adding a multiple of 2^f commutes with the
+    shift, so the reconstruction is the same while every gate is an f-bit
+    table gate (one round more, no 2f-bit DCF walk per element).
 The output mask r_out of spline gates is 0 (include/gates/silu_composite.hpp:
 92), so the LUT's coefficient shares are used directly.
 
-Every step runs in libsuf_hip.so: open2_masked, interval_lut_eval, mul2x
-(the first truncation folded into the product's launch as a table lookup),
-trunc_finish2 for the 2f truncation, lin2.  The truncations' key-only
-precomputation runs on a side stream, overlapped with the first rounds.  The
+Every step runs in libsuf_hip.so: interval_lut_eval2 (both parties, the
+masked open of x in the same launch), mul2x and lin2, each truncation folded
+into the launch producing its masked open as a table lookup.  The truncations' key-only precomputation runs on a side
+stream, overlapped with the first rounds.  The
 dealer builds keys with the library's key builders and host std::mt19937_64
 streams.
 """
@@ -137,11 +141,14 @@ class SplineGate:
             t1 = np.stack([a - a0, b - b0, c - c0], axis=1)
             self.triples.append(tuple(torch.from_numpy(t.view(np.int64).copy()).to(device)
                                       for t in (t0, t1)))
-        # Truncation gates: GapARS by f (after the 2nd product) and 2f (after the 3rd).
+        # Truncation gates, all GapARS by f: after the 2nd product, and twice
+        # after the 3rd (the 2f truncation as two f truncations).
         self.trunc = []
-        for j, fb in enumerate((frac_bits, 2 * frac_bits)):
-            rnd = head[2 + j * native.TRUNC_RAND_WORDS: 2 + (j + 1) * native.TRUNC_RAND_WORDS]
-            self.trunc.append(Trunc(None, fb, n, self.prg_state, rnd=rnd, device=device))
+        w3 = pfss.host_mt19937_64(seed + 2000, native.TRUNC_RAND_WORDS)
+        for j in range(3):
+            rnd = head[2 + j * native.TRUNC_RAND_WORDS: 2 + (j + 1) * native.TRUNC_RAND_WORDS] \
+                if j < 2 else w3
+            self.trunc.append(Trunc(None, frac_bits, n, self.prg_state, rnd=rnd, device=device))
         self.side = torch.cuda.Stream(device=device)
         # Scratch for the online phase.
         self.xhat = torch.empty(n, dtype=torch.int64, device=device)
@@ -161,21 +168,21 @@ class SplineGate:
         n, f, s = self.n, self.f, torch.cuda.current_stream().cuda_stream
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
-        native.call("sufhip_open2_masked", _p(x[0]), _p(x[1]), self.rin[0], self.rin[1], n,
-                    _p(self.xhat), s)
-        for p in (0, 1):
-            native.call("sufhip_interval_lut_eval", _p(self.lut[p]), self.lut_key_bytes, 1,
-                        self.intervals, 4, _p(self.xhat), n, _p(self.coef[p]), s)
         xs = operand(term(x))
+        # Both parties' coefficient rows at x^ = x + r_in, opened in the launch.
+        native.call("sufhip_interval_lut_eval2", _p(self.lut[0]), _p(self.lut[1]),
+                    self.lut_key_bytes, self.intervals, 4, native.ctypes.byref(xs), None,
+                    (self.rin[0] + self.rin[1]) & M64, n, _p(self.coef[0]), _p(self.coef[1]), s)
         # u = c3 * x + c2 << f
         mul2x(operand(term(self.coef, stride=4, off=3)), xs, self.tri[0], n, z=self.u,
               z_add=operand(term(self.coef, stride=4, off=2, shift=f)))
         prep[0].wait(prep[1])
-        t1, t2 = self.trunc
+        t1, t2, t3 = self.trunc
         # y = trunc_f(u * x)
         mul2x(operand(term(self.u)), xs, self.tri[1], n, into=(t1, self.y))
-        # y2 = trunc_2f((y + c1 << f) * x); out = y2 + c0
+        # y2 = trunc_f((y + c1 << f) * x); out = trunc_f(y2 + c0 << f)
         mul2x(operand(term(self.y), term(self.coef, stride=4, off=1, shift=f)), xs, self.tri[2],
               n, into=(t2, self.y2))
-        lin2(operand(term(self.y2), term(self.coef, stride=4, off=0)), n, out=out)
+        lin2(operand(term(self.y2), term(self.coef, stride=4, off=0, shift=f)), n,
+             into=(t3, out))
         return out

@@ -322,11 +322,14 @@ class CoeffLut:
             self.keys.append(torch.from_numpy(blob.view(np.int64).copy()).to(device)
                              .view(torch.uint8))
 
-    def eval2(self, xhat, n, out):
-        """out: pair of int64 [n * words] tensors (AoS rows)."""
-        for p in (0, 1):
-            native.call("sufhip_interval_lut_eval", ptr(self.keys[p]), self.key_bytes, 1,
-                        self.intervals, self.words, ptr(xhat), n, ptr(out[p]), stream_ptr())
+    def eval2(self, xhat, n, out, x=None):
+        """Both parties' rows at the masked open: xhat (device tensor), or
+        with x (an operand) at x_0 + x_1 + mask computed in the same launch.
+        out: pair of int64 [n * words] tensors (AoS rows)."""
+        native.call("sufhip_interval_lut_eval2", ptr(self.keys[0]), ptr(self.keys[1]),
+                    self.key_bytes, self.intervals, self.words,
+                    native.ctypes.byref(x) if x is not None else None, ptr(xhat),
+                    self.mask & M64, n, ptr(out[0]), ptr(out[1]), stream_ptr())
 
 
 def relu_coeffs_for(r_in):

@@ -139,12 +139,13 @@ def spline2(prg, gate, x, idx0=0, sl=None):
     m1 = mul([C[0][:, 3], C[1][:, 3]], [x0, x1], tri[0])
     m1 = [m1[p] + (C[p][:, 2] << sh) for p in (0, 1)]
     pz = mul(m1, [x0, x1], tri[1])
-    t1, t2 = gate.trunc
+    t1, t2, t3 = gate.trunc
     y = trunc2(prg, t1, open2(pz, t1.mask))
     q = [y[p] + (C[p][:, 1] << sh) for p in (0, 1)]
     rz = mul(q, [x0, x1], tri[2])
     y2 = trunc2(prg, t2, open2(rz, t2.mask))
-    return [(y2[p] + C[p][:, 0]).astype(np.uint64) for p in (0, 1)]
+    z3 = [(y2[p] + (C[p][:, 0] << sh)).astype(np.uint64) for p in (0, 1)]
+    return trunc2(prg, t3, open2(z3, t3.mask))
 
 
 def softmax2(prg, sm, x):
@@ -171,7 +172,8 @@ def layernorm2(prg, ln, x):
     sq = beaver2(diff, diff, ln.tri_sq)
     vs = [(ol.row_sum(sq[p], rows, cols) * np.uint64(ln.inv_len)).astype(np.uint64)
           for p in (0, 1)]
-    var = trunc2(prg, ln.tr_var, open2(vs, ln.tr_var.mask))
+    va = trunc2(prg, ln.tr_var[0], open2(vs, ln.tr_var[0].mask))
+    var = trunc2(prg, ln.tr_var[1], open2(va, ln.tr_var[1].mask))
     v = const2(var, ln.eps_q)
     rs = rsqrt2(prg, ln.rsqrt, v, open2(v, ln.rsqrt.lut.mask))
     return beaver_trunc2(prg, diff, rs, ln.tri_norm, ln.tr_norm, row_of=row)
