@@ -366,6 +366,43 @@ int sufhip_interval_lut_eval2(const uint8_t* d_key0, const uint8_t* d_key1, size
                               const uint64_t* d_xhat, uint64_t mask, size_t n, uint64_t* d_out0,
                               uint64_t* d_out1, void* stream);
 
+/* A whole elementwise gate chain for both parties in one launch: the
+ * coefficient LUT at the masked open of x, every Beaver product (opens
+ * summed in registers) and every truncation (table gates, f-bit, the
+ * rsqrt's third f + 1), per element.  The shares equal those of the
+ * round-by-round evaluation with the same material.
+ *   SUFHIP_CHAIN_CUBIC  CubicPolyTask (include/runtime/phase_tasks.hpp:
+ *     2718-3066), 4-word LUT (c0..c3), 3 products, 3 truncations:
+ *     y = tr((c3 x + c2 << f) x); y2 = tr((y + c1 << f) x); out = tr(y2 + c0 << f)
+ *   SUFHIP_CHAIN_RECIP  RecipTask with one NR step (phase_tasks.hpp:3140-3653),
+ *     2-word LUT (c0, c1): y = tr(c1 x) + c0; out = tr(y (2 << f - tr(y x)))
+ *   SUFHIP_CHAIN_RSQRT  RsqrtTask with one NR step (phase_tasks.hpp:1383-1700),
+ *     2-word LUT: y = tr(c1 x) + c0; y2 = tr(y y); h = tr_(f+1)(x y2);
+ *     out = tr(y (3 << (f - 1) - h))  (4 products, 4 truncations)
+ * a / b / c: the products' triple shares as terms (shift 0); trunc[k]: the
+ * truncation gates in order (y ignored), trunc_mask[k] their masks;
+ * frac_bits in [1, 13]; intervals <= 64. */
+#define SUFHIP_CHAIN_CUBIC 0
+#define SUFHIP_CHAIN_RECIP 1
+#define SUFHIP_CHAIN_RSQRT 2
+typedef struct sufhip_chain2_args {
+  int kind;
+  int frac_bits;
+  size_t n;
+  sufhip_operand2 x;
+  const uint8_t* lut[2];
+  size_t lut_key_bytes;
+  int intervals;
+  uint64_t lut_mask;
+  sufhip_term2 a[4];
+  sufhip_term2 b[4];
+  sufhip_term2 c[4];
+  sufhip_trunc_epilogue trunc[4];
+  uint64_t trunc_mask[4];
+  uint64_t* out[2];
+} sufhip_chain2_args;
+int sufhip_gate_chain2(const sufhip_chain2_args* args, void* stream);
+
 /* One pairwise-max round of RowMaxDiffTask (include/nn/row_maxdiff_task.hpp:
  * 49-150), max(a, b) = b + ReLU(a - b), for both parties.  For output slot j:
  *   src_b[j] < 0: next_p[j] = cur_p[src_a[j]] (odd element carried);

@@ -23,9 +23,9 @@ producing their masked open.  Randomness: suf_amd.tasks.Dealer(seed).
 import numpy as np
 import torch
 
-from . import tables
-from .tasks import (CoeffLut, Dealer, Prepared, Triples, Trunc, dev_i32, lin2, mul2x, operand,
-                    pair, row_sum2, term)
+from . import native, tables
+from .tasks import (CoeffLut, Dealer, Prepared, Triples, Trunc, chain2, dev_i32, lin2, mul2x,
+                    operand, pair, row_sum2, term)
 
 
 class Rsqrt:
@@ -49,12 +49,17 @@ class Rsqrt:
     def truncs(self):
         return self.tr
 
-    def eval2(self, v, vhat=None, out=None):
+    def eval2(self, v, vhat=None, out=None, fused=True):
         """v: operand of the values; vhat: their masked open with lut.mask, or
         None to open them inside the LUT launch.  The gate's truncations must
-        have been prepared."""
+        have been prepared.  fused (one NR step, no vhat): the whole chain in
+        one launch."""
         n, f = self.n, self.f
         out = self.y if out is None else out
+        if fused and self.iters == 1 and vhat is None:
+            chain2(native.CHAIN_RSQRT, f, v, n, self.lut.keys, self.lut.key_bytes,
+                   self.lut.intervals, self.lut.mask, self.tri, self.tr, out)
+            return out
         self.lut.eval2(vhat, n, self.coef, x=v if vhat is None else None)
         mul2x(operand(term(self.coef, stride=2, off=1)), v, self.tri[0], n,
               into=(self.tr[0], self.t))

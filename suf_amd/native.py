@@ -23,6 +23,9 @@ TRUNC_TR = 0
 TRUNC_ARS = 1
 TRUNC_GAPARS = 2
 TRUNC_RAND_WORDS = 19
+CHAIN_CUBIC = 0
+CHAIN_RECIP = 1
+CHAIN_RSQRT = 2
 
 c_int = ctypes.c_int
 c_sz = ctypes.c_size_t
@@ -91,6 +94,7 @@ _SIGS = {
                                 c_vp]),
     "sufhip_interval_lut_eval2": (c_int, [c_vp, c_vp, c_sz, c_int, c_int, c_vp, c_vp, c_u64,
                                           c_sz, c_vp, c_vp, c_vp]),
+    "sufhip_gate_chain2": (c_int, [c_vp, c_vp]),
     "sufhip_relu_max_round2": (c_int, [c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_int,
                                        c_u64, c_vp, c_vp, c_vp]),
     "sufhip_seed_from_id": (None, [c_u64, c_u64, c_vp]),
@@ -166,6 +170,14 @@ class TruncEpilogue(ctypes.Structure):
     """sufhip_trunc_epilogue (include/suf_hip.h)."""
     _fields_ = [("key", c_vp * 2), ("table", c_vp * 2), ("work_bytes", c_sz),
                 ("frac_bits", c_int), ("y", c_vp * 2)]
+
+
+class Chain2Args(ctypes.Structure):
+    """sufhip_chain2_args (include/suf_hip.h)."""
+    _fields_ = [("kind", c_int), ("frac_bits", c_int), ("n", c_sz), ("x", Operand2),
+                ("lut", c_vp * 2), ("lut_key_bytes", c_sz), ("intervals", c_int),
+                ("lut_mask", c_u64), ("a", Term2 * 4), ("b", Term2 * 4), ("c", Term2 * 4),
+                ("trunc", TruncEpilogue * 4), ("trunc_mask", c_u64 * 4), ("out", c_vp * 2)]
 
 
 class TruncJob(ctypes.Structure):

@@ -26,8 +26,8 @@ import numpy as np
 import torch
 
 from . import native, spline, tables
-from .tasks import (RELU_ALPHA, CoeffLut, Dealer, Prepared, Triples, Trunc, dev_i32, lin2,
-                    mul2x, operand, pair, relu_coeffs_for, row_sum2, stream_ptr, term)
+from .tasks import (RELU_ALPHA, CoeffLut, Dealer, Prepared, Triples, Trunc, chain2, dev_i32,
+                    lin2, mul2x, operand, pair, relu_coeffs_for, row_sum2, stream_ptr, term)
 
 
 def causal_offsets(heads, seq):
@@ -125,13 +125,18 @@ class Recip:
     def truncs(self):
         return self.tr
 
-    def eval2(self, x, xhat=None, out=None):
+    def eval2(self, x, xhat=None, out=None, fused=True):
         """x: shares of the values; xhat: their masked open with lut.mask, or
         None to open them inside the LUT launch.  The gate's truncations must
-        have been prepared."""
+        have been prepared.  fused (one NR step, no xhat): the whole chain in
+        one launch."""
         n, f = self.n, self.f
         out = self.y if out is None else out
         xs = operand(term(x))
+        if fused and self.iters == 1 and xhat is None:
+            chain2(native.CHAIN_RECIP, f, xs, n, self.lut.keys, self.lut.key_bytes,
+                   self.lut.intervals, self.lut.mask, self.tri, self.tr, out)
+            return out
         self.lut.eval2(xhat, n, self.coef, x=xs if xhat is None else None)
         mul2x(operand(term(self.coef, stride=2, off=1)), xs, self.tri[0], n,
               into=(self.tr[0], self.t))

@@ -18,9 +18,11 @@ Protocol, as SUF runs it for SiLU/GeLU-style gates:
 The output mask r_out of spline gates is 0 (include/gates/silu_composite.hpp:
 92), so the LUT's coefficient shares are used directly.
 
-Every step runs in libsuf_hip.so: interval_lut_eval2 (both parties, the
-masked open of x in the same launch), mul2x and lin2, each truncation folded
-into the launch producing its masked open as a table lookup.  The truncations' key-only precomputation runs on a side
+Every step runs in libsuf_hip.so: by default the whole chain in one launch
+(sufhip_gate_chain2: LUT, products and table truncations per element, both
+parties); round by round, interval_lut_eval2 (the open of x in the same
+launch), mul2x and lin2, each truncation folded into the launch producing its
+masked open.  The truncations' key-only precomputation runs on a side
 stream, overlapped with the first rounds.  The
 dealer builds keys with the library's key builders and host std::mt19937_64
 streams.
@@ -29,7 +31,7 @@ import numpy as np
 import torch
 
 from . import native, pfss
-from .tasks import AosTriples, Prepared, Trunc, lin2, mul2x, operand, term
+from .tasks import AosTriples, Prepared, Trunc, chain2, lin2, mul2x, operand, term
 
 M64 = (1 << 64) - 1
 LUT_TWEAK = 7  # seed_from_id tweak of interval LUT keys (cuda/pfss_backend_gpu.cu:508-515)
@@ -161,13 +163,19 @@ class SplineGate:
     def truncs(self):
         return list(self.trunc)
 
-    def eval2(self, x, out, prep=None):
+    def eval2(self, x, out, prep=None, fused=True):
         """x, out: pairs of int64[n] device tensors (party 0, party 1 shares).
         prep: (tasks.Prepared, batch) holding this gate's key-only halves, or
-        None to issue them here on the gate's side stream."""
+        None to issue them here on the gate's side stream.  fused: the whole
+        chain in one launch (sufhip_gate_chain2); else round by round."""
         n, f, s = self.n, self.f, torch.cuda.current_stream().cuda_stream
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
+        if fused:
+            prep[0].wait(prep[1])
+            chain2(native.CHAIN_CUBIC, f, operand(term(x)), n, self.lut, self.lut_key_bytes,
+                   self.intervals, self.rin[0] + self.rin[1], self.tri, self.trunc, out)
+            return out
         xs = operand(term(x))
         # Both parties' coefficient rows at x^ = x + r_in, opened in the launch.
         native.call("sufhip_interval_lut_eval2", _p(self.lut[0]), _p(self.lut[1]),

@@ -376,3 +376,22 @@ class AosTriples:
     def terms(self):
         return (term(self.t, stride=3, off=0), term(self.t, stride=3, off=1),
                 term(self.t, stride=3, off=2))
+
+
+def chain2(kind, f, x, n, lut_keys, lut_key_bytes, intervals, lut_mask, triples, truncs, out):
+    """A whole elementwise gate chain (sufhip_gate_chain2) for both parties:
+    kind native.CHAIN_*, x the input operand, lut_keys both parties' LUT
+    blobs, triples / truncs the chain's products and truncation gates in
+    order, out the output pair."""
+    a = native.Chain2Args()
+    a.kind, a.frac_bits, a.n = kind, f, n
+    a.x = x
+    a.lut[0], a.lut[1] = ptr(lut_keys[0]), ptr(lut_keys[1])
+    a.lut_key_bytes, a.intervals, a.lut_mask = lut_key_bytes, intervals, lut_mask & M64
+    for k, t in enumerate(triples):
+        a.a[k], a.b[k], a.c[k] = t.terms()
+    for k, tr in enumerate(truncs):
+        a.trunc[k] = tr.epilogue(out)
+        a.trunc_mask[k] = tr.mask & M64
+    a.out[0], a.out[1] = ptr(out[0]), ptr(out[1])
+    native.call("sufhip_gate_chain2", native.ctypes.byref(a), stream_ptr())

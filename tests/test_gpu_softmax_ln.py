@@ -101,6 +101,45 @@ def test_recip_shares_and_closed_form():
     assert np.array_equal((g[0] + g[1]).astype(np.uint64), want)
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_recip_chain_fused_and_by_rounds(fused):
+    """The one-launch chain and the round-by-round path (LUT opened in its
+    own launch) give the oracle's shares."""
+    n = 257
+    s = ((np.arange(n, dtype=np.int64) * 7919 + 4096) % (300 << F)).astype(np.uint64)
+    s0, s1 = _share(s, 32)
+    say("recip chain fused=%s n=%d" % (fused, n))
+    rc = softmax.Recip(n, softmax.Dealer(19), STATE, F)
+    for tr in rc.truncs():
+        tr.prepare()
+    out = rc.eval2(_pair_dev(s0, s1), None, fused=fused)
+    g = [u64(out[0]), u64(out[1])]
+    shat = (s + np.uint64(rc.lut.mask)).astype(np.uint64)
+    o = tp.recip2(ol.Prg(STATE), rc, [s0, s1], shat)
+    assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_rsqrt_chain_fused_and_by_rounds(fused):
+    from suf_amd.tasks import operand, term
+    n = 300
+    v = ((np.arange(n, dtype=np.int64) * 613 + 3) % (17 << F)).astype(np.uint64)
+    v0, v1 = _share(v, 42)
+    say("rsqrt chain fused=%s n=%d" % (fused, n))
+    rs = layernorm.Rsqrt(n, softmax.Dealer(20), STATE, F)
+    for tr in rs.truncs():
+        tr.prepare()
+    eps = 4
+    vp = _pair_dev(v0, v1)
+    out = rs.eval2(operand(term(vp), const=eps), None, fused=fused)
+    g = [u64(out[0]), u64(out[1])]
+    ve = [(v0 + np.uint64(eps)).astype(np.uint64), v1]
+    o = tp.rsqrt2(ol.Prg(STATE), rs, ve, tp.open2(ve, rs.lut.mask))
+    assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
+    want = fp.rsqrt_task(rs.table[0], rs.table[1], (v + np.uint64(eps)).astype(np.uint64), F)
+    assert np.array_equal((g[0] + g[1]).astype(np.uint64), want.view(np.uint64))
+
+
 def test_rsqrt_shares_and_closed_form():
     n = 200
     v = (np.arange(n, dtype=np.int64) * 331 + 1) % (20 << F)

@@ -33,8 +33,9 @@ def _oracle_pipeline(gate, x0, x1):
     return tp.spline2(ol.Prg(STATE), gate, [x0, x1])
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("n,seed", [(3000, 7), (777, 8)])
-def test_shares_match_oracle_pipeline(n, seed):
+def test_shares_match_oracle_pipeline(n, seed, fused):
     alpha, coeffs = spline.spline_spec(F, seed=6)
     x = pfss.host_normal_fixed(5 + seed, 3.0, 8.0, F, n)
     x[:6] = np.array([0, 8 << F, (-8 << F) & spline.M64, 1, spline.M64, (3 << F) - 1],
@@ -43,7 +44,7 @@ def test_shares_match_oracle_pipeline(n, seed):
     say("spline gate n=%d seed=%d" % (n, seed))
     gate = spline.SplineGate(n, alpha, coeffs, STATE, F, seed=seed)
     out = [torch.empty(n, dtype=torch.int64, device="cuda") for _ in range(2)]
-    gate.eval2([dev(x0), dev(x1)], out)
+    gate.eval2([dev(x0), dev(x1)], out, fused=fused)
     g = [u64(o) for o in out]
     o = _oracle_pipeline(gate, x0, x1)
     assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
