@@ -403,6 +403,25 @@ typedef struct sufhip_chain2_args {
 } sufhip_chain2_args;
 int sufhip_gate_chain2(const sufhip_chain2_args* args, void* stream);
 
+/* RowMaxDiffTask whole (include/nn/row_maxdiff_task.hpp:49-165) for both
+ * parties in one launch: every round of the pairwise-max tree over the packed
+ * rows [d_row_offsets[r], d_row_offsets[r+1]) (1 <= length <= max_row <= 512,
+ * 2^rounds >= max_row), then d_delta_p[i] = max_p(row) - x_p[i].  Round k
+ * uses keys[k] (both parties' ReLU LUT blobs, as sufhip_relu_max_round2)
+ * and counts its LUT slots like the per-round evaluation:
+ * d_round_offsets[k * rows + r] = the row's first output slot in round k.
+ * Same shares as the per-round kernels followed by the delta step. */
+typedef struct sufhip_relu_round_key {
+  const uint8_t* key[2];
+  size_t key_bytes;
+  int intervals; /* <= 8 */
+  uint64_t mask;
+} sufhip_relu_round_key;
+int sufhip_relu_max_tree2(const uint64_t* d_x0, const uint64_t* d_x1, int rows,
+                          const int32_t* d_row_offsets, int max_row, int rounds,
+                          const int32_t* d_round_offsets, const sufhip_relu_round_key* keys,
+                          uint64_t* d_delta0, uint64_t* d_delta1, void* stream);
+
 /* One pairwise-max round of RowMaxDiffTask (include/nn/row_maxdiff_task.hpp:
  * 49-150), max(a, b) = b + ReLU(a - b), for both parties.  For output slot j:
  *   src_b[j] < 0: next_p[j] = cur_p[src_a[j]] (odd element carried);
@@ -540,13 +559,16 @@ int sufhip_beaver_matmul2d_batched(int party, const uint64_t* d_D_open, const ui
  * cuda_primitives.hpp:149-150): for batch b and party p,
  *   out_p[b] = C_p[b] + D[b] * B_p[b] + A_p[b] * E[b] (+ D[b] * E[b] for p = 0)
  * with D [b][M x K], E [b][K x N], A_p [b][M x K], B_p [b][K x N],
- * C_p and out_p [b][M x N], row-major, mod 2^64. */
+ * C_p and out_p [b][M x N], row-major, mod 2^64.  Small launches split the
+ * 2K inner dimension over slices summed by a second pass: d_work of
+ * sufhip_beaver_matmul2_batched_work_bytes() bytes (0: none needed). */
+size_t sufhip_beaver_matmul2_batched_work_bytes(int batches, int M, int K, int N);
 int sufhip_beaver_matmul2_batched(const uint64_t* d_D_open, const uint64_t* d_E_open,
                                   const uint64_t* d_A0, const uint64_t* d_A1,
                                   const uint64_t* d_B0, const uint64_t* d_B1,
                                   const uint64_t* d_C0, const uint64_t* d_C1, int batches, int M,
-                                  int K, int N, uint64_t* d_out0, uint64_t* d_out1,
-                                  void* stream);
+                                  int K, int N, uint64_t* d_out0, uint64_t* d_out1, void* d_work,
+                                  size_t work_bytes, void* stream);
 
 /* Share x public weight for both parties (nn::matmul_publicW_gpu,
  * src/nn/matmul_gpu.cu:388-720; CPU form src/nn/matmul_publicW.cpp:17-36):

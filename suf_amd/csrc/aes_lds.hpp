@@ -347,12 +347,18 @@ struct AesLds4 {
 };
 
 // Cooperative fill of the replicated table from the constant T table in
-// global memory (`tsrc`, 256 words).  Must be followed by __syncthreads().
+// global memory (`tsrc`, 256 words): one word load per four copies, written
+// as one 16-byte LDS store.  `lds` must be 16-byte aligned.  Must be followed
+// by __syncthreads().
 template <int kCopies>
 __device__ __forceinline__ void fill_ttable(uint32_t* lds, const uint32_t* tsrc) {
+  static_assert(kCopies % 4 == 0, "fill_ttable: copies in groups of four");
+  constexpr int kVec = kCopies / 4;
+  uint4* dst = reinterpret_cast<uint4*>(lds);
   const int nthreads = blockDim.x;
-  for (int i = threadIdx.x; i < 256 * kCopies; i += nthreads) {
-    lds[i] = tsrc[i / kCopies];
+  for (int i = threadIdx.x; i < 256 * kVec; i += nthreads) {
+    const uint32_t v = tsrc[i / kVec];
+    dst[i] = make_uint4(v, v, v, v);
   }
 }
 

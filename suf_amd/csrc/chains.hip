@@ -78,7 +78,7 @@ __device__ __forceinline__ Two trunc(const ChainArgs& A, int j, Two z) {
 template <int kKind>
 __global__ void __launch_bounds__(kBlock) gate_chain_kernel(ChainArgs A) {
   constexpr int W = kKind == SUFHIP_CHAIN_CUBIC ? 4 : 2;
-  __shared__ uint32_t tab[256 * kCopies];
+  __shared__ __align__(16) uint32_t tab[256 * kCopies];
   __shared__ uint4 rk[2][11];
   __shared__ uint64_t cuts[2][kMaxIntervals];
   __shared__ uint64_t pay[2][kMaxIntervals * kMaxWords];

@@ -46,6 +46,12 @@ struct MmArgs {
   const uint64_t* B2[2];
   const uint64_t* C2[2];
   uint64_t* out2[2];
+  // Two-party form with ksplit > 1: grid.z = (2 * batch + party) * ksplit +
+  // slice; slice s sums its share of the 2K inner dimension into
+  // part[s][party][batch] (no C), and reduce2_kernel adds C and the slices.
+  int ksplit;
+  uint64_t* part;
+  int batches;
 };
 
 __device__ __forceinline__ uint64_t scaled(uint64_t acc, const MmArgs& a) {
@@ -69,8 +75,11 @@ __global__ void __launch_bounds__(kMmThreads) beaver_matmul_kernel(MmArgs a) {
   const int tx = tid & 15, ty = tid >> 4;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int M = a.M, K = a.K, N = a.N;
-  const int party = a.two_party ? int(blockIdx.z & 1) : a.party;
-  const size_t b = a.two_party ? blockIdx.z >> 1 : blockIdx.z;
+  const int ks = a.two_party ? a.ksplit : 1;
+  const int slice = int(blockIdx.z) % ks;
+  const int bz = int(blockIdx.z) / ks;
+  const int party = a.two_party ? (bz & 1) : a.party;
+  const size_t b = a.two_party ? size_t(bz >> 1) : blockIdx.z;
   const uint64_t* D = a.D + b * size_t(M) * K;
   const uint64_t* E = a.E + b * size_t(K) * N;
   // Triple shares and output of this (batch, party): shared by every batch
@@ -92,7 +101,9 @@ __global__ void __launch_bounds__(kMmThreads) beaver_matmul_kernel(MmArgs a) {
     }
 
   const int K2 = 2 * K;
-  for (int k0 = 0; k0 < K2; k0 += BK) {
+  const int steps = (K2 + BK - 1) / BK;
+  const int k_first = BK * (steps * slice / ks), k_last = BK * (steps * (slice + 1) / ks);
+  for (int k0 = k_first; k0 < k_last; k0 += BK) {
     // LHS tile: 32 rows x 16 k = 512 values, 2 per lane.  k < K reads D, else A.
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -159,10 +170,40 @@ __global__ void __launch_bounds__(kMmThreads) beaver_matmul_kernel(MmArgs a) {
       const int gn = n0 + 4 * tx + j;
       if (gn >= N) continue;
       const size_t o = size_t(gm) * N + gn;
+      if (ks > 1) {
+        a.part[((size_t(slice) * 2 + party) * a.batches + b) * size_t(M) * N + o] =
+            acc[i][j] + (uint64_t(hi[i][j]) << 32);
+        continue;
+      }
       const uint64_t v = TC[o] + acc[i][j] + (uint64_t(hi[i][j]) << 32);
       OUT[o] = scaled(v, a);
     }
   }
+}
+
+// out_p = C_p + sum over slices of part[slice][p] (two-party k-split).
+__global__ void __launch_bounds__(256)
+    reduce2_kernel(const uint64_t* part, int ksplit, size_t per_party, const uint64_t* C0,
+                   const uint64_t* C1, uint64_t* out0, uint64_t* out1) {
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < 2 * per_party;
+       i += size_t(gridDim.x) * 256) {
+    const int p = i < per_party ? 0 : 1;
+    const size_t j = i - size_t(p) * per_party;
+    uint64_t v = p == 0 ? C0[j] : C1[j];
+    for (int s = 0; s < ksplit; ++s) v += part[(size_t(s) * 2 + p) * per_party + j];
+    (p == 0 ? out0 : out1)[j] = v;
+  }
+}
+
+// Slices of the 2K inner dimension for the two-party form: about 512
+// workgroups per launch, at most 8 slices, at least one 16-deep step each.
+int ksplit_for(int batches, int M, int K, int N) {
+  const long base = long((N + BN - 1) / BN) * ((M + BM - 1) / BM) * 2 * batches;
+  const int steps = (2 * K + BK - 1) / BK;
+  long s = base >= 512 ? 1 : (512 + base - 1) / base;
+  if (s > 8) s = 8;
+  if (s > steps) s = steps;
+  return int(s);
 }
 
 int launch(int party, const uint64_t* D, const uint64_t* E, const uint64_t* A, const uint64_t* B,
@@ -173,7 +214,8 @@ int launch(int party, const uint64_t* D, const uint64_t* E, const uint64_t* A, c
   SUFHIP_REQUIRE(batches <= 65535, "sufhip_beaver_matmul2d: at most 65535 batches");
   SUFHIP_REQUIRE(size_t(K) * 2 < (size_t(1) << 31), "sufhip_beaver_matmul2d: K too large");
   MmArgs a{D, E, A, B, C, out, M, K, N, party, has_scale, mul_const, mul_shift, 0,
-           {nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}};
+           {nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr},
+           1, nullptr, batches};
   const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, batches), block(kMmThreads);
   if (w_transposed)
     hipLaunchKernelGGL(beaver_matmul_kernel<true>, grid, block, 0, as_stream(stream), a);
@@ -182,19 +224,38 @@ int launch(int party, const uint64_t* D, const uint64_t* E, const uint64_t* A, c
   return check_launch("beaver_matmul_kernel");
 }
 
+size_t work2_bytes(int batches, int M, int K, int N) {
+  if (batches <= 0 || M <= 0 || K <= 0 || N <= 0) return 0;
+  const int ks = ksplit_for(batches, M, K, N);
+  return ks > 1 ? size_t(ks) * 2 * size_t(batches) * M * N * 8 : 0;
+}
+
 int launch2(const uint64_t* D, const uint64_t* E, const uint64_t* A0, const uint64_t* A1,
             const uint64_t* B0, const uint64_t* B1, const uint64_t* C0, const uint64_t* C1,
-            int batches, int M, int K, int N, uint64_t* out0, uint64_t* out1, void* stream) {
+            int batches, int M, int K, int N, uint64_t* out0, uint64_t* out1, void* work,
+            size_t work_bytes, void* stream) {
   if (batches <= 0 || M <= 0 || K <= 0 || N <= 0) return SUFHIP_OK;
   SUFHIP_REQUIRE(D && E && A0 && A1 && B0 && B1 && C0 && C1 && out0 && out1,
                  "sufhip_beaver_matmul2_batched: null pointer");
-  SUFHIP_REQUIRE(batches <= 32767, "sufhip_beaver_matmul2_batched: at most 32767 batches");
+  SUFHIP_REQUIRE(batches <= 4095, "sufhip_beaver_matmul2_batched: at most 4095 batches");
   SUFHIP_REQUIRE(size_t(K) * 2 < (size_t(1) << 31), "sufhip_beaver_matmul2_batched: K too large");
+  const int ks = ksplit_for(batches, M, K, N);
+  const size_t need = work2_bytes(batches, M, K, N);
+  SUFHIP_REQUIRE(work_bytes >= need && (need == 0 || work),
+                 "sufhip_beaver_matmul2_batched: workspace smaller than its work bytes");
   MmArgs a{D, E, nullptr, nullptr, nullptr, nullptr, M, K, N, 0, 0, 0, 0, 1,
-           {A0, A1}, {B0, B1}, {C0, C1}, {out0, out1}};
-  const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, 2 * batches), block(kMmThreads);
+           {A0, A1}, {B0, B1}, {C0, C1}, {out0, out1}, ks, static_cast<uint64_t*>(work),
+           batches};
+  const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, 2 * batches * ks), block(kMmThreads);
   hipLaunchKernelGGL(beaver_matmul_kernel<false>, grid, block, 0, as_stream(stream), a);
-  return check_launch("beaver_matmul_kernel (two-party)");
+  if (int rc = check_launch("beaver_matmul_kernel (two-party)")) return rc;
+  if (ks == 1) return SUFHIP_OK;
+  const size_t per_party = size_t(batches) * M * N;
+  size_t g = (2 * per_party + 255) / 256;
+  if (g > 4096) g = 4096;
+  hipLaunchKernelGGL(reduce2_kernel, dim3(unsigned(g)), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint64_t*>(work), ks, per_party, C0, C1, out0, out1);
+  return check_launch("reduce2_kernel");
 }
 
 }  // namespace
@@ -222,14 +283,18 @@ int sufhip_beaver_matmul2d_batched(int party, const uint64_t* d_D_open, const ui
                 K, N, w_transposed, has_scale, mul_const, mul_shift, d_out, stream);
 }
 
+size_t sufhip_beaver_matmul2_batched_work_bytes(int batches, int M, int K, int N) {
+  return work2_bytes(batches, M, K, N);
+}
+
 int sufhip_beaver_matmul2_batched(const uint64_t* d_D_open, const uint64_t* d_E_open,
                                    const uint64_t* d_A0, const uint64_t* d_A1,
                                    const uint64_t* d_B0, const uint64_t* d_B1,
                                    const uint64_t* d_C0, const uint64_t* d_C1, int batches, int M,
-                                   int K, int N, uint64_t* d_out0, uint64_t* d_out1,
-                                   void* stream) {
+                                   int K, int N, uint64_t* d_out0, uint64_t* d_out1, void* d_work,
+                                   size_t work_bytes, void* stream) {
   return launch2(d_D_open, d_E_open, d_A0, d_A1, d_B0, d_B1, d_C0, d_C1, batches, M, K, N, d_out0,
-                 d_out1, stream);
+                 d_out1, d_work, work_bytes, stream);
 }
 
 }  // extern "C"

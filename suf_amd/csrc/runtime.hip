@@ -36,7 +36,7 @@ constexpr int kCtrCopies = 32;
 __global__ void __launch_bounds__(256) aes128_ctr_kernel(uint8_t* __restrict__ out,
                                                          RoundKeys rk, uint64_t ctr_lo,
                                                          uint64_t ctr_hi, size_t blocks) {
-  __shared__ uint32_t lds[256 * kCtrCopies];
+  __shared__ __align__(16) uint32_t lds[256 * kCtrCopies];
   __shared__ uint4 rkl[11];
   fill_ttable<kCtrCopies>(lds, kTDev.v);
   fill_round_keys(rkl, &rk.w, 1);
@@ -56,7 +56,7 @@ __global__ void __launch_bounds__(256) aes128_ctr_kernel(uint8_t* __restrict__ o
 __global__ void __launch_bounds__(256) prg_mmo_kernel(PrgKeys keys, int out_blocks,
                                                       const uint8_t* __restrict__ seeds,
                                                       uint8_t* __restrict__ out, size_t n) {
-  __shared__ uint32_t lds[256 * kCtrCopies];
+  __shared__ __align__(16) uint32_t lds[256 * kCtrCopies];
   __shared__ uint4 rkl[kPrgMaxBlocks * 11];
   fill_ttable<kCtrCopies>(lds, kTDev.v);
   fill_round_keys(rkl, keys.rk, kPrgMaxBlocks);

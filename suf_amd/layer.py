@@ -84,9 +84,13 @@ class PublicMatmulTrunc:
 
 class BatchedTriples:
     """Beaver matrix triples per batch: A [b][M x K], B [b][K x N] uniform,
-    C = A B mod 2^64; party 0 holds the drawn shares."""
+    C = A B mod 2^64; party 0 holds the drawn shares.  Also holds the
+    product's k-split workspace."""
 
     def __init__(self, dealer, batches, M, K, N, device="cuda"):
+        wb = native.load().sufhip_beaver_matmul2_batched_work_bytes(batches, M, K, N)
+        self.work = torch.empty(max(2, (wb + 15) // 8), dtype=torch.int64, device=device)
+        self.work_bytes = self.work.numel() * 8
         A = dealer.words(batches * M * K).reshape(batches, M, K)
         B = dealer.words(batches * K * N).reshape(batches, K, N)
         C = np.matmul(A, B)  # uint64: exact mod 2^64
@@ -102,7 +106,7 @@ class BatchedTriples:
 def _beaver_batched(D, E, tri, batches, M, K, N, out):
     native.call("sufhip_beaver_matmul2_batched", ptr(D), ptr(E), ptr(tri.A[0]), ptr(tri.A[1]),
                 ptr(tri.B[0]), ptr(tri.B[1]), ptr(tri.C[0]), ptr(tri.C[1]), batches, M, K, N,
-                ptr(out[0]), ptr(out[1]), stream_ptr())
+                ptr(out[0]), ptr(out[1]), ptr(tri.work), tri.work_bytes, stream_ptr())
 
 
 def attention_maps(seq, d, heads):

@@ -78,8 +78,10 @@ _SIGS = {
     "sufhip_mul2": (c_int, [c_vp, c_sz, c_vp]),
     "sufhip_add_shifted": (c_int, [c_vp, c_vp, c_sz, c_sz, c_int, c_sz, c_vp, c_vp]),
     "sufhip_lin2": (c_int, [c_vp, c_sz, c_vp, c_vp, c_vp, c_u64, c_vp, c_vp]),
+    "sufhip_beaver_matmul2_batched_work_bytes": (c_sz, [c_int, c_int, c_int, c_int]),
     "sufhip_beaver_matmul2_batched": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
-                                              c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp]),
+                                              c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_sz,
+                                              c_vp]),
     "sufhip_public_w_digits": (c_int, [c_vp, c_sz]),
     "sufhip_public_w_planes_bytes": (c_sz, [c_int, c_int, c_int]),
     "sufhip_public_w_prepare": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp]),
@@ -95,6 +97,8 @@ _SIGS = {
     "sufhip_interval_lut_eval2": (c_int, [c_vp, c_vp, c_sz, c_int, c_int, c_vp, c_vp, c_u64,
                                           c_sz, c_vp, c_vp, c_vp]),
     "sufhip_gate_chain2": (c_int, [c_vp, c_vp]),
+    "sufhip_relu_max_tree2": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_vp, c_vp,
+                                      c_vp, c_vp]),
     "sufhip_relu_max_round2": (c_int, [c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_int,
                                        c_u64, c_vp, c_vp, c_vp]),
     "sufhip_seed_from_id": (None, [c_u64, c_u64, c_vp]),
@@ -178,6 +182,11 @@ class Chain2Args(ctypes.Structure):
                 ("lut", c_vp * 2), ("lut_key_bytes", c_sz), ("intervals", c_int),
                 ("lut_mask", c_u64), ("a", Term2 * 4), ("b", Term2 * 4), ("c", Term2 * 4),
                 ("trunc", TruncEpilogue * 4), ("trunc_mask", c_u64 * 4), ("out", c_vp * 2)]
+
+
+class ReluRoundKey(ctypes.Structure):
+    """sufhip_relu_round_key (include/suf_hip.h)."""
+    _fields_ = [("key", c_vp * 2), ("key_bytes", c_sz), ("intervals", c_int), ("mask", c_u64)]
 
 
 class TruncJob(ctypes.Structure):

@@ -47,6 +47,7 @@ def max_tree_plan(offsets):
     cur_off = offsets.copy()
     cur_len = lens.copy()
     rounds = []
+    round_off = []
     while np.any(cur_len > 1):
         nxt_len = (cur_len + 1) // 2
         nxt_off = np.concatenate([[0], np.cumsum(nxt_len)])
@@ -61,9 +62,20 @@ def max_tree_plan(offsets):
                 src_a[o + pairs] = b + L - 1
                 src_b[o + pairs] = -1
         rounds.append((src_a, src_b, int(cur_off[-1])))
+        round_off.append(nxt_off[:-1].copy())
         cur_off, cur_len = nxt_off, nxt_len
     # Row r's max sits at cur_off[r] of the last level (rows are non-empty).
+    max_tree_plan.round_offsets = round_off
     return rounds, cur_off[:-1].astype(np.int64)
+
+
+def max_tree_round_offsets(offsets):
+    """[rounds][rows] int32: each row's first output slot in each round."""
+    max_tree_plan(offsets)
+    ro = max_tree_plan.round_offsets
+    rows = len(offsets) - 1
+    return np.array(ro, dtype=np.int32).reshape(len(ro), rows) if ro else \
+        np.zeros((0, rows), dtype=np.int32)
 
 
 class RowMaxDiff:
@@ -87,9 +99,27 @@ class RowMaxDiff:
         row = np.repeat(np.arange(self.rows), np.diff(self.offsets))
         self.max_index = dev_i32(max_pos[row], device)
         self.max_len = self.rows
+        self.max_row = int(np.diff(self.offsets).max())
+        self.offs_dev = dev_i32(self.offsets, device)
+        ro = max_tree_round_offsets(self.offsets)
+        self.round_off = dev_i32(ro.ravel() if ro.size else np.zeros(1), device)
+        self.tree_ok = self.max_row <= 512 and len(self.rounds) <= 16
+        self.round_keys = (native.ReluRoundKey * max(1, len(self.rounds)))()
+        for k, rd in enumerate(self.rounds):
+            lut = rd["lut"]
+            rk = self.round_keys[k]
+            rk.key[0], rk.key[1] = lut.keys[0].data_ptr(), lut.keys[1].data_ptr()
+            rk.key_bytes, rk.intervals, rk.mask = lut.key_bytes, lut.intervals, lut.mask
 
-    def eval2(self, x, delta):
-        """x, delta: pairs of int64 [n] device tensors."""
+    def eval2(self, x, delta, fused=True):
+        """x, delta: pairs of int64 [n] device tensors.  fused: the whole tree
+        in one launch (rows up to 512 elements); else one launch per round."""
+        if fused and self.tree_ok:
+            native.call("sufhip_relu_max_tree2", x[0].data_ptr(), x[1].data_ptr(), self.rows,
+                        self.offs_dev.data_ptr(), self.max_row, len(self.rounds),
+                        self.round_off.data_ptr(), self.round_keys, delta[0].data_ptr(),
+                        delta[1].data_ptr(), stream_ptr())
+            return delta
         cur = x
         for rd in self.rounds:
             lut = rd["lut"]

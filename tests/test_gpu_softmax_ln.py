@@ -58,11 +58,16 @@ def test_max_tree_plan_covers_rows():
     assert len(rounds) == 6 and len(max_pos) == 4
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("offsets", [
-    np.array([0, 1, 3, 6, 13, 13 + 128, 13 + 128 + 65], dtype=np.int64),
+    np.array([0, 1, 3, 6, 13, 13 + 128, 13 + 128 + 65, 13 + 128 + 65 + 1000], dtype=np.int64),
     softmax.causal_offsets(2, 16),
+    # Longest rows 300 and 512: two rows and one row per workgroup in the
+    # one-launch tree; 7 rows leave a partial group.
+    np.cumsum([0, 1, 2, 3, 300, 5, 64, 7]).astype(np.int64),
+    np.cumsum([0, 512, 1, 33]).astype(np.int64),
 ])
-def test_row_max_diff_shares(offsets):
+def test_row_max_diff_shares(offsets, fused):
     x = _scores(offsets, 21)
     x[0] = np.uint64(1 << 63)  # most negative value in its own row
     x0, x1 = _share(x, 22)
@@ -70,7 +75,7 @@ def test_row_max_diff_shares(offsets):
     rm = softmax.RowMaxDiff(offsets, softmax.Dealer(5))
     delta = tuple(torch.empty(int(offsets[-1]), dtype=torch.int64, device="cuda")
                   for _ in range(2))
-    rm.eval2(_pair_dev(x0, x1), delta)
+    rm.eval2(_pair_dev(x0, x1), delta, fused=fused)
     g = [u64(delta[0]), u64(delta[1])]
     o = tp.relu_rounds2(rm, [x0, x1])
     assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
