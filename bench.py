@@ -29,8 +29,16 @@ HBM_PEAK_GBPS = 8000.0
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch) and scaled by the
 # counters' reading for a 256 MiB device copy (FETCH x2.0, WRITE x1.0); the
 # commands and raw values are in profiles/dcf_eval_bit_kernel__dcf_batch_n2p20.md.
-MEASURED_TRAFFIC_BYTES = 1258342 * 1024 * 2.0 + 1110.5 * 1024 * 1.0
-VALU_PEAK_GOPS = 256 * 64 * 2.4  # 256 CUs x 64 lanes x 2.4 GHz, 32-bit integer ops
+MEASURED_TRAFFIC_BYTES = 1256045.2 * 1024 * 2.0 + 1233.0 * 1024 * 1.0
+# Instructions per dcf_eval_bit_kernel launch at N = 2^20 (rocprofv3 --pmc
+# SQ_INSTS_VALU SQ_INSTS_LDS, same profile file): fixed by the compiled kernel
+# and N, so lane-ops per second follow from the measured launch time.
+DCF_VALU_INSTS = 534897920
+DCF_LDS_INSTS = 330368256
+VALU_PEAK_GOPS = 256 * 64 * 2.4  # 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz, 32-bit integer ops
+# LDS: 128 bytes per clock per CU (a wave64 4-byte read every 2 clocks, as
+# measured for this kernel's random-index reads) x 256 CUs x 2.4 GHz.
+LDS_PEAK_GBPS = 256 * 128 * 2.4
 
 
 def parse():
@@ -43,6 +51,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gates", action="store_true",
                     help="skip the spline-gate and Beaver matmul pipeline timings")
+    ap.add_argument("--only", choices=["spline", "matmul", "softmax_ln", "layer"],
+                    help="run one gate pipeline alone and print its result object "
+                         "(for profiling; not the benchmark line)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device-to-device copy kernel 5 times "
                          "(reference point for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -484,6 +495,20 @@ def main():
     if a.calibrate_copy:
         calibrate_copy()
         return
+    if a.only:
+        import torch  # noqa: F401  (initialises the device before the library)
+
+        from suf_amd import native
+
+        native.call("sufhip_init", 0)
+        cpu_s = 0.0 if a.no_cpu else a.cpu_seconds / 2
+        run = {"spline": lambda: bench_spline(a.steps, a.warmup, cpu_seconds=cpu_s),
+               "matmul": lambda: bench_matmul(a.steps, a.warmup, cpu_seconds=cpu_s),
+               "softmax_ln": lambda: bench_softmax_ln(a.steps, a.warmup, cpu=not a.no_cpu),
+               "layer": lambda: bench_layer(a.steps, a.warmup, cpu=not a.no_cpu)}[a.only]
+        res = run()
+        print(json.dumps({"only": a.only, **res}), flush=True)
+        sys.exit(0 if res["check"] in ("ok", "not run (--no-cpu)") else 1)
     import numpy as np
     import torch
 
@@ -582,13 +607,27 @@ def main():
             "kernel_ms": kern_ms,
             "bytes_per_launch": key_bytes_per_launch,
             "note": "key bytes streamed per launch / launch time; the kernel is bound by "
-                    "VALU+LDS AES work, see roofline_valu",
+                    "its LDS T-table reads and VALU AES work, see roofline_lds and roofline_valu",
         },
+        # The pipes that bind the AES work: VALU lane-ops and LDS read bytes
+        # per launch (counter totals for N = 2^20) over the measured launch time.
         "roofline_valu": {
             "bound": "valu",
+            "achieved": DCF_VALU_INSTS * 64 / (kern_ms / 1e3) / 1e9 * (n / (1 << 20)),
+            "peak": VALU_PEAK_GOPS,
+            "unit": "Gop/s",
+            "frac": DCF_VALU_INSTS * 64 / (kern_ms / 1e3) / 1e9 * (n / (1 << 20)) / VALU_PEAK_GOPS,
+            "valu_insts_per_launch": DCF_VALU_INSTS,
             "aes_blocks_per_launch": n * 64 * 2,
-            "aes_blocks_per_s": n * 64 * 2 / (kern_ms / 1e3),
-            "peak_gops": VALU_PEAK_GOPS,
+        },
+        "roofline_lds": {
+            "bound": "lds",
+            "achieved": DCF_LDS_INSTS * 256 / (kern_ms / 1e3) / 1e9 * (n / (1 << 20)),
+            "peak": LDS_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": DCF_LDS_INSTS * 256 / (kern_ms / 1e3) / 1e9 * (n / (1 << 20)) / LDS_PEAK_GBPS,
+            "lds_insts_per_launch": DCF_LDS_INSTS,
+            "note": "256 bytes per wave64 4-byte LDS instruction; bank conflicts measured 0",
         },
         "keygen_ms": keygen_ms,
         "secure_layer_ms": None,

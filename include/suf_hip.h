@@ -403,6 +403,50 @@ typedef struct sufhip_chain2_args {
 } sufhip_chain2_args;
 int sufhip_gate_chain2(const sufhip_chain2_args* args, void* stream);
 
+/* Both parties' shares of one Beaver triple set: a, b, c device arrays per
+ * party (b per row for a row-broadcast triple). */
+typedef struct sufhip_triple2 {
+  const uint64_t* a[2];
+  const uint64_t* b[2];
+  const uint64_t* c[2];
+} sufhip_triple2;
+
+/* LayerNormTask whole (include/runtime/phase_tasks.hpp:2186-2668, with
+ * RsqrtTask :1383-1700, as transformer_layer_forward builds it,
+ * src/nn/transformer_layer.cpp:626-760: no gamma/beta, one NR step) for both
+ * parties in one launch, one workgroup per row of the row-major
+ * [rows x cols] input x (cols <= 2048):
+ *   mu  = tr_mean(inv_len * sum_row x)          open masked by mean_mask
+ *   d   = x - mu[row];  q = d * d               Beaver, triple sq (per element)
+ *   va  = tr_var[0](inv_len * sum_row q)        open masked by var_mask[0]
+ *   var = tr_var[1](va)                         open masked by var_mask[1]
+ *   rs  = rsqrt chain at var + eps (party 0 adds eps); its LUT, triples and
+ *         truncations as sufhip_gate_chain2 with kind SUFHIP_CHAIN_RSQRT and
+ *         n = rows (x and out of that struct are ignored)
+ *   out = tr_norm(d * rs[row])                  row-broadcast triple norm,
+ *                                               open masked by norm_mask
+ * Every tr_* is a prepared GapARS table gate (frac_bits <= 14; y ignored).
+ * The shares equal those of the launch-per-step evaluation (sufhip_row_sum2,
+ * sufhip_mul2x, sufhip_lin2, sufhip_gate_chain2 with the same material). */
+typedef struct sufhip_layernorm2_args {
+  const uint64_t* x[2];
+  int rows;
+  int cols;
+  uint64_t inv_len;
+  uint64_t eps;
+  sufhip_trunc_epilogue tr_mean;
+  sufhip_trunc_epilogue tr_var[2];
+  sufhip_trunc_epilogue tr_norm;
+  uint64_t mean_mask;
+  uint64_t var_mask[2];
+  uint64_t norm_mask;
+  sufhip_triple2 sq;
+  sufhip_triple2 norm;
+  sufhip_chain2_args rsqrt;
+  uint64_t* out[2];
+} sufhip_layernorm2_args;
+int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream);
+
 /* RowMaxDiffTask whole (include/nn/row_maxdiff_task.hpp:49-165) for both
  * parties in one launch: every round of the pairwise-max tree over the packed
  * rows [d_row_offsets[r], d_row_offsets[r+1]) (1 <= length <= max_row <= 512,

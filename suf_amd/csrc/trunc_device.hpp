@@ -70,13 +70,12 @@ __device__ __forceinline__ uint64_t trunc_carry_from(const TruncHdr& h, uint64_t
   return (h.party == 0 ? 1 : 0) - h.cw + a;
 }
 
-// One party's GapARS output at the public xhat from the key and its prepared
-// full-domain table (node v's value word holds the carry DCF's share at v).
-// A key that is not a GapARS key for f bits yields 0; the table read stays
-// inside its 2^f nodes either way.
-__device__ __forceinline__ uint64_t trunc_table_eval(const uint8_t* key, const uint4* table,
-                                                     int f, uint64_t xhat) {
-  const TruncHdr h = read_trunc_hdr(key);
+// One party's GapARS output at the public xhat from the key's header and its
+// prepared full-domain table (node v's value word holds the carry DCF's
+// share at v).  A key that is not a GapARS key for f bits yields 0; the table
+// read stays inside its 2^f nodes either way.
+__device__ __forceinline__ uint64_t trunc_table_eval_h(const TruncHdr& h, const uint4* table,
+                                                       int f, uint64_t xhat) {
   if (h.tag != kTruncTag || h.kind != SUFHIP_TRUNC_GAPARS || int(h.f) != f) return 0;
   uint64_t carry = 0;
   if (h.flags & 1) {
@@ -84,6 +83,11 @@ __device__ __forceinline__ uint64_t trunc_table_eval(const uint8_t* key, const u
     carry = trunc_carry_from(h, uint64_t(q.x) | uint64_t(q.y) << 32);
   }
   return trunc_postproc<SUFHIP_TRUNC_GAPARS>(h, f, xhat, carry, 0, 0);
+}
+
+__device__ __forceinline__ uint64_t trunc_table_eval(const uint8_t* key, const uint4* table,
+                                                     int f, uint64_t xhat) {
+  return trunc_table_eval_h(read_trunc_hdr(key), table, f, xhat);
 }
 
 // A truncation gate folded into the launch that produces its masked open.

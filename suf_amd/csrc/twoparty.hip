@@ -32,6 +32,7 @@
 #include "suf_hip.h"
 #include "sufhip_internal.hpp"
 #include "operand_device.hpp"
+#include "reduce_device.hpp"
 #include "trunc_device.hpp"
 
 namespace sufhip {
@@ -138,16 +139,6 @@ __global__ void __launch_bounds__(kBlock) mul2x_kernel(sufhip_mul2x_args a, size
       a.z[1][i] = z1;
     }
   }
-}
-
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint32_t lo = __shfl_xor(uint32_t(v), off, 64);
-    const uint32_t hi = __shfl_xor(uint32_t(v >> 32), off, 64);
-    v += uint64_t(lo) | uint64_t(hi) << 32;
-  }
-  return v;
 }
 
 // One wave per row, four rows per workgroup.

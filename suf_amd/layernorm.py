@@ -24,8 +24,8 @@ import numpy as np
 import torch
 
 from . import native, tables
-from .tasks import (CoeffLut, Dealer, Prepared, Triples, Trunc, chain2, dev_i32, lin2, mul2x,
-                    operand, pair, row_sum2, term)
+from .tasks import (M64, CoeffLut, Dealer, Prepared, Triples, Trunc, chain2, chain2_args,
+                    dev_i32, lin2, mul2x, operand, pair, row_sum2, stream_ptr, term, triple2)
 
 
 class Rsqrt:
@@ -107,14 +107,44 @@ class LayerNormBlock:
     def truncs(self):
         return [self.tr_mean] + self.tr_var + self.rsqrt.truncs() + [self.tr_norm]
 
-    def eval2(self, x, out, prep=None):
+    def block_args(self, x, out):
+        """sufhip_layernorm2_args of the one-launch block over x into out."""
+        a = native.LayerNorm2Args()
+        a.x[0], a.x[1] = x[0].data_ptr(), x[1].data_ptr()
+        a.rows, a.cols = self.rows, self.cols
+        a.inv_len, a.eps = self.inv_len & M64, self.eps_q & M64
+        a.tr_mean = self.tr_mean.epilogue(self.mu)
+        a.tr_var[0] = self.tr_var[0].epilogue(self.va)
+        a.tr_var[1] = self.tr_var[1].epilogue(self.var)
+        a.tr_norm = self.tr_norm.epilogue(out)
+        a.mean_mask = self.tr_mean.mask & M64
+        a.var_mask[0], a.var_mask[1] = self.tr_var[0].mask & M64, self.tr_var[1].mask & M64
+        a.norm_mask = self.tr_norm.mask & M64
+        a.sq, a.norm = triple2(self.tri_sq), triple2(self.tri_norm)
+        rs = self.rsqrt
+        a.rsqrt = chain2_args(native.CHAIN_RSQRT, self.f, None, self.rows, rs.lut.keys,
+                              rs.lut.key_bytes, rs.lut.intervals, rs.lut.mask, rs.tri, rs.tr,
+                              rs.y)
+        a.out[0], a.out[1] = out[0].data_ptr(), out[1].data_ptr()
+        return a
+
+    def fusable(self):
+        return (self.cols <= 2048 and self.rsqrt.iters == 1 and
+                all(t.has_table() for t in self.truncs()))
+
+    def eval2(self, x, out, prep=None, fused=True):
         """x, out: pairs of int64 [rows * cols] device tensors.  prep:
         (tasks.Prepared, batch) holding this block's key-only halves, or None
-        to issue them here on the block's side stream."""
+        to issue them here on the block's side stream.  fused: the whole block
+        in one launch (sufhip_layernorm2); else launch by launch."""
         rows, cols, n = self.rows, self.cols, self.n
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
         prep[0].wait(prep[1])
+        if fused and self.fusable():
+            a = self.block_args(x, out)
+            native.call("sufhip_layernorm2", native.ctypes.byref(a), stream_ptr())
+            return out
         row_sum2(operand(term(x)), rows, cols, mul_const=self.inv_len,
                  into=(self.tr_mean, self.mu))
         diff = operand(term(x), term(self.mu, index=self.row_index, neg=True, length=rows))

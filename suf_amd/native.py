@@ -97,6 +97,7 @@ _SIGS = {
     "sufhip_interval_lut_eval2": (c_int, [c_vp, c_vp, c_sz, c_int, c_int, c_vp, c_vp, c_u64,
                                           c_sz, c_vp, c_vp, c_vp]),
     "sufhip_gate_chain2": (c_int, [c_vp, c_vp]),
+    "sufhip_layernorm2": (c_int, [c_vp, c_vp]),
     "sufhip_relu_max_tree2": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_vp, c_vp,
                                       c_vp, c_vp]),
     "sufhip_relu_max_round2": (c_int, [c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_int,
@@ -182,6 +183,20 @@ class Chain2Args(ctypes.Structure):
                 ("lut", c_vp * 2), ("lut_key_bytes", c_sz), ("intervals", c_int),
                 ("lut_mask", c_u64), ("a", Term2 * 4), ("b", Term2 * 4), ("c", Term2 * 4),
                 ("trunc", TruncEpilogue * 4), ("trunc_mask", c_u64 * 4), ("out", c_vp * 2)]
+
+
+class Triple2(ctypes.Structure):
+    """sufhip_triple2 (include/suf_hip.h)."""
+    _fields_ = [("a", c_vp * 2), ("b", c_vp * 2), ("c", c_vp * 2)]
+
+
+class LayerNorm2Args(ctypes.Structure):
+    """sufhip_layernorm2_args (include/suf_hip.h)."""
+    _fields_ = [("x", c_vp * 2), ("rows", c_int), ("cols", c_int), ("inv_len", c_u64),
+                ("eps", c_u64), ("tr_mean", TruncEpilogue), ("tr_var", TruncEpilogue * 2),
+                ("tr_norm", TruncEpilogue), ("mean_mask", c_u64), ("var_mask", c_u64 * 2),
+                ("norm_mask", c_u64), ("sq", Triple2), ("norm", Triple2), ("rsqrt", Chain2Args),
+                ("out", c_vp * 2)]
 
 
 class ReluRoundKey(ctypes.Structure):

@@ -383,9 +383,27 @@ def chain2(kind, f, x, n, lut_keys, lut_key_bytes, intervals, lut_mask, triples,
     kind native.CHAIN_*, x the input operand, lut_keys both parties' LUT
     blobs, triples / truncs the chain's products and truncation gates in
     order, out the output pair."""
+    a = chain2_args(kind, f, x, n, lut_keys, lut_key_bytes, intervals, lut_mask, triples, truncs,
+                    out)
+    native.call("sufhip_gate_chain2", native.ctypes.byref(a), stream_ptr())
+
+
+def triple2(tri):
+    """sufhip_triple2 of a Triples (b per row when it is row-broadcast)."""
+    t = native.Triple2()
+    for p in (0, 1):
+        t.a[p], t.b[p], t.c[p] = ptr(tri.a[p]), ptr(tri.b[p]), ptr(tri.c[p])
+    return t
+
+
+def chain2_args(kind, f, x, n, lut_keys, lut_key_bytes, intervals, lut_mask, triples, truncs,
+                out):
+    """The sufhip_chain2_args of chain2 (x None: an empty operand, for a
+    chain embedded in a block launch)."""
     a = native.Chain2Args()
     a.kind, a.frac_bits, a.n = kind, f, n
-    a.x = x
+    if x is not None:
+        a.x = x
     a.lut[0], a.lut[1] = ptr(lut_keys[0]), ptr(lut_keys[1])
     a.lut_key_bytes, a.intervals, a.lut_mask = lut_key_bytes, intervals, lut_mask & M64
     for k, t in enumerate(triples):
@@ -394,4 +412,4 @@ def chain2(kind, f, x, n, lut_keys, lut_key_bytes, intervals, lut_mask, triples,
         a.trunc[k] = tr.epilogue(out)
         a.trunc_mask[k] = tr.mask & M64
     a.out[0], a.out[1] = ptr(out[0]), ptr(out[1])
-    native.call("sufhip_gate_chain2", native.ctypes.byref(a), stream_ptr())
+    return a

@@ -206,18 +206,22 @@ def test_softmax_block_config_shape_twice():
         assert np.array_equal(_recon(out), prob.view(np.uint64))
 
 
-def test_layernorm_small_shares():
-    rows, cols = 4, 96
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("rows,cols", [(4, 96), (3, 1100)])
+def test_layernorm_small_shares(rows, cols, fused):
+    """The one-launch block and the launch-per-step path give the oracle's
+    shares (cols 1100: five elements per thread, a partial last one)."""
     x = pfss.host_normal_fixed(60, 1.0, 0.0, F, rows * cols)
     x[:cols] = x[:cols] * np.uint64(3)  # a wider row
     x0, x1 = _share(x, 61)
-    say("layernorm %dx%d" % (rows, cols))
+    say("layernorm %dx%d fused=%s" % (rows, cols, fused))
     ln = layernorm.LayerNormBlock(rows, cols, STATE, F, seed=14)
     out = tuple(torch.empty(rows * cols, dtype=torch.int64, device="cuda") for _ in range(2))
-    ln.eval2(_pair_dev(x0, x1), out)
+    ln.eval2(_pair_dev(x0, x1), out, fused=fused)
     y, st = fp.layernorm(x, rows, cols, F, ln.inv_len, ln.eps_q, ln.rsqrt.table)
-    assert np.array_equal(_recon(ln.mu), st["mu"].view(np.uint64))
-    assert np.array_equal(_recon(ln.var), st["var"].view(np.uint64))
+    if not fused:  # the block launch keeps its intermediates in registers
+        assert np.array_equal(_recon(ln.mu), st["mu"].view(np.uint64))
+        assert np.array_equal(_recon(ln.var), st["var"].view(np.uint64))
     assert np.array_equal(_recon(out), y.view(np.uint64))
     # Share level: the whole chain on the oracle.
     o = tp.layernorm2(ol.Prg(STATE), ln, [x0, x1])
@@ -234,9 +238,26 @@ def test_layernorm_config_shape_twice():
     y, _ = fp.layernorm(x, rows, cols, F, ln.inv_len, ln.eps_q, ln.rsqrt.table)
     xin = _pair_dev(x0, x1)
     out = tuple(torch.empty(rows * cols, dtype=torch.int64, device="cuda") for _ in range(2))
-    for _ in range(2):
-        ln.eval2(xin, out)
+    shares = []
+    for fused in (True, True, False):
+        ln.eval2(xin, out, fused=fused)
         assert np.array_equal(_recon(out), y.view(np.uint64))
+        shares.append((u64(out[0]), u64(out[1])))
+    for g in shares[1:]:
+        assert np.array_equal(g[0], shares[0][0]) and np.array_equal(g[1], shares[0][1])
+
+
+def test_layernorm_block_rejects_wide_rows():
+    ln = layernorm.LayerNormBlock(2, 8, STATE, F, seed=15)
+    x = tuple(torch.zeros(16, dtype=torch.int64, device="cuda") for _ in range(2))
+    out = tuple(torch.empty(16, dtype=torch.int64, device="cuda") for _ in range(2))
+    a = ln.block_args(x, out)
+    a.cols = 4096
+    with pytest.raises(native.SufHipError):
+        native.call("sufhip_layernorm2", native.ctypes.byref(a), None)
+    a.cols, a.rsqrt.kind = 8, native.CHAIN_RECIP
+    with pytest.raises(native.SufHipError):
+        native.call("sufhip_layernorm2", native.ctypes.byref(a), None)
 
 
 def test_lin2_and_row_sum2_bounds():
