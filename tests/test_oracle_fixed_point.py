@@ -1,8 +1,9 @@
 """Pins the closed forms of oracle/fixed_point.py (softmax / LayerNorm task
 chains) and the dealer tables they evaluate, without any GPU:
 
-  * against the real functions in float64 (exp(-t), 1/x, 1/sqrt(x), softmax,
-    layer norm) within the accuracy the 12-fraction-bit tables allow;
+  * against the real functions in float64 (exp(-t), 1/x, 1/sqrt(x), GeLU,
+    softmax, layer norm, causal attention, a whole GPT-2 block) within the
+    accuracy the 12-fraction-bit tables allow;
   * against brute force (row max, piece selection at every boundary);
   * against values computed by hand from the reference formulas.
 A planted mistake (a dropped NR step, an off-by-one shift, a wrong piece)
@@ -141,6 +142,80 @@ def test_layernorm_closed_form_tracks_float():
     var = (d * d).sum(axis=1) * 5 / ONE
     ref = d / np.sqrt(var + 1 / 1024)[:, None]
     assert np.abs(y.reshape(rows, cols) / ONE - ref).max() < 0.05
+
+
+def _erf_gelu(u):
+    return 0.5 * u * (1.0 + np.vectorize(math.erf)(u / math.sqrt(2.0)))
+
+
+def _float_ln(v):
+    mu = v.mean(axis=1, keepdims=True)
+    dd = v - mu
+    return dd / np.sqrt((dd * dd).mean(axis=1, keepdims=True) + 1.0 / 1024)
+
+
+def _float_attention(qkv, seq, d, heads):
+    dh = d // heads
+    out = np.zeros((seq, d))
+    causal = np.tril(np.ones((seq, seq))) > 0
+    for h in range(heads):
+        Q = qkv[:, h * dh:(h + 1) * dh]
+        K = qkv[:, d + h * dh:d + (h + 1) * dh]
+        V = qkv[:, 2 * d + h * dh:2 * d + (h + 1) * dh]
+        S = np.where(causal, Q @ K.T / math.sqrt(dh), -np.inf)
+        P = np.exp(S - S.max(axis=1, keepdims=True))
+        out[:, h * dh:(h + 1) * dh] = (P / P.sum(axis=1, keepdims=True)) @ V
+    return out
+
+
+def test_gelu_table_tracks_gelu():
+    """x Phi(x) (erf form) on [-10, 10): within 0.005; 0 below -8, x above 8."""
+    a, c = tables.gelu_table(F)
+    x = np.arange(-10 * ONE, 10 * ONE, 7, dtype=np.int64)
+    y = fp.cubic_task(a, c, x, F) / ONE
+    assert np.abs(y - _erf_gelu(x / ONE)).max() < 0.005
+    assert np.all(y[x < -8 * ONE] == 0)
+    assert np.array_equal(fp.cubic_task(a, c, x[x >= 8 * ONE], F), x[x >= 8 * ONE])
+
+
+def test_attention_closed_form_tracks_float():
+    """Causal multi-head attention on Q12 QKV rows (4 heads of 16) against the
+    float64 softmax(Q K^T / sqrt(dh)) V."""
+    seq, d, heads = 16, 64, 4
+    rng = np.random.default_rng(7)
+    qkv = np.round(rng.normal(0, 1, size=(seq, 3 * d)) * ONE).astype(np.int64)
+    ctx, st = fp.attention(qkv.reshape(-1), seq, d, heads, F, tables.nexp_table(F),
+                           tables.recip_table(F))
+    ref = _float_attention(qkv / ONE, seq, d, heads)
+    assert np.abs(ctx.reshape(seq, d) / ONE - ref).max() < 0.05
+    assert len(st["scores"]) == heads * seq * (seq + 1) // 2
+
+
+def test_transformer_layer_closed_form_tracks_float():
+    """The whole layer (weights N(0, 0.1), so that every branch moves the
+    output by more than 1) against a float64 GPT-2 block without biases or
+    gamma/beta; each stage also against float64 applied to the closed form's
+    own input of that stage."""
+    seq, d, heads, ffn = 16, 64, 4, 256
+    rng = np.random.default_rng(8)
+    W = {k: np.round(rng.normal(0, 0.1, size=sh) * ONE).astype(np.int64)
+         for k, sh in [("Wqkv", (d, 3 * d)), ("Wout", (d, d)), ("W1", (d, ffn)),
+                       ("W2", (ffn, d))]}
+    x = np.round(rng.normal(0, 1, size=(seq, d)) * ONE).astype(np.int64)
+    tabs = {"nexp": tables.nexp_table(F), "recip": tables.recip_table(F),
+            "rsqrt": tables.rsqrt_table(F), "gelu": tables.gelu_table(F)}
+    out, st = fp.transformer_layer(x.reshape(-1), W, seq, d, heads, ffn, F, tabs,
+                                   tables.inv_len_qf(d), tables.eps_qf())
+    Wf = {k: v / ONE for k, v in W.items()}
+    xf = x / ONE
+    r1 = _float_attention(_float_ln(xf) @ Wf["Wqkv"], seq, d, heads) @ Wf["Wout"] + xf
+    ref = _erf_gelu(_float_ln(r1) @ Wf["W1"]) @ Wf["W2"] + r1
+    assert np.abs(ref - xf).max() > 1.0
+    assert np.abs(out.reshape(seq, d) / ONE - ref).max() < 0.06
+    assert np.abs(st["h1"].reshape(seq, d) / ONE - _float_ln(xf)).max() < 0.02
+    ctx_ref = _float_attention(st["qkv"].reshape(seq, 3 * d) / ONE, seq, d, heads)
+    assert np.abs(st["ctx"].reshape(seq, d) / ONE - ctx_ref).max() < 0.05
+    assert np.abs(st["g"] / ONE - _erf_gelu(st["u"] / ONE)).max() < 0.005
 
 
 def test_mul_shift_refuses_out_of_range():
