@@ -466,6 +466,49 @@ int sufhip_relu_max_tree2(const uint64_t* d_x0, const uint64_t* d_x1, int rows,
                           const int32_t* d_round_offsets, const sufhip_relu_round_key* keys,
                           uint64_t* d_delta0, uint64_t* d_delta1, void* stream);
 
+/* SoftmaxBlockTask whole (include/nn/softmax_block_task.hpp:97-450, fed by
+ * RowMaxDiffTask, include/nn/row_maxdiff_task.hpp:49-165) for both parties in
+ * one launch, one wavefront per packed row [d_row_offsets[r],
+ * d_row_offsets[r+1]) (1 <= length <= max_row <= 512):
+ *   s     = x at the row's elements; with pre_truncs = 1 or 2, s is replaced
+ *           by pre[q](open of s masked by pre_mask[q]) in turn (the scores'
+ *           truncations of attention_forward)
+ *   max   = the ReLU pairwise-max tree over s (rounds <= 10, keys and
+ *           d_round_offsets as sufhip_relu_max_tree2)
+ *   e     = nexp chain at max - s (sufhip_gate_chain2 material, kind CUBIC,
+ *           n = the packed element count; x and out of that struct ignored)
+ *   inv   = recip chain at the row sum of e (kind RECIP, n = rows)
+ *   prob  = tr_norm(e * inv[row]) (row-broadcast triple norm, open masked
+ *           by norm_mask)
+ * and writes prob to out (if given) and/or, with d_dense given, the open
+ * P - A of the next Beaver product over the dense [rows x dense_cols]
+ * layout: d_dense[r * dense_cols + j] = (prob_0 - a_0) + (prob_1 - a_1) for
+ * j < length, (0 - a_0) + (0 - a_1) for length <= j < dense_cols
+ * (dense_a[p] [rows * dense_cols]).  Shares equal those of the launch-per-
+ * step evaluation with the same material. */
+typedef struct sufhip_softmax2_args {
+  sufhip_operand2 x;
+  int pre_truncs;
+  sufhip_trunc_epilogue pre[2];
+  uint64_t pre_mask[2];
+  int rows;
+  const int32_t* d_row_offsets;
+  int max_row;
+  int rounds;
+  const int32_t* d_round_offsets;
+  sufhip_relu_round_key keys[10];
+  sufhip_chain2_args nexp;
+  sufhip_chain2_args recip;
+  sufhip_triple2 norm;
+  sufhip_trunc_epilogue tr_norm;
+  uint64_t norm_mask;
+  uint64_t* out[2];
+  uint64_t* d_dense;
+  const uint64_t* dense_a[2];
+  int dense_cols;
+} sufhip_softmax2_args;
+int sufhip_softmax2(const sufhip_softmax2_args* args, void* stream);
+
 /* One pairwise-max round of RowMaxDiffTask (include/nn/row_maxdiff_task.hpp:
  * 49-150), max(a, b) = b + ReLU(a - b), for both parties.  For output slot j:
  *   src_b[j] < 0: next_p[j] = cur_p[src_a[j]] (odd element carried);

@@ -168,7 +168,10 @@ struct AesLds {
   }
 
   // Full AES-128 encryption of (s0..s3); rk points at the 11 round keys
-  // (uint4 per round, usually in LDS).
+  // (uint4 per round, usually in LDS).  The nine middle rounds stay a loop:
+  // the kernels that use this table inline it at many sites, and unrolled
+  // copies (~5 KB each) overflow the instruction cache of a latency-bound
+  // kernel, while the loop costs three scalar instructions per round.
   __device__ __forceinline__ void encrypt(uint32_t& s0, uint32_t& s1, uint32_t& s2, uint32_t& s3,
                                           const uint4* rk) const {
     uint4 k = rk[0];
@@ -176,7 +179,7 @@ struct AesLds {
     s1 ^= k.y;
     s2 ^= k.z;
     s3 ^= k.w;
-#pragma unroll
+#pragma unroll 1
     for (int r = 1; r < 10; ++r) {
       k = rk[r];
       round(s0, s1, s2, s3, k.x, k.y, k.z, k.w);
@@ -190,6 +193,43 @@ struct AesLds {
     s1 = o1;
     s2 = o2;
     s3 = o3;
+  }
+
+  // N independent encryptions in lockstep (state n under round keys rk[n]):
+  // each round issues the table reads of all N states before any of them is
+  // used, so a lane pays about one block's latency for N blocks.  For the
+  // latency-bound kernels, where a lane encrypts several blocks whose inputs
+  // are all known.
+  template <int N>
+  __device__ __forceinline__ void encrypt_n(uint32_t (&st)[N][4], const uint4* const (&rk)[N]) const {
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const uint4 k = rk[n][0];
+      st[n][0] ^= k.x;
+      st[n][1] ^= k.y;
+      st[n][2] ^= k.z;
+      st[n][3] ^= k.w;
+    }
+#pragma unroll 1
+    for (int r = 1; r < 10; ++r) {
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const uint4 k = rk[n][r];
+        round(st[n][0], st[n][1], st[n][2], st[n][3], k.x, k.y, k.z, k.w);
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const uint4 k = rk[n][10];
+      const uint32_t o0 = last_col(st[n][0], st[n][1], st[n][2], st[n][3]) ^ k.x;
+      const uint32_t o1 = last_col(st[n][1], st[n][2], st[n][3], st[n][0]) ^ k.y;
+      const uint32_t o2 = last_col(st[n][2], st[n][3], st[n][0], st[n][1]) ^ k.z;
+      const uint32_t o3 = last_col(st[n][3], st[n][0], st[n][1], st[n][2]) ^ k.w;
+      st[n][0] = o0;
+      st[n][1] = o1;
+      st[n][2] = o2;
+      st[n][3] = o3;
+    }
   }
 
   // Only byte 0 of the ciphertext: rounds 1-8 in full, column 0 of round 9,
@@ -347,17 +387,22 @@ struct AesLds4 {
 };
 
 // Cooperative fill of the replicated table from the constant T table in
-// global memory (`tsrc`, 256 words): one word load per four copies, written
-// as one 16-byte LDS store.  `lds` must be 16-byte aligned.  Must be followed
-// by __syncthreads().
+// global memory (`tsrc`, 256 words): the 256 words are loaded once (one
+// global round trip) into a 1 KB LDS staging copy, then replicated from LDS
+// with 16-byte stores.  `lds` must be 16-byte aligned.  Contains a barrier,
+// so every thread of the workgroup must call it; must be followed by
+// __syncthreads() before the table is read.
 template <int kCopies>
 __device__ __forceinline__ void fill_ttable(uint32_t* lds, const uint32_t* tsrc) {
   static_assert(kCopies % 4 == 0, "fill_ttable: copies in groups of four");
   constexpr int kVec = kCopies / 4;
-  uint4* dst = reinterpret_cast<uint4*>(lds);
+  __shared__ uint32_t stage[256];
   const int nthreads = blockDim.x;
+  for (int i = threadIdx.x; i < 256; i += nthreads) stage[i] = tsrc[i];
+  __syncthreads();
+  uint4* dst = reinterpret_cast<uint4*>(lds);
   for (int i = threadIdx.x; i < 256 * kVec; i += nthreads) {
-    const uint32_t v = tsrc[i / kVec];
+    const uint32_t v = stage[i / kVec];
     dst[i] = make_uint4(v, v, v, v);
   }
 }

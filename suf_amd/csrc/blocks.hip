@@ -9,10 +9,13 @@
 //
 //   layernorm2_kernel  LayerNormTask (include/runtime/phase_tasks.hpp:
 //                      2186-2668) with RsqrtTask (:1383-1700)
+//   softmax2_kernel    SoftmaxBlockTask (include/nn/softmax_block_task.hpp:
+//                      97-450) with RowMaxDiffTask, nExp, row sum, Recip
 #include <hip/hip_runtime.h>
 
 #include "chain_device.hpp"
 #include "reduce_device.hpp"
+#include "relu_tree_device.hpp"
 
 namespace sufhip {
 namespace {
@@ -52,8 +55,10 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
   if (threadIdx.x < 8) th[threadIdx.x >> 1][threadIdx.x & 1] =
       read_trunc_hdr(A.tr[threadIdx.x >> 1].key[threadIdx.x & 1]);
   __syncthreads();
+  chain_compare(A.rs, L);
+  __syncthreads();
   const AesLds<kLnCopies> aes{tab, threadIdx.x % kLnCopies};
-  const ChainKeyInfo K = chain_key_info(A.rs);
+  const ChainKeyInfo K = chain_key_info(A.rs, L);
   auto gate = [&](int j, uint64_t v) {
     return Two{{trunc_table_eval_h(th[j][0], A.tr[j].table[0], A.tr[j].f, v),
                 trunc_table_eval_h(th[j][1], A.tr[j].table[1], A.tr[j].f, v)}};
@@ -63,12 +68,7 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
     const size_t base = size_t(r) * size_t(cols);
     // The row's rsqrt triples, one word per lane (visible to lane 0 after
     // the row sum's barriers).
-    if (threadIdx.x < 24) {
-      const int k = threadIdx.x / 6, w = (threadIdx.x / 2) % 3, p = threadIdx.x & 1;
-      const sufhip_term2& t = w == 0 ? A.rs.a[k] : (w == 1 ? A.rs.b[k] : A.rs.c[k]);
-      const uint64_t v = term_at(t, p, size_t(r));
-      (w == 0 ? pre.a : (w == 1 ? pre.b : pre.c))[k][p] = v;
-    }
+    if (threadIdx.x < 24) pre.word(threadIdx.x) = chain_triple_word(A.rs, threadIdx.x, size_t(r));
     // Loads in the order of use (x, the square's triple, the norm triple):
     // each step then waits only for its own words, and the norm triple's
     // arrive while lane 0 runs the rsqrt chain.
@@ -153,6 +153,214 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
   }
 }
 
+// Softmax rows: one wavefront per row, groups of `waves` rows per workgroup.
+// The row's scores go to registers and to level 0 of the max tree in LDS;
+// after the tree every step is wave-local (the row sum is a wave reduction,
+// the reciprocal runs on lane 0 and is broadcast by a lane shuffle).
+constexpr int kSmRounds = 10;
+constexpr int kSmMaxRow = 512;
+constexpr int kSmWaves = 4;
+constexpr int kSmCopies = 32;
+constexpr size_t kSmLdsCap = 65536;
+constexpr int kSmLock = 1;  // nExp chains per lane evaluated in lockstep
+
+struct SmArgs {
+  sufhip_operand2 x;
+  int pre;
+  TruncEpi pre_tr[2];
+  uint64_t pre_mask[2];
+  const int32_t* offs;
+  const int32_t* round_off;
+  TreeKeys<kSmRounds> keys;
+  int rows, max_row, waves;
+  ChainArgs nexp, recip;
+  sufhip_triple2 norm;
+  TruncEpi tr_norm;
+  uint64_t norm_mask;
+  uint64_t* out[2];
+  uint64_t* dense;
+  const uint64_t* dense_a[2];
+  int dense_cols;
+};
+
+struct SmStatic {
+  uint32_t tab[256 * kSmCopies];
+  TreeLds<kSmRounds> t;
+  ChainLds nexp, recip;
+  ChainPreN<3> rpre[kSmWaves];  // each row's reciprocal triples
+  uint32_t j0[kSmWaves][kSmRounds];  // each row's tree slot offsets
+};
+
+__device__ __forceinline__ uint64_t bcast_lane0(uint64_t v) {
+  const uint32_t lo = __shfl(uint32_t(v), 0, 64);
+  const uint32_t hi = __shfl(uint32_t(v >> 32), 0, 64);
+  return uint64_t(lo) | uint64_t(hi) << 32;
+}
+
+template <int kPer>
+__global__ void __launch_bounds__(64 * kSmWaves) softmax2_kernel(SmArgs a) {
+  __shared__ __align__(16) SmStatic st;
+  extern __shared__ uint64_t rowbuf[];
+  const int mr = a.max_row;
+  fill_ttable<kSmCopies>(st.tab, kTDev.v);
+  tree_stage(a.keys, st.t);
+  chain_stage(a.nexp, 4, st.nexp);
+  chain_stage(a.recip, 2, st.recip);
+  __syncthreads();
+  tree_compare(a.keys, st.t);
+  chain_compare(a.nexp, st.nexp);
+  chain_compare(a.recip, st.recip);
+  __syncthreads();
+  const AesLds<kSmCopies> aes{st.tab, threadIdx.x % kSmCopies};
+  const ChainKeyInfo Kn = chain_key_info(a.nexp, st.nexp);
+  const ChainKeyInfo Kr = chain_key_info(a.recip, st.recip);
+  const uint32_t shared = ~st.t.diff;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint64_t* even = rowbuf + size_t(wave) * tree_row_words(mr);
+  uint64_t* odd = even + 2 * size_t(mr);
+  for (int g = blockIdx.x; g * a.waves < a.rows; g += gridDim.x) {
+    const int r = g * a.waves + wave;
+    int b = 0, len = 0;
+    if (r < a.rows) {
+      b = a.offs[r];
+      len = a.offs[r + 1] - b;
+      if (len < 1 || len > mr) len = 0;  // refused on the host
+    }
+    // Loads that need no open, issued now to land while the tree runs: the
+    // reciprocal's triples (one word per lane, to LDS) and, for short rows,
+    // every element's normalisation triple (registers).
+    if (len > 0 && lane < 18) st.rpre[wave].word(lane) = chain_triple_word(a.recip, lane, size_t(r));
+    tree_row_offsets(a.keys, a.round_off, a.rows, r, len, st.j0[wave]);
+    constexpr bool kPre = kPer <= 2;
+    uint64_t na[kPre ? kPer : 1][2], nc[kPre ? kPer : 1][2];
+    if constexpr (kPre) {
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int j = lane + 64 * k;
+        const size_t i = size_t(b) + size_t(j < len ? j : 0);
+        na[k][0] = j < len ? a.norm.a[0][i] : 0;
+        na[k][1] = j < len ? a.norm.a[1][i] : 0;
+        nc[k][0] = j < len ? a.norm.c[0][i] : 0;
+        nc[k][1] = j < len ? a.norm.c[1][i] : 0;
+      }
+    }
+    // Scores, through the optional truncations of their open.
+    uint64_t s[kPer][2];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int j = lane + 64 * k;
+      s[k][0] = s[k][1] = 0;
+      if (j < len) {
+        const size_t i = size_t(b) + size_t(j);
+        uint64_t v0 = operand_at(a.x, 0, i), v1 = operand_at(a.x, 1, i);
+        for (int q = 0; q < a.pre; ++q) {
+          const uint64_t o = v0 + v1 + a.pre_mask[q];
+          v0 = trunc_table_eval(a.pre_tr[q].key[0], a.pre_tr[q].table[0], a.pre_tr[q].f, o);
+          v1 = trunc_table_eval(a.pre_tr[q].key[1], a.pre_tr[q].table[1], a.pre_tr[q].f, o);
+        }
+        s[k][0] = v0;
+        s[k][1] = v1;
+        even[j] = v0;
+        even[mr + j] = v1;
+      }
+    }
+    __syncthreads();
+    const int level =
+        tree_row<kSmRounds, kSmCopies>(a.keys, st.t, aes, even, odd, mr, len, st.j0[wave], shared);
+    const uint64_t* fin = (level & 1) ? odd : even;
+    const int fw = (level & 1) ? (mr + 1) / 2 : mr;
+    const uint64_t m0 = len > 0 ? fin[0] : 0, m1 = len > 0 ? fin[fw] : 0;
+    // e = nExp(max - s), summed over the row; the lane's elements kSmLock at
+    // a time, their chains in lockstep (elements past the row end compute on
+    // clamped indices and are dropped).
+    uint64_t e[kPer][2];
+    uint64_t es0 = 0, es1 = 0;
+#pragma unroll
+    for (int k0 = 0; k0 < kPer; k0 += kSmLock) {
+      size_t ii[kSmLock];
+      Two dl[kSmLock], ev[kSmLock];
+      chain_loader<SUFHIP_CHAIN_CUBIC> pl[kSmLock] = {};
+#pragma unroll
+      for (int u = 0; u < kSmLock; ++u) {
+        const int j = lane + 64 * (k0 + u);
+        ii[u] = size_t(b) + size_t(j < len ? j : 0);
+        dl[u] = Two{{m0 - s[k0 + u][0], m1 - s[k0 + u][1]}};
+        pl[u] = chain_loader<SUFHIP_CHAIN_CUBIC>{&a.nexp, ii[u]};
+      }
+      chain_eval_m<SUFHIP_CHAIN_CUBIC, kSmCopies, kSmLock>(a.nexp, st.nexp, Kn, aes, ii, dl, pl,
+                                                            ev);
+#pragma unroll
+      for (int u = 0; u < kSmLock; ++u) {
+        const bool ok = lane + 64 * (k0 + u) < len;
+        e[k0 + u][0] = ok ? ev[u].v[0] : 0;
+        e[k0 + u][1] = ok ? ev[u].v[1] : 0;
+        es0 += e[k0 + u][0];
+        es1 += e[k0 + u][1];
+      }
+    }
+    es0 = wave_sum_u64(es0);
+    es1 = wave_sum_u64(es1);
+    // inv = Recip(row sum) on lane 0.
+    uint64_t inv0 = 0, inv1 = 0;
+    if (lane == 0 && len > 0) {
+      const Two iv = chain_eval<SUFHIP_CHAIN_RECIP, kSmCopies>(
+          a.recip, st.recip, Kr, aes, size_t(r), Two{{es0, es1}}, st.rpre[wave]);
+      inv0 = iv.v[0];
+      inv1 = iv.v[1];
+    }
+    inv0 = bcast_lane0(inv0);
+    inv1 = bcast_lane0(inv1);
+    // prob = tr_norm(e * inv[row]) (row-broadcast Beaver), and the next
+    // product's open over the dense row.
+    if (len > 0) {
+      const uint64_t nb0 = a.norm.b[0][r], nb1 = a.norm.b[1][r];
+      const uint64_t ee = (inv0 - nb0) + (inv1 - nb1);
+      const size_t drow = size_t(r) * size_t(a.dense_cols);
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int j = lane + 64 * k;
+        if (j < len) {
+          const size_t i = size_t(b) + size_t(j);
+          uint64_t a0, a1, c0, c1;
+          if constexpr (kPre) {
+            a0 = na[k][0];
+            a1 = na[k][1];
+            c0 = nc[k][0];
+            c1 = nc[k][1];
+          } else {
+            a0 = a.norm.a[0][i];
+            a1 = a.norm.a[1][i];
+            c0 = a.norm.c[0][i];
+            c1 = a.norm.c[1][i];
+          }
+          const uint64_t dd = (e[k][0] - a0) + (e[k][1] - a1);
+          const uint64_t z0 = c0 + dd * nb0 + ee * a0 + dd * ee;
+          const uint64_t z1 = c1 + dd * nb1 + ee * a1;
+          const uint64_t o = z0 + z1 + a.norm_mask;
+          const uint64_t p0 =
+              trunc_table_eval(a.tr_norm.key[0], a.tr_norm.table[0], a.tr_norm.f, o);
+          const uint64_t p1 =
+              trunc_table_eval(a.tr_norm.key[1], a.tr_norm.table[1], a.tr_norm.f, o);
+          if (a.out[0]) {
+            a.out[0][i] = p0;
+            a.out[1][i] = p1;
+          }
+          if (a.dense) {
+            const size_t di = drow + size_t(j);
+            a.dense[di] = (p0 - a.dense_a[0][di]) + (p1 - a.dense_a[1][di]);
+          }
+        }
+      }
+      if (a.dense)
+        for (int j = len + lane; j < a.dense_cols; j += 64) {
+          const size_t di = drow + size_t(j);
+          a.dense[di] = (uint64_t(0) - a.dense_a[0][di]) + (uint64_t(0) - a.dense_a[1][di]);
+        }
+    }
+    __syncthreads();  // the row buffers are rewritten by the next group
+  }
+}
+
 int triple_ok(const sufhip_triple2& t) {
   return t.a[0] && t.a[1] && t.b[0] && t.b[1] && t.c[0] && t.c[1];
 }
@@ -221,6 +429,76 @@ int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
   else
     hipLaunchKernelGGL(layernorm2_kernel<kLnMaxPer>, dim3(grid), dim3(kLnBlock), 0, s, A);
   return check_launch("layernorm2_kernel");
+}
+
+
+int sufhip_softmax2(const sufhip_softmax2_args* args, void* stream) {
+  SUFHIP_REQUIRE(args != nullptr, "sufhip_softmax2: null args");
+  const sufhip_softmax2_args& g = *args;
+  SUFHIP_REQUIRE(g.rows >= 0, "sufhip_softmax2: rows < 0");
+  SUFHIP_REQUIRE(g.max_row >= 1 && g.max_row <= kSmMaxRow,
+                 "sufhip_softmax2: rows of 1..512 elements");
+  SUFHIP_REQUIRE(g.pre_truncs >= 0 && g.pre_truncs <= 2, "sufhip_softmax2: pre_truncs in [0, 2]");
+  SmArgs A{};
+  if (int rc = make_tree_keys<kSmRounds>(g.keys, g.rounds, g.max_row, "sufhip_softmax2", &A.keys))
+    return rc;
+  if (g.rows == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(g.d_row_offsets && (g.rounds == 0 || g.d_round_offsets),
+                 "sufhip_softmax2: null offsets");
+  SUFHIP_REQUIRE(g.nexp.kind == SUFHIP_CHAIN_CUBIC && g.recip.kind == SUFHIP_CHAIN_RECIP &&
+                     g.recip.n == size_t(g.rows),
+                 "sufhip_softmax2: nexp must be CUBIC and recip RECIP over rows elements");
+  const size_t n = g.nexp.n;
+  if (int rc = make_chain_args(g.nexp, false, "sufhip_softmax2 nexp", &A.nexp)) return rc;
+  if (int rc = make_chain_args(g.recip, false, "sufhip_softmax2 recip", &A.recip)) return rc;
+  if (int rc = check_operand(g.x, n, "sufhip_softmax2 x")) return rc;
+  SUFHIP_REQUIRE(g.x.t[0].p[0] != nullptr, "sufhip_softmax2: empty input operand");
+  for (int q = 0; q < g.pre_truncs; ++q)
+    if (int rc = table_epi(g.pre[q], n, "sufhip_softmax2 pre", &A.pre_tr[q])) return rc;
+  SUFHIP_REQUIRE(triple_ok(g.norm), "sufhip_softmax2: the norm triple is missing");
+  if (int rc = table_epi(g.tr_norm, n, "sufhip_softmax2 tr_norm", &A.tr_norm)) return rc;
+  SUFHIP_REQUIRE((g.out[0] == nullptr) == (g.out[1] == nullptr),
+                 "sufhip_softmax2: out needs both parties or neither");
+  SUFHIP_REQUIRE(g.out[0] || g.d_dense, "sufhip_softmax2: no output");
+  SUFHIP_REQUIRE(!g.d_dense || (g.dense_a[0] && g.dense_a[1] && g.dense_cols >= g.max_row),
+                 "sufhip_softmax2: the dense open needs both a shares and dense_cols >= max_row");
+  A.x = g.x;
+  A.pre = g.pre_truncs;
+  A.pre_mask[0] = g.pre_mask[0];
+  A.pre_mask[1] = g.pre_mask[1];
+  A.offs = g.d_row_offsets;
+  A.round_off = g.d_round_offsets;
+  A.rows = g.rows;
+  A.max_row = g.max_row;
+  A.norm = g.norm;
+  A.norm_mask = g.norm_mask;
+  A.out[0] = g.out[0];
+  A.out[1] = g.out[1];
+  A.dense = g.d_dense;
+  A.dense_a[0] = g.dense_a[0];
+  A.dense_a[1] = g.dense_a[1];
+  A.dense_cols = g.d_dense ? g.dense_cols : 0;
+  const size_t row_bytes = tree_row_words(g.max_row) * sizeof(uint64_t);
+  int waves = kSmWaves;
+  while (waves > 1 && sizeof(SmStatic) + size_t(waves) * row_bytes > kSmLdsCap) waves /= 2;
+  SUFHIP_REQUIRE(sizeof(SmStatic) + size_t(waves) * row_bytes <= kSmLdsCap,
+                 "sufhip_softmax2: rows too long for the workgroup's LDS");
+  A.waves = waves;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const int groups = (g.rows + waves - 1) / waves;
+  const int grid = groups < cus * 2 ? groups : cus * 2;
+  const dim3 block(64 * waves);
+  const size_t dyn = size_t(waves) * row_bytes;
+  hipStream_t s = as_stream(stream);
+  if (g.max_row <= 128)
+    hipLaunchKernelGGL(softmax2_kernel<2>, dim3(grid), block, dyn, s, A);
+  else if (g.max_row <= 256)
+    hipLaunchKernelGGL(softmax2_kernel<4>, dim3(grid), block, dyn, s, A);
+  else
+    hipLaunchKernelGGL(softmax2_kernel<8>, dim3(grid), block, dyn, s, A);
+  return check_launch("softmax2_kernel");
 }
 
 }  // extern "C"

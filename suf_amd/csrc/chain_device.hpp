@@ -59,6 +59,7 @@ struct ChainLds {
   uint4 rk[2][11];
   uint64_t cuts[2][kChainMaxIntervals];
   uint64_t pay[2][kChainMaxIntervals * kChainMaxWords];
+  uint32_t diff;  // nonzero: the two blobs' keystreams differ (chain_compare)
 };
 
 // Sources of an element's triple shares for product k, both parties:
@@ -67,8 +68,9 @@ struct ChainLds {
 // chain_loader loads each product's shares when it is reached (for the
 // element-parallel kernel, where other waves hide the latency and registers
 // set the occupancy).
-struct ChainPre {
-  uint64_t a[4][2], b[4][2], c[4][2];
+template <int kProds>
+struct ChainPreN {
+  uint64_t a[kProds][2], b[kProds][2], c[kProds][2];
   __device__ __forceinline__ void get(int k, uint64_t* a3, uint64_t* b3, uint64_t* c3) const {
     for (int p = 0; p < 2; ++p) {
       a3[p] = a[k][p];
@@ -76,17 +78,44 @@ struct ChainPre {
       c3[p] = c[k][p];
     }
   }
+  // Word w of 6 * kProds: (product, a | b | c, party).
+  __device__ __forceinline__ uint64_t& word(int w) {
+    const int k = w / 6, q = (w / 2) % 3, p = w & 1;
+    return (q == 0 ? a : (q == 1 ? b : c))[k][p];
+  }
 };
+using ChainPre = ChainPreN<4>;
+
+// The triple word w (see ChainPreN::word) of element i.
+__device__ __forceinline__ uint64_t chain_triple_word(const ChainArgs& A, int w, size_t i) {
+  const int k = w / 6, q = (w / 2) % 3, p = w & 1;
+  return term_at(q == 0 ? A.a[k] : (q == 1 ? A.b[k] : A.c[k]), p, i);
+}
+
+// All products' triple shares of element i in registers.
+template <int kProds>
+__device__ __forceinline__ ChainPreN<kProds> chain_prefetch(const ChainArgs& A, size_t i) {
+  ChainPreN<kProds> P;
+#pragma unroll
+  for (int k = 0; k < kProds; ++k)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      P.a[k][p] = term_at(A.a[k], p, i);
+      P.b[k][p] = term_at(A.b[k], p, i);
+      P.c[k][p] = term_at(A.c[k], p, i);
+    }
+  return P;
+}
 
 template <int kKind>
 struct chain_loader {
-  const ChainArgs& A;
+  const ChainArgs* A;
   size_t i;
   __device__ __forceinline__ void get(int k, uint64_t* a3, uint64_t* b3, uint64_t* c3) const {
     for (int p = 0; p < 2; ++p) {
-      a3[p] = term_at(A.a[k], p, i);
-      b3[p] = term_at(A.b[k], p, i);
-      c3[p] = term_at(A.c[k], p, i);
+      a3[p] = term_at(A->a[k], p, i);
+      b3[p] = term_at(A->b[k], p, i);
+      c3[p] = term_at(A->c[k], p, i);
     }
   }
 };
@@ -96,10 +125,16 @@ constexpr int chain_products() {
   return kKind == SUFHIP_CHAIN_RSQRT ? 4 : 3;
 }
 
-// Per-party LUT header fields: input mask, keystream nonce, party.
+// Per-party LUT header fields: input mask, keystream nonce, party; and
+// whether both parties' blobs carry the same AES key, nonce, input mask and
+// cut points.  SUF's dealer derives one key per gate (seed_from_id,
+// cuda/pfss_backend_gpu.cu:508-515): party 0's share is the keystream and
+// party 1's the payload row minus it, so with both parties in one process
+// one keystream block serves both.
 struct ChainKeyInfo {
   uint64_t m[2], nonce[2];
   int party[2];
+  bool same_ks;
 };
 
 __device__ __forceinline__ uint64_t chain_mask_bits(int bits) {
@@ -107,28 +142,77 @@ __device__ __forceinline__ uint64_t chain_mask_bits(int bits) {
 }
 
 // Cooperative staging (every thread of the workgroup); the caller syncs.
+// Each thread handles a flat range of (party, round key | cut | payload word)
+// items, all loads issued before the stores.
 __device__ __forceinline__ void chain_stage(const ChainArgs& A, int W, ChainLds& L) {
   const int nint = A.intervals;
-  for (int p = 0; p < 2; ++p) {
-    const uint8_t* k = A.lut[p];
-    const uint32_t* rkg = reinterpret_cast<const uint32_t*>(k + 40);
-    for (int i = threadIdx.x; i < 11; i += blockDim.x)
-      L.rk[p][i] = make_uint4(rkg[4 * i], rkg[4 * i + 1], rkg[4 * i + 2], rkg[4 * i + 3]);
-    const uint64_t* cg = reinterpret_cast<const uint64_t*>(k + kChainLutHdr);
-    const uint64_t* pg = cg + (nint + 1);
-    for (int i = threadIdx.x; i < nint; i += blockDim.x) L.cuts[p][i] = cg[i];
-    for (int i = threadIdx.x; i < nint * W; i += blockDim.x) L.pay[p][i] = pg[i];
+  if (threadIdx.x == 0) L.diff = 0;
+  const int per = 11 + nint + nint * W;  // items per party
+  for (int base = 0; base < 2 * per; base += 4 * blockDim.x) {
+    uint4 v[4];
+    int item[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      item[u] = base + u * blockDim.x + threadIdx.x;
+      if (item[u] >= 2 * per) continue;
+      const int p = item[u] / per, w = item[u] % per;
+      const uint8_t* k = A.lut[p];
+      const uint64_t* cg = reinterpret_cast<const uint64_t*>(k + kChainLutHdr);
+      if (w < 11) {
+        const uint32_t* rkg = reinterpret_cast<const uint32_t*>(k + 40) + 4 * w;
+        v[u] = make_uint4(rkg[0], rkg[1], rkg[2], rkg[3]);
+      } else {
+        const uint64_t x = w < 11 + nint ? cg[w - 11] : cg[nint + 1 + (w - 11 - nint)];
+        v[u] = make_uint4(uint32_t(x), uint32_t(x >> 32), 0, 0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (item[u] >= 2 * per) continue;
+      const int p = item[u] / per, w = item[u] % per;
+      const uint64_t x = uint64_t(v[u].x) | uint64_t(v[u].y) << 32;
+      if (w < 11)
+        L.rk[p][w] = v[u];
+      else if (w < 11 + nint)
+        L.cuts[p][w - 11] = x;
+      else
+        L.pay[p][w - 11 - nint] = x;
+    }
   }
 }
 
 
-__device__ __forceinline__ ChainKeyInfo chain_key_info(const ChainArgs& A) {
+// Between the staging barrier and the next one (every thread): one staged
+// word pair per lane (round keys, cut points, header), a difference sets
+// L.diff.
+__device__ __forceinline__ void chain_compare(const ChainArgs& A, ChainLds& L) {
+  const int nint = A.intervals;
+  for (int t = threadIdx.x; t < 12 + nint; t += blockDim.x) {
+    bool differ;
+    if (t < 11) {
+      const uint4 a = L.rk[0][t], b = L.rk[1][t];
+      differ = ((a.x ^ b.x) | (a.y ^ b.y) | (a.z ^ b.z) | (a.w ^ b.w)) != 0;
+    } else if (t == 11) {
+      const uint64_t* h0 = reinterpret_cast<const uint64_t*>(A.lut[0]);
+      const uint64_t* h1 = reinterpret_cast<const uint64_t*>(A.lut[1]);
+      differ = h0[2] != h1[2] || (h0[0] & 0xffff) != (h1[0] & 0xffff);  // nonce, in_bits
+    } else {
+      differ = L.cuts[0][t - 12] != L.cuts[1][t - 12];
+    }
+    if (differ) atomicOr(&L.diff, 1u);
+  }
+}
+
+// After the barrier that follows chain_compare: the header fields and the
+// shared-keystream test.
+__device__ __forceinline__ ChainKeyInfo chain_key_info(const ChainArgs& A, const ChainLds& L) {
   ChainKeyInfo K;
   for (int p = 0; p < 2; ++p) {
     K.m[p] = chain_mask_bits(*reinterpret_cast<const uint16_t*>(A.lut[p]));
     K.party[p] = A.lut[p][8];
     K.nonce[p] = *reinterpret_cast<const uint64_t*>(A.lut[p] + 16);
   }
+  K.same_ks = L.diff == 0;
   return K;
 }
 
@@ -149,62 +233,152 @@ __device__ __forceinline__ Two chain_trunc(const ChainArgs& A, int j, Two z) {
               trunc_table_eval(A.tkey[j][1], A.ttab[j][1], A.tf[j], zh)}};
 }
 
-// The whole chain for element i with input shares x, its triple shares
-// from P (ChainPre or chain_loader).
+// The whole chain for M elements at once (element m: index i[m], input
+// shares x[m], triple shares from P[m], a ChainPreN or chain_loader), results
+// in out[m].  Every step runs for all M elements before the next, so the
+// LUT's AES blocks (both parties, W / 2 blocks each, per element) are
+// encrypted in lockstep and the truncations' table reads of a step are in
+// flight together: a lane pays one latency per step, not one per element and
+// party.
+template <int kKind, int kCopies, int M, class Src>
+__device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds& L,
+                                             const ChainKeyInfo& K, const AesLds<kCopies>& aes,
+                                             const size_t (&i)[M], const Two (&x)[M],
+                                             const Src (&P)[M], Two (&out)[M]) {
+  constexpr int W = kKind == SUFHIP_CHAIN_CUBIC ? 4 : 2;
+  constexpr int NB = W / 2;  // AES blocks per element and party
+  constexpr int NS = M * NB;  // blocks per party
+  const int nint = A.intervals, f = A.f;
+  int iv[M][2];
+  uint32_t st[2][NS][4];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const uint64_t xh = x[m].v[0] + x[m].v[1] + A.lut_mask;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const uint64_t xm = xh & K.m[p];
+      int lo = 0, hi = nint;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if ((L.cuts[p][mid] & K.m[p]) <= xm)
+          lo = mid + 1;
+        else
+          hi = mid;
+      }
+      iv[m][p] = lo - 1 < 0 ? 0 : lo - 1;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint64_t ctr =
+            K.nonce[p] ^ (uint64_t(i[m]) << 32) ^ (uint64_t(iv[m][p]) * W + uint64_t(2 * b));
+        st[p][m * NB + b][0] = uint32_t(ctr);
+        st[p][m * NB + b][1] = uint32_t(ctr >> 32);
+        st[p][m * NB + b][2] = 0;
+        st[p][m * NB + b][3] = 0;
+      }
+    }
+  }
+  // Party 0's blocks, at most four in lockstep (more keep too many table
+  // reads in flight for the register file); party 1's only where its
+  // keystream differs (never for blobs from one dealer key).
+  constexpr int kLock = NS < 4 ? NS : 4;
+  bool own1 = !K.same_ks;
+#pragma unroll
+  for (int m = 0; m < M; ++m) own1 = own1 || iv[m][0] != iv[m][1];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    if (p == 1 && !own1) continue;
+#pragma unroll
+    for (int n0 = 0; n0 < NS; n0 += kLock) {
+      uint32_t sub[kLock][4];
+      const uint4* subk[kLock];
+#pragma unroll
+      for (int u = 0; u < kLock; ++u) {
+        subk[u] = L.rk[p];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sub[u][q] = st[p][n0 + u][q];
+      }
+      aes.template encrypt_n<kLock>(sub, subk);
+#pragma unroll
+      for (int u = 0; u < kLock; ++u)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) st[p][n0 + u][q] = sub[u][q];
+    }
+  }
+  uint64_t cf[M][2][W];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int n = m * NB + b;  // party p's block, or party 0's when shared
+        const bool mine = p == 1 && own1;
+        const uint64_t k0 = uint64_t(mine ? st[1][n][0] : st[0][n][0]) |
+                            uint64_t(mine ? st[1][n][1] : st[0][n][1]) << 32;
+        const uint64_t k1 = uint64_t(mine ? st[1][n][2] : st[0][n][2]) |
+                            uint64_t(mine ? st[1][n][3] : st[0][n][3]) << 32;
+        const uint64_t* row = L.pay[p] + size_t(iv[m][p]) * W;
+        cf[m][p][2 * b] = K.party[p] == 0 ? k0 : row[2 * b] - k0;
+        cf[m][p][2 * b + 1] = K.party[p] == 0 ? k1 : row[2 * b + 1] - k1;
+      }
+  Two t1[M], t2[M];
+  if constexpr (kKind == SUFHIP_CHAIN_CUBIC) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      Two mm = chain_beaver(P[m], 0, Two{{cf[m][0][3], cf[m][1][3]}}, x[m]);
+      mm.v[0] += cf[m][0][2] << f;
+      mm.v[1] += cf[m][1][2] << f;
+      t1[m] = chain_trunc(A, 0, chain_beaver(P[m], 1, mm, x[m]));
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const Two q{{t1[m].v[0] + (cf[m][0][1] << f), t1[m].v[1] + (cf[m][1][1] << f)}};
+      t2[m] = chain_trunc(A, 1, chain_beaver(P[m], 2, q, x[m]));
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      out[m] = chain_trunc(
+          A, 2, Two{{t2[m].v[0] + (cf[m][0][0] << f), t2[m].v[1] + (cf[m][1][0] << f)}});
+  } else {
+    Two y[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const Two t = chain_trunc(A, 0, chain_beaver(P[m], 0, Two{{cf[m][0][1], cf[m][1][1]}}, x[m]));
+      y[m] = Two{{t.v[0] + cf[m][0][0], t.v[1] + cf[m][1][0]}};
+    }
+    if constexpr (kKind == SUFHIP_CHAIN_RECIP) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) t1[m] = chain_trunc(A, 1, chain_beaver(P[m], 1, y[m], x[m]));
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const Two two{{(uint64_t(2) << f) - t1[m].v[0], uint64_t(0) - t1[m].v[1]}};
+        out[m] = chain_trunc(A, 2, chain_beaver(P[m], 2, y[m], two));
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < M; ++m) t1[m] = chain_trunc(A, 1, chain_beaver(P[m], 1, y[m], y[m]));
+#pragma unroll
+      for (int m = 0; m < M; ++m) t2[m] = chain_trunc(A, 2, chain_beaver(P[m], 2, x[m], t1[m]));
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const Two inner{{(uint64_t(3) << (f - 1)) - t2[m].v[0], uint64_t(0) - t2[m].v[1]}};
+        out[m] = chain_trunc(A, 3, chain_beaver(P[m], 3, y[m], inner));
+      }
+    }
+  }
+}
+
+// The whole chain for one element (chain_eval_m with M = 1).
 template <int kKind, int kCopies, class Src>
 __device__ __forceinline__ Two chain_eval(const ChainArgs& A, const ChainLds& L,
                                           const ChainKeyInfo& K, const AesLds<kCopies>& aes,
                                           size_t i, Two x, const Src& P) {
-  constexpr int W = kKind == SUFHIP_CHAIN_CUBIC ? 4 : 2;
-  const int nint = A.intervals, f = A.f;
-  const uint64_t xh = x.v[0] + x.v[1] + A.lut_mask;
-  uint64_t cf[2][W];
-  for (int p = 0; p < 2; ++p) {
-    const uint64_t xm = xh & K.m[p];
-    int lo = 0, hi = nint;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if ((L.cuts[p][mid] & K.m[p]) <= xm)
-        lo = mid + 1;
-      else
-        hi = mid;
-    }
-    int iv = lo - 1;
-    if (iv < 0) iv = 0;
-#pragma unroll
-    for (int w = 0; w < W; w += 2) {
-      const uint64_t ctr = K.nonce[p] ^ (uint64_t(i) << 32) ^ (uint64_t(iv) * W + uint64_t(w));
-      uint32_t s0 = uint32_t(ctr), s1 = uint32_t(ctr >> 32), s2 = 0, s3 = 0;
-      aes.encrypt(s0, s1, s2, s3, L.rk[p]);
-      const uint64_t k0 = uint64_t(s0) | uint64_t(s1) << 32;
-      const uint64_t k1 = uint64_t(s2) | uint64_t(s3) << 32;
-      const uint64_t* row = L.pay[p] + size_t(iv) * W;
-      cf[p][w] = K.party[p] == 0 ? k0 : row[w] - k0;
-      cf[p][w + 1] = K.party[p] == 0 ? k1 : row[w + 1] - k1;
-    }
-  }
-  if constexpr (kKind == SUFHIP_CHAIN_CUBIC) {
-    Two mm = chain_beaver(P, 0, Two{{cf[0][3], cf[1][3]}}, x);
-    mm.v[0] += cf[0][2] << f;
-    mm.v[1] += cf[1][2] << f;
-    const Two y = chain_trunc(A, 0, chain_beaver(P, 1, mm, x));
-    const Two q{{y.v[0] + (cf[0][1] << f), y.v[1] + (cf[1][1] << f)}};
-    const Two y2 = chain_trunc(A, 1, chain_beaver(P, 2, q, x));
-    return chain_trunc(A, 2, Two{{y2.v[0] + (cf[0][0] << f), y2.v[1] + (cf[1][0] << f)}});
-  } else {
-    const Two t = chain_trunc(A, 0, chain_beaver(P, 0, Two{{cf[0][1], cf[1][1]}}, x));
-    const Two y{{t.v[0] + cf[0][0], t.v[1] + cf[1][0]}};
-    if constexpr (kKind == SUFHIP_CHAIN_RECIP) {
-      const Two xy = chain_trunc(A, 1, chain_beaver(P, 1, y, x));
-      const Two two{{(uint64_t(2) << f) - xy.v[0], uint64_t(0) - xy.v[1]}};
-      return chain_trunc(A, 2, chain_beaver(P, 2, y, two));
-    } else {
-      const Two y2 = chain_trunc(A, 1, chain_beaver(P, 1, y, y));
-      const Two h = chain_trunc(A, 2, chain_beaver(P, 2, x, y2));
-      const Two inner{{(uint64_t(3) << (f - 1)) - h.v[0], uint64_t(0) - h.v[1]}};
-      return chain_trunc(A, 3, chain_beaver(P, 3, y, inner));
-    }
-  }
+  const size_t ii[1] = {i};
+  const Two xx[1] = {x};
+  const Src pp[1] = {P};
+  Two out[1];
+  chain_eval_m<kKind, kCopies, 1>(A, L, K, aes, ii, xx, pp, out);
+  return out[0];
 }
 
 // Host: validates a chain's arguments for n elements and converts them.

@@ -26,12 +26,14 @@ __global__ void __launch_bounds__(kBlock) gate_chain_kernel(ChainArgs A) {
   fill_ttable<kCopies>(tab, kTDev.v);
   chain_stage(A, W, L);
   __syncthreads();
+  chain_compare(A, L);
+  __syncthreads();
   const AesLds<kCopies> aes{tab, threadIdx.x % kCopies};
-  const ChainKeyInfo K = chain_key_info(A);
+  const ChainKeyInfo K = chain_key_info(A, L);
   for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < A.n;
        i += size_t(gridDim.x) * kBlock) {
     const Two x{{operand_at(A.x, 0, i), operand_at(A.x, 1, i)}};
-    const Two res = chain_eval<kKind, kCopies>(A, L, K, aes, i, x, chain_loader<kKind>{A, i});
+    const Two res = chain_eval<kKind, kCopies>(A, L, K, aes, i, x, chain_loader<kKind>{&A, i});
     A.out[0][i] = res.v[0];
     A.out[1][i] = res.v[1];
   }

@@ -26,6 +26,7 @@
 
 #include "aes_lds.hpp"
 #include "operand_device.hpp"
+#include "relu_tree_device.hpp"
 #include "sufhip_internal.hpp"
 
 namespace sufhip {
@@ -385,18 +386,10 @@ __global__ void __launch_bounds__(kLutBlock) lut_bcast2_kernel(Lut2Args a) {
 }
 
 // The whole pairwise-max tree of RowMaxDiffTask in one launch: each
-// wavefront of a workgroup owns one row (groups of kTreeWaves rows, grid-
-// stride), keeps both parties' current level of the row in LDS and runs every
-// round with that round's ReLU LUT keys (staged in LDS once per workgroup).
-// A lane works on one (slot, party) item, so one AES block per item; the
-// keystream counters are the per-round kernel's (slot j = the row's offset in
-// that round's output + pair index).  Then writes delta = max - x.  Level 0
-// of a row (its inputs) and the odd levels live in two buffers, [party]
-// [max_row] and [party][ceil(max_row / 2)], in dynamic LDS; a level never
-// outgrows the buffer it is written to.  Every wave runs the same number of
-// rounds, so the workgroup barriers are uniform.
+// wavefront of a workgroup owns one row (groups of `waves` rows, grid-
+// stride), runs every round (relu_tree_device.hpp) and writes
+// delta = max - x.
 constexpr int kTreeRounds = 16;
-constexpr int kTreeIntervals = 8;
 constexpr int kTreeMaxRow = 512;
 constexpr int kTreeCopies = kLutCopies;
 constexpr int kTreeWaves = 4;
@@ -407,10 +400,7 @@ struct ReluTreeArgs {
   uint64_t* delta[2];
   const int32_t* offs;       // [rows + 1]
   const int32_t* round_off;  // [rounds][rows]: the row's first output slot per round
-  const uint8_t* key[kTreeRounds][2];
-  uint64_t mask[kTreeRounds];
-  int intervals[kTreeRounds];
-  int rounds;
+  TreeKeys<kTreeRounds> keys;
   int rows;
   int max_row;
   int waves;  // rows per workgroup (1, 2 or 4); blockDim.x == 64 * waves
@@ -418,45 +408,22 @@ struct ReluTreeArgs {
 
 struct ReluTreeStatic {
   uint32_t tab[256 * kTreeCopies];
-  uint4 rk[kTreeRounds][2][11];
-  uint64_t cuts[kTreeRounds][2][kTreeIntervals];
-  uint64_t pay[kTreeRounds][2][2 * kTreeIntervals];
-  uint64_t nonce[kTreeRounds][2];
-  uint64_t in_mask[kTreeRounds][2];
-  int party[kTreeRounds][2];
+  TreeLds<kTreeRounds> t;
+  uint32_t j0[kTreeWaves][kTreeRounds];
 };
-
-// Dynamic LDS words (u64) per wave for rows of up to max_row elements.
-__host__ __device__ inline size_t tree_row_words(int max_row) {
-  return size_t(2) * (size_t(max_row) + size_t(max_row + 1) / 2);
-}
 
 __global__ void __launch_bounds__(64 * kTreeWaves) relu_max_tree2_kernel(ReluTreeArgs a) {
   __shared__ __align__(16) ReluTreeStatic st;
   extern __shared__ uint64_t rowbuf[];
-  const int mr = a.max_row, half = (mr + 1) / 2;
+  const int mr = a.max_row;
   fill_ttable<kTreeCopies>(st.tab, kTDev.v);
-  for (int k = 0; k < a.rounds; ++k) {
-    for (int p = 0; p < 2; ++p) {
-      const uint8_t* key = a.key[k][p];
-      const int nint = a.intervals[k];
-      const uint32_t* rkg = reinterpret_cast<const uint32_t*>(key + 40);
-      for (int i = threadIdx.x; i < 11; i += blockDim.x)
-        st.rk[k][p][i] = make_uint4(rkg[4 * i], rkg[4 * i + 1], rkg[4 * i + 2], rkg[4 * i + 3]);
-      const uint64_t* cg = reinterpret_cast<const uint64_t*>(key + kLutHdr);
-      for (int i = threadIdx.x; i < nint; i += blockDim.x) st.cuts[k][p][i] = cg[i];
-      for (int i = threadIdx.x; i < 2 * nint; i += blockDim.x) st.pay[k][p][i] = cg[nint + 1 + i];
-      if (threadIdx.x == 0) {
-        st.nonce[k][p] = ld64(key + 16);
-        st.in_mask[k][p] = mask_bits(*reinterpret_cast<const uint16_t*>(key));
-        st.party[k][p] = key[8];
-      }
-    }
-  }
+  tree_stage(a.keys, st.t);
+  __syncthreads();
+  tree_compare(a.keys, st.t);
   __syncthreads();
   const AesLds<kTreeCopies> aes{st.tab, threadIdx.x % kTreeCopies};
+  const uint32_t shared = ~st.t.diff;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  // This wave's buffers: level-0/even [2][mr], odd [2][half].
   uint64_t* even = rowbuf + size_t(wave) * tree_row_words(mr);
   uint64_t* odd = even + 2 * size_t(mr);
   for (int g = blockIdx.x; g * a.waves < a.rows; g += gridDim.x) {
@@ -467,52 +434,18 @@ __global__ void __launch_bounds__(64 * kTreeWaves) relu_max_tree2_kernel(ReluTre
       full = a.offs[r + 1] - b;
       if (full < 1 || full > mr) full = 0;  // refused on the host
     }
+    tree_row_offsets(a.keys, a.round_off, a.rows, r, full, st.j0[wave]);
     for (int i = lane; i < full; i += 64) {
       even[i] = a.x[0][b + i];
       even[mr + i] = a.x[1][b + i];
     }
     __syncthreads();
-    int len = full, level = 0;
-    for (int k = 0; k < a.rounds; ++k) {
-      if (len > 1) {
-        const uint64_t* src = (level & 1) ? odd : even;
-        const int sw = (level & 1) ? half : mr;  // party stride of src
-        uint64_t* dst = (level & 1) ? even : odd;
-        const int dw = (level & 1) ? mr : half;
-        const int pairs = len >> 1, nlen = (len + 1) >> 1;
-        const uint32_t j0 = uint32_t(a.round_off[size_t(k) * a.rows + r]);
-        for (int i = lane; i < 2 * nlen; i += 64) {
-          const int t = i >> 1, p = i & 1;
-          uint64_t o;
-          if (t < pairs) {
-            const uint64_t xa0 = src[2 * t], xb0 = src[2 * t + 1];
-            const uint64_t xa1 = src[sw + 2 * t], xb1 = src[sw + 2 * t + 1];
-            const uint64_t xhat = (xa0 - xb0) + (xa1 - xb1) + a.mask[k];
-            const uint64_t m = st.in_mask[k][p];
-            const int iv = interval_of(xhat & m, a.intervals[k], m,
-                                       [&](int c) { return st.cuts[k][p][c]; });
-            const uint64_t ctr = st.nonce[k][p] ^ (uint64_t(j0 + t) << 32) ^ (uint64_t(iv) * 2);
-            uint32_t s0 = uint32_t(ctr), s1 = uint32_t(ctr >> 32), s2 = 0, s3 = 0;
-            aes.encrypt(s0, s1, s2, s3, st.rk[k][p]);
-            const uint64_t k0 = uint64_t(s0) | uint64_t(s1) << 32;
-            const uint64_t k1 = uint64_t(s2) | uint64_t(s3) << 32;
-            const bool p0 = st.party[k][p] == 0;
-            const uint64_t q0 = p0 ? k0 : st.pay[k][p][2 * iv] - k0;
-            const uint64_t q1 = p0 ? k1 : st.pay[k][p][2 * iv + 1] - k1;
-            o = (p ? xb1 : xb0) + q0 + q1 * xhat;
-          } else {
-            o = src[p * sw + 2 * t];
-          }
-          dst[p * dw + t] = o;
-        }
-        len = nlen;
-        ++level;
-      }
-      __syncthreads();
-    }
+    const int level =
+        tree_row<kTreeRounds, kTreeCopies>(a.keys, st.t, aes, even, odd, mr, full, st.j0[wave],
+                                           shared);
     if (full > 0) {
       const uint64_t* fin = (level & 1) ? odd : even;
-      const int fw = (level & 1) ? half : mr;
+      const int fw = (level & 1) ? (mr + 1) / 2 : mr;
       const uint64_t m0 = fin[0], m1 = fin[fw];
       for (int i = lane; i < full; i += 64) {
         a.delta[0][b + i] = m0 - a.x[0][b + i];
@@ -687,38 +620,25 @@ int sufhip_relu_max_tree2(const uint64_t* d_x0, const uint64_t* d_x1, int rows,
                           const int32_t* d_row_offsets, int max_row, int rounds,
                           const int32_t* d_round_offsets, const sufhip_relu_round_key* keys,
                           uint64_t* d_delta0, uint64_t* d_delta1, void* stream) {
-  SUFHIP_REQUIRE(rows >= 0 && rounds >= 0 && rounds <= kTreeRounds,
-                 "sufhip_relu_max_tree2: rounds in [0, 16]");
+  SUFHIP_REQUIRE(rows >= 0, "sufhip_relu_max_tree2: rows < 0");
   SUFHIP_REQUIRE(max_row >= 1 && max_row <= kTreeMaxRow,
                  "sufhip_relu_max_tree2: rows of 1..512 elements");
-  SUFHIP_REQUIRE((1 << rounds) >= max_row, "sufhip_relu_max_tree2: too few rounds for max_row");
+  ReluTreeArgs a{};
+  if (int rc = make_tree_keys<kTreeRounds>(keys, rounds, max_row, "sufhip_relu_max_tree2",
+                                           &a.keys))
+    return rc;
   if (rows == 0) return SUFHIP_OK;
   SUFHIP_REQUIRE(d_x0 && d_x1 && d_row_offsets && d_delta0 && d_delta1 &&
-                     (rounds == 0 || (d_round_offsets && keys)),
+                     (rounds == 0 || d_round_offsets),
                  "sufhip_relu_max_tree2: null pointer");
-  ReluTreeArgs a{};
   a.x[0] = d_x0;
   a.x[1] = d_x1;
   a.delta[0] = d_delta0;
   a.delta[1] = d_delta1;
   a.offs = d_row_offsets;
   a.round_off = d_round_offsets;
-  a.rounds = rounds;
   a.rows = rows;
   a.max_row = max_row;
-  for (int k = 0; k < rounds; ++k) {
-    const sufhip_relu_round_key& rk = keys[k];
-    SUFHIP_REQUIRE(rk.intervals >= 1 && rk.intervals <= kTreeIntervals &&
-                       rk.key_bytes == sufhip_interval_lut_key_bytes(rk.intervals, 2),
-                   "sufhip_relu_max_tree2: a round's LUT geometry is invalid");
-    SUFHIP_REQUIRE(rk.key[0] && rk.key[1] && (reinterpret_cast<uintptr_t>(rk.key[0]) & 7) == 0 &&
-                       (reinterpret_cast<uintptr_t>(rk.key[1]) & 7) == 0,
-                   "sufhip_relu_max_tree2: round keys must be non-null and 8-byte aligned");
-    a.key[k][0] = rk.key[0];
-    a.key[k][1] = rk.key[1];
-    a.mask[k] = rk.mask;
-    a.intervals[k] = rk.intervals;
-  }
   // Rows per workgroup: as many (4, 2, 1) as fit the LDS cap beside the
   // staged table and keys.
   const size_t row_bytes = tree_row_words(max_row) * sizeof(uint64_t);

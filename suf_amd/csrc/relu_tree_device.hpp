@@ -1,0 +1,281 @@
+// The pairwise-max tree of RowMaxDiffTask (include/nn/row_maxdiff_task.hpp:
+// 49-165) over one row per wavefront, both parties: max(a, b) = b + ReLU(a -
+// b), the ReLU as an interval LUT of its public-x^ coefficients (2 words,
+// AES-CTR keystream, pfss_kernels.cu:545-719).  Shared by the tree kernel
+// (lut.hip) and the softmax row block (blocks.hip).
+//
+// A lane works on one (slot, party) item, so one AES block per item; the
+// keystream counters are those of the per-round evaluation (slot j = the
+// row's offset in that round's output + pair index).  Level 0 of a row (its
+// inputs) and the odd levels live in two LDS buffers per wave, [party]
+// [max_row] and [party][ceil(max_row / 2)]; a level never outgrows the buffer
+// it is written to.  Every wave of a workgroup runs the same number of
+// rounds, so the workgroup barriers inside are uniform.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "aes_lds.hpp"
+#include "suf_hip.h"
+#include "sufhip_internal.hpp"
+
+namespace sufhip {
+
+constexpr int kTreeIntervals = 8;
+constexpr size_t kTreeLutHdr = 216;
+
+template <int kRounds>
+struct TreeKeys {
+  const uint8_t* key[kRounds][2];
+  uint64_t mask[kRounds];
+  int intervals[kRounds];
+  int rounds;
+};
+
+template <int kRounds>
+struct TreeLds {
+  uint4 rk[kRounds][2][11];
+  uint64_t cuts[kRounds][2][kTreeIntervals];
+  uint64_t pay[kRounds][2][2 * kTreeIntervals];
+  uint64_t nonce[kRounds][2];
+  uint64_t in_mask[kRounds][2];
+  int party[kRounds][2];
+  uint32_t diff;  // bit k: round k's two blobs differ (tree_compare)
+};
+
+// Dynamic LDS words (u64) per wave for rows of up to max_row elements.
+__host__ __device__ inline size_t tree_row_words(int max_row) {
+  return size_t(2) * (size_t(max_row) + size_t(max_row + 1) / 2);
+}
+
+// Cooperative staging of every round's keys (all threads); the caller syncs.
+// A thread owns one (party, item) of every round: a round key, a cut point
+// or payload word, or the header fields.  Its loads of all rounds are
+// unrolled and issued before its LDS stores (the round count is uniform),
+// so the staging costs about one memory round trip.
+template <int kRounds>
+__device__ __forceinline__ void tree_stage(const TreeKeys<kRounds>& K, TreeLds<kRounds>& L) {
+  constexpr int kItems = 11 + 3 * kTreeIntervals + 1;
+  if (threadIdx.x == 0) L.diff = 0;
+  for (int it = threadIdx.x; it < 2 * kItems; it += blockDim.x) {
+    const int p = it / kItems, w = it % kItems;
+    if (w < 11) {
+      uint4 v[kRounds];
+#pragma unroll
+      for (int k = 0; k < kRounds; ++k)
+        if (k < K.rounds) {
+          const uint32_t* rkg =
+              reinterpret_cast<const uint32_t*>((p ? K.key[k][1] : K.key[k][0]) + 40) + 4 * w;
+          v[k] = make_uint4(rkg[0], rkg[1], rkg[2], rkg[3]);
+        }
+#pragma unroll
+      for (int k = 0; k < kRounds; ++k)
+        if (k < K.rounds) L.rk[k][p][w] = v[k];
+    } else if (w < 11 + 3 * kTreeIntervals) {
+      const int c = w - 11;  // cut c (< nint), or payload word c - kTreeIntervals (< 2 nint)
+      uint64_t v[kRounds];
+#pragma unroll
+      for (int k = 0; k < kRounds; ++k)
+        if (k < K.rounds) {
+          const int nint = K.intervals[k];
+          const bool cut = c < kTreeIntervals;
+          const bool valid = cut ? c < nint : c - kTreeIntervals < 2 * nint;
+          const int idx = !valid ? 0 : (cut ? c : nint + 1 + (c - kTreeIntervals));
+          const uint64_t* cg =
+              reinterpret_cast<const uint64_t*>((p ? K.key[k][1] : K.key[k][0]) + kTreeLutHdr);
+          v[k] = cg[idx];
+          if (!valid) v[k] = 0;
+        }
+#pragma unroll
+      for (int k = 0; k < kRounds; ++k)
+        if (k < K.rounds) {
+          if (c < kTreeIntervals)
+            L.cuts[k][p][c] = v[k];
+          else
+            L.pay[k][p][c - kTreeIntervals] = v[k];
+        }
+    } else {
+      uint64_t h0[kRounds], h1[kRounds], h2[kRounds];
+#pragma unroll
+      for (int k = 0; k < kRounds; ++k)
+        if (k < K.rounds) {
+          const uint64_t* hw = reinterpret_cast<const uint64_t*>(p ? K.key[k][1] : K.key[k][0]);
+          h0[k] = hw[0];  // in_bits in the low 16 bits
+          h1[k] = hw[1];  // party in the low byte
+          h2[k] = hw[2];  // keystream nonce
+        }
+#pragma unroll
+      for (int k = 0; k < kRounds; ++k)
+        if (k < K.rounds) {
+          const int bits = int(h0[k] & 0xffff);
+          L.nonce[k][p] = h2[k];
+          L.in_mask[k][p] =
+              bits <= 0 ? 0 : (bits >= 64 ? ~uint64_t(0) : (uint64_t(1) << bits) - 1);
+          L.party[k][p] = int(h1[k] & 0xff);
+        }
+    }
+  }
+}
+
+// Loads row r's slot offset of every round (round_off[k * rows + r]) into
+// j0[k], one round per lane; call before the barrier that precedes tree_row.
+template <int kRounds>
+__device__ __forceinline__ void tree_row_offsets(const TreeKeys<kRounds>& K,
+                                                 const int32_t* round_off, int rows, int r,
+                                                 int len, uint32_t* j0) {
+  const int lane = threadIdx.x & 63;
+  if (len > 1 && lane < K.rounds) j0[lane] = uint32_t(round_off[size_t(lane) * rows + r]);
+}
+
+// Between the staging barrier and the next one (every thread): one staged
+// word pair per lane, a difference sets round k's bit of L.diff.  After
+// that barrier, bit k of ~L.diff says that round k's two blobs carry the
+// same AES key, nonce, input mask and cut points (SUF's dealer derives one
+// key per gate, cuda/pfss_backend_gpu.cu:508-515), so that one keystream
+// block serves both parties of a slot.  tree_stage zeroes L.diff.
+template <int kRounds>
+__device__ __forceinline__ void tree_compare(const TreeKeys<kRounds>& K, TreeLds<kRounds>& L) {
+  constexpr int kPer = 11 + kTreeIntervals + 1;  // round key words, cuts, header
+  for (int t = threadIdx.x; t < K.rounds * kPer; t += blockDim.x) {
+    const int k = t / kPer, w = t % kPer;
+    bool differ;
+    if (w < 11) {
+      const uint4 a = L.rk[k][0][w], b = L.rk[k][1][w];
+      differ = ((a.x ^ b.x) | (a.y ^ b.y) | (a.z ^ b.z) | (a.w ^ b.w)) != 0;
+    } else if (w < 11 + kTreeIntervals) {
+      const int c = w - 11;
+      differ = c < K.intervals[k] && L.cuts[k][0][c] != L.cuts[k][1][c];
+    } else {
+      differ = L.nonce[k][0] != L.nonce[k][1] || L.in_mask[k][0] != L.in_mask[k][1];
+    }
+    if (differ) atomicOr(&L.diff, 1u << k);
+  }
+}
+
+// Interval of xhat in round k's cut points of party p (upper bound minus one).
+template <int kRounds>
+__device__ __forceinline__ int tree_interval(const TreeKeys<kRounds>& K,
+                                             const TreeLds<kRounds>& L, int k, int p,
+                                             uint64_t xhat) {
+  const uint64_t m = L.in_mask[k][p];
+  const uint64_t xm = xhat & m;
+  int lo = 0, hi = K.intervals[k];
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if ((L.cuts[k][p][mid] & m) <= xm)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo - 1 < 0 ? 0 : lo - 1;
+}
+
+// Runs every round over this wave's row of `len` elements whose level 0 is
+// in even[0..len) (party 0) and even[mr..mr+len) (party 1); j0[k] is the
+// row's first slot in round k (tree_row_offsets, written before a barrier);
+// bit k of `shared` is clear in L.diff (tree_compare).  Returns the level count; the row's max is
+// at index 0 of the final level's buffer (even if the count is even, odd
+// otherwise; party stride mr or ceil(mr / 2)).  Every thread of the
+// workgroup must call it (len 0 for an idle wave).
+template <int kRounds, int kCopies>
+__device__ __forceinline__ int tree_row(const TreeKeys<kRounds>& K, const TreeLds<kRounds>& L,
+                                        const AesLds<kCopies>& aes, uint64_t* even,
+                                        uint64_t* odd, int mr, int len, const uint32_t* j0s,
+                                        uint32_t shared) {
+  const int lane = threadIdx.x & 63, half = (mr + 1) / 2;
+  int level = 0;
+  for (int k = 0; k < K.rounds; ++k) {
+    if (len > 1) {
+      const uint64_t* src = (level & 1) ? odd : even;
+      const int sw = (level & 1) ? half : mr;  // party stride of src
+      uint64_t* dst = (level & 1) ? even : odd;
+      const int dw = (level & 1) ? mr : half;
+      const int pairs = len >> 1, nlen = (len + 1) >> 1;
+      const uint32_t j0 = j0s[k];
+      const bool one_ks = (shared >> k) & 1u;
+      // A lane per slot, both parties: one keystream block when the blobs
+      // share it, else one per party (in lockstep).
+      for (int t = lane; t < nlen; t += 64) {
+        uint64_t o[2];
+        if (t < pairs) {
+          const uint64_t xa0 = src[2 * t], xb0 = src[2 * t + 1];
+          const uint64_t xa1 = src[sw + 2 * t], xb1 = src[sw + 2 * t + 1];
+          const uint64_t xhat = (xa0 - xb0) + (xa1 - xb1) + K.mask[k];
+          int iv[2];
+          uint32_t st[2][4];
+          for (int p = 0; p < 2; ++p) {
+            iv[p] = (p == 1 && one_ks) ? iv[0] : tree_interval(K, L, k, p, xhat);
+            const uint64_t ctr = L.nonce[k][p] ^ (uint64_t(j0 + uint32_t(t)) << 32) ^
+                                 (uint64_t(iv[p]) * 2);
+            st[p][0] = uint32_t(ctr);
+            st[p][1] = uint32_t(ctr >> 32);
+            st[p][2] = 0;
+            st[p][3] = 0;
+          }
+          if (one_ks) {
+            aes.encrypt(st[0][0], st[0][1], st[0][2], st[0][3], L.rk[k][0]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) st[1][q] = st[0][q];
+          } else {
+            const uint4* rks[2] = {L.rk[k][0], L.rk[k][1]};
+            aes.template encrypt_n<2>(st, rks);
+          }
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const uint64_t k0 = uint64_t(st[p][0]) | uint64_t(st[p][1]) << 32;
+            const uint64_t k1 = uint64_t(st[p][2]) | uint64_t(st[p][3]) << 32;
+            const bool p0 = L.party[k][p] == 0;
+            const uint64_t q0 = p0 ? k0 : L.pay[k][p][2 * iv[p]] - k0;
+            const uint64_t q1 = p0 ? k1 : L.pay[k][p][2 * iv[p] + 1] - k1;
+            o[p] = (p ? xb1 : xb0) + q0 + q1 * xhat;
+          }
+        } else {
+          o[0] = src[2 * t];
+          o[1] = src[sw + 2 * t];
+        }
+        dst[t] = o[0];
+        dst[dw + t] = o[1];
+      }
+      len = nlen;
+      ++level;
+    }
+    __syncthreads();
+  }
+  return level;
+}
+
+// Host: validates the rounds' keys for rows of up to max_row elements.
+template <int kRounds>
+inline int make_tree_keys(const sufhip_relu_round_key* keys, int rounds, int max_row,
+                          const char* what, TreeKeys<kRounds>* out) {
+  auto fail = [&](const char* msg) {
+    set_error(std::string(what) + ": " + msg);
+    return SUFHIP_ERR_INVALID;
+  };
+  if (rounds < 0 || rounds > kRounds) return fail("too many rounds");
+  if (max_row < 1 || (max_row > 1 && rounds < 1) || (1LL << rounds) < max_row)
+    return fail("too few rounds for max_row");
+  if (rounds > 0 && !keys) return fail("null round keys");
+  TreeKeys<kRounds> K{};
+  K.rounds = rounds;
+  for (int k = 0; k < rounds; ++k) {
+    const sufhip_relu_round_key& rk = keys[k];
+    if (rk.intervals < 1 || rk.intervals > kTreeIntervals ||
+        rk.key_bytes != sufhip_interval_lut_key_bytes(rk.intervals, 2))
+      return fail("a round's LUT geometry is invalid");
+    if (!rk.key[0] || !rk.key[1] || (reinterpret_cast<uintptr_t>(rk.key[0]) & 7) != 0 ||
+        (reinterpret_cast<uintptr_t>(rk.key[1]) & 7) != 0)
+      return fail("round keys must be non-null and 8-byte aligned");
+    K.key[k][0] = rk.key[0];
+    K.key[k][1] = rk.key[1];
+    K.mask[k] = rk.mask;
+    K.intervals[k] = rk.intervals;
+  }
+  *out = K;
+  return SUFHIP_OK;
+}
+
+}  // namespace sufhip

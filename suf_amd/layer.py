@@ -180,9 +180,10 @@ class AttentionCore:
     def truncs(self):
         return self.tr_s + [self.tr_c] + self.softmax.truncs()
 
-    def eval2(self, qkv, out, prep=None):
+    def eval2(self, qkv, out, prep=None, fused=True):
         """prep: (tasks.Prepared, batch) holding the key-only halves of
-        truncs(), or None to issue them here."""
+        truncs(), or None to issue them here.  fused: scores, softmax and the
+        next open in one launch (sufhip_softmax2); else launch by launch."""
         seq, d, h, dh, mp = self.seq, self.d, self.heads, self.dh, self.maps
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
@@ -192,14 +193,20 @@ class AttentionCore:
         lin2(operand(term(qkv, index=mp["gk"]), term(self.tri_qk.B, neg=True)), h * seq * dh,
              xhat=self.E)
         _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S)
-        # Masked open of inv_sqrt * S at the packed causal positions, truncation by 2f.
         prep[0].wait(prep[1])
-        lin2(operand(term(self.S, index=mp["gs"], mul=self.inv_sqrt)), self.n,
-             into=(self.tr_s[0], self.sa))
-        lin2(operand(term(self.sa)), self.n, into=(self.tr_s[1], self.scores))
-        self.softmax.eval2(self.scores, self.prob, prep=prep)
-        lin2(operand(term(self.prob, index=mp["gp"]), term(self.tri_pv.A, neg=True)),
-             h * seq * seq, xhat=self.D2)
+        scaled = operand(term(self.S, index=mp["gs"], mul=self.inv_sqrt))
+        if fused and self.softmax.fusable():
+            # One launch: the masked open of inv_sqrt * S at the packed causal
+            # positions truncated by 2f, the softmax block, and the open of
+            # P - A over the dense [heads][seq][seq] layout.
+            self.softmax.eval_block(scaled, pre=self.tr_s,
+                                    dense=(self.D2, self.tri_pv.A, seq))
+        else:
+            lin2(scaled, self.n, into=(self.tr_s[0], self.sa))
+            lin2(operand(term(self.sa)), self.n, into=(self.tr_s[1], self.scores))
+            self.softmax.eval2(self.scores, self.prob, prep=prep, fused=False)
+            lin2(operand(term(self.prob, index=mp["gp"]), term(self.tri_pv.A, neg=True)),
+                 h * seq * seq, xhat=self.D2)
         lin2(operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True)), h * seq * dh,
              xhat=self.E)
         _beaver_batched(self.D2, self.E, self.tri_pv, h, seq, seq, dh, self.Z)

@@ -98,6 +98,7 @@ _SIGS = {
                                           c_sz, c_vp, c_vp, c_vp]),
     "sufhip_gate_chain2": (c_int, [c_vp, c_vp]),
     "sufhip_layernorm2": (c_int, [c_vp, c_vp]),
+    "sufhip_softmax2": (c_int, [c_vp, c_vp]),
     "sufhip_relu_max_tree2": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_vp, c_vp,
                                       c_vp, c_vp]),
     "sufhip_relu_max_round2": (c_int, [c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_vp, c_vp, c_sz, c_int,
@@ -202,6 +203,17 @@ class LayerNorm2Args(ctypes.Structure):
 class ReluRoundKey(ctypes.Structure):
     """sufhip_relu_round_key (include/suf_hip.h)."""
     _fields_ = [("key", c_vp * 2), ("key_bytes", c_sz), ("intervals", c_int), ("mask", c_u64)]
+
+
+class Softmax2Args(ctypes.Structure):
+    """sufhip_softmax2_args (include/suf_hip.h)."""
+    _fields_ = [("x", Operand2), ("pre_truncs", c_int), ("pre", TruncEpilogue * 2),
+                ("pre_mask", c_u64 * 2), ("rows", c_int), ("d_row_offsets", c_vp),
+                ("max_row", c_int), ("rounds", c_int), ("d_round_offsets", c_vp),
+                ("keys", ReluRoundKey * 10), ("nexp", Chain2Args), ("recip", Chain2Args),
+                ("norm", Triple2), ("tr_norm", TruncEpilogue), ("norm_mask", c_u64),
+                ("out", c_vp * 2), ("d_dense", c_vp), ("dense_a", c_vp * 2),
+                ("dense_cols", c_int)]
 
 
 class TruncJob(ctypes.Structure):

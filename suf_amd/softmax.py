@@ -26,8 +26,9 @@ import numpy as np
 import torch
 
 from . import native, spline, tables
-from .tasks import (RELU_ALPHA, CoeffLut, Dealer, Prepared, Triples, Trunc, chain2, dev_i32,
-                    lin2, mul2x, operand, pair, relu_coeffs_for, row_sum2, stream_ptr, term)
+from .tasks import (M64, RELU_ALPHA, CoeffLut, Dealer, Prepared, Triples, Trunc, chain2,
+                    chain2_args, dev_i32, lin2, mul2x, operand, pair, relu_coeffs_for, row_sum2,
+                    stream_ptr, term, triple2)
 
 
 def causal_offsets(heads, seq):
@@ -214,12 +215,62 @@ class SoftmaxBlock:
     def truncs(self):
         return self.nexp.truncs() + self.recip.truncs() + [self.tr]
 
-    def eval2(self, x, out, prep=None):
+    def fusable(self):
+        rm = self.rowmax
+        return (rm.max_row <= 512 and len(rm.rounds) <= 10 and self.recip.iters == 1 and
+                all(t.has_table() for t in self.truncs()))
+
+    def block_args(self, x, out=None, pre=(), dense=None):
+        """sufhip_softmax2_args of the one-launch block: x an operand over the
+        packed scores, pre up to two Trunc gates applied to its open first,
+        out a pair for the probabilities and/or dense = (d_open, (a0, a1),
+        cols) for the open P - A of the next Beaver product."""
+        a = native.Softmax2Args()
+        a.x = x
+        a.pre_truncs = len(pre)
+        for q, t in enumerate(pre):
+            a.pre[q] = t.epilogue(self.delta)
+            a.pre_mask[q] = t.mask & M64
+        rm = self.rowmax
+        a.rows, a.d_row_offsets, a.max_row = self.rows, rm.offs_dev.data_ptr(), rm.max_row
+        a.rounds, a.d_round_offsets = len(rm.rounds), rm.round_off.data_ptr()
+        for k in range(len(rm.rounds)):
+            a.keys[k] = rm.round_keys[k]
+        g = self.nexp
+        a.nexp = chain2_args(native.CHAIN_CUBIC, self.f, None, self.n, g.lut, g.lut_key_bytes,
+                             g.intervals, g.rin[0] + g.rin[1], g.tri, g.trunc, self.e)
+        rc = self.recip
+        a.recip = chain2_args(native.CHAIN_RECIP, self.f, None, self.rows, rc.lut.keys,
+                              rc.lut.key_bytes, rc.lut.intervals, rc.lut.mask, rc.tri, rc.tr,
+                              rc.y)
+        a.norm = triple2(self.tri)
+        a.tr_norm = self.tr.epilogue(self.e)
+        a.norm_mask = self.tr.mask & M64
+        if out is not None:
+            a.out[0], a.out[1] = out[0].data_ptr(), out[1].data_ptr()
+        if dense is not None:
+            a.d_dense = dense[0].data_ptr()
+            a.dense_a[0], a.dense_a[1] = dense[1][0].data_ptr(), dense[1][1].data_ptr()
+            a.dense_cols = dense[2]
+        return a
+
+    def eval_block(self, x, out=None, pre=(), dense=None):
+        """The whole block in one launch (sufhip_softmax2); see block_args.
+        The gates' key-only halves must have been prepared."""
+        a = self.block_args(x, out, pre, dense)
+        native.call("sufhip_softmax2", native.ctypes.byref(a), stream_ptr())
+
+    def eval2(self, x, out, prep=None, fused=True):
         """x, out: pairs of int64 [n] device tensors (packed rows).  prep:
         (tasks.Prepared, batch) holding this block's key-only halves, or None
-        to issue them here on the block's side stream."""
+        to issue them here on the block's side stream.  fused: the whole
+        block in one launch (sufhip_softmax2); else launch by launch."""
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
+        if fused and self.fusable():
+            prep[0].wait(prep[1])
+            self.eval_block(operand(term(x)), out)
+            return out
         self.rowmax.eval2(x, self.delta)
         self.nexp.eval2(self.delta, self.e, prep=prep)
         row_sum2(operand(term(self.e)), self.rows, offsets=self.offs_dev, sums=self.s)

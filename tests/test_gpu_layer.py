@@ -124,14 +124,21 @@ def test_attention_core_reconstructs(seq, d, heads):
     at = layer.AttentionCore(seq, d, heads, Dealer(6), STATE, F)
     for t in at.truncs():
         t.prepare()
-    out = tuple(torch.empty(seq * d, dtype=torch.int64, device="cuda") for _ in range(2))
-    at.eval2((dev(q0), dev(q1)), out)
     tabs = _tabs()
     want, st = fp.attention(qkv, seq, d, heads, F, tabs["nexp"], tabs["recip"])
-    sc = (u64(at.scores[0]) + u64(at.scores[1])).astype(np.uint64)
-    assert np.array_equal(sc, st["scores"].view(np.uint64))
-    rec = (u64(out[0]) + u64(out[1])).astype(np.uint64)
-    assert np.array_equal(rec, want.view(np.uint64))
+    shares = []
+    for fused in (False, True):
+        out = tuple(torch.empty(seq * d, dtype=torch.int64, device="cuda") for _ in range(2))
+        at.eval2((dev(q0), dev(q1)), out, fused=fused)
+        if not fused:  # the one-launch softmax keeps the scores on chip
+            sc = (u64(at.scores[0]) + u64(at.scores[1])).astype(np.uint64)
+            assert np.array_equal(sc, st["scores"].view(np.uint64))
+        rec = (u64(out[0]) + u64(out[1])).astype(np.uint64)
+        assert np.array_equal(rec, want.view(np.uint64))
+        shares.append((u64(out[0]), u64(out[1])))
+    # Same dealer material: the fused path's shares equal the per-launch path's.
+    assert np.array_equal(shares[0][0], shares[1][0])
+    assert np.array_equal(shares[0][1], shares[1][1])
 
 
 def test_layer_small_reconstructs():

@@ -168,26 +168,51 @@ def test_rsqrt_shares_and_closed_form():
 
 
 @pytest.mark.parametrize("heads,seq", [(1, 8), (2, 33)])
-def test_softmax_block_small(heads, seq):
+@pytest.mark.parametrize("fused", [True, False])
+def test_softmax_block_small(heads, seq, fused):
     offs = softmax.causal_offsets(heads, seq)
     n = int(offs[-1])
     x = _scores(offs, 50 + seq)
     x0, x1 = _share(x, 51)
-    say("softmax block heads=%d seq=%d n=%d" % (heads, seq, n))
+    say("softmax block heads=%d seq=%d n=%d fused=%s" % (heads, seq, n, fused))
     sm = softmax.SoftmaxBlock(offs, STATE, F, seed=13)
     out = tuple(torch.empty(n, dtype=torch.int64, device="cuda") for _ in range(2))
-    sm.eval2(_pair_dev(x0, x1), out)
+    sm.eval2(_pair_dev(x0, x1), out, fused=fused)
     prob, st = fp.softmax_block(x, offs, sm.nexp_table, sm.recip.table, F)
-    assert np.array_equal(_recon(sm.delta), st["delta"].view(np.uint64))
-    assert np.array_equal(_recon(sm.e), st["exp"].view(np.uint64))
-    assert np.array_equal(_recon(sm.s), st["sum"].view(np.uint64))
+    if not fused:  # the one-launch block keeps its intermediates on chip
+        assert np.array_equal(_recon(sm.delta), st["delta"].view(np.uint64))
+        assert np.array_equal(_recon(sm.e), st["exp"].view(np.uint64))
+        assert np.array_equal(_recon(sm.s), st["sum"].view(np.uint64))
     assert np.array_equal(_recon(out), prob.view(np.uint64))
     # Share level: the whole chain on the oracle.
     o, st2 = tp.softmax2(ol.Prg(STATE), sm, [x0, x1])
-    for k, dv in (("delta", sm.delta), ("exp", sm.e), ("sum", sm.s)):
-        assert np.array_equal(u64(dv[0]), st2[k][0]) and np.array_equal(u64(dv[1]), st2[k][1])
+    if not fused:
+        for k, dv in (("delta", sm.delta), ("exp", sm.e), ("sum", sm.s)):
+            assert np.array_equal(u64(dv[0]), st2[k][0]) and np.array_equal(u64(dv[1]),
+                                                                            st2[k][1])
     g = [u64(out[0]), u64(out[1])]
     assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
+
+
+@pytest.mark.parametrize("lens", [[1, 2, 3, 300, 5, 64, 7], [200, 1, 33], [512, 2]])
+def test_softmax_block_ragged_rows_fused(lens):
+    """Ragged rows through the one-launch block (rows up to 300 / 200 / 512:
+    one, two or four rows per workgroup, 8 or 4 elements per lane): shares
+    equal the launch-by-launch path's and the oracle's."""
+    offs = np.cumsum([0] + lens).astype(np.int64)
+    n = int(offs[-1])
+    x = _scores(offs, 70 + len(lens))
+    x0, x1 = _share(x, 71)
+    say("softmax block ragged rows %s" % (lens,))
+    sm = softmax.SoftmaxBlock(offs, STATE, F, seed=17)
+    outs = []
+    for fused in (True, False):
+        out = tuple(torch.empty(n, dtype=torch.int64, device="cuda") for _ in range(2))
+        sm.eval2(_pair_dev(x0, x1), out, fused=fused)
+        outs.append((u64(out[0]), u64(out[1])))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    prob, _ = fp.softmax_block(x, offs, sm.nexp_table, sm.recip.table, F)
+    assert np.array_equal((outs[0][0] + outs[0][1]).astype(np.uint64), prob.view(np.uint64))
 
 
 def test_softmax_block_config_shape_twice():
