@@ -662,8 +662,9 @@ int sufhip_beaver_matmul2_batched(const uint64_t* d_D_open, const uint64_t* d_E_
  * Y_p = X_p * W mod 2^64, X_p [M x K] u64 shares, W [K x N] public int64, on
  * the int8 matrix cores with W in `digits` balanced base-256 digit planes.
  * sufhip_public_w_digits: host helper, the digits the weights need (1..8).
- * sufhip_public_w_prepare: W's planes [digits][N][K] (done once per weight;
- * d_planes of sufhip_public_w_planes_bytes bytes, 16-byte aligned).
+ * sufhip_public_w_prepare: W's planes, k-blocked [digits][K/32][N][32] int8
+ * (done once per weight; d_planes of sufhip_public_w_planes_bytes bytes,
+ * 16-byte aligned; an opaque layout for sufhip_matmul_public2).
  * sufhip_matmul_public2: M, K, N multiples of 32, digits in 1..4 with
  * digits * K < 2^17 (exact int32 accumulation); writes the shares
  * (d_out0 and d_out1) and/or the masked open d_zhat = Y_0 + Y_1 + mask that

@@ -12,15 +12,18 @@
 // i.e. sum_{j<J} (8 - j) int8 GEMMs (15 for J = 2).  |S_s| <= J K 2^14 < 2^31
 // for K < 2^17 / J, so int32 accumulation is exact.
 //
-// W's digit planes [J][N][K] are prepared once (public weights are fixed:
-// the reference caches them on the device too, matmul_gpu.cu:620-674).
-// Per call: split X_0, X_1 into planes [8][2M][K] (party 0's rows first),
-// then one wave per 32 x 32 output tile and k-slice computes the tile for
-// party 0 and then party 1, and writes either the shares, or only the masked
-// open zhat = Y_0 + Y_1 + mask that the following truncation gate consumes
+// Digit planes are k-blocked: a plane is [K / 32][rows][32] int8, so the
+// 32 rows x 32 k of one MFMA step are a contiguous 1 KB block and one 16-byte
+// load per lane fetches it whole.  W's planes [J][K/32][N][32] are prepared
+// once (public weights are fixed: the reference caches them on the device
+// too, matmul_gpu.cu:620-674).  Per call: split X_0, X_1 into planes
+// [8][K/32][2M][32] (party 0's rows first), then a workgroup of two waves,
+// one per party, computes a 32 x 32 output tile over a k-slice with loads
+// three steps ahead, and writes either the shares, or only the masked open
+// zhat = Y_0 + Y_1 + mask that the following truncation gate consumes
 // (TruncTask after every public matmul: attention_block.cpp:1136-1230,
-// mlp_block.cpp:378-767).  Small grids split k over slices whose partial sums a
-// reduction pass adds.
+// mlp_block.cpp:378-767), the two parties' tiles summed through LDS.  Small
+// grids split k over slices whose partial sums a reduction pass adds.
 #include <hip/hip_runtime.h>
 
 #include "suf_hip.h"
@@ -44,11 +47,18 @@ __device__ __forceinline__ void digits8(uint64_t v, uint32_t (&d)[kPlanes]) {
   }
 }
 
-// X_0, X_1 [M][K] -> planes [8][2M][K]; one lane per 4 consecutive k of a row.
+// Byte offset of (row, k) in a k-blocked plane of `rows` rows.
+__device__ __forceinline__ size_t kblock_off(size_t row, int k, size_t rows) {
+  return (size_t(k >> 5) * rows + row) * 32 + size_t(k & 31);
+}
+
+// X_0, X_1 [M][K] -> planes [8][K/32][2M][32]; one lane per 4 consecutive k
+// of a row.
 __global__ void __launch_bounds__(256)
     split_x2_kernel(const uint64_t* X0, const uint64_t* X1, int M, int K, int8_t* planes) {
   const size_t quads = size_t(2) * M * K / 4;
-  const size_t plane = size_t(2) * M * K;
+  const size_t rows = size_t(2) * M;
+  const size_t plane = rows * K;
   for (size_t q = size_t(blockIdx.x) * 256 + threadIdx.x; q < quads; q += size_t(gridDim.x) * 256) {
     const size_t idx = 4 * q;
     const size_t row = idx / size_t(K);
@@ -62,13 +72,14 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int i = 0; i < kPlanes; ++i) pk[i] |= d[i] << (8 * t);
     }
+    const size_t off = kblock_off(row, k, rows);
 #pragma unroll
     for (int i = 0; i < kPlanes; ++i)
-      *reinterpret_cast<uint32_t*>(planes + i * plane + idx) = pk[i];
+      *reinterpret_cast<uint32_t*>(planes + i * plane + off) = pk[i];
   }
 }
 
-// W [K][N] -> planes [J][N][K]; one lane per (n, 4 consecutive k).
+// W [K][N] -> planes [J][K/32][N][32]; one lane per (n, 4 consecutive k).
 __global__ void __launch_bounds__(256)
     split_w_kernel(const int64_t* W, int K, int N, int J, int8_t* planes) {
   const size_t quads = size_t(N) * K / 4;
@@ -84,8 +95,8 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int i = 0; i < kPlanes; ++i) pk[i] |= d[i] << (8 * t);
     }
-    for (int j = 0; j < J; ++j)
-      *reinterpret_cast<uint32_t*>(planes + j * plane + size_t(n) * K + k) = pk[j];
+    const size_t off = kblock_off(size_t(n), k, size_t(N));
+    for (int j = 0; j < J; ++j) *reinterpret_cast<uint32_t*>(planes + j * plane + off) = pk[j];
   }
 }
 
@@ -100,8 +111,8 @@ __device__ __forceinline__ v4i load16(const int8_t* p) {
 }
 
 struct PubArgs {
-  const int8_t* Lp;  // [8][2M][K]
-  const int8_t* Wp;  // [J][N][K]
+  const int8_t* Lp;  // [8][K/32][2M][32]
+  const int8_t* Wp;  // [J][K/32][N][32]
   int M, K, N;
   uint64_t* out[2];  // shares (or NULL)
   uint64_t* zhat;    // masked open (or NULL)
@@ -110,72 +121,98 @@ struct PubArgs {
   TruncEpi epi;      // the open feeds this truncation gate (replaces zhat)
 };
 
-// One wave per 32 x 32 tile and k-slice; grid = (N / 32, M / 32, slices).
-// MFMA operand layout (checked on the device for matmul_mfma.hip): lane l
-// supplies row / column l % 32 at k = 16 (l / 32) + byte; accumulator register
-// r of lane l is row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+constexpr int kPubAhead = 2;  // k-steps of loads in flight per wave
+
+// Workgroup = two waves, wave p computing party p's 32 x 32 tile over one
+// k-slice; grid = (N / 32, M / 32, slices).  MFMA operand layout (checked on
+// the device for matmul_mfma.hip): lane l supplies row / column l % 32 at
+// k = 16 (l / 32) + byte; accumulator register r of lane l is row 8 (r / 4)
+// + 4 (l / 32) + r % 4, column l % 32.
 template <int J>
-__global__ void __launch_bounds__(64) public_mfma_kernel(PubArgs a) {
-  const int l = threadIdx.x;
+__global__ void __launch_bounds__(128, 2) public_mfma_kernel(PubArgs a) {
+  __shared__ uint64_t other[16][64];  // party 1's tile, for the open
+  const int l = threadIdx.x & 63, p = threadIdx.x >> 6;
   const int M = a.M, K = a.K, N = a.N;
   const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
   const int steps = K / 32;
-  const int k_begin = 32 * (steps * int(blockIdx.z) / int(gridDim.z));
-  const int k_end = 32 * (steps * (int(blockIdx.z) + 1) / int(gridDim.z));
-  const size_t lplane = size_t(2) * M * K, wplane = size_t(N) * K;
-  const int8_t* wcol = a.Wp + size_t(n0 + (l & 31)) * K + 16 * (l >> 5);
-  const int col = n0 + (l & 31);
-  uint64_t tot[16];
+  const int s_begin = steps * int(blockIdx.z) / int(gridDim.z);
+  const int s_end = steps * (int(blockIdx.z) + 1) / int(gridDim.z);
+  const size_t lrows = size_t(2) * M;
+  const size_t lplane = lrows * K, wplane = size_t(N) * K;
+  // This lane's 16 bytes of step s: row (or column) l % 32, bytes 16 (l / 32).
+  const int8_t* lbase = a.Lp + size_t(p * M + m0 + (l & 31)) * 32 + 16 * (l >> 5);
+  const int8_t* wbase = a.Wp + size_t(n0 + (l & 31)) * 32 + 16 * (l >> 5);
+  const size_t lstep = lrows * 32, wstep = size_t(N) * 32;
+  v16i acc[kPlanes];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) tot[r] = 0;
-  for (int p = 0; p < 2; ++p) {
-    const int8_t* lrow = a.Lp + size_t(p * M + m0 + (l & 31)) * K + 16 * (l >> 5);
-    v16i acc[kPlanes];
+  for (int s = 0; s < kPlanes; ++s)
 #pragma unroll
-    for (int s = 0; s < kPlanes; ++s)
+    for (int r = 0; r < 16; ++r) acc[s][r] = 0;
+  v4i x[kPubAhead][kPlanes], w[kPubAhead][J];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[s][r] = 0;
-    v4i x[kPlanes], w[J];
+  for (int q = 0; q < kPubAhead; ++q) {
+    const int st = s_begin + q < s_end ? s_begin + q : s_begin;  // in bounds
 #pragma unroll
-    for (int i = 0; i < kPlanes; ++i) x[i] = load16(lrow + i * lplane + k_begin);
+    for (int i = 0; i < kPlanes; ++i) x[q][i] = load16(lbase + i * lplane + size_t(st) * lstep);
 #pragma unroll
-    for (int j = 0; j < J; ++j) w[j] = load16(wcol + j * wplane + k_begin);
-    for (int k = k_begin; k < k_end; k += 32) {
-      v4i nx[kPlanes], nw[J];
-      const int kn = k + 32 < k_end ? k + 32 : k;  // last step reloads in bounds
+    for (int j = 0; j < J; ++j) w[q][j] = load16(wbase + j * wplane + size_t(st) * wstep);
+  }
+  for (int st = s_begin; st < s_end; ++st) {
 #pragma unroll
-      for (int i = 0; i < kPlanes; ++i) nx[i] = load16(lrow + i * lplane + kn);
+    for (int j = 0; j < J; ++j)
 #pragma unroll
-      for (int j = 0; j < J; ++j) nw[j] = load16(wcol + j * wplane + kn);
+      for (int i = 0; i + j < kPlanes; ++i)
+        acc[i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x[0][i], w[0][j], acc[i + j], 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < J; ++j)
+    for (int q = 0; q + 1 < kPubAhead; ++q) {
 #pragma unroll
-        for (int i = 0; i + j < kPlanes; ++i)
-          acc[i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x[i], w[j], acc[i + j], 0, 0, 0);
+      for (int i = 0; i < kPlanes; ++i) x[q][i] = x[q + 1][i];
 #pragma unroll
-      for (int i = 0; i < kPlanes; ++i) x[i] = nx[i];
-#pragma unroll
-      for (int j = 0; j < J; ++j) w[j] = nw[j];
+      for (int j = 0; j < J; ++j) w[q][j] = w[q + 1][j];
     }
+    const int sn = st + kPubAhead < s_end ? st + kPubAhead : s_begin;  // in bounds
+#pragma unroll
+    for (int i = 0; i < kPlanes; ++i)
+      x[kPubAhead - 1][i] = load16(lbase + i * lplane + size_t(sn) * lstep);
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      w[kPubAhead - 1][j] = load16(wbase + j * wplane + size_t(sn) * wstep);
+  }
+  const int col = n0 + (l & 31);
+  uint64_t v[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    v[r] = 0;
+#pragma unroll
+    for (int s = 0; s < kPlanes; ++s) v[r] += uint64_t(int64_t(acc[s][r])) << (8 * s);
+  }
+  if (gridDim.z > 1) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-      uint64_t v = 0;
+      a.part[((size_t(blockIdx.z) * 2 + p) * M + row) * N + col] = v[r];
+    }
+    return;
+  }
+  if (a.out[p]) {
 #pragma unroll
-      for (int s = 0; s < kPlanes; ++s) v += uint64_t(int64_t(acc[s][r])) << (8 * s);
-      if (gridDim.z > 1) {
-        a.part[((size_t(blockIdx.z) * 2 + p) * M + row) * N + col] = v;
-      } else if (a.out[p]) {
-        a.out[p][size_t(row) * N + col] = v;
-      }
-      tot[r] += v;
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+      a.out[p][size_t(row) * N + col] = v[r];
     }
   }
-  if (gridDim.z == 1 && (a.zhat || a.epi.on)) {
+  if (a.zhat || a.epi.on) {
+    if (p == 1) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-      put_open(a.epi, a.zhat, size_t(row) * N + col, tot[r] + a.mask);
+      for (int r = 0; r < 16; ++r) other[r][l] = v[r];
+    }
+    __syncthreads();
+    if (p == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+        put_open(a.epi, a.zhat, size_t(row) * N + col, v[r] + other[r][l] + a.mask);
+      }
     }
   }
 }
@@ -196,13 +233,14 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// k-slices so that a launch has about 512 waves (each wave does both parties).
+// k-slices so that a launch has about 512 workgroups (two waves each) and a
+// slice has at least four k-steps.
 int pub_slices(int M, int K, int N) {
   const int tiles = (M / 32) * (N / 32);
   const int steps = K / 32;
   int s = tiles >= 512 ? 1 : (512 + tiles - 1) / tiles;
   if (s > 8) s = 8;
-  if (s > steps) s = steps;
+  if (s > steps / 4) s = steps / 4 > 0 ? steps / 4 : 1;
   return s;
 }
 
@@ -292,10 +330,10 @@ int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int
   PubArgs a{Lp, d_planes, M, K, N, {d_out0, d_out1}, d_zhat, mask, part, epi};
   const dim3 grid(N / 32, M / 32, sl);
   switch (digits) {
-    case 1: hipLaunchKernelGGL(public_mfma_kernel<1>, grid, dim3(64), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(public_mfma_kernel<2>, grid, dim3(64), 0, s, a); break;
-    case 3: hipLaunchKernelGGL(public_mfma_kernel<3>, grid, dim3(64), 0, s, a); break;
-    default: hipLaunchKernelGGL(public_mfma_kernel<4>, grid, dim3(64), 0, s, a); break;
+    case 1: hipLaunchKernelGGL(public_mfma_kernel<1>, grid, dim3(128), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(public_mfma_kernel<2>, grid, dim3(128), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(public_mfma_kernel<3>, grid, dim3(128), 0, s, a); break;
+    default: hipLaunchKernelGGL(public_mfma_kernel<4>, grid, dim3(128), 0, s, a); break;
   }
   if (int rc = check_launch("public_mfma_kernel")) return rc;
   if (sl == 1) return SUFHIP_OK;
