@@ -133,10 +133,19 @@ __global__ void __launch_bounds__(128, 2) public_mfma_kernel(PubArgs a) {
   __shared__ uint64_t other[16][64];  // party 1's tile, for the open
   const int l = threadIdx.x & 63, p = threadIdx.x >> 6;
   const int M = a.M, K = a.K, N = a.N;
-  const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs
+  // (each with its own L2), so workgroup id g runs on XCD g % 8.  Give XCD x
+  // a contiguous range of (column tile, row tile, slice) in that nesting, so
+  // that its L2 holds 1/8 of W's columns (and all of X) instead of all of W.
+  const int gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
+  const int total = gx * gy * gz;
+  int g = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  if (total % 8 == 0) g = (g % 8) * (total / 8) + g / 8;
+  const int slice = g % gz, tile_y = (g / gz) % gy, tile_x = g / (gz * gy);
+  const int m0 = tile_y * 32, n0 = tile_x * 32;
   const int steps = K / 32;
-  const int s_begin = steps * int(blockIdx.z) / int(gridDim.z);
-  const int s_end = steps * (int(blockIdx.z) + 1) / int(gridDim.z);
+  const int s_begin = steps * slice / gz;
+  const int s_end = steps * (slice + 1) / gz;
   const size_t lrows = size_t(2) * M;
   const size_t lplane = lrows * K, wplane = size_t(N) * K;
   // This lane's 16 bytes of step s: row (or column) l % 32, bytes 16 (l / 32).
@@ -186,11 +195,11 @@ __global__ void __launch_bounds__(128, 2) public_mfma_kernel(PubArgs a) {
 #pragma unroll
     for (int s = 0; s < kPlanes; ++s) v[r] += uint64_t(int64_t(acc[s][r])) << (8 * s);
   }
-  if (gridDim.z > 1) {
+  if (gz > 1) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-      a.part[((size_t(blockIdx.z) * 2 + p) * M + row) * N + col] = v[r];
+      a.part[((size_t(slice) * 2 + p) * M + row) * N + col] = v[r];
     }
     return;
   }

@@ -63,6 +63,10 @@ int frontier_bits(int f, size_t n) {
 // 2^(d-1) slots after them.
 int walk_bits(int d) { return d < kWalkFrontierBits ? d : kWalkFrontierBits; }
 
+// The batched prepare walks a table gate's whole domain (d = f <= 14) in one
+// launch: a lane per table entry, no expansion launches after it.
+int batch_walk_bits(int d, int f) { return d == f && f <= kTruncTableBits ? d : walk_bits(d); }
+
 size_t frontier_nodes(int d) {
   if (d == 0) return 0;
   return (size_t(1) << d) + (d > walk_bits(d) ? size_t(1) << (d - 1) : 0);
@@ -562,7 +566,7 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
     const int m = count - base < kBatchJobs ? count - base : kBatchJobs;
     // Per job: its depth d, walked depth k0 and the two workspace regions,
     // alternated so that depth d ends in the first (as sufhip_trunc_prepare).
-    int d[kBatchJobs], cur[kBatchJobs];
+    int d[kBatchJobs], k0s[kBatchJobs], cur[kBatchJobs];
     uint4* lvl[kBatchJobs][2];
     int maxd = 0;
     for (int i = 0; i < m; ++i) {
@@ -571,7 +575,8 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
                                jb.d_key, jb.key_bytes, jb.n, jb.d_work, jb.work_bytes))
         return rc;
       d[i] = frontier_bits(jb.frac_bits, jb.n);
-      const int k0 = walk_bits(d[i]);
+      k0s[i] = batch_walk_bits(d[i], jb.frac_bits);
+      const int k0 = k0s[i];
       lvl[i][0] = static_cast<uint4*>(jb.d_work);
       lvl[i][1] = d[i] > 0 ? lvl[i][0] + 2 * (size_t(1) << d[i]) : nullptr;
       cur[i] = (d[i] - k0) & 1;
@@ -582,7 +587,7 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
     wa.begin[0] = 0;
     for (int i = 0; i < m; ++i) {
       const sufhip_trunc_job& jb = jobs[base + i];
-      const int k0 = walk_bits(d[i]);
+      const int k0 = k0s[i];
       wa.key[wa.count] = jb.d_key;
       wa.out[wa.count] = lvl[i][cur[i]];
       wa.f[wa.count] = jb.frac_bits;
@@ -602,7 +607,7 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
       ea.level = level;
       ea.begin[0] = 0;
       for (int i = 0; i < m; ++i) {
-        if (d[i] <= level) continue;
+        if (d[i] <= level || k0s[i] > level) continue;
         ea.key[ea.count] = jobs[base + i].d_key;
         ea.in[ea.count] = lvl[i][cur[i]];
         ea.out[ea.count] = lvl[i][cur[i] ^ 1];
@@ -611,6 +616,7 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
         ++ea.count;
         cur[i] ^= 1;
       }
+      if (ea.count == 0) continue;  // every job of this level was walked
       unsigned int eg = 0, eb = 0;
       if (int rc = spread_grid(ea.begin[ea.count], &eg, &eb)) return rc;
       hipLaunchKernelGGL(trunc_batch_expand_kernel, dim3(eg), dim3(eb), 0, s, ea);
