@@ -214,16 +214,19 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
 /* A truncation folded into the launch that produces its masked open: for a
  * GapARS gate with frac_bits <= 14 whose keys were prepared (full-domain
  * tables), y[p][i] receives party p's truncated share at the open value
+ * (plus add[p][i] when add is given: a residual folded into the same write)
  * instead of the open being written.  key / table: both parties' key blobs
  * (8-byte aligned) and prepared workspaces (16-byte aligned) of
  * work_bytes >= sufhip_trunc_work_bytes(frac_bits, n) each.  A key that is
- * not a GapARS key for frac_bits yields zeros. */
+ * not a GapARS key for frac_bits yields zeros.  The whole-chain and block
+ * entry points take no addend. */
 typedef struct sufhip_trunc_epilogue {
   const uint8_t* key[2];
   const void* table[2];
   size_t work_bytes;
   int frac_bits;
   uint64_t* y[2];
+  const uint64_t* add[2];
 } sufhip_trunc_epilogue;
 
 /* ---------------------------------------------------------------------- */
@@ -316,6 +319,19 @@ typedef struct sufhip_operand2 {
 int sufhip_lin2(const sufhip_operand2* x, size_t n, uint64_t* d_out0, uint64_t* d_out1,
                 uint64_t* d_xhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,
                 void* stream);
+
+/* Up to 4 independent sufhip_lin2 evaluations (each with the meaning of
+ * sufhip_lin2's arguments) in one launch: opens of one protocol round that
+ * do not depend on each other. */
+typedef struct sufhip_lin2_job {
+  sufhip_operand2 x;
+  size_t n;
+  uint64_t* out[2];
+  uint64_t* xhat;
+  uint64_t mask;
+  const sufhip_trunc_epilogue* trunc;
+} sufhip_lin2_job;
+int sufhip_lin2_batch(const sufhip_lin2_job* jobs, int count, void* stream);
 
 /* Beaver product for both parties with general operands (MulTask and
  * MulRowBroadcastTask, phase_tasks.hpp:198-402, 1810-2185; beaver_mul_kernel

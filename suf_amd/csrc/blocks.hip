@@ -367,6 +367,10 @@ int triple_ok(const sufhip_triple2& t) {
 
 int table_epi(const sufhip_trunc_epilogue& t, size_t n, const char* what, TruncEpi* e) {
   sufhip_trunc_epilogue c = t;
+  if (c.add[0] || c.add[1]) {
+    set_error(std::string(what) + ": the block's truncations take no addend");
+    return SUFHIP_ERR_INVALID;
+  }
   uint64_t dummy = 0;
   c.y[0] = c.y[1] = &dummy;  // the block writes its own outputs
   return make_epi(&c, n, what, e);

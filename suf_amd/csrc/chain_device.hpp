@@ -430,6 +430,7 @@ inline int make_chain_args(const sufhip_chain2_args& g, bool own_io, const char*
     const int want_f = (g.kind == SUFHIP_CHAIN_RSQRT && k == 2) ? g.frac_bits + 1 : g.frac_bits;
     if (g.trunc[k].frac_bits != want_f) return fail("truncation gate of the wrong width");
     sufhip_trunc_epilogue t = g.trunc[k];
+    if (t.add[0] || t.add[1]) return fail("a chain's truncations take no addend");
     uint64_t dummy = 0;
     t.y[0] = t.y[1] = &dummy;  // outputs are the chain's own
     TruncEpi e;

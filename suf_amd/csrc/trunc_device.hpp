@@ -95,16 +95,23 @@ struct TruncEpi {
   const uint8_t* key[2];
   const uint4* table[2];
   uint64_t* y[2];
+  const uint64_t* add[2];  // optional addend of the outputs (a residual)
   int f;
   int on;
 };
 
-// Writes the open value v of element i: the gate's two output shares when
-// the epilogue is on, else the open itself (if requested).
+// Writes the open value v of element i: the gate's two output shares (plus
+// the addend) when the epilogue is on, else the open itself (if requested).
 __device__ __forceinline__ void put_open(const TruncEpi& e, uint64_t* hat, size_t i, uint64_t v) {
   if (e.on) {
-    e.y[0][i] = trunc_table_eval(e.key[0], e.table[0], e.f, v);
-    e.y[1][i] = trunc_table_eval(e.key[1], e.table[1], e.f, v);
+    uint64_t y0 = trunc_table_eval(e.key[0], e.table[0], e.f, v);
+    uint64_t y1 = trunc_table_eval(e.key[1], e.table[1], e.f, v);
+    if (e.add[0]) {
+      y0 += e.add[0][i];
+      y1 += e.add[1][i];
+    }
+    e.y[0][i] = y0;
+    e.y[1][i] = y1;
   } else if (hat) {
     hat[i] = v;
   }
@@ -112,8 +119,13 @@ __device__ __forceinline__ void put_open(const TruncEpi& e, uint64_t* hat, size_
 
 // Validates an epilogue for n elements and converts it (NULL -> off).
 inline int make_epi(const sufhip_trunc_epilogue* t, size_t n, const char* what, TruncEpi* out) {
-  *out = TruncEpi{{nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}, 0, 0};
+  *out = TruncEpi{{nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr},
+                  0, 0};
   if (!t) return SUFHIP_OK;
+  if ((t->add[0] == nullptr) != (t->add[1] == nullptr)) {
+    set_error(std::string(what) + ": truncation epilogue addend needs both parties or neither");
+    return SUFHIP_ERR_INVALID;
+  }
   const bool ok = t->frac_bits >= 1 && t->frac_bits <= kTruncTableBits && t->key[0] &&
                   t->key[1] && t->table[0] && t->table[1] && t->y[0] && t->y[1] &&
                   (reinterpret_cast<uintptr_t>(t->key[0]) & 7) == 0 &&
@@ -132,6 +144,7 @@ inline int make_epi(const sufhip_trunc_epilogue* t, size_t n, const char* what, 
   *out = TruncEpi{{t->key[0], t->key[1]},
                   {static_cast<const uint4*>(t->table[0]), static_cast<const uint4*>(t->table[1])},
                   {t->y[0], t->y[1]},
+                  {t->add[0], t->add[1]},
                   t->frac_bits,
                   1};
   return SUFHIP_OK;

@@ -118,6 +118,34 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
+constexpr int kLin2Jobs = 4;
+
+struct Lin2Batch {
+  sufhip_operand2 x[kLin2Jobs];
+  size_t n[kLin2Jobs];
+  uint64_t* out[kLin2Jobs][2];
+  uint64_t* xhat[kLin2Jobs];
+  uint64_t mask[kLin2Jobs];
+  TruncEpi epi[kLin2Jobs];
+  unsigned begin[kLin2Jobs + 1];  // each job's first workgroup
+  int count;
+};
+
+// Workgroups [begin[j], begin[j + 1]) grid-stride over job j's elements.
+__global__ void __launch_bounds__(kBlock) lin2_batch_kernel(Lin2Batch b) {
+  int j = 0;
+  while (j + 1 < b.count && blockIdx.x >= b.begin[j + 1]) ++j;
+  const unsigned groups = b.begin[j + 1] - b.begin[j];
+  const size_t stride = size_t(groups) * kBlock;
+  for (size_t i = size_t(blockIdx.x - b.begin[j]) * kBlock + threadIdx.x; i < b.n[j];
+       i += stride) {
+    const uint64_t x0 = operand_at(b.x[j], 0, i), x1 = operand_at(b.x[j], 1, i);
+    if (b.out[j][0]) b.out[j][0][i] = x0;
+    if (b.out[j][1]) b.out[j][1][i] = x1;
+    put_open(b.epi[j], b.xhat[j], i, x0 + x1 + b.mask[j]);
+  }
+}
+
 __global__ void __launch_bounds__(kBlock) mul2x_kernel(sufhip_mul2x_args a, size_t n, TruncEpi epi) {
   const size_t stride = size_t(gridDim.x) * kBlock;
   const bool open = a.zhat != nullptr || epi.on;
@@ -244,6 +272,34 @@ int sufhip_lin2(const sufhip_operand2* x, size_t n, uint64_t* d_out0, uint64_t* 
   hipLaunchKernelGGL(lin2_kernel, dim3(ew_grid(n)), dim3(kBlock), 0, as_stream(stream), *x, n,
                      d_out0, d_out1, d_xhat, mask, epi);
   return check_launch("lin2_kernel");
+}
+
+int sufhip_lin2_batch(const sufhip_lin2_job* jobs, int count, void* stream) {
+  SUFHIP_REQUIRE(count >= 0 && count <= kLin2Jobs && (count == 0 || jobs),
+                 "sufhip_lin2_batch: 0..4 jobs");
+  Lin2Batch b{};
+  b.begin[0] = 0;
+  for (int k = 0; k < count; ++k) {
+    const sufhip_lin2_job& jb = jobs[k];
+    if (jb.n == 0) continue;
+    SUFHIP_REQUIRE(jb.n < kMaxElems, "sufhip_lin2_batch: n too large");
+    SUFHIP_REQUIRE(jb.out[0] || jb.out[1] || jb.xhat || jb.trunc, "sufhip_lin2_batch: no output");
+    if (int rc = check_operand(jb.x, jb.n, "sufhip_lin2_batch")) return rc;
+    const int c = b.count;
+    if (int rc = make_epi(jb.trunc, jb.n, "sufhip_lin2_batch", &b.epi[c])) return rc;
+    b.x[c] = jb.x;
+    b.n[c] = jb.n;
+    b.out[c][0] = jb.out[0];
+    b.out[c][1] = jb.out[1];
+    b.xhat[c] = jb.xhat;
+    b.mask[c] = jb.mask;
+    b.begin[c + 1] = b.begin[c] + ew_grid(jb.n);
+    ++b.count;
+  }
+  if (b.count == 0) return SUFHIP_OK;
+  hipLaunchKernelGGL(lin2_batch_kernel, dim3(b.begin[b.count]), dim3(kBlock), 0,
+                     as_stream(stream), b);
+  return check_launch("lin2_batch_kernel");
 }
 
 int sufhip_mul2x(const sufhip_mul2x_args* args, size_t n, void* stream) {

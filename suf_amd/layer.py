@@ -32,8 +32,8 @@ import torch
 from . import native, spline, tables
 from .layernorm import LayerNormBlock
 from .softmax import SoftmaxBlock, causal_offsets
-from .tasks import (Dealer, Prepared, Trunc, dev, dev_i32, lin2, operand, pair, ptr, stream_ptr,
-                    term)
+from .tasks import (Dealer, Prepared, Trunc, dev, dev_i32, lin2, lin2_batch, operand, pair, ptr,
+                    stream_ptr, term)
 
 M64 = (1 << 64) - 1
 
@@ -72,13 +72,16 @@ class PublicMatmulTrunc:
                     native.ctypes.byref(trunc) if trunc is not None else None,
                     ptr(self.work), self.work_bytes, stream_ptr())
 
-    def eval2(self, X, out):
-        """Its truncation must have been prepared."""
+    def eval2(self, X, out, add=None):
+        """out = trunc_f(X W) (+ the pair `add`: a residual).  Its truncation
+        must have been prepared."""
         if self.tr.has_table():
-            self.product2(X, mask=self.tr.mask, trunc=self.tr.epilogue(out))
+            self.product2(X, mask=self.tr.mask, trunc=self.tr.epilogue(out, add))
         else:
             self.product2(X, zhat=self.zhat, mask=self.tr.mask)
             self.tr.finish(self.zhat, out)
+            if add is not None:
+                lin2(operand(term(out), term(add)), self.M * self.N, out=out)
         return out
 
 
@@ -167,6 +170,7 @@ class AttentionCore:
         hsd = heads * seq * dh
         self.D = torch.empty(hsd, dtype=torch.int64, device=device)
         self.E = torch.empty(hsd, dtype=torch.int64, device=device)
+        self.E2 = torch.empty(hsd, dtype=torch.int64, device=device)
         self.D2 = torch.empty(heads * seq * seq, dtype=torch.int64, device=device)
         self.S = pair(heads * seq * seq, device)
         self.Z = pair(hsd, device)
@@ -187,11 +191,13 @@ class AttentionCore:
         seq, d, h, dh, mp = self.seq, self.d, self.heads, self.dh, self.maps
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
-        # D = open(Q_h - A), E = open(K_h^T - B), then the per-head products.
-        lin2(operand(term(qkv, index=mp["gq"]), term(self.tri_qk.A, neg=True)), h * seq * dh,
-             xhat=self.D)
-        lin2(operand(term(qkv, index=mp["gk"]), term(self.tri_qk.B, neg=True)), h * seq * dh,
-             xhat=self.E)
+        # D = open(Q_h - A), E = open(K_h^T - B), and already the second
+        # product's E2 = open(V_h - B2), in one launch; then the per-head products.
+        hsd = h * seq * dh
+        lin2_batch([
+            (operand(term(qkv, index=mp["gq"]), term(self.tri_qk.A, neg=True)), hsd, self.D, 0),
+            (operand(term(qkv, index=mp["gk"]), term(self.tri_qk.B, neg=True)), hsd, self.E, 0),
+            (operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True)), hsd, self.E2, 0)])
         _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S)
         prep[0].wait(prep[1])
         scaled = operand(term(self.S, index=mp["gs"], mul=self.inv_sqrt))
@@ -207,9 +213,7 @@ class AttentionCore:
             self.softmax.eval2(self.scores, self.prob, prep=prep, fused=False)
             lin2(operand(term(self.prob, index=mp["gp"]), term(self.tri_pv.A, neg=True)),
                  h * seq * seq, xhat=self.D2)
-        lin2(operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True)), h * seq * dh,
-             xhat=self.E)
-        _beaver_batched(self.D2, self.E, self.tri_pv, h, seq, seq, dh, self.Z)
+        _beaver_batched(self.D2, self.E2, self.tri_pv, h, seq, seq, dh, self.Z)
         lin2(operand(term(self.Z, index=mp["gc"])), seq * d, into=(self.tr_c, out))
         return out
 
@@ -251,9 +255,8 @@ class TransformerLayer:
                                     frac_bits, device)
         self.side = torch.cuda.Stream(device=device)
         n = seq * d
-        self.h1, self.qkvs, self.ctx, self.a = pair(n), pair(3 * n), pair(n), pair(n)
-        self.r1, self.h2, self.u, self.g, self.m = pair(n), pair(n), pair(seq * ffn), \
-            pair(seq * ffn), pair(n)
+        self.h1, self.qkvs, self.ctx = pair(n), pair(3 * n), pair(n)
+        self.r1, self.h2, self.u, self.g = pair(n), pair(n), pair(seq * ffn), pair(seq * ffn)
 
     def stage_truncs(self):
         """The layer's truncation gates in four batches, in order of need."""
@@ -275,7 +278,6 @@ class TransformerLayer:
                 ev.record()
                 marks.append(ev)
 
-        n = self.seq * self.d
         mark()
         self.ln1.eval2(x, self.h1, prep=(prep, 0))
         mark()
@@ -285,8 +287,7 @@ class TransformerLayer:
         self.attn.eval2(self.qkvs, self.ctx, prep=(prep, 1))
         mark()
         prep.wait(2)
-        self.proj.eval2(self.ctx, self.a)
-        lin2(operand(term(self.a), term(x)), n, out=self.r1)
+        self.proj.eval2(self.ctx, self.r1, add=x)  # r1 = trunc(ctx Wout) + x
         mark()
         self.ln2.eval2(self.r1, self.h2, prep=(prep, 2))
         mark()
@@ -295,7 +296,6 @@ class TransformerLayer:
         mark()
         self.gelu.eval2(self.u, self.g, prep=(prep, 3))
         mark()
-        self.w2.eval2(self.g, self.m)
-        lin2(operand(term(self.m), term(self.r1)), n, out=out)
+        self.w2.eval2(self.g, out, add=self.r1)  # out = trunc(g W2) + r1
         mark()
         return out

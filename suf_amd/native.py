@@ -97,6 +97,7 @@ _SIGS = {
     "sufhip_interval_lut_eval2": (c_int, [c_vp, c_vp, c_sz, c_int, c_int, c_vp, c_vp, c_u64,
                                           c_sz, c_vp, c_vp, c_vp]),
     "sufhip_gate_chain2": (c_int, [c_vp, c_vp]),
+    "sufhip_lin2_batch": (c_int, [c_vp, c_int, c_vp]),
     "sufhip_layernorm2": (c_int, [c_vp, c_vp]),
     "sufhip_softmax2": (c_int, [c_vp, c_vp]),
     "sufhip_relu_max_tree2": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_vp, c_vp,
@@ -175,7 +176,7 @@ class Mul2xArgs(ctypes.Structure):
 class TruncEpilogue(ctypes.Structure):
     """sufhip_trunc_epilogue (include/suf_hip.h)."""
     _fields_ = [("key", c_vp * 2), ("table", c_vp * 2), ("work_bytes", c_sz),
-                ("frac_bits", c_int), ("y", c_vp * 2)]
+                ("frac_bits", c_int), ("y", c_vp * 2), ("add", c_vp * 2)]
 
 
 class Chain2Args(ctypes.Structure):
@@ -184,6 +185,12 @@ class Chain2Args(ctypes.Structure):
                 ("lut", c_vp * 2), ("lut_key_bytes", c_sz), ("intervals", c_int),
                 ("lut_mask", c_u64), ("a", Term2 * 4), ("b", Term2 * 4), ("c", Term2 * 4),
                 ("trunc", TruncEpilogue * 4), ("trunc_mask", c_u64 * 4), ("out", c_vp * 2)]
+
+
+class Lin2Job(ctypes.Structure):
+    """sufhip_lin2_job (include/suf_hip.h)."""
+    _fields_ = [("x", Operand2), ("n", c_sz), ("out", c_vp * 2), ("xhat", c_vp),
+                ("mask", c_u64), ("trunc", c_vp)]
 
 
 class Triple2(ctypes.Structure):

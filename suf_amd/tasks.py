@@ -116,6 +116,15 @@ def lin2(x, n, out=None, xhat=None, mask=0, into=None):
     _after(fin)
 
 
+def lin2_batch(jobs):
+    """Up to four independent lin2 opens in one launch: jobs of (operand, n,
+    xhat, mask)."""
+    arr = (native.Lin2Job * len(jobs))()
+    for k, (x, n, xhat, mask) in enumerate(jobs):
+        arr[k].x, arr[k].n, arr[k].xhat, arr[k].mask = x, n, ptr(xhat), mask & M64
+    native.call("sufhip_lin2_batch", arr, len(jobs), stream_ptr())
+
+
 def mul2x(u, v, tri, n, z=None, zhat=None, open_mask=0, z_add=None, into=None):
     """Beaver product of two operands with triple `tri` (a Triples); writes
     the shares to z (pair), the masked open of the product to zhat, or with
@@ -218,13 +227,17 @@ class Trunc:
             out.append(j)
         return out
 
-    def epilogue(self, y):
+    def epilogue(self, y, add=None):
+        """The sufhip_trunc_epilogue writing the gate's outputs to the pair y
+        (plus the pair `add`, if given)."""
         e = native.TruncEpilogue()
         e.key[0], e.key[1] = ptr(self.keys[0]), ptr(self.keys[1])
         e.table[0], e.table[1] = ptr(self.work[0]), ptr(self.work[1])
         e.work_bytes = self.work_bytes
         e.frac_bits = self.f
         e.y[0], e.y[1] = ptr(y[0]), ptr(y[1])
+        if add is not None:
+            e.add[0], e.add[1] = ptr(add[0]), ptr(add[1])
         return e
 
     def prepare(self, stream=None):

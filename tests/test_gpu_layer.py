@@ -85,6 +85,40 @@ def test_public_matmul_trunc_reconstructs():
     rec = (u64(out[0]) + u64(out[1])).astype(np.uint64)
     want = fp.matmul_shift(X.view(np.int64).reshape(M, K), W, F).ravel().view(np.uint64)
     assert np.array_equal(rec, want)
+    # With a residual folded into the truncation's write: the same shares plus
+    # the addend, per party.
+    r = pfss.host_mt19937_64(74, 2 * M * N).reshape(2, M * N)
+    res = (dev(r[0]), dev(r[1]))
+    out2 = tuple(torch.empty(M * N, dtype=torch.int64, device="cuda") for _ in range(2))
+    pm.eval2((dev(x0), dev(x1)), out2, add=res)
+    for p in (0, 1):
+        assert np.array_equal(u64(out2[p]), (u64(out[p]) + r[p]).astype(np.uint64))
+
+
+def test_lin2_batch_matches_single_launches():
+    """Four opens of different sizes in one launch equal four sufhip_lin2
+    calls; a batch with a bad operand is refused on the host."""
+    from suf_amd.tasks import lin2, lin2_batch, operand, term
+    sizes = [1000, 1, 70000, 257]
+    jobs, want, keep = [], [], []  # keep: the operands' tensors stay alive until the batch
+    for k, n in enumerate(sizes):
+        v = pfss.host_mt19937_64(80 + k, 3 * n).reshape(3, n)
+        a = (dev(v[0]), dev(v[1]))
+        b = (dev(v[2]), dev(v[2]))
+        keep.append((a, b))
+        x = operand(term(a), term(b, neg=True), const=k + 1)
+        hat = torch.empty(n, dtype=torch.int64, device="cuda")
+        ref = torch.empty(n, dtype=torch.int64, device="cuda")
+        lin2(x, n, xhat=ref, mask=1000 + k)
+        jobs.append((x, n, hat, 1000 + k))
+        want.append(ref)
+    say("lin2 batch %s" % sizes)
+    lin2_batch(jobs)
+    for (_, _, hat, _), ref in zip(jobs, want):
+        assert np.array_equal(u64(hat), u64(ref))
+    bad = term((dev(np.zeros(4, np.uint64)), dev(np.zeros(4, np.uint64))))  # 4 < n elements
+    with pytest.raises(native.SufHipError):
+        lin2_batch([(operand(bad), 1000, jobs[0][2], 0)])
 
 
 def test_beaver_matmul2_batched_vs_oracle():
