@@ -271,7 +271,7 @@ __global__ void __launch_bounds__(256) trunc_eval_table_kernel(TruncEvalArgs a) 
 // Key-only halves of several gates at once: the walk to depth min(d, 12) of
 // every job in one launch (lanes [begin[j], begin[j+1]) belong to job j),
 // then per level one launch expanding every job that goes deeper.
-constexpr int kBatchJobs = 24;
+constexpr int kBatchJobs = 32;
 
 struct BatchLevelArgs {
   Prg4 prg;

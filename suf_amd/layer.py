@@ -259,18 +259,20 @@ class TransformerLayer:
         self.r1, self.h2, self.u, self.g = pair(n), pair(n), pair(seq * ffn), pair(seq * ffn)
 
     def stage_truncs(self):
-        """The layer's truncation gates in four batches, in order of need."""
-        return [self.ln1.truncs(),
-                self.qkv.truncs() + self.attn.truncs(),
-                self.proj.truncs() + self.ln2.truncs(),
-                self.w1.truncs() + self.gelu.truncs() + self.w2.truncs()]
+        """The layer's truncation gates in three batches, in order of need:
+        LN1 and the QKV product; the attention core; the whole second half
+        (issued once the QKV product is queued, see eval2)."""
+        return [self.ln1.truncs() + self.qkv.truncs(),
+                self.attn.truncs(),
+                self.proj.truncs() + self.ln2.truncs() + self.w1.truncs() + self.gelu.truncs() +
+                self.w2.truncs()]
 
     def eval2(self, x, out, marks=None):
         """x, out: pairs of int64 [seq * d] device tensors.  marks: optional
         list of torch events recorded after each stage (profiling).  The
-        key-only halves of all truncation gates run on a side stream in four
+        key-only halves of all truncation gates run on a side stream in three
         batches, each ahead of the stage that needs it."""
-        prep = Prepared(self.side, self.stage_truncs())
+        prep = Prepared(self.side, self.stage_truncs(), upfront=2)
 
         def mark():
             if marks is not None:
@@ -281,8 +283,8 @@ class TransformerLayer:
         mark()
         self.ln1.eval2(x, self.h1, prep=(prep, 0))
         mark()
-        prep.wait(1)
         self.qkv.eval2(self.h1, self.qkvs)
+        prep.release()  # the second half's gates, after the QKV product
         mark()
         self.attn.eval2(self.qkvs, self.ctx, prep=(prep, 1))
         mark()
@@ -291,10 +293,9 @@ class TransformerLayer:
         mark()
         self.ln2.eval2(self.r1, self.h2, prep=(prep, 2))
         mark()
-        prep.wait(3)
         self.w1.eval2(self.h2, self.u)
         mark()
-        self.gelu.eval2(self.u, self.g, prep=(prep, 3))
+        self.gelu.eval2(self.u, self.g, prep=(prep, 2))
         mark()
         self.w2.eval2(self.g, out, add=self.r1)  # out = trunc(g W2) + r1
         mark()

@@ -269,20 +269,34 @@ def prepare_batch(truncs, stream=None):
 class Prepared:
     """Key-only halves of a block's truncation gates issued on a side stream
     (in batches, in order of need); wait(k) makes the current stream wait for
-    batch k."""
+    batch k.  With upfront = u, only the first u batches are issued now and
+    release() issues the rest once the current stream's work so far is done
+    (so that they overlap later work instead of the next kernels)."""
 
-    def __init__(self, side, batches):
+    def __init__(self, side, batches, upfront=None):
+        self.side = side
+        self.batches = list(batches)
+        self.events = [None] * len(self.batches)
+        self.issued = 0
+        self._issue(len(self.batches) if upfront is None else upfront)
+
+    def _issue(self, upto):
         start = torch.cuda.Event()
         start.record()
-        side.wait_event(start)
-        self.events = []
-        for b in batches:
-            prepare_batch(b, side)
+        self.side.wait_event(start)
+        for k in range(self.issued, upto):
+            prepare_batch(self.batches[k], self.side)
             ev = torch.cuda.Event()
-            ev.record(side)
-            self.events.append(ev)
+            ev.record(self.side)
+            self.events[k] = ev
+        self.issued = max(self.issued, upto)
+
+    def release(self):
+        self._issue(len(self.batches))
 
     def wait(self, k=0):
+        if self.events[k] is None:
+            raise RuntimeError("Prepared.wait: batch %d was not released" % k)
         torch.cuda.current_stream().wait_event(self.events[k])
 
 
