@@ -269,46 +269,109 @@ __global__ void __launch_bounds__(256) trunc_eval_table_kernel(TruncEvalArgs a) 
 }
 
 // Key-only halves of several gates at once: the walk to depth min(d, 12) of
-// every job in one launch (lanes [begin[j], begin[j+1]) belong to job j),
-// then per level one launch expanding every job that goes deeper.
+// up to kWalkJobs jobs in one launch (lanes [begin[j], begin[j+1]) belong to
+// job j), then per level one launch expanding up to kBatchJobs jobs that go
+// deeper.  Both argument blocks stay under 4 KB.
+constexpr int kWalkJobs = 96;
 constexpr int kBatchJobs = 32;
+
+// A table job's lanes walk to depth f - kWalkLocal and expand the last
+// kWalkLocal levels themselves (both children of each node: 4 AES blocks per
+// node instead of 2 per level per entry), so a lane writes 2^kWalkLocal
+// entries and the launch does about half (one local level) or a third (two)
+// of the AES work of one lane per entry.
+#ifndef SUFHIP_WALK_LOCAL
+#define SUFHIP_WALK_LOCAL 2
+#endif
+constexpr int kWalkLocal = SUFHIP_WALK_LOCAL;
+static_assert(kWalkLocal >= 0 && kWalkLocal <= 2, "kWalkLocal: 0, 1 or 2");
+
+struct WalkArgs {
+  Prg4 prg;
+  int count;
+  uint32_t begin[kWalkJobs + 1];
+  const uint8_t* key[kWalkJobs];
+  uint4* out[kWalkJobs];
+  uint32_t geo[kWalkJobs];  // f | d << 8 | e << 16: bits, depth written, local levels
+};
 
 struct BatchLevelArgs {
   Prg4 prg;
   int count;
-  int level;  // expansion: the common input depth; walk: unused
+  int level;  // the common input depth
   uint32_t begin[kBatchJobs + 1];
   const uint8_t* key[kBatchJobs];
   const uint4* in[kBatchJobs];
   uint4* out[kBatchJobs];
   int f[kBatchJobs];
-  int d[kBatchJobs];  // walk: depth walked
 };
 
-__device__ __forceinline__ int batch_job(const BatchLevelArgs& a, uint32_t g) {
-  int j = 0;
-  while (j + 1 < a.count && g >= a.begin[j + 1]) ++j;
-  return j;
+static_assert(sizeof(WalkArgs) <= 4096 && sizeof(BatchLevelArgs) <= 4096,
+              "kernel argument blocks must fit in 4 KB");
+
+__device__ __forceinline__ void put_leaf(uint4* nodes, uint32_t v, const uint8_t* chunk, int f,
+                                         uint32_t party, const Add64State& st) {
+  const uint64_t out = add64_finish(chunk, f, party, st);
+  nodes[2 * v + 1] = make_uint4(uint32_t(out), uint32_t(out >> 32), 0, 0);
 }
 
-__global__ void __launch_bounds__(kDcfBlock) trunc_batch_walk_kernel(BatchLevelArgs a) {
+// The job of lane g: the last j < count with begin[j] <= g (jobs with no
+// lanes share their begin with the next job, so the last such j owns g).
+template <int kJobs>
+__device__ __forceinline__ int batch_job(const uint32_t (&begin)[kJobs + 1], int count,
+                                         uint32_t g) {
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (begin[mid] <= g)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+__global__ void __launch_bounds__(kDcfBlock) trunc_batch_walk_kernel(WalkArgs a) {
   SUFHIP_DCF_LDS_SETUP(a.prg);
   const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= a.begin[a.count]) return;
-  const int j = batch_job(a, g);
+  const int j = batch_job<kWalkJobs>(a.begin, a.count, g);
   const uint8_t* key = a.key[j];
   const uint32_t v = g - a.begin[j];
   if (!(key[7] & 1)) return;
   const uint32_t party = key[6] & 1u;
   const uint8_t* chunk = key + kHdrBytes + 8;
-  const int f = a.f[j], d = a.d[j];
-  const uint64_t x = uint64_t(v) << (f - d);
+  const uint32_t geo = a.geo[j];
+  const int f = int(geo & 0xff), d = int((geo >> 8) & 0xff), e = int(geo >> 16);
+  const int dw = d - e;  // depth this lane walks to
+  const uint64_t x = uint64_t(v) << (f - dw);
   Add64State st = add64_root(chunk, party);
-  add64_walk(aes, rkl, chunk, f, 0, d, x, party, st);
+  add64_walk(aes, rkl, chunk, f, 0, dw, x, party, st);
   uint4* nodes = a.out[j];
-  if (d == f) {
-    const uint64_t out = add64_finish(chunk, f, party, st);
-    nodes[2 * v + 1] = make_uint4(uint32_t(out), uint32_t(out >> 32), 0, 0);
+  if (e > 0) {
+    // d == f: the children (and grandchildren) of node v are table entries.
+    Add64State c[2] = {st, st};
+#pragma unroll
+    for (uint32_t b = 0; b < 2; ++b)
+      add64_walk(aes, rkl, chunk, f, dw, dw + 1, uint64_t(b) << (f - 1 - dw), party, c[b]);
+    if (e == 1) {
+#pragma unroll
+      for (uint32_t b = 0; b < 2; ++b) put_leaf(nodes, 2 * v + b, chunk, f, party, c[b]);
+    } else {
+#pragma unroll
+      for (uint32_t b = 0; b < 2; ++b) {
+        Add64State g[2] = {c[b], c[b]};
+#pragma unroll
+        for (uint32_t b2 = 0; b2 < 2; ++b2)
+          add64_walk(aes, rkl, chunk, f, dw + 1, dw + 2, uint64_t(b2) << (f - 2 - dw), party,
+                     g[b2]);
+#pragma unroll
+        for (uint32_t b2 = 0; b2 < 2; ++b2)
+          put_leaf(nodes, 4 * v + 2 * b + b2, chunk, f, party, g[b2]);
+      }
+    }
+  } else if (d == f) {
+    put_leaf(nodes, v, chunk, f, party, st);
   } else {
     nodes[2 * v] = make_uint4(st.s0, st.s1, st.s2, st.s3);
     nodes[2 * v + 1] = make_uint4(uint32_t(st.v), uint32_t(st.v >> 32), st.t, 0);
@@ -320,7 +383,7 @@ __global__ void __launch_bounds__(kDcfBlock) trunc_batch_expand_kernel(BatchLeve
   const uint32_t total = a.begin[a.count];
   for (uint32_t g = blockIdx.x * blockDim.x + threadIdx.x; g < total;
        g += gridDim.x * blockDim.x) {
-    const int j = batch_job(a, g);
+    const int j = batch_job<kBatchJobs>(a.begin, a.count, g);
     const uint8_t* key = a.key[j];
     if (!(key[7] & 1)) continue;
     const uint32_t party = key[6] & 1u;
@@ -356,6 +419,21 @@ int spread_grid(size_t count, unsigned int* grid, unsigned int* block) {
   const size_t g = (count + b - 1) / b;
   *block = unsigned(b);
   *grid = unsigned(g < size_t(cus) ? g : size_t(cus));
+  return SUFHIP_OK;
+}
+
+// Launch shape for the batched walk (one lane per walk, no grid stride):
+// the lanes spread over every CU, 128..512 per workgroup.
+int walk_grid(size_t count, unsigned int* grid, unsigned int* block) {
+  int dev = 0, cus = 0;
+  SUFHIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
+  SUFHIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+               "hipDeviceGetAttribute(CU count)");
+  size_t per = (count + size_t(cus) - 1) / size_t(cus);
+  per = (per + 63) / 64 * 64;
+  const size_t b = per < 128 ? 128 : (per > size_t(kDcfBlock) ? size_t(kDcfBlock) : per);
+  *block = unsigned(b);
+  *grid = unsigned((count + b - 1) / b);
   return SUFHIP_OK;
 }
 
@@ -562,12 +640,12 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
   hipStream_t s = as_stream(stream);
   Prg4 prg;
   fill_prg4(prg_state, &prg);
-  for (int base = 0; base < count; base += kBatchJobs) {
-    const int m = count - base < kBatchJobs ? count - base : kBatchJobs;
+  for (int base = 0; base < count; base += kWalkJobs) {
+    const int m = count - base < kWalkJobs ? count - base : kWalkJobs;
     // Per job: its depth d, walked depth k0 and the two workspace regions,
     // alternated so that depth d ends in the first (as sufhip_trunc_prepare).
-    int d[kBatchJobs], k0s[kBatchJobs], cur[kBatchJobs];
-    uint4* lvl[kBatchJobs][2];
+    int d[kWalkJobs], k0s[kWalkJobs], cur[kWalkJobs];
+    uint4* lvl[kWalkJobs][2];
     int maxd = 0;
     for (int i = 0; i < m; ++i) {
       const sufhip_trunc_job& jb = jobs[base + i];
@@ -582,45 +660,50 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
       cur[i] = (d[i] - k0) & 1;
       if (d[i] > maxd) maxd = d[i];
     }
-    BatchLevelArgs wa{};
+    WalkArgs wa{};
     wa.prg = prg;
     wa.begin[0] = 0;
     for (int i = 0; i < m; ++i) {
       const sufhip_trunc_job& jb = jobs[base + i];
       const int k0 = k0s[i];
-      wa.key[wa.count] = jb.d_key;
-      wa.out[wa.count] = lvl[i][cur[i]];
-      wa.f[wa.count] = jb.frac_bits;
-      wa.d[wa.count] = k0;
-      wa.begin[wa.count + 1] = wa.begin[wa.count] + (d[i] > 0 ? (1u << k0) : 0u);
-      ++wa.count;
+      const int e = k0 == jb.frac_bits ? (k0 < kWalkLocal ? k0 : kWalkLocal) : 0;
+      wa.key[i] = jb.d_key;
+      wa.out[i] = lvl[i][cur[i]];
+      wa.geo[i] = uint32_t(jb.frac_bits) | uint32_t(k0) << 8 | uint32_t(e) << 16;
+      wa.begin[i + 1] = wa.begin[i] + (d[i] > 0 ? (1u << (k0 - e)) : 0u);
     }
-    if (wa.begin[wa.count] > 0) {
-      const unsigned b = kDcfBlock;
-      const unsigned g = (wa.begin[wa.count] + b - 1) / b;
+    wa.count = m;
+    if (wa.begin[m] > 0) {
+      unsigned int g = 0, b = 0;
+      if (int rc = walk_grid(wa.begin[m], &g, &b)) return rc;
       hipLaunchKernelGGL(trunc_batch_walk_kernel, dim3(g), dim3(b), 0, s, wa);
       if (int rc = check_launch("trunc_batch_walk_kernel")) return rc;
     }
     for (int level = kWalkFrontierBits; level < maxd; ++level) {
-      BatchLevelArgs ea{};
-      ea.prg = prg;
-      ea.level = level;
-      ea.begin[0] = 0;
-      for (int i = 0; i < m; ++i) {
-        if (d[i] <= level || k0s[i] > level) continue;
-        ea.key[ea.count] = jobs[base + i].d_key;
-        ea.in[ea.count] = lvl[i][cur[i]];
-        ea.out[ea.count] = lvl[i][cur[i] ^ 1];
-        ea.f[ea.count] = jobs[base + i].frac_bits;
-        ea.begin[ea.count + 1] = ea.begin[ea.count] + (2u << level);
-        ++ea.count;
-        cur[i] ^= 1;
+      // Jobs still expanding at this level, kBatchJobs per launch.
+      int deep[kWalkJobs], nd = 0;
+      for (int i = 0; i < m; ++i)
+        if (d[i] > level && k0s[i] <= level) deep[nd++] = i;
+      for (int q0 = 0; q0 < nd; q0 += kBatchJobs) {
+        BatchLevelArgs ea{};
+        ea.prg = prg;
+        ea.level = level;
+        ea.begin[0] = 0;
+        for (int q = q0; q < nd && q < q0 + kBatchJobs; ++q) {
+          const int i = deep[q];
+          ea.key[ea.count] = jobs[base + i].d_key;
+          ea.in[ea.count] = lvl[i][cur[i]];
+          ea.out[ea.count] = lvl[i][cur[i] ^ 1];
+          ea.f[ea.count] = jobs[base + i].frac_bits;
+          ea.begin[ea.count + 1] = ea.begin[ea.count] + (2u << level);
+          ++ea.count;
+          cur[i] ^= 1;
+        }
+        unsigned int eg = 0, eb = 0;
+        if (int rc = spread_grid(ea.begin[ea.count], &eg, &eb)) return rc;
+        hipLaunchKernelGGL(trunc_batch_expand_kernel, dim3(eg), dim3(eb), 0, s, ea);
+        if (int rc = check_launch("trunc_batch_expand_kernel")) return rc;
       }
-      if (ea.count == 0) continue;  // every job of this level was walked
-      unsigned int eg = 0, eb = 0;
-      if (int rc = spread_grid(ea.begin[ea.count], &eg, &eb)) return rc;
-      hipLaunchKernelGGL(trunc_batch_expand_kernel, dim3(eg), dim3(eb), 0, s, ea);
-      if (int rc = check_launch("trunc_batch_expand_kernel")) return rc;
     }
   }
   return SUFHIP_OK;

@@ -267,12 +267,20 @@ class TransformerLayer:
                 self.proj.truncs() + self.ln2.truncs() + self.w1.truncs() + self.gelu.truncs() +
                 self.w2.truncs()]
 
-    def eval2(self, x, out, marks=None):
+    def eval2(self, x, out, marks=None, overlap_prepare=False):
         """x, out: pairs of int64 [seq * d] device tensors.  marks: optional
         list of torch events recorded after each stage (profiling).  The
-        key-only halves of all truncation gates run on a side stream in three
-        batches, each ahead of the stage that needs it."""
-        prep = Prepared(self.side, self.stage_truncs(), upfront=2)
+        key-only halves of all truncation gates run first, in one batched
+        walk on the current stream; with overlap_prepare they run on a side
+        stream instead, in three batches, each ahead of the stage that needs
+        it (a fork or join between streams costs about as much as it
+        hides)."""
+        if overlap_prepare:
+            prep = Prepared(self.side, self.stage_truncs(), upfront=2)
+            b = lambda k: k  # noqa: E731
+        else:
+            prep = Prepared(None, [sum(self.stage_truncs(), [])])
+            b = lambda k: 0  # noqa: E731
 
         def mark():
             if marks is not None:
@@ -281,21 +289,21 @@ class TransformerLayer:
                 marks.append(ev)
 
         mark()
-        self.ln1.eval2(x, self.h1, prep=(prep, 0))
+        self.ln1.eval2(x, self.h1, prep=(prep, b(0)))
         mark()
         self.qkv.eval2(self.h1, self.qkvs)
         prep.release()  # the second half's gates, after the QKV product
         mark()
-        self.attn.eval2(self.qkvs, self.ctx, prep=(prep, 1))
+        self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)))
         mark()
-        prep.wait(2)
+        prep.wait(b(2))
         self.proj.eval2(self.ctx, self.r1, add=x)  # r1 = trunc(ctx Wout) + x
         mark()
-        self.ln2.eval2(self.r1, self.h2, prep=(prep, 2))
+        self.ln2.eval2(self.r1, self.h2, prep=(prep, b(2)))
         mark()
         self.w1.eval2(self.h2, self.u)
         mark()
-        self.gelu.eval2(self.u, self.g, prep=(prep, 2))
+        self.gelu.eval2(self.u, self.g, prep=(prep, b(2)))
         mark()
         self.w2.eval2(self.g, out, add=self.r1)  # out = trunc(g W2) + r1
         mark()

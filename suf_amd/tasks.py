@@ -271,7 +271,9 @@ class Prepared:
     (in batches, in order of need); wait(k) makes the current stream wait for
     batch k.  With upfront = u, only the first u batches are issued now and
     release() issues the rest once the current stream's work so far is done
-    (so that they overlap later work instead of the next kernels)."""
+    (so that they overlap later work instead of the next kernels).  With
+    side = None the batches are issued on the current stream itself and
+    wait() has nothing to order."""
 
     def __init__(self, side, batches, upfront=None):
         self.side = side
@@ -281,6 +283,11 @@ class Prepared:
         self._issue(len(self.batches) if upfront is None else upfront)
 
     def _issue(self, upto):
+        if self.side is None:
+            for k in range(self.issued, upto):
+                prepare_batch(self.batches[k])
+            self.issued = max(self.issued, upto)
+            return
         start = torch.cuda.Event()
         start.record()
         self.side.wait_event(start)
@@ -295,9 +302,10 @@ class Prepared:
         self._issue(len(self.batches))
 
     def wait(self, k=0):
-        if self.events[k] is None:
+        if k >= self.issued:
             raise RuntimeError("Prepared.wait: batch %d was not released" % k)
-        torch.cuda.current_stream().wait_event(self.events[k])
+        if self.side is not None:
+            torch.cuda.current_stream().wait_event(self.events[k])
 
 
 def rotated_lut(alpha, coeffs, r_in):
