@@ -346,6 +346,64 @@ struct AesLds4 {
     const uint32_t c0 = col(s0, s1, s2, s3, rk[9].x);
     return (t<3, 0>(c0) ^ rk[10].x) & 0xffu;
   }
+  // Value of lane (q + k) % 4 of this lane's quad (DPP quad permute).
+  template <int k>
+  __device__ __forceinline__ static uint32_t quad_rot(uint32_t v) {
+    constexpr int ctrl = ((0 + k) & 3) | ((1 + k) & 3) << 2 | ((2 + k) & 3) << 4 | ((3 + k) & 3) << 6;
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), ctrl, 0xf, 0xf, false));
+  }
+  // Column-parallel AES-128 over a quad of lanes (lanes 4m..4m+3, all
+  // active): lane q = lane & 3 holds column q of the state and reads column
+  // q of round key r at rkq[4 r].  A lane looks up the four bytes of its own
+  // column -- byte k feeds output column q - k through T_k -- and takes the
+  // other three terms of its column from lanes q + 1, q + 2 and q + 3 (DPP
+  // quad permutes).  Per round a lane issues 4 table reads and about 8 VALU
+  // operations instead of 16 and 24: a quarter of encrypt()'s dependent
+  // issue time for one block, at 4 lanes per block.  encrypt_quad_n runs
+  // N independent blocks in lockstep (their table reads issued together).
+  template <int N>
+  __device__ __forceinline__ void encrypt_quad_n(uint32_t (&s)[N],
+                                                 const uint32_t* const (&rkq)[N]) const {
+#pragma unroll
+    for (int n = 0; n < N; ++n) s[n] ^= rkq[n][0];
+#pragma unroll
+    for (int r = 1; r < 10; ++r) {
+      uint32_t a[N][4];
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        a[n][0] = t<0, 0>(s[n]);
+        a[n][1] = t<1, 1>(s[n]);
+        a[n][2] = t<2, 2>(s[n]);
+        a[n][3] = t<3, 3>(s[n]);
+      }
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+        s[n] = a[n][0] ^ quad_rot<1>(a[n][1]) ^ quad_rot<2>(a[n][2]) ^ quad_rot<3>(a[n][3]) ^
+               rkq[n][4 * r];
+    }
+    // Final round: S(x) is byte 0 of T3[x], bytes 1 and 2 of T0[x] and
+    // byte 3 of T1[x].
+    uint32_t u[N][4];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      u[n][0] = t<3, 0>(s[n]);
+      u[n][1] = t<0, 1>(s[n]);
+      u[n][2] = t<0, 2>(s[n]);
+      u[n][3] = t<1, 3>(s[n]);
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const uint32_t lo = (u[n][0] & 0xffu) | (quad_rot<1>(u[n][1]) & 0xff00u);
+      const uint32_t hi = (quad_rot<2>(u[n][2]) & 0xff0000u) | (quad_rot<3>(u[n][3]) & 0xff000000u);
+      s[n] = (lo | hi) ^ rkq[n][40];
+    }
+  }
+  __device__ __forceinline__ uint32_t encrypt_quad(uint32_t pt, const uint32_t* rkq) const {
+    uint32_t s[1] = {pt};
+    const uint32_t* const k[1] = {rkq};
+    encrypt_quad_n<1>(s, k);
+    return s[0];
+  }
   // Ciphertext words 0 and 1 only (the final round skips columns 2 and 3).
   __device__ __forceinline__ void encrypt_lo2(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t s3,
                                               const uint4* rk, uint32_t& o0,

@@ -275,16 +275,22 @@ __global__ void __launch_bounds__(256) trunc_eval_table_kernel(TruncEvalArgs a) 
 constexpr int kWalkJobs = 96;
 constexpr int kBatchJobs = 32;
 
-// A table job's lanes walk to depth f - kWalkLocal and expand the last
-// kWalkLocal levels themselves (both children of each node: 4 AES blocks per
-// node instead of 2 per level per entry), so a lane writes 2^kWalkLocal
-// entries and the launch does about half (one local level) or a third (two)
-// of the AES work of one lane per entry.
+// A table job's walks go to depth f - kWalkLocal and expand the last
+// kWalkLocal levels themselves (both children of each node), so a walk writes
+// 2^kWalkLocal entries: 2 (f - kWalkLocal) + 4 (2^kWalkLocal - 1) AES blocks
+// per 2^kWalkLocal entries instead of 2 f per entry.
 #ifndef SUFHIP_WALK_LOCAL
-#define SUFHIP_WALK_LOCAL 2
+#define SUFHIP_WALK_LOCAL 4
 #endif
 constexpr int kWalkLocal = SUFHIP_WALK_LOCAL;
-static_assert(kWalkLocal >= 0 && kWalkLocal <= 2, "kWalkLocal: 0, 1 or 2");
+static_assert(kWalkLocal >= 1 && kWalkLocal <= 4, "kWalkLocal: 1..4");
+// Up to 1024 lanes per workgroup: the walk's 8 lanes per node and one
+// workgroup per CU (128 KB of AES tables) must cover a batch in one round.
+constexpr int kWalkBlock = 1024;
+#ifndef SUFHIP_WALK_GROUP
+#define SUFHIP_WALK_GROUP 4
+#endif
+constexpr int kWalkGroup = SUFHIP_WALK_GROUP;  // lockstep width of the expansion
 
 struct WalkArgs {
   Prg4 prg;
@@ -309,12 +315,6 @@ struct BatchLevelArgs {
 static_assert(sizeof(WalkArgs) <= 4096 && sizeof(BatchLevelArgs) <= 4096,
               "kernel argument blocks must fit in 4 KB");
 
-__device__ __forceinline__ void put_leaf(uint4* nodes, uint32_t v, const uint8_t* chunk, int f,
-                                         uint32_t party, const Add64State& st) {
-  const uint64_t out = add64_finish(chunk, f, party, st);
-  nodes[2 * v + 1] = make_uint4(uint32_t(out), uint32_t(out >> 32), 0, 0);
-}
-
 // The job of lane g: the last j < count with begin[j] <= g (jobs with no
 // lanes share their begin with the next job, so the last such j owns g).
 template <int kJobs>
@@ -331,50 +331,163 @@ __device__ __forceinline__ int batch_job(const uint32_t (&begin)[kJobs + 1], int
   return lo;
 }
 
-__global__ void __launch_bounds__(kDcfBlock) trunc_batch_walk_kernel(WalkArgs a) {
+// One walk per 8 lanes.  Lanes 0-3 of the group compute the next-seed block
+// AES_{K_{2b}}(s) and lanes 4-7 the value block AES_{K_{2b+1}}(s), column-
+// parallel (AesLds4::encrypt_quad): lane q of either half holds word q of the
+// seed.  A level is then about a quarter of the dependent issue time of the
+// one-lane walk (add64_walk), which bounds these latency-bound launches.
+struct Walk8 {
+  uint32_t s;  // seed word q (both halves)
+  uint32_t t;  // control bit (both halves)
+  uint64_t v;  // accumulated value, low 64 bits (value half)
+};
+
+// Little-endian word at byte address p + 4 idx (any alignment; reads the
+// aligned words idx and idx + 1 around it).
+__device__ __forceinline__ uint32_t word_at(const uint8_t* p, int idx) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+  return __builtin_amdgcn_alignbyte(w[idx + 1], w[idx], uint32_t(a & 3));
+}
+
+__device__ __forceinline__ uint32_t row_shr4(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x114, 0xf, 0xf, false));
+}
+
+template <int kLane>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_mov_dpp(int(v), kLane * 0x55, 0xf, 0xf, false));
+}
+
+struct Walk8Ctx {
+  const DcfAes& aes;
+  const uint4* rkl;
+  const uint8_t* chunk;
+  uint4* nodes;
+  int f;
+  uint32_t party, h, q;
+};
+
+// One level (record cw) of N independent walks in lockstep: walk n goes
+// from state par[(b0 + n) >> 1] towards child bit (b0 + n) & 1 (the walk
+// loop passes N = 1 and its own bit as b0).  add64_walk's level on 8 lanes.
+template <int N>
+__device__ __forceinline__ void walk8_step_n(const Walk8Ctx& c, const uint8_t* cw, uint32_t b0,
+                                             const Walk8* par, Walk8* kid) {
+  const uint32_t csq = word_at(cw, int(c.q));
+  const uint64_t cv = uint64_t(word_at(cw, 4)) | uint64_t(word_at(cw, 5)) << 32;
+  const uint32_t tb = cw[32];
+  uint32_t o[N];
+  const uint32_t* rkq[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    const uint32_t b = N == 1 ? b0 : ((b0 + n) & 1u);
+    o[n] = par[N == 1 ? 0 : (b0 + n) >> 1].s;
+    rkq[n] = reinterpret_cast<const uint32_t*>(c.rkl + 11 * (2 * b + c.h)) + c.q;
+  }
+  c.aes.encrypt_quad_n<N>(o, rkq);
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    const Walk8& w = par[N == 1 ? 0 : (b0 + n) >> 1];
+    const uint32_t b = N == 1 ? b0 : ((b0 + n) & 1u);
+    uint32_t on = o[n] ^ w.s;
+    // Value half: the low 64 bits of its block; seed half: bit 127 of its block.
+    const uint64_t vd0 = uint64_t(quad_bcast<0>(on)) | uint64_t(quad_bcast<1>(on)) << 32;
+    uint32_t tn = quad_bcast<3>(on) >> 31;
+    if (c.q == 3) on &= 0x7fffffffu;
+    on ^= csq & (0u - w.t);
+    tn ^= ((b ? tb : (tb >> 1)) & 1u) & w.t;
+    const uint64_t vd = vd0 + (w.t ? cv : 0);
+    Walk8 r;
+    r.v = w.v + (c.party ? 0 - vd : vd);
+    // The seed half's next seed and t move to the value half (lane - 4).
+    const uint32_t os = row_shr4(on), ts = row_shr4(tn);
+    r.s = c.h ? os : on;
+    r.t = c.h ? ts : tn;
+    kid[n] = r;
+  }
+}
+
+// Table entry `leaf` from a depth-f state (add64_finish), written by lane 0
+// of the value half, which holds the seed, t and v.
+__device__ __forceinline__ void walk8_leaf(const Walk8Ctx& c, const Walk8& w, uint32_t leaf) {
+  const uint8_t* np1 = c.chunk + 16 + 33 * c.f;
+  const uint64_t s64 = uint64_t(quad_bcast<0>(w.s)) | uint64_t(quad_bcast<1>(w.s)) << 32;
+  const uint64_t n64 = uint64_t(word_at(np1, 0)) | uint64_t(word_at(np1, 1)) << 32;
+  const uint64_t sv = s64 + (w.t ? n64 : 0);
+  const uint64_t out = w.v + (c.party ? 0 - sv : sv);
+  if (c.h == 1 && c.q == 0)
+    c.nodes[2 * leaf + 1] = make_uint4(uint32_t(out), uint32_t(out >> 32), 0, 0);
+}
+
+// Breadth-first expansion of the subtree below a depth-(f - E) node: the
+// 2^(L+1) children of level L in lockstep groups of kWalkGroup, then the
+// table entries (v << E) | i in order.
+template <int L, int E>
+__device__ __forceinline__ void walk8_expand(const Walk8Ctx& c, const uint8_t* cw,
+                                             const Walk8 (&par)[1 << L], uint32_t v) {
+  if constexpr (L == E) {
+    walk8_leaf(c, par[0], v);  // E = 0
+  } else if constexpr (L + 1 == E) {
+    // The last level: each group's children are written as soon as they exist.
+    constexpr int kKids = 2 << L;
+    constexpr int kGroup = kKids < kWalkGroup ? kKids : kWalkGroup;
+#pragma unroll
+    for (int b0 = 0; b0 < kKids; b0 += kGroup) {
+      Walk8 kid[kGroup];
+      walk8_step_n<kGroup>(c, cw, b0, par, kid);
+#pragma unroll
+      for (int i = 0; i < kGroup; ++i) walk8_leaf(c, kid[i], (v << E) | uint32_t(b0 + i));
+    }
+  } else {
+    constexpr int kKids = 2 << L;
+    constexpr int kGroup = kKids < kWalkGroup ? kKids : kWalkGroup;
+    Walk8 kid[kKids];
+#pragma unroll
+    for (int b0 = 0; b0 < kKids; b0 += kGroup) walk8_step_n<kGroup>(c, cw, b0, par, kid + b0);
+    walk8_expand<L + 1, E>(c, cw + 33, kid, v);
+  }
+}
+
+__global__ void __launch_bounds__(kWalkBlock) trunc_batch_walk_kernel(WalkArgs a) {
   SUFHIP_DCF_LDS_SETUP(a.prg);
-  const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t gl = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t g = gl >> 3;  // walk; whole 8-lane groups leave together
   if (g >= a.begin[a.count]) return;
   const int j = batch_job<kWalkJobs>(a.begin, a.count, g);
   const uint8_t* key = a.key[j];
   const uint32_t v = g - a.begin[j];
   if (!(key[7] & 1)) return;
-  const uint32_t party = key[6] & 1u;
-  const uint8_t* chunk = key + kHdrBytes + 8;
   const uint32_t geo = a.geo[j];
   const int f = int(geo & 0xff), d = int((geo >> 8) & 0xff), e = int(geo >> 16);
-  const int dw = d - e;  // depth this lane walks to
+  const uint8_t* chunk = key + kHdrBytes + 8;
+  const Walk8Ctx c{aes, rkl, chunk, a.out[j], f, uint32_t(key[6] & 1u), (gl >> 2) & 1u, gl & 3u};
+  const int dw = d - e;  // depth walked before the local expansion
   const uint64_t x = uint64_t(v) << (f - dw);
-  Add64State st = add64_root(chunk, party);
-  add64_walk(aes, rkl, chunk, f, 0, dw, x, party, st);
-  uint4* nodes = a.out[j];
-  if (e > 0) {
-    // d == f: the children (and grandchildren) of node v are table entries.
-    Add64State c[2] = {st, st};
-#pragma unroll
-    for (uint32_t b = 0; b < 2; ++b)
-      add64_walk(aes, rkl, chunk, f, dw, dw + 1, uint64_t(b) << (f - 1 - dw), party, c[b]);
-    if (e == 1) {
-#pragma unroll
-      for (uint32_t b = 0; b < 2; ++b) put_leaf(nodes, 2 * v + b, chunk, f, party, c[b]);
-    } else {
-#pragma unroll
-      for (uint32_t b = 0; b < 2; ++b) {
-        Add64State g[2] = {c[b], c[b]};
-#pragma unroll
-        for (uint32_t b2 = 0; b2 < 2; ++b2)
-          add64_walk(aes, rkl, chunk, f, dw + 1, dw + 2, uint64_t(b2) << (f - 2 - dw), party,
-                     g[b2]);
-#pragma unroll
-        for (uint32_t b2 = 0; b2 < 2; ++b2)
-          put_leaf(nodes, 4 * v + 2 * b + b2, chunk, f, party, g[b2]);
-      }
-    }
+  Walk8 w;
+  w.s = word_at(chunk, int(c.q));
+  if (c.q == 3) w.s &= 0x7fffffffu;
+  w.t = c.party;
+  w.v = 0;
+  const uint8_t* cw = chunk + 16;
+  for (int i = 0; i < dw; ++i, cw += 33) {
+    Walk8 n[1];
+    walk8_step_n<1>(c, cw, uint32_t(x >> (f - 1 - i)) & 1u, &w, n);
+    w = n[0];
+  }
+  if (e == kWalkLocal) {
+    const Walk8 root[1] = {w};
+    walk8_expand<0, kWalkLocal>(c, cw, root, v);
   } else if (d == f) {
-    put_leaf(nodes, v, chunk, f, party, st);
+    walk8_leaf(c, w, v);
   } else {
-    nodes[2 * v] = make_uint4(st.s0, st.s1, st.s2, st.s3);
-    nodes[2 * v + 1] = make_uint4(uint32_t(st.v), uint32_t(st.v >> 32), st.t, 0);
+    // Frontier node for the expansion launches: {s0..s3}, {v_lo, v_hi, t, 0}.
+    const uint4 sn = make_uint4(quad_bcast<0>(w.s), quad_bcast<1>(w.s), quad_bcast<2>(w.s),
+                                quad_bcast<3>(w.s));
+    if (c.h == 1 && c.q == 0) {
+      c.nodes[2 * v] = sn;
+      c.nodes[2 * v + 1] = make_uint4(uint32_t(w.v), uint32_t(w.v >> 32), w.t, 0);
+    }
   }
 }
 
@@ -422,8 +535,8 @@ int spread_grid(size_t count, unsigned int* grid, unsigned int* block) {
   return SUFHIP_OK;
 }
 
-// Launch shape for the batched walk (one lane per walk, no grid stride):
-// the lanes spread over every CU, 128..512 per workgroup.
+// Launch shape for the batched walk (8 lanes per walk, no grid stride): the
+// lanes spread over every CU, 128..kWalkBlock per workgroup.
 int walk_grid(size_t count, unsigned int* grid, unsigned int* block) {
   int dev = 0, cus = 0;
   SUFHIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
@@ -431,7 +544,7 @@ int walk_grid(size_t count, unsigned int* grid, unsigned int* block) {
                "hipDeviceGetAttribute(CU count)");
   size_t per = (count + size_t(cus) - 1) / size_t(cus);
   per = (per + 63) / 64 * 64;
-  const size_t b = per < 128 ? 128 : (per > size_t(kDcfBlock) ? size_t(kDcfBlock) : per);
+  const size_t b = per < 128 ? 128 : (per > size_t(kWalkBlock) ? size_t(kWalkBlock) : per);
   *block = unsigned(b);
   *grid = unsigned((count + b - 1) / b);
   return SUFHIP_OK;
@@ -666,7 +779,7 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
     for (int i = 0; i < m; ++i) {
       const sufhip_trunc_job& jb = jobs[base + i];
       const int k0 = k0s[i];
-      const int e = k0 == jb.frac_bits ? (k0 < kWalkLocal ? k0 : kWalkLocal) : 0;
+      const int e = k0 == jb.frac_bits && k0 >= kWalkLocal ? kWalkLocal : 0;
       wa.key[i] = jb.d_key;
       wa.out[i] = lvl[i][cur[i]];
       wa.geo[i] = uint32_t(jb.frac_bits) | uint32_t(k0) << 8 | uint32_t(e) << 16;
@@ -675,7 +788,7 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
     wa.count = m;
     if (wa.begin[m] > 0) {
       unsigned int g = 0, b = 0;
-      if (int rc = walk_grid(wa.begin[m], &g, &b)) return rc;
+      if (int rc = walk_grid(8 * size_t(wa.begin[m]), &g, &b)) return rc;
       hipLaunchKernelGGL(trunc_batch_walk_kernel, dim3(g), dim3(b), 0, s, wa);
       if (int rc = check_launch("trunc_batch_walk_kernel")) return rc;
     }

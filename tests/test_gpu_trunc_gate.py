@@ -128,3 +128,34 @@ def test_errors():
                         work=torch.empty(1, dtype=torch.int64, device="cuda"))
     out = pfss.trunc_eval(native.TRUNC_GAPARS, 12, STATE, k0, xd[:0])
     assert out.numel() == 0
+
+
+def test_batched_prepare_matches_single_gate_path():
+    # sufhip_trunc_prepare_batch (8 lanes per walk, local expansion of the
+    # table gates' last levels, up to 96 jobs per walk launch) against the
+    # one-gate prepare of sufhip_trunc_eval: equal shares for every gate.
+    # 52 gates = 104 jobs, so the batch takes two walk launches; the shapes
+    # cover tables (f <= 14, including f below the local expansion depth),
+    # walked prefixes with expansion launches (f = 24, n = 2^16) and
+    # walked-only prefixes.
+    from suf_amd import tasks
+    shapes = [(native.TRUNC_GAPARS, 12, 3000), (native.TRUNC_GAPARS, 13, 500),
+              (native.TRUNC_GAPARS, 14, 700), (native.TRUNC_GAPARS, 2, 100),
+              (native.TRUNC_GAPARS, 5, 64), (native.TRUNC_GAPARS, 24, 1 << 16),
+              (native.TRUNC_GAPARS, 30, 3000), (native.TRUNC_TR, 12, 2000),
+              (native.TRUNC_ARS, 7, 300), (native.TRUNC_ARS, 24, 40)]
+    dealer = tasks.Dealer(77)
+    gates = [tasks.Trunc(dealer, f, n, STATE, kind=kind)
+             for i in range(52) for kind, f, n in [shapes[i % len(shapes)]]]
+    say("batched prepare: %d gates" % len(gates))
+    tasks.prepare_batch(gates)
+    rng = np.random.default_rng(5)
+    for i, g in enumerate(gates):
+        xhat = rng.integers(0, 1 << 64, g.n, dtype=np.uint64)
+        xd = dev(xhat)
+        out = (torch.empty(g.n, dtype=torch.int64, device="cuda"),
+               torch.empty(g.n, dtype=torch.int64, device="cuda"))
+        g.finish(xd, out)
+        for p in (0, 1):
+            want = u64(pfss.trunc_eval(g.kind, g.f, STATE, g.keys[p], xd))
+            assert np.array_equal(u64(out[p]), want), (i, g.kind, g.f, g.n, p)
