@@ -673,6 +673,34 @@ int sufhip_beaver_matmul2_batched(const uint64_t* d_D_open, const uint64_t* d_E_
                                   int K, int N, uint64_t* d_out0, uint64_t* d_out1, void* d_work,
                                   size_t work_bytes, void* stream);
 
+/* The same two-party batched product on the int8 matrix cores, exact
+ * (36 int8 digit GEMMs per operand pair): every operand as balanced
+ * base-256 digit planes, the triple shares' made once with the triples and
+ * the opens' per call.  sufhip_kb_split_batch writes up to
+ * SUFHIP_KB_SPLIT_JOBS operands' planes in one launch: src [batches][rows x
+ * cols] u64 row-major -> planes [8][batches][K/32][R][32] int8 with
+ * (K, R) = (cols, rows) for a left operand (k_is_col = 1: D, A_p) and
+ * (rows, cols) for a right one (k_is_col = 0: E, B_p); rows and cols
+ * multiples of 32, planes of sufhip_kb_planes_bytes() bytes, 16-byte
+ * aligned.  sufhip_beaver_matmul2_mfma_batched: the planes of D, E, A_p,
+ * B_p and C_p, out_p as in sufhip_beaver_matmul2_batched; M, K, N multiples
+ * of 32, K <= 4096 (exact int32 accumulation). */
+#define SUFHIP_KB_SPLIT_JOBS 8
+typedef struct sufhip_kb_split_job {
+  const uint64_t* src;
+  int8_t* planes;
+  int batches, rows, cols;
+  int k_is_col;
+} sufhip_kb_split_job;
+size_t sufhip_kb_planes_bytes(int batches, int rows, int cols);
+int sufhip_kb_split_batch(const sufhip_kb_split_job* jobs, int count, void* stream);
+int sufhip_beaver_matmul2_mfma_batched(const int8_t* d_Dp, const int8_t* d_Ep,
+                                       const int8_t* d_Ap0, const int8_t* d_Ap1,
+                                       const int8_t* d_Bp0, const int8_t* d_Bp1,
+                                       const uint64_t* d_C0, const uint64_t* d_C1, int batches,
+                                       int M, int K, int N, uint64_t* d_out0, uint64_t* d_out1,
+                                       void* stream);
+
 /* Share x public weight for both parties (nn::matmul_publicW_gpu,
  * src/nn/matmul_gpu.cu:388-720; CPU form src/nn/matmul_publicW.cpp:17-36):
  * Y_p = X_p * W mod 2^64, X_p [M x K] u64 shares, W [K x N] public int64, on

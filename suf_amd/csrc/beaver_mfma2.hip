@@ -1,0 +1,239 @@
+// Two-party batched Beaver matrix product over Z_2^64 on the int8 matrix
+// cores (gfx950 v_mfma_i32_32x32x32_i8), exact: the per-head QK^T and PV
+// products of attention_forward (src/nn/attention_block.cpp:1590-1850, the
+// BatchedMatmul2DTask form; element formula of launch_beaver_matmul2d_kernel,
+// cuda/cuda_primitives.cu:391-506).  For batch b and party p:
+//   out_p = C_p + D B_p + A_p E (+ D E for p = 0)   mod 2^64,
+// with the opens D [M x K], E [K x N] and the triple shares A_p, B_p, C_p.
+//
+// Every operand is in balanced base-256 digit planes (digit_planes.hpp), so
+// a product L R mod 2^64 is sum_{s<8} 256^s S_s, S_s = sum_{i+j=s} L_i R_j:
+// 36 int8 GEMMs per operand pair, 72 (party 1) or 108 (party 0) per k-step.
+// |S_s| <= 3 * 8 * K * 2^14 < 2^31 for K < 5461: int32 accumulation is exact.
+// The triple shares' planes are made once, with the triples (like public
+// weights, sufhip_public_w_prepare); the opens' planes per call, all opens of
+// one stage in one launch (sufhip_kb_split_batch).
+//
+// Kernel: a workgroup per (32 x 32 output tile, batch) of two waves per
+// k-slice, wave (slice, p) computing party p's tile over its k-steps; the
+// slices' tiles are added through LDS.  MFMA operand layout (checked on
+// the device for matmul_mfma.hip): lane l supplies row / column l % 32 at
+// k = 16 (l / 32) + byte; accumulator register r of lane l is row 8 (r / 4)
+// + 4 (l / 32) + r % 4, column l % 32.
+#include <hip/hip_runtime.h>
+
+#include "digit_planes.hpp"
+#include "suf_hip.h"
+#include "sufhip_internal.hpp"
+
+namespace sufhip {
+namespace {
+
+constexpr int kSplitJobs = SUFHIP_KB_SPLIT_JOBS;
+constexpr int kMaxBeaverK = 4096;
+
+struct SplitArgs {
+  const uint64_t* src[kSplitJobs];
+  int8_t* planes[kSplitJobs];
+  int batches[kSplitJobs], rows[kSplitJobs], cols[kSplitJobs], k_is_col[kSplitJobs];
+  size_t begin[kSplitJobs + 1];  // lanes (4 k each) of the jobs before
+  int count;
+};
+
+// One lane per 4 consecutive k of one plane row.  Row-side operands
+// (k_is_col: k runs along a source row) take 4 adjacent words; column-side
+// ones 4 words a source row apart, consecutive lanes reading consecutive
+// columns.
+__global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
+  const size_t total = a.begin[a.count];
+  for (size_t g = size_t(blockIdx.x) * 256 + threadIdx.x; g < total;
+       g += size_t(gridDim.x) * 256) {
+    int j = 0;
+    while (j + 1 < a.count && g >= a.begin[j + 1]) ++j;
+    const size_t q = g - a.begin[j];
+    const int rows = a.rows[j], cols = a.cols[j];
+    const bool kc = a.k_is_col[j] != 0;
+    const int K = kc ? cols : rows, R = kc ? rows : cols;
+    const size_t per_batch = size_t(R) * (K / 4);
+    const size_t b = q / per_batch, rem = q % per_batch;
+    int r, k;
+    if (kc) {
+      r = int(rem / (K / 4));
+      k = 4 * int(rem % (K / 4));
+    } else {
+      k = 4 * int(rem / R);
+      r = int(rem % R);
+    }
+    const uint64_t* src = a.src[j] + b * size_t(rows) * cols;
+    uint32_t pk[kDigitPlanes] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint64_t v = kc ? src[size_t(r) * cols + k + t] : src[size_t(k + t) * cols + r];
+      uint32_t d[kDigitPlanes];
+      digits8(v, d);
+#pragma unroll
+      for (int i = 0; i < kDigitPlanes; ++i) pk[i] |= d[i] << (8 * t);
+    }
+    const size_t plane = size_t(a.batches[j]) * R * K;
+    const size_t off = b * size_t(R) * K + kblock_off(size_t(r), k, size_t(R));
+#pragma unroll
+    for (int i = 0; i < kDigitPlanes; ++i)
+      *reinterpret_cast<uint32_t*>(a.planes[j] + i * plane + off) = pk[i];
+  }
+}
+
+struct Bm2Args {
+  const int8_t* D;     // LHS planes [8][b][K/32][M][32]
+  const int8_t* E;     // RHS planes [8][b][K/32][N][32]
+  const int8_t* A[2];  // LHS
+  const int8_t* B[2];  // RHS
+  const uint64_t* C[2];
+  uint64_t* out[2];
+  int batches, M, K, N;
+};
+
+// Waves per party: k-steps st, st + kKWaves, ... go to wave st % kKWaves, so
+// up to kKWaves steps' loads and MFMAs run at once; the partial tiles are
+// added through LDS.
+constexpr int kKWaves = 2;
+
+__global__ void __launch_bounds__(128 * kKWaves) beaver_mfma2_kernel(Bm2Args a) {
+  __shared__ uint64_t part[kKWaves - 1][2][16][64];
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int p = w & 1, kw = w >> 1, kws = blockDim.x / 128;
+  const int M = a.M, K = a.K, N = a.N;
+  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
+  const size_t b = blockIdx.z;
+  const size_t lplane = size_t(a.batches) * M * K, rplane = size_t(a.batches) * N * K;
+  const size_t lb = b * size_t(M) * K + size_t(m0 + (l & 31)) * 32 + 16 * (l >> 5);
+  const size_t rb = b * size_t(N) * K + size_t(n0 + (l & 31)) * 32 + 16 * (l >> 5);
+  const size_t lstep = size_t(M) * 32, rstep = size_t(N) * 32;
+  const int8_t* Ap = a.A[p];
+  const int8_t* Bp = a.B[p];
+  v16i acc[kDigitPlanes];
+#pragma unroll
+  for (int s = 0; s < kDigitPlanes; ++s)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[s][r] = 0;
+  const int steps = K / 32;
+  for (int st = kw; st < steps; st += kws) {
+    v4i d[kDigitPlanes], e[kDigitPlanes], x[kDigitPlanes], y[kDigitPlanes];
+#pragma unroll
+    for (int i = 0; i < kDigitPlanes; ++i) {
+      y[i] = load16(Bp + i * rplane + rb + st * rstep);
+      d[i] = load16(a.D + i * lplane + lb + st * lstep);
+      e[i] = load16(a.E + i * rplane + rb + st * rstep);
+      x[i] = load16(Ap + i * lplane + lb + st * lstep);
+    }
+#pragma unroll
+    for (int i = 0; i < kDigitPlanes; ++i)
+#pragma unroll
+      for (int j = 0; i + j < kDigitPlanes; ++j)
+        acc[i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(d[i], y[j], acc[i + j], 0, 0, 0);
+    if (p == 0) {
+#pragma unroll
+      for (int i = 0; i < kDigitPlanes; ++i)
+#pragma unroll
+        for (int j = 0; i + j < kDigitPlanes; ++j)
+          acc[i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(d[i], e[j], acc[i + j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kDigitPlanes; ++i)
+#pragma unroll
+      for (int j = 0; i + j < kDigitPlanes; ++j)
+        acc[i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x[i], e[j], acc[i + j], 0, 0, 0);
+  }
+  uint64_t v[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    v[r] = 0;
+#pragma unroll
+    for (int s = 0; s < kDigitPlanes; ++s) v[r] += uint64_t(int64_t(acc[s][r])) << (8 * s);
+  }
+  if (kw > 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[kw - 1][p][r][l] = v[r];
+  }
+  __syncthreads();
+  if (kw > 0) return;
+  for (int q = 1; q < kws; ++q) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] += part[q - 1][p][r][l];
+  }
+  const int col = n0 + (l & 31);
+  const size_t ob = b * size_t(M) * N;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    const size_t o = ob + size_t(row) * N + col;
+    a.out[p][o] = a.C[p][o] + v[r];
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+}  // namespace sufhip
+
+using namespace sufhip;
+
+extern "C" {
+
+size_t sufhip_kb_planes_bytes(int batches, int rows, int cols) {
+  if (batches < 1 || rows < 1 || cols < 1 || rows % 32 || cols % 32) return 0;
+  return size_t(kDigitPlanes) * size_t(batches) * size_t(rows) * size_t(cols);
+}
+
+int sufhip_kb_split_batch(const sufhip_kb_split_job* jobs, int count, void* stream) {
+  SUFHIP_REQUIRE(count >= 0 && count <= kSplitJobs && (count == 0 || jobs),
+                 "sufhip_kb_split_batch: 0..SUFHIP_KB_SPLIT_JOBS jobs");
+  SplitArgs a{};
+  a.begin[0] = 0;
+  for (int j = 0; j < count; ++j) {
+    const sufhip_kb_split_job& jb = jobs[j];
+    SUFHIP_REQUIRE(sufhip_kb_planes_bytes(jb.batches, jb.rows, jb.cols) != 0,
+                   "sufhip_kb_split_batch: batches >= 1, rows and cols multiples of 32");
+    SUFHIP_REQUIRE(jb.src && jb.planes && aligned16(jb.planes),
+                   "sufhip_kb_split_batch: null source or planes not 16-byte aligned");
+    a.src[j] = jb.src;
+    a.planes[j] = jb.planes;
+    a.batches[j] = jb.batches;
+    a.rows[j] = jb.rows;
+    a.cols[j] = jb.cols;
+    a.k_is_col[j] = jb.k_is_col ? 1 : 0;
+    a.begin[j + 1] = a.begin[j] + size_t(jb.batches) * jb.rows * jb.cols / 4;
+  }
+  a.count = count;
+  if (a.begin[count] == 0) return SUFHIP_OK;
+  size_t g = (a.begin[count] + 255) / 256;
+  if (g > 4096) g = 4096;
+  hipLaunchKernelGGL(kb_split_kernel, dim3(unsigned(g)), dim3(256), 0, as_stream(stream), a);
+  return check_launch("kb_split_kernel");
+}
+
+int sufhip_beaver_matmul2_mfma_batched(const int8_t* d_Dp, const int8_t* d_Ep,
+                                       const int8_t* d_Ap0, const int8_t* d_Ap1,
+                                       const int8_t* d_Bp0, const int8_t* d_Bp1,
+                                       const uint64_t* d_C0, const uint64_t* d_C1, int batches,
+                                       int M, int K, int N, uint64_t* d_out0, uint64_t* d_out1,
+                                       void* stream) {
+  SUFHIP_REQUIRE(batches >= 0 && batches <= 65535 && M % 32 == 0 && N % 32 == 0 &&
+                     K % 32 == 0 && M >= 0 && N >= 0 && K >= 0 && K <= kMaxBeaverK,
+                 "sufhip_beaver_matmul2_mfma_batched: M, K, N multiples of 32, K <= 4096");
+  if (batches == 0 || M == 0 || N == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(d_Dp && d_Ep && d_Ap0 && d_Ap1 && d_Bp0 && d_Bp1 && d_C0 && d_C1 && d_out0 &&
+                     d_out1,
+                 "sufhip_beaver_matmul2_mfma_batched: null pointer");
+  SUFHIP_REQUIRE(aligned16(d_Dp) && aligned16(d_Ep) && aligned16(d_Ap0) && aligned16(d_Ap1) &&
+                     aligned16(d_Bp0) && aligned16(d_Bp1),
+                 "sufhip_beaver_matmul2_mfma_batched: planes must be 16-byte aligned");
+  Bm2Args a{d_Dp, d_Ep, {d_Ap0, d_Ap1}, {d_Bp0, d_Bp1}, {d_C0, d_C1}, {d_out0, d_out1},
+            batches, M, K, N};
+  const int steps = K / 32;
+  const int kws = steps < 1 ? 1 : (steps < kKWaves ? steps : kKWaves);
+  const dim3 grid(N / 32, M / 32, batches);
+  hipLaunchKernelGGL(beaver_mfma2_kernel, grid, dim3(128 * kws), 0, as_stream(stream), a);
+  return check_launch("beaver_mfma2_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,47 @@
+// Balanced base-256 digit planes for the exact int8 matrix-core products
+// over Z_2^64 (matmul_public.hip, matmul_mfma.hip, beaver_mfma2.hip).
+//
+// v = sum_{i<8} d_i 256^i mod 2^64 with d_i in [-128, 127]: d_i is the low
+// byte as a signed value and v becomes (v - d_i) / 256.  A k-blocked plane
+// stores a [rows x K] operand as [K / 32][rows][32] int8, so the 32 rows x
+// 32 k of one MFMA step are a contiguous 1 KB block and one 16-byte load per
+// lane fetches its row's half of it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace sufhip {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kDigitPlanes = 8;
+
+// The eight digits of v, each as its byte (two's complement) in d[i].
+__device__ __forceinline__ void digits8(uint64_t v, uint32_t (&d)[kDigitPlanes]) {
+#pragma unroll
+  for (int i = 0; i < kDigitPlanes; ++i) {
+    const uint32_t b = uint32_t(v) & 0xffu;
+    d[i] = b;
+    v = (v >> 8) + (b >> 7);  // borrow when the digit is negative
+  }
+}
+
+// Byte offset of (row, k) in a k-blocked plane of `rows` rows.
+__device__ __forceinline__ size_t kblock_off(size_t row, int k, size_t rows) {
+  return (size_t(k >> 5) * rows + row) * 32 + size_t(k & 31);
+}
+
+__device__ __forceinline__ v4i load16(const int8_t* p) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  v4i r;
+  r.x = int(u.x);
+  r.y = int(u.y);
+  r.z = int(u.z);
+  r.w = int(u.w);
+  return r;
+}
+
+}  // namespace sufhip

@@ -27,27 +27,14 @@
 #include <hip/hip_runtime.h>
 
 #include "suf_hip.h"
+#include "digit_planes.hpp"
 #include "sufhip_internal.hpp"
 
 namespace sufhip {
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-
-constexpr int kPlanes = 8;
+constexpr int kPlanes = kDigitPlanes;
 constexpr int kMaxK = 8191;
-
-// Balanced digits of v, packed: byte i of lane word (i) -- returned as 8
-// signed bytes in d[0..7].
-__device__ __forceinline__ void digits(uint64_t v, uint32_t (&d)[kPlanes]) {
-#pragma unroll
-  for (int i = 0; i < kPlanes; ++i) {
-    const uint32_t b = uint32_t(v) & 0xffu;
-    d[i] = b;
-    v = (v >> 8) + (b >> 7);  // borrow when the digit is negative
-  }
-}
 
 // Pass 1: rows of [S0 | S1] (each rows x K, row-major) -> planes [8][rows][2K].
 // One lane per 4 consecutive k of one row.
@@ -64,7 +51,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       uint32_t d[kPlanes];
-      digits(src[t], d);
+      digits8(src[t], d);
 #pragma unroll
       for (int i = 0; i < kPlanes; ++i) pk[i] |= d[i] << (8 * t);
     }
@@ -108,7 +95,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int t = 0; t < 16; ++t) {
     uint32_t d[kPlanes];
-    digits(tile[16 * kg + t][cn], d);
+    digits8(tile[16 * kg + t][cn], d);
 #pragma unroll
     for (int i = 0; i < kPlanes; ++i) pk[i][t >> 2] |= d[i] << (8 * (t & 3));
   }
@@ -118,16 +105,6 @@ __global__ void __launch_bounds__(256)
   for (int i = 0; i < kPlanes; ++i)
     *reinterpret_cast<uint4*>(planes + i * plane + off) =
         make_uint4(pk[i][0], pk[i][1], pk[i][2], pk[i][3]);
-}
-
-__device__ __forceinline__ v4i load16(const int8_t* p) {
-  const uint4 u = *reinterpret_cast<const uint4*>(p);
-  v4i r;
-  r.x = int(u.x);
-  r.y = int(u.y);
-  r.z = int(u.z);
-  r.w = int(u.w);
-  return r;
 }
 
 // Pass 3: one wave per 32 x 32 output tile and k-slice.  grid = (N / 32,

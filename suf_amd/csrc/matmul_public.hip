@@ -28,29 +28,13 @@
 
 #include "suf_hip.h"
 #include "sufhip_internal.hpp"
+#include "digit_planes.hpp"
 #include "trunc_device.hpp"
 
 namespace sufhip {
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-
-constexpr int kPlanes = 8;
-
-__device__ __forceinline__ void digits8(uint64_t v, uint32_t (&d)[kPlanes]) {
-#pragma unroll
-  for (int i = 0; i < kPlanes; ++i) {
-    const uint32_t b = uint32_t(v) & 0xffu;
-    d[i] = b;
-    v = (v >> 8) + (b >> 7);  // borrow when the digit is negative
-  }
-}
-
-// Byte offset of (row, k) in a k-blocked plane of `rows` rows.
-__device__ __forceinline__ size_t kblock_off(size_t row, int k, size_t rows) {
-  return (size_t(k >> 5) * rows + row) * 32 + size_t(k & 31);
-}
+constexpr int kPlanes = kDigitPlanes;
 
 // X_0, X_1 [M][K] -> planes [8][K/32][2M][32]; one lane per 4 consecutive k
 // of a row.
@@ -98,16 +82,6 @@ __global__ void __launch_bounds__(256)
     const size_t off = kblock_off(size_t(n), k, size_t(N));
     for (int j = 0; j < J; ++j) *reinterpret_cast<uint32_t*>(planes + j * plane + off) = pk[j];
   }
-}
-
-__device__ __forceinline__ v4i load16(const int8_t* p) {
-  const uint4 u = *reinterpret_cast<const uint4*>(p);
-  v4i r;
-  r.x = int(u.x);
-  r.y = int(u.y);
-  r.z = int(u.z);
-  r.w = int(u.w);
-  return r;
 }
 
 struct PubArgs {

@@ -85,13 +85,34 @@ class PublicMatmulTrunc:
         return out
 
 
+def kb_planes(batches, rows, cols, device="cuda"):
+    """A buffer for one operand's digit planes (sufhip_kb_split_batch)."""
+    nb = native.load().sufhip_kb_planes_bytes(batches, rows, cols)
+    return torch.empty(max(2, (nb + 15) // 8), dtype=torch.int64, device=device)
+
+
+def kb_split(jobs):
+    """Digit planes of up to 8 operands in one launch: jobs of (src, planes,
+    batches, rows, cols, k_is_col)."""
+    arr = (native.KbSplitJob * len(jobs))()
+    for i, (src, planes, b, r, c, kc) in enumerate(jobs):
+        arr[i].src, arr[i].planes = ptr(src), ptr(planes)
+        arr[i].batches, arr[i].rows, arr[i].cols, arr[i].k_is_col = b, r, c, int(kc)
+    native.call("sufhip_kb_split_batch", arr, len(jobs), stream_ptr())
+
+
 class BatchedTriples:
     """Beaver matrix triples per batch: A [b][M x K], B [b][K x N] uniform,
-    C = A B mod 2^64; party 0 holds the drawn shares.  Also holds the
-    product's k-split workspace."""
+    C = A B mod 2^64; party 0 holds the drawn shares.  When M, K, N are
+    multiples of 32 the product runs on the matrix cores and the shares of A
+    and B are also kept as digit planes (made here, with the triples);
+    otherwise the VALU product's k-split workspace is kept."""
 
     def __init__(self, dealer, batches, M, K, N, device="cuda"):
-        wb = native.load().sufhip_beaver_matmul2_batched_work_bytes(batches, M, K, N)
+        self.shape = (batches, M, K, N)
+        self.mfma = M % 32 == 0 and K % 32 == 0 and N % 32 == 0 and K <= 4096
+        wb = 0 if self.mfma else \
+            native.load().sufhip_beaver_matmul2_batched_work_bytes(batches, M, K, N)
         self.work = torch.empty(max(2, (wb + 15) // 8), dtype=torch.int64, device=device)
         self.work_bytes = self.work.numel() * 8
         A = dealer.words(batches * M * K).reshape(batches, M, K)
@@ -104,9 +125,33 @@ class BatchedTriples:
         self.B = (dev(B0, device), dev(B - B0, device))
         self.C = (dev(C0, device), dev(C - C0, device))
         self.host = (A, B, C, A0, B0, C0)
+        if self.mfma:
+            self.Ap = tuple(kb_planes(batches, M, K, device) for _ in range(2))
+            self.Bp = tuple(kb_planes(batches, K, N, device) for _ in range(2))
+            self.Dp = kb_planes(batches, M, K, device)  # the opens' planes, per call
+            self.Ep = kb_planes(batches, K, N, device)
+            kb_split([(self.A[p], self.Ap[p], batches, M, K, 1) for p in (0, 1)] +
+                     [(self.B[p], self.Bp[p], batches, K, N, 0) for p in (0, 1)])
+
+    def split_jobs(self, D=None, E=None):
+        """kb_split jobs of the opens D [b][M x K] and / or E [b][K x N]."""
+        b, M, K, N = self.shape
+        return ([(D, self.Dp, b, M, K, 1)] if D is not None else []) + \
+            ([(E, self.Ep, b, K, N, 0)] if E is not None else [])
 
 
-def _beaver_batched(D, E, tri, batches, M, K, N, out):
+def _beaver_batched(D, E, tri, batches, M, K, N, out, split=True):
+    """out = the two-party batched Beaver product of the opens D, E with the
+    triples `tri`.  On the matrix cores the opens' planes are made here unless
+    split is False (the caller made them, batched with other opens)."""
+    if tri.mfma:
+        if split:
+            kb_split(tri.split_jobs(D, E))
+        native.call("sufhip_beaver_matmul2_mfma_batched", ptr(tri.Dp), ptr(tri.Ep),
+                    ptr(tri.Ap[0]), ptr(tri.Ap[1]), ptr(tri.Bp[0]), ptr(tri.Bp[1]),
+                    ptr(tri.C[0]), ptr(tri.C[1]), batches, M, K, N, ptr(out[0]), ptr(out[1]),
+                    stream_ptr())
+        return
     native.call("sufhip_beaver_matmul2_batched", ptr(D), ptr(E), ptr(tri.A[0]), ptr(tri.A[1]),
                 ptr(tri.B[0]), ptr(tri.B[1]), ptr(tri.C[0]), ptr(tri.C[1]), batches, M, K, N,
                 ptr(out[0]), ptr(out[1]), ptr(tri.work), tri.work_bytes, stream_ptr())
@@ -198,7 +243,12 @@ class AttentionCore:
             (operand(term(qkv, index=mp["gq"]), term(self.tri_qk.A, neg=True)), hsd, self.D, 0),
             (operand(term(qkv, index=mp["gk"]), term(self.tri_qk.B, neg=True)), hsd, self.E, 0),
             (operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True)), hsd, self.E2, 0)])
-        _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S)
+        if self.tri_qk.mfma and self.tri_pv.mfma:
+            # The three opens' digit planes in one launch.
+            kb_split(self.tri_qk.split_jobs(self.D, self.E) + self.tri_pv.split_jobs(E=self.E2))
+            _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S, split=False)
+        else:
+            _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S)
         prep[0].wait(prep[1])
         scaled = operand(term(self.S, index=mp["gs"], mul=self.inv_sqrt))
         if fused and self.softmax.fusable():
@@ -213,7 +263,11 @@ class AttentionCore:
             self.softmax.eval2(self.scores, self.prob, prep=prep, fused=False)
             lin2(operand(term(self.prob, index=mp["gp"]), term(self.tri_pv.A, neg=True)),
                  h * seq * seq, xhat=self.D2)
-        _beaver_batched(self.D2, self.E2, self.tri_pv, h, seq, seq, dh, self.Z)
+        if self.tri_qk.mfma and self.tri_pv.mfma:
+            kb_split(self.tri_pv.split_jobs(D=self.D2))
+            _beaver_batched(self.D2, self.E2, self.tri_pv, h, seq, seq, dh, self.Z, split=False)
+        else:
+            _beaver_batched(self.D2, self.E2, self.tri_pv, h, seq, seq, dh, self.Z)
         lin2(operand(term(self.Z, index=mp["gc"])), seq * d, into=(self.tr_c, out))
         return out
 

@@ -82,6 +82,11 @@ _SIGS = {
     "sufhip_beaver_matmul2_batched": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                               c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_sz,
                                               c_vp]),
+    "sufhip_kb_planes_bytes": (c_sz, [c_int, c_int, c_int]),
+    "sufhip_kb_split_batch": (c_int, [c_vp, c_int, c_vp]),
+    "sufhip_beaver_matmul2_mfma_batched": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                                   c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp,
+                                                   c_vp]),
     "sufhip_public_w_digits": (c_int, [c_vp, c_sz]),
     "sufhip_public_w_planes_bytes": (c_sz, [c_int, c_int, c_int]),
     "sufhip_public_w_prepare": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp]),
@@ -191,6 +196,12 @@ class Lin2Job(ctypes.Structure):
     """sufhip_lin2_job (include/suf_hip.h)."""
     _fields_ = [("x", Operand2), ("n", c_sz), ("out", c_vp * 2), ("xhat", c_vp),
                 ("mask", c_u64), ("trunc", c_vp)]
+
+
+class KbSplitJob(ctypes.Structure):
+    """sufhip_kb_split_job (include/suf_hip.h)."""
+    _fields_ = [("src", c_vp), ("planes", c_vp), ("batches", c_int), ("rows", c_int),
+                ("cols", c_int), ("k_is_col", c_int)]
 
 
 class Triple2(ctypes.Structure):

@@ -121,12 +121,18 @@ def test_lin2_batch_matches_single_launches():
         lin2_batch([(operand(bad), 1000, jobs[0][2], 0)])
 
 
-def test_beaver_matmul2_batched_vs_oracle():
-    b, M, K, N = 3, 32, 64, 48
+@pytest.mark.parametrize("b,M,K,N", [
+    (3, 32, 64, 48),     # VALU product (N not a multiple of 32)
+    (3, 32, 64, 64),     # matrix cores
+    (2, 64, 128, 32),    # matrix cores, PV-shaped
+    (12, 128, 64, 128),  # matrix cores, the GPT-2 QK^T shape
+])
+def test_beaver_matmul2_batched_vs_oracle(b, M, K, N):
     X = pfss.host_normal_fixed(81, 1.0, 0.0, F, b * M * K).reshape(b, M, K)
     Y = pfss.host_normal_fixed(82, 1.0, 0.0, F, b * K * N).reshape(b, K, N)
     say("beaver matmul2 batched b=%d %dx%dx%d" % (b, M, K, N))
     tri = layer.BatchedTriples(Dealer(5), b, M, K, N)
+    assert tri.mfma == (M % 32 == 0 and K % 32 == 0 and N % 32 == 0)
     A, B, C, A0, B0, C0 = tri.host
     A1, B1, C1 = A - A0, B - B0, C - C0
     x0 = pfss.host_mt19937_64(83, X.size).reshape(X.shape)
@@ -136,12 +142,34 @@ def test_beaver_matmul2_batched_vs_oracle():
     out = tuple(torch.empty(b * M * N, dtype=torch.int64, device="cuda") for _ in range(2))
     layer._beaver_batched(dev(D), dev(E), tri, b, M, K, N, out)
     g = [u64(out[0]).reshape(b, M, N), u64(out[1]).reshape(b, M, N)]
-    for i in range(b):
+    for i in sorted({0, b - 1}):
         for p, (Ap, Bp, Cp) in enumerate(((A0, B0, C0), (A1, B1, C1))):
             o = ol.beaver_matmul(p, D[i], E[i], Ap[i], Bp[i], Cp[i], 1, M, K, N)
             assert np.array_equal(g[p][i].ravel(), np.asarray(o).ravel())
     rec = (g[0] + g[1]).astype(np.uint64)
     assert np.array_equal(rec, np.matmul(X, Y))
+    if tri.mfma:  # the same shares from the VALU product
+        wb = native.load().sufhip_beaver_matmul2_batched_work_bytes(b, M, K, N)
+        work = torch.empty(max(2, (wb + 15) // 8), dtype=torch.int64, device="cuda")
+        ref = tuple(torch.empty(b * M * N, dtype=torch.int64, device="cuda") for _ in range(2))
+        Dd, Ed = dev(D), dev(E)
+        native.call("sufhip_beaver_matmul2_batched", Dd.data_ptr(), Ed.data_ptr(),
+                    tri.A[0].data_ptr(), tri.A[1].data_ptr(), tri.B[0].data_ptr(),
+                    tri.B[1].data_ptr(), tri.C[0].data_ptr(), tri.C[1].data_ptr(), b, M, K, N,
+                    ref[0].data_ptr(), ref[1].data_ptr(), work.data_ptr(), work.numel() * 8,
+                    torch.cuda.current_stream().cuda_stream)
+        for p in (0, 1):
+            assert np.array_equal(u64(ref[p]), u64(out[p]))
+
+
+def test_kb_split_rejects_bad_shapes():
+    src = dev(np.zeros(48 * 64, np.uint64))
+    planes = layer.kb_planes(1, 32, 64)
+    with pytest.raises(native.SufHipError):
+        layer.kb_split([(src, planes, 1, 48, 64, 1)])  # rows not a multiple of 32
+    with pytest.raises(native.SufHipError):
+        layer.kb_split([(src, planes, 1, 32, 64, 1)] * 9)  # more than 8 jobs
+    assert native.load().sufhip_kb_planes_bytes(1, 40, 64) == 0
 
 
 def _layer_case(seq, d, heads, ffn, seed):
