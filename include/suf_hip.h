@@ -398,6 +398,16 @@ int sufhip_interval_lut_eval2(const uint8_t* d_key0, const uint8_t* d_key1, size
  * a / b / c: the products' triple shares as terms (shift 0); trunc[k]: the
  * truncation gates in order (y ignored), trunc_mask[k] their masks;
  * frac_bits in [1, 13]; intervals <= 64. */
+/* Optional output of a producer as the left operand of a following
+ * public-weight product (sufhip_matmul_public2_planes): element i = m cols + k
+ * of party p goes to the balanced base-256 digit planes [8][cols/32][2 rows]
+ * [32] int8 (rows = n / cols; party 0's rows first), 16-byte aligned, cols
+ * and rows multiples of 32.  planes = NULL: none. */
+typedef struct sufhip_x_planes {
+  int8_t* planes;
+  int cols;
+} sufhip_x_planes;
+
 #define SUFHIP_CHAIN_CUBIC 0
 #define SUFHIP_CHAIN_RECIP 1
 #define SUFHIP_CHAIN_RSQRT 2
@@ -415,7 +425,8 @@ typedef struct sufhip_chain2_args {
   sufhip_term2 c[4];
   sufhip_trunc_epilogue trunc[4];
   uint64_t trunc_mask[4];
-  uint64_t* out[2];
+  uint64_t* out[2];        /* may be NULL when out_planes is given */
+  sufhip_x_planes out_planes;
 } sufhip_chain2_args;
 int sufhip_gate_chain2(const sufhip_chain2_args* args, void* stream);
 
@@ -459,7 +470,8 @@ typedef struct sufhip_layernorm2_args {
   sufhip_triple2 sq;
   sufhip_triple2 norm;
   sufhip_chain2_args rsqrt;
-  uint64_t* out[2];
+  uint64_t* out[2];        /* may be NULL when out_planes is given */
+  sufhip_x_planes out_planes;
 } sufhip_layernorm2_args;
 int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream);
 
@@ -720,6 +732,13 @@ size_t sufhip_public_w_planes_bytes(int K, int N, int digits);
 int sufhip_public_w_prepare(const int64_t* d_W, int K, int N, int digits, int8_t* d_planes,
                             void* stream);
 size_t sufhip_matmul_public2_work_bytes(int M, int K, int N);
+/* sufhip_matmul_public2 with X_0, X_1 already as the digit planes a
+ * producer wrote (sufhip_x_planes with cols = K, rows = M); same outputs and
+ * workspace. */
+int sufhip_matmul_public2_planes(const int8_t* d_Xp, int M, int K, int N, const int8_t* d_planes,
+                                 int digits, uint64_t* d_out0, uint64_t* d_out1, uint64_t* d_zhat,
+                                 uint64_t mask, const sufhip_trunc_epilogue* trunc, void* d_work,
+                                 size_t work_bytes, void* stream);
 int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int K, int N,
                           const int8_t* d_planes, int digits, uint64_t* d_out0, uint64_t* d_out1,
                           uint64_t* d_zhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,

@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include "chain_device.hpp"
+#include "digit_planes.hpp"
 #include "reduce_device.hpp"
 #include "relu_tree_device.hpp"
 
@@ -34,6 +35,7 @@ struct LnArgs {
   sufhip_triple2 sq, norm;
   ChainArgs rs;
   uint64_t* out[2];
+  sufhip_x_planes xp;
 };
 
 enum { kTrMean = 0, kTrVar0 = 1, kTrVar1 = 2, kTrNorm = 3 };
@@ -145,8 +147,14 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
         const uint64_t z0 = nc[k][0] + dd * nb0 + ee * na[k][0] + dd * ee;
         const uint64_t z1 = nc[k][1] + dd * nb1 + ee * na[k][1];
         const Two o = gate(kTrNorm, z0 + z1 + A.mask[kTrNorm]);
-        A.out[0][i] = o.v[0];
-        A.out[1][i] = o.v[1];
+        if (A.out[0]) {
+          A.out[0][i] = o.v[0];
+          A.out[1][i] = o.v[1];
+        }
+        if (A.xp.planes) {
+          put_x_digits(A.xp, size_t(A.rows), i, 0, o.v[0]);
+          put_x_digits(A.xp, size_t(A.rows), i, 1, o.v[1]);
+        }
       }
     }
     __syncthreads();  // bc is rewritten for the next row
@@ -389,8 +397,13 @@ int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
   SUFHIP_REQUIRE(g.rows >= 0 && g.cols >= 1 && g.cols <= kLnBlock * kLnMaxPer,
                  "sufhip_layernorm2: cols in [1, 2048]");
   if (g.rows == 0) return SUFHIP_OK;
-  SUFHIP_REQUIRE(g.x[0] && g.x[1] && g.out[0] && g.out[1],
+  SUFHIP_REQUIRE(g.x[0] && g.x[1] && (g.out[0] == nullptr) == (g.out[1] == nullptr) &&
+                     (g.out[0] || g.out_planes.planes),
                  "sufhip_layernorm2: null input or output");
+  SUFHIP_REQUIRE(x_planes_ok(g.out_planes, size_t(g.rows) * size_t(g.cols)) &&
+                     (!g.out_planes.planes || g.out_planes.cols == g.cols),
+                 "sufhip_layernorm2: out_planes needs cols == the row length, rows and cols "
+                 "multiples of 32, 16-byte alignment");
   SUFHIP_REQUIRE(triple_ok(g.sq) && triple_ok(g.norm), "sufhip_layernorm2: a triple is missing");
   SUFHIP_REQUIRE(g.rsqrt.kind == SUFHIP_CHAIN_RSQRT && g.rsqrt.n == size_t(g.rows),
                  "sufhip_layernorm2: the rsqrt chain must be RSQRT over rows elements");
@@ -416,6 +429,7 @@ int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
   A.mask[kTrNorm] = g.norm_mask;
   A.sq = g.sq;
   A.norm = g.norm;
+  A.xp = g.out_planes;
   A.out[0] = g.out[0];
   A.out[1] = g.out[1];
   int dev = 0, cus = 256;

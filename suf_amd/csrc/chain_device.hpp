@@ -23,6 +23,7 @@
 #include <string>
 
 #include "aes_lds.hpp"
+#include "digit_planes.hpp"
 #include "operand_device.hpp"
 #include "suf_hip.h"
 #include "sufhip_internal.hpp"
@@ -46,6 +47,7 @@ struct ChainArgs {
   uint64_t tmask[4];
   int tf[4];
   uint64_t* out[2];
+  sufhip_x_planes xp;
   size_t n;
 };
 
@@ -406,7 +408,10 @@ inline int make_chain_args(const sufhip_chain2_args& g, bool own_io, const char*
       (reinterpret_cast<uintptr_t>(g.lut[1]) & 7) != 0)
     return fail("LUT keys must be 8-byte aligned");
   if (own_io) {
-    if (!g.out[0] || !g.out[1]) return fail("null output");
+    if ((!g.out[0] || !g.out[1]) && !g.out_planes.planes) return fail("null output");
+    if ((g.out[0] == nullptr) != (g.out[1] == nullptr)) return fail("one output share missing");
+    if (!x_planes_ok(g.out_planes, g.n))
+      return fail("out_planes: cols and n / cols multiples of 32, 16-byte aligned");
     if (int rc = check_operand(g.x, g.n, what)) return rc;
   }
   ChainArgs A{};
@@ -419,6 +424,7 @@ inline int make_chain_args(const sufhip_chain2_args& g, bool own_io, const char*
   A.n = g.n;
   A.out[0] = g.out[0];
   A.out[1] = g.out[1];
+  A.xp = own_io ? g.out_planes : sufhip_x_planes{nullptr, 0};
   for (int k = 0; k < prods; ++k) {
     if (!g.a[k].p[0] || !g.b[k].p[0] || !g.c[k].p[0]) return fail("a product's triple is missing");
     if (int rc = check_term(g.a[k], g.n, false, what)) return rc;

@@ -34,8 +34,15 @@ __global__ void __launch_bounds__(kBlock) gate_chain_kernel(ChainArgs A) {
        i += size_t(gridDim.x) * kBlock) {
     const Two x{{operand_at(A.x, 0, i), operand_at(A.x, 1, i)}};
     const Two res = chain_eval<kKind, kCopies>(A, L, K, aes, i, x, chain_loader<kKind>{&A, i});
-    A.out[0][i] = res.v[0];
-    A.out[1][i] = res.v[1];
+    if (A.out[0]) {
+      A.out[0][i] = res.v[0];
+      A.out[1][i] = res.v[1];
+    }
+    if (A.xp.planes) {
+      const size_t rows = A.n / size_t(A.xp.cols);
+      put_x_digits(A.xp, rows, i, 0, res.v[0]);
+      put_x_digits(A.xp, rows, i, 1, res.v[1]);
+    }
   }
 }
 

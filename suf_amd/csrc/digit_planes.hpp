@@ -12,6 +12,8 @@
 
 #include <cstdint>
 
+#include "suf_hip.h"
+
 namespace sufhip {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -42,6 +44,29 @@ __device__ __forceinline__ v4i load16(const int8_t* p) {
   r.z = int(u.z);
   r.w = int(u.w);
   return r;
+}
+
+// Party p's element i of a producer's output into its sufhip_x_planes
+// (rows = the output's row count).
+__device__ __forceinline__ void put_x_digits(const sufhip_x_planes& xp, size_t rows, size_t i,
+                                             int p, uint64_t v) {
+  const size_t cols = size_t(xp.cols);
+  const size_t m = i / cols;
+  const int k = int(i - m * cols);
+  const size_t off = kblock_off(size_t(p) * rows + m, k, 2 * rows);
+  const size_t plane = 2 * rows * cols;
+  uint32_t d[kDigitPlanes];
+  digits8(v, d);
+#pragma unroll
+  for (int q = 0; q < kDigitPlanes; ++q) xp.planes[q * plane + off] = int8_t(d[q]);
+}
+
+// Host: checks an optional sufhip_x_planes for an output of n elements.
+inline bool x_planes_ok(const sufhip_x_planes& xp, size_t n) {
+  if (!xp.planes) return true;
+  if (xp.cols < 32 || xp.cols % 32 || n % size_t(xp.cols)) return false;
+  const size_t rows = n / size_t(xp.cols);
+  return rows % 32 == 0 && (reinterpret_cast<uintptr_t>(xp.planes) & 15) == 0;
 }
 
 }  // namespace sufhip

@@ -282,34 +282,26 @@ size_t sufhip_matmul_public2_work_bytes(int M, int K, int N) {
          (sl > 1 ? size_t(sl) * 2 * size_t(M) * size_t(N) * 8 : 0);
 }
 
-int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int K, int N,
-                          const int8_t* d_planes, int digits, uint64_t* d_out0, uint64_t* d_out1,
-                          uint64_t* d_zhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,
-                          void* d_work, size_t work_bytes, void* stream) {
-  SUFHIP_REQUIRE(shape_ok(M, K, N),
-                 "sufhip_matmul_public2: needs M, K, N multiples of 32 and K < 65536");
-  SUFHIP_REQUIRE(digits >= 1 && digits <= 4 && size_t(digits) * K < (size_t(1) << 17),
-                 "sufhip_matmul_public2: digits must be 1..4 with digits * K < 2^17");
-  SUFHIP_REQUIRE(d_X0 && d_X1 && d_planes && d_work, "sufhip_matmul_public2: null pointer");
-  SUFHIP_REQUIRE((d_out0 == nullptr) == (d_out1 == nullptr),
-                 "sufhip_matmul_public2: give both share outputs or neither");
-  SUFHIP_REQUIRE(d_out0 || d_zhat || trunc, "sufhip_matmul_public2: no output");
+}  // extern "C"
+
+namespace sufhip {
+namespace {
+
+// The product from X's planes Lp ([8][K/32][2M][32]); work holds the
+// k-slices' partial tiles after the X planes region.
+int launch_public2(const char* what, const int8_t* Lp, int M, int K, int N,
+                   const int8_t* d_planes, int digits, uint64_t* d_out0, uint64_t* d_out1,
+                   uint64_t* d_zhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,
+                   void* d_work, size_t work_bytes, hipStream_t s) {
   TruncEpi epi;
-  if (int rc = make_epi(trunc, size_t(M) * N, "sufhip_matmul_public2", &epi)) return rc;
-  SUFHIP_REQUIRE(work_bytes >= sufhip_matmul_public2_work_bytes(M, K, N),
-                 "sufhip_matmul_public2: workspace too small");
-  SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_work) & 15) == 0 &&
-                     (reinterpret_cast<uintptr_t>(d_planes) & 15) == 0,
-                 "sufhip_matmul_public2: workspace and planes must be 16-byte aligned");
-  hipStream_t s = as_stream(stream);
-  int8_t* Lp = static_cast<int8_t*>(d_work);
-  const size_t quads = size_t(2) * M * K / 4;
-  size_t g1 = (quads + 255) / 256;
-  if (g1 > 4096) g1 = 4096;
-  hipLaunchKernelGGL(split_x2_kernel, dim3(unsigned(g1)), dim3(256), 0, s, d_X0, d_X1, M, K, Lp);
-  if (int rc = check_launch("split_x2_kernel")) return rc;
+  if (int rc = make_epi(trunc, size_t(M) * N, what, &epi)) return rc;
+  if (work_bytes < sufhip_matmul_public2_work_bytes(M, K, N)) {
+    set_error(std::string(what) + ": workspace too small");
+    return SUFHIP_ERR_INVALID;
+  }
   const int sl = pub_slices(M, K, N);
-  uint64_t* part = reinterpret_cast<uint64_t*>(Lp + size_t(kPlanes) * 2 * M * K);
+  uint64_t* part =
+      reinterpret_cast<uint64_t*>(static_cast<int8_t*>(d_work) + size_t(kPlanes) * 2 * M * K);
   PubArgs a{Lp, d_planes, M, K, N, {d_out0, d_out1}, d_zhat, mask, part, epi};
   const dim3 grid(N / 32, M / 32, sl);
   switch (digits) {
@@ -326,6 +318,68 @@ int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int
   hipLaunchKernelGGL(public_reduce_kernel, dim3(unsigned(g)), dim3(256), 0, s, part, sl, mn,
                      d_out0, d_out1, d_zhat, mask, epi);
   return check_launch("public_reduce_kernel");
+}
+
+int check_public2(const char* what, int M, int K, int N, const int8_t* d_planes, int digits,
+                  uint64_t* d_out0, uint64_t* d_out1, uint64_t* d_zhat,
+                  const sufhip_trunc_epilogue* trunc, void* d_work) {
+  auto fail = [&](const char* msg) {
+    set_error(std::string(what) + ": " + msg);
+    return SUFHIP_ERR_INVALID;
+  };
+  if (!shape_ok(M, K, N)) return fail("needs M, K, N multiples of 32 and K < 65536");
+  if (digits < 1 || digits > 4 || size_t(digits) * K >= (size_t(1) << 17))
+    return fail("digits must be 1..4 with digits * K < 2^17");
+  if (!d_planes || !d_work) return fail("null pointer");
+  if ((d_out0 == nullptr) != (d_out1 == nullptr)) return fail("give both share outputs or neither");
+  if (!d_out0 && !d_zhat && !trunc) return fail("no output");
+  if ((reinterpret_cast<uintptr_t>(d_work) & 15) != 0 ||
+      (reinterpret_cast<uintptr_t>(d_planes) & 15) != 0)
+    return fail("workspace and planes must be 16-byte aligned");
+  return SUFHIP_OK;
+}
+
+}  // namespace
+}  // namespace sufhip
+
+extern "C" {
+
+int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int K, int N,
+                          const int8_t* d_planes, int digits, uint64_t* d_out0, uint64_t* d_out1,
+                          uint64_t* d_zhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,
+                          void* d_work, size_t work_bytes, void* stream) {
+  const char* what = "sufhip_matmul_public2";
+  if (int rc = check_public2(what, M, K, N, d_planes, digits, d_out0, d_out1, d_zhat, trunc,
+                             d_work))
+    return rc;
+  SUFHIP_REQUIRE(d_X0 && d_X1, "sufhip_matmul_public2: null pointer");
+  hipStream_t s = as_stream(stream);
+  int8_t* Lp = static_cast<int8_t*>(d_work);
+  const size_t quads = size_t(2) * M * K / 4;
+  size_t g1 = (quads + 255) / 256;
+  if (g1 > 4096) g1 = 4096;
+  if (work_bytes < sufhip_matmul_public2_work_bytes(M, K, N)) {
+    set_error("sufhip_matmul_public2: workspace too small");
+    return SUFHIP_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(split_x2_kernel, dim3(unsigned(g1)), dim3(256), 0, s, d_X0, d_X1, M, K, Lp);
+  if (int rc = check_launch("split_x2_kernel")) return rc;
+  return launch_public2(what, Lp, M, K, N, d_planes, digits, d_out0, d_out1, d_zhat, mask, trunc,
+                        d_work, work_bytes, s);
+}
+
+int sufhip_matmul_public2_planes(const int8_t* d_Xp, int M, int K, int N, const int8_t* d_planes,
+                                 int digits, uint64_t* d_out0, uint64_t* d_out1, uint64_t* d_zhat,
+                                 uint64_t mask, const sufhip_trunc_epilogue* trunc, void* d_work,
+                                 size_t work_bytes, void* stream) {
+  const char* what = "sufhip_matmul_public2_planes";
+  if (int rc = check_public2(what, M, K, N, d_planes, digits, d_out0, d_out1, d_zhat, trunc,
+                             d_work))
+    return rc;
+  SUFHIP_REQUIRE(d_Xp && (reinterpret_cast<uintptr_t>(d_Xp) & 15) == 0,
+                 "sufhip_matmul_public2_planes: X planes null or not 16-byte aligned");
+  return launch_public2(what, d_Xp, M, K, N, d_planes, digits, d_out0, d_out1, d_zhat, mask,
+                        trunc, d_work, work_bytes, as_stream(stream));
 }
 
 }  // extern "C"

@@ -65,16 +65,26 @@ class PublicMatmulTrunc:
         return [self.tr]
 
     def product2(self, X, out=None, zhat=None, mask=0, trunc=None):
-        native.call("sufhip_matmul_public2", ptr(X[0]), ptr(X[1]), self.M, self.K, self.N,
-                    ptr(self.planes), self.digits,
-                    ptr(out[0]) if out is not None else None,
-                    ptr(out[1]) if out is not None else None, ptr(zhat), mask & M64,
-                    native.ctypes.byref(trunc) if trunc is not None else None,
-                    ptr(self.work), self.work_bytes, stream_ptr())
+        tail = (ptr(self.planes), self.digits, ptr(out[0]) if out is not None else None,
+                ptr(out[1]) if out is not None else None, ptr(zhat), mask & M64,
+                native.ctypes.byref(trunc) if trunc is not None else None,
+                ptr(self.work), self.work_bytes, stream_ptr())
+        if X is None:
+            native.call("sufhip_matmul_public2_planes", ptr(self.work), self.M, self.K, self.N,
+                        *tail)
+        else:
+            native.call("sufhip_matmul_public2", ptr(X[0]), ptr(X[1]), self.M, self.K, self.N,
+                        *tail)
+
+    def x_planes(self):
+        """(buffer, cols) into which a producer writes X's digit planes for
+        eval2(None, ...): the first region of the workspace."""
+        return (self.work, self.K)
 
     def eval2(self, X, out, add=None):
-        """out = trunc_f(X W) (+ the pair `add`: a residual).  Its truncation
-        must have been prepared."""
+        """out = trunc_f(X W) (+ the pair `add`: a residual).  X = None: X's
+        digit planes were written to x_planes() by its producer.  The
+        truncation must have been prepared."""
         if self.tr.has_table():
             self.product2(X, mask=self.tr.mask, trunc=self.tr.epilogue(out, add))
         else:
@@ -288,8 +298,11 @@ class TransformerLayer:
     """One GPT-2-shaped layer over x [seq x d] Q(f) shares, both parties."""
 
     def __init__(self, prg_state, weights, seq=128, d=768, heads=12, ffn=3072, frac_bits=12,
-                 seed=13, device="cuda"):
+                 seed=13, device="cuda", keep_intermediates=False):
+        """keep_intermediates: also write h1, h2 and g as int64 shares (they
+        otherwise go only to the next product's digit planes)."""
         self.seq, self.d, self.heads, self.ffn, self.f = seq, d, heads, ffn, frac_bits
+        self.keep = keep_intermediates
         self.prg_state = bytes(prg_state)
         dealer = Dealer(seed)
         sub = lambda: dealer.word() >> 1  # noqa: E731
@@ -342,10 +355,19 @@ class TransformerLayer:
                 ev.record()
                 marks.append(ev)
 
+        # LayerNorm and GeLU outputs feed only the next public-weight product:
+        # they are written as its digit planes when the block runs fused.
+        fused_ln = self.ln1.fusable() and self.ln2.fusable()
         mark()
-        self.ln1.eval2(x, self.h1, prep=(prep, b(0)))
-        mark()
-        self.qkv.eval2(self.h1, self.qkvs)
+        if fused_ln:
+            self.ln1.eval2(x, self.h1, prep=(prep, b(0)), planes=self.qkv.x_planes(),
+                           write_out=self.keep)
+            mark()
+            self.qkv.eval2(None, self.qkvs)
+        else:
+            self.ln1.eval2(x, self.h1, prep=(prep, b(0)))
+            mark()
+            self.qkv.eval2(self.h1, self.qkvs)
         prep.release()  # the second half's gates, after the QKV product
         mark()
         self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)))
@@ -353,12 +375,19 @@ class TransformerLayer:
         prep.wait(b(2))
         self.proj.eval2(self.ctx, self.r1, add=x)  # r1 = trunc(ctx Wout) + x
         mark()
-        self.ln2.eval2(self.r1, self.h2, prep=(prep, b(2)))
+        if fused_ln:
+            self.ln2.eval2(self.r1, self.h2, prep=(prep, b(2)), planes=self.w1.x_planes(),
+                           write_out=self.keep)
+            mark()
+            self.w1.eval2(None, self.u)
+        else:
+            self.ln2.eval2(self.r1, self.h2, prep=(prep, b(2)))
+            mark()
+            self.w1.eval2(self.h2, self.u)
         mark()
-        self.w1.eval2(self.h2, self.u)
+        self.gelu.eval2(self.u, self.g, prep=(prep, b(2)), planes=self.w2.x_planes(),
+                        write_out=self.keep)
         mark()
-        self.gelu.eval2(self.u, self.g, prep=(prep, b(2)))
-        mark()
-        self.w2.eval2(self.g, out, add=self.r1)  # out = trunc(g W2) + r1
+        self.w2.eval2(None, out, add=self.r1)  # out = trunc(g W2) + r1
         mark()
         return out

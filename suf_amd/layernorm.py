@@ -25,7 +25,8 @@ import torch
 
 from . import native, tables
 from .tasks import (M64, CoeffLut, Dealer, Prepared, Triples, Trunc, chain2, chain2_args,
-                    dev_i32, lin2, mul2x, operand, pair, row_sum2, stream_ptr, term, triple2)
+                    dev_i32, lin2, mul2x, operand, pair, row_sum2, stream_ptr, term, triple2,
+                    x_planes)
 
 
 class Rsqrt:
@@ -107,8 +108,10 @@ class LayerNormBlock:
     def truncs(self):
         return [self.tr_mean] + self.tr_var + self.rsqrt.truncs() + [self.tr_norm]
 
-    def block_args(self, x, out):
-        """sufhip_layernorm2_args of the one-launch block over x into out."""
+    def block_args(self, x, out, planes=None, write_out=True):
+        """sufhip_layernorm2_args of the one-launch block over x into out
+        (planes = (buffer, cols): also as a public-weight product's digit
+        planes; write_out False: only those)."""
         a = native.LayerNorm2Args()
         a.x[0], a.x[1] = x[0].data_ptr(), x[1].data_ptr()
         a.rows, a.cols = self.rows, self.cols
@@ -125,26 +128,32 @@ class LayerNormBlock:
         a.rsqrt = chain2_args(native.CHAIN_RSQRT, self.f, None, self.rows, rs.lut.keys,
                               rs.lut.key_bytes, rs.lut.intervals, rs.lut.mask, rs.tri, rs.tr,
                               rs.y)
-        a.out[0], a.out[1] = out[0].data_ptr(), out[1].data_ptr()
+        if write_out:
+            a.out[0], a.out[1] = out[0].data_ptr(), out[1].data_ptr()
+        a.out_planes = x_planes(planes)
         return a
 
     def fusable(self):
         return (self.cols <= 2048 and self.rsqrt.iters == 1 and
                 all(t.has_table() for t in self.truncs()))
 
-    def eval2(self, x, out, prep=None, fused=True):
+    def eval2(self, x, out, prep=None, fused=True, planes=None, write_out=True):
         """x, out: pairs of int64 [rows * cols] device tensors.  prep:
         (tasks.Prepared, batch) holding this block's key-only halves, or None
         to issue them here on the block's side stream.  fused: the whole block
-        in one launch (sufhip_layernorm2); else launch by launch."""
+        in one launch (sufhip_layernorm2); else launch by launch.  planes =
+        (buffer, cols), fused only: the output also as a public-weight
+        product's digit planes (write_out False: only those)."""
         rows, cols, n = self.rows, self.cols, self.n
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
         prep[0].wait(prep[1])
         if fused and self.fusable():
-            a = self.block_args(x, out)
+            a = self.block_args(x, out, planes, write_out)
             native.call("sufhip_layernorm2", native.ctypes.byref(a), stream_ptr())
             return out
+        if planes is not None:
+            raise ValueError("LayerNormBlock.eval2: planes need the fused block")
         row_sum2(operand(term(x)), rows, cols, mul_const=self.inv_len,
                  into=(self.tr_mean, self.mu))
         diff = operand(term(x), term(self.mu, index=self.row_index, neg=True, length=rows))

@@ -91,6 +91,8 @@ _SIGS = {
     "sufhip_public_w_planes_bytes": (c_sz, [c_int, c_int, c_int]),
     "sufhip_public_w_prepare": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_vp]),
     "sufhip_matmul_public2_work_bytes": (c_sz, [c_int, c_int, c_int]),
+    "sufhip_matmul_public2_planes": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_vp,
+                                             c_vp, c_u64, c_vp, c_vp, c_sz, c_vp]),
     "sufhip_matmul_public2": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_vp,
                                       c_vp, c_u64, c_vp, c_vp, c_sz, c_vp]),
     "sufhip_trunc_finish2": (c_int, [c_int, c_int, c_vp, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp,
@@ -184,12 +186,18 @@ class TruncEpilogue(ctypes.Structure):
                 ("frac_bits", c_int), ("y", c_vp * 2), ("add", c_vp * 2)]
 
 
+class XPlanes(ctypes.Structure):
+    """sufhip_x_planes (include/suf_hip.h)."""
+    _fields_ = [("planes", c_vp), ("cols", c_int)]
+
+
 class Chain2Args(ctypes.Structure):
     """sufhip_chain2_args (include/suf_hip.h)."""
     _fields_ = [("kind", c_int), ("frac_bits", c_int), ("n", c_sz), ("x", Operand2),
                 ("lut", c_vp * 2), ("lut_key_bytes", c_sz), ("intervals", c_int),
                 ("lut_mask", c_u64), ("a", Term2 * 4), ("b", Term2 * 4), ("c", Term2 * 4),
-                ("trunc", TruncEpilogue * 4), ("trunc_mask", c_u64 * 4), ("out", c_vp * 2)]
+                ("trunc", TruncEpilogue * 4), ("trunc_mask", c_u64 * 4), ("out", c_vp * 2),
+                ("out_planes", XPlanes)]
 
 
 class Lin2Job(ctypes.Structure):
@@ -215,7 +223,7 @@ class LayerNorm2Args(ctypes.Structure):
                 ("eps", c_u64), ("tr_mean", TruncEpilogue), ("tr_var", TruncEpilogue * 2),
                 ("tr_norm", TruncEpilogue), ("mean_mask", c_u64), ("var_mask", c_u64 * 2),
                 ("norm_mask", c_u64), ("sq", Triple2), ("norm", Triple2), ("rsqrt", Chain2Args),
-                ("out", c_vp * 2)]
+                ("out", c_vp * 2), ("out_planes", XPlanes)]
 
 
 class ReluRoundKey(ctypes.Structure):

@@ -163,19 +163,24 @@ class SplineGate:
     def truncs(self):
         return list(self.trunc)
 
-    def eval2(self, x, out, prep=None, fused=True):
+    def eval2(self, x, out, prep=None, fused=True, planes=None, write_out=True):
         """x, out: pairs of int64[n] device tensors (party 0, party 1 shares).
         prep: (tasks.Prepared, batch) holding this gate's key-only halves, or
         None to issue them here on the gate's side stream.  fused: the whole
-        chain in one launch (sufhip_gate_chain2); else round by round."""
+        chain in one launch (sufhip_gate_chain2); else round by round.
+        planes = (buffer, cols), fused only: the output also as a public-weight
+        product's digit planes (write_out False: only those)."""
         n, f, s = self.n, self.f, torch.cuda.current_stream().cuda_stream
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
         if fused:
             prep[0].wait(prep[1])
             chain2(native.CHAIN_CUBIC, f, operand(term(x)), n, self.lut, self.lut_key_bytes,
-                   self.intervals, self.rin[0] + self.rin[1], self.tri, self.trunc, out)
+                   self.intervals, self.rin[0] + self.rin[1], self.tri, self.trunc, out,
+                   planes=planes, write_out=write_out)
             return out
+        if planes is not None:
+            raise ValueError("SplineGate.eval2: planes need the fused chain")
         xs = operand(term(x))
         # Both parties' coefficient rows at x^ = x + r_in, opened in the launch.
         native.call("sufhip_interval_lut_eval2", _p(self.lut[0]), _p(self.lut[1]),

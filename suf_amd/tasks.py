@@ -413,13 +413,26 @@ class AosTriples:
                 term(self.t, stride=3, off=2))
 
 
-def chain2(kind, f, x, n, lut_keys, lut_key_bytes, intervals, lut_mask, triples, truncs, out):
+def x_planes(planes=None):
+    """sufhip_x_planes from (buffer, cols), or none."""
+    xp = native.XPlanes()
+    if planes is not None:
+        xp.planes, xp.cols = ptr(planes[0]), planes[1]
+    return xp
+
+
+def chain2(kind, f, x, n, lut_keys, lut_key_bytes, intervals, lut_mask, triples, truncs, out,
+           planes=None, write_out=True):
     """A whole elementwise gate chain (sufhip_gate_chain2) for both parties:
     kind native.CHAIN_*, x the input operand, lut_keys both parties' LUT
     blobs, triples / truncs the chain's products and truncation gates in
-    order, out the output pair."""
+    order, out the output pair; planes = (buffer, cols): the output also as a
+    public-weight product's digit planes (write_out False: only those)."""
     a = chain2_args(kind, f, x, n, lut_keys, lut_key_bytes, intervals, lut_mask, triples, truncs,
                     out)
+    a.out_planes = x_planes(planes)
+    if not write_out:
+        a.out[0] = a.out[1] = None
     native.call("sufhip_gate_chain2", native.ctypes.byref(a), stream_ptr())
 
 

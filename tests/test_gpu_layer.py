@@ -95,6 +95,41 @@ def test_public_matmul_trunc_reconstructs():
         assert np.array_equal(u64(out2[p]), (u64(out[p]) + r[p]).astype(np.uint64))
 
 
+@pytest.mark.parametrize("producer", ["layernorm", "gelu"])
+def test_producer_planes_feed_public_matmul(producer):
+    """A LayerNorm block or GeLU chain writing its output as the next
+    product's digit planes (sufhip_x_planes) gives the same shares as the
+    product of its int64 output, and the same int64 output beside them."""
+    M, K, N = 64, 96, 64
+    x = pfss.host_normal_fixed(75, 1.0, 0.0, F, M * K)
+    x0, x1 = _pair(x, 76)
+    xin = (dev(x0), dev(x1))
+    W = pfss.host_normal_fixed(77, 0.05, 0.0, F, K * N).view(np.int64).reshape(K, N)
+    pm = layer.PublicMatmulTrunc(M, K, N, W, Dealer(8), STATE, F)
+    say("producer planes: %s %dx%d -> %d" % (producer, M, K, N))
+    if producer == "layernorm":
+        blk = layer.LayerNormBlock(M, K, STATE, F, seed=31)
+        assert blk.fusable()
+    else:
+        tab = tables.gelu_table(F)
+        blk = layer.spline.SplineGate(M * K, tab[0], tab[1], STATE, F, seed=32, nonce=5)
+    for t in blk.truncs():
+        t.prepare()
+    h = tuple(torch.empty(M * K, dtype=torch.int64, device="cuda") for _ in range(2))
+    h2 = tuple(torch.empty(M * K, dtype=torch.int64, device="cuda") for _ in range(2))
+    blk.eval2(xin, h)
+    blk.eval2(xin, h2, planes=pm.x_planes())  # int64 output and planes
+    for p in (0, 1):
+        assert np.array_equal(u64(h[p]), u64(h2[p]))
+    ref = tuple(torch.empty(M * N, dtype=torch.int64, device="cuda") for _ in range(2))
+    got = tuple(torch.empty(M * N, dtype=torch.int64, device="cuda") for _ in range(2))
+    pm.product2(h, out=ref)
+    blk.eval2(xin, h2, planes=pm.x_planes(), write_out=False)
+    pm.product2(None, out=got)
+    for p in (0, 1):
+        assert np.array_equal(u64(ref[p]), u64(got[p]))
+
+
 def test_lin2_batch_matches_single_launches():
     """Four opens of different sizes in one launch equal four sufhip_lin2
     calls; a batch with a bad operand is refused on the host."""
@@ -208,7 +243,7 @@ def test_layer_small_reconstructs():
     W, x = _layer_case(seq, d, heads, ffn, 21)
     x0, x1 = _pair(x, 22)
     say("transformer layer small seq=%d d=%d heads=%d ffn=%d" % (seq, d, heads, ffn))
-    ly = layer.TransformerLayer(STATE, W, seq, d, heads, ffn, F, seed=23)
+    ly = layer.TransformerLayer(STATE, W, seq, d, heads, ffn, F, seed=23, keep_intermediates=True)
     out = tuple(torch.empty(seq * d, dtype=torch.int64, device="cuda") for _ in range(2))
     ly.eval2((dev(x0), dev(x1)), out)
     want, st = fp.transformer_layer(x, W, seq, d, heads, ffn, F, _tabs(),
