@@ -704,6 +704,28 @@ typedef struct sufhip_kb_split_job {
   int batches, rows, cols;
   int k_is_col;
 } sufhip_kb_split_job;
+/* sufhip_beaver_matmul2_mfma_ex: the same product with options.  merge_heads:
+ * outputs at [m][b N + n] (heads side by side, as attention_forward merges
+ * the heads' context) instead of [b][m][n].  trunc (optional): the open
+ * out_0 + out_1 + mask feeds this prepared GapARS table gate (no addend),
+ * whose outputs trunc->y are written at the output positions instead of
+ * out (which may be NULL).  out_planes (optional, merge_heads only, cols =
+ * batches N): the (truncated) outputs also as the digit planes of a
+ * following public-weight product. */
+typedef struct sufhip_beaver_mfma2_args {
+  const int8_t* Dp;
+  const int8_t* Ep;
+  const int8_t* Ap[2];
+  const int8_t* Bp[2];
+  const uint64_t* C[2];
+  int batches, M, K, N;
+  uint64_t* out[2];
+  int merge_heads;
+  const sufhip_trunc_epilogue* trunc;
+  uint64_t mask;
+  sufhip_x_planes out_planes;
+} sufhip_beaver_mfma2_args;
+int sufhip_beaver_matmul2_mfma_ex(const sufhip_beaver_mfma2_args* args, void* stream);
 size_t sufhip_kb_planes_bytes(int batches, int rows, int cols);
 int sufhip_kb_split_batch(const sufhip_kb_split_job* jobs, int count, void* stream);
 int sufhip_beaver_matmul2_mfma_batched(const int8_t* d_Dp, const int8_t* d_Ep,

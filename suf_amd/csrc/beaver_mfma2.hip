@@ -25,6 +25,7 @@
 #include "digit_planes.hpp"
 #include "suf_hip.h"
 #include "sufhip_internal.hpp"
+#include "trunc_device.hpp"
 
 namespace sufhip {
 namespace {
@@ -90,6 +91,10 @@ struct Bm2Args {
   const uint64_t* C[2];
   uint64_t* out[2];
   int batches, M, K, N;
+  int merge;        // outputs at [m][b N + n] instead of [b][m][n]
+  TruncEpi epi;     // on: the open + mask feeds this gate, whose outputs are written
+  uint64_t mask;
+  sufhip_x_planes xp;  // optional digit planes of the (truncated) outputs, merged layout
 };
 
 // Waves per party: k-steps st, st + kKWaves, ... go to wave st % kKWaves, so
@@ -155,18 +160,56 @@ __global__ void __launch_bounds__(128 * kKWaves) beaver_mfma2_kernel(Bm2Args a) 
     for (int r = 0; r < 16; ++r) part[kw - 1][p][r][l] = v[r];
   }
   __syncthreads();
-  if (kw > 0) return;
-  for (int q = 1; q < kws; ++q) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] += part[q - 1][p][r][l];
-  }
   const int col = n0 + (l & 31);
   const size_t ob = b * size_t(M) * N;
+  const size_t ld = size_t(a.batches) * N;  // merged row length
+  if (kw == 0) {
+    for (int q = 1; q < kws; ++q) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
+      for (int r = 0; r < 16; ++r) v[r] += part[q - 1][p][r][l];
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+      v[r] += a.C[p][ob + size_t(row) * N + col];
+    }
+  }
+  if (!a.epi.on) {
+    if (kw > 0) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+      const size_t o = a.merge ? size_t(row) * ld + b * N + col : ob + size_t(row) * N + col;
+      a.out[p][o] = v[r];
+      if (a.xp.planes) put_x_digits(a.xp, size_t(M), o, p, v[r]);
+    }
+    return;
+  }
+  // The open out_0 + out_1 + mask through LDS (the slices' buffer is free
+  // again); wave p then finishes rows r in [8p, 8p + 8) for both parties.
+  __syncthreads();
+  uint64_t(*both)[16][64] = part[0];
+  static_assert(kKWaves >= 2, "the open reuses the slices' LDS");
+  if (kw == 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) both[p][r][l] = v[r];
+  }
+  __syncthreads();
+  if (kw > 0) return;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int r = 8 * p + q;
     const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-    const size_t o = ob + size_t(row) * N + col;
-    a.out[p][o] = a.C[p][o] + v[r];
+    const size_t o = a.merge ? size_t(row) * ld + b * N + col : ob + size_t(row) * N + col;
+    const uint64_t open = both[0][r][l] + both[1][r][l] + a.mask;
+    const uint64_t y0 = trunc_table_eval(a.epi.key[0], a.epi.table[0], a.epi.f, open);
+    const uint64_t y1 = trunc_table_eval(a.epi.key[1], a.epi.table[1], a.epi.f, open);
+    a.epi.y[0][o] = y0;
+    a.epi.y[1][o] = y1;
+    if (a.xp.planes) {
+      put_x_digits(a.xp, size_t(M), o, 0, y0);
+      put_x_digits(a.xp, size_t(M), o, 1, y1);
+    }
   }
 }
 
@@ -211,29 +254,62 @@ int sufhip_kb_split_batch(const sufhip_kb_split_job* jobs, int count, void* stre
   return check_launch("kb_split_kernel");
 }
 
+int sufhip_beaver_matmul2_mfma_ex(const sufhip_beaver_mfma2_args* args, void* stream) {
+  SUFHIP_REQUIRE(args != nullptr, "sufhip_beaver_matmul2_mfma_ex: null args");
+  const sufhip_beaver_mfma2_args& g = *args;
+  const char* what = "sufhip_beaver_matmul2_mfma_ex";
+  SUFHIP_REQUIRE(g.batches >= 0 && g.batches <= 65535 && g.M >= 0 && g.N >= 0 && g.K >= 0 &&
+                     g.M % 32 == 0 && g.N % 32 == 0 && g.K % 32 == 0 && g.K <= kMaxBeaverK,
+                 "sufhip_beaver_matmul2_mfma_ex: M, K, N multiples of 32, K <= 4096");
+  if (g.batches == 0 || g.M == 0 || g.N == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(g.Dp && g.Ep && g.Ap[0] && g.Ap[1] && g.Bp[0] && g.Bp[1] && g.C[0] && g.C[1],
+                 "sufhip_beaver_matmul2_mfma_ex: null operand");
+  SUFHIP_REQUIRE(aligned16(g.Dp) && aligned16(g.Ep) && aligned16(g.Ap[0]) &&
+                     aligned16(g.Ap[1]) && aligned16(g.Bp[0]) && aligned16(g.Bp[1]),
+                 "sufhip_beaver_matmul2_mfma_ex: planes must be 16-byte aligned");
+  const size_t n = size_t(g.batches) * g.M * g.N;
+  Bm2Args a{g.Dp, g.Ep, {g.Ap[0], g.Ap[1]}, {g.Bp[0], g.Bp[1]}, {g.C[0], g.C[1]},
+            {g.out[0], g.out[1]}, g.batches, g.M, g.K, g.N, g.merge_heads ? 1 : 0, TruncEpi{},
+            g.mask, g.out_planes};
+  if (int rc = make_epi(g.trunc, n, what, &a.epi)) return rc;
+  SUFHIP_REQUIRE(a.epi.on || (g.out[0] && g.out[1]),
+                 "sufhip_beaver_matmul2_mfma_ex: outputs (or a truncation) needed");
+  SUFHIP_REQUIRE(!a.epi.on || (a.epi.add[0] == nullptr),
+                 "sufhip_beaver_matmul2_mfma_ex: the truncation takes no addend");
+  SUFHIP_REQUIRE(!g.out_planes.planes ||
+                     (g.merge_heads && g.out_planes.cols == g.batches * g.N &&
+                      x_planes_ok(g.out_planes, n)),
+                 "sufhip_beaver_matmul2_mfma_ex: out_planes need merge_heads, cols = batches N");
+  const int steps = g.K / 32;
+  const int kws = steps < 2 ? 2 : (steps < kKWaves ? steps : kKWaves);
+  const dim3 grid(g.N / 32, g.M / 32, g.batches);
+  hipLaunchKernelGGL(beaver_mfma2_kernel, grid, dim3(128 * kws), 0, as_stream(stream), a);
+  return check_launch("beaver_mfma2_kernel");
+}
+
 int sufhip_beaver_matmul2_mfma_batched(const int8_t* d_Dp, const int8_t* d_Ep,
                                        const int8_t* d_Ap0, const int8_t* d_Ap1,
                                        const int8_t* d_Bp0, const int8_t* d_Bp1,
                                        const uint64_t* d_C0, const uint64_t* d_C1, int batches,
                                        int M, int K, int N, uint64_t* d_out0, uint64_t* d_out1,
                                        void* stream) {
-  SUFHIP_REQUIRE(batches >= 0 && batches <= 65535 && M % 32 == 0 && N % 32 == 0 &&
-                     K % 32 == 0 && M >= 0 && N >= 0 && K >= 0 && K <= kMaxBeaverK,
-                 "sufhip_beaver_matmul2_mfma_batched: M, K, N multiples of 32, K <= 4096");
-  if (batches == 0 || M == 0 || N == 0) return SUFHIP_OK;
-  SUFHIP_REQUIRE(d_Dp && d_Ep && d_Ap0 && d_Ap1 && d_Bp0 && d_Bp1 && d_C0 && d_C1 && d_out0 &&
-                     d_out1,
-                 "sufhip_beaver_matmul2_mfma_batched: null pointer");
-  SUFHIP_REQUIRE(aligned16(d_Dp) && aligned16(d_Ep) && aligned16(d_Ap0) && aligned16(d_Ap1) &&
-                     aligned16(d_Bp0) && aligned16(d_Bp1),
-                 "sufhip_beaver_matmul2_mfma_batched: planes must be 16-byte aligned");
-  Bm2Args a{d_Dp, d_Ep, {d_Ap0, d_Ap1}, {d_Bp0, d_Bp1}, {d_C0, d_C1}, {d_out0, d_out1},
-            batches, M, K, N};
-  const int steps = K / 32;
-  const int kws = steps < 1 ? 1 : (steps < kKWaves ? steps : kKWaves);
-  const dim3 grid(N / 32, M / 32, batches);
-  hipLaunchKernelGGL(beaver_mfma2_kernel, grid, dim3(128 * kws), 0, as_stream(stream), a);
-  return check_launch("beaver_mfma2_kernel");
+  SUFHIP_REQUIRE(d_out0 && d_out1, "sufhip_beaver_matmul2_mfma_batched: null pointer");
+  sufhip_beaver_mfma2_args g{};
+  g.Dp = d_Dp;
+  g.Ep = d_Ep;
+  g.Ap[0] = d_Ap0;
+  g.Ap[1] = d_Ap1;
+  g.Bp[0] = d_Bp0;
+  g.Bp[1] = d_Bp1;
+  g.C[0] = d_C0;
+  g.C[1] = d_C1;
+  g.batches = batches;
+  g.M = M;
+  g.K = K;
+  g.N = N;
+  g.out[0] = d_out0;
+  g.out[1] = d_out1;
+  return sufhip_beaver_matmul2_mfma_ex(&g, stream);
 }
 
 }  // extern "C"

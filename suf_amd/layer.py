@@ -33,7 +33,7 @@ from . import native, spline, tables
 from .layernorm import LayerNormBlock
 from .softmax import SoftmaxBlock, causal_offsets
 from .tasks import (Dealer, Prepared, Trunc, dev, dev_i32, lin2, lin2_batch, operand, pair, ptr,
-                    stream_ptr, term)
+                    stream_ptr, term, x_planes)
 
 M64 = (1 << 64) - 1
 
@@ -150,6 +150,24 @@ class BatchedTriples:
             ([(E, self.Ep, b, K, N, 0)] if E is not None else [])
 
 
+def _beaver_trunc_merged(tri, tr, out, planes=None):
+    """out = tr(the product of tri's opens' planes), heads merged side by side
+    ([m][b N + n]), in the product's launch; planes = (buffer, cols): also as
+    a following public-weight product's digit planes."""
+    b, M, K, N = tri.shape
+    a = native.BeaverMfma2Args()
+    a.Dp, a.Ep = ptr(tri.Dp), ptr(tri.Ep)
+    for p in (0, 1):
+        a.Ap[p], a.Bp[p], a.C[p] = ptr(tri.Ap[p]), ptr(tri.Bp[p]), ptr(tri.C[p])
+    a.batches, a.M, a.K, a.N = b, M, K, N
+    a.merge_heads = 1
+    epi = tr.epilogue(out)
+    a.trunc = native.ctypes.pointer(epi)
+    a.mask = tr.mask & M64
+    a.out_planes = x_planes(planes)
+    native.call("sufhip_beaver_matmul2_mfma_ex", native.ctypes.byref(a), stream_ptr())
+
+
 def _beaver_batched(D, E, tri, batches, M, K, N, out, split=True):
     """out = the two-party batched Beaver product of the opens D, E with the
     triples `tri`.  On the matrix cores the opens' planes are made here unless
@@ -239,10 +257,12 @@ class AttentionCore:
     def truncs(self):
         return self.tr_s + [self.tr_c] + self.softmax.truncs()
 
-    def eval2(self, qkv, out, prep=None, fused=True):
+    def eval2(self, qkv, out, prep=None, fused=True, planes=None):
         """prep: (tasks.Prepared, batch) holding the key-only halves of
         truncs(), or None to issue them here.  fused: scores, softmax and the
-        next open in one launch (sufhip_softmax2); else launch by launch."""
+        next open in one launch (sufhip_softmax2); else launch by launch.
+        planes = (buffer, cols): the context also as the output projection's
+        digit planes (matrix-core products only)."""
         seq, d, h, dh, mp = self.seq, self.d, self.heads, self.dh, self.maps
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
@@ -253,7 +273,7 @@ class AttentionCore:
             (operand(term(qkv, index=mp["gq"]), term(self.tri_qk.A, neg=True)), hsd, self.D, 0),
             (operand(term(qkv, index=mp["gk"]), term(self.tri_qk.B, neg=True)), hsd, self.E, 0),
             (operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True)), hsd, self.E2, 0)])
-        if self.tri_qk.mfma and self.tri_pv.mfma:
+        if self.mfma():
             # The three opens' digit planes in one launch.
             kb_split(self.tri_qk.split_jobs(self.D, self.E) + self.tri_pv.split_jobs(E=self.E2))
             _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S, split=False)
@@ -273,13 +293,21 @@ class AttentionCore:
             self.softmax.eval2(self.scores, self.prob, prep=prep, fused=False)
             lin2(operand(term(self.prob, index=mp["gp"]), term(self.tri_pv.A, neg=True)),
                  h * seq * seq, xhat=self.D2)
-        if self.tri_qk.mfma and self.tri_pv.mfma:
+        if self.mfma():
+            # PV, the context's truncation and the head merge in one launch.
             kb_split(self.tri_pv.split_jobs(D=self.D2))
-            _beaver_batched(self.D2, self.E2, self.tri_pv, h, seq, seq, dh, self.Z, split=False)
-        else:
-            _beaver_batched(self.D2, self.E2, self.tri_pv, h, seq, seq, dh, self.Z)
+            _beaver_trunc_merged(self.tri_pv, self.tr_c, out, planes)
+            return out
+        if planes is not None:
+            raise ValueError("AttentionCore.eval2: planes need the matrix-core products")
+        _beaver_batched(self.D2, self.E2, self.tri_pv, h, seq, seq, dh, self.Z)
         lin2(operand(term(self.Z, index=mp["gc"])), seq * d, into=(self.tr_c, out))
         return out
+
+    def mfma(self):
+        """The per-head products run on the matrix cores, and the context's
+        truncation is a table gate folded into the PV launch."""
+        return self.tri_qk.mfma and self.tri_pv.mfma and self.tr_c.has_table()
 
 
 def synthetic_weights(d=768, ffn=3072, frac_bits=12, seed=13):
@@ -370,10 +398,16 @@ class TransformerLayer:
             self.qkv.eval2(self.h1, self.qkvs)
         prep.release()  # the second half's gates, after the QKV product
         mark()
-        self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)))
-        mark()
-        prep.wait(b(2))
-        self.proj.eval2(self.ctx, self.r1, add=x)  # r1 = trunc(ctx Wout) + x
+        if self.attn.mfma():
+            self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)), planes=self.proj.x_planes())
+            mark()
+            prep.wait(b(2))
+            self.proj.eval2(None, self.r1, add=x)  # r1 = trunc(ctx Wout) + x
+        else:
+            self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)))
+            mark()
+            prep.wait(b(2))
+            self.proj.eval2(self.ctx, self.r1, add=x)
         mark()
         if fused_ln:
             self.ln2.eval2(self.r1, self.h2, prep=(prep, b(2)), planes=self.w1.x_planes(),

@@ -83,6 +83,7 @@ _SIGS = {
                                               c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_sz,
                                               c_vp]),
     "sufhip_kb_planes_bytes": (c_sz, [c_int, c_int, c_int]),
+    "sufhip_beaver_matmul2_mfma_ex": (c_int, [c_vp, c_vp]),
     "sufhip_kb_split_batch": (c_int, [c_vp, c_int, c_vp]),
     "sufhip_beaver_matmul2_mfma_batched": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                                    c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp,
@@ -204,6 +205,14 @@ class Lin2Job(ctypes.Structure):
     """sufhip_lin2_job (include/suf_hip.h)."""
     _fields_ = [("x", Operand2), ("n", c_sz), ("out", c_vp * 2), ("xhat", c_vp),
                 ("mask", c_u64), ("trunc", c_vp)]
+
+
+class BeaverMfma2Args(ctypes.Structure):
+    """sufhip_beaver_mfma2_args (include/suf_hip.h)."""
+    _fields_ = [("Dp", c_vp), ("Ep", c_vp), ("Ap", c_vp * 2), ("Bp", c_vp * 2), ("C", c_vp * 2),
+                ("batches", c_int), ("M", c_int), ("K", c_int), ("N", c_int), ("out", c_vp * 2),
+                ("merge_heads", c_int), ("trunc", ctypes.POINTER(TruncEpilogue)),
+                ("mask", c_u64), ("out_planes", XPlanes)]
 
 
 class KbSplitJob(ctypes.Structure):

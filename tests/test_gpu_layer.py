@@ -197,6 +197,43 @@ def test_beaver_matmul2_batched_vs_oracle(b, M, K, N):
             assert np.array_equal(u64(ref[p]), u64(out[p]))
 
 
+def test_beaver_trunc_merged_matches_separate_launches():
+    """PV with the context's truncation and head merge folded into the
+    product's launch (sufhip_beaver_matmul2_mfma_ex) gives the shares of the
+    product, a gather and a truncation launch; its digit-plane output feeds
+    the output projection like the merged shares do."""
+    h, seq, dh = 4, 64, 32
+    d = h * dh
+    say("beaver trunc merged h=%d seq=%d dh=%d" % (h, seq, dh))
+    tri = layer.BatchedTriples(Dealer(9), h, seq, seq, dh)
+    assert tri.mfma
+    tr = layer.Trunc(Dealer(10), F, seq * d, STATE)
+    tr.prepare()
+    P = pfss.host_normal_fixed(85, 0.3, 0.0, F, h * seq * seq).reshape(h, seq, seq)
+    V = pfss.host_normal_fixed(86, 1.0, 0.0, F, h * seq * dh).reshape(h, seq, dh)
+    A, B, C, A0, B0, C0 = tri.host
+    D = (P - A).astype(np.uint64)
+    E = (V - B).astype(np.uint64)
+    Z = tuple(torch.empty(h * seq * dh, dtype=torch.int64, device="cuda") for _ in range(2))
+    layer._beaver_batched(dev(D), dev(E), tri, h, seq, seq, dh, Z)
+    mp = layer.attention_maps(seq, d, h)
+    gc = layer.dev_i32(mp["gc"])
+    ref = tuple(torch.empty(seq * d, dtype=torch.int64, device="cuda") for _ in range(2))
+    layer.lin2(layer.operand(layer.term(Z, index=gc)), seq * d, into=(tr, ref))
+    W = pfss.host_normal_fixed(87, 0.05, 0.0, F, d * 64).view(np.int64).reshape(d, 64)
+    pm = layer.PublicMatmulTrunc(seq, d, 64, W, Dealer(11), STATE, F)
+    got = tuple(torch.empty(seq * d, dtype=torch.int64, device="cuda") for _ in range(2))
+    layer._beaver_trunc_merged(tri, tr, got, pm.x_planes())  # tri.Dp / Ep hold D, E
+    for p in (0, 1):
+        assert np.array_equal(u64(got[p]), u64(ref[p]))
+    y_ref = tuple(torch.empty(seq * 64, dtype=torch.int64, device="cuda") for _ in range(2))
+    y_got = tuple(torch.empty(seq * 64, dtype=torch.int64, device="cuda") for _ in range(2))
+    pm.product2(None, out=y_got)
+    pm.product2(ref, out=y_ref)
+    for p in (0, 1):
+        assert np.array_equal(u64(y_got[p]), u64(y_ref[p]))
+
+
 def test_kb_split_rejects_bad_shapes():
     src = dev(np.zeros(48 * 64, np.uint64))
     planes = layer.kb_planes(1, 32, 64)
