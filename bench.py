@@ -72,6 +72,35 @@ def calibrate_copy():
     print(json.dumps({"calibrate_copy_bytes": n, "launches": 5}), flush=True)
 
 
+def _graph_ms(run, steps, warmup):
+    """(ms per run() as one HIP graph replay, ms per eager run()): run()
+    issues the whole gate on torch's current stream."""
+    import torch
+
+    from suf_amd import tasks
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / steps
+    g = tasks.capture(run)
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, eager_ms
+
+
 def bench_spline(steps, warmup, n=1 << 20, frac_bits=12, cpu_seconds=0.0):
     """The spline gate (interval LUT + three Beaver products + GapARS by f and
     2f) for both parties on N = 2^20 inputs x = clip(3 N(0,1), +-8) in Q12
@@ -87,23 +116,22 @@ def bench_spline(steps, warmup, n=1 << 20, frac_bits=12, cpu_seconds=0.0):
     x = pfss.host_normal_fixed(5, 3.0, 8.0, frac_bits, n)
     x0 = pfss.host_mt19937_64(8, n)
     x1 = (x - x0).astype(np.uint64)
+    from suf_amd import tasks
+
     gate = spline.SplineGate(n, alpha, coeffs, state, frac_bits, seed=7)
     xd = [torch.from_numpy(v.view(np.int64).copy()).cuda() for v in (x0, x1)]
     out = [torch.empty(n, dtype=torch.int64, device="cuda") for _ in range(2)]
-    for _ in range(warmup):
-        gate.eval2(xd, out)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        gate.eval2(xd, out)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+
+    def run():
+        # The truncations' key-only halves first, on the same stream.
+        gate.eval2(xd, out, prep=(tasks.Prepared(None, [gate.truncs()]), 0))
+
+    ms, eager_ms = _graph_ms(run, steps, warmup)
     rec = (out[0].cpu().numpy().view(np.uint64) + out[1].cpu().numpy().view(np.uint64))
     ok = bool(np.array_equal(rec.astype(np.uint64),
                              spline.spline_eval_ref(alpha, coeffs, x, frac_bits)))
-    res = {"ms": ms, "n": n, "frac_bits": frac_bits, "intervals": int(gate.intervals),
+    res = {"ms": ms, "eager_ms": eager_ms, "n": n, "frac_bits": frac_bits,
+           "intervals": int(gate.intervals),
            "trunc": "GapARS f=%d (x3: the 2f truncation as two f truncations)" % frac_bits,
            "steps": steps, "check": "ok" if ok else "MISMATCH"}
     if cpu_seconds > 0:
@@ -193,22 +221,23 @@ def bench_matmul(steps, warmup, M=128, K=768, N=3072, frac_bits=12, cpu_seconds=
     for _ in range(warmup):
         g.eval2(Xd, Wd, out)
     torch.cuda.synchronize()
+    # The product's own time (eager, events around it), then the whole gate
+    # as one graph replay.
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
     for s in range(steps):
         g.eval2(Xd, Wd, out, events=ev[s])
-    e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
     mm_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    ms, eager_ms = _graph_ms(lambda: g.eval2(Xd, Wd, out), steps, warmup)
     prod = X.view(np.int64).reshape(M, K) @ W.view(np.int64).reshape(K, N)
     rec = (out[0].cpu().numpy().view(np.uint64) + out[1].cpu().numpy().view(np.uint64))
     ok = bool(np.array_equal(rec.astype(np.uint64), (prod >> frac_bits).view(np.uint64).ravel()))
     macs = 2 * 2 * M * K * N  # both parties, [D | A] x [B' ; E] is a 2K-deep product
-    res = {"ms": ms, "shape": [M, K, N], "matmul_ms": mm_ms, "u64_macs": macs,
+    res = {"ms": ms, "eager_ms": eager_ms, "shape": [M, K, N], "matmul_ms": mm_ms,
+           "u64_macs": macs,
            "u64_mac_per_s": macs / (mm_ms / 1e3), "trunc": "GapARS f=%d" % frac_bits,
-           "matmul_kernel": "int8-limb MFMA" if g.mm_work is not None else "u64 VALU",
+           "matmul_kernel": ("two-party int8-digit MFMA, truncation fused" if g.fused else
+                             "int8-limb MFMA" if g.mm_work is not None else "u64 VALU"),
            "steps": steps, "check": "ok" if ok else "MISMATCH"}
     if cpu_seconds > 0:
         res["cpu_baseline"] = cpu_matmul_baseline(g, state, Xd, Wd, out, cpu_seconds)
@@ -291,21 +320,30 @@ def bench_softmax_ln(steps, warmup, frac_bits=12, cpu=True):
     ln = layernorm.LayerNormBlock(rows, cols, state, frac_bits, seed=12)
     sout = tuple(torch.empty(n_sm, dtype=torch.int64, device="cuda") for _ in range(2))
     lout = tuple(torch.empty(rows * cols, dtype=torch.int64, device="cuda") for _ in range(2))
-    for _ in range(warmup):
-        sm.eval2(sin, sout)
-        ln.eval2(lin, lout)
-    torch.cuda.synchronize()
+    from suf_amd import tasks
+
+    def run(ev=None):
+        # Both blocks' truncation key-only halves in one batched walk first,
+        # on the same stream; then the two one-launch blocks.
+        prep = (tasks.Prepared(None, [sm.truncs() + ln.truncs()]), 0)
+        if ev:
+            ev[0].record()
+        sm.eval2(sin, sout, prep=prep)
+        if ev:
+            ev[1].record()
+        ln.eval2(lin, lout, prep=prep)
+        if ev:
+            ev[2].record()
+
+    ms, eager_ms = _graph_ms(run, steps, warmup)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     for s in range(steps):
-        ev[s][0].record()
-        sm.eval2(sin, sout)
-        ev[s][1].record()
-        ln.eval2(lin, lout)
-        ev[s][2].record()
+        run(ev[s])
     torch.cuda.synchronize()
     sm_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]))
     ln_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
-    res = {"ms": sm_ms + ln_ms, "softmax_ms": sm_ms, "layernorm_ms": ln_ms,
+    res = {"ms": ms, "eager_ms": eager_ms, "softmax_ms": sm_ms, "layernorm_ms": ln_ms,
+           "split": "softmax_ms / layernorm_ms: eager, without the shared prepare walk",
            "softmax_shape": "12 heads x 128 causal rows (%d scores)" % n_sm,
            "layernorm_shape": [rows, cols], "frac_bits": frac_bits, "steps": steps,
            "check": "not run (--no-cpu)"}

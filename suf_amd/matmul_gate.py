@@ -89,11 +89,25 @@ class BeaverMatmulTrunc:
         if use_mfma and mfma_ok(M, K, N):
             wb = lib.sufhip_beaver_matmul2d_mfma_work_bytes(M, K, N)
             self.mm_work = torch.empty((wb + 7) // 8, dtype=torch.int64, device="cuda")
+        # Two-party matrix-core form: both parties' products in one launch with
+        # the truncation folded in, the triple shares' digit planes made here.
+        self.fused = (use_mfma and M % 32 == 0 and K % 32 == 0 and N % 32 == 0 and K <= 4096 and
+                      frac_bits <= 13)
+        if self.fused:
+            from . import layer, tasks
+            self.tr = tasks.Trunc(None, frac_bits, M * N, self.prg_state, rnd=rnd)
+            self.Ap = tuple(layer.kb_planes(1, M, K) for _ in range(2))
+            self.Bp = tuple(layer.kb_planes(1, K, N) for _ in range(2))
+            self.Dp, self.Ep = layer.kb_planes(1, M, K), layer.kb_planes(1, K, N)
+            layer.kb_split([(self.A[p], self.Ap[p], 1, M, K, 1) for p in (0, 1)] +
+                           [(self.B[p], self.Bp[p], 1, K, N, 0) for p in (0, 1)])
 
     def eval2(self, X, W, out, events=None):
         """X, W, out: pairs of device int64 tensors (party shares).  events:
-        optional list of 2 torch events recorded around the two matmuls."""
+        optional list of 2 torch events recorded around the matmul."""
         M, K, N, s = self.M, self.K, self.N, _stream()
+        if self.fused:
+            return self._eval2_fused(X, W, out, events)
         # Key-only half of the truncation (both parties) on a side stream,
         # overlapped with the opens and the matmuls.
         start = torch.cuda.Event()
@@ -123,4 +137,31 @@ class BeaverMatmulTrunc:
             native.call("sufhip_trunc_finish", native.TRUNC_GAPARS, self.f,
                         pfss._state_buf(self.prg_state), _p(self.keys[p]), self.keys[p].numel(),
                         _p(self.zhat), M * N, _p(out[p]), _p(self.work[p]), self.work_bytes, s)
+        return out
+
+    def _eval2_fused(self, X, W, out, events=None):
+        """The truncation's key-only half, the opens D and E (one launch),
+        their digit planes (one launch), then both parties' products with the
+        truncation of their masked open in one launch; all on the current
+        stream."""
+        from . import layer, tasks
+        M, K, N = self.M, self.K, self.N
+        self.tr.prepare()
+        tasks.lin2_batch([
+            (tasks.operand(tasks.term(X), tasks.term(self.A, neg=True)), M * K, self.D, 0),
+            (tasks.operand(tasks.term(W), tasks.term(self.B, neg=True)), K * N, self.E, 0)])
+        if events:
+            events[0].record()
+        layer.kb_split([(self.D, self.Dp, 1, M, K, 1), (self.E, self.Ep, 1, K, N, 0)])
+        a = native.BeaverMfma2Args()
+        a.Dp, a.Ep = _p(self.Dp), _p(self.Ep)
+        for p in (0, 1):
+            a.Ap[p], a.Bp[p], a.C[p] = _p(self.Ap[p]), _p(self.Bp[p]), _p(self.C[p])
+        a.batches, a.M, a.K, a.N = 1, M, K, N
+        epi = self.tr.epilogue(out)
+        a.trunc = native.ctypes.pointer(epi)
+        a.mask = self.tr.mask & M64
+        native.call("sufhip_beaver_matmul2_mfma_ex", native.ctypes.byref(a), _stream())
+        if events:
+            events[1].record()
         return out
