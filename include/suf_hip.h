@@ -323,6 +323,16 @@ int sufhip_lin2(const sufhip_operand2* x, size_t n, uint64_t* d_out0, uint64_t* 
 /* Up to 4 independent sufhip_lin2 evaluations (each with the meaning of
  * sufhip_lin2's arguments) in one launch: opens of one protocol round that
  * do not depend on each other. */
+/* Optional output of an open as the digit planes of a two-party Beaver
+ * product's operand (sufhip_kb_split_batch's layout): element i of the
+ * [batches][rows x cols] open goes to planes [8][batches][K/32][R][32] with
+ * (K, R) = (cols, rows) for k_is_col = 1 and (rows, cols) otherwise; rows and
+ * cols multiples of 32, 16-byte aligned.  planes = NULL: none. */
+typedef struct sufhip_kb_planes {
+  int8_t* planes;
+  int batches, rows, cols;
+  int k_is_col;
+} sufhip_kb_planes;
 typedef struct sufhip_lin2_job {
   sufhip_operand2 x;
   size_t n;
@@ -330,6 +340,7 @@ typedef struct sufhip_lin2_job {
   uint64_t* xhat;
   uint64_t mask;
   const sufhip_trunc_epilogue* trunc;
+  sufhip_kb_planes xhat_planes; /* the open also as digit planes (n = batches rows cols) */
 } sufhip_lin2_job;
 int sufhip_lin2_batch(const sufhip_lin2_job* jobs, int count, void* stream);
 
@@ -534,6 +545,7 @@ typedef struct sufhip_softmax2_args {
   uint64_t* d_dense;
   const uint64_t* dense_a[2];
   int dense_cols;
+  sufhip_kb_planes dense_planes; /* the dense open also as digit planes, rows x dense_cols */
 } sufhip_softmax2_args;
 int sufhip_softmax2(const sufhip_softmax2_args* args, void* stream);
 

@@ -189,6 +189,7 @@ struct SmArgs {
   uint64_t* dense;
   const uint64_t* dense_a[2];
   int dense_cols;
+  sufhip_kb_planes dkb;  // the dense open also as digit planes
 };
 
 struct SmStatic {
@@ -355,14 +356,18 @@ __global__ void __launch_bounds__(64 * kSmWaves) softmax2_kernel(SmArgs a) {
           }
           if (a.dense) {
             const size_t di = drow + size_t(j);
-            a.dense[di] = (p0 - a.dense_a[0][di]) + (p1 - a.dense_a[1][di]);
+            const uint64_t dv = (p0 - a.dense_a[0][di]) + (p1 - a.dense_a[1][di]);
+            a.dense[di] = dv;
+            if (a.dkb.planes) put_kb_digits(a.dkb, di, dv);
           }
         }
       }
       if (a.dense)
         for (int j = len + lane; j < a.dense_cols; j += 64) {
           const size_t di = drow + size_t(j);
-          a.dense[di] = (uint64_t(0) - a.dense_a[0][di]) + (uint64_t(0) - a.dense_a[1][di]);
+          const uint64_t dv = (uint64_t(0) - a.dense_a[0][di]) + (uint64_t(0) - a.dense_a[1][di]);
+          a.dense[di] = dv;
+          if (a.dkb.planes) put_kb_digits(a.dkb, di, dv);
         }
     }
     __syncthreads();  // the row buffers are rewritten by the next group
@@ -496,6 +501,10 @@ int sufhip_softmax2(const sufhip_softmax2_args* args, void* stream) {
   A.dense_a[0] = g.dense_a[0];
   A.dense_a[1] = g.dense_a[1];
   A.dense_cols = g.d_dense ? g.dense_cols : 0;
+  SUFHIP_REQUIRE(!g.dense_planes.planes ||
+                     (g.d_dense && kb_planes_ok(g.dense_planes, size_t(g.rows) * g.dense_cols)),
+                 "sufhip_softmax2: dense_planes need d_dense and cover rows x dense_cols");
+  A.dkb = g.d_dense ? g.dense_planes : sufhip_kb_planes{nullptr, 0, 0, 0, 0};
   const size_t row_bytes = tree_row_words(g.max_row) * sizeof(uint64_t);
   int waves = kSmWaves;
   while (waves > 1 && sizeof(SmStatic) + size_t(waves) * row_bytes > kSmLdsCap) waves /= 2;

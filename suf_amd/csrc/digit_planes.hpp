@@ -61,6 +61,29 @@ __device__ __forceinline__ void put_x_digits(const sufhip_x_planes& xp, size_t r
   for (int q = 0; q < kDigitPlanes; ++q) xp.planes[q * plane + off] = int8_t(d[q]);
 }
 
+// Element i of a [batches][rows x cols] open into its sufhip_kb_planes.
+__device__ __forceinline__ void put_kb_digits(const sufhip_kb_planes& o, size_t i, uint64_t v) {
+  const size_t rc = size_t(o.rows) * size_t(o.cols);
+  const size_t b = i / rc, rem = i - b * rc;
+  const int r = int(rem / size_t(o.cols)), c = int(rem - size_t(r) * size_t(o.cols));
+  const bool kc = o.k_is_col != 0;
+  const size_t R = size_t(kc ? o.rows : o.cols);
+  const size_t off = b * rc + kblock_off(size_t(kc ? r : c), kc ? c : r, R);
+  const size_t plane = size_t(o.batches) * rc;
+  uint32_t d[kDigitPlanes];
+  digits8(v, d);
+#pragma unroll
+  for (int q = 0; q < kDigitPlanes; ++q) o.planes[q * plane + off] = int8_t(d[q]);
+}
+
+// Host: checks an optional sufhip_kb_planes for an open of n elements.
+inline bool kb_planes_ok(const sufhip_kb_planes& o, size_t n) {
+  if (!o.planes) return true;
+  return o.batches >= 1 && o.rows >= 32 && o.cols >= 32 && o.rows % 32 == 0 &&
+         o.cols % 32 == 0 && size_t(o.batches) * size_t(o.rows) * size_t(o.cols) == n &&
+         (reinterpret_cast<uintptr_t>(o.planes) & 15) == 0;
+}
+
 // Host: checks an optional sufhip_x_planes for an output of n elements.
 inline bool x_planes_ok(const sufhip_x_planes& xp, size_t n) {
   if (!xp.planes) return true;

@@ -32,6 +32,7 @@
 #include "suf_hip.h"
 #include "sufhip_internal.hpp"
 #include "operand_device.hpp"
+#include "digit_planes.hpp"
 #include "reduce_device.hpp"
 #include "trunc_device.hpp"
 
@@ -127,6 +128,7 @@ struct Lin2Batch {
   uint64_t* xhat[kLin2Jobs];
   uint64_t mask[kLin2Jobs];
   TruncEpi epi[kLin2Jobs];
+  sufhip_kb_planes kb[kLin2Jobs];
   unsigned begin[kLin2Jobs + 1];  // each job's first workgroup
   int count;
 };
@@ -143,6 +145,7 @@ __global__ void __launch_bounds__(kBlock) lin2_batch_kernel(Lin2Batch b) {
     if (b.out[j][0]) b.out[j][0][i] = x0;
     if (b.out[j][1]) b.out[j][1][i] = x1;
     put_open(b.epi[j], b.xhat[j], i, x0 + x1 + b.mask[j]);
+    if (b.kb[j].planes) put_kb_digits(b.kb[j], i, x0 + x1 + b.mask[j]);
   }
 }
 
@@ -283,7 +286,11 @@ int sufhip_lin2_batch(const sufhip_lin2_job* jobs, int count, void* stream) {
     const sufhip_lin2_job& jb = jobs[k];
     if (jb.n == 0) continue;
     SUFHIP_REQUIRE(jb.n < kMaxElems, "sufhip_lin2_batch: n too large");
-    SUFHIP_REQUIRE(jb.out[0] || jb.out[1] || jb.xhat || jb.trunc, "sufhip_lin2_batch: no output");
+    SUFHIP_REQUIRE(jb.out[0] || jb.out[1] || jb.xhat || jb.trunc || jb.xhat_planes.planes,
+                   "sufhip_lin2_batch: no output");
+    SUFHIP_REQUIRE(kb_planes_ok(jb.xhat_planes, jb.n),
+                   "sufhip_lin2_batch: xhat_planes must cover n = batches rows cols, rows and "
+                   "cols multiples of 32, 16-byte aligned");
     if (int rc = check_operand(jb.x, jb.n, "sufhip_lin2_batch")) return rc;
     const int c = b.count;
     if (int rc = make_epi(jb.trunc, jb.n, "sufhip_lin2_batch", &b.epi[c])) return rc;
@@ -293,6 +300,7 @@ int sufhip_lin2_batch(const sufhip_lin2_job* jobs, int count, void* stream) {
     b.out[c][1] = jb.out[1];
     b.xhat[c] = jb.xhat;
     b.mask[c] = jb.mask;
+    b.kb[c] = jb.xhat_planes;
     b.begin[c + 1] = b.begin[c] + ew_grid(jb.n);
     ++b.count;
   }

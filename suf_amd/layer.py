@@ -269,24 +269,28 @@ class AttentionCore:
         # D = open(Q_h - A), E = open(K_h^T - B), and already the second
         # product's E2 = open(V_h - B2), in one launch; then the per-head products.
         hsd = h * seq * dh
-        lin2_batch([
-            (operand(term(qkv, index=mp["gq"]), term(self.tri_qk.A, neg=True)), hsd, self.D, 0),
-            (operand(term(qkv, index=mp["gk"]), term(self.tri_qk.B, neg=True)), hsd, self.E, 0),
-            (operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True)), hsd, self.E2, 0)])
+        gq = operand(term(qkv, index=mp["gq"]), term(self.tri_qk.A, neg=True))
+        gk = operand(term(qkv, index=mp["gk"]), term(self.tri_qk.B, neg=True))
+        gv = operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True))
         if self.mfma():
-            # The three opens' digit planes in one launch.
-            kb_split(self.tri_qk.split_jobs(self.D, self.E) + self.tri_pv.split_jobs(E=self.E2))
+            # The three opens go straight to the products' digit planes.
+            lin2_batch([(gq, hsd, None, 0, (self.tri_qk.Dp, h, seq, dh, 1)),
+                        (gk, hsd, None, 0, (self.tri_qk.Ep, h, dh, seq, 0)),
+                        (gv, hsd, None, 0, (self.tri_pv.Ep, h, seq, dh, 0))])
             _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S, split=False)
         else:
+            lin2_batch([(gq, hsd, self.D, 0), (gk, hsd, self.E, 0), (gv, hsd, self.E2, 0)])
             _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S)
         prep[0].wait(prep[1])
         scaled = operand(term(self.S, index=mp["gs"], mul=self.inv_sqrt))
         if fused and self.softmax.fusable():
             # One launch: the masked open of inv_sqrt * S at the packed causal
             # positions truncated by 2f, the softmax block, and the open of
-            # P - A over the dense [heads][seq][seq] layout.
+            # P - A over the dense [heads][seq][seq] layout (also as PV's
+            # digit planes on the matrix cores).
+            dp = (self.tri_pv.Dp, h, seq, seq, 1) if self.mfma() else None
             self.softmax.eval_block(scaled, pre=self.tr_s,
-                                    dense=(self.D2, self.tri_pv.A, seq))
+                                    dense=(self.D2, self.tri_pv.A, seq, dp))
         else:
             lin2(scaled, self.n, into=(self.tr_s[0], self.sa))
             lin2(operand(term(self.sa)), self.n, into=(self.tr_s[1], self.scores))
@@ -295,7 +299,8 @@ class AttentionCore:
                  h * seq * seq, xhat=self.D2)
         if self.mfma():
             # PV, the context's truncation and the head merge in one launch.
-            kb_split(self.tri_pv.split_jobs(D=self.D2))
+            if not (fused and self.softmax.fusable()):
+                kb_split(self.tri_pv.split_jobs(D=self.D2))
             _beaver_trunc_merged(self.tri_pv, self.tr_c, out, planes)
             return out
         if planes is not None:

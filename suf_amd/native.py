@@ -201,10 +201,16 @@ class Chain2Args(ctypes.Structure):
                 ("out_planes", XPlanes)]
 
 
+class KbPlanes(ctypes.Structure):
+    """sufhip_kb_planes (include/suf_hip.h)."""
+    _fields_ = [("planes", c_vp), ("batches", c_int), ("rows", c_int), ("cols", c_int),
+                ("k_is_col", c_int)]
+
+
 class Lin2Job(ctypes.Structure):
     """sufhip_lin2_job (include/suf_hip.h)."""
     _fields_ = [("x", Operand2), ("n", c_sz), ("out", c_vp * 2), ("xhat", c_vp),
-                ("mask", c_u64), ("trunc", c_vp)]
+                ("mask", c_u64), ("trunc", c_vp), ("xhat_planes", KbPlanes)]
 
 
 class BeaverMfma2Args(ctypes.Structure):
@@ -248,7 +254,7 @@ class Softmax2Args(ctypes.Structure):
                 ("keys", ReluRoundKey * 10), ("nexp", Chain2Args), ("recip", Chain2Args),
                 ("norm", Triple2), ("tr_norm", TruncEpilogue), ("norm_mask", c_u64),
                 ("out", c_vp * 2), ("d_dense", c_vp), ("dense_a", c_vp * 2),
-                ("dense_cols", c_int)]
+                ("dense_cols", c_int), ("dense_planes", KbPlanes)]
 
 
 class TruncJob(ctypes.Structure):

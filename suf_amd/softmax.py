@@ -26,9 +26,9 @@ import numpy as np
 import torch
 
 from . import native, spline, tables
-from .tasks import (M64, RELU_ALPHA, CoeffLut, Dealer, Prepared, Triples, Trunc, chain2,
-                    chain2_args, dev_i32, lin2, mul2x, operand, pair, relu_coeffs_for, row_sum2,
-                    stream_ptr, term, triple2)
+from .tasks import (M64, RELU_ALPHA, chain2, chain2_args, CoeffLut, Dealer, dev_i32, kb_planes_out,
+                    lin2, mul2x, operand, pair, Prepared, relu_coeffs_for, row_sum2, stream_ptr,
+                    term, triple2, Triples, Trunc)
 
 
 def causal_offsets(heads, seq):
@@ -252,6 +252,8 @@ class SoftmaxBlock:
             a.d_dense = dense[0].data_ptr()
             a.dense_a[0], a.dense_a[1] = dense[1][0].data_ptr(), dense[1][1].data_ptr()
             a.dense_cols = dense[2]
+            if len(dense) > 3 and dense[3] is not None:
+                a.dense_planes = kb_planes_out(dense[3])
         return a
 
     def eval_block(self, x, out=None, pre=(), dense=None):

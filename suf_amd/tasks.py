@@ -116,12 +116,25 @@ def lin2(x, n, out=None, xhat=None, mask=0, into=None):
     _after(fin)
 
 
+def kb_planes_out(spec):
+    """sufhip_kb_planes from (planes, batches, rows, cols, k_is_col), or none."""
+    o = native.KbPlanes()
+    if spec is not None:
+        o.planes = ptr(spec[0])
+        o.batches, o.rows, o.cols, o.k_is_col = spec[1], spec[2], spec[3], int(spec[4])
+    return o
+
+
 def lin2_batch(jobs):
     """Up to four independent lin2 opens in one launch: jobs of (operand, n,
-    xhat, mask)."""
+    xhat, mask) or (operand, n, xhat, mask, planes): planes = (buffer,
+    batches, rows, cols, k_is_col) also writes the open as a two-party
+    product operand's digit planes (xhat may then be None)."""
     arr = (native.Lin2Job * len(jobs))()
-    for k, (x, n, xhat, mask) in enumerate(jobs):
+    for k, jb in enumerate(jobs):
+        x, n, xhat, mask = jb[:4]
         arr[k].x, arr[k].n, arr[k].xhat, arr[k].mask = x, n, ptr(xhat), mask & M64
+        arr[k].xhat_planes = kb_planes_out(jb[4] if len(jb) > 4 else None)
     native.call("sufhip_lin2_batch", arr, len(jobs), stream_ptr())
 
 
