@@ -307,3 +307,34 @@ def test_layer_config_shape_twice():
         ly.eval2(xin, out)
         rec = (u64(out[0]) + u64(out[1])).astype(np.uint64)
         assert np.array_equal(rec, want.view(np.uint64))
+
+
+def test_plane_outputs_reject_bad_layouts():
+    """The digit-plane outputs and inputs are checked on the host: a plane
+    layout that does not cover the open, a head-merged plane output without
+    merge_heads, and unaligned X planes are refused before any launch."""
+    x = (dev(np.zeros(64 * 64, np.uint64)), dev(np.zeros(64 * 64, np.uint64)))
+    planes = layer.kb_planes(1, 64, 64)
+    with pytest.raises(native.SufHipError):  # 64 x 64 planes for 32 x 64 elements
+        layer.lin2_batch([(layer.operand(layer.term(x)), 32 * 64, None, 0,
+                           (planes, 1, 64, 64, 1))])
+    with pytest.raises(native.SufHipError):  # rows not a multiple of 32
+        layer.lin2_batch([(layer.operand(layer.term(x)), 48 * 64, None, 0,
+                           (planes, 1, 48, 64, 1))])
+    tri = layer.BatchedTriples(Dealer(12), 2, 32, 32, 32)
+    a = native.BeaverMfma2Args()
+    a.Dp, a.Ep = tri.Dp.data_ptr(), tri.Ep.data_ptr()
+    for p in (0, 1):
+        a.Ap[p], a.Bp[p], a.C[p] = tri.Ap[p].data_ptr(), tri.Bp[p].data_ptr(), tri.C[p].data_ptr()
+    out = tuple(torch.empty(2 * 32 * 32, dtype=torch.int64, device="cuda") for _ in range(2))
+    a.batches, a.M, a.K, a.N = 2, 32, 32, 32
+    a.out[0], a.out[1] = out[0].data_ptr(), out[1].data_ptr()
+    a.out_planes.planes, a.out_planes.cols = planes.data_ptr(), 64  # without merge_heads
+    with pytest.raises(native.SufHipError):
+        native.call("sufhip_beaver_matmul2_mfma_ex", native.ctypes.byref(a), 0)
+    W = np.ones((64, 32), np.int64)
+    pm = layer.PublicMatmulTrunc(32, 64, 32, W, Dealer(13), STATE, F)
+    with pytest.raises(native.SufHipError):  # X planes not 16-byte aligned
+        native.call("sufhip_matmul_public2_planes", pm.work.data_ptr() + 8, 32, 64, 32,
+                    pm.planes.data_ptr(), pm.digits, out[0].data_ptr(), out[1].data_ptr(), None,
+                    0, None, pm.work.data_ptr(), pm.work_bytes, 0)
