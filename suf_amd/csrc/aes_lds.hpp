@@ -444,6 +444,124 @@ struct AesLds4 {
   }
 };
 
+// Two-table variant for kernels that cannot spend AesLds4's 128 KB:
+// T0 = T and T1 = rotl(8)(T), kCopies-way replicated (kCopies <= 32) in a
+// 64 KB span, byte address e * 256 + j * 128 + c * 4 (the first half of
+// AesLds4's layout; lane l reads copy l % kCopies).  T2 and T3 are rotl(16)
+// of T0 and T1, so a column is
+//   T0[a] ^ T1[b] ^ rotl16(T0[c] ^ T1[d]) ^ k:
+// four single-instruction lookups (v_perm_b32 of the state word and a
+// per-lane base), one rotate and three XORs -- about 32 VALU operations per
+// round against 52 for the single-table form's shifted addresses and three
+// rotates per column.
+template <int kCopies>
+struct AesLds2 {
+  static_assert(kCopies >= 4 && kCopies <= 32 && (kCopies & (kCopies - 1)) == 0,
+                "AesLds2: 4..32 copies, a power of two");
+  static constexpr int kSpanWords = 256 * 64;  // 64 KB whatever kCopies is
+  const uint32_t* lds;
+  uint32_t base[2];
+
+  __device__ __forceinline__ static AesLds2 make(const uint32_t* lds) {
+    const uint32_t c4 = (threadIdx.x % kCopies) * 4u;
+    return AesLds2{lds, {c4, c4 | 128u}};
+  }
+  template <int j, int k>
+  __device__ __forceinline__ uint32_t t(uint32_t w) const {
+    // byte0 <- base byte0, byte1 <- w byte k, bytes 2 and 3 <- 0
+    const uint32_t addr = __builtin_amdgcn_perm(w, base[j], 0x0c0c0000u | uint32_t(4 + k) << 8);
+    return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(lds) + addr);
+  }
+  __device__ __forceinline__ static uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+  }
+  __device__ __forceinline__ uint32_t col(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                          uint32_t k) const {
+    return xor3(t<0, 0>(a), t<1, 1>(b), k) ^ rotl32(t<0, 2>(c) ^ t<1, 3>(d), 16);
+  }
+  __device__ __forceinline__ void round(uint32_t& s0, uint32_t& s1, uint32_t& s2, uint32_t& s3,
+                                        uint32_t k0, uint32_t k1, uint32_t k2,
+                                        uint32_t k3) const {
+    const uint32_t n0 = col(s0, s1, s2, s3, k0);
+    const uint32_t n1 = col(s1, s2, s3, s0, k1);
+    const uint32_t n2 = col(s2, s3, s0, s1, k2);
+    const uint32_t n3 = col(s3, s0, s1, s2, k3);
+    s0 = n0;
+    s1 = n1;
+    s2 = n2;
+    s3 = n3;
+  }
+  // Final round: S(x) is byte 1 (and byte 2) of T0[x] and byte 3 of T1[x].
+  __device__ __forceinline__ uint32_t last_col(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                               uint32_t k) const {
+    const uint32_t lo = __builtin_amdgcn_perm(t<0, 1>(b), t<0, 0>(a), 0x0c0c0501u);  // bytes 0,1
+    const uint32_t hi = __builtin_amdgcn_perm(t<1, 3>(d), t<0, 2>(c), 0x07020c0cu);  // bytes 2,3
+    return (lo | hi) ^ k;
+  }
+  __device__ __forceinline__ void last(uint32_t& s0, uint32_t& s1, uint32_t& s2, uint32_t& s3,
+                                       const uint4 k) const {
+    const uint32_t o0 = last_col(s0, s1, s2, s3, k.x);
+    const uint32_t o1 = last_col(s1, s2, s3, s0, k.y);
+    const uint32_t o2 = last_col(s2, s3, s0, s1, k.z);
+    const uint32_t o3 = last_col(s3, s0, s1, s2, k.w);
+    s0 = o0;
+    s1 = o1;
+    s2 = o2;
+    s3 = o3;
+  }
+  // Same contract as AesLds::encrypt; the middle rounds stay a loop for the
+  // same instruction-cache reason.
+  __device__ __forceinline__ void encrypt(uint32_t& s0, uint32_t& s1, uint32_t& s2, uint32_t& s3,
+                                          const uint4* rk) const {
+    uint4 k = rk[0];
+    s0 ^= k.x;
+    s1 ^= k.y;
+    s2 ^= k.z;
+    s3 ^= k.w;
+#pragma unroll 1
+    for (int r = 1; r < 10; ++r) {
+      k = rk[r];
+      round(s0, s1, s2, s3, k.x, k.y, k.z, k.w);
+    }
+    last(s0, s1, s2, s3, rk[10]);
+  }
+  template <int N>
+  __device__ __forceinline__ void encrypt_n(uint32_t (&st)[N][4], const uint4* const (&rk)[N]) const {
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const uint4 k = rk[n][0];
+      st[n][0] ^= k.x;
+      st[n][1] ^= k.y;
+      st[n][2] ^= k.z;
+      st[n][3] ^= k.w;
+    }
+#pragma unroll 1
+    for (int r = 1; r < 10; ++r) {
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const uint4 k = rk[n][r];
+        round(st[n][0], st[n][1], st[n][2], st[n][3], k.x, k.y, k.z, k.w);
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) last(st[n][0], st[n][1], st[n][2], st[n][3], rk[n][10]);
+  }
+  // Cooperative fill of the used words of the span from T in global memory
+  // (staged once in LDS); contains a barrier, follow with __syncthreads().
+  __device__ __forceinline__ static void fill(uint32_t* lds, const uint32_t* tsrc) {
+    constexpr int kVec = kCopies / 4;  // uint4 stores per (entry, table)
+    __shared__ uint32_t stage[256];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) stage[i] = tsrc[i];
+    __syncthreads();
+    uint4* dst = reinterpret_cast<uint4*>(lds);
+    for (int q = threadIdx.x; q < 256 * 2 * kVec; q += blockDim.x) {
+      const int e = q / (2 * kVec), j = (q / kVec) & 1, v4 = q % kVec;
+      const uint32_t v = rotl32(stage[e], 8 * j);
+      dst[e * 16 + j * 8 + v4] = make_uint4(v, v, v, v);
+    }
+  }
+};
+
 // Cooperative fill of the replicated table from the constant T table in
 // global memory (`tsrc`, 256 words): the 256 words are loaded once (one
 // global round trip) into a 1 KB LDS staging copy, then replicated from LDS

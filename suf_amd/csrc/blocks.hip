@@ -25,6 +25,7 @@ constexpr int kLnBlock = 256;
 constexpr int kLnWaves = kLnBlock / 64;
 constexpr int kLnMaxPer = 8;  // elements per thread: cols <= 2048
 constexpr int kLnCopies = 4;  // the T table serves one lane per workgroup
+using LnAes = AesLds<kLnCopies>;  // one lane's chain: the small table fills fastest
 
 struct LnArgs {
   const uint64_t* x[2];
@@ -59,7 +60,7 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
   __syncthreads();
   chain_compare(A.rs, L);
   __syncthreads();
-  const AesLds<kLnCopies> aes{tab, threadIdx.x % kLnCopies};
+  const LnAes aes{tab, threadIdx.x % kLnCopies};
   const ChainKeyInfo K = chain_key_info(A.rs, L);
   auto gate = [&](int j, uint64_t v) {
     return Two{{trunc_table_eval_h(th[j][0], A.tr[j].table[0], A.tr[j].f, v),
@@ -131,7 +132,7 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
     if (threadIdx.x == 0) {
       const Two v{{var.v[0] + A.eps, var.v[1]}};
       const Two rs =
-          chain_eval<SUFHIP_CHAIN_RSQRT, kLnCopies>(A.rs, L, K, aes, size_t(r), v, pre);
+          chain_eval<SUFHIP_CHAIN_RSQRT, LnAes>(A.rs, L, K, aes, size_t(r), v, pre);
       bc[0] = rs.v[0];
       bc[1] = rs.v[1];
     }
@@ -169,6 +170,7 @@ constexpr int kSmRounds = 10;
 constexpr int kSmMaxRow = 512;
 constexpr int kSmWaves = 4;
 constexpr int kSmCopies = 32;
+using SmAes = AesLds<kSmCopies>;  // two workgroups per CU need the 32 KB table
 constexpr size_t kSmLdsCap = 65536;
 constexpr int kSmLock = 1;  // nExp chains per lane evaluated in lockstep
 
@@ -220,7 +222,7 @@ __global__ void __launch_bounds__(64 * kSmWaves) softmax2_kernel(SmArgs a) {
   chain_compare(a.nexp, st.nexp);
   chain_compare(a.recip, st.recip);
   __syncthreads();
-  const AesLds<kSmCopies> aes{st.tab, threadIdx.x % kSmCopies};
+  const SmAes aes{st.tab, threadIdx.x % kSmCopies};
   const ChainKeyInfo Kn = chain_key_info(a.nexp, st.nexp);
   const ChainKeyInfo Kr = chain_key_info(a.recip, st.recip);
   const uint32_t shared = ~st.t.diff;
@@ -275,7 +277,7 @@ __global__ void __launch_bounds__(64 * kSmWaves) softmax2_kernel(SmArgs a) {
     }
     __syncthreads();
     const int level =
-        tree_row<kSmRounds, kSmCopies>(a.keys, st.t, aes, even, odd, mr, len, st.j0[wave], shared);
+        tree_row<kSmRounds, SmAes>(a.keys, st.t, aes, even, odd, mr, len, st.j0[wave], shared);
     const uint64_t* fin = (level & 1) ? odd : even;
     const int fw = (level & 1) ? (mr + 1) / 2 : mr;
     const uint64_t m0 = len > 0 ? fin[0] : 0, m1 = len > 0 ? fin[fw] : 0;
@@ -296,8 +298,8 @@ __global__ void __launch_bounds__(64 * kSmWaves) softmax2_kernel(SmArgs a) {
         dl[u] = Two{{m0 - s[k0 + u][0], m1 - s[k0 + u][1]}};
         pl[u] = chain_loader<SUFHIP_CHAIN_CUBIC>{&a.nexp, ii[u]};
       }
-      chain_eval_m<SUFHIP_CHAIN_CUBIC, kSmCopies, kSmLock>(a.nexp, st.nexp, Kn, aes, ii, dl, pl,
-                                                            ev);
+      chain_eval_m<SUFHIP_CHAIN_CUBIC, SmAes, kSmLock>(a.nexp, st.nexp, Kn, aes, ii, dl, pl,
+                                                        ev);
 #pragma unroll
       for (int u = 0; u < kSmLock; ++u) {
         const bool ok = lane + 64 * (k0 + u) < len;
@@ -312,7 +314,7 @@ __global__ void __launch_bounds__(64 * kSmWaves) softmax2_kernel(SmArgs a) {
     // inv = Recip(row sum) on lane 0.
     uint64_t inv0 = 0, inv1 = 0;
     if (lane == 0 && len > 0) {
-      const Two iv = chain_eval<SUFHIP_CHAIN_RECIP, kSmCopies>(
+      const Two iv = chain_eval<SUFHIP_CHAIN_RECIP, SmAes>(
           a.recip, st.recip, Kr, aes, size_t(r), Two{{es0, es1}}, st.rpre[wave]);
       inv0 = iv.v[0];
       inv1 = iv.v[1];

@@ -242,9 +242,9 @@ __device__ __forceinline__ Two chain_trunc(const ChainArgs& A, int j, Two z) {
 // encrypted in lockstep and the truncations' table reads of a step are in
 // flight together: a lane pays one latency per step, not one per element and
 // party.
-template <int kKind, int kCopies, int M, class Src>
+template <int kKind, class Aes, int M, class Src>
 __device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds& L,
-                                             const ChainKeyInfo& K, const AesLds<kCopies>& aes,
+                                             const ChainKeyInfo& K, const Aes& aes,
                                              const size_t (&i)[M], const Two (&x)[M],
                                              const Src (&P)[M], Two (&out)[M]) {
   constexpr int W = kKind == SUFHIP_CHAIN_CUBIC ? 4 : 2;
@@ -371,15 +371,15 @@ __device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds&
 }
 
 // The whole chain for one element (chain_eval_m with M = 1).
-template <int kKind, int kCopies, class Src>
+template <int kKind, class Aes, class Src>
 __device__ __forceinline__ Two chain_eval(const ChainArgs& A, const ChainLds& L,
-                                          const ChainKeyInfo& K, const AesLds<kCopies>& aes,
+                                          const ChainKeyInfo& K, const Aes& aes,
                                           size_t i, Two x, const Src& P) {
   const size_t ii[1] = {i};
   const Two xx[1] = {x};
   const Src pp[1] = {P};
   Two out[1];
-  chain_eval_m<kKind, kCopies, 1>(A, L, K, aes, ii, xx, pp, out);
+  chain_eval_m<kKind, Aes, 1>(A, L, K, aes, ii, xx, pp, out);
   return out[0];
 }
 

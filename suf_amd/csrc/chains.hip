@@ -15,25 +15,26 @@
 namespace sufhip {
 namespace {
 
-constexpr int kBlock = 256;
+constexpr int kBlock = 512;  // two workgroups of the 72 KB LDS footprint per CU
 constexpr int kCopies = 32;
+using ChainAes = AesLds2<kCopies>;
 
 template <int kKind>
 __global__ void __launch_bounds__(kBlock) gate_chain_kernel(ChainArgs A) {
   constexpr int W = kKind == SUFHIP_CHAIN_CUBIC ? 4 : 2;
-  __shared__ __align__(16) uint32_t tab[256 * kCopies];
+  __shared__ __align__(16) uint32_t tab[ChainAes::kSpanWords];
   __shared__ ChainLds L;
-  fill_ttable<kCopies>(tab, kTDev.v);
+  ChainAes::fill(tab, kTDev.v);
   chain_stage(A, W, L);
   __syncthreads();
   chain_compare(A, L);
   __syncthreads();
-  const AesLds<kCopies> aes{tab, threadIdx.x % kCopies};
+  const ChainAes aes = ChainAes::make(tab);
   const ChainKeyInfo K = chain_key_info(A, L);
   for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < A.n;
        i += size_t(gridDim.x) * kBlock) {
     const Two x{{operand_at(A.x, 0, i), operand_at(A.x, 1, i)}};
-    const Two res = chain_eval<kKind, kCopies>(A, L, K, aes, i, x, chain_loader<kKind>{&A, i});
+    const Two res = chain_eval<kKind, ChainAes>(A, L, K, aes, i, x, chain_loader<kKind>{&A, i});
     if (A.out[0]) {
       A.out[0][i] = res.v[0];
       A.out[1][i] = res.v[1];
@@ -51,7 +52,7 @@ unsigned int chain_grid(size_t n) {
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   const size_t need = (n + kBlock - 1) / kBlock;
-  const size_t cap = size_t(cus) * 4;
+  const size_t cap = size_t(cus) * 2;
   return static_cast<unsigned int>(need < cap ? need : cap);
 }
 

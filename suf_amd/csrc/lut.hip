@@ -441,7 +441,7 @@ __global__ void __launch_bounds__(64 * kTreeWaves) relu_max_tree2_kernel(ReluTre
     }
     __syncthreads();
     const int level =
-        tree_row<kTreeRounds, kTreeCopies>(a.keys, st.t, aes, even, odd, mr, full, st.j0[wave],
+        tree_row<kTreeRounds, AesLds<kTreeCopies>>(a.keys, st.t, aes, even, odd, mr, full, st.j0[wave],
                                            shared);
     if (full > 0) {
       const uint64_t* fin = (level & 1) ? odd : even;

@@ -180,9 +180,9 @@ __device__ __forceinline__ int tree_interval(const TreeKeys<kRounds>& K,
 // at index 0 of the final level's buffer (even if the count is even, odd
 // otherwise; party stride mr or ceil(mr / 2)).  Every thread of the
 // workgroup must call it (len 0 for an idle wave).
-template <int kRounds, int kCopies>
+template <int kRounds, class Aes>
 __device__ __forceinline__ int tree_row(const TreeKeys<kRounds>& K, const TreeLds<kRounds>& L,
-                                        const AesLds<kCopies>& aes, uint64_t* even,
+                                        const Aes& aes, uint64_t* even,
                                         uint64_t* odd, int mr, int len, const uint32_t* j0s,
                                         uint32_t shared) {
   const int lane = threadIdx.x & 63, half = (mr + 1) / 2;
