@@ -37,14 +37,18 @@ struct SplitArgs {
   const uint64_t* src[kSplitJobs];
   int8_t* planes[kSplitJobs];
   int batches[kSplitJobs], rows[kSplitJobs], cols[kSplitJobs], k_is_col[kSplitJobs];
-  size_t begin[kSplitJobs + 1];  // lanes (4 k each) of the jobs before
+  size_t begin[kSplitJobs + 1];  // lanes of the jobs before (4 or 16 k each)
   int count;
 };
 
-// One lane per 4 consecutive k of one plane row.  Row-side operands
-// (k_is_col: k runs along a source row) take 4 adjacent words; column-side
-// ones 4 words a source row apart, consecutive lanes reading consecutive
-// columns.
+// Row-side operands (k_is_col: k runs along a source row) take one lane
+// per 4 consecutive k of one plane row: 4 adjacent words in, consecutive
+// lanes writing consecutive 4-byte groups.  Column-side operands take one
+// lane per 16 k of one plane row: 16 words a source row apart, the two
+// halves of a 32-byte row segment on adjacent lanes and consecutive lane
+// pairs on consecutive columns, so that every segment of every plane is
+// written whole by one wave's 16-byte stores (never assembled from partial
+// writes of lanes in other workgroups).
 __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
   const size_t total = a.begin[a.count];
   for (size_t g = size_t(blockIdx.x) * 256 + threadIdx.x; g < total;
@@ -55,31 +59,45 @@ __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
     const int rows = a.rows[j], cols = a.cols[j];
     const bool kc = a.k_is_col[j] != 0;
     const int K = kc ? cols : rows, R = kc ? rows : cols;
-    const size_t per_batch = size_t(R) * (K / 4);
-    const size_t b = q / per_batch, rem = q % per_batch;
-    int r, k;
-    if (kc) {
-      r = int(rem / (K / 4));
-      k = 4 * int(rem % (K / 4));
-    } else {
-      k = 4 * int(rem / R);
-      r = int(rem % R);
-    }
-    const uint64_t* src = a.src[j] + b * size_t(rows) * cols;
-    uint32_t pk[kDigitPlanes] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint64_t v = kc ? src[size_t(r) * cols + k + t] : src[size_t(k + t) * cols + r];
-      uint32_t d[kDigitPlanes];
-      digits8(v, d);
-#pragma unroll
-      for (int i = 0; i < kDigitPlanes; ++i) pk[i] |= d[i] << (8 * t);
-    }
     const size_t plane = size_t(a.batches[j]) * R * K;
-    const size_t off = b * size_t(R) * K + kblock_off(size_t(r), k, size_t(R));
+    if (kc) {
+      const size_t per_batch = size_t(R) * (K / 4);
+      const size_t b = q / per_batch, rem = q % per_batch;
+      const int r = int(rem / (K / 4)), k = 4 * int(rem % (K / 4));
+      const uint64_t* src = a.src[j] + b * size_t(rows) * cols + size_t(r) * cols + k;
+      uint32_t pk[kDigitPlanes] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < kDigitPlanes; ++i)
-      *reinterpret_cast<uint32_t*>(a.planes[j] + i * plane + off) = pk[i];
+      for (int t = 0; t < 4; ++t) {
+        uint32_t d[kDigitPlanes];
+        digits8(src[t], d);
+#pragma unroll
+        for (int i = 0; i < kDigitPlanes; ++i) pk[i] |= d[i] << (8 * t);
+      }
+      const size_t off = b * size_t(R) * K + kblock_off(size_t(r), k, size_t(R));
+#pragma unroll
+      for (int i = 0; i < kDigitPlanes; ++i)
+        *reinterpret_cast<uint32_t*>(a.planes[j] + i * plane + off) = pk[i];
+    } else {
+      const size_t per_batch = size_t(R) * (K / 16);
+      const size_t b = q / per_batch, rem = q % per_batch;
+      const int h = int(rem & 1), kb = int(rem / (2 * size_t(R)));
+      const int r = int((rem >> 1) % size_t(R));
+      const int k0 = 32 * kb + 16 * h;
+      const uint64_t* src = a.src[j] + b * size_t(rows) * cols + size_t(k0) * cols + r;
+      int8_t* dst = a.planes[j] + b * size_t(R) * K + kblock_off(size_t(r), k0, size_t(R));
+      uint32_t pk[kDigitPlanes][4] = {};
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        uint32_t d[kDigitPlanes];
+        digits8(src[size_t(t) * cols], d);
+#pragma unroll
+        for (int i = 0; i < kDigitPlanes; ++i) pk[i][t >> 2] |= d[i] << (8 * (t & 3));
+      }
+#pragma unroll
+      for (int i = 0; i < kDigitPlanes; ++i)
+        *reinterpret_cast<uint4*>(dst + i * plane) =
+            make_uint4(pk[i][0], pk[i][1], pk[i][2], pk[i][3]);
+    }
   }
 }
 
@@ -244,7 +262,8 @@ int sufhip_kb_split_batch(const sufhip_kb_split_job* jobs, int count, void* stre
     a.rows[j] = jb.rows;
     a.cols[j] = jb.cols;
     a.k_is_col[j] = jb.k_is_col ? 1 : 0;
-    a.begin[j + 1] = a.begin[j] + size_t(jb.batches) * jb.rows * jb.cols / 4;
+    const size_t n = size_t(jb.batches) * jb.rows * jb.cols;
+    a.begin[j + 1] = a.begin[j] + n / (jb.k_is_col ? 4 : 16);
   }
   a.count = count;
   if (a.begin[count] == 0) return SUFHIP_OK;
