@@ -234,6 +234,9 @@ def bench_matmul(steps, warmup, M=128, K=768, N=3072, frac_bits=12, cpu_seconds=
     ok = bool(np.array_equal(rec.astype(np.uint64), (prod >> frac_bits).view(np.uint64).ravel()))
     macs = 2 * 2 * M * K * N  # both parties, [D | A] x [B' ; E] is a 2K-deep product
     res = {"ms": ms, "eager_ms": eager_ms, "shape": [M, K, N], "matmul_ms": mm_ms,
+           "matmul_part": ("opens written as digit planes + both products + truncation "
+                           "(eager, events around them)" if g.fused else
+                           "both products (eager, events around them)"),
            "u64_macs": macs,
            "u64_mac_per_s": macs / (mm_ms / 1e3), "trunc": "GapARS f=%d" % frac_bits,
            "matmul_kernel": ("two-party int8-digit MFMA, truncation fused" if g.fused else

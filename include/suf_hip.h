@@ -740,6 +740,21 @@ typedef struct sufhip_beaver_mfma2_args {
 int sufhip_beaver_matmul2_mfma_ex(const sufhip_beaver_mfma2_args* args, void* stream);
 size_t sufhip_kb_planes_bytes(int batches, int rows, int cols);
 int sufhip_kb_split_batch(const sufhip_kb_split_job* jobs, int count, void* stream);
+/* sufhip_kb_open_split_batch: up to SUFHIP_KB_SPLIT_JOBS masked opens of
+ * Beaver operands written straight as their digit planes, with no u64 open
+ * in memory: element i is a[0][i] + a[1][i] - b[0][i] - b[1][i] (D = X - A
+ * or E = W - B from both parties' shares: materialize_open of the Beaver
+ * matmul, src/nn/matmul_beaver.cpp:34-53), laid out as in
+ * sufhip_kb_split_batch.  a[0]
+ * and a[1] are required; b[p] = NULL subtracts nothing. */
+typedef struct sufhip_kb_open_job {
+  const uint64_t* a[2];
+  const uint64_t* b[2];
+  int8_t* planes;
+  int batches, rows, cols;
+  int k_is_col;
+} sufhip_kb_open_job;
+int sufhip_kb_open_split_batch(const sufhip_kb_open_job* jobs, int count, void* stream);
 int sufhip_beaver_matmul2_mfma_batched(const int8_t* d_Dp, const int8_t* d_Ep,
                                        const int8_t* d_Ap0, const int8_t* d_Ap1,
                                        const int8_t* d_Bp0, const int8_t* d_Bp1,

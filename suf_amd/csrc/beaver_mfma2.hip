@@ -35,6 +35,8 @@ constexpr int kMaxBeaverK = 4096;
 
 struct SplitArgs {
   const uint64_t* src[kSplitJobs];
+  const uint64_t* add[kSplitJobs];     // optional: + add[i]
+  const uint64_t* sub[kSplitJobs][2];  // optional: - sub[0][i] - sub[1][i]
   int8_t* planes[kSplitJobs];
   int batches[kSplitJobs], rows[kSplitJobs], cols[kSplitJobs], k_is_col[kSplitJobs];
   size_t begin[kSplitJobs + 1];  // lanes of the jobs before (4 or 16 k each)
@@ -49,6 +51,14 @@ struct SplitArgs {
 // pairs on consecutive columns, so that every segment of every plane is
 // written whole by one wave's 16-byte stores (never assembled from partial
 // writes of lanes in other workgroups).
+__device__ __forceinline__ uint64_t split_val(const SplitArgs& a, int j, size_t i) {
+  uint64_t v = a.src[j][i];
+  if (a.add[j]) v += a.add[j][i];
+  if (a.sub[j][0]) v -= a.sub[j][0][i];
+  if (a.sub[j][1]) v -= a.sub[j][1][i];
+  return v;
+}
+
 __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
   const size_t total = a.begin[a.count];
   for (size_t g = size_t(blockIdx.x) * 256 + threadIdx.x; g < total;
@@ -64,12 +74,12 @@ __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
       const size_t per_batch = size_t(R) * (K / 4);
       const size_t b = q / per_batch, rem = q % per_batch;
       const int r = int(rem / (K / 4)), k = 4 * int(rem % (K / 4));
-      const uint64_t* src = a.src[j] + b * size_t(rows) * cols + size_t(r) * cols + k;
+      const size_t src = b * size_t(rows) * cols + size_t(r) * cols + k;
       uint32_t pk[kDigitPlanes] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         uint32_t d[kDigitPlanes];
-        digits8(src[t], d);
+        digits8(split_val(a, j, src + t), d);
 #pragma unroll
         for (int i = 0; i < kDigitPlanes; ++i) pk[i] |= d[i] << (8 * t);
       }
@@ -83,13 +93,13 @@ __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
       const int h = int(rem & 1), kb = int(rem / (2 * size_t(R)));
       const int r = int((rem >> 1) % size_t(R));
       const int k0 = 32 * kb + 16 * h;
-      const uint64_t* src = a.src[j] + b * size_t(rows) * cols + size_t(k0) * cols + r;
+      const size_t src = b * size_t(rows) * cols + size_t(k0) * cols + r;
       int8_t* dst = a.planes[j] + b * size_t(R) * K + kblock_off(size_t(r), k0, size_t(R));
       uint32_t pk[kDigitPlanes][4] = {};
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
         uint32_t d[kDigitPlanes];
-        digits8(src[size_t(t) * cols], d);
+        digits8(split_val(a, j, src + size_t(t) * cols), d);
 #pragma unroll
         for (int i = 0; i < kDigitPlanes; ++i) pk[i][t >> 2] |= d[i] << (8 * (t & 3));
       }
@@ -238,6 +248,41 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 using namespace sufhip;
 
+namespace sufhip {
+namespace {
+
+// Shape checks and lane count of split job j (sources already set).
+int split_job(SplitArgs& a, int j, int8_t* planes, int batches, int rows, int cols,
+              int k_is_col, const char* what) {
+  const bool shape = batches >= 1 && rows >= 32 && cols >= 32 && rows % 32 == 0 &&
+                     cols % 32 == 0;
+  if (!shape || !planes || !aligned16(planes)) {
+    set_error(std::string(what) +
+              ": batches >= 1, rows and cols multiples of 32, planes 16-byte aligned");
+    return SUFHIP_ERR_INVALID;
+  }
+  a.planes[j] = planes;
+  a.batches[j] = batches;
+  a.rows[j] = rows;
+  a.cols[j] = cols;
+  a.k_is_col[j] = k_is_col ? 1 : 0;
+  const size_t n = size_t(batches) * rows * cols;
+  a.begin[j + 1] = a.begin[j] + n / (k_is_col ? 4 : 16);
+  return SUFHIP_OK;
+}
+
+int launch_split(SplitArgs& a, int count, void* stream) {
+  a.count = count;
+  if (a.begin[count] == 0) return SUFHIP_OK;
+  size_t g = (a.begin[count] + 255) / 256;
+  if (g > 4096) g = 4096;
+  hipLaunchKernelGGL(kb_split_kernel, dim3(unsigned(g)), dim3(256), 0, as_stream(stream), a);
+  return check_launch("kb_split_kernel");
+}
+
+}  // namespace
+}  // namespace sufhip
+
 extern "C" {
 
 size_t sufhip_kb_planes_bytes(int batches, int rows, int cols) {
@@ -249,28 +294,33 @@ int sufhip_kb_split_batch(const sufhip_kb_split_job* jobs, int count, void* stre
   SUFHIP_REQUIRE(count >= 0 && count <= kSplitJobs && (count == 0 || jobs),
                  "sufhip_kb_split_batch: 0..SUFHIP_KB_SPLIT_JOBS jobs");
   SplitArgs a{};
-  a.begin[0] = 0;
   for (int j = 0; j < count; ++j) {
     const sufhip_kb_split_job& jb = jobs[j];
-    SUFHIP_REQUIRE(sufhip_kb_planes_bytes(jb.batches, jb.rows, jb.cols) != 0,
-                   "sufhip_kb_split_batch: batches >= 1, rows and cols multiples of 32");
-    SUFHIP_REQUIRE(jb.src && jb.planes && aligned16(jb.planes),
-                   "sufhip_kb_split_batch: null source or planes not 16-byte aligned");
+    SUFHIP_REQUIRE(jb.src, "sufhip_kb_split_batch: null source");
     a.src[j] = jb.src;
-    a.planes[j] = jb.planes;
-    a.batches[j] = jb.batches;
-    a.rows[j] = jb.rows;
-    a.cols[j] = jb.cols;
-    a.k_is_col[j] = jb.k_is_col ? 1 : 0;
-    const size_t n = size_t(jb.batches) * jb.rows * jb.cols;
-    a.begin[j + 1] = a.begin[j] + n / (jb.k_is_col ? 4 : 16);
+    if (int rc = split_job(a, j, jb.planes, jb.batches, jb.rows, jb.cols, jb.k_is_col,
+                           "sufhip_kb_split_batch"))
+      return rc;
   }
-  a.count = count;
-  if (a.begin[count] == 0) return SUFHIP_OK;
-  size_t g = (a.begin[count] + 255) / 256;
-  if (g > 4096) g = 4096;
-  hipLaunchKernelGGL(kb_split_kernel, dim3(unsigned(g)), dim3(256), 0, as_stream(stream), a);
-  return check_launch("kb_split_kernel");
+  return launch_split(a, count, stream);
+}
+
+int sufhip_kb_open_split_batch(const sufhip_kb_open_job* jobs, int count, void* stream) {
+  SUFHIP_REQUIRE(count >= 0 && count <= kSplitJobs && (count == 0 || jobs),
+                 "sufhip_kb_open_split_batch: 0..SUFHIP_KB_SPLIT_JOBS jobs");
+  SplitArgs a{};
+  for (int j = 0; j < count; ++j) {
+    const sufhip_kb_open_job& jb = jobs[j];
+    SUFHIP_REQUIRE(jb.a[0] && jb.a[1], "sufhip_kb_open_split_batch: null share a[0] or a[1]");
+    a.src[j] = jb.a[0];
+    a.add[j] = jb.a[1];
+    a.sub[j][0] = jb.b[0];
+    a.sub[j][1] = jb.b[1];
+    if (int rc = split_job(a, j, jb.planes, jb.batches, jb.rows, jb.cols, jb.k_is_col,
+                           "sufhip_kb_open_split_batch"))
+      return rc;
+  }
+  return launch_split(a, count, stream);
 }
 
 int sufhip_beaver_matmul2_mfma_ex(const sufhip_beaver_mfma2_args* args, void* stream) {

@@ -111,6 +111,20 @@ def kb_split(jobs):
     native.call("sufhip_kb_split_batch", arr, len(jobs), stream_ptr())
 
 
+def kb_open_split(jobs):
+    """Masked opens written straight as digit planes, up to 8 in one launch:
+    jobs of (a, b, planes, batches, rows, cols, k_is_col) with a and b pairs
+    of share arrays (b may be None); element i is a0 + a1 - b0 - b1."""
+    arr = (native.KbOpenJob * len(jobs))()
+    for i, (a, b, planes, nb, r, c, kc) in enumerate(jobs):
+        arr[i].a[0], arr[i].a[1] = ptr(a[0]), ptr(a[1])
+        if b is not None:
+            arr[i].b[0], arr[i].b[1] = ptr(b[0]), ptr(b[1])
+        arr[i].planes = ptr(planes)
+        arr[i].batches, arr[i].rows, arr[i].cols, arr[i].k_is_col = nb, r, c, int(kc)
+    native.call("sufhip_kb_open_split_batch", arr, len(jobs), stream_ptr())
+
+
 class BatchedTriples:
     """Beaver matrix triples per batch: A [b][M x K], B [b][K x N] uniform,
     C = A B mod 2^64; party 0 holds the drawn shares.  When M, K, N are

@@ -140,19 +140,16 @@ class BeaverMatmulTrunc:
         return out
 
     def _eval2_fused(self, X, W, out, events=None):
-        """The truncation's key-only half, the opens D and E (one launch),
-        their digit planes (one launch), then both parties' products with the
-        truncation of their masked open in one launch; all on the current
-        stream."""
-        from . import layer, tasks
+        """The truncation's key-only half, the opens D = X - A and E = W - B
+        written straight as their digit planes (one launch), then both
+        parties' products with the truncation of their masked open in one
+        launch; all on the current stream."""
+        from . import layer
         M, K, N = self.M, self.K, self.N
         self.tr.prepare()
-        tasks.lin2_batch([
-            (tasks.operand(tasks.term(X), tasks.term(self.A, neg=True)), M * K, self.D, 0),
-            (tasks.operand(tasks.term(W), tasks.term(self.B, neg=True)), K * N, self.E, 0)])
         if events:
             events[0].record()
-        layer.kb_split([(self.D, self.Dp, 1, M, K, 1), (self.E, self.Ep, 1, K, N, 0)])
+        layer.kb_open_split([(X, self.A, self.Dp, 1, M, K, 1), (W, self.B, self.Ep, 1, K, N, 0)])
         a = native.BeaverMfma2Args()
         a.Dp, a.Ep = _p(self.Dp), _p(self.Ep)
         for p in (0, 1):

@@ -85,6 +85,7 @@ _SIGS = {
     "sufhip_kb_planes_bytes": (c_sz, [c_int, c_int, c_int]),
     "sufhip_beaver_matmul2_mfma_ex": (c_int, [c_vp, c_vp]),
     "sufhip_kb_split_batch": (c_int, [c_vp, c_int, c_vp]),
+    "sufhip_kb_open_split_batch": (c_int, [c_vp, c_int, c_vp]),
     "sufhip_beaver_matmul2_mfma_batched": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                                    c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp,
                                                    c_vp]),
@@ -225,6 +226,12 @@ class KbSplitJob(ctypes.Structure):
     """sufhip_kb_split_job (include/suf_hip.h)."""
     _fields_ = [("src", c_vp), ("planes", c_vp), ("batches", c_int), ("rows", c_int),
                 ("cols", c_int), ("k_is_col", c_int)]
+
+
+class KbOpenJob(ctypes.Structure):
+    """sufhip_kb_open_job (include/suf_hip.h)."""
+    _fields_ = [("a", c_vp * 2), ("b", c_vp * 2), ("planes", c_vp), ("batches", c_int),
+                ("rows", c_int), ("cols", c_int), ("k_is_col", c_int)]
 
 
 class Triple2(ctypes.Structure):

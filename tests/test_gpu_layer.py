@@ -338,3 +338,29 @@ def test_plane_outputs_reject_bad_layouts():
         native.call("sufhip_matmul_public2_planes", pm.work.data_ptr() + 8, 32, 64, 32,
                     pm.planes.data_ptr(), pm.digits, out[0].data_ptr(), out[1].data_ptr(), None,
                     0, None, pm.work.data_ptr(), pm.work_bytes, 0)
+
+
+@pytest.mark.parametrize("shape", [(1, 64, 96, 1), (1, 96, 64, 0), (3, 32, 64, 0)])
+def test_kb_open_split_matches_open_then_split(shape):
+    """The open-and-split launch writes the same digit planes as the open
+    a0 + a1 - b0 - b1 in u64 followed by the split, with and without b."""
+    nb, r, c, kc = shape
+    print("[gpu-case] kb_open_split", shape, flush=True)
+    g = np.random.default_rng(7)
+    n = nb * r * c
+    a = tuple(dev(g.integers(0, 2**63, n, dtype=np.uint64) * 2 + 1) for _ in range(2))
+    b = tuple(dev(g.integers(0, 2**63, n, dtype=np.uint64)) for _ in range(2))
+    for use_b in (True, False):
+        opened = a[0] + a[1] - (b[0] + b[1] if use_b else 0)
+        want = layer.kb_planes(nb, r, c)
+        got = layer.kb_planes(nb, r, c)
+        want.fill_(0)
+        got.fill_(0x5a5a)  # every planes byte must be written
+        layer.kb_split([(opened, want, nb, r, c, kc)])
+        layer.kb_open_split([(a, b if use_b else None, got, nb, r, c, kc)])
+        torch.cuda.synchronize()
+        nbytes = native.load().sufhip_kb_planes_bytes(nb, r, c)
+        assert torch.equal(got.view(torch.uint8)[:nbytes], want.view(torch.uint8)[:nbytes]), \
+            (shape, use_b)
+    with pytest.raises(native.SufHipError):  # rows not a multiple of 32
+        layer.kb_open_split([(a, b, layer.kb_planes(1, 64, 64), 1, 48, 64, 1)])
