@@ -530,8 +530,8 @@ def cpu_baseline(keys0, keys1, xhat, gpu_bits0, gpu_bits1, seconds):
 def main():
     a = parse()
     if a.gpus != 1:
-        print("bench.py: this build runs on one GPU only (got --gpus %d); "
-              "multi-GPU sharding is described in DESIGN.md, not implemented" % a.gpus)
+        print("bench.py: measures one GPU only (got --gpus %d); sharding the key "
+              "batch and the layer across GPUs is not implemented" % a.gpus)
         sys.exit(2)
     if a.calibrate_copy:
         calibrate_copy()
