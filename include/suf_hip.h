@@ -175,6 +175,21 @@ size_t sufhip_trunc_work_bytes(int frac_bits, size_t n);
 int sufhip_trunc_eval(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,
                       size_t key_bytes, const uint64_t* d_xhat, size_t n, uint64_t* d_y,
                       void* d_work, size_t work_bytes, void* stream);
+/* sufhip_trunc_eval without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The carry frontier lives in a static per-GPU array
+ * of sufhip_trunc_noalloc_max_work_bytes() = 1 MiB: enough for any n when
+ * frac_bits <= 14, and for n < 2^16 above that; a (frac_bits, n) whose
+ * sufhip_trunc_work_bytes() exceeds it is rejected with SUFHIP_ERR_INVALID.
+ * Every call on one GPU uses that GPU's one array, which keeps the last
+ * call's contents: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller.  Same shares as
+ * sufhip_trunc_eval. */
+size_t sufhip_trunc_noalloc_max_work_bytes(void);
+int sufhip_trunc_eval_noalloc(int kind, int frac_bits, const uint8_t* prg_state,
+                              const uint8_t* d_key, size_t key_bytes, const uint64_t* d_xhat,
+                              size_t n, uint64_t* d_y, void* stream);
 /* The two halves of sufhip_trunc_eval.  prepare reads only the key (it fills
  * d_work with the carry DCF's prefix frontier for a batch of n points), so a
  * caller may run it before the inputs exist, e.g. on another stream while

@@ -30,6 +30,7 @@
 // one launch.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <string>
 
 #include "dcf_device.hpp"
@@ -584,7 +585,63 @@ int launch_finish(int kind, const TruncEvalArgs& a, int parties, hipStream_t s) 
 
 using namespace sufhip;
 
+// Workspace of sufhip_trunc_eval_noalloc: a file-scope device array, so that
+// the entry point needs no allocation.  Each GPU the library runs on holds its
+// own copy for the life of the process.  In host code `scratch` names a host
+// stand-in, not device memory: the array's device address on each GPU comes
+// from hipGetSymbolAddress (noalloc_scratch below) and only that address is
+// passed to kernels.  1 MiB holds the carry frontier of any batch for
+// frac_bits <= 14 (the full-domain table, 786,432 bytes at f = 14) and of
+// batches below 2^16 points for larger frac_bits.
+static constexpr size_t kNoAllocScratchBytes = size_t(1) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kNoAllocMaxDevices];
+
+// The current device's address of `scratch`, looked up once per device (with
+// that device current) and kept.
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  SUFHIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
+  SUFHIP_REQUIRE(dev >= 0 && dev < kNoAllocMaxDevices,
+                 "sufhip_trunc_eval_noalloc: device index beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    SUFHIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    SUFHIP_REQUIRE(p != nullptr, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SUFHIP_OK;
+}
+
+}  // namespace
+
 extern "C" {
+
+size_t sufhip_trunc_noalloc_max_work_bytes(void) { return kNoAllocScratchBytes; }
+
+int sufhip_trunc_eval_noalloc(int kind, int frac_bits, const uint8_t* prg_state,
+                              const uint8_t* d_key, size_t key_bytes, const uint64_t* d_xhat,
+                              size_t n, uint64_t* d_y, void* stream) {
+  const size_t need = sufhip_trunc_work_bytes(frac_bits, n);
+  SUFHIP_REQUIRE(need <= kNoAllocScratchBytes,
+                 "sufhip_trunc_eval_noalloc: the carry frontier for this (frac_bits, n) needs " +
+                     std::to_string(need) + " bytes, above the " +
+                     std::to_string(kNoAllocScratchBytes) +
+                     "-byte static workspace (use sufhip_trunc_eval with a workspace)");
+  void* work = nullptr;
+  if (need > 0) {
+    if (int rc = noalloc_scratch(&work)) return rc;
+  }
+  return sufhip_trunc_eval(kind, frac_bits, prg_state, d_key, key_bytes, d_xhat, n, d_y, work,
+                           need > 0 ? kNoAllocScratchBytes : 0, stream);
+}
 
 size_t sufhip_trunc_key_bytes(int kind, int frac_bits) {
   if (!valid_kind(kind) || frac_bits < 1 || frac_bits > 62) return 0;

@@ -67,6 +67,8 @@ _SIGS = {
     "sufhip_trunc_work_bytes": (c_sz, [c_int, c_sz]),
     "sufhip_trunc_eval": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp, c_sz,
                                   c_vp]),
+    "sufhip_trunc_noalloc_max_work_bytes": (c_sz, []),
+    "sufhip_trunc_eval_noalloc": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp]),
     "sufhip_trunc_prepare": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_sz, c_vp, c_sz, c_vp]),
     "sufhip_trunc_finish": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp, c_sz,
                                     c_vp]),
