@@ -20,6 +20,12 @@
 #include "oracle.h"
 
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
 
 static uint8_t g_sbox[256];
 static int g_sbox_ready = 0;
@@ -61,6 +67,9 @@ static void build_sbox(void) {
   g_sbox_ready = 1;
 }
 
+/* The S-box is built before any caller's threads start. */
+__attribute__((constructor)) static void init_sbox(void) { build_sbox(); }
+
 void orc_aes128_expand(const uint8_t key[16], uint8_t rk[176]) {
   build_sbox();
   memcpy(rk, key, 16);
@@ -101,6 +110,98 @@ void orc_aes128_encrypt(const uint8_t rk[176], const uint8_t in[16], uint8_t out
     for (int i = 0; i < 16; i++) s[i] = (uint8_t)(u[i] ^ rk[16 * round + i]);
   }
   memcpy(out, s, 16);
+}
+
+/* The same cipher on the x86 AES instructions (Intel's AES-NI: AESENC runs
+ * SubBytes, ShiftRows, MixColumns and AddRoundKey of one middle round,
+ * AESENCLAST the final round), taking the FIPS-197 key schedule above as
+ * sixteen-byte round keys.  It is used when the CPU has the instructions and
+ * not disabled by orc_aes_use_ni(0); tests/test_oracle_aes.py checks it
+ * byte for byte against orc_aes128_encrypt. */
+static int g_ni = -1; /* -1: not yet probed */
+
+int orc_aes_ni_available(void) {
+#if defined(__x86_64__)
+  __builtin_cpu_init();
+  return __builtin_cpu_supports("aes") ? 1 : 0;
+#else
+  return 0;
+#endif
+}
+
+void orc_aes_use_ni(int on) { g_ni = on ? orc_aes_ni_available() : 0; }
+
+int orc_aes_ni_active(void) {
+  if (g_ni < 0) g_ni = orc_aes_ni_available();
+  return g_ni;
+}
+
+#if defined(__x86_64__)
+__attribute__((target("aes,sse2"))) static void ni_encrypt(const uint8_t rk[176],
+                                                            const uint8_t in[16],
+                                                            uint8_t out[16]) {
+  __m128i s = _mm_xor_si128(_mm_loadu_si128((const __m128i*)in),
+                            _mm_loadu_si128((const __m128i*)rk));
+  for (int r = 1; r < 10; r++) s = _mm_aesenc_si128(s, _mm_loadu_si128((const __m128i*)(rk + 16 * r)));
+  s = _mm_aesenclast_si128(s, _mm_loadu_si128((const __m128i*)(rk + 160)));
+  _mm_storeu_si128((__m128i*)out, s);
+}
+
+/* MMO blocks out[i] = AES_{rk[i]}(seed) xor seed for i < nb <= 8, the blocks'
+ * rounds interleaved. */
+__attribute__((target("aes,sse2"))) static void ni_mmo(const uint8_t (*rk)[176], int nb,
+                                                        const uint8_t seed[16], uint8_t* out) {
+  const __m128i sd = _mm_loadu_si128((const __m128i*)seed);
+  __m128i s[8];
+  for (int i = 0; i < nb; i++) s[i] = _mm_xor_si128(sd, _mm_loadu_si128((const __m128i*)rk[i]));
+  for (int r = 1; r < 10; r++)
+    for (int i = 0; i < nb; i++)
+      s[i] = _mm_aesenc_si128(s[i], _mm_loadu_si128((const __m128i*)(rk[i] + 16 * r)));
+  for (int i = 0; i < nb; i++) {
+    s[i] = _mm_aesenclast_si128(s[i], _mm_loadu_si128((const __m128i*)(rk[i] + 160)));
+    _mm_storeu_si128((__m128i*)(out + 16 * i), _mm_xor_si128(s[i], sd));
+  }
+}
+#endif
+
+void orc_aes128_encrypt_fast(const uint8_t rk[176], const uint8_t in[16], uint8_t out[16]) {
+#if defined(__x86_64__)
+  if (orc_aes_ni_active()) {
+    ni_encrypt(rk, in, out);
+    return;
+  }
+#endif
+  orc_aes128_encrypt(rk, in, out);
+}
+
+int orc_mmo_fast(const uint8_t (*rk)[176], int nb, const uint8_t seed[16], uint8_t* out) {
+#if defined(__x86_64__)
+  if (nb <= 8 && orc_aes_ni_active()) {
+    ni_mmo(rk, nb, seed, out);
+    return 1;
+  }
+#endif
+  (void)rk;
+  (void)nb;
+  (void)seed;
+  (void)out;
+  return 0;
+}
+
+void orc_set_threads(int n) {
+#ifdef _OPENMP
+  omp_set_num_threads(n > 0 ? n : omp_get_num_procs());
+#else
+  (void)n;
+#endif
+}
+
+int orc_get_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
 }
 
 void orc_aes128_ctr(const uint8_t rk[176], uint64_t ctr_lo, uint64_t ctr_hi,

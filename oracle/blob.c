@@ -46,7 +46,7 @@ static void st64(uint8_t* p, uint64_t v) { memcpy(p, &v, 8); }
 static void keystream(const uint8_t* rk, uint64_t ctr, uint64_t* ks0, uint64_t* ks1) {
   uint8_t blk[16] = {0}, out[16];
   st64(blk, ctr);
-  orc_aes128_encrypt(rk, blk, out);
+  orc_aes128_encrypt_fast(rk, blk, out);
   *ks0 = ld64(out);
   *ks1 = ld64(out + 8);
 }
@@ -82,6 +82,7 @@ void orc_packed_build_key(int party, uint64_t nonce, int in_bits, const uint64_t
 
 void orc_packed_eval(const uint8_t* keys, size_t key_bytes, int broadcast,
                      const uint64_t* xs, size_t n, uint64_t* out) {
+#pragma omp parallel for schedule(static)
   for (size_t idx = 0; idx < n; idx++) {
     const uint8_t* k = broadcast ? keys : keys + idx * key_bytes;
     int in_bits = ld16(k), num_thr = ld16(k + 2), party = k[4];
@@ -137,6 +138,7 @@ void orc_lut_eval(const uint8_t* keys, size_t key_bytes, int broadcast,
  * element's index in the whole batch. */
 void orc_lut_eval_at(const uint8_t* keys, size_t key_bytes, int broadcast,
                      const uint64_t* xs, size_t n, size_t idx0, uint64_t* out) {
+#pragma omp parallel for schedule(static)
   for (size_t i = 0; i < n; i++) {
     const size_t idx = idx0 + i;
     const uint8_t* k = broadcast ? keys : keys + i * key_bytes;

@@ -75,6 +75,7 @@ void orc_prg_init(orc_prg_state* p, const uint8_t* state, int state_len) {
 }
 
 void orc_prg(const orc_prg_state* p, uint8_t* out, int out_len, const uint8_t seed[16]) {
+  if (orc_mmo_fast((const uint8_t(*)[176])p->rk, out_len / 16, seed, out)) return;
   for (int i = 0; i < out_len / 16; i++) {
     orc_aes128_encrypt(p->rk[i], seed, out + 16 * i);
     for (int j = 0; j < 16; j++) out[16 * i + j] ^= seed[j];

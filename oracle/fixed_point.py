@@ -11,6 +11,8 @@ faithful ARS both reconstruct to it while |x| < 2^62), so the chains reduce
 to these formulas.  Products are checked against 2^62 before they are
 formed: an input outside that range raises instead of wrapping.
 
+  spline_closed_form  the spline gate of CubicPolyTask's reference path
+                  (include/runtime/phase_tasks.hpp:2933-2945) with exact shifts
   cubic_task      CubicPolyTask (include/runtime/phase_tasks.hpp:2933-3061)
   recip_task      RecipTask (phase_tasks.hpp:3190-3540; NR step of
                   ref_reciprocal_fixed, include/gates/reciprocal_gate.hpp:96-109)
@@ -66,6 +68,30 @@ def mul_shift(a, b, s, what="mul_shift"):
 def piece_index(alpha, x):
     """Piece of each u64 input: the last alpha_i <= x (alpha[0] = 0)."""
     return np.searchsorted(np.asarray(alpha, dtype=np.uint64), _u64(_i64(x)), side="right") - 1
+
+
+def spline_closed_form(alpha, coeffs, x, frac_bits):
+    """The spline gate at x (u64 ring values): piece i of the sorted piece
+    starts alpha (x's last start <= x), then
+    y = ((c3 x + c2 2^f) x >> f) + c1 2^f) x >> 2f) + c0 with arithmetic
+    shifts (phase_tasks.hpp:2933-2945).  Raises if an intermediate could
+    leave (-2^62, 2^62) for these inputs."""
+    x = np.asarray(x, dtype=np.uint64)
+    piece = np.searchsorted(alpha, x, side="right") - 1
+    c = coeffs[piece]
+    xs = x.view(np.int64)
+    f = frac_bits
+    cx = int(np.abs(coeffs).max())
+    xm = int(np.abs(xs).max()) if xs.size else 0
+    u_max = cx * xm + (cx << f)
+    q_max = ((u_max * xm) >> f) + 1 + (cx << f)
+    if max(u_max * xm, q_max * xm) >= 1 << 62:
+        raise ValueError("spline_closed_form: inputs outside the exact int64 range")
+    u = c[:, 3] * xs + (c[:, 2] << f)
+    p2 = (u * xs) >> f
+    q = p2 + (c[:, 1] << f)
+    y = ((q * xs) >> (2 * f)) + c[:, 0]
+    return y.view(np.uint64)
 
 
 def cubic_task(alpha, coeffs, x, f):

@@ -148,6 +148,7 @@ int orc_trunc_eval(const orc_prg_state* p, int kind, int f, const uint8_t* key,
   const uint8_t* wrap_key = carry_key + pad8(ckb);
   const uint8_t* sign_key = wrap_key + pad8(ukb);
   const uint64_t one = party == 0 ? 1 : 0;
+#pragma omp parallel for schedule(static)
   for (size_t i = 0; i < n; i++) {
     const uint64_t x = xhat[i];
     uint64_t carry = 0, wrap = 0, sign = 0;

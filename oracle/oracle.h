@@ -36,6 +36,19 @@ extern "C" {
 /* ---------------- AES-128 (FIPS-197) ---------------- */
 void orc_aes128_expand(const uint8_t key[16], uint8_t rk[176]);
 void orc_aes128_encrypt(const uint8_t rk[176], const uint8_t in[16], uint8_t out[16]);
+/* The same cipher on the x86 AES instructions when the CPU has them (else
+ * orc_aes128_encrypt): orc_aes_use_ni(0 / 1) turns that path off / on,
+ * orc_aes_ni_active() says which is in use.  orc_mmo_fast writes nb <= 8
+ * MMO blocks AES_{rk[i]}(seed) ^ seed and returns 1, or returns 0 (nothing
+ * written) when the AES instructions are off. */
+int orc_aes_ni_available(void);
+void orc_aes_use_ni(int on);
+int orc_aes_ni_active(void);
+void orc_aes128_encrypt_fast(const uint8_t rk[176], const uint8_t in[16], uint8_t out[16]);
+int orc_mmo_fast(const uint8_t (*rk)[176], int nb, const uint8_t seed[16], uint8_t* out);
+/* OpenMP threads of the per-element loops (n <= 0: all processors). */
+void orc_set_threads(int n);
+int orc_get_threads(void);
 /* CTR block i = AES(le64(ctr_lo + i) || le64(ctr_hi)); out is [blocks][16]. */
 void orc_aes128_ctr(const uint8_t rk[176], uint64_t ctr_lo, uint64_t ctr_hi,
                     size_t blocks, uint8_t* out);
@@ -128,6 +141,7 @@ void orc_beaver_matmul(int party, const uint64_t* D, const uint64_t* E, const ui
                        const uint64_t* B, const uint64_t* C, int batches, int M, int K,
                        int N, int w_transposed, int has_scale, int64_t mul_const,
                        int mul_shift, uint64_t* out, int threads);
+void orc_matmul_public(const uint64_t* X, const int64_t* W, int M, int K, int N, uint64_t* Y);
 void orc_row_mean(const uint64_t* mat, int rows, int cols, const int* valid_lens,
                   uint64_t* out);
 void orc_open_add(const uint64_t* local, const uint64_t* remote, int eff_bits, uint64_t* out,

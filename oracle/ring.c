@@ -163,6 +163,19 @@ void orc_beaver_matmul(int party, const uint64_t* D, const uint64_t* E, const ui
       }
 }
 
+/* src/nn/matmul_publicW.cpp:17-36: Y = X * W mod 2^64 for a share X [M x K]
+ * and public int64 W [K x N] (the reference layer passes no bias), with the
+ * reference's loop order; OpenMP over the outputs. */
+void orc_matmul_public(const uint64_t* X, const int64_t* W, int M, int K, int N, uint64_t* Y) {
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int m = 0; m < M; m++)
+    for (int n = 0; n < N; n++) {
+      uint64_t acc = 0;
+      for (int k = 0; k < K; k++) acc += X[(size_t)m * K + k] * (uint64_t)W[(size_t)k * N + n];
+      Y[(size_t)m * N + n] = acc;
+    }
+}
+
 /* Bit packing of fixed-width values, LSB-first within little-endian u64 words
  * (cuda/pfss_backend_gpu.cu:118-138, cuda/pfss_kernels.cu:722-812). */
 void orc_pack_eff_bits(const uint64_t* in, int eff_bits, uint64_t* packed, size_t n) {

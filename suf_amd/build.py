@@ -10,6 +10,7 @@ units whose object file is newer than every source and header.
 import argparse
 import glob
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -34,7 +35,24 @@ HIPCC_FLAGS = [
     "-I" + CSRC,
     # Keep the compiler from emitting packed FP32 instructions.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Per-kernel register and private-segment report, checked below.
+    "-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics",
 ]
+
+# Kernels allowed a private segment, with the reason.  Every other kernel
+# must report ScratchSize 0, or the build fails.
+SCRATCH_ALLOWED = {
+    # Dealer-side keygen (not on the online path): the four PRG blocks of a
+    # level, indexed by the block loop, spill 144 bytes per lane.
+    "dcf_gen_kernel": "dealer keygen",
+    "trunc_gen_kernel": "dealer keygen",
+    # SGPR spill slots only: the block's ~100 uniform pointers exceed the
+    # SGPR file, and the compiler keeps the overflow in VGPR lanes
+    # (v_writelane / v_readlane).  The frame size is reported, but the kernel
+    # has no scratch memory instruction (tests/test_build_scratch.py).
+    "softmax2_kernel": "SGPR spill slots in VGPR lanes, no scratch memory access",
+}
+RESOURCE_REPORT = os.path.join(LIBDIR, "kernel_resources.txt")
 
 
 def hipcc():
@@ -55,16 +73,76 @@ def _stale(src, obj):
     return any(os.path.getmtime(p) > t for p in [src] + _deps())
 
 
+def parse_resource_usage(text):
+    """{kernel symbol: {field: value}} from -Rpass-analysis=kernel-resource-usage
+    remarks (Function Name, VGPRs, AGPRs, ScratchSize, Occupancy, ...)."""
+    out, cur = {}, None
+    for line in text.splitlines():
+        if "kernel-resource-usage" not in line:
+            continue
+        m = re.search(r"remark:\s+(.*?)\s*\[-Rpass-analysis", line)
+        if not m:
+            continue
+        body = m.group(1)
+        if body.startswith("Function Name:"):
+            cur = body.split(":", 1)[1].strip()
+            out[cur] = {}
+        elif cur is not None and ":" in body:
+            k, v = body.rsplit(":", 1)
+            out[cur][k.strip()] = v.strip()
+    return out
+
+
 def _compile(args):
     cc, src, obj = args
     tmp = obj + ".tmp"
     cmd = [cc] + HIPCC_FLAGS + ["-c", src, "-o", tmp]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:
+        out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
         raise RuntimeError("hipcc failed for %s:\n%s" % (os.path.basename(src), out))
+    out = "\n".join(l for l in r.stdout.splitlines()
+                    if "packed-fp32-ops" not in l and "kernel-resource-usage" not in l)
     os.replace(tmp, obj)
+    with open(obj + ".res", "w") as f:
+        f.write(r.stdout)
     return out
+
+
+def kernel_resources():
+    """Resource report of every kernel in the last build (from the remarks
+    each object's compile wrote next to it)."""
+    res = {}
+    for p in sorted(glob.glob(os.path.join(OBJDIR, "*.o.res"))):
+        for k, v in parse_resource_usage(open(p).read()).items():
+            v["file"] = os.path.basename(p)[:-len(".o.res")]
+            res[k] = v
+    return res
+
+
+def scratch_allowed(symbol):
+    return next((why for name, why in SCRATCH_ALLOWED.items() if name in symbol), None)
+
+
+def check_scratch(res):
+    """Fails on any kernel with a private segment that SCRATCH_ALLOWED does
+    not name; writes the report to suf_amd/lib/kernel_resources.txt."""
+    bad = []
+    lines = []
+    for k in sorted(res):
+        v = res[k]
+        sc = int(v.get("ScratchSize [bytes/lane]", "0"))
+        why = scratch_allowed(k)
+        lines.append("%-70s %-18s VGPR %4s AGPR %4s scratch %4d occupancy %s%s" % (
+            k, v["file"], v.get("VGPRs", "?"), v.get("AGPRs", "?"), sc, v.get("Occupancy [waves/SIMD]", "?"),
+            ("  (allowed: %s)" % why) if sc and why else ""))
+        if sc and not why:
+            bad.append("%s (%s): %d bytes/lane" % (k, v["file"], sc))
+    with open(RESOURCE_REPORT, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    if bad:
+        raise RuntimeError("kernels with private scratch (see %s):\n  %s"
+                           % (RESOURCE_REPORT, "\n  ".join(bad)))
 
 
 def build(if_stale=False, jobs=None):
@@ -90,6 +168,7 @@ def build(if_stale=False, jobs=None):
         if r.returncode != 0:
             raise RuntimeError("link failed:\n" + r.stdout)
         os.replace(tmp, LIB)
+    check_scratch(kernel_resources())
     return LIB
 
 

@@ -195,6 +195,27 @@ struct AesLds {
     s3 = o3;
   }
 
+  // encrypt() with all rounds unrolled, for round keys held in registers (a
+  // per-element key read from HBM): a runtime round index into a register
+  // array would put the keys in private scratch memory.
+  __device__ __forceinline__ void encrypt_unrolled(uint32_t& s0, uint32_t& s1, uint32_t& s2,
+                                                   uint32_t& s3, const uint4 (&rk)[11]) const {
+    s0 ^= rk[0].x;
+    s1 ^= rk[0].y;
+    s2 ^= rk[0].z;
+    s3 ^= rk[0].w;
+#pragma unroll
+    for (int r = 1; r < 10; ++r) round(s0, s1, s2, s3, rk[r].x, rk[r].y, rk[r].z, rk[r].w);
+    const uint32_t o0 = last_col(s0, s1, s2, s3) ^ rk[10].x;
+    const uint32_t o1 = last_col(s1, s2, s3, s0) ^ rk[10].y;
+    const uint32_t o2 = last_col(s2, s3, s0, s1) ^ rk[10].z;
+    const uint32_t o3 = last_col(s3, s0, s1, s2) ^ rk[10].w;
+    s0 = o0;
+    s1 = o1;
+    s2 = o2;
+    s3 = o3;
+  }
+
   // N independent encryptions in lockstep (state n under round keys rk[n]):
   // each round issues the table reads of all N states before any of them is
   // used, so a lane pays about one block's latency for N blocks.  For the

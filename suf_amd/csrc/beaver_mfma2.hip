@@ -312,6 +312,8 @@ int sufhip_kb_open_split_batch(const sufhip_kb_open_job* jobs, int count, void* 
   for (int j = 0; j < count; ++j) {
     const sufhip_kb_open_job& jb = jobs[j];
     SUFHIP_REQUIRE(jb.a[0] && jb.a[1], "sufhip_kb_open_split_batch: null share a[0] or a[1]");
+    SUFHIP_REQUIRE((jb.b[0] == nullptr) == (jb.b[1] == nullptr),
+                   "sufhip_kb_open_split_batch: give both shares of b or neither");
     a.src[j] = jb.a[0];
     a.add[j] = jb.a[1];
     a.sub[j][0] = jb.b[0];

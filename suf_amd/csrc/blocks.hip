@@ -264,7 +264,11 @@ __global__ void __launch_bounds__(64 * kSmWaves) softmax2_kernel(SmArgs a) {
       if (j < len) {
         const size_t i = size_t(b) + size_t(j);
         uint64_t v0 = operand_at(a.x, 0, i), v1 = operand_at(a.x, 1, i);
-        for (int q = 0; q < a.pre; ++q) {
+        // Compile-time gate indices: a runtime index into the by-value
+        // argument block would copy it to private scratch memory.
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          if (q >= a.pre) break;
           const uint64_t o = v0 + v1 + a.pre_mask[q];
           v0 = trunc_table_eval(a.pre_tr[q].key[0], a.pre_tr[q].table[0], a.pre_tr[q].f, o);
           v1 = trunc_table_eval(a.pre_tr[q].key[1], a.pre_tr[q].table[1], a.pre_tr[q].f, o);

@@ -92,6 +92,7 @@ __device__ __forceinline__ int interval_of(uint64_t x, int intervals, uint64_t m
   return iv;
 }
 
+// Round keys in LDS (broadcast keys) or in registers (per-element keys).
 __device__ __forceinline__ void keystream(const AesLds<kLutCopies>& aes, const uint4* rk,
                                           uint64_t ctr, uint64_t& k0, uint64_t& k1) {
   uint32_t s0 = uint32_t(ctr), s1 = uint32_t(ctr >> 32), s2 = 0, s3 = 0;
@@ -100,7 +101,16 @@ __device__ __forceinline__ void keystream(const AesLds<kLutCopies>& aes, const u
   k1 = uint64_t(s2) | uint64_t(s3) << 32;
 }
 
-__device__ __forceinline__ void write_masked_row(const AesLds<kLutCopies>& aes, const uint4* rk,
+__device__ __forceinline__ void keystream(const AesLds<kLutCopies>& aes, const RegKeys& rk,
+                                          uint64_t ctr, uint64_t& k0, uint64_t& k1) {
+  uint32_t s0 = uint32_t(ctr), s1 = uint32_t(ctr >> 32), s2 = 0, s3 = 0;
+  aes.encrypt_unrolled(s0, s1, s2, s3, rk.r);
+  k0 = uint64_t(s0) | uint64_t(s1) << 32;
+  k1 = uint64_t(s2) | uint64_t(s3) << 32;
+}
+
+template <typename RK>
+__device__ __forceinline__ void write_masked_row(const AesLds<kLutCopies>& aes, const RK& rk,
                                                  uint64_t nonce, size_t idx, int iv, int ow,
                                                  int party, const uint64_t* row, uint64_t* out) {
   for (int w = 0; w < ow; w += 2) {
@@ -159,7 +169,7 @@ __global__ void __launch_bounds__(kLutBlock) lut_keyed_kernel(LutArgs a, int bro
     const uint64_t* cg = reinterpret_cast<const uint64_t*>(k + kLutHdr);
     const uint64_t x = a.xs[e] & m;
     const int iv = interval_of(x, nint, m, [&](int i) { return cg[i]; });
-    write_masked_row(aes, rk.r, nonce, e, iv, ow, party, cg + (nint + 1) + size_t(iv) * ow,
+    write_masked_row(aes, rk, nonce, e, iv, ow, party, cg + (nint + 1) + size_t(iv) * ow,
                      a.out + e * size_t(ow));
   }
 }
@@ -195,8 +205,8 @@ __device__ __forceinline__ uint64_t cmp_word(uint64_t x, uint64_t m, int num_thr
   return word;
 }
 
-template <typename ThrAt>
-__device__ __forceinline__ void packed_one(const AesLds<kLutCopies>& aes, const uint4* rk,
+template <typename RK, typename ThrAt>
+__device__ __forceinline__ void packed_one(const AesLds<kLutCopies>& aes, const RK& rk,
                                            uint64_t nonce, int party, uint64_t x, uint64_t m,
                                            int num_thr, int ow, bool sorted, size_t idx,
                                            const ThrAt& thr, uint64_t* out) {
@@ -257,7 +267,7 @@ __global__ void __launch_bounds__(kLutBlock) packed_keyed_kernel(PackedArgs a, i
     const uint64_t m = mask_bits(*reinterpret_cast<const uint16_t*>(k));
     const uint64_t* tg = reinterpret_cast<const uint64_t*>(k + kPackedHdr);
     const RegKeys rk = load_round_keys(k + 32);
-    packed_one(aes, rk.r, ld64(k + 8), k[4], a.xs[e] & m, m,
+    packed_one(aes, rk, ld64(k + 8), k[4], a.xs[e] & m, m,
                a.num_thr, a.out_words, (k[5] & 1u) != 0, e, [&](int i) { return tg[i]; },
                a.out + e * size_t(a.out_words));
   }

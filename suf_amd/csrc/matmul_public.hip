@@ -95,7 +95,13 @@ struct PubArgs {
   TruncEpi epi;      // the open feeds this truncation gate (replaces zhat)
 };
 
-constexpr int kPubAhead = 2;  // k-steps of loads in flight per wave
+// k-steps of loads in flight per wave: two for the 2-digit weights of the
+// layer (10 fragments a step), one for 3- and 4-digit weights, whose second
+// step in flight would not fit beside the 128 accumulator registers.
+template <int J>
+constexpr int pub_ahead() {
+  return J <= 2 ? 2 : 1;
+}
 
 // Workgroup = two waves, wave p computing party p's 32 x 32 tile over one
 // k-slice; grid = (N / 32, M / 32, slices).  MFMA operand layout (checked on
@@ -131,6 +137,7 @@ __global__ void __launch_bounds__(128, 2) public_mfma_kernel(PubArgs a) {
   for (int s = 0; s < kPlanes; ++s)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[s][r] = 0;
+  constexpr int kPubAhead = pub_ahead<J>();
   v4i x[kPubAhead][kPlanes], w[kPubAhead][J];
 #pragma unroll
   for (int q = 0; q < kPubAhead; ++q) {

@@ -77,23 +77,26 @@ class BeaverMatmulTrunc:
         r = int(rnd[0])
         self.rin = (int(rnd[1]), (r - int(rnd[1])) & M64)
         self.keys = pfss.trunc_gen(native.TRUNC_GAPARS, frac_bits, self.prg_state, rnd)
-        self.work_bytes = lib.sufhip_trunc_work_bytes(frac_bits, M * N)
-        self.work = [torch.empty(max(2, (self.work_bytes + 15) // 8), dtype=torch.int64,
-                                 device="cuda") for _ in range(2)]
-        self.side = torch.cuda.Stream()
-        self.D = torch.empty(M * K, dtype=torch.int64, device="cuda")
-        self.E = torch.empty(K * N, dtype=torch.int64, device="cuda")
-        self.Z = [torch.empty(M * N, dtype=torch.int64, device="cuda") for _ in range(2)]
-        self.zhat = torch.empty(M * N, dtype=torch.int64, device="cuda")
-        self.mm_work = None
-        if use_mfma and mfma_ok(M, K, N):
-            wb = lib.sufhip_beaver_matmul2d_mfma_work_bytes(M, K, N)
-            self.mm_work = torch.empty((wb + 7) // 8, dtype=torch.int64, device="cuda")
         # Two-party matrix-core form: both parties' products in one launch with
         # the truncation folded in, the triple shares' digit planes made here.
+        # The launch-per-step form's buffers (u64 opens, products, masked open,
+        # truncation workspaces) exist only when it is the form in use.
         self.fused = (use_mfma and M % 32 == 0 and K % 32 == 0 and N % 32 == 0 and K <= 4096 and
                       frac_bits <= 13)
-        if self.fused:
+        self.mm_work = None
+        if not self.fused:
+            self.work_bytes = lib.sufhip_trunc_work_bytes(frac_bits, M * N)
+            self.work = [torch.empty(max(2, (self.work_bytes + 15) // 8), dtype=torch.int64,
+                                     device="cuda") for _ in range(2)]
+            self.side = torch.cuda.Stream()
+            self.D = torch.empty(M * K, dtype=torch.int64, device="cuda")
+            self.E = torch.empty(K * N, dtype=torch.int64, device="cuda")
+            self.Z = [torch.empty(M * N, dtype=torch.int64, device="cuda") for _ in range(2)]
+            self.zhat = torch.empty(M * N, dtype=torch.int64, device="cuda")
+            if use_mfma and mfma_ok(M, K, N):
+                wb = lib.sufhip_beaver_matmul2d_mfma_work_bytes(M, K, N)
+                self.mm_work = torch.empty((wb + 7) // 8, dtype=torch.int64, device="cuda")
+        else:
             from . import layer, tasks
             self.tr = tasks.Trunc(None, frac_bits, M * N, self.prg_state, rnd=rnd)
             self.Ap = tuple(layer.kb_planes(1, M, K) for _ in range(2))

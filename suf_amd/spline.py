@@ -31,7 +31,8 @@ import numpy as np
 import torch
 
 from . import native, pfss
-from .tasks import AosTriples, Prepared, Trunc, chain2, lin2, mul2x, operand, term
+from .tasks import (AosTriples, Prepared, Trunc, chain2, lin2, mul2x, operand, rotated_lut,
+                    term)
 
 M64 = (1 << 64) - 1
 LUT_TWEAK = 7  # seed_from_id tweak of interval LUT keys (cuda/pfss_backend_gpu.cu:508-515)
@@ -57,50 +58,6 @@ def spline_spec(frac_bits=12, seed=6, coeff_bits=15):
     half = 1 << (coeff_bits - 1)
     c = (w % np.uint64(1 << coeff_bits)).astype(np.int64) - half
     return np.array(alpha, dtype=np.uint64), c.reshape(len(alpha), 4)
-
-
-def spline_eval_ref(alpha, coeffs, x, frac_bits):
-    """Plain fixed-point evaluation of the spline at x (u64 ring values): the
-    closed form of CubicPolyTask's reference path (phase_tasks.hpp:2933-2945)
-    with exact arithmetic shifts, in int64 numpy.  Raises if an intermediate
-    could leave (-2^62, 2^62) for these inputs."""
-    x = np.asarray(x, dtype=np.uint64)
-    piece = np.searchsorted(alpha, x, side="right") - 1
-    c = coeffs[piece]
-    xs = x.view(np.int64)
-    f = frac_bits
-    cx = int(np.abs(coeffs).max())
-    xm = int(np.abs(xs).max()) if xs.size else 0
-    u_max = cx * xm + (cx << f)
-    q_max = ((u_max * xm) >> f) + 1 + (cx << f)
-    if max(u_max * xm, q_max * xm) >= 1 << 62:
-        raise ValueError("spline_eval_ref: inputs outside the exact int64 range")
-    u = c[:, 3] * xs + (c[:, 2] << f)
-    p2 = (u * xs) >> f
-    q = p2 + (c[:, 1] << f)
-    y = ((q * xs) >> (2 * f)) + c[:, 0]
-    return y.view(np.uint64)
-
-
-def rotated_lut(alpha, coeffs, r_in):
-    """Interval LUT geometry over x^ = x + r_in: cutpoints [k + 1] (the last is
-    the 2^64 sentinel 0) and payload [k][4] words (c0..c3)."""
-    ivs = []
-    bounds = [int(a) for a in alpha] + [1 << 64]
-    for i in range(len(alpha)):
-        s = (bounds[i] + r_in) & M64
-        e = (bounds[i + 1] + r_in) & M64
-        pay = [int(v) & M64 for v in coeffs[i]]
-        if s < e:
-            ivs.append((s, e, pay))
-        else:
-            ivs.append((s, 0, pay))
-            if e != 0:
-                ivs.append((0, e, pay))
-    ivs.sort(key=lambda t: t[0])
-    cuts = [ivs[0][0]] + [hi for _, hi, _ in ivs]
-    payload = [w for _, _, pay in ivs for w in pay]
-    return np.array(cuts, dtype=np.uint64), np.array(payload, dtype=np.uint64), len(ivs)
 
 
 def _split(v, s):

@@ -63,6 +63,11 @@ def _load_oracle():
                                       ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, ctypes.c_int64, ctypes.c_int, u64p,
                                       ctypes.c_int]
+    lib.orc_aes_use_ni.argtypes = [ctypes.c_int]
+    lib.orc_set_threads.argtypes = [ctypes.c_int]
+    lib.orc_aes128_encrypt_fast.argtypes = [u8p, u8p, u8p]
+    lib.orc_matmul_public.argtypes = [u64p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, u64p]
     lib.orc_add_rout_aos.argtypes = [u64p, c_sz, ctypes.c_int, u64p, ctypes.c_int]
     lib.orc_open_add.argtypes = [u64p, u64p, ctypes.c_int, u64p, c_sz, ctypes.c_int,
                                  ctypes.c_uint64, ctypes.c_int]
@@ -112,6 +117,45 @@ def aes_encrypt(key: bytes, block: bytes) -> bytes:
     out = np.zeros(16, dtype=np.uint8)
     LIB.orc_aes128_encrypt(ptr(rk), ptr(b), ptr(out))
     return out.tobytes()
+
+
+def aes_encrypt_fast(key: bytes, block: bytes) -> bytes:
+    """The AES-NI path (or the FIPS restatement when it is off)."""
+    rk = aes_expand(key)
+    inp = np.frombuffer(block, dtype=np.uint8).copy()
+    out = np.zeros(16, dtype=np.uint8)
+    LIB.orc_aes128_encrypt_fast(ptr(rk), ptr(inp), ptr(out))
+    return out.tobytes()
+
+
+def aes_use_ni(on):
+    """Selects the oracle's AES: the x86 AES instructions (when the CPU has
+    them) or the FIPS-197 restatement.  Returns the previous setting."""
+    prev = LIB.orc_aes_ni_active()
+    LIB.orc_aes_use_ni(1 if on else 0)
+    return prev
+
+
+def aes_ni_available():
+    return bool(LIB.orc_aes_ni_available())
+
+
+def set_threads(n):
+    """OpenMP threads of the oracle's per-element loops (<= 0: all processors)."""
+    LIB.orc_set_threads(int(n))
+
+
+def get_threads():
+    return int(LIB.orc_get_threads())
+
+
+def matmul_public(X, W, M, K, N):
+    """X [M x K] u64 share times public int64 W [K x N], mod 2^64."""
+    X = np.ascontiguousarray(X, dtype=np.uint64)
+    W = np.ascontiguousarray(W, dtype=np.int64)
+    out = np.empty(M * N, dtype=np.uint64)
+    LIB.orc_matmul_public(ptr(X, u64p), W.ctypes.data, M, K, N, ptr(out, u64p))
+    return out
 
 
 def myl7_key_bytes(in_bits, payload_len):

@@ -364,3 +364,37 @@ def test_kb_open_split_matches_open_then_split(shape):
             (shape, use_b)
     with pytest.raises(native.SufHipError):  # rows not a multiple of 32
         layer.kb_open_split([(a, b, layer.kb_planes(1, 64, 64), 1, 48, 64, 1)])
+    for one_sided in ((b[0], None), (None, b[1])):  # one share of b only
+        arr = (native.KbOpenJob * 1)()
+        arr[0].a[0], arr[0].a[1] = a[0].data_ptr(), a[1].data_ptr()
+        arr[0].b[0] = one_sided[0].data_ptr() if one_sided[0] is not None else None
+        arr[0].b[1] = one_sided[1].data_ptr() if one_sided[1] is not None else None
+        arr[0].planes = layer.kb_planes(nb, r, c).data_ptr()
+        arr[0].batches, arr[0].rows, arr[0].cols, arr[0].k_is_col = nb, r, c, kc
+        with pytest.raises(native.SufHipError, match="both shares of b"):
+            native.call("sufhip_kb_open_split_batch", arr, 1, 0)
+
+
+def test_kb_open_split_two_jobs_mixed():
+    """One launch with two jobs: a column-side open with b (k_is_col 1) and a
+    row-side open without b (k_is_col 0), each equal to its own open + split."""
+    print("[gpu-case] kb_open_split two mixed jobs", flush=True)
+    g = np.random.default_rng(8)
+    specs = [(1, 64, 96, 1, True), (2, 32, 64, 0, False)]
+    jobs, wants = [], []
+    for nb, r, c, kc, use_b in specs:
+        n = nb * r * c
+        a = tuple(dev(g.integers(0, 2**64, n, dtype=np.uint64)) for _ in range(2))
+        b = tuple(dev(g.integers(0, 2**64, n, dtype=np.uint64)) for _ in range(2))
+        opened = a[0] + a[1] - (b[0] + b[1] if use_b else 0)
+        want = layer.kb_planes(nb, r, c)
+        want.fill_(0)
+        layer.kb_split([(opened, want, nb, r, c, kc)])
+        got = layer.kb_planes(nb, r, c)
+        got.fill_(0x5a5a)
+        jobs.append((a, b if use_b else None, got, nb, r, c, kc))
+        wants.append((want, native.load().sufhip_kb_planes_bytes(nb, r, c)))
+    layer.kb_open_split(jobs)
+    torch.cuda.synchronize()
+    for (want, nbytes), job in zip(wants, jobs):
+        assert torch.equal(job[2].view(torch.uint8)[:nbytes], want.view(torch.uint8)[:nbytes])

@@ -7,6 +7,7 @@ import numpy as np
 import pytest
 import torch
 
+import fixed_point as fp
 import oracle_lib as ol
 import twoparty_oracle as tp
 from gpu_util import dev, host, say, u64
@@ -49,7 +50,7 @@ def test_shares_match_oracle_pipeline(n, seed, fused):
     o = _oracle_pipeline(gate, x0, x1)
     assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
     rec = (g[0] + g[1]).astype(np.uint64)
-    assert np.array_equal(rec, spline.spline_eval_ref(alpha, coeffs, x, F))
+    assert np.array_equal(rec, fp.spline_closed_form(alpha, coeffs, x, F))
 
 
 def test_full_size_reconstructs_twice():
@@ -61,7 +62,7 @@ def test_full_size_reconstructs_twice():
     gate = spline.SplineGate(n, alpha, coeffs, STATE, F, seed=7)
     xd = [dev(x0), dev(x1)]
     out = [torch.empty(n, dtype=torch.int64, device="cuda") for _ in range(2)]
-    want = spline.spline_eval_ref(alpha, coeffs, x, F)
+    want = fp.spline_closed_form(alpha, coeffs, x, F)
     for _ in range(2):  # the gate's scratch is reused across calls
         gate.eval2(xd, out)
         rec = (u64(out[0]) + u64(out[1])).astype(np.uint64)

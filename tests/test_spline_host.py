@@ -9,6 +9,7 @@ import tempfile
 import numpy as np
 import pytest
 
+import fixed_point as fp
 import oracle_lib as ol
 from suf_amd import native, spline
 
@@ -45,12 +46,12 @@ def test_rotated_lut_selects_the_piece(r_in):
     assert np.array_equal(rec.reshape(-1, 4), coeffs[piece].view(np.uint64))
 
 
-def test_spline_eval_ref_matches_python_ints():
+def test_spline_closed_form_matches_python_ints():
     alpha, coeffs = spline.spline_spec(F, seed=6)
     rng = np.random.default_rng(2)
     x = np.array([int(v) & spline.M64 for v in rng.integers(-(8 << F), 8 << F, 300)],
                  dtype=np.uint64)
-    got = spline.spline_eval_ref(alpha, coeffs, x, F)
+    got = fp.spline_closed_form(alpha, coeffs, x, F)
     for xi, gi in zip(x, got):
         xs = int(xi) - (1 << 64) if int(xi) >> 63 else int(xi)
         piece = int(np.searchsorted(alpha, xi, side="right")) - 1
