@@ -271,12 +271,14 @@ class AttentionCore:
     def truncs(self):
         return self.tr_s + [self.tr_c] + self.softmax.truncs()
 
-    def eval2(self, qkv, out, prep=None, fused=True, planes=None):
+    def eval2(self, qkv, out, prep=None, fused=True, planes=None, sm_marks=None):
         """prep: (tasks.Prepared, batch) holding the key-only halves of
         truncs(), or None to issue them here.  fused: scores, softmax and the
         next open in one launch (sufhip_softmax2); else launch by launch.
         planes = (buffer, cols): the context also as the output projection's
-        digit planes (matrix-core products only)."""
+        digit planes (matrix-core products only).  sm_marks: optional list
+        that receives two timing events around the one-launch softmax block
+        (eager profiling)."""
         seq, d, h, dh, mp = self.seq, self.d, self.heads, self.dh, self.maps
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
@@ -303,8 +305,14 @@ class AttentionCore:
             # P - A over the dense [heads][seq][seq] layout (also as PV's
             # digit planes on the matrix cores).
             dp = (self.tri_pv.Dp, h, seq, seq, 1) if self.mfma() else None
+            if sm_marks is not None:
+                sm_marks.append(torch.cuda.Event(enable_timing=True))
+                sm_marks[-1].record()
             self.softmax.eval_block(scaled, pre=self.tr_s,
                                     dense=(self.D2, self.tri_pv.A, seq, dp))
+            if sm_marks is not None:
+                sm_marks.append(torch.cuda.Event(enable_timing=True))
+                sm_marks[-1].record()
         else:
             lin2(scaled, self.n, into=(self.tr_s[0], self.sa))
             lin2(operand(term(self.sa)), self.n, into=(self.tr_s[1], self.scores))
@@ -381,14 +389,14 @@ class TransformerLayer:
                 self.proj.truncs() + self.ln2.truncs() + self.w1.truncs() + self.gelu.truncs() +
                 self.w2.truncs()]
 
-    def eval2(self, x, out, marks=None, overlap_prepare=False):
+    def eval2(self, x, out, marks=None, overlap_prepare=False, sm_marks=None):
         """x, out: pairs of int64 [seq * d] device tensors.  marks: optional
         list of torch events recorded after each stage (profiling).  The
         key-only halves of all truncation gates run first, in one batched
         walk on the current stream; with overlap_prepare they run on a side
         stream instead, in three batches, each ahead of the stage that needs
         it (a fork or join between streams costs about as much as it
-        hides)."""
+        hides).  sm_marks: see AttentionCore.eval2."""
         if overlap_prepare:
             prep = Prepared(self.side, self.stage_truncs(), upfront=2)
             b = lambda k: k  # noqa: E731
@@ -418,12 +426,13 @@ class TransformerLayer:
         prep.release()  # the second half's gates, after the QKV product
         mark()
         if self.attn.mfma():
-            self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)), planes=self.proj.x_planes())
+            self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)), planes=self.proj.x_planes(),
+                            sm_marks=sm_marks)
             mark()
             prep.wait(b(2))
             self.proj.eval2(None, self.r1, add=x)  # r1 = trunc(ctx Wout) + x
         else:
-            self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)))
+            self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)), sm_marks=sm_marks)
             mark()
             prep.wait(b(2))
             self.proj.eval2(self.ctx, self.r1, add=x)

@@ -107,7 +107,9 @@ class BeaverMatmulTrunc:
 
     def eval2(self, X, W, out, events=None):
         """X, W, out: pairs of device int64 tensors (party shares).  events:
-        optional list of 2 torch events recorded around the matmul."""
+        optional list of 2 torch events recorded around the matmul, or of 3
+        in the fused form: before the opens, between the opens and the
+        product, after the product."""
         M, K, N, s = self.M, self.K, self.N, _stream()
         if self.fused:
             return self._eval2_fused(X, W, out, events)
@@ -153,6 +155,8 @@ class BeaverMatmulTrunc:
         if events:
             events[0].record()
         layer.kb_open_split([(X, self.A, self.Dp, 1, M, K, 1), (W, self.B, self.Ep, 1, K, N, 0)])
+        if events and len(events) > 2:
+            events[1].record()
         a = native.BeaverMfma2Args()
         a.Dp, a.Ep = _p(self.Dp), _p(self.Ep)
         for p in (0, 1):
@@ -163,5 +167,5 @@ class BeaverMatmulTrunc:
         a.mask = self.tr.mask & M64
         native.call("sufhip_beaver_matmul2_mfma_ex", native.ctypes.byref(a), _stream())
         if events:
-            events[1].record()
+            events[-1].record()
         return out

@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "suf_hip.h"
+#include "suf_hip/cuda_primitives.hpp"
 #include "suf_hip/hip_pfss_backend.hpp"
 
 using suf_hip::HipPfssBackend;
@@ -199,6 +200,72 @@ static void test_errors() {
   CHECK(threw, "eval on a malformed key must throw");
 }
 
+// SUF's launchers by their reference names (include/suf_hip/cuda_primitives.hpp
+// over the C ABI): a Beaver product and ragged row sums reconstruct their
+// closed forms, and a launch the C ABI rejects throws.
+static void test_launcher_shim() {
+  const size_t n = 1000;
+  std::mt19937_64 rng(5);
+  std::vector<uint64_t> x(n), y(n), a0(n), a1(n), b0(n), b1(n), c0(n), c1(n), d(n), e(n);
+  for (size_t i = 0; i < n; ++i) {
+    x[i] = rng(), y[i] = rng();
+    const uint64_t a = rng(), b = rng();
+    a0[i] = rng(), b0[i] = rng(), c0[i] = rng();
+    a1[i] = a - a0[i], b1[i] = b - b0[i], c1[i] = a * b - c0[i];
+    d[i] = x[i] - a, e[i] = y[i] - b;
+  }
+  auto up = [](const std::vector<uint64_t>& v) {
+    void* p = nullptr;
+    if (sufhip_malloc(&p, v.size() * 8) || sufhip_memcpy_h2d(p, v.data(), v.size() * 8, nullptr))
+      throw std::runtime_error("upload failed");
+    return static_cast<uint64_t*>(p);
+  };
+  uint64_t *dx = up(x), *dy = up(y), *dd = up(d), *de = up(e);
+  uint64_t* da[2] = {up(a0), up(a1)};
+  uint64_t* db[2] = {up(b0), up(b1)};
+  uint64_t* dc[2] = {up(c0), up(c1)};
+  uint64_t* dz[2] = {up(x), up(x)};
+  for (int p = 0; p < 2; ++p)
+    launch_beaver_mul_kernel(p, dx, dy, da[p], db[p], dc[p], dd, de, dz[p], n, nullptr);
+  std::vector<uint64_t> z0(n), z1(n);
+  sufhip_memcpy_d2h(z0.data(), dz[0], n * 8, nullptr);
+  sufhip_memcpy_d2h(z1.data(), dz[1], n * 8, nullptr);
+  sufhip_stream_synchronize(nullptr);
+  for (size_t i = 0; i < n; ++i) CHECK(z0[i] + z1[i] == x[i] * y[i], "launcher Beaver product at %zu", i);
+  // Ragged rows of lengths 1..40 packed back to back.
+  std::vector<int> offs{0};
+  for (int r = 1; r <= 40; ++r) offs.push_back(offs.back() + r);
+  std::vector<uint64_t> vals(offs.back());
+  for (auto& v : vals) v = rng();
+  void* doffs = nullptr;
+  sufhip_malloc(&doffs, offs.size() * sizeof(int));
+  sufhip_memcpy_h2d(doffs, offs.data(), offs.size() * sizeof(int), nullptr);
+  uint64_t* dvals = up(vals);
+  uint64_t* dsum = up(std::vector<uint64_t>(40));
+  launch_row_sum_ragged_kernel(dvals, static_cast<const int*>(doffs), 40, dsum, nullptr);
+  std::vector<uint64_t> sums(40);
+  sufhip_memcpy_d2h(sums.data(), dsum, 40 * 8, nullptr);
+  sufhip_stream_synchronize(nullptr);
+  for (int r = 0; r < 40; ++r) {
+    uint64_t want = 0;
+    for (int j = offs[r]; j < offs[r + 1]; ++j) want += vals[j];
+    CHECK(sums[r] == want, "launcher ragged row sum %d", r);
+  }
+  bool threw = false;
+  try {
+    launch_pack_eff_bits_kernel(dx, 65, dz[0], n, nullptr);  // eff_bits out of range
+  } catch (const std::runtime_error&) {
+    threw = true;
+  }
+  CHECK(threw, "a launch the C ABI rejects must throw");
+  for (void* p : {static_cast<void*>(dx), static_cast<void*>(dy), static_cast<void*>(dd),
+                  static_cast<void*>(de), static_cast<void*>(da[0]), static_cast<void*>(da[1]),
+                  static_cast<void*>(db[0]), static_cast<void*>(db[1]), static_cast<void*>(dc[0]),
+                  static_cast<void*>(dc[1]), static_cast<void*>(dz[0]), static_cast<void*>(dz[1]),
+                  doffs, static_cast<void*>(dvals), static_cast<void*>(dsum)})
+    sufhip_free(p);
+}
+
 static void test_factory() {
   setenv("SUF_PFSS_BACKEND", "HIP", 1);
   auto be = suf_hip::make_hip_backend_from_env();
@@ -223,6 +290,7 @@ int main() {
     test_lut();
     test_packed();
     test_errors();
+    test_launcher_shim();
     test_factory();
   } catch (const std::exception& e) {
     std::fprintf(stderr, "exception: %s\n", e.what());

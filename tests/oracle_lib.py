@@ -365,7 +365,7 @@ def open_add(local, remote, eff_bits, n, ring_bits, ring_mask, sign_extend):
 
 
 def beaver_matmul(party, D, E, A, B, C, batches, M, K, N, w_t=0, has_scale=0, mul_const=0,
-                  mul_shift=0, threads=8):
+                  mul_shift=0, threads=0):
     out = np.zeros(batches * M * N, dtype=np.uint64)
     LIB.orc_beaver_matmul(party, *(ptr(_u64(v), u64p) for v in (D, E, A, B, C)), batches, M, K, N,
                           w_t, has_scale, mul_const, mul_shift, ptr(out, u64p), threads)

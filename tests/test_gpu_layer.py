@@ -309,6 +309,31 @@ def test_layer_config_shape_twice():
         assert np.array_equal(rec, want.view(np.uint64))
 
 
+@pytest.mark.parametrize("seq,d,heads,ffn", [(32, 64, 2, 128), (128, 768, 12, 3072)])
+def test_layer_shares_equal_twoparty_oracle(seq, d, heads, ffn):
+    """Both parties' shares of every stage and of the output equal the
+    oracle's two-party composition of the same protocol steps (LayerNorm,
+    public products with their truncation gates, per-head Beaver products,
+    the softmax block, GeLU) on the same dealer material."""
+    import twoparty_oracle as tp
+
+    W, x = _layer_case(seq, d, heads, ffn, 31)
+    x0, x1 = _pair(x, 32)
+    say("transformer layer shares vs two-party oracle seq=%d d=%d heads=%d ffn=%d"
+        % (seq, d, heads, ffn))
+    ly = layer.TransformerLayer(STATE, W, seq, d, heads, ffn, F, seed=33, keep_intermediates=True)
+    out = tuple(torch.empty(seq * d, dtype=torch.int64, device="cuda") for _ in range(2))
+    ly.eval2((dev(x0), dev(x1)), out)
+    torch.cuda.synchronize()
+    want, st = tp.layer2(ol.Prg(STATE), ly, (x0, x1))
+    for name, t in (("h1", ly.h1), ("qkv", ly.qkvs), ("ctx", ly.ctx), ("r1", ly.r1),
+                    ("h2", ly.h2), ("u", ly.u), ("g", ly.g)):
+        for p in (0, 1):
+            assert np.array_equal(u64(t[p]), st[name][p]), (name, p)
+    for p in (0, 1):
+        assert np.array_equal(u64(out[p]), want[p]), p
+
+
 def test_plane_outputs_reject_bad_layouts():
     """The digit-plane outputs and inputs are checked on the host: a plane
     layout that does not cover the open, a head-merged plane output without

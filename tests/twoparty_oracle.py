@@ -177,3 +177,74 @@ def layernorm2(prg, ln, x):
     v = const2(var, ln.eps_q)
     rs = rsqrt2(prg, ln.rsqrt, v, open2(v, ln.rsqrt.lut.mask))
     return beaver_trunc2(prg, diff, rs, ln.tri_norm, ln.tr_norm, row_of=row)
+
+
+def public_trunc2(prg, pm, x, add=None):
+    """layer.PublicMatmulTrunc: trunc_f(X_p W) for both parties (the masked
+    open Y_0 + Y_1 + r into the gate), plus the pair `add` (a residual)."""
+    M, K, N = pm.M, pm.K, pm.N
+    y = [ol.matmul_public(u(x[p]), pm.W, M, K, N) for p in (0, 1)]
+    out = trunc2(prg, pm.tr, open2(y, pm.tr.mask))
+    return out if add is None else add2(out, add)
+
+
+def _batched_beaver2(tri, D, E):
+    """Both parties' products C_p + D B_p + A_p E (+ D E, party 0) per batch
+    of a layer.BatchedTriples, for the opens D [b][M x K], E [b][K x N]."""
+    b, M, K, N = tri.shape
+    A, B, C, A0, B0, C0 = tri.host
+    sh = [(A0, B0, C0), ((A - A0).astype(np.uint64), (B - B0).astype(np.uint64),
+                         (C - C0).astype(np.uint64))]
+    D = u(D).reshape(b, M * K)
+    E = u(E).reshape(b, K * N)
+    out = []
+    for p in (0, 1):
+        a, bb, c = (np.ascontiguousarray(v, dtype=np.uint64).reshape(b, -1) for v in sh[p])
+        z = np.empty((b, M * N), dtype=np.uint64)
+        for h in range(b):
+            z[h] = ol.beaver_matmul(p, D[h], E[h], a[h], bb[h], c[h], 1, M, K, N, threads=0)
+        out.append(z.ravel())
+    return out
+
+
+def attention2(prg, at, qkv):
+    """layer.AttentionCore on the QKV shares [seq x 3d]: the context shares
+    [seq x d], and the stages."""
+    mp = {k: host(v).astype(np.int64) for k, v in at.maps.items()}
+    q = [u(qkv[p])[mp["gq"]] for p in (0, 1)]
+    k = [u(qkv[p])[mp["gk"]] for p in (0, 1)]
+    v = [u(qkv[p])[mp["gv"]] for p in (0, 1)]
+    A_qk = at.tri_qk.host[3], (at.tri_qk.host[0] - at.tri_qk.host[3]).astype(np.uint64)
+    B_qk = at.tri_qk.host[4], (at.tri_qk.host[1] - at.tri_qk.host[4]).astype(np.uint64)
+    A_pv = at.tri_pv.host[3], (at.tri_pv.host[0] - at.tri_pv.host[3]).astype(np.uint64)
+    B_pv = at.tri_pv.host[4], (at.tri_pv.host[1] - at.tri_pv.host[4]).astype(np.uint64)
+    D = ((q[0] - A_qk[0].ravel()) + (q[1] - A_qk[1].ravel())).astype(np.uint64)
+    E = ((k[0] - B_qk[0].ravel()) + (k[1] - B_qk[1].ravel())).astype(np.uint64)
+    E2 = ((v[0] - B_pv[0].ravel()) + (v[1] - B_pv[1].ravel())).astype(np.uint64)
+    S = _batched_beaver2(at.tri_qk, D, E)
+    sc = [(S[p][mp["gs"]] * np.uint64(at.inv_sqrt)).astype(np.uint64) for p in (0, 1)]
+    sa = trunc2(prg, at.tr_s[0], open2(sc, at.tr_s[0].mask))
+    scores = trunc2(prg, at.tr_s[1], open2(sa, at.tr_s[1].mask))
+    prob, _ = softmax2(prg, at.softmax, scores)
+    pz = [np.concatenate([prob[p], np.zeros(1, np.uint64)]) for p in (0, 1)]
+    pd = [pz[p][mp["gp"]] for p in (0, 1)]
+    D2 = ((pd[0] - A_pv[0].ravel()) + (pd[1] - A_pv[1].ravel())).astype(np.uint64)
+    Z = _batched_beaver2(at.tri_pv, D2, E2)
+    zc = [Z[p][mp["gc"]] for p in (0, 1)]
+    ctx = trunc2(prg, at.tr_c, open2(zc, at.tr_c.mask))
+    return ctx, {"scores": scores, "prob": prob}
+
+
+def layer2(prg, ly, x):
+    """layer.TransformerLayer on the input shares x [seq x d]: the output
+    shares and the stages, in the order the layer runs its protocol steps."""
+    h1 = layernorm2(prg, ly.ln1, x)
+    qkv = public_trunc2(prg, ly.qkv, h1)
+    ctx, st = attention2(prg, ly.attn, qkv)
+    r1 = public_trunc2(prg, ly.proj, ctx, add=x)
+    h2 = layernorm2(prg, ly.ln2, r1)
+    uu = public_trunc2(prg, ly.w1, h2)
+    g = spline2(prg, ly.gelu, uu)
+    out = public_trunc2(prg, ly.w2, g, add=r1)
+    st.update({"h1": h1, "qkv": qkv, "ctx": ctx, "r1": r1, "h2": h2, "u": uu, "g": g})
+    return out, st
