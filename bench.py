@@ -29,7 +29,7 @@ HBM_PEAK_GBPS = 8000.0
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch) and scaled by the
 # counters' reading for a 256 MiB device copy (FETCH x2.0, WRITE x1.0); the
 # commands and raw values are in profiles/dcf_eval_bit_kernel__dcf_batch_n2p20.md.
-MEASURED_TRAFFIC_BYTES = 1256045.2 * 1024 * 2.0 + 1233.0 * 1024 * 1.0
+MEASURED_TRAFFIC_BYTES = 1255360.3 * 1024 * 2.0 + 1230.1 * 1024 * 1.0
 # Instructions per dcf_eval_bit_kernel launch at N = 2^20 (rocprofv3 --pmc
 # SQ_INSTS_VALU SQ_INSTS_LDS, same profile file): fixed by the compiled kernel
 # and N, so lane-ops per second follow from the measured launch time.
