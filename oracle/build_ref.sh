@@ -1,7 +1,9 @@
 #!/bin/sh
 # Builds the reference's myl7/fss v0.7.1 DCF (vendored in the reference tree
 # at third_party/myl7_fss, source files used unmodified and in place) into
-# oracle/_ref/, one library per output group, plus oracle/ref_shim.cpp.
+# oracle/_ref/, one library per output group, plus oracle/ref_shim.cpp, and
+# the gate-table dump driver oracle/ref_tables.cpp over the reference's
+# header-only table builders.
 # Compile definitions follow the reference's myl7_core target
 # (CMakeLists.txt:84-93): kBlocks=8, kLambda=16, OpenSSL libcrypto, OpenMP.
 # Outputs go only to oracle/_ref/ (git-ignored).  Without the reference tree
@@ -26,4 +28,8 @@ for grp in bytes u128_le; do
     "$OUT/obj/group_$grp.o" "$OUT/obj/ref_shim.o" -lcrypto
   mv "$OUT/libmyl7ref_$grp.so.tmp" "$OUT/libmyl7ref_$grp.so"
 done
-echo "build_ref: built $OUT/libmyl7ref_bytes.so $OUT/libmyl7ref_u128_le.so"
+# The gate-table dump driver (tests/golden/make_tables.py runs it): the
+# reference's header-only table and SUF builders, included in place.
+g++ -std=c++17 -O1 -I"$REF/include" "$HERE/ref_tables.cpp" -o "$OUT/ref_tables.tmp"
+mv "$OUT/ref_tables.tmp" "$OUT/ref_tables"
+echo "build_ref: built $OUT/libmyl7ref_bytes.so $OUT/libmyl7ref_u128_le.so $OUT/ref_tables"
