@@ -835,6 +835,79 @@ int sufhip_unpack_add_mod(const uint64_t* d_local_share, const uint64_t* d_packe
                           uint64_t ring_mask, void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* Composite gates with boolean outputs (SUF l_out > 0), both parties on one */
+/* GPU: the selector network and boolean-DAG Beaver evaluation of            */
+/* composite_eval_batch_backend (include/gates/composite_fss.hpp:2132-2456,  */
+/* selectors_from_cutbits_block :893-974, eval_bool_xor_view                 */
+/* include/gates/bool_dag_xor.hpp:13-104), and the bucket staging of x^      */
+/* that PfssSuperBatch::flush_eval does (src/runtime/pfss_superbatch.cpp:    */
+/* 740-930).                                                                 */
+/* ---------------------------------------------------------------------- */
+
+/* One job's masked inputs in a bucket: len values from src (device; plain
+ * u64 when eff_bits == 64, else an LSB-first bitstream of eff_bits-wide
+ * values in u64 words, the pack_eff_bits layout) to bucket[dst, dst + len). */
+#define SUFHIP_STAGE_MAX_SEGS 64
+typedef struct sufhip_stage_seg {
+  const void* src;
+  size_t len;
+  size_t dst;
+  int eff_bits;
+} sufhip_stage_seg;
+/* All of a bucket's segments in one launch (segments may not overlap). */
+int sufhip_stage_hatx(const sufhip_stage_seg* segs, int count, uint64_t* d_bucket,
+                      size_t bucket_len, void* stream);
+
+/* Boolean program instructions (int32: opcode in bits 0-3, operand above),
+ * postfix over XOR-shared bits: VAR pushes predicate query q's bit, WRAP
+ * the low bit of wrap bit w's additive share, CONST a constant (party 0's
+ * share); NOT, XOR, AND, OR pop their operands (AND and OR take one bit
+ * triple each, in program order). */
+#define SUFHIP_BOOL_VAR 0
+#define SUFHIP_BOOL_WRAP 1
+#define SUFHIP_BOOL_CONST 2
+#define SUFHIP_BOOL_NOT 3
+#define SUFHIP_BOOL_XOR 4
+#define SUFHIP_BOOL_AND 5
+#define SUFHIP_BOOL_OR 6
+#define SUFHIP_BOOL_MAX_STACK 16
+#define SUFHIP_COMPOSITE_MAX_ELL 8
+#define SUFHIP_COMPOSITE_MAX_CUTS 31
+#define SUFHIP_COMPOSITE_MAX_WRAP 32
+#define SUFHIP_COMPOSITE_MAX_PROG 384
+
+/* The x^-domain segments of the gate are delimited by `cuts` cut points; cut
+ * bit k of element i is 1[xhat_i < cut_k] (XOR-shared bytes, bit 0).
+ * Segment s's output j is program k = s ell + j: instructions
+ * prog[prog_off[k], prog_off[k + 1]).  Triples (additive u64, [T][3][n] per
+ * party: a, b, c) are consumed by index: cut k's b2a at k; the chain product
+ * of selector s (1 <= s < cuts) at cuts + s - 1; output bit (s, j)'s b2a at
+ * B + k and its selector product at B + (cuts + 1) ell + k, B = max(0,
+ * 2 cuts - 1); T = sufhip_composite_bool_triples(cuts, ell).  Bit triples
+ * ([and_count][n] bytes per party, bit 0 a, bit 1 b, bit 2 c = a AND b over
+ * both parties' XOR shares) in program order.  out[p]: [n][ell] additive
+ * shares of the boolean outputs. */
+typedef struct sufhip_composite_bool_args {
+  size_t n;
+  int queries;
+  int cuts;
+  int ell;
+  int wraps;
+  int and_count;
+  int prog_len;
+  const uint8_t* pred[2];    /* [queries][n] */
+  const uint8_t* cut[2];     /* [cuts][n] */
+  const uint8_t* bit_tri[2]; /* [and_count][n] */
+  const uint64_t* tri[2];    /* [T][3][n] */
+  uint64_t* out[2];          /* [n][ell] */
+  uint64_t wrap[2][SUFHIP_COMPOSITE_MAX_WRAP];
+  int16_t prog_off[(SUFHIP_COMPOSITE_MAX_CUTS + 1) * SUFHIP_COMPOSITE_MAX_ELL + 1];
+  int32_t prog[SUFHIP_COMPOSITE_MAX_PROG];
+} sufhip_composite_bool_args;
+size_t sufhip_composite_bool_triples(int cuts, int ell);
+int sufhip_composite_bool2(const sufhip_composite_bool_args* args, void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* Host-side helpers for seeded synthetic inputs                            */
 /* ---------------------------------------------------------------------- */
 /* out[i] = the i-th output of std::mt19937_64(seed). */

@@ -196,6 +196,8 @@ void orc_set_threads(int n) {
 #endif
 }
 
+int orc_threads_or_default(int n) { return n > 0 ? n : orc_get_threads(); }
+
 int orc_get_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

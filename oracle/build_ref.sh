@@ -3,7 +3,8 @@
 # at third_party/myl7_fss, source files used unmodified and in place) into
 # oracle/_ref/, one library per output group, plus oracle/ref_shim.cpp, and
 # the gate-table dump driver oracle/ref_tables.cpp over the reference's
-# header-only table builders.
+# header-only table builders, and oracle/ref_suf_eval.cpp over its
+# header-only eval_suf_ref.
 # Compile definitions follow the reference's myl7_core target
 # (CMakeLists.txt:84-93): kBlocks=8, kLambda=16, OpenSSL libcrypto, OpenMP.
 # Outputs go only to oracle/_ref/ (git-ignored).  Without the reference tree
@@ -32,4 +33,7 @@ done
 # reference's header-only table and SUF builders, included in place.
 g++ -std=c++17 -O1 -I"$REF/include" "$HERE/ref_tables.cpp" -o "$OUT/ref_tables.tmp"
 mv "$OUT/ref_tables.tmp" "$OUT/ref_tables"
-echo "build_ref: built $OUT/libmyl7ref_bytes.so $OUT/libmyl7ref_u128_le.so $OUT/ref_tables"
+# The SUF reference-evaluation driver (tests/golden/make_suf_ref.py runs it).
+g++ -std=c++17 -O1 -I"$REF/include" "$HERE/ref_suf_eval.cpp" -o "$OUT/ref_suf_eval.tmp"
+mv "$OUT/ref_suf_eval.tmp" "$OUT/ref_suf_eval"
+echo "build_ref: built $OUT/libmyl7ref_bytes.so $OUT/libmyl7ref_u128_le.so $OUT/ref_tables $OUT/ref_suf_eval"

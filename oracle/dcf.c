@@ -244,7 +244,7 @@ int orc_myl7_eval_many_bit(const orc_prg_state* p, int group, int in_bits, size_
                            uint8_t* out, int threads) {
   int bad = 0;
   (void)threads;
-#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1) reduction(| : bad)
+#pragma omp parallel for schedule(static) num_threads(orc_threads_or_default(threads)) reduction(| : bad)
   for (long i = 0; i < (long)n; i++) {
     uint8_t buf[4096];
     const uint8_t* k = keys + (size_t)i * key_bytes;

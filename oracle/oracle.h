@@ -49,6 +49,8 @@ int orc_mmo_fast(const uint8_t (*rk)[176], int nb, const uint8_t seed[16], uint8
 /* OpenMP threads of the per-element loops (n <= 0: all processors). */
 void orc_set_threads(int n);
 int orc_get_threads(void);
+/* n when positive, else the current OpenMP default. */
+int orc_threads_or_default(int n);
 /* CTR block i = AES(le64(ctr_lo + i) || le64(ctr_hi)); out is [blocks][16]. */
 void orc_aes128_ctr(const uint8_t rk[176], uint64_t ctr_lo, uint64_t ctr_hi,
                     size_t blocks, uint8_t* out);

@@ -147,7 +147,7 @@ void orc_beaver_matmul(int party, const uint64_t* D, const uint64_t* E, const ui
                        int mul_shift, uint64_t* out, int threads) {
   (void)threads;
   size_t MK = (size_t)M * K, KN = (size_t)K * N, MN = (size_t)M * N;
-#pragma omp parallel for collapse(2) schedule(static) num_threads(threads > 0 ? threads : 1)
+#pragma omp parallel for collapse(2) schedule(static) num_threads(orc_threads_or_default(threads))
   for (int b = 0; b < batches; b++)
     for (int m = 0; m < M; m++)
       for (int n = 0; n < N; n++) {

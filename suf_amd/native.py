@@ -70,6 +70,9 @@ _SIGS = {
     "sufhip_trunc_noalloc_max_work_bytes": (c_sz, []),
     "sufhip_trunc_eval_noalloc": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp]),
     "sufhip_trunc_prepare": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_sz, c_vp, c_sz, c_vp]),
+    "sufhip_stage_hatx": (c_int, [c_vp, c_int, c_vp, c_sz, c_vp]),
+    "sufhip_composite_bool_triples": (c_sz, [c_int, c_int]),
+    "sufhip_composite_bool2": (c_int, [c_vp, c_vp]),
     "sufhip_trunc_finish": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp, c_sz,
                                     c_vp]),
     "sufhip_beaver_matmul2d_mfma_work_bytes": (c_sz, [c_int, c_int, c_int]),
@@ -270,6 +273,29 @@ class TruncJob(ctypes.Structure):
     """sufhip_trunc_job (include/suf_hip.h)."""
     _fields_ = [("kind", c_int), ("frac_bits", c_int), ("d_key", c_vp), ("key_bytes", c_sz),
                 ("n", c_sz), ("d_work", c_vp), ("work_bytes", c_sz)]
+
+
+BOOL_VAR, BOOL_WRAP, BOOL_CONST, BOOL_NOT, BOOL_XOR, BOOL_AND, BOOL_OR = range(7)
+COMPOSITE_MAX_ELL = 8
+COMPOSITE_MAX_CUTS = 31
+COMPOSITE_MAX_WRAP = 32
+COMPOSITE_MAX_PROG = 384
+STAGE_MAX_SEGS = 64
+
+
+class StageSeg(ctypes.Structure):
+    """sufhip_stage_seg (include/suf_hip.h)."""
+    _fields_ = [("src", c_vp), ("len", c_sz), ("dst", c_sz), ("eff_bits", c_int)]
+
+
+class CompositeBoolArgs(ctypes.Structure):
+    """sufhip_composite_bool_args (include/suf_hip.h)."""
+    _fields_ = [("n", c_sz), ("queries", c_int), ("cuts", c_int), ("ell", c_int),
+                ("wraps", c_int), ("and_count", c_int), ("prog_len", c_int),
+                ("pred", c_vp * 2), ("cut", c_vp * 2), ("bit_tri", c_vp * 2), ("tri", c_vp * 2),
+                ("out", c_vp * 2), ("wrap", (c_u64 * COMPOSITE_MAX_WRAP) * 2),
+                ("prog_off", ctypes.c_int16 * ((COMPOSITE_MAX_CUTS + 1) * COMPOSITE_MAX_ELL + 1)),
+                ("prog", ctypes.c_int32 * COMPOSITE_MAX_PROG)]
 
 
 class SufHipError(RuntimeError):

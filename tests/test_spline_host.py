@@ -84,3 +84,28 @@ int main(void) {
     assert want.pop("size") == ctypes.sizeof(native.Mul2Args)
     for name, off in want.items():
         assert getattr(native.Mul2Args, name).offset == off, name
+
+
+def _c_offsets(struct, fields):
+    src = "#include <stdio.h>\n#include <stddef.h>\n#include \"suf_hip.h\"\nint main(void) {\n"
+    src += '  printf("size %%zu\\n", sizeof(%s));\n' % struct
+    for f in fields:
+        src += '  printf("%s %%zu\\n", offsetof(%s, %s));\n' % (f, struct, f)
+    src += "  return 0;\n}\n"
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "l.c")
+        exe = os.path.join(d, "l")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-I" + os.path.join(ol.ROOT, "include"), c, "-o", exe], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    return dict((l.split()[0], int(l.split()[1])) for l in out.splitlines())
+
+
+@pytest.mark.parametrize("struct,cls", [("sufhip_composite_bool_args", "CompositeBoolArgs"),
+                                        ("sufhip_stage_seg", "StageSeg")])
+def test_composite_struct_layouts_match_c(struct, cls):
+    k = getattr(native, cls)
+    want = _c_offsets(struct, [f[0] for f in k._fields_])
+    assert want.pop("size") == ctypes.sizeof(k)
+    for name, off in want.items():
+        assert getattr(k, name).offset == off, name

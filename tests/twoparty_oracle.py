@@ -248,3 +248,88 @@ def layer2(prg, ly, x):
     out = public_trunc2(prg, ly.w2, g, add=r1)
     st.update({"h1": h1, "qkv": qkv, "ctx": ctx, "r1": r1, "h2": h2, "u": uu, "g": g})
     return out, st
+
+
+def composite_bool2(g, pred, cut):
+    """Both parties' [n][l] additive boolean outputs of a
+    composite.CompositeGate from the XOR-shared bits pred[p] ([Q][n] uint8)
+    and cut[p] ([C][n]): b2a of the cut bits and the one-hot selectors
+    (selectors_from_cutbits_block, include/gates/composite_fss.hpp:893-974),
+    each segment's boolean programs over XOR shares (eval_bool_xor_view,
+    include/gates/bool_dag_xor.hpp:13-104, with a constant held by party 0),
+    b2a of the output bits and the selector-weighted sum
+    (composite_fss.hpp:2132-2200), every product on the gate's triple of its
+    index."""
+    n, C, ell = g.n, len(g.cuts), g.ell
+    S = C + 1
+    tri = [host(g.tri[p]).view(np.uint64).reshape(g.T, 3, n) for p in (0, 1)]
+    bt = [host(g.bit_tri[p]).reshape(g.and_count, n) if g.and_count else None for p in (0, 1)]
+    one, zero = np.ones(n, np.uint64), np.zeros(n, np.uint64)
+
+    def mul(t, x, y):
+        a = [tri[p][t, 0] for p in (0, 1)]
+        b = [tri[p][t, 1] for p in (0, 1)]
+        c = [tri[p][t, 2] for p in (0, 1)]
+        d = ((u(x[0]) - a[0]) + (u(x[1]) - a[1])).astype(np.uint64)
+        e = ((u(y[0]) - b[0]) + (u(y[1]) - b[1])).astype(np.uint64)
+        return [(c[0] + d * b[0] + e * a[0] + d * e).astype(np.uint64),
+                (c[1] + d * b[1] + e * a[1]).astype(np.uint64)]
+
+    def b2a(t, b0, b1):
+        b0, b1 = u(b0 & 1), u(b1 & 1)
+        z = mul(t, [b0, zero], [zero, b1])
+        return [(b0 - np.uint64(2) * z[0]).astype(np.uint64),
+                (b1 - np.uint64(2) * z[1]).astype(np.uint64)]
+
+    cut_add = [b2a(k, cut[0][k].astype(np.uint64), cut[1][k].astype(np.uint64))
+               for k in range(C)]
+    B = max(0, 2 * C - 1)
+    and_idx = 0
+    out = [np.zeros((n, ell), np.uint64), np.zeros((n, ell), np.uint64)]
+    for s in range(S):
+        if C == 0:
+            sel = [one, zero]
+        elif s == 0:
+            sel = cut_add[0]
+        elif s == C:
+            sel = [(one - cut_add[C - 1][0]).astype(np.uint64),
+                   (zero - cut_add[C - 1][1]).astype(np.uint64)]
+        else:
+            sel = mul(C + s - 1, [(one - cut_add[s - 1][0]).astype(np.uint64),
+                                  (zero - cut_add[s - 1][1]).astype(np.uint64)], cut_add[s])
+        for j in range(ell):
+            k = s * ell + j
+            stack = []
+            for ins in g.prog[g.prog_off[k]:g.prog_off[k + 1]]:
+                op, arg = ins & 0xF, ins >> 4
+                if op == 0:  # query bit
+                    stack.append([pred[0][arg] & 1, pred[1][arg] & 1])
+                elif op == 1:  # wrap: low bit of the additive share
+                    stack.append([np.full(n, int(g.wrap_share[p][arg]) & 1, np.uint8)
+                                  for p in (0, 1)])
+                elif op == 2:  # constant on party 0's share
+                    stack.append([np.full(n, arg & 1, np.uint8), np.zeros(n, np.uint8)])
+                elif op == 3:  # NOT
+                    stack[-1] = [stack[-1][0] ^ 1, stack[-1][1]]
+                else:
+                    y = stack.pop()
+                    x = stack.pop()
+                    r = [x[0] ^ y[0], x[1] ^ y[1]]
+                    if op in (5, 6):  # AND / OR: one bit triple
+                        t = [bt[p][and_idx] for p in (0, 1)]
+                        and_idx += 1
+                        a = [t[p] & 1 for p in (0, 1)]
+                        b = [(t[p] >> 1) & 1 for p in (0, 1)]
+                        c = [(t[p] >> 2) & 1 for p in (0, 1)]
+                        e = x[0] ^ x[1] ^ a[0] ^ a[1]
+                        f = y[0] ^ y[1] ^ b[0] ^ b[1]
+                        z = [c[0] ^ (e & b[0]) ^ (f & a[0]) ^ (e & f), c[1] ^ (e & b[1]) ^ (f & a[1])]
+                        r = z if op == 5 else [r[0] ^ z[0], r[1] ^ z[1]]
+                    stack.append(r)
+            assert len(stack) == 1
+            bx = stack[0]
+            badd = b2a(B + k, bx[0].astype(np.uint64), bx[1].astype(np.uint64))
+            z = mul(B + S * ell + k, sel, badd)
+            out[0][:, j] += z[0]
+            out[1][:, j] += z[1]
+    return out
