@@ -80,6 +80,8 @@ int sufhip_event_create(void** ev);
 int sufhip_event_destroy(void* ev);
 int sufhip_event_record(void* ev, void* stream);
 int sufhip_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Blocks the calling thread until the recorded work of `ev` has completed. */
+int sufhip_event_synchronize(void* ev);
 
 /* ---------------------------------------------------------------------- */
 /* AES-128 and the myl7 PRG                                                 */

@@ -3,8 +3,8 @@
 # at third_party/myl7_fss, source files used unmodified and in place) into
 # oracle/_ref/, one library per output group, plus oracle/ref_shim.cpp, and
 # the gate-table dump driver oracle/ref_tables.cpp over the reference's
-# header-only table builders, and oracle/ref_suf_eval.cpp over its
-# header-only eval_suf_ref.
+# header-only table builders, oracle/ref_suf_eval.cpp over its header-only
+# eval_suf_ref, and oracle/ref_tape.cpp over its header-only TapeWriter.
 # Compile definitions follow the reference's myl7_core target
 # (CMakeLists.txt:84-93): kBlocks=8, kLambda=16, OpenSSL libcrypto, OpenMP.
 # Outputs go only to oracle/_ref/ (git-ignored).  Without the reference tree
@@ -36,4 +36,7 @@ mv "$OUT/ref_tables.tmp" "$OUT/ref_tables"
 # The SUF reference-evaluation driver (tests/golden/make_suf_ref.py runs it).
 g++ -std=c++17 -O1 -I"$REF/include" "$HERE/ref_suf_eval.cpp" -o "$OUT/ref_suf_eval.tmp"
 mv "$OUT/ref_suf_eval.tmp" "$OUT/ref_suf_eval"
-echo "build_ref: built $OUT/libmyl7ref_bytes.so $OUT/libmyl7ref_u128_le.so $OUT/ref_tables $OUT/ref_suf_eval"
+# The tape-record driver (tests/golden/make_tape.py runs it).
+g++ -std=c++20 -O1 -I"$REF/include" "$HERE/ref_tape.cpp" -o "$OUT/ref_tape.tmp"
+mv "$OUT/ref_tape.tmp" "$OUT/ref_tape"
+echo "build_ref: built $OUT/libmyl7ref_bytes.so $OUT/libmyl7ref_u128_le.so $OUT/ref_tables $OUT/ref_suf_eval $OUT/ref_tape"

@@ -203,6 +203,12 @@ int sufhip_event_record(void* ev, void* stream) {
   return SUFHIP_OK;
 }
 
+int sufhip_event_synchronize(void* ev) {
+  SUFHIP_REQUIRE(ev, "sufhip_event_synchronize: null event");
+  SUFHIP_CHECK(hipEventSynchronize(reinterpret_cast<hipEvent_t>(ev)), "hipEventSynchronize");
+  return SUFHIP_OK;
+}
+
 int sufhip_event_elapsed_ms(void* start, void* stop, float* ms) {
   SUFHIP_REQUIRE(start && stop && ms, "sufhip_event_elapsed_ms: null");
   SUFHIP_CHECK(hipEventSynchronize(reinterpret_cast<hipEvent_t>(stop)), "hipEventSynchronize");

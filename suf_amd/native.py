@@ -55,6 +55,7 @@ _SIGS = {
     "sufhip_event_destroy": (c_int, [c_vp]),
     "sufhip_event_record": (c_int, [c_vp, c_vp]),
     "sufhip_event_elapsed_ms": (c_int, [c_vp, c_vp, c_vp]),
+    "sufhip_event_synchronize": (c_int, [c_vp]),
     "sufhip_aes128_ctr": (c_int, [c_vp, c_vp, c_u64, c_u64, c_sz, c_vp]),
     "sufhip_prg_mmo": (c_int, [c_vp, c_vp, c_sz, c_int, c_vp, c_vp]),
     "sufhip_dcf_key_bytes": (c_sz, [c_int, c_int]),
