@@ -909,6 +909,26 @@ typedef struct sufhip_composite_bool_args {
 size_t sufhip_composite_bool_triples(int cuts, int ell);
 int sufhip_composite_bool2(const sufhip_composite_bool_args* args, void* stream);
 
+/* One flush of a two-party open collector (the device path of
+ * OpenCollector::flush, src/runtime/open_collector.cpp:357-791): the
+ * requests' shares (device, both parties) are gathered, each party's are
+ * packed to eff_bits (the message it sends: launch_pack_eff_bits_kernel),
+ * and party 0's own shares plus party 1's unpacked message give the opened
+ * values (launch_unpack_add_mod_kernel; launch_unpack_add_to_signed_kernel
+ * when sign_extend), masked to ring_bits, back to back in request order in
+ * d_opened: (s0 + (s1 mod 2^eff_bits)) mod 2^ring_bits, exact when
+ * eff_bits >= ring_bits or party 1's shares fit eff_bits.  Four launches
+ * for any number of requests.  d_work: 8-byte aligned,
+ * sufhip_open_flush2_work_bytes(total, eff_bits) bytes. */
+typedef struct sufhip_open_req {
+  const uint64_t* share[2];
+  size_t len;
+} sufhip_open_req;
+size_t sufhip_open_flush2_work_bytes(size_t total, int eff_bits);
+int sufhip_open_flush2(const sufhip_open_req* reqs, int count, int eff_bits, int ring_bits,
+                       int sign_extend, uint64_t* d_opened, void* d_work, size_t work_bytes,
+                       void* stream);
+
 /* ---------------------------------------------------------------------- */
 /* Host-side helpers for seeded synthetic inputs                            */
 /* ---------------------------------------------------------------------- */

@@ -72,6 +72,8 @@ _SIGS = {
     "sufhip_trunc_eval_noalloc": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp]),
     "sufhip_trunc_prepare": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_sz, c_vp, c_sz, c_vp]),
     "sufhip_stage_hatx": (c_int, [c_vp, c_int, c_vp, c_sz, c_vp]),
+    "sufhip_open_flush2_work_bytes": (c_sz, [c_sz, c_int]),
+    "sufhip_open_flush2": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_sz, c_vp]),
     "sufhip_composite_bool_triples": (c_sz, [c_int, c_int]),
     "sufhip_composite_bool2": (c_int, [c_vp, c_vp]),
     "sufhip_trunc_finish": (c_int, [c_int, c_int, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp, c_sz,
@@ -287,6 +289,11 @@ STAGE_MAX_SEGS = 64
 class StageSeg(ctypes.Structure):
     """sufhip_stage_seg (include/suf_hip.h)."""
     _fields_ = [("src", c_vp), ("len", c_sz), ("dst", c_sz), ("eff_bits", c_int)]
+
+
+class OpenReq(ctypes.Structure):
+    """sufhip_open_req (include/suf_hip.h)."""
+    _fields_ = [("share", c_vp * 2), ("len", c_sz)]
 
 
 class CompositeBoolArgs(ctypes.Structure):

@@ -102,7 +102,8 @@ def _c_offsets(struct, fields):
 
 
 @pytest.mark.parametrize("struct,cls", [("sufhip_composite_bool_args", "CompositeBoolArgs"),
-                                        ("sufhip_stage_seg", "StageSeg")])
+                                        ("sufhip_stage_seg", "StageSeg"),
+                                        ("sufhip_open_req", "OpenReq")])
 def test_composite_struct_layouts_match_c(struct, cls):
     k = getattr(native, cls)
     want = _c_offsets(struct, [f[0] for f in k._fields_])
