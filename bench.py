@@ -382,13 +382,14 @@ def bench_matmul(steps, warmup, M=128, K=768, N=3072, frac_bits=12, cpu_seconds=
                              "int8-limb MFMA" if g.mm_work is not None else "u64 VALU"),
            "steps": steps, "check": "ok" if ok else "MISMATCH"}
     if g.fused:
-        # Per 32 x 32 tile and 32-deep k-step: party 0 runs 3 x 36 digit-plane
-        # MFMAs (D B0, A0 E, D E), party 1 2 x 36; each is 32x32x32 int8 MACs.
-        mfmas = (M // 32) * (N // 32) * (K // 32) * (108 + 72)
+        # Per 32 x 32 tile and 32-deep k-step each party runs 2 x 36
+        # digit-plane MFMAs (party 0: (D + A0) E and D B0; party 1: A1 E and
+        # D B1); each is 32x32x32 int8 MACs.
+        mfmas = (M // 32) * (N // 32) * (K // 32) * (72 + 72)
         res["product_ms"] = prod_ms
         res["roofline"] = roofline_mfma(
-            "beaver_mfma2_kernel", prod_ms, mfmas * 2 * 32 * 32 * 32,
-            "%d v_mfma_i32_32x32x32_i8 (tiles x k-steps x 180 digit products) x 65536 ops" % mfmas)
+            "beaver_bal_kernel", prod_ms, mfmas * 2 * 32 * 32 * 32,
+            "%d v_mfma_i32_32x32x32_i8 (tiles x k-steps x 144 digit products) x 65536 ops" % mfmas)
     if cpu_seconds > 0:
         res["cpu_baseline"] = cpu_matmul_baseline(g, state, Xd, Wd, out, cpu_seconds)
     return res

@@ -344,11 +344,17 @@ int sufhip_lin2(const sufhip_operand2* x, size_t n, uint64_t* d_out0, uint64_t* 
  * product's operand (sufhip_kb_split_batch's layout): element i of the
  * [batches][rows x cols] open goes to planes [8][batches][K/32][R][32] with
  * (K, R) = (cols, rows) for k_is_col = 1 and (rows, cols) otherwise; rows and
- * cols multiples of 32, 16-byte aligned.  planes = NULL: none. */
+ * cols multiples of 32, 16-byte aligned.  planes = NULL: none.
+ * planes_a0 (optional, with a0): also the planes of open[i] + a0[i], a0
+ * indexed like the open -- party 0's own value D + A_0 after the open of
+ * D = X - A, the left operand of its product with E in the balanced form of
+ * sufhip_beaver_matmul2_mfma_ex (Xp). */
 typedef struct sufhip_kb_planes {
   int8_t* planes;
   int batches, rows, cols;
   int k_is_col;
+  int8_t* planes_a0;
+  const uint64_t* a0;
 } sufhip_kb_planes;
 typedef struct sufhip_lin2_job {
   sufhip_operand2 x;
@@ -725,13 +731,16 @@ int sufhip_beaver_matmul2_batched(const uint64_t* d_D_open, const uint64_t* d_E_
  * multiples of 32, planes of sufhip_kb_planes_bytes() bytes, 16-byte
  * aligned.  sufhip_beaver_matmul2_mfma_batched: the planes of D, E, A_p,
  * B_p and C_p, out_p as in sufhip_beaver_matmul2_batched; M, K, N multiples
- * of 32, K <= 4096 (exact int32 accumulation). */
+ * of 32, K <= 4096 (exact int32 accumulation).  planes_a0 (optional, with
+ * a0): also the planes of src[i] + a0[i] (as in sufhip_kb_planes). */
 #define SUFHIP_KB_SPLIT_JOBS 8
 typedef struct sufhip_kb_split_job {
   const uint64_t* src;
   int8_t* planes;
   int batches, rows, cols;
   int k_is_col;
+  int8_t* planes_a0;
+  const uint64_t* a0;
 } sufhip_kb_split_job;
 /* sufhip_beaver_matmul2_mfma_ex: the same product with options.  merge_heads:
  * outputs at [m][b N + n] (heads side by side, as attention_forward merges
@@ -740,7 +749,11 @@ typedef struct sufhip_kb_split_job {
  * whose outputs trunc->y are written at the output positions instead of
  * out (which may be NULL).  out_planes (optional, merge_heads only, cols =
  * batches N): the (truncated) outputs also as the digit planes of a
- * following public-weight product. */
+ * following public-weight product.  Xp (optional): the planes of D + A_0
+ * (party 0's own value after the open, sufhip_kb_planes.planes_a0).  With
+ * it each party's share takes two operand products per k-step,
+ *   out_0 = C_0 + (D + A_0) E + D B_0,   out_1 = C_1 + A_1 E + D B_1,
+ * the same shares as the three-product form that runs without it. */
 typedef struct sufhip_beaver_mfma2_args {
   const int8_t* Dp;
   const int8_t* Ep;
@@ -753,6 +766,7 @@ typedef struct sufhip_beaver_mfma2_args {
   const sufhip_trunc_epilogue* trunc;
   uint64_t mask;
   sufhip_x_planes out_planes;
+  const int8_t* Xp;
 } sufhip_beaver_mfma2_args;
 int sufhip_beaver_matmul2_mfma_ex(const sufhip_beaver_mfma2_args* args, void* stream);
 size_t sufhip_kb_planes_bytes(int batches, int rows, int cols);
@@ -770,6 +784,8 @@ typedef struct sufhip_kb_open_job {
   int8_t* planes;
   int batches, rows, cols;
   int k_is_col;
+  int8_t* planes_a0; /* optional, with a0: planes of the open + a0[i] */
+  const uint64_t* a0;
 } sufhip_kb_open_job;
 int sufhip_kb_open_split_batch(const sufhip_kb_open_job* jobs, int count, void* stream);
 int sufhip_beaver_matmul2_mfma_batched(const int8_t* d_Dp, const int8_t* d_Ep,

@@ -38,6 +38,8 @@ struct SplitArgs {
   const uint64_t* add[kSplitJobs];     // optional: + add[i]
   const uint64_t* sub[kSplitJobs][2];  // optional: - sub[0][i] - sub[1][i]
   int8_t* planes[kSplitJobs];
+  int8_t* planes_a0[kSplitJobs];       // optional: planes of the value + a0[i]
+  const uint64_t* a0[kSplitJobs];
   int batches[kSplitJobs], rows[kSplitJobs], cols[kSplitJobs], k_is_col[kSplitJobs];
   size_t begin[kSplitJobs + 1];  // lanes of the jobs before (4 or 16 k each)
   int count;
@@ -59,6 +61,38 @@ __device__ __forceinline__ uint64_t split_val(const SplitArgs& a, int j, size_t 
   return v;
 }
 
+// Four consecutive k of one plane row: one 4-byte store per plane.
+__device__ __forceinline__ void write4(int8_t* planes, size_t plane, size_t off,
+                                       const uint64_t (&v)[4]) {
+  uint32_t pk[kDigitPlanes] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    uint32_t d[kDigitPlanes];
+    digits8(v[t], d);
+#pragma unroll
+    for (int i = 0; i < kDigitPlanes; ++i) pk[i] |= d[i] << (8 * t);
+  }
+#pragma unroll
+  for (int i = 0; i < kDigitPlanes; ++i)
+    *reinterpret_cast<uint32_t*>(planes + i * plane + off) = pk[i];
+}
+
+// Sixteen k of one plane row (value(t), t < 16): one 16-byte store per plane.
+template <typename F>
+__device__ __forceinline__ void write16(int8_t* dst, size_t plane, F value) {
+  uint32_t pk[kDigitPlanes][4] = {};
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    uint32_t d[kDigitPlanes];
+    digits8(value(t), d);
+#pragma unroll
+    for (int i = 0; i < kDigitPlanes; ++i) pk[i][t >> 2] |= d[i] << (8 * (t & 3));
+  }
+#pragma unroll
+  for (int i = 0; i < kDigitPlanes; ++i)
+    *reinterpret_cast<uint4*>(dst + i * plane) = make_uint4(pk[i][0], pk[i][1], pk[i][2], pk[i][3]);
+}
+
 __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
   const size_t total = a.begin[a.count];
   for (size_t g = size_t(blockIdx.x) * 256 + threadIdx.x; g < total;
@@ -75,18 +109,16 @@ __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
       const size_t b = q / per_batch, rem = q % per_batch;
       const int r = int(rem / (K / 4)), k = 4 * int(rem % (K / 4));
       const size_t src = b * size_t(rows) * cols + size_t(r) * cols + k;
-      uint32_t pk[kDigitPlanes] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        uint32_t d[kDigitPlanes];
-        digits8(split_val(a, j, src + t), d);
-#pragma unroll
-        for (int i = 0; i < kDigitPlanes; ++i) pk[i] |= d[i] << (8 * t);
-      }
       const size_t off = b * size_t(R) * K + kblock_off(size_t(r), k, size_t(R));
+      uint64_t v[4];
 #pragma unroll
-      for (int i = 0; i < kDigitPlanes; ++i)
-        *reinterpret_cast<uint32_t*>(a.planes[j] + i * plane + off) = pk[i];
+      for (int t = 0; t < 4; ++t) v[t] = split_val(a, j, src + t);
+      write4(a.planes[j], plane, off, v);
+      if (a.planes_a0[j]) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] += a.a0[j][src + t];
+        write4(a.planes_a0[j], plane, off, v);
+      }
     } else {
       const size_t per_batch = size_t(R) * (K / 16);
       const size_t b = q / per_batch, rem = q % per_batch;
@@ -94,19 +126,14 @@ __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
       const int r = int((rem >> 1) % size_t(R));
       const int k0 = 32 * kb + 16 * h;
       const size_t src = b * size_t(rows) * cols + size_t(k0) * cols + r;
-      int8_t* dst = a.planes[j] + b * size_t(R) * K + kblock_off(size_t(r), k0, size_t(R));
-      uint32_t pk[kDigitPlanes][4] = {};
-#pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        uint32_t d[kDigitPlanes];
-        digits8(split_val(a, j, src + size_t(t) * cols), d);
-#pragma unroll
-        for (int i = 0; i < kDigitPlanes; ++i) pk[i][t >> 2] |= d[i] << (8 * (t & 3));
+      const size_t off = b * size_t(R) * K + kblock_off(size_t(r), k0, size_t(R));
+      write16(a.planes[j] + off, plane, [&](int t) { return split_val(a, j, src + size_t(t) * cols); });
+      if (a.planes_a0[j]) {
+        const uint64_t* a0 = a.a0[j];
+        write16(a.planes_a0[j] + off, plane, [&](int t) {
+          return split_val(a, j, src + size_t(t) * cols) + a0[src + size_t(t) * cols];
+        });
       }
-#pragma unroll
-      for (int i = 0; i < kDigitPlanes; ++i)
-        *reinterpret_cast<uint4*>(dst + i * plane) =
-            make_uint4(pk[i][0], pk[i][1], pk[i][2], pk[i][3]);
     }
   }
 }
@@ -123,7 +150,50 @@ struct Bm2Args {
   TruncEpi epi;     // on: the open + mask feeds this gate, whose outputs are written
   uint64_t mask;
   sufhip_x_planes xp;  // optional digit planes of the (truncated) outputs, merged layout
+  const int8_t* X;     // balanced form: LHS planes of D + A_0
 };
+
+// Party p's finished 32 x 32 tile values (lane l: column l % 32, rows of
+// the accumulator layout) to out_p, and to the output digit planes.
+__device__ __forceinline__ void bm2_store(const Bm2Args& a, int p, int l, int m0, int n0, size_t b,
+                                          const uint64_t (&v)[16]) {
+  const int M = a.M, N = a.N;
+  const int col = n0 + (l & 31);
+  const size_t ob = b * size_t(M) * N;
+  const size_t ld = size_t(a.batches) * N;  // merged row length
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    const size_t o = a.merge ? size_t(row) * ld + b * N + col : ob + size_t(row) * N + col;
+    a.out[p][o] = v[r];
+    if (a.xp.planes) put_x_digits(a.xp, size_t(M), o, p, v[r]);
+  }
+}
+
+// With the truncation epilogue: both parties' tiles are in LDS (both[p]);
+// wave p opens rows r in [8p, 8p + 8) and writes both parties' outputs.
+__device__ __forceinline__ void bm2_trunc_rows(const Bm2Args& a, int p, int l, int m0, int n0,
+                                               size_t b, const uint64_t (*both)[16][64]) {
+  const int M = a.M, N = a.N;
+  const int col = n0 + (l & 31);
+  const size_t ob = b * size_t(M) * N;
+  const size_t ld = size_t(a.batches) * N;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int r = 8 * p + q;
+    const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    const size_t o = a.merge ? size_t(row) * ld + b * N + col : ob + size_t(row) * N + col;
+    const uint64_t open = both[0][r][l] + both[1][r][l] + a.mask;
+    const uint64_t y0 = trunc_table_eval(a.epi.key[0], a.epi.table[0], a.epi.f, open);
+    const uint64_t y1 = trunc_table_eval(a.epi.key[1], a.epi.table[1], a.epi.f, open);
+    a.epi.y[0][o] = y0;
+    a.epi.y[1][o] = y1;
+    if (a.xp.planes) {
+      put_x_digits(a.xp, size_t(M), o, 0, y0);
+      put_x_digits(a.xp, size_t(M), o, 1, y1);
+    }
+  }
+}
 
 // Waves per party: k-steps st, st + kKWaves, ... go to wave st % kKWaves, so
 // up to kKWaves steps' loads and MFMAs run at once; the partial tiles are
@@ -190,7 +260,6 @@ __global__ void __launch_bounds__(128 * kKWaves) beaver_mfma2_kernel(Bm2Args a) 
   __syncthreads();
   const int col = n0 + (l & 31);
   const size_t ob = b * size_t(M) * N;
-  const size_t ld = size_t(a.batches) * N;  // merged row length
   if (kw == 0) {
     for (int q = 1; q < kws; ++q) {
 #pragma unroll
@@ -203,14 +272,7 @@ __global__ void __launch_bounds__(128 * kKWaves) beaver_mfma2_kernel(Bm2Args a) 
     }
   }
   if (!a.epi.on) {
-    if (kw > 0) return;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-      const size_t o = a.merge ? size_t(row) * ld + b * N + col : ob + size_t(row) * N + col;
-      a.out[p][o] = v[r];
-      if (a.xp.planes) put_x_digits(a.xp, size_t(M), o, p, v[r]);
-    }
+    if (kw == 0) bm2_store(a, p, l, m0, n0, b, v);
     return;
   }
   // The open out_0 + out_1 + mask through LDS (the slices' buffer is free
@@ -223,22 +285,94 @@ __global__ void __launch_bounds__(128 * kKWaves) beaver_mfma2_kernel(Bm2Args a) 
     for (int r = 0; r < 16; ++r) both[p][r][l] = v[r];
   }
   __syncthreads();
-  if (kw > 0) return;
+  if (kw == 0) bm2_trunc_rows(a, p, l, m0, n0, b, both);
+}
+
+// Balanced form (Xp given): wave p computes party p's tile over every
+// k-step as two operand products, (L_p, E) with L_0 = D + A_0 and L_1 = A_1,
+// then (D, B_p): 72 MFMAs per party and step, so the two waves of a tile
+// finish together.  The operand pairs run through a register pipeline
+// kStages deep (a pair's planes are loaded kStages - 1 pairs before its
+// MFMAs), which keeps loads in flight while the wave -- the only one on its
+// SIMD -- multiplies.  Bases are wave-uniform (scalar registers) plus each
+// lane's 32-bit fragment offset.
+constexpr int kStages = 4;
+
+__global__ void __launch_bounds__(128, 1) beaver_bal_kernel(Bm2Args a) {
+  __shared__ uint64_t both[2][16][64];
+  const int l = threadIdx.x & 63;
+  const int p = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int M = a.M, K = a.K, N = a.N;
+  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
+  const size_t b = blockIdx.z;
+  // Byte offsets within the operands' planes fit 32 bits (checked on the host).
+  const uint32_t lplane = uint32_t(a.batches) * M * K, rplane = uint32_t(a.batches) * N * K;
+  const uint32_t lstep = uint32_t(M) * 32, rstep = uint32_t(N) * 32;
+  const uint32_t fo = uint32_t(l & 31) * 32 + 16 * uint32_t(l >> 5);
+  const uint32_t lb0 = uint32_t(b) * M * K + uint32_t(m0) * 32;
+  const uint32_t rb0 = uint32_t(b) * N * K + uint32_t(n0) * 32;
+  const int8_t* Lx = (p == 0 ? a.X : a.A[1]) + lb0;
+  const int8_t* Ld = a.D + lb0;
+  const int8_t* Re = a.E + rb0;
+  const int8_t* Rb = (p == 0 ? a.B[0] : a.B[1]) + rb0;
+  v16i acc[kDigitPlanes];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int r = 8 * p + q;
-    const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-    const size_t o = a.merge ? size_t(row) * ld + b * N + col : ob + size_t(row) * N + col;
-    const uint64_t open = both[0][r][l] + both[1][r][l] + a.mask;
-    const uint64_t y0 = trunc_table_eval(a.epi.key[0], a.epi.table[0], a.epi.f, open);
-    const uint64_t y1 = trunc_table_eval(a.epi.key[1], a.epi.table[1], a.epi.f, open);
-    a.epi.y[0][o] = y0;
-    a.epi.y[1][o] = y1;
-    if (a.xp.planes) {
-      put_x_digits(a.xp, size_t(M), o, 0, y0);
-      put_x_digits(a.xp, size_t(M), o, 1, y1);
+  for (int s = 0; s < kDigitPlanes; ++s)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[s][r] = 0;
+  // Operand pairs u = 2 step + (0: (L_p, E), 1: (D, B_p)).  The loop runs
+  // over whole groups of kStages pairs; loads past the last pair repeat it
+  // (in bounds) and their MFMAs are skipped.
+  const int U = 2 * (K / 32);
+  const int Ug = (U + kStages - 1) / kStages * kStages;
+  v4i L[kStages][kDigitPlanes], R[kStages][kDigitPlanes];
+  auto issue = [&](int q, int u) {
+    u = u < U ? u : U - 1;
+    const uint32_t st = uint32_t(u >> 1);
+    const int8_t* lb = (u & 1) ? Ld : Lx;
+    const int8_t* rb = (u & 1) ? Rb : Re;
+#pragma unroll
+    for (int i = 0; i < kDigitPlanes; ++i) {
+      L[q][i] = load16(lb + (i * lplane + st * lstep) + fo);
+      R[q][i] = load16(rb + (i * rplane + st * rstep) + fo);
+    }
+  };
+#pragma unroll
+  for (int q = 0; q < kStages - 1; ++q) issue(q, q);
+  for (int u0 = 0; u0 < Ug; u0 += kStages) {
+#pragma unroll
+    for (int h = 0; h < kStages; ++h) {
+      const int u = u0 + h;
+      issue((h + kStages - 1) % kStages, u + kStages - 1);
+      if (u < U) {
+#pragma unroll
+        for (int i = 0; i < kDigitPlanes; ++i)
+#pragma unroll
+          for (int j = 0; i + j < kDigitPlanes; ++j)
+            acc[i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(L[h][i], R[h][j], acc[i + j], 0,
+                                                              0, 0);
+      }
     }
   }
+  uint64_t v[16];
+  const int col = n0 + (l & 31);
+  const size_t ob = b * size_t(M) * N;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    v[r] = 0;
+#pragma unroll
+    for (int s = 0; s < kDigitPlanes; ++s) v[r] += uint64_t(int64_t(acc[s][r])) << (8 * s);
+    const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    v[r] += a.C[p][ob + size_t(row) * N + col];
+  }
+  if (!a.epi.on) {
+    bm2_store(a, p, l, m0, n0, b, v);
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) both[p][r][l] = v[r];
+  __syncthreads();
+  bm2_trunc_rows(a, p, l, m0, n0, b, both);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -253,15 +387,21 @@ namespace {
 
 // Shape checks and lane count of split job j (sources already set).
 int split_job(SplitArgs& a, int j, int8_t* planes, int batches, int rows, int cols,
-              int k_is_col, const char* what) {
+              int k_is_col, int8_t* planes_a0, const uint64_t* a0, const char* what) {
   const bool shape = batches >= 1 && rows >= 32 && cols >= 32 && rows % 32 == 0 &&
                      cols % 32 == 0;
-  if (!shape || !planes || !aligned16(planes)) {
+  if (!shape || !planes || !aligned16(planes) || !aligned16(planes_a0)) {
     set_error(std::string(what) +
               ": batches >= 1, rows and cols multiples of 32, planes 16-byte aligned");
     return SUFHIP_ERR_INVALID;
   }
+  if ((planes_a0 == nullptr) != (a0 == nullptr)) {
+    set_error(std::string(what) + ": planes_a0 and a0 go together");
+    return SUFHIP_ERR_INVALID;
+  }
   a.planes[j] = planes;
+  a.planes_a0[j] = planes_a0;
+  a.a0[j] = a0;
   a.batches[j] = batches;
   a.rows[j] = rows;
   a.cols[j] = cols;
@@ -299,7 +439,7 @@ int sufhip_kb_split_batch(const sufhip_kb_split_job* jobs, int count, void* stre
     SUFHIP_REQUIRE(jb.src, "sufhip_kb_split_batch: null source");
     a.src[j] = jb.src;
     if (int rc = split_job(a, j, jb.planes, jb.batches, jb.rows, jb.cols, jb.k_is_col,
-                           "sufhip_kb_split_batch"))
+                           jb.planes_a0, jb.a0, "sufhip_kb_split_batch"))
       return rc;
   }
   return launch_split(a, count, stream);
@@ -319,7 +459,7 @@ int sufhip_kb_open_split_batch(const sufhip_kb_open_job* jobs, int count, void* 
     a.sub[j][0] = jb.b[0];
     a.sub[j][1] = jb.b[1];
     if (int rc = split_job(a, j, jb.planes, jb.batches, jb.rows, jb.cols, jb.k_is_col,
-                           "sufhip_kb_open_split_batch"))
+                           jb.planes_a0, jb.a0, "sufhip_kb_open_split_batch"))
       return rc;
   }
   return launch_split(a, count, stream);
@@ -341,7 +481,7 @@ int sufhip_beaver_matmul2_mfma_ex(const sufhip_beaver_mfma2_args* args, void* st
   const size_t n = size_t(g.batches) * g.M * g.N;
   Bm2Args a{g.Dp, g.Ep, {g.Ap[0], g.Ap[1]}, {g.Bp[0], g.Bp[1]}, {g.C[0], g.C[1]},
             {g.out[0], g.out[1]}, g.batches, g.M, g.K, g.N, g.merge_heads ? 1 : 0, TruncEpi{},
-            g.mask, g.out_planes};
+            g.mask, g.out_planes, g.Xp};
   if (int rc = make_epi(g.trunc, n, what, &a.epi)) return rc;
   SUFHIP_REQUIRE(a.epi.on || (g.out[0] && g.out[1]),
                  "sufhip_beaver_matmul2_mfma_ex: outputs (or a truncation) needed");
@@ -351,9 +491,17 @@ int sufhip_beaver_matmul2_mfma_ex(const sufhip_beaver_mfma2_args* args, void* st
                      (g.merge_heads && g.out_planes.cols == g.batches * g.N &&
                       x_planes_ok(g.out_planes, n)),
                  "sufhip_beaver_matmul2_mfma_ex: out_planes need merge_heads, cols = batches N");
+  SUFHIP_REQUIRE(aligned16(g.Xp), "sufhip_beaver_matmul2_mfma_ex: planes must be 16-byte aligned");
+  const dim3 grid(g.N / 32, g.M / 32, g.batches);
+  // The balanced kernel addresses a plane set with 32-bit offsets.
+  const uint64_t plane_set = uint64_t(kDigitPlanes) * uint64_t(g.batches) * uint64_t(g.K) *
+                             uint64_t(g.M > g.N ? g.M : g.N);
+  if (g.Xp && plane_set < (uint64_t(1) << 32)) {
+    hipLaunchKernelGGL(beaver_bal_kernel, grid, dim3(128), 0, as_stream(stream), a);
+    return check_launch("beaver_bal_kernel");
+  }
   const int steps = g.K / 32;
   const int kws = steps < 2 ? 2 : (steps < kKWaves ? steps : kKWaves);
-  const dim3 grid(g.N / 32, g.M / 32, g.batches);
   hipLaunchKernelGGL(beaver_mfma2_kernel, grid, dim3(128 * kws), 0, as_stream(stream), a);
   return check_launch("beaver_mfma2_kernel");
 }

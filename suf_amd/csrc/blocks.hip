@@ -510,7 +510,7 @@ int sufhip_softmax2(const sufhip_softmax2_args* args, void* stream) {
   SUFHIP_REQUIRE(!g.dense_planes.planes ||
                      (g.d_dense && kb_planes_ok(g.dense_planes, size_t(g.rows) * g.dense_cols)),
                  "sufhip_softmax2: dense_planes need d_dense and cover rows x dense_cols");
-  A.dkb = g.d_dense ? g.dense_planes : sufhip_kb_planes{nullptr, 0, 0, 0, 0};
+  A.dkb = g.d_dense ? g.dense_planes : sufhip_kb_planes{};
   const size_t row_bytes = tree_row_words(g.max_row) * sizeof(uint64_t);
   int waves = kSmWaves;
   while (waves > 1 && sizeof(SmStatic) + size_t(waves) * row_bytes > kSmLdsCap) waves /= 2;

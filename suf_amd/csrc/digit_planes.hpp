@@ -74,14 +74,21 @@ __device__ __forceinline__ void put_kb_digits(const sufhip_kb_planes& o, size_t 
   digits8(v, d);
 #pragma unroll
   for (int q = 0; q < kDigitPlanes; ++q) o.planes[q * plane + off] = int8_t(d[q]);
+  if (o.planes_a0) {
+    digits8(v + o.a0[i], d);
+#pragma unroll
+    for (int q = 0; q < kDigitPlanes; ++q) o.planes_a0[q * plane + off] = int8_t(d[q]);
+  }
 }
 
 // Host: checks an optional sufhip_kb_planes for an open of n elements.
 inline bool kb_planes_ok(const sufhip_kb_planes& o, size_t n) {
-  if (!o.planes) return true;
+  if (!o.planes) return !o.planes_a0;
+  if ((o.planes_a0 == nullptr) != (o.a0 == nullptr)) return false;
   return o.batches >= 1 && o.rows >= 32 && o.cols >= 32 && o.rows % 32 == 0 &&
          o.cols % 32 == 0 && size_t(o.batches) * size_t(o.rows) * size_t(o.cols) == n &&
-         (reinterpret_cast<uintptr_t>(o.planes) & 15) == 0;
+         (reinterpret_cast<uintptr_t>(o.planes) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(o.planes_a0) & 15) == 0;
 }
 
 // Host: checks an optional sufhip_x_planes for an output of n elements.

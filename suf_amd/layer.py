@@ -103,25 +103,33 @@ def kb_planes(batches, rows, cols, device="cuda"):
 
 def kb_split(jobs):
     """Digit planes of up to 8 operands in one launch: jobs of (src, planes,
-    batches, rows, cols, k_is_col)."""
+    batches, rows, cols, k_is_col[, planes_a0, a0]); with the last two also
+    the planes of src + a0."""
     arr = (native.KbSplitJob * len(jobs))()
-    for i, (src, planes, b, r, c, kc) in enumerate(jobs):
+    for i, jb in enumerate(jobs):
+        src, planes, b, r, c, kc = jb[:6]
         arr[i].src, arr[i].planes = ptr(src), ptr(planes)
         arr[i].batches, arr[i].rows, arr[i].cols, arr[i].k_is_col = b, r, c, int(kc)
+        if len(jb) > 6:
+            arr[i].planes_a0, arr[i].a0 = ptr(jb[6]), ptr(jb[7])
     native.call("sufhip_kb_split_batch", arr, len(jobs), stream_ptr())
 
 
 def kb_open_split(jobs):
     """Masked opens written straight as digit planes, up to 8 in one launch:
-    jobs of (a, b, planes, batches, rows, cols, k_is_col) with a and b pairs
-    of share arrays (b may be None); element i is a0 + a1 - b0 - b1."""
+    jobs of (a, b, planes, batches, rows, cols, k_is_col[, planes_a0, a0])
+    with a and b pairs of share arrays (b may be None); element i is
+    a0 + a1 - b0 - b1, and with the last two also its + a0[i] planes."""
     arr = (native.KbOpenJob * len(jobs))()
-    for i, (a, b, planes, nb, r, c, kc) in enumerate(jobs):
+    for i, jb in enumerate(jobs):
+        a, b, planes, nb, r, c, kc = jb[:7]
         arr[i].a[0], arr[i].a[1] = ptr(a[0]), ptr(a[1])
         if b is not None:
             arr[i].b[0], arr[i].b[1] = ptr(b[0]), ptr(b[1])
         arr[i].planes = ptr(planes)
         arr[i].batches, arr[i].rows, arr[i].cols, arr[i].k_is_col = nb, r, c, int(kc)
+        if len(jb) > 7:
+            arr[i].planes_a0, arr[i].a0 = ptr(jb[7]), ptr(jb[8])
     native.call("sufhip_kb_open_split_batch", arr, len(jobs), stream_ptr())
 
 
@@ -153,27 +161,39 @@ class BatchedTriples:
             self.Ap = tuple(kb_planes(batches, M, K, device) for _ in range(2))
             self.Bp = tuple(kb_planes(batches, K, N, device) for _ in range(2))
             self.Dp = kb_planes(batches, M, K, device)  # the opens' planes, per call
+            self.Xp = kb_planes(batches, M, K, device)  # D + A_0: party 0's left operand with E
             self.Ep = kb_planes(batches, K, N, device)
             kb_split([(self.A[p], self.Ap[p], batches, M, K, 1) for p in (0, 1)] +
                      [(self.B[p], self.Bp[p], batches, K, N, 0) for p in (0, 1)])
 
     def split_jobs(self, D=None, E=None):
-        """kb_split jobs of the opens D [b][M x K] and / or E [b][K x N]."""
+        """kb_split jobs of the opens D [b][M x K] (with the planes of
+        D + A_0) and / or E [b][K x N]."""
         b, M, K, N = self.shape
-        return ([(D, self.Dp, b, M, K, 1)] if D is not None else []) + \
+        return ([(D, self.Dp, b, M, K, 1, self.Xp, self.A[0])] if D is not None else []) + \
             ([(E, self.Ep, b, K, N, 0)] if E is not None else [])
+
+    def d_planes(self):
+        """A producer's plane spec for the open D: its planes and those of D + A_0."""
+        b, M, K, _ = self.shape
+        return (self.Dp, b, M, K, 1, self.Xp, self.A[0])
+
+    def mfma_args(self):
+        """BeaverMfma2Args with this triple's planes and shape (balanced form)."""
+        b, M, K, N = self.shape
+        a = native.BeaverMfma2Args()
+        a.Dp, a.Ep, a.Xp = ptr(self.Dp), ptr(self.Ep), ptr(self.Xp)
+        for p in (0, 1):
+            a.Ap[p], a.Bp[p], a.C[p] = ptr(self.Ap[p]), ptr(self.Bp[p]), ptr(self.C[p])
+        a.batches, a.M, a.K, a.N = b, M, K, N
+        return a
 
 
 def _beaver_trunc_merged(tri, tr, out, planes=None):
     """out = tr(the product of tri's opens' planes), heads merged side by side
     ([m][b N + n]), in the product's launch; planes = (buffer, cols): also as
     a following public-weight product's digit planes."""
-    b, M, K, N = tri.shape
-    a = native.BeaverMfma2Args()
-    a.Dp, a.Ep = ptr(tri.Dp), ptr(tri.Ep)
-    for p in (0, 1):
-        a.Ap[p], a.Bp[p], a.C[p] = ptr(tri.Ap[p]), ptr(tri.Bp[p]), ptr(tri.C[p])
-    a.batches, a.M, a.K, a.N = b, M, K, N
+    a = tri.mfma_args()
     a.merge_heads = 1
     epi = tr.epilogue(out)
     a.trunc = native.ctypes.pointer(epi)
@@ -189,10 +209,9 @@ def _beaver_batched(D, E, tri, batches, M, K, N, out, split=True):
     if tri.mfma:
         if split:
             kb_split(tri.split_jobs(D, E))
-        native.call("sufhip_beaver_matmul2_mfma_batched", ptr(tri.Dp), ptr(tri.Ep),
-                    ptr(tri.Ap[0]), ptr(tri.Ap[1]), ptr(tri.Bp[0]), ptr(tri.Bp[1]),
-                    ptr(tri.C[0]), ptr(tri.C[1]), batches, M, K, N, ptr(out[0]), ptr(out[1]),
-                    stream_ptr())
+        a = tri.mfma_args()
+        a.out[0], a.out[1] = ptr(out[0]), ptr(out[1])
+        native.call("sufhip_beaver_matmul2_mfma_ex", native.ctypes.byref(a), stream_ptr())
         return
     native.call("sufhip_beaver_matmul2_batched", ptr(D), ptr(E), ptr(tri.A[0]), ptr(tri.A[1]),
                 ptr(tri.B[0]), ptr(tri.B[1]), ptr(tri.C[0]), ptr(tri.C[1]), batches, M, K, N,
@@ -290,7 +309,7 @@ class AttentionCore:
         gv = operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True))
         if self.mfma():
             # The three opens go straight to the products' digit planes.
-            lin2_batch([(gq, hsd, None, 0, (self.tri_qk.Dp, h, seq, dh, 1)),
+            lin2_batch([(gq, hsd, None, 0, self.tri_qk.d_planes()),
                         (gk, hsd, None, 0, (self.tri_qk.Ep, h, dh, seq, 0)),
                         (gv, hsd, None, 0, (self.tri_pv.Ep, h, seq, dh, 0))])
             _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S, split=False)
@@ -304,7 +323,7 @@ class AttentionCore:
             # positions truncated by 2f, the softmax block, and the open of
             # P - A over the dense [heads][seq][seq] layout (also as PV's
             # digit planes on the matrix cores).
-            dp = (self.tri_pv.Dp, h, seq, seq, 1) if self.mfma() else None
+            dp = self.tri_pv.d_planes() if self.mfma() else None
             if sm_marks is not None:
                 sm_marks.append(torch.cuda.Event(enable_timing=True))
                 sm_marks[-1].record()

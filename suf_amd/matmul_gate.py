@@ -102,6 +102,7 @@ class BeaverMatmulTrunc:
             self.Ap = tuple(layer.kb_planes(1, M, K) for _ in range(2))
             self.Bp = tuple(layer.kb_planes(1, K, N) for _ in range(2))
             self.Dp, self.Ep = layer.kb_planes(1, M, K), layer.kb_planes(1, K, N)
+            self.Xp = layer.kb_planes(1, M, K)  # D + A_0, party 0's left operand with E
             layer.kb_split([(self.A[p], self.Ap[p], 1, M, K, 1) for p in (0, 1)] +
                            [(self.B[p], self.Bp[p], 1, K, N, 0) for p in (0, 1)])
 
@@ -154,11 +155,12 @@ class BeaverMatmulTrunc:
         self.tr.prepare()
         if events:
             events[0].record()
-        layer.kb_open_split([(X, self.A, self.Dp, 1, M, K, 1), (W, self.B, self.Ep, 1, K, N, 0)])
+        layer.kb_open_split([(X, self.A, self.Dp, 1, M, K, 1, self.Xp, self.A[0]),
+                             (W, self.B, self.Ep, 1, K, N, 0)])
         if events and len(events) > 2:
             events[1].record()
         a = native.BeaverMfma2Args()
-        a.Dp, a.Ep = _p(self.Dp), _p(self.Ep)
+        a.Dp, a.Ep, a.Xp = _p(self.Dp), _p(self.Ep), _p(self.Xp)
         for p in (0, 1):
             a.Ap[p], a.Bp[p], a.C[p] = _p(self.Ap[p]), _p(self.Bp[p]), _p(self.C[p])
         a.batches, a.M, a.K, a.N = 1, M, K, N

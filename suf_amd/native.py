@@ -213,7 +213,7 @@ class Chain2Args(ctypes.Structure):
 class KbPlanes(ctypes.Structure):
     """sufhip_kb_planes (include/suf_hip.h)."""
     _fields_ = [("planes", c_vp), ("batches", c_int), ("rows", c_int), ("cols", c_int),
-                ("k_is_col", c_int)]
+                ("k_is_col", c_int), ("planes_a0", c_vp), ("a0", c_vp)]
 
 
 class Lin2Job(ctypes.Structure):
@@ -227,19 +227,20 @@ class BeaverMfma2Args(ctypes.Structure):
     _fields_ = [("Dp", c_vp), ("Ep", c_vp), ("Ap", c_vp * 2), ("Bp", c_vp * 2), ("C", c_vp * 2),
                 ("batches", c_int), ("M", c_int), ("K", c_int), ("N", c_int), ("out", c_vp * 2),
                 ("merge_heads", c_int), ("trunc", ctypes.POINTER(TruncEpilogue)),
-                ("mask", c_u64), ("out_planes", XPlanes)]
+                ("mask", c_u64), ("out_planes", XPlanes), ("Xp", c_vp)]
 
 
 class KbSplitJob(ctypes.Structure):
     """sufhip_kb_split_job (include/suf_hip.h)."""
     _fields_ = [("src", c_vp), ("planes", c_vp), ("batches", c_int), ("rows", c_int),
-                ("cols", c_int), ("k_is_col", c_int)]
+                ("cols", c_int), ("k_is_col", c_int), ("planes_a0", c_vp), ("a0", c_vp)]
 
 
 class KbOpenJob(ctypes.Structure):
     """sufhip_kb_open_job (include/suf_hip.h)."""
     _fields_ = [("a", c_vp * 2), ("b", c_vp * 2), ("planes", c_vp), ("batches", c_int),
-                ("rows", c_int), ("cols", c_int), ("k_is_col", c_int)]
+                ("rows", c_int), ("cols", c_int), ("k_is_col", c_int), ("planes_a0", c_vp),
+                ("a0", c_vp)]
 
 
 class Triple2(ctypes.Structure):

@@ -117,11 +117,16 @@ def lin2(x, n, out=None, xhat=None, mask=0, into=None):
 
 
 def kb_planes_out(spec):
-    """sufhip_kb_planes from (planes, batches, rows, cols, k_is_col), or none."""
+    """sufhip_kb_planes from (planes, batches, rows, cols, k_is_col) or
+    (planes, batches, rows, cols, k_is_col, planes_a0, a0): the latter also
+    writes the planes of open + a0 (a0 a device tensor indexed like the
+    open), or none."""
     o = native.KbPlanes()
     if spec is not None:
         o.planes = ptr(spec[0])
         o.batches, o.rows, o.cols, o.k_is_col = spec[1], spec[2], spec[3], int(spec[4])
+        if len(spec) > 5:
+            o.planes_a0, o.a0 = ptr(spec[5]), ptr(spec[6])
     return o
 
 

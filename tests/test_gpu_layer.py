@@ -197,6 +197,76 @@ def test_beaver_matmul2_batched_vs_oracle(b, M, K, N):
             assert np.array_equal(u64(ref[p]), u64(out[p]))
 
 
+@pytest.mark.parametrize("b,M,K,N", [
+    (1, 32, 32, 32),      # one k-step: fewer operand pairs than pipeline stages
+    (3, 64, 96, 32),      # 6 pairs: not a multiple of the stage count
+    (2, 32, 160, 64),     # 10 pairs
+    (1, 128, 768, 3072),  # the config-3 product
+])
+def test_beaver_balanced_form_equals_three_product_form(b, M, K, N):
+    """With the planes of D + A_0 (Xp) each party's share takes two operand
+    products per k-step; the shares equal the three-product form's (no Xp),
+    and the oracle's for the small shapes."""
+    say("beaver balanced form b=%d %dx%dx%d" % (b, M, K, N))
+    tri = layer.BatchedTriples(Dealer(31), b, M, K, N)
+    g = np.random.default_rng(b * 7 + K)
+    D = g.integers(0, 2**64, b * M * K, dtype=np.uint64)
+    E = g.integers(0, 2**64, b * K * N, dtype=np.uint64)
+    D[:4] = [2**64 - 1, 2**63, 0x8080808080808080, 0x7F7F7F7F7F7F7F7F]
+    layer.kb_split(tri.split_jobs(dev(D), dev(E)))
+    outs = []
+    for balanced in (True, False):
+        a = tri.mfma_args()
+        if not balanced:
+            a.Xp = None
+        out = tuple(torch.empty(b * M * N, dtype=torch.int64, device="cuda") for _ in range(2))
+        a.out[0], a.out[1] = out[0].data_ptr(), out[1].data_ptr()
+        native.call("sufhip_beaver_matmul2_mfma_ex", native.ctypes.byref(a), 0)
+        outs.append([u64(o).reshape(b, M, N) for o in out])
+    for p in (0, 1):
+        assert np.array_equal(outs[0][p], outs[1][p]), p
+    if b * M * K * N <= 1 << 20:
+        A, B, C, A0, B0, C0 = tri.host
+        for i in range(b):
+            for p, (Ap, Bp, Cp) in enumerate(((A0, B0, C0), (A - A0, B - B0, C - C0))):
+                o = ol.beaver_matmul(p, D.reshape(b, M, K)[i], E.reshape(b, K, N)[i], Ap[i],
+                                     Bp[i], Cp[i], 1, M, K, N)
+                assert np.array_equal(outs[0][p][i].ravel(), np.asarray(o).ravel()), (i, p)
+
+
+@pytest.mark.parametrize("shape", [(1, 64, 96, 1), (2, 32, 64, 1), (1, 96, 64, 0)])
+def test_split_planes_a0_are_planes_of_value_plus_a0(shape):
+    """planes_a0 of a split and of an open-split job are the planes of the
+    value + a0, written in the same launch (every byte)."""
+    nb, r, c, kc = shape
+    say("split planes_a0 %s" % (shape,))
+    g = np.random.default_rng(11)
+    n = nb * r * c
+    src = dev(g.integers(0, 2**64, n, dtype=np.uint64))
+    a0 = dev(g.integers(0, 2**64, n, dtype=np.uint64))
+    a = tuple(dev(g.integers(0, 2**64, n, dtype=np.uint64)) for _ in range(2))
+    bb = tuple(dev(g.integers(0, 2**64, n, dtype=np.uint64)) for _ in range(2))
+    nbytes = native.load().sufhip_kb_planes_bytes(nb, r, c)
+    for value, job in ((src, lambda pl, px: layer.kb_split([(src, pl, nb, r, c, kc, px, a0)])),
+                       (a[0] + a[1] - bb[0] - bb[1],
+                        lambda pl, px: layer.kb_open_split([(a, bb, pl, nb, r, c, kc, px, a0)]))):
+        want, want_x = layer.kb_planes(nb, r, c), layer.kb_planes(nb, r, c)
+        layer.kb_split([(value, want, nb, r, c, kc), (value + a0, want_x, nb, r, c, kc)])
+        got, got_x = layer.kb_planes(nb, r, c), layer.kb_planes(nb, r, c)
+        got.fill_(0x5a5a)
+        got_x.fill_(0x5a5a)
+        job(got, got_x)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.uint8)[:nbytes], want.view(torch.uint8)[:nbytes])
+        assert torch.equal(got_x.view(torch.uint8)[:nbytes], want_x.view(torch.uint8)[:nbytes])
+    with pytest.raises(native.SufHipError, match="planes_a0 and a0"):
+        arr = (native.KbSplitJob * 1)()
+        arr[0].src, arr[0].planes = src.data_ptr(), want.data_ptr()
+        arr[0].batches, arr[0].rows, arr[0].cols, arr[0].k_is_col = nb, r, c, kc
+        arr[0].planes_a0 = want_x.data_ptr()  # without a0
+        native.call("sufhip_kb_split_batch", arr, 1, 0)
+
+
 def test_beaver_trunc_merged_matches_separate_launches():
     """PV with the context's truncation and head merge folded into the
     product's launch (sufhip_beaver_matmul2_mfma_ex) gives the shares of the

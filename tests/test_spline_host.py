@@ -103,7 +103,12 @@ def _c_offsets(struct, fields):
 
 @pytest.mark.parametrize("struct,cls", [("sufhip_composite_bool_args", "CompositeBoolArgs"),
                                         ("sufhip_stage_seg", "StageSeg"),
-                                        ("sufhip_open_req", "OpenReq")])
+                                        ("sufhip_open_req", "OpenReq"),
+                                        ("sufhip_kb_planes", "KbPlanes"),
+                                        ("sufhip_kb_split_job", "KbSplitJob"),
+                                        ("sufhip_kb_open_job", "KbOpenJob"),
+                                        ("sufhip_beaver_mfma2_args", "BeaverMfma2Args"),
+                                        ("sufhip_lin2_job", "Lin2Job")])
 def test_composite_struct_layouts_match_c(struct, cls):
     k = getattr(native, cls)
     want = _c_offsets(struct, [f[0] for f in k._fields_])
