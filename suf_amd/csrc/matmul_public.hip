@@ -95,23 +95,27 @@ struct PubArgs {
   TruncEpi epi;      // the open feeds this truncation gate (replaces zhat)
 };
 
-// k-steps of loads in flight per wave: two for the 2-digit weights of the
-// layer (10 fragments a step), one for 3- and 4-digit weights, whose second
-// step in flight would not fit beside the 128 accumulator registers.
+// k-steps in the register pipeline of a wave: step st's fragments are
+// loaded pub_stages - 1 steps before its MFMAs (8 + J fragments a step).
 template <int J>
-constexpr int pub_ahead() {
-  return J <= 2 ? 2 : 1;
+constexpr int pub_stages() {
+  return J <= 2 ? 5 : 3;
 }
 
 // Workgroup = two waves, wave p computing party p's 32 x 32 tile over one
 // k-slice; grid = (N / 32, M / 32, slices).  MFMA operand layout (checked on
 // the device for matmul_mfma.hip): lane l supplies row / column l % 32 at
 // k = 16 (l / 32) + byte; accumulator register r of lane l is row 8 (r / 4)
-// + 4 (l / 32) + r % 4, column l % 32.
+// + 4 (l / 32) + r % 4, column l % 32.  Plane addresses are a wave-uniform
+// base plus the lane's 32-bit fragment offset (the planes of X and W stay
+// below 4 GB, checked on the host), and the pipeline's buffers rotate by
+// unrolling, so the loads of later steps stay in flight across the MFMAs.
 template <int J>
-__global__ void __launch_bounds__(128, 2) public_mfma_kernel(PubArgs a) {
+__global__ void __launch_bounds__(128, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
+public_mfma_kernel(PubArgs a) {
   __shared__ uint64_t other[16][64];  // party 1's tile, for the open
-  const int l = threadIdx.x & 63, p = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63;
+  const int p = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int M = a.M, K = a.K, N = a.N;
   // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs
   // (each with its own L2), so workgroup id g runs on XCD g % 8.  Give XCD x
@@ -126,48 +130,58 @@ __global__ void __launch_bounds__(128, 2) public_mfma_kernel(PubArgs a) {
   const int steps = K / 32;
   const int s_begin = steps * slice / gz;
   const int s_end = steps * (slice + 1) / gz;
-  const size_t lrows = size_t(2) * M;
-  const size_t lplane = lrows * K, wplane = size_t(N) * K;
-  // This lane's 16 bytes of step s: row (or column) l % 32, bytes 16 (l / 32).
-  const int8_t* lbase = a.Lp + size_t(p * M + m0 + (l & 31)) * 32 + 16 * (l >> 5);
-  const int8_t* wbase = a.Wp + size_t(n0 + (l & 31)) * 32 + 16 * (l >> 5);
-  const size_t lstep = lrows * 32, wstep = size_t(N) * 32;
+  const uint32_t lrows = uint32_t(2) * M;
+  const uint32_t lplane = lrows * K, wplane = uint32_t(N) * K;
+  const uint32_t lstep = lrows * 32, wstep = uint32_t(N) * 32;
+  const uint32_t fo = uint32_t(l & 31) * 32 + 16 * uint32_t(l >> 5);
+  const int8_t* lbase = a.Lp + (uint32_t(p * M + m0) * 32);
+  const int8_t* wbase = a.Wp + uint32_t(n0) * 32;
   v16i acc[kPlanes];
 #pragma unroll
   for (int s = 0; s < kPlanes; ++s)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[s][r] = 0;
-  constexpr int kPubAhead = pub_ahead<J>();
-  v4i x[kPubAhead][kPlanes], w[kPubAhead][J];
+  constexpr int S = pub_stages<J>();
+  constexpr int kMfmas = J * kPlanes - J * (J - 1) / 2;  // digit products i + j < 8, j < J
+  v4i x[S][kPlanes], w[S][J];
+  auto issue = [&](int q, int st) {
+    st = st < s_end ? st : s_end - 1;  // past the slice: repeat its last step (skipped)
+    const uint32_t lo = uint32_t(st) * lstep, wo = uint32_t(st) * wstep;
 #pragma unroll
-  for (int q = 0; q < kPubAhead; ++q) {
-    const int st = s_begin + q < s_end ? s_begin + q : s_begin;  // in bounds
+    for (int i = 0; i < kPlanes; ++i) x[q][i] = load16(lbase + (i * lplane + lo) + fo);
 #pragma unroll
-    for (int i = 0; i < kPlanes; ++i) x[q][i] = load16(lbase + i * lplane + size_t(st) * lstep);
-#pragma unroll
-    for (int j = 0; j < J; ++j) w[q][j] = load16(wbase + j * wplane + size_t(st) * wstep);
-  }
-  for (int st = s_begin; st < s_end; ++st) {
+    for (int j = 0; j < J; ++j) w[q][j] = load16(wbase + (j * wplane + wo) + fo);
+  };
+  auto mfmas = [&](int q) {
 #pragma unroll
     for (int j = 0; j < J; ++j)
 #pragma unroll
       for (int i = 0; i + j < kPlanes; ++i)
-        acc[i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x[0][i], w[0][j], acc[i + j], 0, 0, 0);
+        acc[i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x[q][i], w[q][j], acc[i + j], 0, 0, 0);
+  };
+  // Whole groups of S steps without branches in the loop body (so the
+  // loads' waits stay counted), then the last n % S steps, whose loads the
+  // pipeline already issued into buffers 0 .. n % S - 1.
 #pragma unroll
-    for (int q = 0; q + 1 < kPubAhead; ++q) {
+  for (int q = 0; q < S - 1; ++q) issue(q, s_begin + q);
+  const int n = s_end - s_begin;
+  const int groups = n / S;
+  for (int g2 = 0; g2 < groups; ++g2) {
+    const int t0 = s_begin + g2 * S;
 #pragma unroll
-      for (int i = 0; i < kPlanes; ++i) x[q][i] = x[q + 1][i];
-#pragma unroll
-      for (int j = 0; j < J; ++j) w[q][j] = w[q + 1][j];
+    for (int h = 0; h < S; ++h) {
+      issue((h + S - 1) % S, t0 + h + S - 1);
+      mfmas(h);
+      // Order for the scheduler: this step's loads, then its MFMAs (which
+      // use the fragments loaded S - 1 steps earlier).
+      __builtin_amdgcn_sched_group_barrier(0x020, kPlanes + J, 0);  // VMEM reads
+      __builtin_amdgcn_sched_group_barrier(0x008, kMfmas, 0);       // MFMAs
     }
-    const int sn = st + kPubAhead < s_end ? st + kPubAhead : s_begin;  // in bounds
-#pragma unroll
-    for (int i = 0; i < kPlanes; ++i)
-      x[kPubAhead - 1][i] = load16(lbase + i * lplane + size_t(sn) * lstep);
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-      w[kPubAhead - 1][j] = load16(wbase + j * wplane + size_t(sn) * wstep);
   }
+  const int rest = n - groups * S;
+#pragma unroll
+  for (int h = 0; h < S - 1; ++h)
+    if (h < rest) mfmas(h);
   const int col = n0 + (l & 31);
   uint64_t v[16];
 #pragma unroll
@@ -207,6 +221,216 @@ __global__ void __launch_bounds__(128, 2) public_mfma_kernel(PubArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// The product for N a multiple of 64: a workgroup of four waves covers a
+// 32 x 64 output block for both parties, wave (p, c) party p's 32 x 32
+// sub-tile c.  A k-step's operand blocks -- both parties' 8 X planes and the
+// J W planes of the two sub-tiles, 1 KB each -- go once into LDS with
+// global_load_lds_dwordx4 (each lane's 16 bytes land at 16 lane in the
+// block, which is the MFMA fragment layout) through a kPubStages-deep ring,
+// and each wave reads its 8 + J fragments from there: the workgroup loads
+// each X fragment once instead of once per column tile and each W fragment
+// once instead of once per party.  The DMA of step t + kPubStages - 1 is
+// issued after the barrier of step t (when every wave is done with the
+// stage it overwrites); every wave issues the same number of DMAs each step
+// (dummy blocks pad the stage), so a fixed vmcnt waits for step t exactly.
+// The LDS reads are one asm statement with their wait, so no instruction
+// can touch their registers before the data is there.
+constexpr int kPubStages = 3;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+
+__device__ __forceinline__ void dma16(const int8_t* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)l, 16, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((const lds_u8_t*)p));
+}
+
+// s_waitcnt with vmcnt(N) only (expcnt and lgkmcnt at their maxima).
+template <int N>
+constexpr int vm_wait_imm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  return (N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
+// Blocks of one stage: 16 X planes (party p plane i at 8 p + i), 2 J W
+// planes (sub-tile c plane j at 16 + c J + j), padded to a multiple of the
+// four waves.
+template <int J>
+constexpr int stage_blocks() {
+  return (16 + 2 * J + 3) / 4 * 4;
+}
+
+#define SUFHIP_RD(n, reg, off) "ds_read_b128 %" #n ", %" #reg " offset:" #off "\n"
+#define SUFHIP_RD_X8(xr)                                                                     \
+  SUFHIP_RD(0, xr, 0) SUFHIP_RD(1, xr, 1024) SUFHIP_RD(2, xr, 2048) SUFHIP_RD(3, xr, 3072)    \
+  SUFHIP_RD(4, xr, 4096) SUFHIP_RD(5, xr, 5120) SUFHIP_RD(6, xr, 6144) SUFHIP_RD(7, xr, 7168)
+#define SUFHIP_XOUT                                                                          \
+  "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]), "=&v"(x[6]), \
+      "=&v"(x[7])
+
+// x: the 8 X fragments at ax (1 KB apart); w: the J W fragments at aw.
+template <int J>
+__device__ __forceinline__ void rd_frags(v4i (&x)[kPlanes], v4i (&w)[J], uint32_t ax, uint32_t aw);
+template <>
+__device__ __forceinline__ void rd_frags<1>(v4i (&x)[kPlanes], v4i (&w)[1], uint32_t ax,
+                                            uint32_t aw) {
+  asm volatile(SUFHIP_RD_X8(9) SUFHIP_RD(8, 10, 0) "s_waitcnt lgkmcnt(0)"
+               : SUFHIP_XOUT, "=&v"(w[0])
+               : "v"(ax), "v"(aw));
+}
+template <>
+__device__ __forceinline__ void rd_frags<2>(v4i (&x)[kPlanes], v4i (&w)[2], uint32_t ax,
+                                            uint32_t aw) {
+  asm volatile(SUFHIP_RD_X8(10) SUFHIP_RD(8, 11, 0) SUFHIP_RD(9, 11, 1024) "s_waitcnt lgkmcnt(0)"
+               : SUFHIP_XOUT, "=&v"(w[0]), "=&v"(w[1])
+               : "v"(ax), "v"(aw));
+}
+template <>
+__device__ __forceinline__ void rd_frags<3>(v4i (&x)[kPlanes], v4i (&w)[3], uint32_t ax,
+                                            uint32_t aw) {
+  asm volatile(SUFHIP_RD_X8(11) SUFHIP_RD(8, 12, 0) SUFHIP_RD(9, 12, 1024)
+                   SUFHIP_RD(10, 12, 2048) "s_waitcnt lgkmcnt(0)"
+               : SUFHIP_XOUT, "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2])
+               : "v"(ax), "v"(aw));
+}
+template <>
+__device__ __forceinline__ void rd_frags<4>(v4i (&x)[kPlanes], v4i (&w)[4], uint32_t ax,
+                                            uint32_t aw) {
+  asm volatile(SUFHIP_RD_X8(12) SUFHIP_RD(8, 13, 0) SUFHIP_RD(9, 13, 1024)
+                   SUFHIP_RD(10, 13, 2048) SUFHIP_RD(11, 13, 3072) "s_waitcnt lgkmcnt(0)"
+               : SUFHIP_XOUT, "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
+               : "v"(ax), "v"(aw));
+}
+#undef SUFHIP_RD
+#undef SUFHIP_RD_X8
+#undef SUFHIP_XOUT
+
+template <int J>
+__global__ void __launch_bounds__(256, 1) public_lds_kernel(PubArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int kBlocks = stage_blocks<J>();
+  constexpr int kPerWave = kBlocks / 4;
+  constexpr int kStageBytes = kBlocks * 1024;
+  const int l = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int p = w >> 1, c = w & 1;
+  const int M = a.M, K = a.K, N = a.N;
+  const int gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
+  const int total = gx * gy * gz;
+  int g = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  if (total % 8 == 0) g = (g % 8) * (total / 8) + g / 8;  // XCD-aware order, as above
+  const int slice = g % gz, tile_y = (g / gz) % gy, tile_x = g / (gz * gy);
+  const int m0 = tile_y * 32, n0 = tile_x * 64;
+  const int steps = K / 32;
+  const int s_begin = steps * slice / gz;
+  const int s_end = steps * (slice + 1) / gz;
+  const uint32_t lplane = uint32_t(2) * M * K, wplane = uint32_t(N) * K;
+  const uint32_t lstep = uint32_t(2) * M * 32, wstep = uint32_t(N) * 32;
+  const uint32_t fo = uint32_t(l & 31) * 32 + 16 * uint32_t(l >> 5);
+  // This wave's DMA blocks: b = w kPerWave + q; block bases are uniform.
+  const int8_t* gb[kPerWave];
+  uint32_t gs[kPerWave];
+#pragma unroll
+  for (int q = 0; q < kPerWave; ++q) {
+    int b = w * kPerWave + q;
+    if (b >= 16 + 2 * J) b = 0;  // padding: a valid block, never read
+    if (b < 16) {
+      gb[q] = a.Lp + (uint32_t(b & 7) * lplane + uint32_t((b >> 3) * M + m0) * 32);
+      gs[q] = lstep;
+    } else {
+      const int cc = (b - 16) / J, j = (b - 16) % J;
+      gb[q] = a.Wp + (uint32_t(j) * wplane + uint32_t(n0 + 32 * cc) * 32);
+      gs[q] = wstep;
+    }
+  }
+  auto dma = [&](int stage, int st) {
+    st = st < s_end ? st : s_end - 1;  // past the slice: its last step again (never read)
+    uint8_t* dst = lds + stage * kStageBytes + (w * kPerWave) * 1024;
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) dma16(gb[q] + (uint32_t(st) * gs[q] + fo), dst + q * 1024);
+  };
+  v16i acc[kPlanes];
+#pragma unroll
+  for (int s = 0; s < kPlanes; ++s)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[s][r] = 0;
+  const int n = s_end - s_begin;
+#pragma unroll
+  for (int q = 0; q < kPubStages - 1; ++q) dma(q, s_begin + q);
+  const uint32_t lane_base = lds_addr(lds) + 16 * uint32_t(l);
+  const uint32_t xoff = uint32_t(8 * p) * 1024, woff = uint32_t(16 + c * J) * 1024;
+  int stage = 0;
+  for (int t = 0; t < n; ++t) {
+    __builtin_amdgcn_s_waitcnt(vm_wait_imm<(kPubStages - 2) * kPerWave>());
+    __builtin_amdgcn_s_barrier();
+    dma(stage == 0 ? kPubStages - 1 : stage - 1, s_begin + t + kPubStages - 1);
+    const uint32_t sb = lane_base + uint32_t(stage) * kStageBytes;
+    v4i x[kPlanes], wf[J];
+    rd_frags<J>(x, wf, sb + xoff, sb + woff);
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int i = 0; i + j < kPlanes; ++i)
+        acc[i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x[i], wf[j], acc[i + j], 0, 0, 0);
+    stage = stage + 1 == kPubStages ? 0 : stage + 1;
+  }
+  __builtin_amdgcn_s_waitcnt(vm_wait_imm<0>());  // no DMA may land after the ring is reused
+  const int col = n0 + 32 * c + (l & 31);
+  uint64_t v[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    v[r] = 0;
+#pragma unroll
+    for (int s = 0; s < kPlanes; ++s) v[r] += uint64_t(int64_t(acc[s][r])) << (8 * s);
+  }
+  if (gz > 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+      a.part[((size_t(slice) * 2 + p) * M + row) * N + col] = v[r];
+    }
+    return;
+  }
+  if (a.out[p]) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+      a.out[p][size_t(row) * N + col] = v[r];
+    }
+  }
+  if (a.zhat || a.epi.on) {
+    // Both parties' sub-tiles through LDS (the ring is free); wave (p, c)
+    // then opens rows r in [8 p, 8 p + 8) of sub-tile c.
+    __syncthreads();
+    uint64_t(*both)[2][16][64] = reinterpret_cast<uint64_t(*)[2][16][64]>(lds);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) both[c][p][r][l] = v[r];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int r = 8 * p + q;
+      const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+      put_open(a.epi, a.zhat, size_t(row) * N + col, both[c][0][r][l] + both[c][1][r][l] + a.mask);
+    }
+  }
+}
+
+// The ring's dynamic LDS (60-72 KB; above 64 KB the kernel must allow it).
+template <int J>
+size_t public_lds_bytes() {
+  static const int allowed = [] {
+    return int(hipFuncSetAttribute(reinterpret_cast<const void*>(&public_lds_kernel<J>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   int(size_t(kPubStages) * stage_blocks<J>() * 1024)));
+  }();
+  (void)allowed;
+  return size_t(kPubStages) * stage_blocks<J>() * 1024;
+}
+
 // Slices -> shares and/or the masked open.
 __global__ void __launch_bounds__(256)
     public_reduce_kernel(const uint64_t* part, int slices, size_t mn, uint64_t* out0,
@@ -223,20 +447,28 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// k-slices so that a launch has about 512 workgroups (two waves each) and a
-// slice has at least four k-steps.
+// k-slices so that every wave of a launch is resident at once (one wave per
+// SIMD: 256 four-wave workgroups of 32 x 64 blocks, or 512 two-wave ones of
+// 32 x 32 tiles when N is not a multiple of 64) and a slice has at least
+// four k-steps; one slice needs no reduction pass.
 int pub_slices(int M, int K, int N) {
-  const int tiles = (M / 32) * (N / 32);
+  const bool wide = N % 64 == 0;
+  const int tiles = (M / 32) * (N / (wide ? 64 : 32));
+  const int cap = wide ? 256 : 512;
   const int steps = K / 32;
-  int s = tiles >= 512 ? 1 : (512 + tiles - 1) / tiles;
+  int s = tiles >= cap ? 1 : cap / tiles;
   if (s > 8) s = 8;
   if (s > steps / 4) s = steps / 4 > 0 ? steps / 4 : 1;
   return s;
 }
 
 bool shape_ok(int M, int K, int N) {
+  // The kernel addresses the 8 X planes (2M rows) and the W planes (up to 8)
+  // with 32-bit offsets.
   return M > 0 && K > 0 && N > 0 && M % 32 == 0 && N % 32 == 0 && K % 32 == 0 &&
-         size_t(K) < (size_t(1) << 16);
+         size_t(K) < (size_t(1) << 16) &&
+         uint64_t(kPlanes) * 2 * uint64_t(M) * uint64_t(K) < (uint64_t(1) << 32) &&
+         uint64_t(kPlanes) * uint64_t(N) * uint64_t(K) < (uint64_t(1) << 32);
 }
 
 }  // namespace
@@ -310,14 +542,33 @@ int launch_public2(const char* what, const int8_t* Lp, int M, int K, int N,
   uint64_t* part =
       reinterpret_cast<uint64_t*>(static_cast<int8_t*>(d_work) + size_t(kPlanes) * 2 * M * K);
   PubArgs a{Lp, d_planes, M, K, N, {d_out0, d_out1}, d_zhat, mask, part, epi};
-  const dim3 grid(N / 32, M / 32, sl);
-  switch (digits) {
-    case 1: hipLaunchKernelGGL(public_mfma_kernel<1>, grid, dim3(128), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(public_mfma_kernel<2>, grid, dim3(128), 0, s, a); break;
-    case 3: hipLaunchKernelGGL(public_mfma_kernel<3>, grid, dim3(128), 0, s, a); break;
-    default: hipLaunchKernelGGL(public_mfma_kernel<4>, grid, dim3(128), 0, s, a); break;
+  if (N % 64 == 0) {
+    const dim3 grid(N / 64, M / 32, sl);
+    switch (digits) {
+      case 1:
+        hipLaunchKernelGGL(public_lds_kernel<1>, grid, dim3(256), public_lds_bytes<1>(), s, a);
+        break;
+      case 2:
+        hipLaunchKernelGGL(public_lds_kernel<2>, grid, dim3(256), public_lds_bytes<2>(), s, a);
+        break;
+      case 3:
+        hipLaunchKernelGGL(public_lds_kernel<3>, grid, dim3(256), public_lds_bytes<3>(), s, a);
+        break;
+      default:
+        hipLaunchKernelGGL(public_lds_kernel<4>, grid, dim3(256), public_lds_bytes<4>(), s, a);
+        break;
+    }
+    if (int rc = check_launch("public_lds_kernel")) return rc;
+  } else {
+    const dim3 grid(N / 32, M / 32, sl);
+    switch (digits) {
+      case 1: hipLaunchKernelGGL(public_mfma_kernel<1>, grid, dim3(128), 0, s, a); break;
+      case 2: hipLaunchKernelGGL(public_mfma_kernel<2>, grid, dim3(128), 0, s, a); break;
+      case 3: hipLaunchKernelGGL(public_mfma_kernel<3>, grid, dim3(128), 0, s, a); break;
+      default: hipLaunchKernelGGL(public_mfma_kernel<4>, grid, dim3(128), 0, s, a); break;
+    }
+    if (int rc = check_launch("public_mfma_kernel")) return rc;
   }
-  if (int rc = check_launch("public_mfma_kernel")) return rc;
   if (sl == 1) return SUFHIP_OK;
   const size_t mn = size_t(M) * N;
   size_t g = (mn + 255) / 256;

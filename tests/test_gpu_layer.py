@@ -51,7 +51,10 @@ def _pair(x, seed):
 
 @pytest.mark.parametrize("M,K,N,wmax", [(32, 64, 96, 100), (64, 96, 64, 30000),
                                         (128, 768, 2304, 400), (32, 32, 32, 1 << 20),
-                                        (128, 3072, 768, 500)])
+                                        (128, 3072, 768, 500),
+                                        # N % 64 == 0 (LDS-shared form) with 1, 3, 4 weight digits
+                                        (96, 64, 64, 1), (64, 128, 128, 1 << 20),
+                                        (32, 224, 192, 1 << 30), (32, 1024, 64, 1 << 20)])
 def test_public_matmul_shares(M, K, N, wmax):
     rng = np.random.default_rng(M + K + N)
     W = rng.integers(-wmax, wmax + 1, size=(K, N)).astype(np.int64)
