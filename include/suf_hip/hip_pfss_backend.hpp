@@ -5,11 +5,15 @@
 //
 // DCF keys are real two-party myl7/fss v0.7.1 keys (128-bit seeds, AES-128-MMO
 // PRG) in the Myl7FssBackend blob layout (include/proto/myl7_fss_backend.hpp:
-// 131-213); keygen and evaluation run on the GPU.  Output group: XOR of bytes
-// for 1-byte payloads (XorBytes predicates, the group SUF links), addition
-// mod 2^127 -- so additive mod 2^64 in the low 8 bytes -- for longer payloads
-// (AddU64 predicates and coefficient payloads).  Interval-LUT and packed
-// compare keys use the GpuPfssBackend blob formats and kernel counters.
+// 131-213); keygen and evaluation run on the GPU.  Output group: with
+// Params::xor_payloads, XOR of bytes for every payload length -- the group SUF
+// links myl7 with (third_party/myl7_fss/src/group/bytes.c), so keys made by
+// Myl7FssBackend evaluate as there; by default XOR for 1-byte payloads
+// (XorBytes predicates) and addition mod 2^127 -- additive mod 2^64 in the
+// low 8 bytes -- for longer payloads (AddU64 predicates and coefficient
+// payloads).  A key blob does not record its group: keys made under one
+// setting evaluate correctly only under the same setting.  Interval-LUT and
+// packed compare keys use the GpuPfssBackend blob formats and kernel counters.
 //
 // Conventions follow the reference: one instance per party, calls serialized
 // by an internal mutex, host-output calls return after the device-to-host
@@ -39,6 +43,10 @@ class HipPfssBackend final : public proto::PfssIntervalLutExt,
     // 0: DCF seeds from std::random_device (as Myl7FssBackend); otherwise
     // std::mt19937_64(seed) for reproducible key material.
     uint64_t seed = 0;
+    // true: the XOR byte group for every DCF payload length (Myl7FssBackend's
+    // keys and outputs); false: XOR for 1-byte payloads, addition mod 2^127
+    // for longer ones.
+    bool xor_payloads = false;
   };
 
   HipPfssBackend();
@@ -113,6 +121,7 @@ class HipPfssBackend final : public proto::PfssIntervalLutExt,
                     uint8_t* outs_host) const;
   void sync() const;
   std::vector<uint8_t> random_bytes(size_t n);
+  int group_for(int payload_len) const;
 
   Params params_;
   void* stream_ = nullptr;

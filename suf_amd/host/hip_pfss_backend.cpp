@@ -71,7 +71,6 @@ DcfHeader dcf_header(const uint8_t* k, size_t key_bytes) {
   return h;
 }
 
-int group_for(int payload_len) { return payload_len == 1 ? SUFHIP_GROUP_XOR : SUFHIP_GROUP_ADD; }
 
 void check_dcf_keys(int in_bits, size_t key_bytes, const DcfHeader& h) {
   if (h.in_bits != in_bits) throw std::runtime_error("HipPfssBackend: in_bits mismatch");
@@ -80,6 +79,10 @@ void check_dcf_keys(int in_bits, size_t key_bytes, const DcfHeader& h) {
 }
 
 }  // namespace
+
+int HipPfssBackend::group_for(int payload_len) const {
+  return params_.xor_payloads || payload_len == 1 ? SUFHIP_GROUP_XOR : SUFHIP_GROUP_ADD;
+}
 
 void HipPfssBackend::set_prg_state(const uint8_t state[128]) {
   std::lock_guard<std::mutex> lk(g_prg_mu);

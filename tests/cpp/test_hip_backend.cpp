@@ -9,6 +9,7 @@
 #include <functional>
 #include <random>
 #include <stdexcept>
+#include <string>
 #include <thread>
 #include <vector>
 
@@ -276,7 +277,98 @@ static void test_factory() {
   CHECK(suf_hip::make_hip_backend_from_env() == nullptr, "other kinds are not ours");
 }
 
-int main() {
+static std::vector<uint8_t> unhex(const std::string& h) {
+  std::vector<uint8_t> v(h.size() / 2);
+  for (size_t i = 0; i < v.size(); ++i) v[i] = uint8_t(std::stoul(h.substr(2 * i, 2), nullptr, 16));
+  return v;
+}
+
+// Keys the reference's own myl7 adapter made (XOR group, tests/golden/
+// dcf_myl7.json, written out as text by the pytest wrapper), evaluated by an
+// instance with xor_payloads: every payload share byte-equal to the
+// reference's through eval_dcf, and through eval_dcf_many_u64 (share byte
+// 0 & 1 on a 1-byte key, as the reference's batch), for 1-, 8- and 16-byte
+// payloads.  The default instance gives the additive group for the
+// multi-byte keys, so its shares differ there.
+//   prg <hex 128 bytes>
+//   case <in_bits> <payload_len> <key0 hex> <key1 hex> <n>
+//   x <u64> <out0 hex> <out1 hex>     (n lines)
+static int run_golden(const char* path) {
+  std::FILE* f = std::fopen(path, "r");
+  if (!f) {
+    std::fprintf(stderr, "cannot open %s\n", path);
+    return 2;
+  }
+  char tok[16];
+  char buf[8192], b2[8192], b3[8192];
+  if (std::fscanf(f, "%15s %8191s", tok, buf) != 2 || std::string(tok) != "prg") return 2;
+  const std::vector<uint8_t> prg = unhex(buf);
+  HipPfssBackend::set_prg_state(prg.data());
+  HipPfssBackend::Params xp;
+  xp.xor_payloads = true;
+  HipPfssBackend bx(xp), bdef;
+  int cases = 0, multi = 0, differ = 0;
+  int in_bits, plen, n;
+  while (std::fscanf(f, "%15s %d %d %8191s %8191s %d", tok, &in_bits, &plen, buf, b2, &n) == 6) {
+    proto::FssKey k[2];
+    k[0].bytes = unhex(buf);
+    k[1].bytes = unhex(b2);
+    std::vector<uint64_t> xs;
+    std::vector<std::vector<uint8_t>> want[2];
+    for (int i = 0; i < n; ++i) {
+      unsigned long long x;
+      if (std::fscanf(f, "%15s %llu %8191s %8191s", tok, &x, b2, b3) != 4) return 2;
+      xs.push_back(x);
+      want[0].push_back(unhex(b2));
+      want[1].push_back(unhex(b3));
+    }
+    for (int p = 0; p < 2; ++p) {
+      std::vector<uint8_t> many(size_t(n) * plen);
+      bx.eval_dcf_many_u64(in_bits, k[p].bytes.size(), flatten(k[p], size_t(n)).data(), xs, plen,
+                           many.data());
+      for (int i = 0; i < n; ++i) {
+        const std::vector<uint8_t> one = bx.eval_dcf(in_bits, k[p], bx.u64_to_bits_msb(xs[i], in_bits));
+        // The batch keeps share byte 0 & 1 on a 1-byte key (the reference's
+        // eval_dcf_many_u64), the payload share otherwise.
+        std::vector<uint8_t> want_many = want[p][i];
+        if (plen == 1) want_many[0] &= 1;
+        if (one != want[p][i] || std::memcmp(many.data() + size_t(i) * plen, want_many.data(), plen)) {
+          std::fprintf(stderr, "golden case %d (in_bits %d, payload %d) party %d x %d differs\n",
+                       cases, in_bits, plen, p, i);
+          ++g_fail;
+        }
+        if (plen > 1) {
+          const std::vector<uint8_t> d = bdef.eval_dcf(in_bits, k[p], bdef.u64_to_bits_msb(xs[i], in_bits));
+          differ += d != want[p][i];
+        }
+      }
+    }
+    ++cases;
+    multi += plen > 1;
+  }
+  std::fclose(f);
+  if (cases == 0 || multi == 0) {
+    std::fprintf(stderr, "golden fixture has %d cases, %d with multi-byte payloads\n", cases, multi);
+    return 1;
+  }
+  if (differ == 0) {
+    std::fprintf(stderr, "the additive default gave the XOR shares on every multi-byte key\n");
+    ++g_fail;
+  }
+  if (g_fail) return 1;
+  std::printf("golden xor keys: %d cases (%d multi-byte) passed\n", cases, multi);
+  return 0;
+}
+
+int main(int argc, char** argv) {
+  if (argc > 2 && std::string(argv[1]) == "golden") {
+    try {
+      return run_golden(argv[2]);
+    } catch (const std::exception& e) {
+      std::fprintf(stderr, "exception: %s\n", e.what());
+      return 2;
+    }
+  }
   uint8_t state[128];
   std::mt19937_64 g(3);
   for (auto& b : state) b = uint8_t(g() & 0xFF);
