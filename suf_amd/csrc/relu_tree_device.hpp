@@ -4,9 +4,11 @@
 // AES-CTR keystream, pfss_kernels.cu:545-719).  Shared by the tree kernel
 // (lut.hip) and the softmax row block (blocks.hip).
 //
-// A lane works on one (slot, party) item, so one AES block per item; the
-// keystream counters are those of the per-round evaluation (slot j = the
-// row's offset in that round's output + pair index).  Level 0 of a row (its
+// A slot's AES block is spread over a lane quad, one state column per lane
+// (AesLds::encrypt_quad_n), one block for both parties when their blobs
+// share the keystream; the keystream counters are those of the per-round
+// evaluation (slot j = the row's offset in that round's output + pair
+// index).  Level 0 of a row (its
 // inputs) and the odd levels live in two LDS buffers per wave, [party]
 // [max_row] and [party][ceil(max_row / 2)]; a level never outgrows the buffer
 // it is written to.  Every wave of a workgroup runs the same number of
@@ -173,13 +175,117 @@ __device__ __forceinline__ int tree_interval(const TreeKeys<kRounds>& K,
   return lo - 1 < 0 ? 0 : lo - 1;
 }
 
+// One chunk of a level: pair slots t0 .. t0 + nb - 1 (nb <= 64), each AES
+// block spread over a lane quad (AesLds::encrypt_quad_n).  Quad m = lane / 4
+// encrypts slots t0 + m + 16u for u < U (U = ceil(nb / 16)), so a level of
+// at most 16 pairs costs one block's quad latency instead of a lane's whole
+// block.  Every lane of the quad computes the slot's x^ and interval (the
+// same LDS reads, broadcast); afterwards lane q of quad m gathers block q's
+// four columns (DPP quad broadcasts) and writes slot t0 + m + 16q.  All 64
+// lanes run it (the DPP reads need whole quads); slots past nb compute on a
+// clamped slot and write nothing.
+template <int U, int kRounds, class Aes>
+__device__ __forceinline__ void tree_chunk(const TreeKeys<kRounds>& K, const TreeLds<kRounds>& L,
+                                           const Aes& aes, int k, const uint64_t* src, int sw,
+                                           uint64_t* dst, int dw, uint32_t j0, int t0, int nb,
+                                           bool one_ks) {
+  const int lane = threadIdx.x & 63, q = lane & 3, m = lane >> 2;
+  uint64_t xh[U], xb[U][2];
+  int iv[U][2];
+  uint32_t blk[2][U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int t = t0 + (m + 16 * u < nb ? m + 16 * u : 0);
+    const uint64_t xa0 = src[2 * t], xb0 = src[2 * t + 1];
+    const uint64_t xa1 = src[sw + 2 * t], xb1 = src[sw + 2 * t + 1];
+    xh[u] = (xa0 - xb0) + (xa1 - xb1) + K.mask[k];
+    xb[u][0] = xb0;
+    xb[u][1] = xb1;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      iv[u][p] = (p == 1 && one_ks) ? iv[u][0] : tree_interval(K, L, k, p, xh[u]);
+      const uint64_t ctr =
+          L.nonce[k][p] ^ (uint64_t(j0 + uint32_t(t)) << 32) ^ (uint64_t(iv[u][p]) * 2);
+      blk[p][u] = q == 0 ? uint32_t(ctr) : (q == 1 ? uint32_t(ctr >> 32) : 0u);
+    }
+  }
+  {
+    const uint32_t* rk0 = reinterpret_cast<const uint32_t*>(L.rk[k][0]) + q;
+    const uint32_t* rk1 = reinterpret_cast<const uint32_t*>(L.rk[k][1]) + q;
+    const uint32_t* rks[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) rks[u] = rk0;
+    aes.template encrypt_quad_n<U>(blk[0], rks);
+    if (one_ks) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) blk[1][u] = blk[0][u];
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) rks[u] = rk1;
+      aes.template encrypt_quad_n<U>(blk[1], rks);
+    }
+  }
+  // Lane q takes block q: column c of it is lane c's word of blk[.][q].
+  uint32_t w[2][4];
+  uint64_t x = 0, b[2] = {0, 0};
+  int ivq[2] = {0, 0};
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w[p][c] = 0;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t c0 = quad_bcast<0>(blk[0][u]), c1 = quad_bcast<1>(blk[0][u]);
+    const uint32_t c2 = quad_bcast<2>(blk[0][u]), c3 = quad_bcast<3>(blk[0][u]);
+    uint32_t d0 = c0, d1 = c1, d2 = c2, d3 = c3;
+    if (!one_ks) {
+      d0 = quad_bcast<0>(blk[1][u]);
+      d1 = quad_bcast<1>(blk[1][u]);
+      d2 = quad_bcast<2>(blk[1][u]);
+      d3 = quad_bcast<3>(blk[1][u]);
+    }
+    if (q == u) {
+      w[0][0] = c0;
+      w[0][1] = c1;
+      w[0][2] = c2;
+      w[0][3] = c3;
+      w[1][0] = d0;
+      w[1][1] = d1;
+      w[1][2] = d2;
+      w[1][3] = d3;
+      x = xh[u];
+      b[0] = xb[u][0];
+      b[1] = xb[u][1];
+      ivq[0] = iv[u][0];
+      ivq[1] = iv[u][1];
+    }
+  }
+  const int slot = m + 16 * q;
+  if (q < U && slot < nb) {
+    uint64_t o[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const uint64_t k0 = uint64_t(w[p][0]) | uint64_t(w[p][1]) << 32;
+      const uint64_t k1 = uint64_t(w[p][2]) | uint64_t(w[p][3]) << 32;
+      const bool p0 = L.party[k][p] == 0;
+      const uint64_t q0 = p0 ? k0 : L.pay[k][p][2 * ivq[p]] - k0;
+      const uint64_t q1 = p0 ? k1 : L.pay[k][p][2 * ivq[p] + 1] - k1;
+      o[p] = b[p] + q0 + q1 * x;
+    }
+    dst[t0 + slot] = o[0];
+    dst[dw + t0 + slot] = o[1];
+  }
+}
+
 // Runs every round over this wave's row of `len` elements whose level 0 is
 // in even[0..len) (party 0) and even[mr..mr+len) (party 1); j0[k] is the
 // row's first slot in round k (tree_row_offsets, written before a barrier);
 // bit k of `shared` is clear in L.diff (tree_compare).  Returns the level count; the row's max is
 // at index 0 of the final level's buffer (even if the count is even, odd
 // otherwise; party stride mr or ceil(mr / 2)).  Every thread of the
-// workgroup must call it (len 0 for an idle wave).
+// workgroup must call it (len 0 for an idle wave).  Slot t of a level is
+// pair (2t, 2t + 1) of the level below; an odd level's last element passes
+// through as its last slot.
 template <int kRounds, class Aes>
 __device__ __forceinline__ int tree_row(const TreeKeys<kRounds>& K, const TreeLds<kRounds>& L,
                                         const Aes& aes, uint64_t* even,
@@ -193,53 +299,25 @@ __device__ __forceinline__ int tree_row(const TreeKeys<kRounds>& K, const TreeLd
       const int sw = (level & 1) ? half : mr;  // party stride of src
       uint64_t* dst = (level & 1) ? even : odd;
       const int dw = (level & 1) ? mr : half;
-      const int pairs = len >> 1, nlen = (len + 1) >> 1;
+      const int pairs = len >> 1;
       const uint32_t j0 = j0s[k];
       const bool one_ks = (shared >> k) & 1u;
-      // A lane per slot, both parties: one keystream block when the blobs
-      // share it, else one per party (in lockstep).
-      for (int t = lane; t < nlen; t += 64) {
-        uint64_t o[2];
-        if (t < pairs) {
-          const uint64_t xa0 = src[2 * t], xb0 = src[2 * t + 1];
-          const uint64_t xa1 = src[sw + 2 * t], xb1 = src[sw + 2 * t + 1];
-          const uint64_t xhat = (xa0 - xb0) + (xa1 - xb1) + K.mask[k];
-          int iv[2];
-          uint32_t st[2][4];
-          for (int p = 0; p < 2; ++p) {
-            iv[p] = (p == 1 && one_ks) ? iv[0] : tree_interval(K, L, k, p, xhat);
-            const uint64_t ctr = L.nonce[k][p] ^ (uint64_t(j0 + uint32_t(t)) << 32) ^
-                                 (uint64_t(iv[p]) * 2);
-            st[p][0] = uint32_t(ctr);
-            st[p][1] = uint32_t(ctr >> 32);
-            st[p][2] = 0;
-            st[p][3] = 0;
-          }
-          if (one_ks) {
-            aes.encrypt(st[0][0], st[0][1], st[0][2], st[0][3], L.rk[k][0]);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) st[1][q] = st[0][q];
-          } else {
-            const uint4* rks[2] = {L.rk[k][0], L.rk[k][1]};
-            aes.template encrypt_n<2>(st, rks);
-          }
-#pragma unroll
-          for (int p = 0; p < 2; ++p) {
-            const uint64_t k0 = uint64_t(st[p][0]) | uint64_t(st[p][1]) << 32;
-            const uint64_t k1 = uint64_t(st[p][2]) | uint64_t(st[p][3]) << 32;
-            const bool p0 = L.party[k][p] == 0;
-            const uint64_t q0 = p0 ? k0 : L.pay[k][p][2 * iv[p]] - k0;
-            const uint64_t q1 = p0 ? k1 : L.pay[k][p][2 * iv[p] + 1] - k1;
-            o[p] = (p ? xb1 : xb0) + q0 + q1 * xhat;
-          }
-        } else {
-          o[0] = src[2 * t];
-          o[1] = src[sw + 2 * t];
-        }
-        dst[t] = o[0];
-        dst[dw + t] = o[1];
+      for (int t0 = 0; t0 < pairs; t0 += 64) {
+        const int nb = pairs - t0 < 64 ? pairs - t0 : 64;
+        if (nb > 48)
+          tree_chunk<4>(K, L, aes, k, src, sw, dst, dw, j0, t0, nb, one_ks);
+        else if (nb > 32)
+          tree_chunk<3>(K, L, aes, k, src, sw, dst, dw, j0, t0, nb, one_ks);
+        else if (nb > 16)
+          tree_chunk<2>(K, L, aes, k, src, sw, dst, dw, j0, t0, nb, one_ks);
+        else
+          tree_chunk<1>(K, L, aes, k, src, sw, dst, dw, j0, t0, nb, one_ks);
       }
-      len = nlen;
+      if ((len & 1) && lane == 0) {
+        dst[pairs] = src[2 * pairs];
+        dst[dw + pairs] = src[sw + 2 * pairs];
+      }
+      len = (len + 1) >> 1;
       ++level;
     }
     __syncthreads();

@@ -355,11 +355,6 @@ __device__ __forceinline__ uint32_t row_shr4(uint32_t v) {
   return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x114, 0xf, 0xf, false));
 }
 
-template <int kLane>
-__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
-  return uint32_t(__builtin_amdgcn_mov_dpp(int(v), kLane * 0x55, 0xf, 0xf, false));
-}
-
 struct Walk8Ctx {
   const DcfAes& aes;
   const uint4* rkl;

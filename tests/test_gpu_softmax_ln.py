@@ -83,6 +83,31 @@ def test_row_max_diff_shares(offsets, fused):
     assert np.array_equal((g[0] + g[1]).astype(np.uint64), want)
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_row_max_diff_per_party_keystreams(fused):
+    """Party 1's round keys with another keystream nonce (one bit flipped in
+    its blob, on the host and the device copy): the kernels find the two
+    blobs different and run one keystream per party; each party's shares
+    still equal the oracle's evaluation of its own blob.  (The two shares no
+    longer reconstruct the row maximum, as with any two unrelated blobs.)"""
+    offsets = np.cumsum([0, 1, 2, 3, 300, 5, 64, 7, 128, 17]).astype(np.int64)
+    x = _scores(offsets, 23)
+    x0, x1 = _share(x, 24)
+    say("row max diff, one keystream per party, n=%d fused=%s" % (offsets[-1], fused))
+    rm = softmax.RowMaxDiff(offsets, softmax.Dealer(6))
+    for rd in rm.rounds:
+        lut = rd["lut"]
+        lut.blobs[1] = lut.blobs[1].copy()
+        lut.blobs[1][16] ^= 1
+        lut.keys[1][16] ^= 1
+    delta = tuple(torch.empty(int(offsets[-1]), dtype=torch.int64, device="cuda")
+                  for _ in range(2))
+    rm.eval2(_pair_dev(x0, x1), delta, fused=fused)
+    g = [u64(delta[0]), u64(delta[1])]
+    o = tp.relu_rounds2(rm, [x0, x1])
+    assert np.array_equal(g[0], o[0]) and np.array_equal(g[1], o[1])
+
+
 def test_recip_shares_and_closed_form():
     n = 300
     s = (np.arange(n, dtype=np.int64) * 1499 + 4096) % (200 << F)
