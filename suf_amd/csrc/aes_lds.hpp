@@ -248,10 +248,35 @@ struct AesLds {
     }
 #pragma unroll 1
     for (int r = 1; r < 10; ++r) {
+      // All 16 N table reads (and the round keys) are issued before any is
+      // used: left to itself the scheduler interleaves reads and uses in
+      // runs of a few, and the round then pays the LDS latency several
+      // times over.
+      const uint32_t* p[N][16];
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            p[n][4 * c + j] = tab + (((st[n][(c + j) & 3] >> (8 * j)) & 0xffu) * kCopies + lane_word);
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t v[N][16];
+      uint4 k[N];
 #pragma unroll
       for (int n = 0; n < N; ++n) {
-        const uint4 k = rk[n][r];
-        round(st[n][0], st[n][1], st[n][2], st[n][3], k.x, k.y, k.z, k.w);
+        k[n] = rk[n][r];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[n][i] = *p[n][i];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const uint32_t kk[4] = {k[n].x, k[n].y, k[n].z, k[n].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          st[n][c] = v[n][4 * c] ^ rotl32(v[n][4 * c + 1], 8) ^ rotl32(v[n][4 * c + 2], 16) ^
+                     rotl32(v[n][4 * c + 3], 24) ^ kk[c];
       }
     }
 #pragma unroll
@@ -284,18 +309,26 @@ struct AesLds {
     for (int n = 0; n < N; ++n) s[n] ^= rkq[n][0];
 #pragma unroll 1
     for (int r = 1; r < 10; ++r) {
-      uint32_t a[N][4];
-#pragma unroll
-      for (int n = 0; n < N; ++n) {
-        a[n][0] = b0(s[n]);
-        a[n][1] = rotl32(b1(s[n]), 8);
-        a[n][2] = rotl32(b2(s[n]), 16);
-        a[n][3] = rotl32(b3(s[n]), 24);
-      }
+      // The round's table reads are all issued before any is used.
+      const uint32_t* p[N][4];
 #pragma unroll
       for (int n = 0; n < N; ++n)
-        s[n] = a[n][0] ^ quad_rot<1>(a[n][1]) ^ quad_rot<2>(a[n][2]) ^ quad_rot<3>(a[n][3]) ^
-               rkq[n][4 * r];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          p[n][j] = tab + (((s[n] >> (8 * j)) & 0xffu) * kCopies + lane_word);
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t a[N][4], k[N];
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        k[n] = rkq[n][4 * r];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[n][j] = *p[n][j];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+        s[n] = a[n][0] ^ quad_rot<1>(rotl32(a[n][1], 8)) ^ quad_rot<2>(rotl32(a[n][2], 16)) ^
+               quad_rot<3>(rotl32(a[n][3], 24)) ^ k[n];
     }
     // Final round: S(x) is byte 1 of T(x) (also byte 2).
     uint32_t u[N][4];
@@ -611,15 +644,119 @@ struct AesLds2 {
     }
 #pragma unroll 1
     for (int r = 1; r < 10; ++r) {
+      // All table reads of the round issued before any is used.
+      uint32_t addr[N][16];
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          addr[n][4 * c] = __builtin_amdgcn_perm(st[n][c], base[0], 0x0c0c0400u);
+          addr[n][4 * c + 1] = __builtin_amdgcn_perm(st[n][(c + 1) & 3], base[1], 0x0c0c0500u);
+          addr[n][4 * c + 2] = __builtin_amdgcn_perm(st[n][(c + 2) & 3], base[0], 0x0c0c0600u);
+          addr[n][4 * c + 3] = __builtin_amdgcn_perm(st[n][(c + 3) & 3], base[1], 0x0c0c0700u);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t v[N][16];
+      uint4 k[N];
 #pragma unroll
       for (int n = 0; n < N; ++n) {
-        const uint4 k = rk[n][r];
-        round(st[n][0], st[n][1], st[n][2], st[n][3], k.x, k.y, k.z, k.w);
+        k[n] = rk[n][r];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          v[n][i] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(lds) +
+                                                       addr[n][i]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const uint32_t kk[4] = {k[n].x, k[n].y, k[n].z, k[n].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          st[n][c] = xor3(v[n][4 * c], v[n][4 * c + 1], kk[c]) ^
+                     rotl32(v[n][4 * c + 2] ^ v[n][4 * c + 3], 16);
       }
     }
 #pragma unroll
     for (int n = 0; n < N; ++n) last(st[n][0], st[n][1], st[n][2], st[n][3], rk[n][10]);
   }
+  // Column-parallel encryption over a lane quad (AesLds::encrypt_quad_n's
+  // contract): byte k of a lane's column is looked up in T0 (k even) or T1
+  // (k odd); the terms of bytes 2 and 3 arrive from lanes q + 2 and q + 3
+  // and share one rotate by 16.
+  template <int N>
+  __device__ __forceinline__ void encrypt_quad_n(uint32_t (&s)[N],
+                                                 const uint32_t* const (&rkq)[N]) const {
+#pragma unroll
+    for (int n = 0; n < N; ++n) s[n] ^= rkq[n][0];
+#pragma unroll 1
+    for (int r = 1; r < 10; ++r) {
+      uint32_t addr[N][4];
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        addr[n][0] = __builtin_amdgcn_perm(s[n], base[0], 0x0c0c0400u);
+        addr[n][1] = __builtin_amdgcn_perm(s[n], base[1], 0x0c0c0500u);
+        addr[n][2] = __builtin_amdgcn_perm(s[n], base[0], 0x0c0c0600u);
+        addr[n][3] = __builtin_amdgcn_perm(s[n], base[1], 0x0c0c0700u);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t a[N][4], k[N];
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        k[n] = rkq[n][4 * r];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          a[n][j] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(lds) +
+                                                       addr[n][j]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+        s[n] = xor3(a[n][0], quad_rot<1>(a[n][1]), k[n]) ^
+               rotl32(quad_rot<2>(a[n][2]) ^ quad_rot<3>(a[n][3]), 16);
+    }
+    // Final round: S(x) is byte 1 (and byte 2) of T0[x] and byte 3 of T1[x].
+    uint32_t u[N][4];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      u[n][0] = (t<0, 0>(s[n]) >> 8) & 0xffu;
+      u[n][1] = t<0, 1>(s[n]) & 0xff00u;
+      u[n][2] = t<0, 2>(s[n]) & 0xff0000u;
+      u[n][3] = t<1, 3>(s[n]) & 0xff000000u;
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+      s[n] = (u[n][0] | quad_rot<1>(u[n][1]) | quad_rot<2>(u[n][2]) | quad_rot<3>(u[n][3])) ^
+             rkq[n][40];
+  }
+  // Fill of the whole span by kThreads threads without a barrier: uint4
+  // slot q holds entry q / 16 of table (q / 8) & 1 four times (kCopies ==
+  // 32 uses every word), read straight from T in global memory.  load()
+  // issues a thread's table reads, store() writes its slots, so a caller can
+  // put other loads in flight between the two; follow store() with
+  // __syncthreads().
+  template <int kThreads>
+  struct Filler {
+    static_assert(kCopies == 32, "AesLds2::Filler: the 32-copy span");
+    static constexpr int kSlots = kSpanWords / 4;
+    static constexpr int kPer = (kSlots + kThreads - 1) / kThreads;
+    uint32_t v[kPer];
+    __device__ __forceinline__ void load(const uint32_t* tsrc) {
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int q = int(threadIdx.x) + u * kThreads;
+        v[u] = q < kSlots ? tsrc[q >> 4] : 0u;
+      }
+    }
+    __device__ __forceinline__ void store(uint32_t* lds) const {
+      uint4* dst = reinterpret_cast<uint4*>(lds);
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int q = int(threadIdx.x) + u * kThreads;
+        const uint32_t w = rotl32(v[u], 8 * ((q >> 3) & 1));
+        if (q < kSlots) dst[q] = make_uint4(w, w, w, w);
+      }
+    }
+  };
   // Cooperative fill of the used words of the span from T in global memory
   // (staged once in LDS); contains a barrier, follow with __syncthreads().
   __device__ __forceinline__ static void fill(uint32_t* lds, const uint32_t* tsrc) {

@@ -168,10 +168,14 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
 // the reciprocal runs on lane 0 and is broadcast by a lane shuffle).
 constexpr int kSmRounds = 10;
 constexpr int kSmMaxRow = 512;
-constexpr int kSmWaves = 4;
-constexpr int kSmCopies = 32;
-using SmAes = AesLds<kSmCopies>;  // two workgroups per CU need the 32 KB table
-constexpr size_t kSmLdsCap = 65536;
+// Six rows per workgroup, one workgroup per CU: the 64 KB two-table AES
+// span, the staged keys and six rows of up to 512 elements fit the CU's
+// 160 KB of LDS, and the config's 1536 rows are one workgroup on each of
+// 256 CUs.
+constexpr int kSmWaves = 6;
+constexpr int kSmThreads = 64 * kSmWaves;
+using SmAes = AesLds2<32>;
+constexpr size_t kSmLdsCap = 160 * 1024;
 constexpr int kSmLock = 1;  // nExp chains per lane evaluated in lockstep
 
 struct SmArgs {
@@ -195,7 +199,7 @@ struct SmArgs {
 };
 
 struct SmStatic {
-  uint32_t tab[256 * kSmCopies];
+  uint32_t tab[SmAes::kSpanWords];
   TreeLds<kSmRounds> t;
   ChainLds nexp, recip;
   ChainPreN<3> rpre[kSmWaves];  // each row's reciprocal triples
@@ -208,21 +212,58 @@ __device__ __forceinline__ uint64_t bcast_lane0(uint64_t v) {
   return uint64_t(lo) | uint64_t(hi) << 32;
 }
 
+// Everything the block keeps in LDS for the whole launch -- the AES span,
+// every tree round's keys, both chains' keys -- in one staging pass: a
+// thread issues all of its global loads (about a dozen table words, at most
+// one key item per tree round and a few chain items, spread over the
+// workgroup by a flat item index) before its first LDS store, so staging
+// costs about one memory round trip.  The caller syncs.
+__device__ __forceinline__ void sm_stage(const SmArgs& a, SmStatic& st) {
+  constexpr int kChainBatch = 3;
+  typename SmAes::template Filler<kSmThreads> tf;
+  tf.load(kTDev.v);
+  TreeStager<kSmRounds> ts;
+  ts.load(a.keys);
+  // Chain items continue the tree's flat item space.
+  const int nn = chain_items(a.nexp, 4), nc = nn + chain_items(a.recip, 2);
+  const int shift = (a.keys.rounds * kTreeItems) % kSmThreads;
+  const int first = (int(threadIdx.x) + kSmThreads - shift) % kSmThreads;
+  for (int c0 = first; c0 < nc; c0 += kChainBatch * kSmThreads) {
+    uint4 v[kChainBatch];
+#pragma unroll
+    for (int u = 0; u < kChainBatch; ++u) {
+      const int c = c0 + u * kSmThreads;
+      if (c < nn)
+        v[u] = chain_item_load(a.nexp, 4, c);
+      else if (c < nc)
+        v[u] = chain_item_load(a.recip, 2, c - nn);
+    }
+#pragma unroll
+    for (int u = 0; u < kChainBatch; ++u) {
+      const int c = c0 + u * kSmThreads;
+      if (c < nn)
+        chain_item_store(a.nexp, 4, st.nexp, c, v[u]);
+      else if (c < nc)
+        chain_item_store(a.recip, 2, st.recip, c - nn, v[u]);
+    }
+  }
+  ts.store(st.t);
+  tf.store(st.tab);
+  if (threadIdx.x == 0) st.nexp.diff = st.recip.diff = 0;
+}
+
 template <int kPer>
-__global__ void __launch_bounds__(64 * kSmWaves) softmax2_kernel(SmArgs a) {
+__global__ void __launch_bounds__(kSmThreads) softmax2_kernel(SmArgs a) {
   __shared__ __align__(16) SmStatic st;
   extern __shared__ uint64_t rowbuf[];
   const int mr = a.max_row;
-  fill_ttable<kSmCopies>(st.tab, kTDev.v);
-  tree_stage(a.keys, st.t);
-  chain_stage(a.nexp, 4, st.nexp);
-  chain_stage(a.recip, 2, st.recip);
+  sm_stage(a, st);
   __syncthreads();
   tree_compare(a.keys, st.t);
   chain_compare(a.nexp, st.nexp);
   chain_compare(a.recip, st.recip);
   __syncthreads();
-  const SmAes aes{st.tab, threadIdx.x % kSmCopies};
+  const SmAes aes = SmAes::make(st.tab);
   const ChainKeyInfo Kn = chain_key_info(a.nexp, st.nexp);
   const ChainKeyInfo Kr = chain_key_info(a.recip, st.recip);
   const uint32_t shared = ~st.t.diff;
@@ -380,6 +421,17 @@ __global__ void __launch_bounds__(64 * kSmWaves) softmax2_kernel(SmArgs a) {
   }
 }
 
+// The dynamic LDS of a softmax launch goes past 64 KB; allowed once per
+// kernel.
+template <int kPer>
+bool sm_lds_allowed() {
+  static const bool ok =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&softmax2_kernel<kPer>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          int(kSmLdsCap - sizeof(SmStatic))) == hipSuccess;
+  return ok;
+}
+
 int triple_ok(const sufhip_triple2& t) {
   return t.a[0] && t.a[1] && t.b[0] && t.b[1] && t.c[0] && t.c[1];
 }
@@ -512,18 +564,22 @@ int sufhip_softmax2(const sufhip_softmax2_args* args, void* stream) {
                  "sufhip_softmax2: dense_planes need d_dense and cover rows x dense_cols");
   A.dkb = g.d_dense ? g.dense_planes : sufhip_kb_planes{};
   const size_t row_bytes = tree_row_words(g.max_row) * sizeof(uint64_t);
-  int waves = kSmWaves;
-  while (waves > 1 && sizeof(SmStatic) + size_t(waves) * row_bytes > kSmLdsCap) waves /= 2;
-  SUFHIP_REQUIRE(sizeof(SmStatic) + size_t(waves) * row_bytes <= kSmLdsCap,
+  const int waves = kSmWaves;
+  const size_t dyn = size_t(waves) * row_bytes;
+  SUFHIP_REQUIRE(sizeof(SmStatic) + dyn <= kSmLdsCap,
                  "sufhip_softmax2: rows too long for the workgroup's LDS");
   A.waves = waves;
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const int per_cu = int(kSmLdsCap / (sizeof(SmStatic) + dyn));
   const int groups = (g.rows + waves - 1) / waves;
-  const int grid = groups < cus * 2 ? groups : cus * 2;
-  const dim3 block(64 * waves);
-  const size_t dyn = size_t(waves) * row_bytes;
+  const int grid = groups < cus * per_cu ? groups : cus * per_cu;
+  const dim3 block(kSmThreads);
+  const bool lds_ok = g.max_row <= 128   ? sm_lds_allowed<2>()
+                      : g.max_row <= 256 ? sm_lds_allowed<4>()
+                                         : sm_lds_allowed<8>();
+  SUFHIP_REQUIRE(lds_ok, "sufhip_softmax2: the kernel's LDS size was refused");
   hipStream_t s = as_stream(stream);
   if (g.max_row <= 128)
     hipLaunchKernelGGL(softmax2_kernel<2>, dim3(grid), block, dyn, s, A);

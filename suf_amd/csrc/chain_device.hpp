@@ -61,6 +61,7 @@ struct ChainLds {
   uint4 rk[2][11];
   uint64_t cuts[2][kChainMaxIntervals];
   uint64_t pay[2][kChainMaxIntervals * kChainMaxWords];
+  uint64_t hdr[2][3];  // header words 0-2: in_bits (low 16 bits), party (byte 8), nonce
   uint32_t diff;  // nonzero: the two blobs' keystreams differ (chain_compare)
 };
 
@@ -143,43 +144,63 @@ __device__ __forceinline__ uint64_t chain_mask_bits(int bits) {
   return bits <= 0 ? 0 : (bits >= 64 ? ~uint64_t(0) : (uint64_t(1) << bits) - 1);
 }
 
+// Staging items of a chain's LUT material, both parties: per party the 11
+// round keys, the cut points, the payload words and three header words.
+// Item i is one 16-byte or 8-byte global load (chain_item_load) and one LDS
+// store (chain_item_store), so a caller can issue the loads of several
+// items, of several chains, before any store.
+__device__ __forceinline__ int chain_items(const ChainArgs& A, int W) {
+  return 2 * (11 + A.intervals + A.intervals * W + 3);
+}
+
+__device__ __forceinline__ uint4 chain_item_load(const ChainArgs& A, int W, int i) {
+  const int nint = A.intervals, per = 11 + nint + nint * W + 3;
+  const int p = i / per, w = i % per;
+  const uint8_t* k = p ? A.lut[1] : A.lut[0];
+  const uint64_t* cg = reinterpret_cast<const uint64_t*>(k + kChainLutHdr);
+  uint64_t x;
+  if (w < 11) {
+    const uint64_t* rkg = reinterpret_cast<const uint64_t*>(k + 40) + 2 * w;
+    const uint64_t lo = rkg[0], hi = rkg[1];
+    return make_uint4(uint32_t(lo), uint32_t(lo >> 32), uint32_t(hi), uint32_t(hi >> 32));
+  } else if (w < 11 + nint) {
+    x = cg[w - 11];
+  } else if (w < 11 + nint + nint * W) {
+    x = cg[nint + 1 + (w - 11 - nint)];
+  } else {
+    x = reinterpret_cast<const uint64_t*>(k)[w - (11 + nint + nint * W)];
+  }
+  return make_uint4(uint32_t(x), uint32_t(x >> 32), 0, 0);
+}
+
+__device__ __forceinline__ void chain_item_store(const ChainArgs& A, int W, ChainLds& L, int i,
+                                                 uint4 v) {
+  const int nint = A.intervals, per = 11 + nint + nint * W + 3;
+  const int p = i / per, w = i % per;
+  const uint64_t x = uint64_t(v.x) | uint64_t(v.y) << 32;
+  if (w < 11)
+    L.rk[p][w] = v;
+  else if (w < 11 + nint)
+    L.cuts[p][w - 11] = x;
+  else if (w < 11 + nint + nint * W)
+    L.pay[p][w - 11 - nint] = x;
+  else
+    L.hdr[p][w - (11 + nint + nint * W)] = x;
+}
+
 // Cooperative staging (every thread of the workgroup); the caller syncs.
-// Each thread handles a flat range of (party, round key | cut | payload word)
-// items, all loads issued before the stores.
+// Thread t takes items t + m * blockDim, two at a time with both loads
+// issued before the stores.
 __device__ __forceinline__ void chain_stage(const ChainArgs& A, int W, ChainLds& L) {
-  const int nint = A.intervals;
   if (threadIdx.x == 0) L.diff = 0;
-  const int per = 11 + nint + nint * W;  // items per party
-  for (int base = 0; base < 2 * per; base += 4 * blockDim.x) {
-    uint4 v[4];
-    int item[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      item[u] = base + u * blockDim.x + threadIdx.x;
-      if (item[u] >= 2 * per) continue;
-      const int p = item[u] / per, w = item[u] % per;
-      const uint8_t* k = A.lut[p];
-      const uint64_t* cg = reinterpret_cast<const uint64_t*>(k + kChainLutHdr);
-      if (w < 11) {
-        const uint32_t* rkg = reinterpret_cast<const uint32_t*>(k + 40) + 4 * w;
-        v[u] = make_uint4(rkg[0], rkg[1], rkg[2], rkg[3]);
-      } else {
-        const uint64_t x = w < 11 + nint ? cg[w - 11] : cg[nint + 1 + (w - 11 - nint)];
-        v[u] = make_uint4(uint32_t(x), uint32_t(x >> 32), 0, 0);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (item[u] >= 2 * per) continue;
-      const int p = item[u] / per, w = item[u] % per;
-      const uint64_t x = uint64_t(v[u].x) | uint64_t(v[u].y) << 32;
-      if (w < 11)
-        L.rk[p][w] = v[u];
-      else if (w < 11 + nint)
-        L.cuts[p][w - 11] = x;
-      else
-        L.pay[p][w - 11 - nint] = x;
-    }
+  const int n = chain_items(A, W);
+  for (int i = threadIdx.x; i < n; i += 2 * blockDim.x) {
+    const int i2 = i + blockDim.x;
+    const uint4 v = chain_item_load(A, W, i);
+    uint4 v2 = make_uint4(0, 0, 0, 0);
+    if (i2 < n) v2 = chain_item_load(A, W, i2);
+    chain_item_store(A, W, L, i, v);
+    if (i2 < n) chain_item_store(A, W, L, i2, v2);
   }
 }
 
@@ -194,10 +215,8 @@ __device__ __forceinline__ void chain_compare(const ChainArgs& A, ChainLds& L) {
     if (t < 11) {
       const uint4 a = L.rk[0][t], b = L.rk[1][t];
       differ = ((a.x ^ b.x) | (a.y ^ b.y) | (a.z ^ b.z) | (a.w ^ b.w)) != 0;
-    } else if (t == 11) {
-      const uint64_t* h0 = reinterpret_cast<const uint64_t*>(A.lut[0]);
-      const uint64_t* h1 = reinterpret_cast<const uint64_t*>(A.lut[1]);
-      differ = h0[2] != h1[2] || (h0[0] & 0xffff) != (h1[0] & 0xffff);  // nonce, in_bits
+    } else if (t == 11) {  // nonce, in_bits
+      differ = L.hdr[0][2] != L.hdr[1][2] || (L.hdr[0][0] & 0xffff) != (L.hdr[1][0] & 0xffff);
     } else {
       differ = L.cuts[0][t - 12] != L.cuts[1][t - 12];
     }
@@ -210,9 +229,9 @@ __device__ __forceinline__ void chain_compare(const ChainArgs& A, ChainLds& L) {
 __device__ __forceinline__ ChainKeyInfo chain_key_info(const ChainArgs& A, const ChainLds& L) {
   ChainKeyInfo K;
   for (int p = 0; p < 2; ++p) {
-    K.m[p] = chain_mask_bits(*reinterpret_cast<const uint16_t*>(A.lut[p]));
-    K.party[p] = A.lut[p][8];
-    K.nonce[p] = *reinterpret_cast<const uint64_t*>(A.lut[p] + 16);
+    K.m[p] = chain_mask_bits(int(L.hdr[p][0] & 0xffff));
+    K.party[p] = int(L.hdr[p][1] & 0xff);
+    K.nonce[p] = L.hdr[p][2];
   }
   K.same_ks = L.diff == 0;
   return K;

@@ -53,73 +53,104 @@ __host__ __device__ inline size_t tree_row_words(int max_row) {
   return size_t(2) * (size_t(max_row) + size_t(max_row + 1) / 2);
 }
 
-// Cooperative staging of every round's keys (all threads); the caller syncs.
-// A thread owns one (party, item) of every round: a round key, a cut point
-// or payload word, or the header fields.  Its loads of all rounds are
-// unrolled and issued before its LDS stores (the round count is uniform),
-// so the staging costs about one memory round trip.
+// Staging items of one round's keys: per party the 11 round keys, 8 cut
+// points, 16 payload words and the three header words (in_bits, party,
+// nonce); cut and payload slots past the round's intervals stage zero.
+constexpr int kTreeItemsPerParty = 11 + 3 * kTreeIntervals + 3;
+constexpr int kTreeItems = 2 * kTreeItemsPerParty;  // per round
+
 template <int kRounds>
-__device__ __forceinline__ void tree_stage(const TreeKeys<kRounds>& K, TreeLds<kRounds>& L) {
-  constexpr int kItems = 11 + 3 * kTreeIntervals + 1;
-  if (threadIdx.x == 0) L.diff = 0;
-  for (int it = threadIdx.x; it < 2 * kItems; it += blockDim.x) {
-    const int p = it / kItems, w = it % kItems;
-    if (w < 11) {
-      uint4 v[kRounds];
-#pragma unroll
-      for (int k = 0; k < kRounds; ++k)
-        if (k < K.rounds) {
-          const uint32_t* rkg =
-              reinterpret_cast<const uint32_t*>((p ? K.key[k][1] : K.key[k][0]) + 40) + 4 * w;
-          v[k] = make_uint4(rkg[0], rkg[1], rkg[2], rkg[3]);
-        }
-#pragma unroll
-      for (int k = 0; k < kRounds; ++k)
-        if (k < K.rounds) L.rk[k][p][w] = v[k];
-    } else if (w < 11 + 3 * kTreeIntervals) {
-      const int c = w - 11;  // cut c (< nint), or payload word c - kTreeIntervals (< 2 nint)
-      uint64_t v[kRounds];
-#pragma unroll
-      for (int k = 0; k < kRounds; ++k)
-        if (k < K.rounds) {
-          const int nint = K.intervals[k];
-          const bool cut = c < kTreeIntervals;
-          const bool valid = cut ? c < nint : c - kTreeIntervals < 2 * nint;
-          const int idx = !valid ? 0 : (cut ? c : nint + 1 + (c - kTreeIntervals));
-          const uint64_t* cg =
-              reinterpret_cast<const uint64_t*>((p ? K.key[k][1] : K.key[k][0]) + kTreeLutHdr);
-          v[k] = cg[idx];
-          if (!valid) v[k] = 0;
-        }
-#pragma unroll
-      for (int k = 0; k < kRounds; ++k)
-        if (k < K.rounds) {
-          if (c < kTreeIntervals)
-            L.cuts[k][p][c] = v[k];
-          else
-            L.pay[k][p][c - kTreeIntervals] = v[k];
-        }
+__device__ __forceinline__ uint4 tree_item_load(const TreeKeys<kRounds>& K, int k, int item) {
+  const int p = item / kTreeItemsPerParty, w = item % kTreeItemsPerParty;
+  const uint8_t* blob = p ? K.key[k][1] : K.key[k][0];
+  const int nint = K.intervals[k];
+  const uint64_t* cg = reinterpret_cast<const uint64_t*>(blob + kTreeLutHdr);
+  uint64_t x = 0;
+  if (w < 11) {
+    const uint64_t* rkg = reinterpret_cast<const uint64_t*>(blob + 40) + 2 * w;
+    const uint64_t lo = rkg[0], hi = rkg[1];
+    return make_uint4(uint32_t(lo), uint32_t(lo >> 32), uint32_t(hi), uint32_t(hi >> 32));
+  } else if (w < 11 + kTreeIntervals) {
+    const int c = w - 11;
+    if (c < nint) x = cg[c];
+  } else if (w < 11 + 3 * kTreeIntervals) {
+    const int c = w - 11 - kTreeIntervals;
+    if (c < 2 * nint) x = cg[nint + 1 + c];
+  } else {
+    x = reinterpret_cast<const uint64_t*>(blob)[w - (11 + 3 * kTreeIntervals)];
+  }
+  return make_uint4(uint32_t(x), uint32_t(x >> 32), 0, 0);
+}
+
+template <int kRounds>
+__device__ __forceinline__ void tree_item_store(TreeLds<kRounds>& L, int k, int item, uint4 v) {
+  const int p = item / kTreeItemsPerParty, w = item % kTreeItemsPerParty;
+  const uint64_t x = uint64_t(v.x) | uint64_t(v.y) << 32;
+  if (w < 11) {
+    L.rk[k][p][w] = v;
+  } else if (w < 11 + kTreeIntervals) {
+    L.cuts[k][p][w - 11] = x;
+  } else if (w < 11 + 3 * kTreeIntervals) {
+    L.pay[k][p][w - 11 - kTreeIntervals] = x;
+  } else {
+    const int h = w - (11 + 3 * kTreeIntervals);
+    if (h == 0) {
+      const int bits = int(x & 0xffff);
+      L.in_mask[k][p] = bits <= 0 ? 0 : (bits >= 64 ? ~uint64_t(0) : (uint64_t(1) << bits) - 1);
+    } else if (h == 1) {
+      L.party[k][p] = int(x & 0xff);
     } else {
-      uint64_t h0[kRounds], h1[kRounds], h2[kRounds];
-#pragma unroll
-      for (int k = 0; k < kRounds; ++k)
-        if (k < K.rounds) {
-          const uint64_t* hw = reinterpret_cast<const uint64_t*>(p ? K.key[k][1] : K.key[k][0]);
-          h0[k] = hw[0];  // in_bits in the low 16 bits
-          h1[k] = hw[1];  // party in the low byte
-          h2[k] = hw[2];  // keystream nonce
-        }
-#pragma unroll
-      for (int k = 0; k < kRounds; ++k)
-        if (k < K.rounds) {
-          const int bits = int(h0[k] & 0xffff);
-          L.nonce[k][p] = h2[k];
-          L.in_mask[k][p] =
-              bits <= 0 ? 0 : (bits >= 64 ? ~uint64_t(0) : (uint64_t(1) << bits) - 1);
-          L.party[k][p] = int(h1[k] & 0xff);
-        }
+      L.nonce[k][p] = x;
     }
   }
+}
+
+// Every round's items over the workgroup: round k's item j is flat item
+// k * kTreeItems + j, taken by thread (flat item) % blockDim (two items of a
+// round for a workgroup of fewer than kTreeItems threads), so a thread
+// issues the loads of all its rounds (load) before its LDS stores (store).
+// Rounds are unrolled: their key pointers are then compile-time fields of
+// the argument block.
+template <int kRounds>
+struct TreeStager {
+  uint4 v[kRounds][2];
+  int item[kRounds][2];
+  __device__ __forceinline__ void load(const TreeKeys<kRounds>& K) {
+    const uint32_t bd = blockDim.x;
+#pragma unroll
+    for (int k = 0; k < kRounds; ++k) {
+      item[k][0] = item[k][1] = -1;
+      if (k < K.rounds) {
+        const int j = int((threadIdx.x + uint32_t(kRounds * kTreeItems) * bd -
+                           uint32_t(k * kTreeItems)) % bd);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int jj = j + h * int(bd);
+          if (jj < kTreeItems) {
+            item[k][h] = jj;
+            v[k][h] = tree_item_load(K, k, jj);
+          }
+        }
+      }
+    }
+  }
+  __device__ __forceinline__ void store(TreeLds<kRounds>& L) const {
+    if (threadIdx.x == 0) L.diff = 0;
+#pragma unroll
+    for (int k = 0; k < kRounds; ++k)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        if (item[k][h] >= 0) tree_item_store(L, k, item[k][h], v[k][h]);
+  }
+};
+
+// Cooperative staging of every round's keys (all threads of a workgroup of
+// at least 64); the caller syncs.
+template <int kRounds>
+__device__ __forceinline__ void tree_stage(const TreeKeys<kRounds>& K, TreeLds<kRounds>& L) {
+  TreeStager<kRounds> s;
+  s.load(K);
+  s.store(L);
 }
 
 // Loads row r's slot offset of every round (round_off[k * rows + r]) into
