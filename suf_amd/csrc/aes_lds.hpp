@@ -744,7 +744,7 @@ struct AesLds2 {
 #pragma unroll
       for (int u = 0; u < kPer; ++u) {
         const int q = int(threadIdx.x) + u * kThreads;
-        v[u] = q < kSlots ? tsrc[q >> 4] : 0u;
+        v[u] = tsrc[(q < kSlots ? q : kSlots - 1) >> 4];
       }
     }
     __device__ __forceinline__ void store(uint32_t* lds) const {

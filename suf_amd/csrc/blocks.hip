@@ -222,8 +222,9 @@ __device__ __forceinline__ void sm_stage(const SmArgs& a, SmStatic& st) {
   constexpr int kChainBatch = 3;
   typename SmAes::template Filler<kSmThreads> tf;
   tf.load(kTDev.v);
-  TreeStager<kSmRounds> ts;
-  ts.load(a.keys);
+  static_assert(kSmRounds * kTreeItems <= 2 * kSmThreads, "sm_stage: tree items in one pass");
+  TreeStager<kSmRounds, 2> ts;
+  ts.load(kernarg_tree_keys<kSmRounds>(offsetof(SmArgs, keys)), int(threadIdx.x));
   // Chain items continue the tree's flat item space.
   const int nn = chain_items(a.nexp, 4), nc = nn + chain_items(a.recip, 2);
   const int shift = (a.keys.rounds * kTreeItems) % kSmThreads;
@@ -232,11 +233,12 @@ __device__ __forceinline__ void sm_stage(const SmArgs& a, SmStatic& st) {
     uint4 v[kChainBatch];
 #pragma unroll
     for (int u = 0; u < kChainBatch; ++u) {
-      const int c = c0 + u * kSmThreads;
-      if (c < nn)
-        v[u] = chain_item_load(a.nexp, 4, c);
-      else if (c < nc)
-        v[u] = chain_item_load(a.recip, 2, c - nn);
+      // Unconditional loads on a clamped item (see TreeStager::load).
+      const int c = c0 + u * kSmThreads < nc ? c0 + u * kSmThreads : 0;
+      bool rn, rr;
+      const uint64_t* an = chain_item_addr(a.nexp, 4, c < nn ? c : 0, &rn);
+      const uint64_t* ar = chain_item_addr(a.recip, 2, c < nn ? 0 : c - nn, &rr);
+      v[u] = chain_item_fetch(c < nn ? an : ar, c < nn ? rn : rr);
     }
 #pragma unroll
     for (int u = 0; u < kChainBatch; ++u) {
@@ -249,7 +251,7 @@ __device__ __forceinline__ void sm_stage(const SmArgs& a, SmStatic& st) {
   }
   ts.store(st.t);
   tf.store(st.tab);
-  if (threadIdx.x == 0) st.nexp.diff = st.recip.diff = 0;
+  if (threadIdx.x == 0) st.t.diff = st.nexp.diff = st.recip.diff = 0;
 }
 
 template <int kPer>

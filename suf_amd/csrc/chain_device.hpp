@@ -153,30 +153,44 @@ __device__ __forceinline__ int chain_items(const ChainArgs& A, int W) {
   return 2 * (11 + A.intervals + A.intervals * W + 3);
 }
 
-__device__ __forceinline__ uint4 chain_item_load(const ChainArgs& A, int W, int i) {
+// Address of item i's first word and whether it is a 16-byte round key
+// (branch-free, like tree_item_load: a caller issues the loads of several
+// items, of several chains, before any is used).
+__device__ __forceinline__ const uint64_t* chain_item_addr(const ChainArgs& A, int W, int i,
+                                                          bool* rk16) {
   const int nint = A.intervals, per = 11 + nint + nint * W + 3;
-  const int p = i / per, w = i % per;
+  const int p = i >= per ? 1 : 0;
+  const int w = i - p * per;
   const uint8_t* k = p ? A.lut[1] : A.lut[0];
-  const uint64_t* cg = reinterpret_cast<const uint64_t*>(k + kChainLutHdr);
-  uint64_t x;
-  if (w < 11) {
-    const uint64_t* rkg = reinterpret_cast<const uint64_t*>(k + 40) + 2 * w;
-    const uint64_t lo = rkg[0], hi = rkg[1];
-    return make_uint4(uint32_t(lo), uint32_t(lo >> 32), uint32_t(hi), uint32_t(hi >> 32));
-  } else if (w < 11 + nint) {
-    x = cg[w - 11];
-  } else if (w < 11 + nint + nint * W) {
-    x = cg[nint + 1 + (w - 11 - nint)];
-  } else {
-    x = reinterpret_cast<const uint64_t*>(k)[w - (11 + nint + nint * W)];
-  }
-  return make_uint4(uint32_t(x), uint32_t(x >> 32), 0, 0);
+  const bool rk = w < 11, cut = !rk && w < 11 + nint, pay = !rk && !cut && w < 11 + nint + nint * W;
+  const int off = rk ? 40 + 16 * w
+                     : (cut ? int(kChainLutHdr) + 8 * (w - 11)
+                            : (pay ? int(kChainLutHdr) + 8 * (nint + 1 + (w - 11 - nint))
+                                   : 8 * (w - (11 + nint + nint * W))));
+  *rk16 = rk;
+  return reinterpret_cast<const uint64_t*>(k + off);
+}
+
+// Two 8-byte loads, always issued (the second at the first's address for an
+// 8-byte item).
+__device__ __forceinline__ uint4 chain_item_fetch(const uint64_t* a, bool rk16) {
+  const uint64_t lo = a[0];
+  uint64_t hi = a[rk16 ? 1 : 0];
+  hi = rk16 ? hi : 0;
+  return make_uint4(uint32_t(lo), uint32_t(lo >> 32), uint32_t(hi), uint32_t(hi >> 32));
+}
+
+__device__ __forceinline__ uint4 chain_item_load(const ChainArgs& A, int W, int i) {
+  bool rk16;
+  const uint64_t* a = chain_item_addr(A, W, i, &rk16);
+  return chain_item_fetch(a, rk16);
 }
 
 __device__ __forceinline__ void chain_item_store(const ChainArgs& A, int W, ChainLds& L, int i,
                                                  uint4 v) {
   const int nint = A.intervals, per = 11 + nint + nint * W + 3;
-  const int p = i / per, w = i % per;
+  const int p = i >= per ? 1 : 0;
+  const int w = i - p * per;
   const uint64_t x = uint64_t(v.x) | uint64_t(v.y) << 32;
   if (w < 11)
     L.rk[p][w] = v;

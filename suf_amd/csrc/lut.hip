@@ -427,7 +427,7 @@ __global__ void __launch_bounds__(64 * kTreeWaves) relu_max_tree2_kernel(ReluTre
   extern __shared__ uint64_t rowbuf[];
   const int mr = a.max_row;
   fill_ttable<kTreeCopies>(st.tab, kTDev.v);
-  tree_stage(a.keys, st.t);
+  tree_stage(kernarg_tree_keys<kTreeRounds>(offsetof(ReluTreeArgs, keys)), st.t);
   __syncthreads();
   tree_compare(a.keys, st.t);
   __syncthreads();

@@ -59,32 +59,37 @@ __host__ __device__ inline size_t tree_row_words(int max_row) {
 constexpr int kTreeItemsPerParty = 11 + 3 * kTreeIntervals + 3;
 constexpr int kTreeItems = 2 * kTreeItemsPerParty;  // per round
 
+// Loads item `item` of round k: the item's offset in its blob is selected
+// arithmetically and two 8-byte loads (the second at the first's address for
+// 8-byte items) are always issued, so a thread's loads of several items stay
+// in flight together; items past the round's intervals read the blob's
+// first word and stage zero.  K may live in the kernarg segment (see
+// kernarg_tree_keys), so k may be a runtime index.
 template <int kRounds>
 __device__ __forceinline__ uint4 tree_item_load(const TreeKeys<kRounds>& K, int k, int item) {
-  const int p = item / kTreeItemsPerParty, w = item % kTreeItemsPerParty;
-  const uint8_t* blob = p ? K.key[k][1] : K.key[k][0];
+  const int p = item >= kTreeItemsPerParty ? 1 : 0;
+  const int w = item - p * kTreeItemsPerParty;
+  const uint8_t* blob = K.key[k][p];
   const int nint = K.intervals[k];
-  const uint64_t* cg = reinterpret_cast<const uint64_t*>(blob + kTreeLutHdr);
-  uint64_t x = 0;
-  if (w < 11) {
-    const uint64_t* rkg = reinterpret_cast<const uint64_t*>(blob + 40) + 2 * w;
-    const uint64_t lo = rkg[0], hi = rkg[1];
-    return make_uint4(uint32_t(lo), uint32_t(lo >> 32), uint32_t(hi), uint32_t(hi >> 32));
-  } else if (w < 11 + kTreeIntervals) {
-    const int c = w - 11;
-    if (c < nint) x = cg[c];
-  } else if (w < 11 + 3 * kTreeIntervals) {
-    const int c = w - 11 - kTreeIntervals;
-    if (c < 2 * nint) x = cg[nint + 1 + c];
-  } else {
-    x = reinterpret_cast<const uint64_t*>(blob)[w - (11 + 3 * kTreeIntervals)];
-  }
-  return make_uint4(uint32_t(x), uint32_t(x >> 32), 0, 0);
+  const int c = w - 11, cp = w - 11 - kTreeIntervals, h = w - (11 + 3 * kTreeIntervals);
+  const bool rk = w < 11, cut = !rk && c < kTreeIntervals;
+  const bool pay = !rk && !cut && cp < 2 * kTreeIntervals;
+  const bool zero = (cut && c >= nint) || (pay && cp >= 2 * nint);
+  int off = rk ? 40 + 16 * w
+               : (cut ? int(kTreeLutHdr) + 8 * c
+                      : (pay ? int(kTreeLutHdr) + 8 * (nint + 1 + cp) : 8 * h));
+  off = zero ? 0 : off;
+  const uint64_t* a = reinterpret_cast<const uint64_t*>(blob + off);
+  uint64_t lo = a[0], hi = a[rk ? 1 : 0];
+  lo = zero ? 0 : lo;
+  hi = rk ? hi : 0;
+  return make_uint4(uint32_t(lo), uint32_t(lo >> 32), uint32_t(hi), uint32_t(hi >> 32));
 }
 
 template <int kRounds>
 __device__ __forceinline__ void tree_item_store(TreeLds<kRounds>& L, int k, int item, uint4 v) {
-  const int p = item / kTreeItemsPerParty, w = item % kTreeItemsPerParty;
+  const int p = item >= kTreeItemsPerParty ? 1 : 0;
+  const int w = item - p * kTreeItemsPerParty;
   const uint64_t x = uint64_t(v.x) | uint64_t(v.y) << 32;
   if (w < 11) {
     L.rk[k][p][w] = v;
@@ -105,52 +110,55 @@ __device__ __forceinline__ void tree_item_store(TreeLds<kRounds>& L, int k, int 
   }
 }
 
-// Every round's items over the workgroup: round k's item j is flat item
-// k * kTreeItems + j, taken by thread (flat item) % blockDim (two items of a
-// round for a workgroup of fewer than kTreeItems threads), so a thread
-// issues the loads of all its rounds (load) before its LDS stores (store).
-// Rounds are unrolled: their key pointers are then compile-time fields of
-// the argument block.
+// A kernel's by-value TreeKeys read in place in the kernarg segment: a
+// runtime index into the by-value copy would make the compiler copy the
+// whole argument block to private scratch memory, while indexing the
+// segment is a plain load.  `field` is the keys' byte offset in the
+// kernel's (single, by-value) argument.
 template <int kRounds>
+__device__ __forceinline__ const TreeKeys<kRounds>* kernarg_tree_keys(size_t field) {
+  const uint8_t* base = (const uint8_t*)__builtin_amdgcn_kernarg_segment_ptr();
+  return reinterpret_cast<const TreeKeys<kRounds>*>(base + field);
+}
+
+// The staging items of every round as one flat list (round k's item j is
+// k * kTreeItems + j) over the workgroup: thread t takes items t + m *
+// blockDim in passes of kPer, each pass's loads issued before its stores.
+// load/store split one pass so that a caller can put other loads in flight
+// in between (one pass covers all items when rounds * kTreeItems <= kPer *
+// blockDim).
+template <int kRounds, int kPer>
 struct TreeStager {
-  uint4 v[kRounds][2];
-  int item[kRounds][2];
-  __device__ __forceinline__ void load(const TreeKeys<kRounds>& K) {
-    const uint32_t bd = blockDim.x;
+  uint4 v[kPer];
+  int f[kPer];
+  __device__ __forceinline__ void load(const TreeKeys<kRounds>* K, int f0) {
+    const int n = K->rounds * kTreeItems;
 #pragma unroll
-    for (int k = 0; k < kRounds; ++k) {
-      item[k][0] = item[k][1] = -1;
-      if (k < K.rounds) {
-        const int j = int((threadIdx.x + uint32_t(kRounds * kTreeItems) * bd -
-                           uint32_t(k * kTreeItems)) % bd);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int jj = j + h * int(bd);
-          if (jj < kTreeItems) {
-            item[k][h] = jj;
-            v[k][h] = tree_item_load(K, k, jj);
-          }
-        }
-      }
+    for (int u = 0; u < kPer; ++u) {
+      const int g = f0 + u * int(blockDim.x);
+      f[u] = g < n ? g : -1;
+      const int gc = g < n ? g : 0;
+      v[u] = n > 0 ? tree_item_load(*K, gc / kTreeItems, gc % kTreeItems) : make_uint4(0, 0, 0, 0);
     }
   }
   __device__ __forceinline__ void store(TreeLds<kRounds>& L) const {
-    if (threadIdx.x == 0) L.diff = 0;
 #pragma unroll
-    for (int k = 0; k < kRounds; ++k)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        if (item[k][h] >= 0) tree_item_store(L, k, item[k][h], v[k][h]);
+    for (int u = 0; u < kPer; ++u)
+      if (f[u] >= 0) tree_item_store(L, f[u] / kTreeItems, f[u] % kTreeItems, v[u]);
   }
 };
 
-// Cooperative staging of every round's keys (all threads of a workgroup of
-// at least 64); the caller syncs.
+// Cooperative staging of every round's keys (all threads); K in the kernarg
+// segment (kernarg_tree_keys).  The caller syncs.
 template <int kRounds>
-__device__ __forceinline__ void tree_stage(const TreeKeys<kRounds>& K, TreeLds<kRounds>& L) {
-  TreeStager<kRounds> s;
-  s.load(K);
-  s.store(L);
+__device__ __forceinline__ void tree_stage(const TreeKeys<kRounds>* K, TreeLds<kRounds>& L) {
+  if (threadIdx.x == 0) L.diff = 0;
+  const int n = K->rounds * kTreeItems;
+  for (int f0 = threadIdx.x; f0 < n; f0 += 2 * blockDim.x) {
+    TreeStager<kRounds, 2> s;
+    s.load(K, f0);
+    s.store(L);
+  }
 }
 
 // Loads row r's slot offset of every round (round_off[k * rows + r]) into
