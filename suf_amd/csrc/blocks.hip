@@ -214,79 +214,89 @@ __device__ __forceinline__ uint64_t bcast_lane0(uint64_t v) {
 
 // Everything the block keeps in LDS for the whole launch -- the AES span,
 // every tree round's keys, both chains' keys -- in one staging pass: a
-// thread issues all of its global loads (about a dozen table words, at most
-// one key item per tree round and a few chain items, spread over the
-// workgroup by a flat item index) before its first LDS store, so staging
-// costs about one memory round trip.  The caller syncs.
-__device__ __forceinline__ void sm_stage(const SmArgs& a, SmStatic& st) {
-  constexpr int kChainBatch = 3;
+// thread issues all of its global loads (about a dozen table words, up to
+// two tree items and a few chain items, spread over the workgroup by a flat
+// item index) before its first LDS store, so staging costs about one memory
+// round trip.  load() and store() split the pass so that the first rows'
+// loads go in between; the caller syncs after store().
+struct SmStager {
+  static constexpr int kChainPer = 3;
   typename SmAes::template Filler<kSmThreads> tf;
-  tf.load(kTDev.v);
-  static_assert(kSmRounds * kTreeItems <= 2 * kSmThreads, "sm_stage: tree items in one pass");
   TreeStager<kSmRounds, 2> ts;
-  ts.load(kernarg_tree_keys<kSmRounds>(offsetof(SmArgs, keys)), int(threadIdx.x));
-  // Chain items continue the tree's flat item space.
-  const int nn = chain_items(a.nexp, 4), nc = nn + chain_items(a.recip, 2);
-  const int shift = (a.keys.rounds * kTreeItems) % kSmThreads;
-  const int first = (int(threadIdx.x) + kSmThreads - shift) % kSmThreads;
-  for (int c0 = first; c0 < nc; c0 += kChainBatch * kSmThreads) {
-    uint4 v[kChainBatch];
+  uint4 cv[kChainPer];
+  int c0, nn, nc;
+  __device__ __forceinline__ void load(const SmArgs& a) {
+    static_assert(kSmRounds * kTreeItems <= 2 * kSmThreads, "SmStager: tree items in one pass");
+    tf.load(kTDev.v);
+    ts.load(kernarg_tree_keys<kSmRounds>(offsetof(SmArgs, keys)), int(threadIdx.x));
+    // Chain items continue the tree's flat item space.
+    nn = chain_items(a.nexp, 4);
+    nc = nn + chain_items(a.recip, 2);
+    const int shift = (a.keys.rounds * kTreeItems) % kSmThreads;
+    c0 = (int(threadIdx.x) + kSmThreads - shift) % kSmThreads;
 #pragma unroll
-    for (int u = 0; u < kChainBatch; ++u) {
+    for (int u = 0; u < kChainPer; ++u) {
       // Unconditional loads on a clamped item (see TreeStager::load).
       const int c = c0 + u * kSmThreads < nc ? c0 + u * kSmThreads : 0;
       bool rn, rr;
       const uint64_t* an = chain_item_addr(a.nexp, 4, c < nn ? c : 0, &rn);
       const uint64_t* ar = chain_item_addr(a.recip, 2, c < nn ? 0 : c - nn, &rr);
-      v[u] = chain_item_fetch(c < nn ? an : ar, c < nn ? rn : rr);
-    }
-#pragma unroll
-    for (int u = 0; u < kChainBatch; ++u) {
-      const int c = c0 + u * kSmThreads;
-      if (c < nn)
-        chain_item_store(a.nexp, 4, st.nexp, c, v[u]);
-      else if (c < nc)
-        chain_item_store(a.recip, 2, st.recip, c - nn, v[u]);
+      cv[u] = chain_item_fetch(c < nn ? an : ar, c < nn ? rn : rr);
     }
   }
-  ts.store(st.t);
-  tf.store(st.tab);
-  if (threadIdx.x == 0) st.t.diff = st.nexp.diff = st.recip.diff = 0;
-}
+  __device__ __forceinline__ void store(const SmArgs& a, SmStatic& st) const {
+#pragma unroll
+    for (int u = 0; u < kChainPer; ++u) {
+      const int c = c0 + u * kSmThreads;
+      if (c < nn)
+        chain_item_store(a.nexp, 4, st.nexp, c, cv[u]);
+      else if (c < nc)
+        chain_item_store(a.recip, 2, st.recip, c - nn, cv[u]);
+    }
+    // Chains with more items than one pass covers (wide LUTs): the rest
+    // item by item.
+    for (int c = c0 + kChainPer * kSmThreads; c < nc; c += kSmThreads) {
+      if (c < nn)
+        chain_item_store(a.nexp, 4, st.nexp, c, chain_item_load(a.nexp, 4, c));
+      else
+        chain_item_store(a.recip, 2, st.recip, c - nn, chain_item_load(a.recip, 2, c - nn));
+    }
+    ts.store(st.t);
+    tf.store(st.tab);
+    if (threadIdx.x == 0) st.t.diff = st.nexp.diff = st.recip.diff = 0;
+  }
+};
 
 template <int kPer>
 __global__ void __launch_bounds__(kSmThreads) softmax2_kernel(SmArgs a) {
   __shared__ __align__(16) SmStatic st;
   extern __shared__ uint64_t rowbuf[];
   const int mr = a.max_row;
-  sm_stage(a, st);
-  __syncthreads();
-  tree_compare(a.keys, st.t);
-  chain_compare(a.nexp, st.nexp);
-  chain_compare(a.recip, st.recip);
-  __syncthreads();
-  const SmAes aes = SmAes::make(st.tab);
-  const ChainKeyInfo Kn = chain_key_info(a.nexp, st.nexp);
-  const ChainKeyInfo Kr = chain_key_info(a.recip, st.recip);
-  const uint32_t shared = ~st.t.diff;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   uint64_t* even = rowbuf + size_t(wave) * tree_row_words(mr);
   uint64_t* odd = even + 2 * size_t(mr);
-  for (int g = blockIdx.x; g * a.waves < a.rows; g += gridDim.x) {
+  constexpr bool kPre = kPer <= 2;
+  int b = 0, len = 0;
+  uint64_t na[kPre ? kPer : 1][2], nc[kPre ? kPer : 1][2];
+  uint64_t s[kPer][2];
+  // Group g's row loads: offsets, the loads that need no open (issued now
+  // to land while the tree runs: the reciprocal's triples, one word per
+  // lane, to LDS, and for short rows every element's normalisation triple),
+  // and the scores through the optional truncations of their open, into
+  // registers and level 0 of the tree.  They touch no staged LDS, so for
+  // rows of up to 128 elements the first group's run before the staging and
+  // overlap its loads (longer rows keep too many scores in registers).
+  auto load_rows = [&](int g) {
     const int r = g * a.waves + wave;
-    int b = 0, len = 0;
+    b = 0;
+    len = 0;
     if (r < a.rows) {
       b = a.offs[r];
       len = a.offs[r + 1] - b;
       if (len < 1 || len > mr) len = 0;  // refused on the host
     }
-    // Loads that need no open, issued now to land while the tree runs: the
-    // reciprocal's triples (one word per lane, to LDS) and, for short rows,
-    // every element's normalisation triple (registers).
     if (len > 0 && lane < 18) st.rpre[wave].word(lane) = chain_triple_word(a.recip, lane, size_t(r));
     tree_row_offsets(a.keys, a.round_off, a.rows, r, len, st.j0[wave]);
-    constexpr bool kPre = kPer <= 2;
-    uint64_t na[kPre ? kPer : 1][2], nc[kPre ? kPer : 1][2];
     if constexpr (kPre) {
 #pragma unroll
       for (int k = 0; k < kPer; ++k) {
@@ -298,8 +308,6 @@ __global__ void __launch_bounds__(kSmThreads) softmax2_kernel(SmArgs a) {
         nc[k][1] = j < len ? a.norm.c[1][i] : 0;
       }
     }
-    // Scores, through the optional truncations of their open.
-    uint64_t s[kPer][2];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int j = lane + 64 * k;
@@ -322,7 +330,28 @@ __global__ void __launch_bounds__(kSmThreads) softmax2_kernel(SmArgs a) {
         even[mr + j] = v1;
       }
     }
-    __syncthreads();
+  };
+  {
+    SmStager stager;
+    stager.load(a);
+    if constexpr (kPre) load_rows(blockIdx.x);
+    stager.store(a, st);
+  }
+  __syncthreads();
+  tree_compare(a.keys, st.t);
+  chain_compare(a.nexp, st.nexp);
+  chain_compare(a.recip, st.recip);
+  __syncthreads();
+  const SmAes aes = SmAes::make(st.tab);
+  const ChainKeyInfo Kn = chain_key_info(a.nexp, st.nexp);
+  const ChainKeyInfo Kr = chain_key_info(a.recip, st.recip);
+  const uint32_t shared = ~st.t.diff;
+  for (int g = blockIdx.x; g * a.waves < a.rows; g += gridDim.x) {
+    if (!kPre || g != int(blockIdx.x)) {
+      load_rows(g);
+      __syncthreads();
+    }
+    const int r = g * a.waves + wave;
     const int level =
         tree_row<kSmRounds, SmAes>(a.keys, st.t, aes, even, odd, mr, len, st.j0[wave], shared);
     const uint64_t* fin = (level & 1) ? odd : even;

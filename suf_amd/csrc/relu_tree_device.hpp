@@ -321,10 +321,12 @@ __device__ __forceinline__ void tree_chunk(const TreeKeys<kRounds>& K, const Tre
 // row's first slot in round k (tree_row_offsets, written before a barrier);
 // bit k of `shared` is clear in L.diff (tree_compare).  Returns the level count; the row's max is
 // at index 0 of the final level's buffer (even if the count is even, odd
-// otherwise; party stride mr or ceil(mr / 2)).  Every thread of the
-// workgroup must call it (len 0 for an idle wave).  Slot t of a level is
-// pair (2t, 2t + 1) of the level below; an odd level's last element passes
-// through as its last slot.
+// otherwise; party stride mr or ceil(mr / 2)).  Slot t of a level is pair
+// (2t, 2t + 1) of the level below; an odd level's last element passes
+// through as its last slot.  A wave touches only its own row buffers, so
+// the levels synchronise the wave alone (LDS operations of one wave complete
+// in order; the fence keeps the compiler from moving a level's reads above
+// the previous level's writes) and a row stops when its length reaches one.
 template <int kRounds, class Aes>
 __device__ __forceinline__ int tree_row(const TreeKeys<kRounds>& K, const TreeLds<kRounds>& L,
                                         const Aes& aes, uint64_t* even,
@@ -332,8 +334,8 @@ __device__ __forceinline__ int tree_row(const TreeKeys<kRounds>& K, const TreeLd
                                         uint32_t shared) {
   const int lane = threadIdx.x & 63, half = (mr + 1) / 2;
   int level = 0;
-  for (int k = 0; k < K.rounds; ++k) {
-    if (len > 1) {
+  for (int k = 0; k < K.rounds && len > 1; ++k) {
+    {
       const uint64_t* src = (level & 1) ? odd : even;
       const int sw = (level & 1) ? half : mr;  // party stride of src
       uint64_t* dst = (level & 1) ? even : odd;
@@ -359,7 +361,9 @@ __device__ __forceinline__ int tree_row(const TreeKeys<kRounds>& K, const TreeLd
       len = (len + 1) >> 1;
       ++level;
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
   return level;
 }
