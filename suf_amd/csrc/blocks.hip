@@ -176,7 +176,7 @@ constexpr int kSmWaves = 6;
 constexpr int kSmThreads = 64 * kSmWaves;
 using SmAes = AesLds2<32>;
 constexpr size_t kSmLdsCap = 160 * 1024;
-constexpr int kSmLock = 1;  // nExp chains per lane evaluated in lockstep
+constexpr int kSmLock = 2;  // nExp chains per lane evaluated in lockstep
 
 struct SmArgs {
   sufhip_operand2 x;
@@ -202,6 +202,7 @@ struct SmStatic {
   uint32_t tab[SmAes::kSpanWords];
   TreeLds<kSmRounds> t;
   ChainLds nexp, recip;
+  TruncHdr thn[3][2], thr[3][2];  // the chains' truncation key headers
   ChainPreN<3> rpre[kSmWaves];  // each row's reciprocal triples
   uint32_t j0[kSmWaves][kSmRounds];  // each row's tree slot offsets
 };
@@ -263,6 +264,8 @@ struct SmStager {
     }
     ts.store(st.t);
     tf.store(st.tab);
+    chain_stage_trunc_hdrs<3>(a.nexp, st.thn);
+    chain_stage_trunc_hdrs<3>(a.recip, st.thr);
     if (threadIdx.x == 0) st.t.diff = st.nexp.diff = st.recip.diff = 0;
   }
 };
@@ -366,16 +369,16 @@ __global__ void __launch_bounds__(kSmThreads) softmax2_kernel(SmArgs a) {
     for (int k0 = 0; k0 < kPer; k0 += kSmLock) {
       size_t ii[kSmLock];
       Two dl[kSmLock], ev[kSmLock];
-      chain_loader<SUFHIP_CHAIN_CUBIC> pl[kSmLock] = {};
+      plain_loader<SUFHIP_CHAIN_CUBIC> pl[kSmLock] = {};
 #pragma unroll
       for (int u = 0; u < kSmLock; ++u) {
         const int j = lane + 64 * (k0 + u);
         ii[u] = size_t(b) + size_t(j < len ? j : 0);
         dl[u] = Two{{m0 - s[k0 + u][0], m1 - s[k0 + u][1]}};
-        pl[u] = chain_loader<SUFHIP_CHAIN_CUBIC>{&a.nexp, ii[u]};
+        pl[u] = plain_loader<SUFHIP_CHAIN_CUBIC>{&a.nexp, ii[u]};
       }
       chain_eval_m<SUFHIP_CHAIN_CUBIC, SmAes, kSmLock>(a.nexp, st.nexp, Kn, aes, ii, dl, pl,
-                                                        ev);
+                                                        ev, st.thn);
 #pragma unroll
       for (int u = 0; u < kSmLock; ++u) {
         const bool ok = lane + 64 * (k0 + u) < len;
@@ -391,7 +394,7 @@ __global__ void __launch_bounds__(kSmThreads) softmax2_kernel(SmArgs a) {
     uint64_t inv0 = 0, inv1 = 0;
     if (lane == 0 && len > 0) {
       const Two iv = chain_eval<SUFHIP_CHAIN_RECIP, SmAes>(
-          a.recip, st.recip, Kr, aes, size_t(r), Two{{es0, es1}}, st.rpre[wave]);
+          a.recip, st.recip, Kr, aes, size_t(r), Two{{es0, es1}}, st.rpre[wave], st.thr);
       inv0 = iv.v[0];
       inv1 = iv.v[1];
     }
@@ -562,6 +565,9 @@ int sufhip_softmax2(const sufhip_softmax2_args* args, void* stream) {
                  "sufhip_softmax2: nexp must be CUBIC and recip RECIP over rows elements");
   const size_t n = g.nexp.n;
   if (int rc = make_chain_args(g.nexp, false, "sufhip_softmax2 nexp", &A.nexp)) return rc;
+  SUFHIP_REQUIRE(A.nexp.plain,
+                 "sufhip_softmax2: the nExp chain's triples must be plain arrays (no index, "
+                 "multiplier, shift or negation; stride 1 or 3)");
   if (int rc = make_chain_args(g.recip, false, "sufhip_softmax2 recip", &A.recip)) return rc;
   if (int rc = check_operand(g.x, n, "sufhip_softmax2 x")) return rc;
   SUFHIP_REQUIRE(g.x.t[0].p[0] != nullptr, "sufhip_softmax2: empty input operand");

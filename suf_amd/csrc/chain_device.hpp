@@ -49,6 +49,19 @@ struct ChainArgs {
   uint64_t* out[2];
   sufhip_x_planes xp;
   size_t n;
+  // plain: every product's a, b and c is an array of at least n rows with
+  // no index, multiplier, shift or negation, all with one stride (1, or 3
+  // for interleaved triples): pa/pb/pc point at their offsets and row i of
+  // a term is p[i * pstride].  plain_x: x is one such term of stride 1.  The
+  // kernels then read the triple shares (plain_loader) and x[p][i] straight
+  // from these pointers, which keeps the general terms' fields out of the
+  // scalar registers.
+  bool plain, plain_x;
+  int pstride;
+  const uint64_t* px[2];
+  const uint64_t* pa[4][2];
+  const uint64_t* pb[4][2];
+  const uint64_t* pc[4][2];
 };
 
 struct Two {
@@ -122,6 +135,26 @@ struct chain_loader {
     }
   }
 };
+
+// Triple shares of product k from the plain pointers (ChainArgs::plain).
+template <int kKind>
+struct plain_loader {
+  const ChainArgs* A;
+  size_t i;
+  __device__ __forceinline__ void get(int k, uint64_t* a3, uint64_t* b3, uint64_t* c3) const {
+    const size_t j = i * size_t(A->pstride);
+    for (int p = 0; p < 2; ++p) {
+      a3[p] = A->pa[k][p][j];
+      b3[p] = A->pb[k][p][j];
+      c3[p] = A->pc[k][p][j];
+    }
+  }
+};
+
+// x's shares of element i for a plain chain.
+__device__ __forceinline__ uint64_t plain_x(const ChainArgs& A, int p, size_t i) {
+  return A.px[p][i] + (p == 0 ? A.x.party0_const : 0);
+}
 
 template <int kKind>
 constexpr int chain_products() {
@@ -262,10 +295,28 @@ __device__ __forceinline__ Two chain_beaver(const Src& P, int k, Two u, Two v) {
 }
 
 // Truncation gate j at the masked open of z, both parties.
-__device__ __forceinline__ Two chain_trunc(const ChainArgs& A, int j, Two z) {
+// th: the gates' key headers staged in LDS (chain_stage_trunc_hdrs), or
+// nullptr to read them from the keys.
+__device__ __forceinline__ Two chain_trunc(const ChainArgs& A, int j, Two z,
+                                          const TruncHdr (*th)[2]) {
   const uint64_t zh = z.v[0] + z.v[1] + A.tmask[j];
+  if (th)
+    return Two{{trunc_table_eval_h(th[j][0], A.ttab[j][0], A.tf[j], zh),
+                trunc_table_eval_h(th[j][1], A.ttab[j][1], A.tf[j], zh)}};
   return Two{{trunc_table_eval(A.tkey[j][0], A.ttab[j][0], A.tf[j], zh),
               trunc_table_eval(A.tkey[j][1], A.ttab[j][1], A.tf[j], zh)}};
+}
+
+// The chain's truncation key headers into LDS (threads 0 .. 2 * prods - 1;
+// the caller syncs): per use an LDS read instead of a header held in scalar
+// registers for the whole launch.
+template <int kProds>
+__device__ __forceinline__ void chain_stage_trunc_hdrs(const ChainArgs& A, TruncHdr (*th)[2]) {
+#pragma unroll
+  for (int j = 0; j < kProds; ++j)
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+      if (threadIdx.x == uint32_t(2 * j + p)) th[j][p] = read_trunc_hdr(A.tkey[j][p]);
 }
 
 // The whole chain for M elements at once (element m: index i[m], input
@@ -279,7 +330,8 @@ template <int kKind, class Aes, int M, class Src>
 __device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds& L,
                                              const ChainKeyInfo& K, const Aes& aes,
                                              const size_t (&i)[M], const Two (&x)[M],
-                                             const Src (&P)[M], Two (&out)[M]) {
+                                             const Src (&P)[M], Two (&out)[M],
+                                             const TruncHdr (*th)[2] = nullptr) {
   constexpr int W = kKind == SUFHIP_CHAIN_CUBIC ? 4 : 2;
   constexpr int NB = W / 2;  // AES blocks per element and party
   constexpr int NS = M * NB;  // blocks per party
@@ -291,16 +343,20 @@ __device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds&
     const uint64_t xh = x[m].v[0] + x[m].v[1] + A.lut_mask;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      const uint64_t xm = xh & K.m[p];
-      int lo = 0, hi = nint;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if ((L.cuts[p][mid] & K.m[p]) <= xm)
-          lo = mid + 1;
-        else
-          hi = mid;
+      if (p == 1 && K.same_ks) {
+        iv[m][1] = iv[m][0];  // the same cut points and input mask
+      } else {
+        const uint64_t xm = xh & K.m[p];
+        int lo = 0, hi = nint;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if ((L.cuts[p][mid] & K.m[p]) <= xm)
+            lo = mid + 1;
+          else
+            hi = mid;
+        }
+        iv[m][p] = lo - 1 < 0 ? 0 : lo - 1;
       }
-      iv[m][p] = lo - 1 < 0 ? 0 : lo - 1;
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const uint64_t ctr =
@@ -363,41 +419,42 @@ __device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds&
       Two mm = chain_beaver(P[m], 0, Two{{cf[m][0][3], cf[m][1][3]}}, x[m]);
       mm.v[0] += cf[m][0][2] << f;
       mm.v[1] += cf[m][1][2] << f;
-      t1[m] = chain_trunc(A, 0, chain_beaver(P[m], 1, mm, x[m]));
+      t1[m] = chain_trunc(A, 0, chain_beaver(P[m], 1, mm, x[m]), th);
     }
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const Two q{{t1[m].v[0] + (cf[m][0][1] << f), t1[m].v[1] + (cf[m][1][1] << f)}};
-      t2[m] = chain_trunc(A, 1, chain_beaver(P[m], 2, q, x[m]));
+      t2[m] = chain_trunc(A, 1, chain_beaver(P[m], 2, q, x[m]), th);
     }
 #pragma unroll
     for (int m = 0; m < M; ++m)
       out[m] = chain_trunc(
-          A, 2, Two{{t2[m].v[0] + (cf[m][0][0] << f), t2[m].v[1] + (cf[m][1][0] << f)}});
+          A, 2, Two{{t2[m].v[0] + (cf[m][0][0] << f), t2[m].v[1] + (cf[m][1][0] << f)}}, th);
   } else {
     Two y[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const Two t = chain_trunc(A, 0, chain_beaver(P[m], 0, Two{{cf[m][0][1], cf[m][1][1]}}, x[m]));
+      const Two t =
+          chain_trunc(A, 0, chain_beaver(P[m], 0, Two{{cf[m][0][1], cf[m][1][1]}}, x[m]), th);
       y[m] = Two{{t.v[0] + cf[m][0][0], t.v[1] + cf[m][1][0]}};
     }
     if constexpr (kKind == SUFHIP_CHAIN_RECIP) {
 #pragma unroll
-      for (int m = 0; m < M; ++m) t1[m] = chain_trunc(A, 1, chain_beaver(P[m], 1, y[m], x[m]));
+      for (int m = 0; m < M; ++m) t1[m] = chain_trunc(A, 1, chain_beaver(P[m], 1, y[m], x[m]), th);
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         const Two two{{(uint64_t(2) << f) - t1[m].v[0], uint64_t(0) - t1[m].v[1]}};
-        out[m] = chain_trunc(A, 2, chain_beaver(P[m], 2, y[m], two));
+        out[m] = chain_trunc(A, 2, chain_beaver(P[m], 2, y[m], two), th);
       }
     } else {
 #pragma unroll
-      for (int m = 0; m < M; ++m) t1[m] = chain_trunc(A, 1, chain_beaver(P[m], 1, y[m], y[m]));
+      for (int m = 0; m < M; ++m) t1[m] = chain_trunc(A, 1, chain_beaver(P[m], 1, y[m], y[m]), th);
 #pragma unroll
-      for (int m = 0; m < M; ++m) t2[m] = chain_trunc(A, 2, chain_beaver(P[m], 2, x[m], t1[m]));
+      for (int m = 0; m < M; ++m) t2[m] = chain_trunc(A, 2, chain_beaver(P[m], 2, x[m], t1[m]), th);
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         const Two inner{{(uint64_t(3) << (f - 1)) - t2[m].v[0], uint64_t(0) - t2[m].v[1]}};
-        out[m] = chain_trunc(A, 3, chain_beaver(P[m], 3, y[m], inner));
+        out[m] = chain_trunc(A, 3, chain_beaver(P[m], 3, y[m], inner), th);
       }
     }
   }
@@ -407,12 +464,13 @@ __device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds&
 template <int kKind, class Aes, class Src>
 __device__ __forceinline__ Two chain_eval(const ChainArgs& A, const ChainLds& L,
                                           const ChainKeyInfo& K, const Aes& aes,
-                                          size_t i, Two x, const Src& P) {
+                                          size_t i, Two x, const Src& P,
+                                          const TruncHdr (*th)[2] = nullptr) {
   const size_t ii[1] = {i};
   const Two xx[1] = {x};
   const Src pp[1] = {P};
   Two out[1];
-  chain_eval_m<kKind, Aes, 1>(A, L, K, aes, ii, xx, pp, out);
+  chain_eval_m<kKind, Aes, 1>(A, L, K, aes, ii, xx, pp, out, th);
   return out[0];
 }
 
@@ -480,6 +538,28 @@ inline int make_chain_args(const sufhip_chain2_args& g, bool own_io, const char*
     A.ttab[k][1] = e.table[1];
     A.tmask[k] = g.trunc_mask[k];
     A.tf[k] = e.f;
+  }
+  auto plain = [&](const sufhip_term2& t, size_t stride) {
+    return t.p[0] && t.p[1] && !t.index && t.stride == stride && t.shift == 0 && !t.negate &&
+           (t.mul == 0 || t.mul == 1) && t.len >= g.n;
+  };
+  A.plain_x = plain(g.x.t[0], 1) && !g.x.t[1].p[0] && !g.x.t[1].p[1];
+  if (A.plain_x) {
+    A.px[0] = g.x.t[0].p[0];
+    A.px[1] = g.x.t[0].p[1];
+  }
+  const size_t st = g.a[0].stride;
+  A.plain = st == 1 || st == 3;
+  for (int k = 0; k < prods; ++k)
+    A.plain = A.plain && plain(g.a[k], st) && plain(g.b[k], st) && plain(g.c[k], st);
+  if (A.plain) {
+    A.pstride = int(st);
+    for (int k = 0; k < prods; ++k)
+      for (int p = 0; p < 2; ++p) {
+        A.pa[k][p] = g.a[k].p[p] + g.a[k].off;
+        A.pb[k][p] = g.b[k].p[p] + g.b[k].off;
+        A.pc[k][p] = g.c[k].p[p] + g.c[k].off;
+      }
   }
   *out = A;
   return SUFHIP_OK;

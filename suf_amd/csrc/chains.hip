@@ -19,13 +19,18 @@ constexpr int kBlock = 512;  // two workgroups of the 72 KB LDS footprint per CU
 constexpr int kCopies = 32;
 using ChainAes = AesLds2<kCopies>;
 
-template <int kKind>
+// kPlain: x and the triple shares are plain arrays (ChainArgs::plain and
+// plain_x), read through plain pointers.
+template <int kKind, bool kPlain>
 __global__ void __launch_bounds__(kBlock) gate_chain_kernel(ChainArgs A) {
   constexpr int W = kKind == SUFHIP_CHAIN_CUBIC ? 4 : 2;
+  constexpr int kProds = chain_products<kKind>();
   __shared__ __align__(16) uint32_t tab[ChainAes::kSpanWords];
   __shared__ ChainLds L;
+  __shared__ TruncHdr th[kProds][2];
   ChainAes::fill(tab, kTDev.v);
   chain_stage(A, W, L);
+  chain_stage_trunc_hdrs<kProds>(A, th);
   __syncthreads();
   chain_compare(A, L);
   __syncthreads();
@@ -33,8 +38,14 @@ __global__ void __launch_bounds__(kBlock) gate_chain_kernel(ChainArgs A) {
   const ChainKeyInfo K = chain_key_info(A, L);
   for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < A.n;
        i += size_t(gridDim.x) * kBlock) {
-    const Two x{{operand_at(A.x, 0, i), operand_at(A.x, 1, i)}};
-    const Two res = chain_eval<kKind, ChainAes>(A, L, K, aes, i, x, chain_loader<kKind>{&A, i});
+    Two res;
+    if constexpr (kPlain) {
+      const Two x{{plain_x(A, 0, i), plain_x(A, 1, i)}};
+      res = chain_eval<kKind, ChainAes>(A, L, K, aes, i, x, plain_loader<kKind>{&A, i}, th);
+    } else {
+      const Two x{{operand_at(A.x, 0, i), operand_at(A.x, 1, i)}};
+      res = chain_eval<kKind, ChainAes>(A, L, K, aes, i, x, chain_loader<kKind>{&A, i}, th);
+    }
     if (A.out[0]) {
       A.out[0][i] = res.v[0];
       A.out[1][i] = res.v[1];
@@ -71,12 +82,19 @@ int sufhip_gate_chain2(const sufhip_chain2_args* args, void* stream) {
   if (g.n == 0) return SUFHIP_OK;
   const dim3 grid(chain_grid(g.n)), block(kBlock);
   hipStream_t s = as_stream(stream);
-  if (g.kind == SUFHIP_CHAIN_CUBIC)
-    hipLaunchKernelGGL(gate_chain_kernel<SUFHIP_CHAIN_CUBIC>, grid, block, 0, s, A);
+  const bool plain = A.plain && A.plain_x;
+  if (g.kind == SUFHIP_CHAIN_CUBIC && plain)
+    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_CUBIC, true>), grid, block, 0, s, A);
+  else if (g.kind == SUFHIP_CHAIN_CUBIC)
+    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_CUBIC, false>), grid, block, 0, s, A);
+  else if (g.kind == SUFHIP_CHAIN_RECIP && plain)
+    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_RECIP, true>), grid, block, 0, s, A);
   else if (g.kind == SUFHIP_CHAIN_RECIP)
-    hipLaunchKernelGGL(gate_chain_kernel<SUFHIP_CHAIN_RECIP>, grid, block, 0, s, A);
+    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_RECIP, false>), grid, block, 0, s, A);
+  else if (plain)
+    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_RSQRT, true>), grid, block, 0, s, A);
   else
-    hipLaunchKernelGGL(gate_chain_kernel<SUFHIP_CHAIN_RSQRT>, grid, block, 0, s, A);
+    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_RSQRT, false>), grid, block, 0, s, A);
   return check_launch("gate_chain_kernel");
 }
 
