@@ -224,12 +224,15 @@ struct SmStager {
   static constexpr int kChainPer = 3;
   typename SmAes::template Filler<kSmThreads> tf;
   TreeStager<kSmRounds, 2> ts;
+  TruncHdrStager<3> hn, hr;
   uint4 cv[kChainPer];
   int c0, nn, nc;
   __device__ __forceinline__ void load(const SmArgs& a) {
     static_assert(kSmRounds * kTreeItems <= 2 * kSmThreads, "SmStager: tree items in one pass");
     tf.load(kTDev.v);
     ts.load(kernarg_tree_keys<kSmRounds>(offsetof(SmArgs, keys)), int(threadIdx.x));
+    hn.load(a.nexp, 0);
+    hr.load(a.recip, 64);
     // Chain items continue the tree's flat item space.
     nn = chain_items(a.nexp, 4);
     nc = nn + chain_items(a.recip, 2);
@@ -264,8 +267,8 @@ struct SmStager {
     }
     ts.store(st.t);
     tf.store(st.tab);
-    chain_stage_trunc_hdrs<3>(a.nexp, st.thn);
-    chain_stage_trunc_hdrs<3>(a.recip, st.thr);
+    hn.store(st.thn);
+    hr.store(st.thr);
     if (threadIdx.x == 0) st.t.diff = st.nexp.diff = st.recip.diff = 0;
   }
 };

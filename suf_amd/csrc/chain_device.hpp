@@ -235,6 +235,33 @@ __device__ __forceinline__ void chain_item_store(const ChainArgs& A, int W, Chai
     L.hdr[p][w - (11 + nint + nint * W)] = x;
 }
 
+// A chain's items over a workgroup of kThreads threads in one pass of kPer
+// items per thread (thread t takes items t + u * kThreads), loads issued
+// before stores; items beyond kPer * kThreads go item by item in store().
+template <int kThreads, int kPer>
+struct ChainStager {
+  uint4 v[kPer];
+  int n;
+  __device__ __forceinline__ void load(const ChainArgs& A, int W) {
+    n = chain_items(A, W);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int c = int(threadIdx.x) + u * kThreads;
+      v[u] = chain_item_load(A, W, c < n ? c : 0);
+    }
+  }
+  __device__ __forceinline__ void store(const ChainArgs& A, int W, ChainLds& L) const {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int c = int(threadIdx.x) + u * kThreads;
+      if (c < n) chain_item_store(A, W, L, c, v[u]);
+    }
+    for (int c = int(threadIdx.x) + kPer * kThreads; c < n; c += kThreads)
+      chain_item_store(A, W, L, c, chain_item_load(A, W, c));
+    if (threadIdx.x == 0) L.diff = 0;
+  }
+};
+
 // Cooperative staging (every thread of the workgroup); the caller syncs.
 // Thread t takes items t + m * blockDim, two at a time with both loads
 // issued before the stores.
@@ -307,16 +334,39 @@ __device__ __forceinline__ Two chain_trunc(const ChainArgs& A, int j, Two z,
               trunc_table_eval(A.tkey[j][1], A.ttab[j][1], A.tf[j], zh)}};
 }
 
-// The chain's truncation key headers into LDS (threads 0 .. 2 * prods - 1;
-// the caller syncs): per use an LDS read instead of a header held in scalar
-// registers for the whole launch.
+// The chain's truncation key headers into LDS, one (gate, party) per thread
+// from thread `first` on: per use an LDS read instead of a header held in
+// scalar registers for the whole launch.  load() issues the thread's eight
+// key-word loads (unconditionally: other threads read gate 0's key) so that
+// they share a round trip with the caller's other staging loads; store()
+// writes the decoded header; the caller syncs.
+template <int kProds>
+struct TruncHdrStager {
+  uint64_t w[8];
+  int slot;
+  __device__ __forceinline__ void load(const ChainArgs& A, int first) {
+    const int t = int(threadIdx.x) - first;
+    slot = t >= 0 && t < 2 * kProds ? t : -1;
+    const uint8_t* key = A.tkey[0][0];
+#pragma unroll
+    for (int j = 0; j < kProds; ++j)
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        if (slot == 2 * j + p) key = A.tkey[j][p];
+    const uint64_t* kw = reinterpret_cast<const uint64_t*>(key);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = kw[i];
+  }
+  __device__ __forceinline__ void store(TruncHdr (*th)[2]) const {
+    if (slot >= 0) th[slot >> 1][slot & 1] = decode_trunc_hdr(w);
+  }
+};
+
 template <int kProds>
 __device__ __forceinline__ void chain_stage_trunc_hdrs(const ChainArgs& A, TruncHdr (*th)[2]) {
-#pragma unroll
-  for (int j = 0; j < kProds; ++j)
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-      if (threadIdx.x == uint32_t(2 * j + p)) th[j][p] = read_trunc_hdr(A.tkey[j][p]);
+  TruncHdrStager<kProds> s;
+  s.load(A, 0);
+  s.store(th);
 }
 
 // The whole chain for M elements at once (element m: index i[m], input

@@ -28,9 +28,19 @@ __global__ void __launch_bounds__(kBlock) gate_chain_kernel(ChainArgs A) {
   __shared__ __align__(16) uint32_t tab[ChainAes::kSpanWords];
   __shared__ ChainLds L;
   __shared__ TruncHdr th[kProds][2];
-  ChainAes::fill(tab, kTDev.v);
-  chain_stage(A, W, L);
-  chain_stage_trunc_hdrs<kProds>(A, th);
+  // Staging in one pass: the span's slots, the LUT items and the gates'
+  // key headers all loaded before the first LDS store.
+  {
+    TruncHdrStager<kProds> hs;
+    ChainAes::Filler<kBlock> tf;
+    ChainStager<kBlock, 2> cs;
+    hs.load(A, 0);
+    tf.load(kTDev.v);
+    cs.load(A, W);
+    cs.store(A, W, L);
+    tf.store(tab);
+    hs.store(th);
+  }
   __syncthreads();
   chain_compare(A, L);
   __syncthreads();

@@ -29,6 +29,25 @@ struct TruncHdr {
 };
 
 // Header word 0: tag | kind << 32 | f << 40 | party << 48 | flags << 56.
+// decode_trunc_hdr takes the key's first 8 words (word 1 is unused).
+__device__ __forceinline__ TruncHdr decode_trunc_hdr(const uint64_t (&w)[8]) {
+  const uint64_t h0 = w[0];
+  TruncHdr h;
+  h.tag = uint32_t(h0);
+  h.kind = uint32_t(h0 >> 32) & 0xffu;
+  h.f = uint32_t(h0 >> 40) & 0xffu;
+  h.party = uint32_t(h0 >> 48) & 1u;
+  h.flags = uint32_t(h0 >> 56);
+  h.r_hi = w[2];
+  h.base = w[3];
+  h.cw = w[4];
+  h.sw = w[5];
+  h.m = w[6];
+  h.ckb = uint32_t(w[7]);
+  h.ukb = uint32_t(w[7] >> 32);
+  return h;
+}
+
 __device__ __forceinline__ TruncHdr read_trunc_hdr(const uint8_t* key) {
   const uint64_t* w = reinterpret_cast<const uint64_t*>(key);
   const uint64_t h0 = w[0];
