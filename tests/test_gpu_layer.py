@@ -496,3 +496,33 @@ def test_kb_open_split_two_jobs_mixed():
     torch.cuda.synchronize()
     for (want, nbytes), job in zip(wants, jobs):
         assert torch.equal(job[2].view(torch.uint8)[:nbytes], want.view(torch.uint8)[:nbytes])
+
+
+@pytest.mark.parametrize("shape", [(1, 64, 96, 1), (2, 96, 64, 0), (3, 32, 64, 0)])
+def test_lin2_batch_planes_match_open_then_split(shape):
+    """lin2_batch's digit-plane output of an open (row-side layouts written in
+    16-row runs, column-side element by element; with the planes of open + a0
+    beside them) equals the open x0 + x1 + mask followed by the split."""
+    nb, r, c, kc = shape
+    print("[gpu-case] lin2_batch planes", shape, flush=True)
+    g = np.random.default_rng(9)
+    n = nb * r * c
+    x = tuple(dev(g.integers(0, 2**64, n, dtype=np.uint64)) for _ in range(2))
+    a0 = dev(g.integers(0, 2**64, n, dtype=np.uint64))
+    mask = int(g.integers(0, 2**63)) * 2 + 1
+    opened = x[0] + x[1] + torch.tensor(np.uint64(mask).view(np.int64), device="cuda")
+    want = layer.kb_planes(nb, r, c)
+    want_x = layer.kb_planes(nb, r, c)
+    layer.kb_split([(opened, want, nb, r, c, kc), (opened + a0, want_x, nb, r, c, kc)])
+    got = layer.kb_planes(nb, r, c)
+    got_x = layer.kb_planes(nb, r, c)
+    got.fill_(0x5a5a)
+    got_x.fill_(0x5a5a)
+    xhat = torch.empty(n, dtype=torch.int64, device="cuda")
+    layer.lin2_batch([(layer.operand(layer.term(x)), n, xhat, mask,
+                       (got, nb, r, c, kc, got_x, a0))])
+    torch.cuda.synchronize()
+    nbytes = native.load().sufhip_kb_planes_bytes(nb, r, c)
+    assert torch.equal(xhat, opened)
+    assert torch.equal(got.view(torch.uint8)[:nbytes], want.view(torch.uint8)[:nbytes])
+    assert torch.equal(got_x.view(torch.uint8)[:nbytes], want_x.view(torch.uint8)[:nbytes])
