@@ -538,7 +538,10 @@ int sufhip_relu_max_tree2(const uint64_t* d_x0, const uint64_t* d_x1, int rows,
  *   max   = the ReLU pairwise-max tree over s (rounds <= 10, keys and
  *           d_round_offsets as sufhip_relu_max_tree2)
  *   e     = nexp chain at max - s (sufhip_gate_chain2 material, kind CUBIC,
- *           n = the packed element count; x and out of that struct ignored)
+ *           n = the packed element count; x and out of that struct ignored;
+ *           its triple shares plain arrays: no index, multiplier, shift or
+ *           negation, all of stride 1 or all of stride 3, else
+ *           SUFHIP_ERR_INVALID)
  *   inv   = recip chain at the row sum of e (kind RECIP, n = rows)
  *   prob  = tr_norm(e * inv[row]) (row-broadcast triple norm, open masked
  *           by norm_mask)
