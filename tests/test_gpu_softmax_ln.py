@@ -331,3 +331,21 @@ def test_lin2_and_row_sum2_bounds():
         lin2(operand(bad), n, out=out)
     with pytest.raises(native.SufHipError):
         lin2(operand(term(a, stride=2, off=2)), n, out=out)
+
+
+def test_softmax_block_rejects_indexed_nexp_triples():
+    """The one-launch block reads the nExp triples through plain pointers;
+    a triple share with a row index (or a shift, multiplier, negation or a
+    stride other than 1 or 3) is refused on the host before any launch."""
+    offs = softmax.causal_offsets(1, 8)
+    n = int(offs[-1])
+    sm = softmax.SoftmaxBlock(offs, STATE, F, seed=13)
+    for tr in sm.truncs():
+        tr.prepare()
+    x = _pair_dev(*_share(_scores(offs, 5), 6))
+    out = tuple(torch.empty(n, dtype=torch.int64, device="cuda") for _ in range(2))
+    a = sm.block_args(softmax.operand(softmax.term(x)), out)
+    idx = torch.zeros(n, dtype=torch.int32, device="cuda")
+    a.nexp.a[0].index = idx.data_ptr()
+    with pytest.raises(native.SufHipError, match="plain arrays"):
+        native.call("sufhip_softmax2", native.ctypes.byref(a), 0)
