@@ -15,8 +15,13 @@
 //
 // One element per lane; each lane streams its own key front to back
 // (33 bytes per level), so successive levels hit the same cache lines.
+//
+// The bit modes run 1024 lanes per CU (four waves per SIMD): their walk keeps
+// the round keys in scalar registers and fits in 64 VGPRs, and the table
+// lookups that bound it overlap better with more waves.
 #include <hip/hip_runtime.h>
 
+#include <cstddef>
 #include <cstring>
 
 #include "dcf_device.hpp"
@@ -35,13 +40,17 @@ struct DcfEvalArgs {
   int in_bits;
   int chunks;     // chunks to evaluate (1 for the bit modes)
   int out_bytes;  // bytes per element (OUT_BYTES)
+  DcfKeySel key_sel;  // the bit modes' round keys (scalar loads)
 };
 
+constexpr int kDcfBitBlock = 1024;
+
 template <int kMode>
-__global__ void __launch_bounds__(kDcfBlock) dcf_eval_bit_kernel(DcfEvalArgs a) {
-  SUFHIP_DCF_LDS_SETUP(a.prg);
-  const size_t stride = size_t(gridDim.x) * kDcfBlock;
-  for (size_t base = size_t(blockIdx.x) * kDcfBlock; base < a.n; base += stride) {
+__global__ void __launch_bounds__(kDcfBitBlock) dcf_eval_bit_kernel(DcfEvalArgs a) {
+  SUFHIP_DCF_TABLE_SETUP();
+  const KeySelPtr keys = kernarg_key_sel(offsetof(DcfEvalArgs, key_sel));
+  const size_t stride = size_t(gridDim.x) * kDcfBitBlock;
+  for (size_t base = size_t(blockIdx.x) * kDcfBitBlock; base < a.n; base += stride) {
     const size_t e = base + threadIdx.x;
     uint32_t bit = 0;
     if (e < a.n) {
@@ -49,7 +58,7 @@ __global__ void __launch_bounds__(kDcfBlock) dcf_eval_bit_kernel(DcfEvalArgs a) 
       const uint32_t party = key[2] & 1u;
       uint64_t x = a.xs[e];
       if (a.in_bits < 64) x &= (uint64_t(1) << a.in_bits) - 1;
-      bit = walk_bit(aes, rkl, key + 8, a.in_bits, x, party);
+      bit = walk_bit(aes, keys, key + 8, a.in_bits, x, party);
     }
     if constexpr (kMode == SUFHIP_DCF_OUT_BIT) {
       if (e < a.n) static_cast<uint8_t*>(a.out)[e] = uint8_t(bit);
@@ -200,17 +209,23 @@ int sufhip_dcf_eval(int group, int in_bits, int payload_len, const uint8_t* prg_
   a.in_bits = in_bits;
   a.chunks = 1;
   a.out_bytes = out_mode == SUFHIP_DCF_OUT_BYTES ? out_bytes : 1;
-  unsigned int g = 0;
-  if (int rc = dcf_grid(n, &g)) return rc;
-  const dim3 grid(g), block(kDcfBlock);
   hipStream_t s = as_stream(stream);
-  if (out_mode == SUFHIP_DCF_OUT_BIT) {
-    hipLaunchKernelGGL((dcf_eval_bit_kernel<SUFHIP_DCF_OUT_BIT>), grid, block, 0, s, a);
-  } else if (out_mode == SUFHIP_DCF_OUT_PACKED) {
-    SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_out) & 7) == 0,
-                   "sufhip_dcf_eval: packed output must be 8-byte aligned");
-    hipLaunchKernelGGL((dcf_eval_bit_kernel<SUFHIP_DCF_OUT_PACKED>), grid, block, 0, s, a);
+  if (out_mode != SUFHIP_DCF_OUT_BYTES) {
+    fill_key_sel(a.prg, &a.key_sel);
+    unsigned int g = 0;
+    if (int rc = dcf_grid(n, &g, kDcfBitBlock)) return rc;
+    const dim3 grid(g), block(kDcfBitBlock);
+    if (out_mode == SUFHIP_DCF_OUT_BIT) {
+      hipLaunchKernelGGL((dcf_eval_bit_kernel<SUFHIP_DCF_OUT_BIT>), grid, block, 0, s, a);
+    } else {
+      SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_out) & 7) == 0,
+                     "sufhip_dcf_eval: packed output must be 8-byte aligned");
+      hipLaunchKernelGGL((dcf_eval_bit_kernel<SUFHIP_DCF_OUT_PACKED>), grid, block, 0, s, a);
+    }
   } else {
+    unsigned int g = 0;
+    if (int rc = dcf_grid(n, &g)) return rc;
+    const dim3 grid(g), block(kDcfBlock);
     a.chunks = (out_bytes + 15) / 16;
     if (group == SUFHIP_GROUP_XOR)
       hipLaunchKernelGGL((dcf_eval_bytes_kernel<SUFHIP_GROUP_XOR>), grid, block, 0, s, a);

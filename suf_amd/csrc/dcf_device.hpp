@@ -66,23 +66,6 @@ struct CwBit {
   uint32_t tb;
 };
 
-__device__ __forceinline__ CwBit load_cw_bit(const uint8_t* p) {
-  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-  const uint32_t sh = uint32_t(a & 3);
-  // Bytes [0, 17) and byte 32 of the record; words 0..4 and 8 of the aligned
-  // window always lie inside the record (it is 33 bytes, sh <= 3).
-  uint32_t r0 = q[0], r1 = q[1], r2 = q[2], r3 = q[3], r4 = q[4], r8 = q[8];
-  CwBit c;
-  c.s[0] = __builtin_amdgcn_alignbyte(r1, r0, sh);
-  c.s[1] = __builtin_amdgcn_alignbyte(r2, r1, sh);
-  c.s[2] = __builtin_amdgcn_alignbyte(r3, r2, sh);
-  c.s[3] = __builtin_amdgcn_alignbyte(r4, r3, sh);
-  c.v0 = (r4 >> (8 * sh)) & 0xffu;
-  c.tb = (r8 >> (8 * sh)) & 0xffu;
-  return c;
-}
-
 struct CwFull {
   uint32_t s[4];
   uint32_t v[4];
@@ -129,46 +112,205 @@ __device__ __forceinline__ void load16(const uint8_t* p, bool more, uint32_t (&w
   w[3] = __builtin_amdgcn_alignbyte(r4, r3, sh);
 }
 
-// Bit-mode walk of one chunk: returns share byte 0 & 1.
-__device__ __forceinline__ uint32_t walk_bit(const DcfAes& aes, const uint4* rkl,
+// ---------------------------------------------------------------------------
+// Bit-mode walk (share byte 0 & 1) with the round keys in scalar registers.
+//
+// At level i every lane needs K_{2 x_i} (next seed) and K_{2 x_i + 1} (value
+// block), x_i being its own input bit.  With m = -x_i (all ones or zero) they
+// are K_0 ^ (m & (K_0 ^ K_2)) and K_1 ^ (m & (K_1 ^ K_3)): the four uniform
+// words of each pair come from the kernel argument through the scalar unit,
+// and the per-lane choice is one 3-input bit operation per key word.  Reading
+// the chosen keys from LDS instead costs 20 ds_read_b128 per level (about 4
+// LDS clocks each) on the pipe that bounds the walk, and 80 VGPRs.
+//
+// DcfKeySel row r: K_0[r], (K_0 ^ K_2)[r], K_1[r], (K_1 ^ K_3)[r].
+struct DcfKeySel {
+  uint32_t w[11][16];
+};
+
+void fill_key_sel(const Prg4& p, DcfKeySel* k) {
+  for (int r = 0; r < 11; ++r)
+    for (int j = 0; j < 4; ++j) {
+      k->w[r][j] = p.rk[0][4 * r + j];
+      k->w[r][4 + j] = p.rk[0][4 * r + j] ^ p.rk[2][4 * r + j];
+      k->w[r][8 + j] = p.rk[1][4 * r + j];
+      k->w[r][12 + j] = p.rk[1][4 * r + j] ^ p.rk[3][4 * r + j];
+    }
+}
+
+// A DcfKeySel inside the kernel's by-value argument, addressed through the
+// constant (kernel-argument) address space so that its loads are scalar.
+typedef const __attribute__((address_space(4))) uint32_t* KeySelPtr;
+
+__device__ __forceinline__ KeySelPtr kernarg_key_sel(size_t field) {
+  return (KeySelPtr)((const __attribute__((address_space(4))) uint8_t*)
+                         __builtin_amdgcn_kernarg_segment_ptr() + field);
+}
+
+#define SUFHIP_BITOP3(a, b, c, f) __builtin_amdgcn_bitop3_b32((a), (b), (c), (f))
+// x ^ (m & d) as one v_bitop3 (truth table over src0 = 0xf0, src1 = 0xcc,
+// src2 = 0xaa).
+__device__ __forceinline__ uint32_t xor_and(uint32_t x, uint32_t m, uint32_t d) {
+  return SUFHIP_BITOP3(x, m, d, 0x78);
+}
+
+__device__ __forceinline__ uint32_t lds_word(const uint32_t* lds, uint32_t byte_addr) {
+  return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(lds) + byte_addr);
+}
+
+// One middle round of the seed block A and of columns [0, kB) of the value
+// block B, in three groups: every table address, then every table read with
+// the round's key loads, then the combines.  The scheduling barriers keep the
+// compiler from interleaving reads with their uses (each read's latency
+// would then be paid in turn).
+template <int kB>
+__device__ __forceinline__ void key_sel_round(const AesLds4& aes, KeySelPtr q, uint32_t m,
+                                              uint32_t (&A)[4], uint32_t (&B)[4]) {
+  constexpr int kN = 16 + 4 * kB;
+  uint32_t ad[kN];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ad[4 * c + j] = __builtin_amdgcn_perm(A[(c + j) & 3], aes.base[j], AesLds4::sel(j));
+      if (c < kB)
+        ad[16 + 4 * c + j] = __builtin_amdgcn_perm(B[(c + j) & 3], aes.base[j], AesLds4::sel(j));
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t tv[kN];
+#pragma unroll
+  for (int n = 0; n < kN; ++n) tv[n] = lds_word(aes.lds, ad[n]);
+  uint32_t kq[16];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) kq[n] = q[n];
+#pragma unroll
+  for (int c = 0; c < kB; ++c) {
+    kq[8 + c] = q[8 + c];
+    kq[12 + c] = q[12 + c];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    A[c] = xor_and(SUFHIP_BITOP3(SUFHIP_BITOP3(tv[4 * c], tv[4 * c + 1], tv[4 * c + 2], 0x96),
+                                 tv[4 * c + 3], kq[c], 0x96),
+                   m, kq[4 + c]);
+#pragma unroll
+  for (int c = 0; c < kB; ++c)
+    B[c] = xor_and(SUFHIP_BITOP3(SUFHIP_BITOP3(tv[16 + 4 * c], tv[17 + 4 * c], tv[18 + 4 * c], 0x96),
+                                 tv[19 + 4 * c], kq[8 + c], 0x96),
+                   m, kq[12 + c]);
+}
+
+// The aligned words of a 33-byte correction-word record that hold s_cw,
+// byte 0 of v_cw and the t byte (words 0..4 and 8), read with global loads:
+// a flat load also counts on the LDS wait counter, so every LDS wait of the
+// level would wait for it too.
+struct CwRaw {
+  uint32_t r[6];
+  uint32_t sh;
+};
+
+typedef const __attribute__((address_space(1))) uint32_t* GlobalWords;
+
+__device__ __forceinline__ CwRaw load_cw_raw(const uint8_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  GlobalWords q = (GlobalWords)(a & ~uintptr_t(3));
+  CwRaw c;
+  c.r[0] = q[0];
+  c.r[1] = q[1];
+  c.r[2] = q[2];
+  c.r[3] = q[3];
+  c.r[4] = q[4];
+  c.r[5] = q[8];
+  c.sh = uint32_t(a & 3);
+  return c;
+}
+
+__device__ __forceinline__ CwBit decode_cw(const CwRaw& w) {
+  CwBit c;
+  c.s[0] = __builtin_amdgcn_alignbyte(w.r[1], w.r[0], w.sh);
+  c.s[1] = __builtin_amdgcn_alignbyte(w.r[2], w.r[1], w.sh);
+  c.s[2] = __builtin_amdgcn_alignbyte(w.r[3], w.r[2], w.sh);
+  c.s[3] = __builtin_amdgcn_alignbyte(w.r[4], w.r[3], w.sh);
+  c.v0 = (w.r[4] >> (8 * w.sh)) & 0xffu;
+  c.tb = (w.r[5] >> (8 * w.sh)) & 0xffu;
+  return c;
+}
+
+// Bit-mode walk of one chunk: returns share byte 0 & 1.  The seed block is
+// AES_{K_{2 x_i}}(s) ^ s in full; of the value block only byte 0 is formed
+// (round 9 column 0, then one final S-box byte).
+__device__ __forceinline__ uint32_t walk_bit(const AesLds4& aes, KeySelPtr keys,
                                              const uint8_t* chunk, int in_bits, uint64_t x,
                                              uint32_t party) {
   uint32_t seed[4];
   load16(chunk, true, seed);
-  uint32_t s0 = seed[0], s1 = seed[1], s2 = seed[2], s3 = seed[3] & 0x7fffffffu;
+  uint32_t s[4] = {seed[0], seed[1], seed[2], seed[3] & 0x7fffffffu};
   uint32_t t = party;
   uint32_t v = 0;
   const uint8_t* cw = chunk + 16;
   for (int i = 0; i < in_bits; ++i, cw += 33) {
     const uint32_t xi = uint32_t(x >> (in_bits - 1 - i)) & 1u;
-    const CwBit c = load_cw_bit(cw);
-    uint32_t a0 = s0, a1 = s1, a2 = s2, a3 = s3;
-const uint4* ks = rkl + 22 * xi;  // K_{2 x_i}: next seed
-    const uint4* kv = ks + 11;         // K_{2 x_i + 1}: value block
-    aes.encrypt(a0, a1, a2, a3, ks);
-    const uint32_t vb = (aes.encrypt_byte0(s0, s1, s2, s3, kv) ^ s0) & 1u;
-    a0 ^= s0;
-    a1 ^= s1;
-    a2 ^= s2;
-    a3 ^= s3;
-    uint32_t tn = a3 >> 31;
-    a3 &= 0x7fffffffu;
+    const uint32_t m = 0u - xi;
+    const CwRaw cr = load_cw_raw(cw);
+    // An opaque copy of the key pointer per level: the compiler would
+    // otherwise hoist all 176 key words out of the level loop into scalar
+    // registers it does not have.
+    KeySelPtr k = keys;
+    asm volatile("" : "+s"(k));
+    uint32_t A[4], B[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      A[j] = xor_and(s[j], m, k[4 + j]) ^ k[j];
+      B[j] = xor_and(s[j], m, k[12 + j]) ^ k[8 + j];
+    }
+#pragma unroll
+    for (int r = 1; r < 9; ++r) key_sel_round<4>(aes, k + 16 * r, m, A, B);
+    key_sel_round<1>(aes, k + 16 * 9, m, A, B);
+    // Final round of the seed block: S(x) is byte 0 of T3[x], bytes 1 and 2
+    // of T0[x] and byte 3 of T1[x]; byte 0 of the value block from T3.
+    uint32_t ad[17];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      ad[4 * c + 0] = __builtin_amdgcn_perm(A[c], aes.base[3], AesLds4::sel(0));
+      ad[4 * c + 1] = __builtin_amdgcn_perm(A[(c + 1) & 3], aes.base[0], AesLds4::sel(1));
+      ad[4 * c + 2] = __builtin_amdgcn_perm(A[(c + 2) & 3], aes.base[0], AesLds4::sel(2));
+      ad[4 * c + 3] = __builtin_amdgcn_perm(A[(c + 3) & 3], aes.base[1], AesLds4::sel(3));
+    }
+    ad[16] = __builtin_amdgcn_perm(B[0], aes.base[3], AesLds4::sel(0));
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t tv[17];
+#pragma unroll
+    for (int n = 0; n < 17; ++n) tv[n] = lds_word(aes.lds, ad[n]);
+    const KeySelPtr q = k + 160;
+    uint32_t kq[10];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) kq[n] = q[n];
+    kq[8] = q[8];
+    kq[9] = q[12];
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t lo = __builtin_amdgcn_perm(tv[4 * c + 1], tv[4 * c], 0x0c0c0500u);
+      const uint32_t hi = __builtin_amdgcn_perm(tv[4 * c + 3], tv[4 * c + 2], 0x07020c0cu);
+      // ((lo | hi) ^ s) ^ K_sel: the Matyas-Meyer-Oseas output of the seed block.
+      o[c] = xor_and(SUFHIP_BITOP3(lo, hi, s[c], 0x56) ^ kq[c], m, kq[4 + c]);
+    }
+    const uint32_t vb = xor_and(tv[16] ^ s[0] ^ kq[8], m, kq[9]) & 1u;
+    const CwBit c = decode_cw(cr);
+    uint32_t tn = o[3] >> 31;
+    o[3] &= 0x7fffffffu;
     const uint32_t tmask = 0u - t;
-    a0 ^= c.s[0] & tmask;
-    a1 ^= c.s[1] & tmask;
-    a2 ^= c.s[2] & tmask;
-    a3 ^= c.s[3] & tmask;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = o[j] ^ (c.s[j] & tmask);
     tn ^= ((xi ? c.tb : (c.tb >> 1)) & 1u) & t;
     v ^= vb ^ (c.v0 & t & 1u);
-    s0 = a0;
-    s1 = a1;
-    s2 = a2;
-    s3 = a3;
     t = tn;
   }
   uint32_t np1[4];
   load16(cw, false, np1);
-  return (v ^ s0 ^ (np1[0] & t)) & 1u;
+  return (v ^ s[0] ^ (np1[0] & t)) & 1u;
 }
 
 // Full-block walk of one chunk (any group): returns the 16-byte share.
@@ -313,6 +455,14 @@ __device__ __forceinline__ uint64_t add64_finish(const uint8_t* chunk, int in_bi
   if (st.t) s += uint64_t(np1[0]) | uint64_t(np1[1]) << 32;
   return st.v + (party ? 0 - s : s);
 }
+
+// Stages the replicated tables in LDS (the bit-mode walk's setup).
+#define SUFHIP_DCF_TABLE_SETUP()                                   \
+  __shared__ __align__(16) uint32_t tabs[DcfAes::kWords];          \
+  __shared__ uint32_t tstage[256];                                 \
+  DcfAes::fill(tabs, tstage, kTDev.v);                             \
+  __syncthreads();                                                 \
+  const DcfAes aes = DcfAes::make(tabs)
 
 // Stages the replicated tables and the K_0..K_3 round keys in LDS.
 #define SUFHIP_DCF_LDS_SETUP(PRG)                                  \
@@ -485,12 +635,12 @@ void fill_prg4(const uint8_t* state, Prg4* p) {
 
 // Grid for the grid-stride DCF kernels: one workgroup per CU (LDS-limited),
 // never more workgroups than the batch needs.
-int dcf_grid(size_t n, unsigned int* grid) {
+int dcf_grid(size_t n, unsigned int* grid, int block = kDcfBlock) {
   int dev = 0, cus = 0;
   SUFHIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
   SUFHIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
                "hipDeviceGetAttribute(CU count)");
-  const size_t need = (n + kDcfBlock - 1) / kDcfBlock;
+  const size_t need = (n + size_t(block) - 1) / size_t(block);
   *grid = static_cast<unsigned int>(need < size_t(cus) ? need : size_t(cus));
   return SUFHIP_OK;
 }
