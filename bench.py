@@ -29,15 +29,15 @@ HBM_PEAK_GBPS = 8000.0
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch) and scaled by the
 # counters' reading for a 256 MiB device copy (FETCH x2.0, WRITE x1.0); the
 # commands and raw values are in profiles/dcf_eval_bit_kernel__dcf_batch_n2p20.md.
-MEASURED_TRAFFIC_BYTES = 1255360.3 * 1024 * 2.0 + 1230.1 * 1024 * 1.0
+MEASURED_TRAFFIC_BYTES = 2131324.3 * 1024 * 2.0 + 1200.3 * 1024 * 1.0
 # Instructions per dcf_eval_bit_kernel launch at N = 2^20 (rocprofv3 --pmc
 # SQ_INSTS_VALU SQ_INSTS_LDS, same profile file): fixed by the compiled kernel
 # and N, so lane-ops per second follow from the measured launch time.
-DCF_VALU_INSTS = 534897920
-DCF_LDS_INSTS = 330368256
+DCF_VALU_INSTS = 593684480
+DCF_LDS_INSTS = 307299328
 VALU_PEAK_GOPS = 256 * 64 * 2.4  # 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz, 32-bit integer ops
-# LDS: 128 bytes per clock per CU (a wave64 4-byte read every 2 clocks, as
-# measured for this kernel's random-index reads) x 256 CUs x 2.4 GHz.
+# LDS: 128 bytes per clock per CU for 4-byte reads (a wave64 ds_read_b32 every
+# 2 clocks, random or consecutive addresses alike, measured) x 256 CUs x 2.4 GHz.
 LDS_PEAK_GBPS = 256 * 128 * 2.4
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, 5.0 POP/s
 
