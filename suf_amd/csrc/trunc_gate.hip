@@ -471,9 +471,16 @@ __global__ void __launch_bounds__(kWalkBlock) trunc_batch_walk_kernel(WalkArgs a
     walk8_step_n<1>(c, cw, uint32_t(x >> (f - 1 - i)) & 1u, &w, n);
     w = n[0];
   }
-  if (e == kWalkLocal) {
+  if (e > 0) {
     const Walk8 root[1] = {w};
-    walk8_expand<0, kWalkLocal>(c, cw, root, v);
+    if (e == 1)
+      walk8_expand<0, 1>(c, cw, root, v);
+    else if (e == 2)
+      walk8_expand<0, 2>(c, cw, root, v);
+    else if (e == 3)
+      walk8_expand<0, 3>(c, cw, root, v);
+    else
+      walk8_expand<0, kWalkLocal>(c, cw, root, v);
   } else if (d == f) {
     walk8_leaf(c, w, v);
   } else {
@@ -513,13 +520,19 @@ __global__ void __launch_bounds__(kDcfBlock) trunc_batch_expand_kernel(BatchLeve
   }
 }
 
+int cu_count(int* cus) {
+  int dev = 0;
+  SUFHIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
+  SUFHIP_CHECK(hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev),
+               "hipDeviceGetAttribute(CU count)");
+  return SUFHIP_OK;
+}
+
 // Launch shape for the frontier kernels: spread `count` lanes over all CUs
 // (one workgroup per CU, the AES tables fill its LDS), 256..512 lanes each.
 int spread_grid(size_t count, unsigned int* grid, unsigned int* block) {
-  int dev = 0, cus = 0;
-  SUFHIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
-  SUFHIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
-               "hipDeviceGetAttribute(CU count)");
+  int cus = 0;
+  if (int rc = cu_count(&cus)) return rc;
   // At least 256 lanes per workgroup: every lane helps fill the LDS tables,
   // which dominates small launches.
   size_t per = (count + size_t(cus) - 1) / size_t(cus);
@@ -534,10 +547,8 @@ int spread_grid(size_t count, unsigned int* grid, unsigned int* block) {
 // Launch shape for the batched walk (8 lanes per walk, no grid stride): the
 // lanes spread over every CU, 128..kWalkBlock per workgroup.
 int walk_grid(size_t count, unsigned int* grid, unsigned int* block) {
-  int dev = 0, cus = 0;
-  SUFHIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
-  SUFHIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
-               "hipDeviceGetAttribute(CU count)");
+  int cus = 0;
+  if (int rc = cu_count(&cus)) return rc;
   size_t per = (count + size_t(cus) - 1) / size_t(cus);
   per = (per + 63) / 64 * 64;
   const size_t b = per < 128 ? 128 : (per > size_t(kWalkBlock) ? size_t(kWalkBlock) : per);
@@ -825,13 +836,29 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
       cur[i] = (d[i] - k0) & 1;
       if (d[i] > maxd) maxd = d[i];
     }
+    // Local levels of the full-domain walks: a walk level costs about as
+    // much as one lockstep group of the expansion, so the walks go as deep as
+    // the lanes allow -- the fewest local levels whose walks fit one full
+    // workgroup per CU (at most kWalkLocal).
+    int cus = 0;
+    if (int rc = cu_count(&cus)) return rc;
+    int el = 0;
+    for (; el < kWalkLocal; ++el) {
+      size_t lanes = 0;
+      for (int i = 0; i < m; ++i) {
+        const int k0 = k0s[i];
+        const int e = k0 == jobs[base + i].frac_bits && k0 >= el ? el : 0;
+        lanes += d[i] > 0 ? 8 * (size_t(1) << (k0 - e)) : 0;
+      }
+      if (lanes <= size_t(cus) * kWalkBlock) break;
+    }
     WalkArgs wa{};
     wa.prg = prg;
     wa.begin[0] = 0;
     for (int i = 0; i < m; ++i) {
       const sufhip_trunc_job& jb = jobs[base + i];
       const int k0 = k0s[i];
-      const int e = k0 == jb.frac_bits && k0 >= kWalkLocal ? kWalkLocal : 0;
+      const int e = k0 == jb.frac_bits && k0 >= el ? el : 0;
       wa.key[i] = jb.d_key;
       wa.out[i] = lvl[i][cur[i]];
       wa.geo[i] = uint32_t(jb.frac_bits) | uint32_t(k0) << 8 | uint32_t(e) << 16;
