@@ -256,3 +256,34 @@ def test_full_size_batch_reconstructs():
     for j, i in enumerate(range(0, n, n // 16)):
         ref = ol.myl7_eval(prg, 0, 64, k0h[j], int(xhat[i]), 1)[0] & 1
         assert int(host(b0[i:i + 1])[0]) == ref
+
+
+@pytest.mark.parametrize("mode", ["bit", "packed"])
+def test_multi_pass_ragged_batch(mode):
+    """More keys than one grid-stride pass of the bit-mode kernel covers (1024
+    lanes on each of 256 CUs), ending in a partial wave: both parties' bits
+    XOR to 1[x < alpha], and equal bit 0 of the full-share (bytes) walk."""
+    n = 256 * 1024 + 1000 + 37
+    say("dcf multi-pass ragged n=%d mode=%s" % (n, mode))
+    state = _state(5)
+    rng = np.random.default_rng(9)
+    alphas = rng.integers(0, 2**63, size=n).astype(np.uint64) * np.uint64(2)
+    seeds = rng.integers(0, 256, size=(n, 32), dtype=np.uint8)
+    k0, k1 = pfss.dcf_gen(native.GROUP_XOR, 64, state, dev(alphas),
+                          dev(np.array([1], dtype=np.uint8)), dev(seeds))
+    xs = (alphas.astype(object) + rng.integers(-2, 3, size=n).astype(object))
+    xs = np.array([int(v) % (1 << 64) for v in xs], dtype=np.uint64)
+    xd = dev(xs)
+    got = []
+    for keys in (k0, k1):
+        out = pfss.dcf_eval(0, 64, 1, state, keys, xd, MODES[mode])
+        if mode == "packed":
+            w = u64(out)
+            bits = ((w[np.arange(n) // 64] >> (np.arange(n) % 64).astype(np.uint64)) & np.uint64(1))
+            bits = bits.astype(np.uint8)
+        else:
+            bits = host(out)[:n]
+        full = host(pfss.dcf_eval(0, 64, 1, state, keys, xd, native.DCF_OUT_BYTES, out_bytes=1))
+        assert np.array_equal(bits, full.reshape(-1)[:n] & 1)
+        got.append(bits)
+    assert np.array_equal(got[0] ^ got[1], (xs < alphas).astype(np.uint8))
