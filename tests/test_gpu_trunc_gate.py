@@ -159,3 +159,25 @@ def test_batched_prepare_matches_single_gate_path():
         for p in (0, 1):
             want = u64(pfss.trunc_eval(g.kind, g.f, STATE, g.keys[p], xd))
             assert np.array_equal(u64(out[p]), want), (i, g.kind, g.f, g.n, p)
+
+
+@pytest.mark.parametrize("gates", [3, 6, 12, 24, 40])
+def test_batched_prepare_every_local_depth(gates):
+    """One walk launch expands E local levels, the fewest whose walks fit one
+    full workgroup per CU: with f = 12 tables (two per gate) and 256 CUs,
+    3 / 6 / 12 / 24 / 40 gates give E = 0 / 1 / 2 / 3 / 4.  Every gate's
+    shares equal the one-gate path's."""
+    from suf_amd import tasks
+    dealer = tasks.Dealer(100 + gates)
+    gs = [tasks.Trunc(dealer, 12, 256, STATE) for _ in range(gates)]
+    say("batched prepare, %d gates (f = 12)" % gates)
+    tasks.prepare_batch(gs)
+    rng = np.random.default_rng(gates)
+    for i, g in enumerate(gs):
+        xd = dev(rng.integers(0, 1 << 64, g.n, dtype=np.uint64))
+        out = (torch.empty(g.n, dtype=torch.int64, device="cuda"),
+               torch.empty(g.n, dtype=torch.int64, device="cuda"))
+        g.finish(xd, out)
+        for p in (0, 1):
+            want = u64(pfss.trunc_eval(g.kind, g.f, STATE, g.keys[p], xd))
+            assert np.array_equal(u64(out[p]), want), (gates, i, p)
