@@ -838,8 +838,10 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
     }
     // Local levels of the full-domain walks: a walk level costs about as
     // much as one lockstep group of the expansion, so the walks go as deep as
-    // the lanes allow -- the fewest local levels whose walks fit one full
-    // workgroup per CU (at most kWalkLocal).
+    // the lanes allow -- the fewest local levels whose walks take less than
+    // three quarters of one full workgroup per CU (at most kWalkLocal; past
+    // that the extra waves per SIMD slow every level more than a local level
+    // costs).
     int cus = 0;
     if (int rc = cu_count(&cus)) return rc;
     int el = 0;
@@ -850,7 +852,7 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
         const int e = k0 == jobs[base + i].frac_bits && k0 >= el ? el : 0;
         lanes += d[i] > 0 ? 8 * (size_t(1) << (k0 - e)) : 0;
       }
-      if (lanes <= size_t(cus) * kWalkBlock) break;
+      if (4 * lanes < 3 * size_t(cus) * kWalkBlock) break;
     }
     WalkArgs wa{};
     wa.prg = prg;

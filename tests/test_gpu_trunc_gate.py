@@ -161,12 +161,12 @@ def test_batched_prepare_matches_single_gate_path():
             assert np.array_equal(u64(out[p]), want), (i, g.kind, g.f, g.n, p)
 
 
-@pytest.mark.parametrize("gates", [3, 6, 12, 24, 40])
+@pytest.mark.parametrize("gates", [2, 4, 8, 16, 40])
 def test_batched_prepare_every_local_depth(gates):
-    """One walk launch expands E local levels, the fewest whose walks fit one
-    full workgroup per CU: with f = 12 tables (two per gate) and 256 CUs,
-    3 / 6 / 12 / 24 / 40 gates give E = 0 / 1 / 2 / 3 / 4.  Every gate's
-    shares equal the one-gate path's."""
+    """One walk launch expands E local levels, the fewest whose walks take
+    less than three quarters of one full workgroup per CU: with f = 12 tables
+    (two per gate) and 256 CUs, 2 / 4 / 8 / 16 / 40 gates give E = 0 / 1 / 2
+    / 3 / 4.  Every gate's shares equal the one-gate path's."""
     from suf_amd import tasks
     dealer = tasks.Dealer(100 + gates)
     gs = [tasks.Trunc(dealer, 12, 256, STATE) for _ in range(gates)]
