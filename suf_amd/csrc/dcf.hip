@@ -16,9 +16,10 @@
 // One element per lane; each lane streams its own key front to back
 // (33 bytes per level), so successive levels hit the same cache lines.
 //
-// The bit modes run 1024 lanes per CU (four waves per SIMD): their walk keeps
-// the round keys in scalar registers and fits in 64 VGPRs, and the table
-// lookups that bound it overlap better with more waves.
+// The evaluation kernels run 1024 lanes per CU (four waves per SIMD): their
+// walks keep the round keys in scalar registers and fit in the 128 VGPRs
+// that allows, and the table lookups that bound them overlap better with
+// more waves.
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -71,11 +72,12 @@ __global__ void __launch_bounds__(kDcfBitBlock) dcf_eval_bit_kernel(DcfEvalArgs 
 }
 
 template <int kGroup>
-__global__ void __launch_bounds__(kDcfBlock) dcf_eval_bytes_kernel(DcfEvalArgs a) {
-  SUFHIP_DCF_LDS_SETUP(a.prg);
-  const size_t stride = size_t(gridDim.x) * kDcfBlock;
+__global__ void __launch_bounds__(kDcfBitBlock) dcf_eval_bytes_kernel(DcfEvalArgs a) {
+  SUFHIP_DCF_TABLE_SETUP();
+  const KeySelPtr keys = kernarg_key_sel(offsetof(DcfEvalArgs, key_sel));
+  const size_t stride = size_t(gridDim.x) * kDcfBitBlock;
   const size_t chunk_bytes = 32 + 33 * size_t(a.in_bits);
-  for (size_t e = size_t(blockIdx.x) * kDcfBlock + threadIdx.x; e < a.n; e += stride) {
+  for (size_t e = size_t(blockIdx.x) * kDcfBitBlock + threadIdx.x; e < a.n; e += stride) {
     const uint8_t* key = a.broadcast ? a.keys : a.keys + e * a.key_bytes;
     const uint32_t party = key[2] & 1u;
     uint64_t x = a.xs[e];
@@ -83,7 +85,7 @@ __global__ void __launch_bounds__(kDcfBlock) dcf_eval_bytes_kernel(DcfEvalArgs a
     uint8_t* out = static_cast<uint8_t*>(a.out) + e * size_t(a.out_bytes);
     for (int c = 0; c < a.chunks; ++c) {
       const bool more = (c + 1) * chunk_bytes + 8 < a.key_bytes;
-      U128 r = walk_full<kGroup>(aes, rkl, key + 8 + c * chunk_bytes, a.in_bits, x, party, more);
+      U128 r = walk_full<kGroup>(aes, keys, key + 8 + c * chunk_bytes, a.in_bits, x, party, more);
       const int base = 16 * c;
       const int take = a.out_bytes - base < 16 ? a.out_bytes - base : 16;
       for (int b = 0; b < take; ++b) {
@@ -210,8 +212,8 @@ int sufhip_dcf_eval(int group, int in_bits, int payload_len, const uint8_t* prg_
   a.chunks = 1;
   a.out_bytes = out_mode == SUFHIP_DCF_OUT_BYTES ? out_bytes : 1;
   hipStream_t s = as_stream(stream);
+  fill_key_sel(a.prg, &a.key_sel);
   if (out_mode != SUFHIP_DCF_OUT_BYTES) {
-    fill_key_sel(a.prg, &a.key_sel);
     unsigned int g = 0;
     if (int rc = dcf_grid(n, &g, kDcfBitBlock)) return rc;
     const dim3 grid(g), block(kDcfBitBlock);
@@ -224,8 +226,8 @@ int sufhip_dcf_eval(int group, int in_bits, int payload_len, const uint8_t* prg_
     }
   } else {
     unsigned int g = 0;
-    if (int rc = dcf_grid(n, &g)) return rc;
-    const dim3 grid(g), block(kDcfBlock);
+    if (int rc = dcf_grid(n, &g, kDcfBitBlock)) return rc;
+    const dim3 grid(g), block(kDcfBitBlock);
     a.chunks = (out_bytes + 15) / 16;
     if (group == SUFHIP_GROUP_XOR)
       hipLaunchKernelGGL((dcf_eval_bytes_kernel<SUFHIP_GROUP_XOR>), grid, block, 0, s, a);

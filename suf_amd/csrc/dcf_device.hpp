@@ -72,22 +72,6 @@ struct CwFull {
   uint32_t tb;
 };
 
-__device__ __forceinline__ CwFull load_cw_full(const uint8_t* p) {
-  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-  const uint32_t sh = uint32_t(a & 3);
-  uint32_t r[9];
-#pragma unroll
-  for (int j = 0; j < 9; ++j) r[j] = q[j];
-  CwFull c;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    c.s[j] = __builtin_amdgcn_alignbyte(r[j + 1], r[j], sh);
-    c.v[j] = __builtin_amdgcn_alignbyte(r[j + 5], r[j + 4], sh);
-  }
-  c.tb = (r[8] >> (8 * sh)) & 0xffu;
-  return c;
-}
 
 // Reads 16 bytes at p.  When p + 16 is the end of the key (`more` false) and
 // p is not 4-byte aligned, the last sh bytes come from byte loads so that no
@@ -313,55 +297,117 @@ __device__ __forceinline__ uint32_t walk_bit(const AesLds4& aes, KeySelPtr keys,
   return (v ^ s[0] ^ (np1[0] & t)) & 1u;
 }
 
-// Full-block walk of one chunk (any group): returns the 16-byte share.
+// The aligned words 0..8 around a 33-byte correction-word record (s_cw,
+// v_cw, the t byte), read with global loads at the start of a level and
+// decoded after its AES (as CwRaw for the bit walk).
+struct CwRawFull {
+  uint32_t r[9];
+  uint32_t sh;
+};
+
+__device__ __forceinline__ CwRawFull load_cw_raw_full(const uint8_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  GlobalWords q = (GlobalWords)(a & ~uintptr_t(3));
+  CwRawFull c;
+#pragma unroll
+  for (int j = 0; j < 9; ++j) c.r[j] = q[j];
+  c.sh = uint32_t(a & 3);
+  return c;
+}
+
+__device__ __forceinline__ CwFull decode_cw_full(const CwRawFull& w) {
+  CwFull c;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    c.s[j] = __builtin_amdgcn_alignbyte(w.r[j + 1], w.r[j], w.sh);
+    c.v[j] = __builtin_amdgcn_alignbyte(w.r[j + 5], w.r[j + 4], w.sh);
+  }
+  c.tb = (w.r[8] >> (8 * w.sh)) & 0xffu;
+  return c;
+}
+
+// Full-block walk of one chunk (any group): returns the 16-byte share.  The
+// same scheme as walk_bit -- round keys chosen per lane from scalar
+// registers, grouped rounds -- with both blocks computed in full.
 template <int kGroup>
-__device__ __forceinline__ U128 walk_full(const DcfAes& aes, const uint4* rkl,
-                                          const uint8_t* chunk, int in_bits, uint64_t x,
-                                          uint32_t party, bool more_after) {
+__device__ __forceinline__ U128 walk_full(const AesLds4& aes, KeySelPtr keys, const uint8_t* chunk,
+                                          int in_bits, uint64_t x, uint32_t party,
+                                          bool more_after) {
   uint32_t seed[4];
   load16(chunk, true, seed);
-  uint32_t s0 = seed[0], s1 = seed[1], s2 = seed[2], s3 = seed[3] & 0x7fffffffu;
+  uint32_t s[4] = {seed[0], seed[1], seed[2], seed[3] & 0x7fffffffu};
   uint32_t t = party;
   U128 v{0, 0};
   const uint8_t* cw = chunk + 16;
   for (int i = 0; i < in_bits; ++i, cw += 33) {
     const uint32_t xi = uint32_t(x >> (in_bits - 1 - i)) & 1u;
-    const CwFull c = load_cw_full(cw);
-    const uint4* ks = rkl + 22 * xi;
-    const uint4* kv = ks + 11;
-    uint32_t a0 = s0, a1 = s1, a2 = s2, a3 = s3;
-    uint32_t b0 = s0, b1 = s1, b2 = s2, b3 = s3;
-    aes.encrypt(a0, a1, a2, a3, ks);
-    aes.encrypt(b0, b1, b2, b3, kv);
-    a0 ^= s0;
-    a1 ^= s1;
-    a2 ^= s2;
-    a3 ^= s3;
-    U128 vd = mk(b0 ^ s0, b1 ^ s1, b2 ^ s2, (b3 ^ s3) & 0x7fffffffu);
-    uint32_t tn = a3 >> 31;
-    a3 &= 0x7fffffffu;
+    const uint32_t m = 0u - xi;
+    const CwRawFull cr = load_cw_raw_full(cw);
+    KeySelPtr k = keys;
+    asm volatile("" : "+s"(k));
+    uint32_t A[4], B[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      A[j] = xor_and(s[j], m, k[4 + j]) ^ k[j];
+      B[j] = xor_and(s[j], m, k[12 + j]) ^ k[8 + j];
+    }
+#pragma unroll
+    for (int r = 1; r < 10; ++r) key_sel_round<4>(aes, k + 16 * r, m, A, B);
+    // Final round of both blocks: S(x) is byte 0 of T3[x], bytes 1 and 2 of
+    // T0[x] and byte 3 of T1[x].
+    uint32_t ad[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      ad[4 * c + 0] = __builtin_amdgcn_perm(A[c], aes.base[3], AesLds4::sel(0));
+      ad[4 * c + 1] = __builtin_amdgcn_perm(A[(c + 1) & 3], aes.base[0], AesLds4::sel(1));
+      ad[4 * c + 2] = __builtin_amdgcn_perm(A[(c + 2) & 3], aes.base[0], AesLds4::sel(2));
+      ad[4 * c + 3] = __builtin_amdgcn_perm(A[(c + 3) & 3], aes.base[1], AesLds4::sel(3));
+      ad[16 + 4 * c + 0] = __builtin_amdgcn_perm(B[c], aes.base[3], AesLds4::sel(0));
+      ad[16 + 4 * c + 1] = __builtin_amdgcn_perm(B[(c + 1) & 3], aes.base[0], AesLds4::sel(1));
+      ad[16 + 4 * c + 2] = __builtin_amdgcn_perm(B[(c + 2) & 3], aes.base[0], AesLds4::sel(2));
+      ad[16 + 4 * c + 3] = __builtin_amdgcn_perm(B[(c + 3) & 3], aes.base[1], AesLds4::sel(3));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t tv[32];
+#pragma unroll
+    for (int n = 0; n < 32; ++n) tv[n] = lds_word(aes.lds, ad[n]);
+    const KeySelPtr q = k + 160;
+    uint32_t kq[16];
+#pragma unroll
+    for (int n = 0; n < 16; ++n) kq[n] = q[n];
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t o[4], ob[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t lo = __builtin_amdgcn_perm(tv[4 * c + 1], tv[4 * c], 0x0c0c0500u);
+      const uint32_t hi = __builtin_amdgcn_perm(tv[4 * c + 3], tv[4 * c + 2], 0x07020c0cu);
+      o[c] = xor_and(SUFHIP_BITOP3(lo, hi, s[c], 0x56) ^ kq[c], m, kq[4 + c]);
+      const uint32_t lb = __builtin_amdgcn_perm(tv[16 + 4 * c + 1], tv[16 + 4 * c], 0x0c0c0500u);
+      const uint32_t hb = __builtin_amdgcn_perm(tv[16 + 4 * c + 3], tv[16 + 4 * c + 2], 0x07020c0cu);
+      ob[c] = xor_and(SUFHIP_BITOP3(lb, hb, s[c], 0x56) ^ kq[8 + c], m, kq[12 + c]);
+    }
+    const CwFull c = decode_cw_full(cr);
+    U128 vd = mk(ob[0], ob[1], ob[2], ob[3] & 0x7fffffffu);
+    uint32_t tn = o[3] >> 31;
+    o[3] &= 0x7fffffffu;
     if (t) {
-      a0 ^= c.s[0];
-      a1 ^= c.s[1];
-      a2 ^= c.s[2];
-      a3 ^= c.s[3];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] ^= c.s[j];
       tn ^= (xi ? c.tb : (c.tb >> 1)) & 1u;
       vd = gadd<kGroup>(vd, mk(c.v[0], c.v[1], c.v[2], c.v[3]));
     }
     if (party) vd = gneg<kGroup>(vd);
     v = gadd<kGroup>(v, vd);
-    s0 = a0;
-    s1 = a1;
-    s2 = a2;
-    s3 = a3;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = o[j];
     t = tn;
   }
   uint32_t np1[4];
   load16(cw, more_after, np1);
-  U128 s = mk(s0, s1, s2, s3);
-  if (t) s = gadd<kGroup>(s, mk(np1[0], np1[1], np1[2], np1[3]));
-  if (party) s = gneg<kGroup>(s);
-  return gadd<kGroup>(v, s);
+  U128 sv = mk(s[0], s[1], s[2], s[3]);
+  if (t) sv = gadd<kGroup>(sv, mk(np1[0], np1[1], np1[2], np1[3]));
+  if (party) sv = gneg<kGroup>(sv);
+  return gadd<kGroup>(v, sv);
 }
 
 // Additive-group walk that keeps only the low 64 bits of the 16-byte
