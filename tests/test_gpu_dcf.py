@@ -287,3 +287,35 @@ def test_multi_pass_ragged_batch(mode):
         assert np.array_equal(bits, full.reshape(-1)[:n] & 1)
         got.append(bits)
     assert np.array_equal(got[0] ^ got[1], (xs < alphas).astype(np.uint8))
+
+
+def test_bytes_multi_pass_additive_group():
+    """The full-share walk over several grid-stride passes (1024 lanes on each
+    of 256 CUs) in the additive group with an 8-byte payload: byte 0 of the
+    two shares sums to payload[0] exactly where x < alpha, and the shares at
+    indices around every pass boundary equal the oracle's."""
+    n = 2 * 256 * 1024 + 517
+    plen = 8
+    say("dcf bytes multi-pass additive n=%d" % n)
+    state = _state(8)
+    prg = ol.Prg(state)
+    rng = np.random.default_rng(13)
+    alphas = rng.integers(0, 2**63, size=n).astype(np.uint64) * np.uint64(2)
+    seeds = rng.integers(0, 256, size=(n, 32), dtype=np.uint8)
+    payload = rng.integers(1, 256, size=plen, dtype=np.uint8)
+    k0, k1 = pfss.dcf_gen(native.GROUP_ADD, 64, state, dev(alphas), dev(payload), dev(seeds))
+    xs = np.array([(int(a) + int(d)) % (1 << 64) for a, d in
+                   zip(alphas, rng.integers(-2, 3, size=n))], dtype=np.uint64)
+    xd = dev(xs)
+    outs = [host(pfss.dcf_eval(native.GROUP_ADD, 64, plen, state, keys, xd, native.DCF_OUT_BYTES,
+                               out_bytes=plen)).reshape(n, plen) for keys in (k0, k1)]
+    b0 = (outs[0][:, 0].astype(np.int64) + outs[1][:, 0].astype(np.int64)) & 0xFF
+    assert np.array_equal(b0, np.where(xs < alphas, int(payload[0]), 0))
+    stride = 256 * 1024
+    idx = sorted({0, 1, stride - 1, stride, stride + 1, 2 * stride - 1, 2 * stride, n - 1} |
+                 set(range(0, n, 9973)))
+    for p, keys in ((0, k0), (1, k1)):
+        kh = host(keys[torch.tensor(idx, device="cuda")])
+        for j, i in enumerate(idx):
+            ref = ol.myl7_eval(prg, native.GROUP_ADD, 64, kh[j], int(xs[i]), plen)
+            assert outs[p][i].tobytes() == ref.tobytes(), (p, i)
