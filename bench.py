@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gates", action="store_true",
                     help="skip the spline-gate and Beaver matmul pipeline timings")
+    ap.add_argument("--no-shared", action="store_true",
+                    help="configs 2, 4, 5: skip the shared-keystream timings (profiling runs)")
     ap.add_argument("--only", choices=["spline", "matmul", "softmax_ln", "layer"],
                     help="run one gate pipeline alone and print its result object "
                          "(for profiling; not the benchmark line)")
@@ -135,12 +137,12 @@ def roofline_hbm(kernel, kernel_ms, bytes_per_launch, basis, note=None, traffic=
     return r
 
 
-def roofline_mfma(kernel, kernel_ms, ops_per_launch, basis, note=None):
+def roofline_mfma(kernel, kernel_ms, ops_per_launch, basis, note=None, traffic=None):
     """The same for a matrix-core kernel: int8 MFMA ops per launch / the
     measured launch time, against the dense int8 peak (5.0 POP/s)."""
     achieved = ops_per_launch / (kernel_ms / 1e3) / 1e12
     r = {"bound": "mfma", "achieved": achieved, "peak": INT8_PEAK_TOPS, "unit": "TOP/s (int8)",
-         "frac": achieved / INT8_PEAK_TOPS, "traffic": None, "kernel": kernel,
+         "frac": achieved / INT8_PEAK_TOPS, "traffic": traffic, "kernel": kernel,
          "kernel_ms": kernel_ms, "ops_per_launch": ops_per_launch, "basis": basis}
     if note:
         r["note"] = note
@@ -196,56 +198,56 @@ def _timed(fn, threads):
         ol.set_threads(0)
 
 
-def _party1_nonce_flip(luts):
-    """Flips one bit of the nonce (bytes 16..23 of the blob) of each party-1
-    interval-LUT key in place.  The kernels then find the two parties' blobs
-    different and compute one keystream per party; the shares are wrong
-    until the flip is undone (calling this again)."""
-    for t in luts:
-        t[16] ^= 1
+# Algorithmic HBM bytes of the two-party task kernels: the streams each
+# element (or row) brings in or sends out, both parties.  The truncation
+# gates' full-domain tables (2^f entries of which an evaluation reads the
+# 16-byte value half) and the LUT blobs are read by every workgroup but
+# stay in L2, so they count once per launch, at most 2^f x 16 bytes per gate
+# and party.  A CUBIC chain (spline gate, GeLU, nExp) streams x (16), three
+# products' triples (3 x 2 parties x 3 words x 8 = 144) and the output (16).
+CHAIN_CUBIC_BYTES = 16 + 144 + 16
 
 
-def _gate_luts(*objs):
-    """Party 1's LUT key tensors of spline gates, CoeffLuts and the blocks
-    built from them."""
-    out = []
-    for o in objs:
-        name = type(o).__name__
-        if name == "SplineGate":
-            out.append(o.lut[1])
-        elif name == "CoeffLut":
-            out.append(o.keys[1])
-        elif name == "SoftmaxBlock":
-            out += _gate_luts(o.nexp, o.recip.lut) + [r["lut"].keys[1] for r in o.rowmax.rounds]
-        elif name == "LayerNormBlock":
-            out += _gate_luts(o.rsqrt.lut)
-        elif name == "TransformerLayer":
-            out += _gate_luts(o.ln1, o.attn.softmax, o.ln2, o.gelu)
-    return out
-
-
-# Algorithmic HBM bytes per element of the two-party task kernels: both
-# parties' operands and outputs, and the truncation-table reads (16 bytes per
-# gate and party).  A CUBIC chain (spline gate, GeLU, nExp) reads x (16),
-# three products' triples (3 x 2 parties x 3 words x 8 = 144), three gates'
-# table entries (96) and writes 16.
-CHAIN_CUBIC_BYTES = 16 + 144 + 96 + 16
+def trunc_table_bytes(gates, f=12):
+    """Bytes of the value halves of `gates` truncation tables, both parties."""
+    return gates * 2 * (1 << f) * 16
 
 
 def softmax_bytes(n_packed, rows, pre=0, indexed_input=False, out_written=True, n_dense=0,
                   dense_planes=False):
-    """softmax2_kernel: per packed element the scores (16, + a 4-byte index),
-    `pre` gates' table reads (32 each), the nExp chain (triples 144 + tables
-    96), the normalisation's a and c shares (32) and table read (32), the
-    probabilities (16); per row the reciprocal chain (triples 144 + tables
-    96), the normalisation's b shares (16) and the row offset (4); per dense
-    element the A shares (16) and the open (8, + 8 for its digit planes)."""
-    per = 16 + (4 if indexed_input else 0) + 32 * pre + 144 + 96 + 32 + 32 + \
-        (16 if out_written else 0)
-    return n_packed * per + rows * (144 + 96 + 16 + 4) + n_dense * (16 + 8 + (8 if dense_planes else 0))
+    """softmax2_kernel's streams: per packed element the scores (16, + a
+    4-byte index), the nExp chain's triples (144), the normalisation's a and
+    c shares (32), the probabilities (16); per row the reciprocal chain's
+    triples (144), the normalisation's b shares (16) and the row offset (4);
+    per dense element the A shares (16) and the open (8, + 8 for its digit
+    planes); once per launch the tables of the `pre` score truncations, the
+    nExp and reciprocal chains' three gates each and the normalisation's."""
+    per = 16 + (4 if indexed_input else 0) + 144 + 32 + (16 if out_written else 0)
+    return (n_packed * per + rows * (144 + 16 + 4)
+            + n_dense * (16 + 8 + (8 if dense_planes else 0))
+            + trunc_table_bytes(pre + 3 + 3 + 1))
 
 
-def bench_spline(steps, warmup, n=1 << 20, frac_bits=12, cpu_seconds=0.0):
+# HBM traffic per launch of the config 2-5 kernels at the default shapes with
+# per-party keystreams: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE (KiB per
+# dispatch, mean over the run's launches of the kernel), scaled by the
+# counters' reading for a 256 MiB device copy (FETCH x2.0, WRITE x1.0); the
+# commands and raw values are in profiles/gate_pipelines__spline_n2p20__
+# matmul_128x768x3072__softmax_ln.md and profiles/secure_layer__gpt2_small_
+# seq128.md.  None where not measured.
+def _traffic(fetch_kib, write_kib):
+    if fetch_kib is None or write_kib is None:
+        return None
+    return fetch_kib * 1024 * 2.0 + write_kib * 1024 * 1.0
+
+
+SPLINE_CHAIN_TRAFFIC = _traffic(86130.5, 16384.0)
+MATMUL_PRODUCT_TRAFFIC = _traffic(41173, 6144)
+SOFTMAX_TRAFFIC = _traffic(15061.2, 1560.6)
+LAYER_SOFTMAX_TRAFFIC = _traffic(17833.8, 4622.8)
+
+
+def bench_spline(steps, warmup, n=1 << 20, frac_bits=12, cpu_seconds=0.0, shared=True):
     """The spline gate (interval LUT + three Beaver products + GapARS by f and
     2f) for both parties on N = 2^20 inputs x = clip(3 N(0,1), +-8) in Q12
     (Box-Muller on mt(5)); coefficients from mt(6); dealer randomness mt(7).
@@ -269,36 +271,38 @@ def bench_spline(steps, warmup, n=1 << 20, frac_bits=12, cpu_seconds=0.0):
         # The truncations' key-only halves first, on the same stream.
         gate.eval2(xd, out, prep=(tasks.Prepared(None, [gate.truncs()]), 0))
 
-    ms, eager_ms = _graph_ms(run, steps, warmup)
     # The chain launch alone (its truncations prepared once beforehand).
     prepared = tasks.Prepared(None, [gate.truncs()])
     chain = lambda: gate.eval2(xd, out, prep=(prepared, 0))  # noqa: E731
-    chain()
-    chain_ms = _launch_ms(chain, steps)
-    gpu = [out[0].cpu().numpy().view(np.uint64).copy(), out[1].cpu().numpy().view(np.uint64).copy()]
-    # Two keystreams (one per party) instead of the shared one.
-    luts = _gate_luts(gate)
-    _party1_nonce_flip(luts)
-    try:
+    with pfss.keystream_per_party():
+        ms, eager_ms = _graph_ms(run, steps, warmup)
         chain()
-        unshared_ms = _launch_ms(chain, steps)
-    finally:
-        _party1_nonce_flip(luts)
+        chain_ms = _launch_ms(chain, steps)
+    gpu = [out[0].cpu().numpy().view(np.uint64).copy(), out[1].cpu().numpy().view(np.uint64).copy()]
+    # The same with one keystream for both parties (one process, one dealer key).
+    ms_shared = chain_ms_shared = None
+    if shared:
+        ms_shared, _ = _graph_ms(run, steps, warmup)
+        chain()
+        chain_ms_shared = _launch_ms(chain, steps)
+    nbytes = CHAIN_CUBIC_BYTES * n + trunc_table_bytes(3, frac_bits)
     res = {"ms": ms, "eager_ms": eager_ms, "n": n, "frac_bits": frac_bits,
            "intervals": int(gate.intervals),
            "trunc": "GapARS f=%d (x3: the 2f truncation as two f truncations)" % frac_bits,
            "steps": steps,
-           "roofline": roofline_hbm("gate_chain_kernel (CUBIC)", chain_ms, CHAIN_CUBIC_BYTES * n,
-                                    "%d B per element (x 16, triples 144, truncation-table reads "
-                                    "96, out 16) x N" % CHAIN_CUBIC_BYTES,
-                                    note="the chain's AES-CTR keystream and dependent steps bind "
-                                         "it, not HBM"),
-           "keystream_shared": True,
-           "chain_ms_unshared": unshared_ms,
-           "keystream_note": "both parties' LUT blobs come from one dealer key "
-                             "(seed_from_id), so one process computes each keystream block once "
-                             "for both; chain_ms_unshared is the same launch with a keystream "
-                             "per party, as two separate parties would compute them",
+           "roofline": roofline_hbm("gate_chain_kernel (CUBIC)", chain_ms, nbytes,
+                                    "%d B per element (x 16, triples 144, out 16) x N + 3 "
+                                    "truncation tables once (2 x 2^%d x 16 B each)"
+                                    % (CHAIN_CUBIC_BYTES, frac_bits),
+                                    note="per-party keystreams; the chain's AES-CTR keystream "
+                                         "and dependent steps bind it, not HBM",
+                                    traffic=SPLINE_CHAIN_TRAFFIC if n == 1 << 20 else None),
+           "keystream": "per party",
+           "ms_shared": ms_shared, "chain_ms_shared": chain_ms_shared,
+           "keystream_note": "ms and the roofline: each party computes its own LUT keystream, "
+                             "as two parties in separate processes do.  Both parties' blobs come "
+                             "from one dealer key (seed_from_id), so one process can compute each "
+                             "keystream block once for both: *_shared",
            "check": "not run (--no-cpu)"}
     if cpu_seconds > 0:
         res.update(cpu_spline_baseline(gate, state, x, x0, x1, gpu, alpha, coeffs, frac_bits))
@@ -389,7 +393,8 @@ def bench_matmul(steps, warmup, M=128, K=768, N=3072, frac_bits=12, cpu_seconds=
         res["product_ms"] = prod_ms
         res["roofline"] = roofline_mfma(
             "beaver_bal_kernel", prod_ms, mfmas * 2 * 32 * 32 * 32,
-            "%d v_mfma_i32_32x32x32_i8 (tiles x k-steps x 144 digit products) x 65536 ops" % mfmas)
+            "%d v_mfma_i32_32x32x32_i8 (tiles x k-steps x 144 digit products) x 65536 ops" % mfmas,
+            traffic=MATMUL_PRODUCT_TRAFFIC if (M, K, N) == (128, 768, 3072) else None)
     if cpu_seconds > 0:
         res["cpu_baseline"] = cpu_matmul_baseline(g, state, Xd, Wd, out, cpu_seconds)
     return res
@@ -452,7 +457,7 @@ def cpu_matmul_baseline(g, state, Xd, Wd, out, seconds):
                       % (rows, M, T, mism), "mismatches": mism, "host": host_info()}
 
 
-def bench_softmax_ln(steps, warmup, frac_bits=12, cpu=True):
+def bench_softmax_ln(steps, warmup, frac_bits=12, cpu=True, shared=True):
     """Softmax over 12 heads x 128 x 128 causal score rows (scores
     round(N(0,2) 2^12), mt(11)) followed by LayerNorm over 128 x 768
     (round(N(0,1) 2^12), mt(12)), both parties; shares from mt(111), mt(121);
@@ -498,21 +503,23 @@ def bench_softmax_ln(steps, warmup, frac_bits=12, cpu=True):
         if ev:
             ev[2].record()
 
-    ms, eager_ms = _graph_ms(run, steps, warmup)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
-    for s in range(steps):
-        run(ev[s])
-    torch.cuda.synchronize()
-    sm_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]))
-    ln_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
+    def split_ms():
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        for s in range(steps):
+            run(ev[s])
+        torch.cuda.synchronize()
+        return (float(np.mean([e[0].elapsed_time(e[1]) for e in ev])),
+                float(np.mean([e[1].elapsed_time(e[2]) for e in ev])))
+
+    with pfss.keystream_per_party():
+        ms, eager_ms = _graph_ms(run, steps, warmup)
+        sm_ms, ln_ms = split_ms()
     gpu_s = [sout[p].cpu().numpy().view(np.uint64).copy() for p in (0, 1)]
     gpu_l = [lout[p].cpu().numpy().view(np.uint64).copy() for p in (0, 1)]
-    luts = _gate_luts(sm, ln)
-    _party1_nonce_flip(luts)
-    try:
-        unshared_ms, _ = _graph_ms(run, steps, 1)
-    finally:
-        _party1_nonce_flip(luts)
+    ms_shared = sm_ms_shared = ln_ms_shared = None
+    if shared:
+        ms_shared, _ = _graph_ms(run, steps, 1)
+        sm_ms_shared, ln_ms_shared = split_ms()
     res = {"ms": ms, "eager_ms": eager_ms, "softmax_ms": sm_ms, "layernorm_ms": ln_ms,
            "split": "softmax_ms / layernorm_ms: each block's one launch, eager, without the "
                     "shared prepare walk",
@@ -520,12 +527,18 @@ def bench_softmax_ln(steps, warmup, frac_bits=12, cpu=True):
            "layernorm_shape": [rows, cols], "frac_bits": frac_bits, "steps": steps,
            "roofline": roofline_hbm(
                "softmax2_kernel", sm_ms, softmax_bytes(n_sm, len(offs) - 1),
-               "per score 16 in + nExp chain 240 + normalisation 64 + 16 out, per row 260",
-               note="bound by each row's chain of dependent steps (max tree rounds, keystream "
-                    "AES, table reads), not HBM"),
-           "layernorm_bytes": rows * cols * (16 + 48 + 32 + 32 + 16),
-           "keystream_shared": True, "ms_unshared": unshared_ms,
-           "keystream_note": "ms_unshared: the same graph with a keystream per party",
+               "per score 16 in + nExp triples 144 + normalisation shares 32 + 16 out; per row "
+               "164; 7 truncation tables once (2 x 2^12 x 16 B each)",
+               note="per-party keystreams; bound by each row's chain of dependent steps (max "
+                    "tree rounds, keystream AES, table reads), not HBM",
+               traffic=SOFTMAX_TRAFFIC),
+           "layernorm_bytes": rows * cols * (16 + 48 + 32 + 16),
+           "keystream": "per party",
+           "ms_shared": ms_shared, "softmax_ms_shared": sm_ms_shared,
+           "layernorm_ms_shared": ln_ms_shared,
+           "keystream_note": "ms, the split and the roofline: each party computes its own LUT "
+                             "keystreams; *_shared: one keystream block for both parties (one "
+                             "process, one dealer key per gate)",
            "check": "not run (--no-cpu)"}
     if cpu:
         res.update(cpu_softmax_ln_baseline(state, sm, ln, (s0, s1), (l0, l1), sc, xl, gpu_s,
@@ -585,7 +598,7 @@ LAYER_DEVIATIONS = [
 ]
 
 
-def bench_layer(steps, warmup, frac_bits=12, cpu=True):
+def bench_layer(steps, warmup, frac_bits=12, cpu=True, shared=True):
     """One GPT-2-small-shaped secure layer (hidden 768, 12 heads, seq 128, FFN
     3072, GeLU) for both parties: weights round(N(0,0.02) 2^12) (mt(13) and
     derived seeds), input x = round(N(0,1) 2^12) (mt(14)) shared with mt(141);
@@ -606,59 +619,57 @@ def bench_layer(steps, warmup, frac_bits=12, cpu=True):
     xin = (dev(x0), dev(x1))
     ly = layer.TransformerLayer(state, W, seq, d, heads, ffn, frac_bits, seed=13)
     out = tuple(torch.empty(seq * d, dtype=torch.int64, device="cuda") for _ in range(2))
-    for _ in range(warmup):
-        ly.eval2(xin, out)
-    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        ly.eval2(xin, out)
-    e1.record()
-    torch.cuda.synchronize()
-    eager_ms = e0.elapsed_time(e1) / steps
-    # Per-stage split of one more eager run (events between stages; launch
-    # overhead included, so the stages sum to more than the graph replay),
-    # and the softmax block's launch in each eager run.
-    stages = ["ln1", "qkv", "attention", "out_proj+residual", "ln2", "w1", "gelu",
-              "w2+residual"]
-    m = []
-    ly.eval2(xin, out, marks=m)
-    torch.cuda.synchronize()
-    per_stage = {stages[i]: m[i].elapsed_time(m[i + 1]) for i in range(len(stages))}
-    smk = []
-    for _ in range(steps):
-        ly.eval2(xin, out, sm_marks=smk)
-    torch.cuda.synchronize()
-    sm_ms = float(np.mean([smk[2 * i].elapsed_time(smk[2 * i + 1]) for i in range(len(smk) // 2)]))
-    eager_out = [out[0].cpu().numpy().view(np.uint64).copy(),
-                 out[1].cpu().numpy().view(np.uint64).copy()]
-    g = tasks.capture(lambda: ly.eval2(xin, out))
-    torch.cuda.synchronize()
-    replay_ok = True
-    for _ in range(2):  # replays agree with the eager result
-        g.replay()
-        torch.cuda.synchronize()
-        replay_ok = replay_ok and all(np.array_equal(out[p].cpu().numpy().view(np.uint64),
-                                                     eager_out[p]) for p in (0, 1))
-    e0.record()
-    for _ in range(steps):
-        g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    graph_ms = e0.elapsed_time(e1) / steps
-    luts = _gate_luts(ly)
-    _party1_nonce_flip(luts)
-    try:
-        for _ in range(2):
-            g.replay()
+
+    def timed(fn):
         e0.record()
         for _ in range(steps):
-            g.replay()
+            fn()
         e1.record()
         torch.cuda.synchronize()
-        unshared_ms = e0.elapsed_time(e1) / steps
-    finally:
-        _party1_nonce_flip(luts)
+        return e0.elapsed_time(e1) / steps
+
+    def measure():
+        """(graph ms, eager ms, per-stage eager ms, softmax launch ms, graph,
+        eager outputs, replays match) under the current keystream policy."""
+        for _ in range(warmup):
+            ly.eval2(xin, out)
+        torch.cuda.synchronize()
+        eager_ms = timed(lambda: ly.eval2(xin, out))
+        # Per-stage split of one more eager run (events between stages;
+        # launch overhead included, so the stages sum to more than the graph
+        # replay), and the softmax block's launch in each eager run.
+        stages = ["ln1", "qkv", "attention", "out_proj+residual", "ln2", "w1", "gelu",
+                  "w2+residual"]
+        m = []
+        ly.eval2(xin, out, marks=m)
+        torch.cuda.synchronize()
+        per_stage = {stages[i]: m[i].elapsed_time(m[i + 1]) for i in range(len(stages))}
+        smk = []
+        for _ in range(steps):
+            ly.eval2(xin, out, sm_marks=smk)
+        torch.cuda.synchronize()
+        sm_ms = float(np.mean([smk[2 * i].elapsed_time(smk[2 * i + 1])
+                               for i in range(len(smk) // 2)]))
+        eager_out = [out[0].cpu().numpy().view(np.uint64).copy(),
+                     out[1].cpu().numpy().view(np.uint64).copy()]
+        g = tasks.capture(lambda: ly.eval2(xin, out))
+        torch.cuda.synchronize()
+        ok = True
+        for _ in range(2):  # replays agree with the eager result
+            g.replay()
+            torch.cuda.synchronize()
+            ok = ok and all(np.array_equal(out[p].cpu().numpy().view(np.uint64), eager_out[p])
+                            for p in (0, 1))
+        return timed(g.replay), eager_ms, per_stage, sm_ms, g, eager_out, ok
+
+    with pfss.keystream_per_party():
+        graph_ms, eager_ms, per_stage, sm_ms, g, eager_out, replay_ok = measure()
+    graph_ms_shared = eager_ms_shared = sm_ms_shared = None
+    if shared:
+        graph_ms_shared, eager_ms_shared, _, sm_ms_shared, _, eager_shared, ok_shared = measure()
+        replay_ok = replay_ok and ok_shared and all(
+            np.array_equal(eager_out[p], eager_shared[p]) for p in (0, 1))
     at = ly.attn
     res = {"ms": graph_ms, "eager_ms": eager_ms, "stages_eager_ms": per_stage,
            "shape": {"seq": seq, "hidden": d, "heads": heads, "ffn": ffn}, "frac_bits": frac_bits,
@@ -668,11 +679,18 @@ def bench_layer(steps, warmup, frac_bits=12, cpu=True):
                sm_ms, softmax_bytes(at.n, heads * seq, pre=2, indexed_input=True,
                                     out_written=False, n_dense=heads * seq * seq,
                                     dense_planes=True),
-               "per packed score 20 in + 2 truncations 64 + nExp chain 240 + normalisation 64, "
-               "per row 260, per dense entry 32",
-               note="the layer's largest kernel; bound by each row's dependent chain"),
-           "keystream_shared": True, "ms_unshared": unshared_ms,
-           "keystream_note": "ms_unshared: the same graph with a keystream per party",
+               "per packed score 20 in + nExp triples 144 + normalisation shares 32; per row "
+               "164; per dense entry 32; 9 truncation tables once (2 x 2^12 x 16 B each)",
+               note="per-party keystreams; the layer's largest kernel, bound by each row's "
+                    "dependent chain",
+               traffic=LAYER_SOFTMAX_TRAFFIC),
+           "keystream": "per party",
+           "ms_shared": graph_ms_shared, "eager_ms_shared": eager_ms_shared,
+           "softmax_ms_shared": sm_ms_shared,
+           "keystream_note": "ms, the stages and the roofline: each party computes its own LUT "
+                             "keystreams, as two parties in separate processes do; *_shared: "
+                             "one keystream block for both parties (one process, one dealer key "
+                             "per gate); both policies give the same shares",
            "protocol_deviations": LAYER_DEVIATIONS,
            "check": "not run (--no-cpu)" if replay_ok else "MISMATCH"}
     if cpu:
@@ -781,10 +799,13 @@ def main():
 
         native.call("sufhip_init", 0)
         cpu_s = 0.0 if a.no_cpu else a.cpu_seconds / 2
-        run = {"spline": lambda: bench_spline(a.steps, a.warmup, cpu_seconds=cpu_s),
+        sh = not a.no_shared
+        run = {"spline": lambda: bench_spline(a.steps, a.warmup, cpu_seconds=cpu_s, shared=sh),
                "matmul": lambda: bench_matmul(a.steps, a.warmup, cpu_seconds=cpu_s),
-               "softmax_ln": lambda: bench_softmax_ln(a.steps, a.warmup, cpu=not a.no_cpu),
-               "layer": lambda: bench_layer(a.steps, a.warmup, cpu=not a.no_cpu)}[a.only]
+               "softmax_ln": lambda: bench_softmax_ln(a.steps, a.warmup, cpu=not a.no_cpu,
+                                                      shared=sh),
+               "layer": lambda: bench_layer(a.steps, a.warmup, cpu=not a.no_cpu,
+                                            shared=sh)}[a.only]
         res = run()
         print(json.dumps({"only": a.only, **res}), flush=True)
         sys.exit(0 if res["check"] in ("ok", "not run (--no-cpu)") else 1)
@@ -916,19 +937,23 @@ def main():
     progress("dcf batch: %.3g evals/s" % value)
     if not a.no_gates:
         gate_cpu = 0.0 if a.no_cpu else a.cpu_seconds / 2
-        line["spline_gate"] = bench_spline(max(a.steps // 2, 1), 2, cpu_seconds=gate_cpu)
+        sh = not a.no_shared
+        line["spline_gate"] = bench_spline(max(a.steps // 2, 1), 2, cpu_seconds=gate_cpu,
+                                           shared=sh)
         progress("spline gate: %.4f ms" % line["spline_gate"]["ms"])
         line["beaver_matmul_trunc"] = bench_matmul(max(a.steps // 2, 1), 2, cpu_seconds=gate_cpu)
         progress("beaver matmul + trunc: %.4f ms" % line["beaver_matmul_trunc"]["ms"])
-        line["softmax_layernorm"] = bench_softmax_ln(max(a.steps // 2, 1), 2, cpu=not a.no_cpu)
+        line["softmax_layernorm"] = bench_softmax_ln(max(a.steps // 2, 1), 2, cpu=not a.no_cpu,
+                                                     shared=sh)
         progress("softmax + layernorm: %.4f ms" % line["softmax_layernorm"]["ms"])
-        line["secure_layer"] = bench_layer(max(a.steps // 2, 1), 2, cpu=not a.no_cpu)
+        line["secure_layer"] = bench_layer(max(a.steps // 2, 1), 2, cpu=not a.no_cpu, shared=sh)
         progress("secure layer: %.4f ms" % line["secure_layer"]["ms"])
         line["secure_layer_ms"] = line["secure_layer"]["ms"]
         line["secure_layer_note"] = ("one HIP-graph replay of suf_amd/layer.py's two-party "
-                                     "layer (both parties, one GPU, keystreams shared); "
-                                     "protocol deviations from transformer_layer_forward are "
-                                     "listed in secure_layer.protocol_deviations")
+                                     "layer (both parties, one GPU, each party's LUT "
+                                     "keystreams its own); protocol deviations from "
+                                     "transformer_layer_forward are listed in "
+                                     "secure_layer.protocol_deviations")
         ok = ok and line["spline_gate"]["check"] in ("ok", "not run (--no-cpu)")
         ok = ok and line["beaver_matmul_trunc"]["check"] == "ok"
         ok = ok and line["softmax_layernorm"]["check"] in ("ok", "not run (--no-cpu)")

@@ -62,6 +62,20 @@ int sufhip_abi_version(void);
 const char* sufhip_last_error(void);
 /* Selects the device for the calling thread and loads the kernels. */
 int sufhip_init(int device);
+/* Keystream policy of the two-party LUT evaluations (gate chains, the
+ * softmax and LayerNorm blocks, the max tree).  SUF's dealer gives both
+ * parties of a LUT gate one AES key (seed_from_id,
+ * cuda/pfss_backend_gpu.cu:508-515), so with both parties in one process a
+ * kernel can compute each keystream block once for both (per_party = 0, the
+ * default; used only where the two blobs' keys, nonce, mask and cut points
+ * compare equal on the device).  per_party = 1 makes every kernel compute
+ * each party's keystream and interval search from that party's own blob, as
+ * two parties in separate processes do: the same shares, the two-process
+ * cost.  Process-wide; read when a launch is issued, so a captured HIP graph
+ * keeps the policy it was captured with.  No counterpart in the reference
+ * (its parties never share a process). */
+int sufhip_set_keystream_per_party(int per_party);
+int sufhip_keystream_per_party(void);
 int sufhip_device_count(int* count);
 int sufhip_stream_create(void** stream);
 int sufhip_stream_destroy(void* stream);
@@ -930,14 +944,15 @@ int sufhip_composite_bool2(const sufhip_composite_bool_args* args, void* stream)
 
 /* One flush of a two-party open collector (the device path of
  * OpenCollector::flush, src/runtime/open_collector.cpp:357-791): the
- * requests' shares (device, both parties) are gathered, each party's are
+ * requests' shares (device, both parties) are gathered, party 1's are
  * packed to eff_bits (the message it sends: launch_pack_eff_bits_kernel),
  * and party 0's own shares plus party 1's unpacked message give the opened
  * values (launch_unpack_add_mod_kernel; launch_unpack_add_to_signed_kernel
  * when sign_extend), masked to ring_bits, back to back in request order in
  * d_opened: (s0 + (s1 mod 2^eff_bits)) mod 2^ring_bits, exact when
- * eff_bits >= ring_bits or party 1's shares fit eff_bits.  Four launches
- * for any number of requests.  d_work: 8-byte aligned,
+ * eff_bits >= ring_bits or party 1's shares fit eff_bits.  Launches:
+ * 2 * ceil(count / 64) gathers, one pack, one unpack-add (four for up to 64
+ * requests).  d_work: 8-byte aligned,
  * sufhip_open_flush2_work_bytes(total, eff_bits) bytes. */
 typedef struct sufhip_open_req {
   const uint64_t* share[2];

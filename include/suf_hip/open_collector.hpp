@@ -9,10 +9,10 @@
 //   * reserve() hands out device views for party 0 and party 1 (the
 //     caller's kernels fill them); enqueue() takes two device share vectors,
 //     which it reads at flush() without copying them first;
-//   * flush() takes no party or channel: each party's shares are packed to
-//     eff_bits (the message it would send) and party 0 adds party 1's
-//     unpacked message, all in four launches on the collector's stream
-//     (sufhip_open_flush2).  It returns without waiting for the GPU:
+//   * flush() takes no party or channel: party 1's shares are packed to
+//     eff_bits (the message it would send) and party 0 adds that unpacked
+//     message to its own, on the collector's stream (sufhip_open_flush2:
+//     2 * ceil(requests / 64) gather launches, one pack, one unpack-add).  It returns without waiting for the GPU:
 //     view_device_u64() pointers are valid in that stream's order; view() and
 //     view_u64() copy the opened values to the host once per flush and wait.
 //   * Stats::wire_bytes_sent counts one party's packed message, the bytes it

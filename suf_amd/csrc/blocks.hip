@@ -269,7 +269,11 @@ struct SmStager {
     tf.store(st.tab);
     hn.store(st.thn);
     hr.store(st.thr);
-    if (threadIdx.x == 0) st.t.diff = st.nexp.diff = st.recip.diff = 0;
+    if (threadIdx.x == 0) {
+      st.t.diff = a.keys.own_ks;
+      st.nexp.diff = a.nexp.own_ks;
+      st.recip.diff = a.recip.own_ks;
+    }
   }
 };
 

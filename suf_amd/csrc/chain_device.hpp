@@ -62,6 +62,9 @@ struct ChainArgs {
   const uint64_t* pa[4][2];
   const uint64_t* pb[4][2];
   const uint64_t* pc[4][2];
+  // Nonzero: each party's keystream and interval search from its own blob,
+  // even where the blobs compare equal (sufhip_set_keystream_per_party).
+  uint32_t own_ks;
 };
 
 struct Two {
@@ -258,7 +261,7 @@ struct ChainStager {
     }
     for (int c = int(threadIdx.x) + kPer * kThreads; c < n; c += kThreads)
       chain_item_store(A, W, L, c, chain_item_load(A, W, c));
-    if (threadIdx.x == 0) L.diff = 0;
+    if (threadIdx.x == 0) L.diff = A.own_ks;
   }
 };
 
@@ -266,7 +269,7 @@ struct ChainStager {
 // Thread t takes items t + m * blockDim, two at a time with both loads
 // issued before the stores.
 __device__ __forceinline__ void chain_stage(const ChainArgs& A, int W, ChainLds& L) {
-  if (threadIdx.x == 0) L.diff = 0;
+  if (threadIdx.x == 0) L.diff = A.own_ks;
   const int n = chain_items(A, W);
   for (int i = threadIdx.x; i < n; i += 2 * blockDim.x) {
     const int i2 = i + blockDim.x;
@@ -611,6 +614,7 @@ inline int make_chain_args(const sufhip_chain2_args& g, bool own_io, const char*
         A.pc[k][p] = g.c[k].p[p] + g.c[k].off;
       }
   }
+  A.own_ks = keystream_per_party() ? 1u : 0u;
   *out = A;
   return SUFHIP_OK;
 }

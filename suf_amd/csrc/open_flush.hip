@@ -1,13 +1,16 @@
 // One flush of a two-party open collector on the GPU: the device path of
 // OpenCollector::flush (src/runtime/open_collector.cpp:357-791) for both
 // parties in one process.  The requests' shares are gathered into one
-// bucket per party (sufhip_stage_hatx, up to 64 requests a launch), each
-// party's bucket is packed to eff_bits -- the message it would send
-// (launch_pack_eff_bits_kernel) -- and party 0's view adds party 1's
-// unpacked message to its own shares (launch_unpack_add_mod_kernel, or the
-// sign-extending form): four launches however many requests.  The opened
-// values stay on the device, back to back in request order, for the PFSS
-// evaluation that consumes them (OpenCollector::view_device_u64).
+// bucket per party (sufhip_stage_hatx, up to 64 requests a launch), party
+// 1's bucket is packed to eff_bits -- the message it sends
+// (launch_pack_eff_bits_kernel) -- and party 0's view adds that unpacked
+// message to its own shares (launch_unpack_add_mod_kernel, or the
+// sign-extending form).  Party 0's message is not formed: with both parties
+// in one process the opened values are shared, and nothing would read it.
+// That is 2 * ceil(count / 64) gather launches, one pack and one unpack-add
+// (four launches for up to 64 requests).  The opened values stay on the
+// device, back to back in request order, for the PFSS evaluation that
+// consumes them (OpenCollector::view_device_u64).
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -31,7 +34,7 @@ extern "C" {
 
 size_t sufhip_open_flush2_work_bytes(size_t total, int eff_bits) {
   if (eff_bits < 1 || eff_bits > 64) return 0;
-  return 2 * total * 8 + 2 * (packed_words_of(total, eff_bits) + 1) * 8;
+  return 2 * total * 8 + (packed_words_of(total, eff_bits) + 1) * 8;
 }
 
 int sufhip_open_flush2(const sufhip_open_req* reqs, int count, int eff_bits, int ring_bits,
@@ -53,7 +56,7 @@ int sufhip_open_flush2(const sufhip_open_req* reqs, int count, int eff_bits, int
   SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_work) & 7) == 0,
                  "sufhip_open_flush2: workspace must be 8-byte aligned");
   uint64_t* bucket[2] = {static_cast<uint64_t*>(d_work), static_cast<uint64_t*>(d_work) + total};
-  uint64_t* msg[2] = {bucket[1] + total, bucket[1] + total + packed_words_of(total, eff_bits) + 1};
+  uint64_t* msg1 = bucket[1] + total;
   // Gather both parties' shares, 64 requests per launch and party.
   for (int p = 0; p < 2; ++p) {
     size_t pos = 0;
@@ -68,14 +71,13 @@ int sufhip_open_flush2(const sufhip_open_req* reqs, int count, int eff_bits, int
       if (int rc = sufhip_stage_hatx(segs, m, bucket[p], total, stream)) return rc;
     }
   }
-  // Each party's message; party 0 opens with party 1's.
-  for (int p = 0; p < 2; ++p)
-    if (int rc = sufhip_pack_eff_bits(bucket[p], eff_bits, msg[p], total, stream)) return rc;
+  // Party 1's message; party 0 opens with it.
+  if (int rc = sufhip_pack_eff_bits(bucket[1], eff_bits, msg1, total, stream)) return rc;
   const uint64_t mask = ring_bits >= 64 ? ~uint64_t(0) : (uint64_t(1) << ring_bits) - 1;
   return sign_extend
-             ? sufhip_unpack_add_to_signed(bucket[0], msg[1], eff_bits, d_opened, total, ring_bits,
+             ? sufhip_unpack_add_to_signed(bucket[0], msg1, eff_bits, d_opened, total, ring_bits,
                                            mask, stream)
-             : sufhip_unpack_add_mod(bucket[0], msg[1], eff_bits, d_opened, total, ring_bits, mask,
+             : sufhip_unpack_add_mod(bucket[0], msg1, eff_bits, d_opened, total, ring_bits, mask,
                                      stream);
 }
 

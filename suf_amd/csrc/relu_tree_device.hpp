@@ -35,6 +35,9 @@ struct TreeKeys {
   uint64_t mask[kRounds];
   int intervals[kRounds];
   int rounds;
+  // All ones: every round's keystreams and interval searches per party,
+  // even where the blobs compare equal (sufhip_set_keystream_per_party).
+  uint32_t own_ks;
 };
 
 template <int kRounds>
@@ -152,7 +155,7 @@ struct TreeStager {
 // segment (kernarg_tree_keys).  The caller syncs.
 template <int kRounds>
 __device__ __forceinline__ void tree_stage(const TreeKeys<kRounds>* K, TreeLds<kRounds>& L) {
-  if (threadIdx.x == 0) L.diff = 0;
+  if (threadIdx.x == 0) L.diff = K->own_ks;
   const int n = K->rounds * kTreeItems;
   for (int f0 = threadIdx.x; f0 < n; f0 += 2 * blockDim.x) {
     TreeStager<kRounds, 2> s;
@@ -176,7 +179,8 @@ __device__ __forceinline__ void tree_row_offsets(const TreeKeys<kRounds>& K,
 // that barrier, bit k of ~L.diff says that round k's two blobs carry the
 // same AES key, nonce, input mask and cut points (SUF's dealer derives one
 // key per gate, cuda/pfss_backend_gpu.cu:508-515), so that one keystream
-// block serves both parties of a slot.  tree_stage zeroes L.diff.
+// block serves both parties of a slot.  tree_stage starts L.diff at
+// TreeKeys::own_ks (zero unless every keystream is per party).
 template <int kRounds>
 __device__ __forceinline__ void tree_compare(const TreeKeys<kRounds>& K, TreeLds<kRounds>& L) {
   constexpr int kPer = 11 + kTreeIntervals + 1;  // round key words, cuts, header
@@ -395,6 +399,7 @@ inline int make_tree_keys(const sufhip_relu_round_key* keys, int rounds, int max
     K.mask[k] = rk.mask;
     K.intervals[k] = rk.intervals;
   }
+  K.own_ks = keystream_per_party() ? ~0u : 0u;
   *out = K;
   return SUFHIP_OK;
 }

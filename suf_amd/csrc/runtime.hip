@@ -2,6 +2,7 @@
 // memory, events; the AES-128-CTR and myl7 PRG kernels; seeded host inputs.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <random>
@@ -14,9 +15,12 @@ namespace sufhip {
 
 namespace {
 thread_local std::string t_last_error;
+std::atomic<bool> g_keystream_per_party{false};
 }
 
 void set_error(const std::string& msg) { t_last_error = msg; }
+
+bool keystream_per_party() { return g_keystream_per_party.load(); }
 void clear_error() { t_last_error.clear(); }
 
 int hip_status(hipError_t st, const char* what) {
@@ -88,6 +92,13 @@ using namespace sufhip;
 extern "C" {
 
 int sufhip_abi_version(void) { return SUFHIP_ABI_VERSION; }
+
+int sufhip_set_keystream_per_party(int per_party) {
+  g_keystream_per_party.store(per_party != 0);
+  return SUFHIP_OK;
+}
+
+int sufhip_keystream_per_party(void) { return g_keystream_per_party.load() ? 1 : 0; }
 
 const char* sufhip_last_error(void) { return t_last_error.c_str(); }
 

@@ -36,6 +36,10 @@ int hip_status(hipError_t st, const char* what);
 // Checks the launch that was just issued.
 int check_launch(const char* what);
 
+// sufhip_set_keystream_per_party's policy: true when every two-party LUT
+// kernel computes each party's keystream from its own blob.
+bool keystream_per_party();
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline unsigned int grid_for(size_t n, unsigned int block) {

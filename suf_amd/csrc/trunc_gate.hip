@@ -479,8 +479,8 @@ __global__ void __launch_bounds__(kWalkBlock) trunc_batch_walk_kernel(WalkArgs a
       walk8_expand<0, 2>(c, cw, root, v);
     else if (e == 3)
       walk8_expand<0, 3>(c, cw, root, v);
-    else
-      walk8_expand<0, kWalkLocal>(c, cw, root, v);
+    else  // e == 4: the host picks e <= kWalkLocal <= 4 (static_assert above)
+      walk8_expand<0, 4>(c, cw, root, v);
   } else if (d == f) {
     walk8_leaf(c, w, v);
   } else {

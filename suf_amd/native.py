@@ -40,6 +40,8 @@ _SIGS = {
     "sufhip_abi_version": (c_int, []),
     "sufhip_last_error": (ctypes.c_char_p, []),
     "sufhip_init": (c_int, [c_int]),
+    "sufhip_set_keystream_per_party": (c_int, [c_int]),
+    "sufhip_keystream_per_party": (c_int, []),
     "sufhip_device_count": (c_int, [c_vp]),
     "sufhip_stream_create": (c_int, [c_vp]),
     "sufhip_stream_destroy": (c_int, [c_vp]),

@@ -5,11 +5,27 @@ runs in libsuf_hip.so.  u64 ring values are carried in torch.int64 tensors
 (same bits).  Names follow the reference's backend operations
 (include/proto/myl7_fss_backend.hpp, include/proto/backend_gpu.hpp).
 """
+import contextlib
+
 import torch
 
 from . import native
 
 PRG_STATE_BYTES = 128
+
+
+@contextlib.contextmanager
+def keystream_per_party(on=True):
+    """Within the block, every two-party LUT launch computes each party's
+    keystream from its own blob (sufhip_set_keystream_per_party): the same
+    shares, the cost of two parties in separate processes.  Launches (and
+    graphs) issued inside keep that policy."""
+    prev = native.load().sufhip_keystream_per_party()
+    native.call("sufhip_set_keystream_per_party", 1 if on else 0)
+    try:
+        yield
+    finally:
+        native.call("sufhip_set_keystream_per_party", prev)
 
 
 def _stream():
