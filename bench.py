@@ -232,9 +232,9 @@ def softmax_bytes(n_packed, rows, pre=0, indexed_input=False, out_written=True, 
 # per-party keystreams: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE (KiB per
 # dispatch, mean over the run's launches of the kernel), scaled by the
 # counters' reading for a 256 MiB device copy (FETCH x2.0, WRITE x1.0); the
-# commands and raw values are in profiles/gate_pipelines__spline_n2p20__
-# matmul_128x768x3072__softmax_ln.md and profiles/secure_layer__gpt2_small_
-# seq128.md.  None where not measured.
+# commands and raw values are in profiles/per_party_keystreams__spline_n2p20__
+# softmax_ln__secure_layer.md (the matmul product's in profiles/gate_pipelines__
+# spline_n2p20__matmul_128x768x3072__softmax_ln.md).
 def _traffic(fetch_kib, write_kib):
     if fetch_kib is None or write_kib is None:
         return None

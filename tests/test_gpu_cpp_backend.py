@@ -1,8 +1,10 @@
 """Runs the C++ two-party test of HipPfssBackend (tests/cpp/test_hip_backend.cpp,
 built by `python -m suf_amd.build`) on the GPU: the proto-interface backend,
 a dealer instance plus one instance per party thread, reconstructing DCF,
-interval-LUT and packed-compare outputs against their closed forms; and the
-reference's own XOR-group keys evaluated byte-equal to its shares."""
+interval-LUT and packed-compare outputs against their closed forms and SUF's
+AddU64 truncation route (composite_gen_trunc_gate's queries, the host bool
+plan, launch_trunc_postproc_kernel on last_device_bools()) against x >> f;
+and the reference's own XOR-group keys evaluated byte-equal to its shares."""
 import json
 import os
 import subprocess
@@ -50,3 +52,16 @@ def test_cpp_backend_evaluates_reference_xor_keys():
     print(r.stderr)
     assert r.returncode == 0, r.stderr
     assert "golden xor keys" in r.stdout
+
+
+def test_cpp_trunc_route_timings():
+    """Times SUF's AddU64 truncation route through the backend (host bool
+    plan, then the postproc launcher), its device-kept form and the fused
+    truncation gate, both parties, GapARS f = 12 at 2^16 and 2^20 points;
+    the shares of these routes are checked by test_cpp_two_party_backend."""
+    assert os.path.exists(EXE), "C++ test driver not built: run python -m suf_amd.build"
+    r = subprocess.run([EXE, "time-trunc"], capture_output=True, text=True, timeout=110)
+    print(r.stdout)
+    print(r.stderr)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.count("trunc routes GapARS") == 2
