@@ -29,11 +29,19 @@ Online: the DCF bits of every query and cut at the public x^ (one launch per
 key and party), the whole selector / boolean network for both parties in one
 launch (sufhip_composite_bool2), and the arithmetic words through the
 interval LUT of the rotated pieces (sufhip_interval_lut_eval2).
+
+Offline key material travels as one composite tape per party
+(gates::write_composite_tape, composite_fss.hpp:2458-2641; suf_amd/tape.py):
+party_tape(p) writes it, and CompositeGate.from_tapes(compiled(), tapes)
+rebuilds the gate's device key material from the two tapes and the dealer's
+public compilation, as composite_eval_batch_from_tape pairs a tape with the
+CompiledSUFGate (composite_fss.hpp:2622-2641).
 """
 import numpy as np
 import torch
 
 from . import native, pfss
+from . import tape as tapefmt
 from .tasks import CoeffLut, Dealer, ptr, stream_ptr
 
 M64 = (1 << 64) - 1
@@ -216,10 +224,132 @@ class CompositeGate:
         t0 = np.stack([a0, b0, c0], axis=1)
         t1 = np.stack([a - a0, b - b0, c - c0], axis=1)
         self.tri = [torch.from_numpy(t.view(np.int64).ravel().copy()).to(device) for t in (t0, t1)]
-        self.pred = [torch.empty(max(1, len(queries)) * n, dtype=torch.uint8, device=device)
+        # The mask's shares (the tapes' r_in_share), drawn last so that the
+        # material above does not depend on them.
+        s0 = dealer.word()
+        self.r_in_share = [s0, (self.r_in - s0) & M64]
+        self._buffers(device)
+
+    def _buffers(self, device):
+        n = self.n
+        self.pred = [torch.empty(max(1, len(self.queries)) * n, dtype=torch.uint8, device=device)
                      for _ in range(2)]
         self.cutb = [torch.empty(max(1, len(self.cuts)) * n, dtype=torch.uint8, device=device)
                      for _ in range(2)]
+
+    def compiled(self):
+        """The dealer's public compilation (CompiledSUFGate's role): what the
+        evaluation needs besides the parties' key material."""
+        lut = None
+        if self.lut is not None:
+            lut = {"intervals": int(self.lut.intervals), "words": int(self.lut.words),
+                   "key_bytes": int(self.lut.key_bytes), "mask": int(self.lut.mask)}
+        return {"n": self.n, "r": self.r, "ell": self.ell, "r_in": int(self.r_in),
+                "queries": [(int(b), int(t)) for b, t in self.queries],
+                "cuts": [int(c) for c in self.cuts], "segs": list(self.segs),
+                "wraps": len(self.wrap_bits), "prog": list(self.prog),
+                "prog_off": list(self.prog_off), "and_count": self.and_count, "T": self.T,
+                "lut": lut, "spec": self.spec}
+
+    def party_key(self, p):
+        """Party p's key material as a composite tape key (suf_amd/tape.py):
+        the mask and wrap shares, one DCF key per query and per cut (XOR
+        bytes, 1-byte payload, MSB-first), the interval-LUT blob of the
+        arithmetic words (additive), T x n Beaver triples {a, b, c} (triple t
+        of element i at t n + i) and and_count x n bit triples."""
+        n = self.n
+        k = tapefmt.empty_key()
+        k["r_in_share"] = self.r_in_share[p]
+        k["wrap_share"] = np.asarray(self.wrap_share[p], dtype=np.uint64)
+        k["pred_keys"] = [bytes(kp[1 + p].cpu().numpy().tobytes()) for kp in self.query_keys]
+        k["cut_pred_keys"] = [bytes(kp[1 + p].cpu().numpy().tobytes()) for kp in self.cut_keys]
+        if self.lut is not None:
+            k["coeff_keys"] = [bytes(self.lut.blobs[p].tobytes())]
+        tri = self.tri[p].cpu().numpy().view(np.uint64).reshape(self.T, 3, n)
+        k["triples"] = tri.transpose(0, 2, 1).reshape(self.T * n, 3)
+        if self.and_count:
+            bt = self.bit_tri[p].cpu().numpy()
+            k["bit_triples"] = np.stack([bt & 1, (bt >> 1) & 1, (bt >> 2) & 1], axis=1)
+        return k
+
+    def party_tape(self, p):
+        """Party p's composite tape (bytes)."""
+        return tapefmt.write_composite_tape(self.party_key(p))
+
+    @classmethod
+    def from_tapes(cls, compiled, tapes, prg_state, device="cuda"):
+        """A gate whose key material comes from the two parties' composite
+        tapes (bytes), evaluated under the dealer's compilation `compiled`
+        (CompositeGate.compiled()).  Raises ValueError if a tape does not fit
+        the compilation."""
+        c = compiled
+        g = cls.__new__(cls)
+        g.n, g.r, g.ell, g.r_in = c["n"], c["r"], c["ell"], c["r_in"]
+        g.prg_state = bytes(prg_state)
+        g.spec = c.get("spec")
+        g.queries = [tuple(q) for q in c["queries"]]
+        g.cuts, g.segs = list(c["cuts"]), list(c["segs"])
+        g.prog, g.prog_off = list(c["prog"]), list(c["prog_off"])
+        g.and_count, g.T = c["and_count"], c["T"]
+        n = g.n
+        keys = [tapefmt.read_composite_tape(t) for t in tapes]
+        for p, k in enumerate(keys):
+            def bad(what):
+                return ValueError("CompositeGate.from_tapes: party %d tape: %s" % (p, what))
+            if len(k["pred_keys"]) != len(g.queries) or len(k["cut_pred_keys"]) != len(g.cuts):
+                raise bad("key counts differ from the compilation")
+            if k["pred_meta"][1:] != (tapefmt.XOR_BYTES, 1) or \
+                    k["cut_pred_meta"][1:] != (tapefmt.XOR_BYTES, 1):
+                raise bad("predicate keys must be XOR bytes with a 1-byte output")
+            if len(k["wrap_share"]) != c["wraps"]:
+                raise bad("wrap share count")
+            if k["triples"].shape[0] != g.T * n or k["bit_triples"].shape[0] != g.and_count * n:
+                raise bad("triple counts")
+            if len(k["coeff_keys"]) != (1 if c["lut"] else 0):
+                raise bad("coefficient key count")
+            for blob, (bits, _) in zip(k["pred_keys"], g.queries):
+                if len(blob) != pfss.dcf_key_bytes(bits, 1) or blob[0] != bits:
+                    raise bad("a predicate key has the wrong size or input width")
+            for blob in k["cut_pred_keys"]:
+                if len(blob) != pfss.dcf_key_bytes(64, 1) or blob[0] != 64:
+                    raise bad("a cut key has the wrong size or input width")
+        g.r_in_share = [k["r_in_share"] for k in keys]
+        g.wrap_bits = [None] * c["wraps"]  # clear bits stay with the dealer
+        g.wrap_share = [np.asarray(k["wrap_share"], dtype=np.uint64) for k in keys]
+
+        def dev_bytes(blob):
+            return torch.from_numpy(np.frombuffer(blob, dtype=np.uint8).copy()).to(device)
+
+        g.query_keys = [(bits, dev_bytes(keys[0]["pred_keys"][q]), dev_bytes(keys[1]["pred_keys"][q]))
+                        for q, (bits, _) in enumerate(g.queries)]
+        g.cut_keys = [(64, dev_bytes(keys[0]["cut_pred_keys"][q]),
+                       dev_bytes(keys[1]["cut_pred_keys"][q])) for q in range(len(g.cuts))]
+        g.tri = []
+        for k in keys:
+            t = k["triples"].reshape(g.T, n, 3).transpose(0, 2, 1)
+            g.tri.append(torch.from_numpy(np.ascontiguousarray(t).view(np.int64).ravel().copy())
+                         .to(device))
+        if g.and_count:
+            g.bit_tri = []
+            for k in keys:
+                bt = k["bit_triples"].astype(np.uint8)
+                packed = (bt[:, 0] & 1) | ((bt[:, 1] & 1) << 1) | ((bt[:, 2] & 1) << 2)
+                g.bit_tri.append(torch.from_numpy(packed.astype(np.uint8)).to(device))
+        else:
+            g.bit_tri = [None, None]
+        g.lut = None
+        if c["lut"]:
+            lut = CoeffLut.__new__(CoeffLut)
+            lut.words, lut.intervals = c["lut"]["words"], c["lut"]["intervals"]
+            lut.key_bytes, lut.mask = c["lut"]["key_bytes"], c["lut"]["mask"]
+            lut.blobs = [np.frombuffer(k["coeff_keys"][0], dtype=np.uint8).copy() for k in keys]
+            if any(b.size != lut.key_bytes for b in lut.blobs):
+                raise ValueError("CompositeGate.from_tapes: coefficient key size")
+            lut.keys = [torch.from_numpy(b.view(np.int64).copy()).to(device).view(torch.uint8)
+                        for b in lut.blobs]
+            g.lut = lut
+        g._buffers(device)
+        return g
 
     def _dcf_key(self, dealer, bits, theta, device):
         seeds = torch.from_numpy(dealer.words(4).view(np.uint8).copy()).to(device).reshape(1, 32)

@@ -272,7 +272,37 @@ static void test_gpu(const std::string& dir) {
   std::remove(path.c_str());
 }
 
+static void write_file(const std::string& path, const std::vector<uint8_t>& v) {
+  std::FILE* f = std::fopen(path.c_str(), "wb");
+  if (!f || std::fwrite(v.data(), 1, v.size(), f) != v.size())
+    throw std::runtime_error("cannot write " + path);
+  std::fclose(f);
+}
+
 int main(int argc, char** argv) {
+  // composite-rw <in> <out>: the C++ reader and writer over a composite tape
+  // written elsewhere (the Python host side); composite-write <out>: a tape
+  // of the random key above, for the Python reader.
+  if (argc == 4 && std::string(argv[1]) == "composite-rw") {
+    try {
+      const std::vector<uint8_t> t = read_file(argv[2]);
+      write_file(argv[3], write_composite_tape(read_composite_tape(t.data(), t.size())));
+    } catch (const std::exception& e) {
+      std::fprintf(stderr, "exception: %s\n", e.what());
+      return 2;
+    }
+    return 0;
+  }
+  if (argc == 3 && std::string(argv[1]) == "composite-write") {
+    std::mt19937_64 g(11);
+    try {
+      write_file(argv[2], write_composite_tape(random_key(g)));
+    } catch (const std::exception& e) {
+      std::fprintf(stderr, "exception: %s\n", e.what());
+      return 2;
+    }
+    return 0;
+  }
   if (argc < 3) {
     std::fprintf(stderr, "usage: test_tape cpu <golden tape> | gpu <scratch dir>\n");
     return 2;

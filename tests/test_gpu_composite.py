@@ -140,3 +140,38 @@ def test_composite_refuses_malformed_programs():
     a.prog[0] = native.BOOL_VAR | (a.queries << 4)  # query index out of range
     with pytest.raises(native.SufHipError, match="malformed"):
         native.call("sufhip_composite_bool2", native.ctypes.byref(a), 0)
+
+
+@pytest.mark.parametrize("spec", [cs.MIXED, cs.DRELU], ids=["mixed", "drelu"])
+def test_composite_gate_from_tapes_gives_the_dealt_shares(spec, tmp_path):
+    """Each party's key material written to a composite tape file
+    (write_composite_tape's format), read back, and loaded into a gate built
+    from the tapes and the dealer's compilation alone: the boolean and
+    arithmetic shares equal those of the dealt gate, byte for byte."""
+    n = 1 << 14
+    gate = _run(spec, n, 11, share_check=False)
+    x = _inputs(n, 11)
+    xd = dev((x + np.uint64(gate.r_in)).astype(np.uint64))
+    paths = []
+    for p in (0, 1):
+        path = tmp_path / ("party%d.tape" % p)
+        path.write_bytes(gate.party_tape(p))
+        paths.append(path)
+    tapes = [pth.read_bytes() for pth in paths]
+    say("composite gate from tapes n=%d (%d + %d tape bytes)" % (n, len(tapes[0]), len(tapes[1])))
+    g2 = composite.CompositeGate.from_tapes(gate.compiled(), tapes, STATE)
+    assert (g2.r_in_share[0] + g2.r_in_share[1]) & M64 == gate.r_in
+    outs = []
+    for g in (gate, g2):
+        ob = tuple(torch.empty(n * g.ell, dtype=torch.int64, device="cuda") for _ in range(2))
+        oa = tuple(torch.empty(n * g.r, dtype=torch.int64, device="cuda") for _ in range(2))
+        g.eval2(xd, ob, oa)
+        torch.cuda.synchronize()
+        outs.append([u64(t) for t in ob + oa])
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+    # A tape whose key counts do not fit the compilation is refused.
+    other = composite.CompositeGate(cs.DRELU if spec is cs.MIXED else cs.MIXED, n, STATE, seed=12)
+    with pytest.raises(ValueError, match="from_tapes"):
+        composite.CompositeGate.from_tapes(gate.compiled(), [other.party_tape(0),
+                                                             other.party_tape(1)], STATE)
