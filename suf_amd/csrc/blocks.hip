@@ -400,7 +400,7 @@ __global__ void __launch_bounds__(kSmThreads) softmax2_kernel(SmArgs a) {
     // inv = Recip(row sum) on lane 0.
     uint64_t inv0 = 0, inv1 = 0;
     if (lane == 0 && len > 0) {
-      const Two iv = chain_eval<SUFHIP_CHAIN_RECIP, SmAes>(
+      const Two iv = chain_eval<SUFHIP_CHAIN_RECIP, SmAes, ChainPreN<3>, true>(
           a.recip, st.recip, Kr, aes, size_t(r), Two{{es0, es1}}, st.rpre[wave], st.thr);
       inv0 = iv.v[0];
       inv1 = iv.v[1];

@@ -378,8 +378,11 @@ __device__ __forceinline__ void chain_stage_trunc_hdrs(const ChainArgs& A, Trunc
 // LUT's AES blocks (both parties, W / 2 blocks each, per element) are
 // encrypted in lockstep and the truncations' table reads of a step are in
 // flight together: a lane pays one latency per step, not one per element and
-// party.
-template <int kKind, class Aes, int M, class Src>
+// party.  kLockBoth: when party 1 needs its own keystream and each party has
+// at most two blocks, both parties' blocks run as one lockstep group (for
+// the latency-bound chains of the block kernels; the throughput-bound chain
+// kernel keeps the smaller register footprint of one party at a time).
+template <int kKind, class Aes, int M, class Src, bool kLockBoth = false>
 __device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds& L,
                                              const ChainKeyInfo& K, const Aes& aes,
                                              const size_t (&i)[M], const Two (&x)[M],
@@ -423,14 +426,36 @@ __device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds&
   }
   // Party 0's blocks, at most four in lockstep (more keep too many table
   // reads in flight for the register file); party 1's only where its
-  // keystream differs (never for blobs from one dealer key).
+  // keystream differs (never for blobs from one dealer key, always under
+  // the per-party policy).  A chain of at most two blocks per party runs
+  // both parties' blocks in one lockstep group when party 1 needs its own:
+  // one AES latency instead of two.
   constexpr int kLock = NS < 4 ? NS : 4;
   bool own1 = !K.same_ks;
 #pragma unroll
   for (int m = 0; m < M; ++m) own1 = own1 || iv[m][0] != iv[m][1];
+  bool both = false;
+  if constexpr (kLockBoth && 2 * NS <= 4) {
+    if (own1) {
+      uint32_t sub[2 * NS][4];
+      const uint4* subk[2 * NS];
+#pragma unroll
+      for (int u = 0; u < 2 * NS; ++u) {
+        subk[u] = L.rk[u / NS];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sub[u][q] = st[u / NS][u % NS][q];
+      }
+      aes.template encrypt_n<2 * NS>(sub, subk);
+#pragma unroll
+      for (int u = 0; u < 2 * NS; ++u)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) st[u / NS][u % NS][q] = sub[u][q];
+      both = true;
+    }
+  }
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    if (p == 1 && !own1) continue;
+    if (both || (p == 1 && !own1)) continue;
 #pragma unroll
     for (int n0 = 0; n0 < NS; n0 += kLock) {
       uint32_t sub[kLock][4];
@@ -514,7 +539,7 @@ __device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds&
 }
 
 // The whole chain for one element (chain_eval_m with M = 1).
-template <int kKind, class Aes, class Src>
+template <int kKind, class Aes, class Src, bool kLockBoth = false>
 __device__ __forceinline__ Two chain_eval(const ChainArgs& A, const ChainLds& L,
                                           const ChainKeyInfo& K, const Aes& aes,
                                           size_t i, Two x, const Src& P,
@@ -523,7 +548,7 @@ __device__ __forceinline__ Two chain_eval(const ChainArgs& A, const ChainLds& L,
   const Two xx[1] = {x};
   const Src pp[1] = {P};
   Two out[1];
-  chain_eval_m<kKind, Aes, 1>(A, L, K, aes, ii, xx, pp, out, th);
+  chain_eval_m<kKind, Aes, 1, Src, kLockBoth>(A, L, K, aes, ii, xx, pp, out, th);
   return out[0];
 }
 

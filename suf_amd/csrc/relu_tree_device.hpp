@@ -258,11 +258,29 @@ __device__ __forceinline__ void tree_chunk(const TreeKeys<kRounds>& K, const Tre
     const uint32_t* rks[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) rks[u] = rk0;
-    aes.template encrypt_quad_n<U>(blk[0], rks);
     if (one_ks) {
+      aes.template encrypt_quad_n<U>(blk[0], rks);
 #pragma unroll
       for (int u = 0; u < U; ++u) blk[1][u] = blk[0][u];
+    } else if constexpr (U <= 2) {
+      // Both parties' blocks in one lockstep group: one quad-AES latency.
+      uint32_t b2[2 * U];
+      const uint32_t* k2[2 * U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        b2[u] = blk[0][u];
+        b2[U + u] = blk[1][u];
+        k2[u] = rk0;
+        k2[U + u] = rk1;
+      }
+      aes.template encrypt_quad_n<2 * U>(b2, k2);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        blk[0][u] = b2[u];
+        blk[1][u] = b2[U + u];
+      }
     } else {
+      aes.template encrypt_quad_n<U>(blk[0], rks);
 #pragma unroll
       for (int u = 0; u < U; ++u) rks[u] = rk1;
       aes.template encrypt_quad_n<U>(blk[1], rks);
