@@ -51,6 +51,7 @@ SCRATCH_ALLOWED = {
     # (v_writelane / v_readlane).  The frame size is reported, but the kernel
     # has no scratch memory instruction (tests/test_build_scratch.py).
     "softmax2_kernel": "SGPR spill slots in VGPR lanes, no scratch memory access",
+    "softmax2_team_kernel": "SGPR spill slots in VGPR lanes, no scratch memory access",
 }
 RESOURCE_REPORT = os.path.join(LIBDIR, "kernel_resources.txt")
 

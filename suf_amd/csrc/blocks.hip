@@ -220,15 +220,16 @@ __device__ __forceinline__ uint64_t bcast_lane0(uint64_t v) {
 // item index) before its first LDS store, so staging costs about one memory
 // round trip.  load() and store() split the pass so that the first rows'
 // loads go in between; the caller syncs after store().
-struct SmStager {
-  static constexpr int kChainPer = 3;
-  typename SmAes::template Filler<kSmThreads> tf;
+template <int kThreads>
+struct SmStagerT {
+  static constexpr int kChainPer = (3 * kSmThreads + kThreads - 1) / kThreads;
+  typename SmAes::template Filler<kThreads> tf;
   TreeStager<kSmRounds, 2> ts;
   TruncHdrStager<3> hn, hr;
   uint4 cv[kChainPer];
   int c0, nn, nc;
   __device__ __forceinline__ void load(const SmArgs& a) {
-    static_assert(kSmRounds * kTreeItems <= 2 * kSmThreads, "SmStager: tree items in one pass");
+    static_assert(kSmRounds * kTreeItems <= 2 * kThreads, "SmStager: tree items in one pass");
     tf.load(kTDev.v);
     ts.load(kernarg_tree_keys<kSmRounds>(offsetof(SmArgs, keys)), int(threadIdx.x));
     hn.load(a.nexp, 0);
@@ -236,12 +237,12 @@ struct SmStager {
     // Chain items continue the tree's flat item space.
     nn = chain_items(a.nexp, 4);
     nc = nn + chain_items(a.recip, 2);
-    const int shift = (a.keys.rounds * kTreeItems) % kSmThreads;
-    c0 = (int(threadIdx.x) + kSmThreads - shift) % kSmThreads;
+    const int shift = (a.keys.rounds * kTreeItems) % kThreads;
+    c0 = (int(threadIdx.x) + kThreads - shift) % kThreads;
 #pragma unroll
     for (int u = 0; u < kChainPer; ++u) {
       // Unconditional loads on a clamped item (see TreeStager::load).
-      const int c = c0 + u * kSmThreads < nc ? c0 + u * kSmThreads : 0;
+      const int c = c0 + u * kThreads < nc ? c0 + u * kThreads : 0;
       bool rn, rr;
       const uint64_t* an = chain_item_addr(a.nexp, 4, c < nn ? c : 0, &rn);
       const uint64_t* ar = chain_item_addr(a.recip, 2, c < nn ? 0 : c - nn, &rr);
@@ -251,7 +252,7 @@ struct SmStager {
   __device__ __forceinline__ void store(const SmArgs& a, SmStatic& st) const {
 #pragma unroll
     for (int u = 0; u < kChainPer; ++u) {
-      const int c = c0 + u * kSmThreads;
+      const int c = c0 + u * kThreads;
       if (c < nn)
         chain_item_store(a.nexp, 4, st.nexp, c, cv[u]);
       else if (c < nc)
@@ -259,7 +260,7 @@ struct SmStager {
     }
     // Chains with more items than one pass covers (wide LUTs): the rest
     // item by item.
-    for (int c = c0 + kChainPer * kSmThreads; c < nc; c += kSmThreads) {
+    for (int c = c0 + kChainPer * kThreads; c < nc; c += kThreads) {
       if (c < nn)
         chain_item_store(a.nexp, 4, st.nexp, c, chain_item_load(a.nexp, 4, c));
       else
@@ -276,6 +277,7 @@ struct SmStager {
     }
   }
 };
+using SmStager = SmStagerT<kSmThreads>;
 
 template <int kPer>
 __global__ void __launch_bounds__(kSmThreads) softmax2_kernel(SmArgs a) {
@@ -462,6 +464,221 @@ __global__ void __launch_bounds__(kSmThreads) softmax2_kernel(SmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Rows of up to 128 elements on a team of two waves: six rows per
+// workgroup of 768 lanes (twelve waves, three per SIMD; the LDS is the
+// six-row kernel's).  Wave t of a row's team holds element lane + 64 t.
+// The max tree's first two levels (up to 64 and 32 pairs) are split between
+// the team's waves, with a workgroup barrier after each; the shorter levels
+// run on the team's first wave.  Each lane then runs one element's nExp
+// chain with both parties' keystream blocks in one lockstep group, the
+// row sum adds the two waves' partial sums through LDS, the reciprocal runs
+// on the first wave's lane 0, and each wave normalises its elements.  The
+// per-wave work of the tree's wide levels, of the nExp chain and of the
+// normalisation halves; every output equals the one-wave-per-row kernel's.
+constexpr int kSmTeam = 2;
+constexpr int kSmTeamThreads = 64 * kSmWaves * kSmTeam;
+constexpr int kSmTeamMaxRow = 128;
+
+// Levels 0 and 1 split over the team (pairs [32 t, 32 t + 32) and
+// [16 t, 16 t + 16)), a workgroup barrier after each; later levels on wave
+// t = 0 only (its wave-local ordering as in tree_row).  Every thread of the
+// workgroup runs the same number of barriers.  Returns the level count (the
+// same in both waves).
+template <class Aes>
+__device__ __forceinline__ int tree_row_team(const TreeKeys<kSmRounds>& K,
+                                             const TreeLds<kSmRounds>& L, const Aes& aes,
+                                             uint64_t* even, uint64_t* odd, int mr, int len,
+                                             const uint32_t* j0s, uint32_t shared, int tw) {
+  const int lane = threadIdx.x & 63, half = (mr + 1) / 2;
+  int level = 0;
+  for (int k = 0; k < K.rounds; ++k) {
+    const bool split = k < 2;
+    if (len > 1) {
+      const uint64_t* src = (level & 1) ? odd : even;
+      const int sw = (level & 1) ? half : mr;
+      uint64_t* dst = (level & 1) ? even : odd;
+      const int dw = (level & 1) ? mr : half;
+      const int pairs = len >> 1;
+      const uint32_t j0 = j0s[k];
+      const bool one_ks = (shared >> k) & 1u;
+      if (split) {
+        const int per = k == 0 ? 32 : 16;
+        const int t0 = per * tw;
+        const int nb = pairs - t0 < per ? pairs - t0 : per;
+        if (nb > 16)
+          tree_chunk<2>(K, L, aes, k, src, sw, dst, dw, j0, t0, nb, one_ks);
+        else if (nb > 0)
+          tree_chunk<1>(K, L, aes, k, src, sw, dst, dw, j0, t0, nb, one_ks);
+      } else if (tw == 0) {
+        for (int t0 = 0; t0 < pairs; t0 += 64) {
+          const int nb = pairs - t0 < 64 ? pairs - t0 : 64;
+          if (nb > 48)
+            tree_chunk<4>(K, L, aes, k, src, sw, dst, dw, j0, t0, nb, one_ks);
+          else if (nb > 32)
+            tree_chunk<3>(K, L, aes, k, src, sw, dst, dw, j0, t0, nb, one_ks);
+          else if (nb > 16)
+            tree_chunk<2>(K, L, aes, k, src, sw, dst, dw, j0, t0, nb, one_ks);
+          else
+            tree_chunk<1>(K, L, aes, k, src, sw, dst, dw, j0, t0, nb, one_ks);
+        }
+      }
+      if ((len & 1) && lane == 0 && tw == 0) {
+        dst[pairs] = src[2 * pairs];
+        dst[dw + pairs] = src[sw + 2 * pairs];
+      }
+      len = (len + 1) >> 1;
+      ++level;
+    }
+    if (split) {
+      __syncthreads();
+    } else if (tw == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+  return level;
+}
+
+__global__ void __launch_bounds__(kSmTeamThreads) softmax2_team_kernel(SmArgs a) {
+  __shared__ __align__(16) SmStatic st;
+  __shared__ uint64_t part[kSmWaves][kSmTeam][2];  // the team's partial row sums
+  __shared__ uint64_t invs[kSmWaves][2];           // the row's reciprocal shares
+  extern __shared__ uint64_t rowbuf[];
+  const int mr = a.max_row;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int slot = wave >> 1, tw = wave & 1;  // row slot in the group, wave in the team
+  const int j = lane + 64 * tw;               // this lane's element of the row
+  uint64_t* even = rowbuf + size_t(slot) * tree_row_words(mr);
+  uint64_t* odd = even + 2 * size_t(mr);
+  int b = 0, len = 0;
+  uint64_t na0 = 0, na1 = 0, nc0 = 0, nc1 = 0, s0 = 0, s1 = 0;
+  // The row group's loads, as in softmax2_kernel (one element per lane).
+  auto load_rows = [&](int g) {
+    const int r = g * a.waves + slot;
+    b = 0;
+    len = 0;
+    if (r < a.rows) {
+      b = a.offs[r];
+      len = a.offs[r + 1] - b;
+      if (len < 1 || len > mr) len = 0;  // refused on the host
+    }
+    if (tw == 0) {
+      if (len > 0 && lane < 18)
+        st.rpre[slot].word(lane) = chain_triple_word(a.recip, lane, size_t(r));
+      tree_row_offsets(a.keys, a.round_off, a.rows, r, len, st.j0[slot]);
+    }
+    const size_t i = size_t(b) + size_t(j < len ? j : 0);
+    na0 = j < len ? a.norm.a[0][i] : 0;
+    na1 = j < len ? a.norm.a[1][i] : 0;
+    nc0 = j < len ? a.norm.c[0][i] : 0;
+    nc1 = j < len ? a.norm.c[1][i] : 0;
+    s0 = s1 = 0;
+    if (j < len) {
+      uint64_t v0 = operand_at(a.x, 0, i), v1 = operand_at(a.x, 1, i);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        if (q >= a.pre) break;
+        const uint64_t o = v0 + v1 + a.pre_mask[q];
+        v0 = trunc_table_eval(a.pre_tr[q].key[0], a.pre_tr[q].table[0], a.pre_tr[q].f, o);
+        v1 = trunc_table_eval(a.pre_tr[q].key[1], a.pre_tr[q].table[1], a.pre_tr[q].f, o);
+      }
+      s0 = v0;
+      s1 = v1;
+      even[j] = v0;
+      even[mr + j] = v1;
+    }
+  };
+  {
+    SmStagerT<kSmTeamThreads> stager;
+    stager.load(a);
+    load_rows(blockIdx.x);
+    stager.store(a, st);
+  }
+  __syncthreads();
+  tree_compare(a.keys, st.t);
+  chain_compare(a.nexp, st.nexp);
+  chain_compare(a.recip, st.recip);
+  __syncthreads();
+  const SmAes aes = SmAes::make(st.tab);
+  const ChainKeyInfo Kn = chain_key_info(a.nexp, st.nexp);
+  const ChainKeyInfo Kr = chain_key_info(a.recip, st.recip);
+  const uint32_t shared = ~st.t.diff;
+  for (int g = blockIdx.x; g * a.waves < a.rows; g += gridDim.x) {
+    if (g != int(blockIdx.x)) {
+      load_rows(g);
+      __syncthreads();
+    }
+    const int r = g * a.waves + slot;
+    const int level = tree_row_team<SmAes>(a.keys, st.t, aes, even, odd, mr, len, st.j0[slot],
+                                           shared, tw);
+    __syncthreads();  // the first wave's later levels, for the second wave
+    const uint64_t* fin = (level & 1) ? odd : even;
+    const int fw = (level & 1) ? (mr + 1) / 2 : mr;
+    const uint64_t m0 = len > 0 ? fin[0] : 0, m1 = len > 0 ? fin[fw] : 0;
+    // e = nExp(max - s) for this lane's element, both parties' keystream
+    // blocks in one lockstep group (elements past the row end compute on a
+    // clamped index and are dropped).
+    const bool ok = j < len;
+    const size_t ii = size_t(b) + size_t(ok ? j : 0);
+    const Two ev = chain_eval<SUFHIP_CHAIN_CUBIC, SmAes, plain_loader<SUFHIP_CHAIN_CUBIC>, true>(
+        a.nexp, st.nexp, Kn, aes, ii, Two{{m0 - s0, m1 - s1}},
+        plain_loader<SUFHIP_CHAIN_CUBIC>{&a.nexp, ii}, st.thn);
+    const uint64_t e0 = ok ? ev.v[0] : 0, e1 = ok ? ev.v[1] : 0;
+    const uint64_t ps0 = wave_sum_u64(e0), ps1 = wave_sum_u64(e1);
+    if (lane == 0) {
+      part[slot][tw][0] = ps0;
+      part[slot][tw][1] = ps1;
+    }
+    __syncthreads();
+    // inv = Recip(row sum) on the first wave's lane 0.
+    if (tw == 0 && lane == 0 && len > 0) {
+      const Two es{{part[slot][0][0] + part[slot][1][0], part[slot][0][1] + part[slot][1][1]}};
+      const Two iv = chain_eval<SUFHIP_CHAIN_RECIP, SmAes, ChainPreN<3>, true>(
+          a.recip, st.recip, Kr, aes, size_t(r), es, st.rpre[slot], st.thr);
+      invs[slot][0] = iv.v[0];
+      invs[slot][1] = iv.v[1];
+    }
+    __syncthreads();
+    // prob = tr_norm(e * inv[row]) (row-broadcast Beaver), and the next
+    // product's open over the dense row.
+    if (len > 0) {
+      const uint64_t inv0 = invs[slot][0], inv1 = invs[slot][1];
+      const uint64_t nb0 = a.norm.b[0][r], nb1 = a.norm.b[1][r];
+      const uint64_t ee = (inv0 - nb0) + (inv1 - nb1);
+      const size_t drow = size_t(r) * size_t(a.dense_cols);
+      if (ok) {
+        const size_t i = size_t(b) + size_t(j);
+        const uint64_t dd = (e0 - na0) + (e1 - na1);
+        const uint64_t z0 = nc0 + dd * nb0 + ee * na0 + dd * ee;
+        const uint64_t z1 = nc1 + dd * nb1 + ee * na1;
+        const uint64_t o = z0 + z1 + a.norm_mask;
+        const uint64_t p0 = trunc_table_eval(a.tr_norm.key[0], a.tr_norm.table[0], a.tr_norm.f, o);
+        const uint64_t p1 = trunc_table_eval(a.tr_norm.key[1], a.tr_norm.table[1], a.tr_norm.f, o);
+        if (a.out[0]) {
+          a.out[0][i] = p0;
+          a.out[1][i] = p1;
+        }
+        if (a.dense) {
+          const size_t di = drow + size_t(j);
+          const uint64_t dv = (p0 - a.dense_a[0][di]) + (p1 - a.dense_a[1][di]);
+          a.dense[di] = dv;
+          if (a.dkb.planes) put_kb_digits(a.dkb, di, dv);
+        }
+      }
+      if (a.dense)
+        for (int jj = len + j; jj < a.dense_cols; jj += 64 * kSmTeam) {
+          const size_t di = drow + size_t(jj);
+          const uint64_t dv = (uint64_t(0) - a.dense_a[0][di]) + (uint64_t(0) - a.dense_a[1][di]);
+          a.dense[di] = dv;
+          if (a.dkb.planes) put_kb_digits(a.dkb, di, dv);
+        }
+    }
+    __syncthreads();  // the row buffers are rewritten by the next group
+  }
+}
+
 // The dynamic LDS of a softmax launch goes past 64 KB; allowed once per
 // kernel.
 template <int kPer>
@@ -470,6 +687,16 @@ bool sm_lds_allowed() {
       hipFuncSetAttribute(reinterpret_cast<const void*>(&softmax2_kernel<kPer>),
                           hipFuncAttributeMaxDynamicSharedMemorySize,
                           int(kSmLdsCap - sizeof(SmStatic))) == hipSuccess;
+  return ok;
+}
+
+constexpr size_t kSmTeamStatic = sizeof(SmStatic) + sizeof(uint64_t) * kSmWaves * (2 * kSmTeam + 2);
+
+bool sm_team_lds_allowed() {
+  static const bool ok =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&softmax2_team_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          int(kSmLdsCap - kSmTeamStatic)) == hipSuccess;
   return ok;
 }
 
@@ -620,11 +847,17 @@ int sufhip_softmax2(const sufhip_softmax2_args* args, void* stream) {
   const int groups = (g.rows + waves - 1) / waves;
   const int grid = groups < cus * per_cu ? groups : cus * per_cu;
   const dim3 block(kSmThreads);
+  hipStream_t s = as_stream(stream);
+  if (g.max_row <= kSmTeamMaxRow) {
+    SUFHIP_REQUIRE(kSmTeamStatic + dyn <= kSmLdsCap && sm_team_lds_allowed(),
+                   "sufhip_softmax2: the kernel's LDS size was refused");
+    hipLaunchKernelGGL(softmax2_team_kernel, dim3(grid), dim3(kSmTeamThreads), dyn, s, A);
+    return check_launch("softmax2_team_kernel");
+  }
   const bool lds_ok = g.max_row <= 128   ? sm_lds_allowed<2>()
                       : g.max_row <= 256 ? sm_lds_allowed<4>()
                                          : sm_lds_allowed<8>();
   SUFHIP_REQUIRE(lds_ok, "sufhip_softmax2: the kernel's LDS size was refused");
-  hipStream_t s = as_stream(stream);
   if (g.max_row <= 128)
     hipLaunchKernelGGL(softmax2_kernel<2>, dim3(grid), block, dyn, s, A);
   else if (g.max_row <= 256)
