@@ -783,6 +783,46 @@ def cpu_baseline(keys0, keys1, xhat, gpu_bits0, gpu_bits1, seconds):
     }
 
 
+def cpu_baseline_reference(keys0, keys1, xhat, gpu_bits0, gpu_bits1, seconds):
+    """The reference's own CPU backend on the same keys: Myl7FssBackend::
+    eval_dcf_many_u64 (include/proto/myl7_fss_backend.hpp:73-100, a serial
+    loop over keys; dcf.c and aes128_mmo.c with OpenSSL EVP AES) compiled from
+    the reference sources by oracle/build_ref.sh into oracle/_ref.  One
+    thread, as the reference's batch loop runs; keys cycled for the time
+    budget; shares compared with the GPU's.  None where that build is absent."""
+    import numpy as np
+
+    ol, _, _ = _oracle()
+    if not ol.ref_available(ol.GROUP_XOR):
+        return None
+    ref = ol.ref_lib(ol.GROUP_XOR)
+    state = ol.mt64_bytes(3, 128)
+    ref.ref_prg_init(ol.ptr(state), ol.PRG_STATE_BYTES)
+    n, kb = keys0.shape
+    xs = np.ascontiguousarray(xhat[:n], dtype=np.uint64)
+    out = np.zeros(n, dtype=np.uint8)
+    done, mism = 0, 0
+    t0 = time.perf_counter()
+    while True:
+        for keys, gb in ((keys0, gpu_bits0), (keys1, gpu_bits1)):
+            flat = np.ascontiguousarray(keys)
+            rc = ref.ref_adapter_eval_many(64, kb, ol.ptr(flat), ol.ptr(xs, ol.u64p), n, 1,
+                                           ol.ptr(out))
+            if rc != 0:
+                return None
+            mism += int(np.count_nonzero(out != gb[:n]))
+            done += n
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": done / dt, "unit": "evals/s", "cores": 1, "kind": "reference",
+            "sample": "%d DCF evals over the first %d keys per party of the same N=2^20 batch "
+                      "(cycled): the reference's Myl7FssBackend::eval_dcf_many_u64 built from "
+                      "its own sources (oracle/build_ref.sh), one thread as its batch loop; "
+                      "shares compared with the GPU: %d mismatches" % (done, n, mism),
+            "mismatches": mism, "host": host_info()}
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -964,6 +1004,11 @@ def main():
         g1 = out1[:sample].cpu().numpy()
         line["cpu_baseline"] = cpu_baseline(k0[:sample].cpu().numpy(), k1[:sample].cpu().numpy(),
                                             xhat[:sample], g0, g1, a.cpu_seconds)
+        refn = 1 << 12
+        ref = cpu_baseline_reference(k0[:refn].cpu().numpy(), k1[:refn].cpu().numpy(),
+                                     xhat[:refn], g0[:refn], g1[:refn], a.cpu_seconds / 2)
+        if ref is not None:
+            line["cpu_baseline_reference"] = ref
     print(json.dumps(line), flush=True)
     if not ok:
         sys.exit(1)
