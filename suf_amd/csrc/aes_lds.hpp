@@ -459,6 +459,93 @@ struct AesLds4 {
     const uint32_t c0 = col(s0, s1, s2, s3, rk[9].x);
     return (t<3, 0>(c0) ^ rk[10].x) & 0xffu;
   }
+  // N independent blocks in lockstep (AesLds2::encrypt_n's contract): each
+  // round computes every table address, then issues every table read and
+  // round key, then combines (two 3-input XORs per column), with scheduling
+  // barriers between the three groups.
+  template <int N>
+  __device__ __forceinline__ void encrypt_n(uint32_t (&st)[N][4], const uint4* const (&rk)[N]) const {
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const uint4 k = rk[n][0];
+      st[n][0] ^= k.x;
+      st[n][1] ^= k.y;
+      st[n][2] ^= k.z;
+      st[n][3] ^= k.w;
+    }
+#pragma unroll 1
+    for (int r = 1; r < 10; ++r) {
+      uint32_t addr[N][16];
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            addr[n][4 * c + j] = __builtin_amdgcn_perm(st[n][(c + j) & 3], base[j], sel(j));
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t v[N][16];
+      uint4 k[N];
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        k[n] = rk[n][r];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          v[n][i] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(lds) +
+                                                       addr[n][i]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const uint32_t kk[4] = {k[n].x, k[n].y, k[n].z, k[n].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          st[n][c] = xor3(xor3(v[n][4 * c], v[n][4 * c + 1], v[n][4 * c + 2]), v[n][4 * c + 3],
+                          kk[c]);
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const uint4 k = rk[n][10];
+      const uint32_t o0 = last_col(st[n][0], st[n][1], st[n][2], st[n][3], k.x);
+      const uint32_t o1 = last_col(st[n][1], st[n][2], st[n][3], st[n][0], k.y);
+      const uint32_t o2 = last_col(st[n][2], st[n][3], st[n][0], st[n][1], k.z);
+      const uint32_t o3 = last_col(st[n][3], st[n][0], st[n][1], st[n][2], k.w);
+      st[n][0] = o0;
+      st[n][1] = o1;
+      st[n][2] = o2;
+      st[n][3] = o3;
+    }
+  }
+  // Staging split into loads and stores (AesLds2::Filler's contract), so a
+  // kernel can issue its other staging loads between them: each of kThreads
+  // threads loads the T words of its slots, then stores them rotated into
+  // the four tables, four copies per 16-byte store.
+  template <int kThreads>
+  struct Filler {
+    static constexpr int kSlots = kWords / 4;
+    static constexpr int kPer = (kSlots + kThreads - 1) / kThreads;
+    uint32_t v[kPer];
+    __device__ __forceinline__ static int entry(int q) { return ((4 * q) >> 6) & 255; }
+    __device__ __forceinline__ void load(const uint32_t* tsrc) {
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int q = int(threadIdx.x) + u * kThreads;
+        v[u] = tsrc[entry(q < kSlots ? q : kSlots - 1)];
+      }
+    }
+    __device__ __forceinline__ void store(uint32_t* lds) const {
+      uint4* dst = reinterpret_cast<uint4*>(lds);
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int q = int(threadIdx.x) + u * kThreads;
+        const int i = 4 * q;
+        const int j = 2 * (i >> 14) + ((i >> 5) & 1);
+        const uint32_t w = rotl32(v[u], 8 * j);
+        if (q < kSlots) dst[q] = make_uint4(w, w, w, w);
+      }
+    }
+  };
   // Column-parallel AES-128 over a quad of lanes (lanes 4m..4m+3, all
   // active): lane q = lane & 3 holds column q of the state and reads column
   // q of round key r at rkq[4 r].  A lane looks up the four bytes of its own

@@ -15,24 +15,46 @@
 namespace sufhip {
 namespace {
 
-constexpr int kBlock = 512;  // two workgroups of the 72 KB LDS footprint per CU
-constexpr int kCopies = 32;
-using ChainAes = AesLds2<kCopies>;
+// Two forms.  The narrow one runs two 512-lane workgroups per CU on the
+// two-table AES span (64 KB of LDS each).  The wide one runs one 1024-lane
+// workgroup per CU (four waves per SIMD, at most 128 VGPRs) on the
+// four-table AES (128 KB): two 3-input XORs per column where the two-table
+// span needs a rotate and three XORs, a quarter fewer VALU operations per
+// round on the pipe that bounds the chain, at twice the staging per
+// workgroup and without a second workgroup to overlap it.  Batches of at
+// least two full passes of the chip take the wide form.
+template <bool kWide>
+struct ChainCfg {
+  static constexpr int kBlock = 512;
+  using Aes = AesLds2<32>;
+  static constexpr int kTabWords = Aes::kSpanWords;
+  static constexpr int kPerCu = 2;
+};
+template <>
+struct ChainCfg<true> {
+  static constexpr int kBlock = 1024;
+  using Aes = AesLds4;
+  static constexpr int kTabWords = Aes::kWords;
+  static constexpr int kPerCu = 1;
+};
 
 // kPlain: x and the triple shares are plain arrays (ChainArgs::plain and
 // plain_x), read through plain pointers.
-template <int kKind, bool kPlain>
-__global__ void __launch_bounds__(kBlock) gate_chain_kernel(ChainArgs A) {
+template <int kKind, bool kPlain, bool kWide>
+__global__ void __launch_bounds__(ChainCfg<kWide>::kBlock) gate_chain_kernel(ChainArgs A) {
+  using Cfg = ChainCfg<kWide>;
+  using ChainAes = typename Cfg::Aes;
+  constexpr int kBlock = Cfg::kBlock;
   constexpr int W = kKind == SUFHIP_CHAIN_CUBIC ? 4 : 2;
   constexpr int kProds = chain_products<kKind>();
-  __shared__ __align__(16) uint32_t tab[ChainAes::kSpanWords];
+  __shared__ __align__(16) uint32_t tab[Cfg::kTabWords];
   __shared__ ChainLds L;
   __shared__ TruncHdr th[kProds][2];
-  // Staging in one pass: the span's slots, the LUT items and the gates'
+  // Staging in one pass: the tables' slots, the LUT items and the gates'
   // key headers all loaded before the first LDS store.
   {
     TruncHdrStager<kProds> hs;
-    ChainAes::Filler<kBlock> tf;
+    typename ChainAes::template Filler<kBlock> tf;
     ChainStager<kBlock, 2> cs;
     hs.load(A, 0);
     tf.load(kTDev.v);
@@ -68,13 +90,25 @@ __global__ void __launch_bounds__(kBlock) gate_chain_kernel(ChainArgs A) {
   }
 }
 
-unsigned int chain_grid(size_t n) {
+int cu_count() {
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  const size_t need = (n + kBlock - 1) / kBlock;
-  const size_t cap = size_t(cus) * 2;
-  return static_cast<unsigned int>(need < cap ? need : cap);
+  return cus;
+}
+
+template <int kKind, bool kPlain>
+void launch_chain(const ChainArgs& A, hipStream_t s) {
+  const size_t cus = size_t(cu_count());
+  const bool wide = A.n >= 2 * cus * size_t(ChainCfg<true>::kBlock);
+  const size_t block = wide ? ChainCfg<true>::kBlock : ChainCfg<false>::kBlock;
+  const size_t cap = cus * (wide ? ChainCfg<true>::kPerCu : ChainCfg<false>::kPerCu);
+  const size_t need = (A.n + block - 1) / block;
+  const dim3 grid(unsigned(need < cap ? need : cap));
+  if (wide)
+    hipLaunchKernelGGL((gate_chain_kernel<kKind, kPlain, true>), grid, dim3(block), 0, s, A);
+  else
+    hipLaunchKernelGGL((gate_chain_kernel<kKind, kPlain, false>), grid, dim3(block), 0, s, A);
 }
 
 }  // namespace
@@ -90,21 +124,20 @@ int sufhip_gate_chain2(const sufhip_chain2_args* args, void* stream) {
   ChainArgs A;
   if (int rc = make_chain_args(g, true, "sufhip_gate_chain2", &A)) return rc;
   if (g.n == 0) return SUFHIP_OK;
-  const dim3 grid(chain_grid(g.n)), block(kBlock);
   hipStream_t s = as_stream(stream);
   const bool plain = A.plain && A.plain_x;
   if (g.kind == SUFHIP_CHAIN_CUBIC && plain)
-    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_CUBIC, true>), grid, block, 0, s, A);
+    launch_chain<SUFHIP_CHAIN_CUBIC, true>(A, s);
   else if (g.kind == SUFHIP_CHAIN_CUBIC)
-    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_CUBIC, false>), grid, block, 0, s, A);
+    launch_chain<SUFHIP_CHAIN_CUBIC, false>(A, s);
   else if (g.kind == SUFHIP_CHAIN_RECIP && plain)
-    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_RECIP, true>), grid, block, 0, s, A);
+    launch_chain<SUFHIP_CHAIN_RECIP, true>(A, s);
   else if (g.kind == SUFHIP_CHAIN_RECIP)
-    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_RECIP, false>), grid, block, 0, s, A);
+    launch_chain<SUFHIP_CHAIN_RECIP, false>(A, s);
   else if (plain)
-    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_RSQRT, true>), grid, block, 0, s, A);
+    launch_chain<SUFHIP_CHAIN_RSQRT, true>(A, s);
   else
-    hipLaunchKernelGGL((gate_chain_kernel<SUFHIP_CHAIN_RSQRT, false>), grid, block, 0, s, A);
+    launch_chain<SUFHIP_CHAIN_RSQRT, false>(A, s);
   return check_launch("gate_chain_kernel");
 }
 

@@ -349,3 +349,37 @@ def test_softmax_block_rejects_indexed_nexp_triples():
     a.nexp.a[0].index = idx.data_ptr()
     with pytest.raises(native.SufHipError, match="plain arrays"):
         native.call("sufhip_softmax2", native.ctypes.byref(a), 0)
+
+
+@pytest.mark.parametrize("kind", ["recip", "rsqrt"])
+def test_chain_wide_form_matches_oracle(kind):
+    """Batches of at least two passes of 1024-lane workgroups over every CU
+    take the chain kernel's four-table form (one workgroup per CU); the
+    shares equal the oracle's, with a partial last pass, under either
+    keystream policy."""
+    from suf_amd.tasks import operand, term
+    n = 2 * 256 * 1024 + 333
+    v = ((np.arange(n, dtype=np.int64) * 613 + 3) % (17 << F)).astype(np.uint64)
+    v0, v1 = _share(v, 43)
+    say("%s chain, wide form, n=%d" % (kind, n))
+    if kind == "recip":
+        g = softmax.Recip(n, softmax.Dealer(21), STATE, F)
+    else:
+        g = layernorm.Rsqrt(n, softmax.Dealer(22), STATE, F)
+    for tr in g.truncs():
+        tr.prepare()
+    vp = _pair_dev(v0, v1)
+    outs = []
+    for per_party in (False, True):
+        with pfss.keystream_per_party(per_party):
+            if kind == "recip":
+                out = g.eval2(vp, None, fused=True)
+            else:
+                out = g.eval2(operand(term(vp)), None, fused=True)
+        outs.append([u64(out[0]), u64(out[1])])
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    if kind == "recip":
+        o = tp.recip2(ol.Prg(STATE), g, [v0, v1], (v + np.uint64(g.lut.mask)).astype(np.uint64))
+    else:
+        o = tp.rsqrt2(ol.Prg(STATE), g, [v0, v1], tp.open2([v0, v1], g.lut.mask))
+    assert np.array_equal(outs[0][0], o[0]) and np.array_equal(outs[0][1], o[1])

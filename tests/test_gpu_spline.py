@@ -35,7 +35,10 @@ def _oracle_pipeline(gate, x0, x1):
 
 
 @pytest.mark.parametrize("fused", [True, False])
-@pytest.mark.parametrize("n,seed", [(3000, 7), (777, 8)])
+@pytest.mark.parametrize("n,seed", [(3000, 7), (777, 8),
+                                    # two full passes and a partial third of the chain
+                                    # kernel's wide form
+                                    (2 * 256 * 1024 + 777, 9)])
 def test_shares_match_oracle_pipeline(n, seed, fused):
     alpha, coeffs = spline.spline_spec(F, seed=6)
     x = pfss.host_normal_fixed(5 + seed, 3.0, 8.0, F, n)
