@@ -128,13 +128,16 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
     block_sum2_u64<kLnWaves>(q0, q1, red);
     const Two va = gate(kTrVar0, q0 * A.inv_len + q1 * A.inv_len + A.mask[kTrVar0]);
     const Two var = gate(kTrVar1, va.v[0] + va.v[1] + A.mask[kTrVar1]);
-    // rsqrt of the row's variance on one lane.
-    if (threadIdx.x == 0) {
+    // rsqrt of the row's variance on the first wave (its keystream blocks
+    // column-parallel on eight lanes, the rest of the chain on every lane).
+    if (threadIdx.x < 64) {
       const Two v{{var.v[0] + A.eps, var.v[1]}};
       const Two rs =
-          chain_eval<SUFHIP_CHAIN_RSQRT, LnAes>(A.rs, L, K, aes, size_t(r), v, pre);
-      bc[0] = rs.v[0];
-      bc[1] = rs.v[1];
+          chain_eval_quad<SUFHIP_CHAIN_RSQRT, LnAes>(A.rs, L, K, aes, size_t(r), v, pre);
+      if (threadIdx.x == 0) {
+        bc[0] = rs.v[0];
+        bc[1] = rs.v[1];
+      }
     }
     __syncthreads();
     // out = tr_norm(d * rs[row]) (row-broadcast Beaver).
@@ -399,16 +402,15 @@ __global__ void __launch_bounds__(kSmThreads) softmax2_kernel(SmArgs a) {
     }
     es0 = wave_sum_u64(es0);
     es1 = wave_sum_u64(es1);
-    // inv = Recip(row sum) on lane 0.
+    // inv = Recip(row sum) on the whole wave (its keystream blocks
+    // column-parallel on eight lanes, every lane ends with the result).
     uint64_t inv0 = 0, inv1 = 0;
-    if (lane == 0 && len > 0) {
-      const Two iv = chain_eval<SUFHIP_CHAIN_RECIP, SmAes, ChainPreN<3>, true>(
+    if (len > 0) {
+      const Two iv = chain_eval_quad<SUFHIP_CHAIN_RECIP, SmAes, ChainPreN<3>>(
           a.recip, st.recip, Kr, aes, size_t(r), Two{{es0, es1}}, st.rpre[wave], st.thr);
       inv0 = iv.v[0];
       inv1 = iv.v[1];
     }
-    inv0 = bcast_lane0(inv0);
-    inv1 = bcast_lane0(inv1);
     // prob = tr_norm(e * inv[row]) (row-broadcast Beaver), and the next
     // product's open over the dense row.
     if (len > 0) {
@@ -632,13 +634,16 @@ __global__ void __launch_bounds__(kSmTeamThreads) softmax2_team_kernel(SmArgs a)
       part[slot][tw][1] = ps1;
     }
     __syncthreads();
-    // inv = Recip(row sum) on the first wave's lane 0.
-    if (tw == 0 && lane == 0 && len > 0) {
+    // inv = Recip(row sum) on the first wave (its keystream blocks
+    // column-parallel on eight lanes).
+    if (tw == 0 && len > 0) {
       const Two es{{part[slot][0][0] + part[slot][1][0], part[slot][0][1] + part[slot][1][1]}};
-      const Two iv = chain_eval<SUFHIP_CHAIN_RECIP, SmAes, ChainPreN<3>, true>(
+      const Two iv = chain_eval_quad<SUFHIP_CHAIN_RECIP, SmAes, ChainPreN<3>>(
           a.recip, st.recip, Kr, aes, size_t(r), es, st.rpre[slot], st.thr);
-      invs[slot][0] = iv.v[0];
-      invs[slot][1] = iv.v[1];
+      if (lane == 0) {
+        invs[slot][0] = iv.v[0];
+        invs[slot][1] = iv.v[1];
+      }
     }
     __syncthreads();
     // prob = tr_norm(e * inv[row]) (row-broadcast Beaver), and the next

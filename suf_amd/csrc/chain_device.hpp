@@ -372,6 +372,61 @@ __device__ __forceinline__ void chain_stage_trunc_hdrs(const ChainArgs& A, Trunc
   s.store(th);
 }
 
+// The products and truncations of a chain from its LUT coefficients cf
+// (per element m and party p, W words), results in out[m].
+template <int kKind, int M, class Src>
+__device__ __forceinline__ void chain_finish_m(
+    const ChainArgs& A, const uint64_t (&cf)[M][2][kKind == SUFHIP_CHAIN_CUBIC ? 4 : 2],
+    const Two (&x)[M], const Src (&P)[M], Two (&out)[M], const TruncHdr (*th)[2]) {
+  const int f = A.f;
+  Two t1[M], t2[M];
+  if constexpr (kKind == SUFHIP_CHAIN_CUBIC) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      Two mm = chain_beaver(P[m], 0, Two{{cf[m][0][3], cf[m][1][3]}}, x[m]);
+      mm.v[0] += cf[m][0][2] << f;
+      mm.v[1] += cf[m][1][2] << f;
+      t1[m] = chain_trunc(A, 0, chain_beaver(P[m], 1, mm, x[m]), th);
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const Two q{{t1[m].v[0] + (cf[m][0][1] << f), t1[m].v[1] + (cf[m][1][1] << f)}};
+      t2[m] = chain_trunc(A, 1, chain_beaver(P[m], 2, q, x[m]), th);
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      out[m] = chain_trunc(
+          A, 2, Two{{t2[m].v[0] + (cf[m][0][0] << f), t2[m].v[1] + (cf[m][1][0] << f)}}, th);
+  } else {
+    Two y[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const Two t =
+          chain_trunc(A, 0, chain_beaver(P[m], 0, Two{{cf[m][0][1], cf[m][1][1]}}, x[m]), th);
+      y[m] = Two{{t.v[0] + cf[m][0][0], t.v[1] + cf[m][1][0]}};
+    }
+    if constexpr (kKind == SUFHIP_CHAIN_RECIP) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) t1[m] = chain_trunc(A, 1, chain_beaver(P[m], 1, y[m], x[m]), th);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const Two two{{(uint64_t(2) << f) - t1[m].v[0], uint64_t(0) - t1[m].v[1]}};
+        out[m] = chain_trunc(A, 2, chain_beaver(P[m], 2, y[m], two), th);
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < M; ++m) t1[m] = chain_trunc(A, 1, chain_beaver(P[m], 1, y[m], y[m]), th);
+#pragma unroll
+      for (int m = 0; m < M; ++m) t2[m] = chain_trunc(A, 2, chain_beaver(P[m], 2, x[m], t1[m]), th);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const Two inner{{(uint64_t(3) << (f - 1)) - t2[m].v[0], uint64_t(0) - t2[m].v[1]}};
+        out[m] = chain_trunc(A, 3, chain_beaver(P[m], 3, y[m], inner), th);
+      }
+    }
+  }
+}
+
 // The whole chain for M elements at once (element m: index i[m], input
 // shares x[m], triple shares from P[m], a ChainPreN or chain_loader), results
 // in out[m].  Every step runs for all M elements before the next, so the
@@ -391,7 +446,7 @@ __device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds&
   constexpr int W = kKind == SUFHIP_CHAIN_CUBIC ? 4 : 2;
   constexpr int NB = W / 2;  // AES blocks per element and party
   constexpr int NS = M * NB;  // blocks per party
-  const int nint = A.intervals, f = A.f;
+  const int nint = A.intervals;
   int iv[M][2];
   uint32_t st[2][NS][4];
 #pragma unroll
@@ -490,52 +545,7 @@ __device__ __forceinline__ void chain_eval_m(const ChainArgs& A, const ChainLds&
         cf[m][p][2 * b] = K.party[p] == 0 ? k0 : row[2 * b] - k0;
         cf[m][p][2 * b + 1] = K.party[p] == 0 ? k1 : row[2 * b + 1] - k1;
       }
-  Two t1[M], t2[M];
-  if constexpr (kKind == SUFHIP_CHAIN_CUBIC) {
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      Two mm = chain_beaver(P[m], 0, Two{{cf[m][0][3], cf[m][1][3]}}, x[m]);
-      mm.v[0] += cf[m][0][2] << f;
-      mm.v[1] += cf[m][1][2] << f;
-      t1[m] = chain_trunc(A, 0, chain_beaver(P[m], 1, mm, x[m]), th);
-    }
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const Two q{{t1[m].v[0] + (cf[m][0][1] << f), t1[m].v[1] + (cf[m][1][1] << f)}};
-      t2[m] = chain_trunc(A, 1, chain_beaver(P[m], 2, q, x[m]), th);
-    }
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-      out[m] = chain_trunc(
-          A, 2, Two{{t2[m].v[0] + (cf[m][0][0] << f), t2[m].v[1] + (cf[m][1][0] << f)}}, th);
-  } else {
-    Two y[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const Two t =
-          chain_trunc(A, 0, chain_beaver(P[m], 0, Two{{cf[m][0][1], cf[m][1][1]}}, x[m]), th);
-      y[m] = Two{{t.v[0] + cf[m][0][0], t.v[1] + cf[m][1][0]}};
-    }
-    if constexpr (kKind == SUFHIP_CHAIN_RECIP) {
-#pragma unroll
-      for (int m = 0; m < M; ++m) t1[m] = chain_trunc(A, 1, chain_beaver(P[m], 1, y[m], x[m]), th);
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const Two two{{(uint64_t(2) << f) - t1[m].v[0], uint64_t(0) - t1[m].v[1]}};
-        out[m] = chain_trunc(A, 2, chain_beaver(P[m], 2, y[m], two), th);
-      }
-    } else {
-#pragma unroll
-      for (int m = 0; m < M; ++m) t1[m] = chain_trunc(A, 1, chain_beaver(P[m], 1, y[m], y[m]), th);
-#pragma unroll
-      for (int m = 0; m < M; ++m) t2[m] = chain_trunc(A, 2, chain_beaver(P[m], 2, x[m], t1[m]), th);
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const Two inner{{(uint64_t(3) << (f - 1)) - t2[m].v[0], uint64_t(0) - t2[m].v[1]}};
-        out[m] = chain_trunc(A, 3, chain_beaver(P[m], 3, y[m], inner), th);
-      }
-    }
-  }
+  chain_finish_m<kKind, M, Src>(A, cf, x, P, out, th);
 }
 
 // The whole chain for one element (chain_eval_m with M = 1).
@@ -549,6 +559,69 @@ __device__ __forceinline__ Two chain_eval(const ChainArgs& A, const ChainLds& L,
   const Src pp[1] = {P};
   Two out[1];
   chain_eval_m<kKind, Aes, 1, Src, kLockBoth>(A, L, K, aes, ii, xx, pp, out, th);
+  return out[0];
+}
+
+// One element's RECIP or RSQRT chain computed by a whole wave (the per-row
+// reciprocal and rsqrt of the block kernels): every lane runs the interval
+// searches, products and truncations on the same (wave-uniform) i, x and
+// triples, so every lane ends with the result, while the LUT keystream block
+// of party p is encrypted column-parallel by lanes 4 p .. 4 p + 3
+// (Aes::encrypt_quad_n, both parties' quads at once) and broadcast with
+// readlane.  That is one quad-AES latency instead of a lane's two blocks.
+// Party 1's block comes from its own blob; where the blobs are equal it is
+// party 0's block, as in chain_eval_m.
+template <int kKind, class Aes, class Src>
+__device__ __forceinline__ Two chain_eval_quad(const ChainArgs& A, const ChainLds& L,
+                                               const ChainKeyInfo& K, const Aes& aes, size_t i,
+                                               Two x, const Src& P,
+                                               const TruncHdr (*th)[2] = nullptr) {
+  static_assert(kKind != SUFHIP_CHAIN_CUBIC, "chain_eval_quad: one keystream block per party");
+  constexpr int W = 2;
+  const int lane = threadIdx.x & 63;
+  const uint64_t xh = x.v[0] + x.v[1] + A.lut_mask;
+  int iv[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const uint64_t xm = xh & K.m[p];
+    int lo = 0, hi = A.intervals;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if ((L.cuts[p][mid] & K.m[p]) <= xm)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    iv[p] = lo - 1 < 0 ? 0 : lo - 1;
+  }
+  uint32_t ks = 0;
+  if (lane < 8) {
+    // Selects, not indexing: a lane-dependent index into the register
+    // arrays iv and K.nonce would put them in private memory.
+    const bool p1 = lane >= 4;
+    const int q = lane & 3;
+    const uint64_t ctr =
+        (p1 ? K.nonce[1] : K.nonce[0]) ^ (uint64_t(i) << 32) ^ (uint64_t(p1 ? iv[1] : iv[0]) * W);
+    uint32_t s[1] = {q == 0 ? uint32_t(ctr) : (q == 1 ? uint32_t(ctr >> 32) : 0u)};
+    const uint32_t* const rk[1] = {reinterpret_cast<const uint32_t*>(L.rk[p1 ? 1 : 0]) + q};
+    aes.template encrypt_quad_n<1>(s, rk);
+    ks = s[0];  // column q of party p's block
+  }
+  uint64_t cf[1][2][W];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const uint64_t k0 = uint64_t(uint32_t(__builtin_amdgcn_readlane(int(ks), 4 * p))) |
+                        uint64_t(uint32_t(__builtin_amdgcn_readlane(int(ks), 4 * p + 1))) << 32;
+    const uint64_t k1 = uint64_t(uint32_t(__builtin_amdgcn_readlane(int(ks), 4 * p + 2))) |
+                        uint64_t(uint32_t(__builtin_amdgcn_readlane(int(ks), 4 * p + 3))) << 32;
+    const uint64_t* row = L.pay[p] + size_t(iv[p]) * W;
+    cf[0][p][0] = K.party[p] == 0 ? k0 : row[0] - k0;
+    cf[0][p][1] = K.party[p] == 0 ? k1 : row[1] - k1;
+  }
+  const Two xx[1] = {x};
+  const Src pp[1] = {P};
+  Two out[1];
+  chain_finish_m<kKind, 1, Src>(A, cf, xx, pp, out, th);
   return out[0];
 }
 
