@@ -110,14 +110,28 @@ def _graph_ms(run, steps, warmup):
     return e0.elapsed_time(e1) / steps, eager_ms
 
 
+# Device-side spin (core clock cycles, ~0.2-0.4 ms) queued before a start
+# event: while it runs the host stages the launch to be timed, so the event
+# pair brackets the kernel, not the host's launch overhead on an idle stream.
+SPIN_CYCLES = 500_000
+
+
+def spin():
+    import torch
+
+    torch.cuda._sleep(SPIN_CYCLES)
+
+
 def _launch_ms(run, steps):
     """Mean ms of one launch: events on torch's current stream (the stream
-    the launch goes to) right before and after each of `steps` calls."""
+    the launch goes to) right before and after each of `steps` calls, each
+    start event behind a device-side spin."""
     import numpy as np
     import torch
 
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
     for s in range(steps):
+        spin()
         ev[s][0].record()
         run()
         ev[s][1].record()
@@ -215,7 +229,7 @@ def trunc_table_bytes(gates, f=12):
 
 def softmax_bytes(n_packed, rows, pre=0, indexed_input=False, out_written=True, n_dense=0,
                   dense_planes=False):
-    """softmax2_kernel's streams: per packed element the scores (16, + a
+    """The softmax block kernels' streams: per packed element the scores (16, + a
     4-byte index), the nExp chain's triples (144), the normalisation's a and
     c shares (32), the probabilities (16); per row the reciprocal chain's
     triples (144), the normalisation's b shares (16) and the row offset (4);
@@ -241,10 +255,10 @@ def _traffic(fetch_kib, write_kib):
     return fetch_kib * 1024 * 2.0 + write_kib * 1024 * 1.0
 
 
-SPLINE_CHAIN_TRAFFIC = _traffic(86130.5, 16384.0)
+SPLINE_CHAIN_TRAFFIC = _traffic(85280.0, 16384.0)
 MATMUL_PRODUCT_TRAFFIC = _traffic(41173, 6144)
-SOFTMAX_TRAFFIC = _traffic(15061.2, 1560.6)
-LAYER_SOFTMAX_TRAFFIC = _traffic(17833.8, 4622.8)
+SOFTMAX_TRAFFIC = _traffic(14919.3, 1560.0)
+LAYER_SOFTMAX_TRAFFIC = _traffic(17666.4, 4616.1)
 
 
 def bench_spline(steps, warmup, n=1 << 20, frac_bits=12, cpu_seconds=0.0, shared=True):
@@ -495,21 +509,24 @@ def bench_softmax_ln(steps, warmup, frac_bits=12, cpu=True, shared=True):
         # on the same stream; then the two one-launch blocks.
         prep = (tasks.Prepared(None, [sm.truncs() + ln.truncs()]), 0)
         if ev:
+            spin()
             ev[0].record()
         sm.eval2(sin, sout, prep=prep)
         if ev:
             ev[1].record()
+            spin()
+            ev[2].record()
         ln.eval2(lin, lout, prep=prep)
         if ev:
-            ev[2].record()
+            ev[3].record()
 
     def split_ms():
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
         for s in range(steps):
             run(ev[s])
         torch.cuda.synchronize()
         return (float(np.mean([e[0].elapsed_time(e[1]) for e in ev])),
-                float(np.mean([e[1].elapsed_time(e[2]) for e in ev])))
+                float(np.mean([e[2].elapsed_time(e[3]) for e in ev])))
 
     with pfss.keystream_per_party():
         ms, eager_ms = _graph_ms(run, steps, warmup)
@@ -526,7 +543,7 @@ def bench_softmax_ln(steps, warmup, frac_bits=12, cpu=True, shared=True):
            "softmax_shape": "12 heads x 128 causal rows (%d scores)" % n_sm,
            "layernorm_shape": [rows, cols], "frac_bits": frac_bits, "steps": steps,
            "roofline": roofline_hbm(
-               "softmax2_kernel", sm_ms, softmax_bytes(n_sm, len(offs) - 1),
+               "softmax2_team_kernel", sm_ms, softmax_bytes(n_sm, len(offs) - 1),
                "per score 16 in + nExp triples 144 + normalisation shares 32 + 16 out; per row "
                "164; 7 truncation tables once (2 x 2^12 x 16 B each)",
                note="per-party keystreams; bound by each row's chain of dependent steps (max "
@@ -647,7 +664,7 @@ def bench_layer(steps, warmup, frac_bits=12, cpu=True, shared=True):
         per_stage = {stages[i]: m[i].elapsed_time(m[i + 1]) for i in range(len(stages))}
         smk = []
         for _ in range(steps):
-            ly.eval2(xin, out, sm_marks=smk)
+            ly.eval2(xin, out, sm_marks=smk, sm_spin=spin)
         torch.cuda.synchronize()
         sm_ms = float(np.mean([smk[2 * i].elapsed_time(smk[2 * i + 1])
                                for i in range(len(smk) // 2)]))
@@ -675,7 +692,7 @@ def bench_layer(steps, warmup, frac_bits=12, cpu=True, shared=True):
            "shape": {"seq": seq, "hidden": d, "heads": heads, "ffn": ffn}, "frac_bits": frac_bits,
            "ring": "Z_2^64", "steps": steps, "graph_replays_match_eager": replay_ok,
            "roofline": roofline_hbm(
-               "softmax2_kernel (scores' two truncations, softmax, open of P - A as planes)",
+               "softmax2_team_kernel (scores' two truncations, softmax, open of P - A as planes)",
                sm_ms, softmax_bytes(at.n, heads * seq, pre=2, indexed_input=True,
                                     out_written=False, n_dense=heads * seq * seq,
                                     dense_planes=True),

@@ -290,14 +290,17 @@ class AttentionCore:
     def truncs(self):
         return self.tr_s + [self.tr_c] + self.softmax.truncs()
 
-    def eval2(self, qkv, out, prep=None, fused=True, planes=None, sm_marks=None):
+    def eval2(self, qkv, out, prep=None, fused=True, planes=None, sm_marks=None,
+              sm_spin=None):
         """prep: (tasks.Prepared, batch) holding the key-only halves of
         truncs(), or None to issue them here.  fused: scores, softmax and the
         next open in one launch (sufhip_softmax2); else launch by launch.
         planes = (buffer, cols): the context also as the output projection's
         digit planes (matrix-core products only).  sm_marks: optional list
         that receives two timing events around the one-launch softmax block
-        (eager profiling)."""
+        (eager profiling); sm_spin: optional callable that queues device work
+        before the first of them (a spin that hides the host's staging of the
+        launch, so the events bracket the kernel)."""
         seq, d, h, dh, mp = self.seq, self.d, self.heads, self.dh, self.maps
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
@@ -325,6 +328,8 @@ class AttentionCore:
             # digit planes on the matrix cores).
             dp = self.tri_pv.d_planes() if self.mfma() else None
             if sm_marks is not None:
+                if sm_spin is not None:
+                    sm_spin()
                 sm_marks.append(torch.cuda.Event(enable_timing=True))
                 sm_marks[-1].record()
             self.softmax.eval_block(scaled, pre=self.tr_s,
@@ -408,14 +413,14 @@ class TransformerLayer:
                 self.proj.truncs() + self.ln2.truncs() + self.w1.truncs() + self.gelu.truncs() +
                 self.w2.truncs()]
 
-    def eval2(self, x, out, marks=None, overlap_prepare=False, sm_marks=None):
+    def eval2(self, x, out, marks=None, overlap_prepare=False, sm_marks=None, sm_spin=None):
         """x, out: pairs of int64 [seq * d] device tensors.  marks: optional
         list of torch events recorded after each stage (profiling).  The
         key-only halves of all truncation gates run first, in one batched
         walk on the current stream; with overlap_prepare they run on a side
         stream instead, in three batches, each ahead of the stage that needs
         it (a fork or join between streams costs about as much as it
-        hides).  sm_marks: see AttentionCore.eval2."""
+        hides).  sm_marks, sm_spin: see AttentionCore.eval2."""
         if overlap_prepare:
             prep = Prepared(self.side, self.stage_truncs(), upfront=2)
             b = lambda k: k  # noqa: E731
@@ -446,12 +451,13 @@ class TransformerLayer:
         mark()
         if self.attn.mfma():
             self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)), planes=self.proj.x_planes(),
-                            sm_marks=sm_marks)
+                            sm_marks=sm_marks, sm_spin=sm_spin)
             mark()
             prep.wait(b(2))
             self.proj.eval2(None, self.r1, add=x)  # r1 = trunc(ctx Wout) + x
         else:
-            self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)), sm_marks=sm_marks)
+            self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)), sm_marks=sm_marks,
+                            sm_spin=sm_spin)
             mark()
             prep.wait(b(2))
             self.proj.eval2(self.ctx, self.r1, add=x)

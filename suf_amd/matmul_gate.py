@@ -152,13 +152,8 @@ class BeaverMatmulTrunc:
         launch; all on the current stream."""
         from . import layer
         M, K, N = self.M, self.K, self.N
-        self.tr.prepare()
-        if events:
-            events[0].record()
-        layer.kb_open_split([(X, self.A, self.Dp, 1, M, K, 1, self.Xp, self.A[0]),
-                             (W, self.B, self.Ep, 1, K, N, 0)])
-        if events and len(events) > 2:
-            events[1].record()
+        # The product's arguments are staged first, so that its launch
+        # follows the opens' with no host work in between.
         a = native.BeaverMfma2Args()
         a.Dp, a.Ep, a.Xp = _p(self.Dp), _p(self.Ep), _p(self.Xp)
         for p in (0, 1):
@@ -167,6 +162,13 @@ class BeaverMatmulTrunc:
         epi = self.tr.epilogue(out)
         a.trunc = native.ctypes.pointer(epi)
         a.mask = self.tr.mask & M64
+        self.tr.prepare()
+        if events:
+            events[0].record()
+        layer.kb_open_split([(X, self.A, self.Dp, 1, M, K, 1, self.Xp, self.A[0]),
+                             (W, self.B, self.Ep, 1, K, N, 0)])
+        if events and len(events) > 2:
+            events[1].record()
         native.call("sufhip_beaver_matmul2_mfma_ex", native.ctypes.byref(a), _stream())
         if events:
             events[-1].record()
