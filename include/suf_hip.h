@@ -794,7 +794,13 @@ int sufhip_kb_split_batch(const sufhip_kb_split_job* jobs, int count, void* stre
  * or E = W - B from both parties' shares: materialize_open of the Beaver
  * matmul, src/nn/matmul_beaver.cpp:34-53), laid out as in
  * sufhip_kb_split_batch.  a[0]
- * and a[1] are required; b[p] = NULL subtracts nothing. */
+ * and a[1] are required; b[p] = NULL subtracts nothing.
+ * a_stride: an optional strided view of a[0] and a[1] (u64 units, each >= 0):
+ * element (batch, row, col) of a[p] is read at a[p][a_stride[0] * batch +
+ * a_stride[1] * row + a_stride[2] * col], e.g. one head's Q, K^T or V inside
+ * the [seq x 3d] rows of a QKV product (attention_block.cpp:1517-1531 splits
+ * them by copies).  All three zero: a[p] is [batches][rows][cols] like b[p].
+ * The caller keeps every viewed element inside a[p]'s allocation. */
 typedef struct sufhip_kb_open_job {
   const uint64_t* a[2];
   const uint64_t* b[2];
@@ -803,6 +809,7 @@ typedef struct sufhip_kb_open_job {
   int k_is_col;
   int8_t* planes_a0; /* optional, with a0: planes of the open + a0[i] */
   const uint64_t* a0;
+  int64_t a_stride[3];
 } sufhip_kb_open_job;
 int sufhip_kb_open_split_batch(const sufhip_kb_open_job* jobs, int count, void* stream);
 int sufhip_beaver_matmul2_mfma_batched(const int8_t* d_Dp, const int8_t* d_Ep,

@@ -41,58 +41,65 @@ struct SplitArgs {
   int8_t* planes_a0[kSplitJobs];       // optional: planes of the value + a0[i]
   const uint64_t* a0[kSplitJobs];
   int batches[kSplitJobs], rows[kSplitJobs], cols[kSplitJobs], k_is_col[kSplitJobs];
-  size_t begin[kSplitJobs + 1];  // lanes of the jobs before (4 or 16 k each)
+  // src and add read through a strided view (batch, row, col strides; all
+  // zero: the plain [batches][rows][cols] index of the other arrays).
+  size_t view[kSplitJobs][3];
+  size_t begin[kSplitJobs + 1];  // lanes of the jobs before (set by launch_split)
   int count;
 };
 
-// Row-side operands (k_is_col: k runs along a source row) take one lane
-// per 4 consecutive k of one plane row: 4 adjacent words in, consecutive
-// lanes writing consecutive 4-byte groups.  Column-side operands take one
-// lane per 16 k of one plane row: 16 words a source row apart, the two
-// halves of a 32-byte row segment on adjacent lanes and consecutive lane
-// pairs on consecutive columns, so that every segment of every plane is
-// written whole by one wave's 16-byte stores (never assembled from partial
-// writes of lanes in other workgroups).
-__device__ __forceinline__ uint64_t split_val(const SplitArgs& a, int j, size_t i) {
-  uint64_t v = a.src[j][i];
-  if (a.add[j]) v += a.add[j][i];
+static_assert(sizeof(SplitArgs) <= 4096, "kernel argument block must fit in 4 KB");
+
+// Row-side operands (k_is_col: k runs along a source row) take one lane per
+// 4 consecutive k of one plane row: 4 adjacent words in, consecutive lanes
+// writing consecutive 4-byte groups.  Column-side operands take one lane per
+// kColK (4 or 16) k of one plane row: kColK words a source row apart, the
+// 32 / kColK lanes of a 32-byte plane segment adjacent (k fastest, then the
+// column), so that every segment of every plane is written whole by one
+// wave's kColK-byte stores (never assembled from partial writes of lanes in
+// other workgroups).  16 k per lane reads 32 columns of 2 row groups per
+// wave; 4 k per lane gives four times the lanes, for launches too small to
+// fill the chip at 16.
+// Element i (plain index) whose src / add index is iv (the view's).
+__device__ __forceinline__ uint64_t split_val(const SplitArgs& a, int j, size_t i, size_t iv) {
+  uint64_t v = a.src[j][iv];
+  if (a.add[j]) v += a.add[j][iv];
   if (a.sub[j][0]) v -= a.sub[j][0][i];
   if (a.sub[j][1]) v -= a.sub[j][1][i];
   return v;
 }
 
-// Four consecutive k of one plane row: one 4-byte store per plane.
-__device__ __forceinline__ void write4(int8_t* planes, size_t plane, size_t off,
-                                       const uint64_t (&v)[4]) {
-  uint32_t pk[kDigitPlanes] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    uint32_t d[kDigitPlanes];
-    digits8(v[t], d);
-#pragma unroll
-    for (int i = 0; i < kDigitPlanes; ++i) pk[i] |= d[i] << (8 * t);
-  }
-#pragma unroll
-  for (int i = 0; i < kDigitPlanes; ++i)
-    *reinterpret_cast<uint32_t*>(planes + i * plane + off) = pk[i];
+// The view index of element (b, r, c), or its plain index without a view.
+__device__ __forceinline__ size_t view_index(const SplitArgs& a, int j, size_t b, size_t r,
+                                             size_t c, size_t plain) {
+  const size_t(&st)[3] = a.view[j];
+  return (st[0] | st[1] | st[2]) ? b * st[0] + r * st[1] + c * st[2] : plain;
 }
 
-// Sixteen k of one plane row (value(t), t < 16): one 16-byte store per plane.
-template <typename F>
-__device__ __forceinline__ void write16(int8_t* dst, size_t plane, F value) {
-  uint32_t pk[kDigitPlanes][4] = {};
+// kN consecutive k of one plane row (v[t], t < kN): one kN-byte store per plane.
+template <int kN>
+__device__ __forceinline__ void write_k(int8_t* planes, size_t plane, size_t off,
+                                        const uint64_t (&v)[kN]) {
+  static_assert(kN == 4 || kN == 16, "4 or 16 k per store");
+  uint32_t pk[kDigitPlanes][kN / 4] = {};
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
+  for (int t = 0; t < kN; ++t) {
     uint32_t d[kDigitPlanes];
-    digits8(value(t), d);
+    digits8(v[t], d);
 #pragma unroll
     for (int i = 0; i < kDigitPlanes; ++i) pk[i][t >> 2] |= d[i] << (8 * (t & 3));
   }
 #pragma unroll
-  for (int i = 0; i < kDigitPlanes; ++i)
-    *reinterpret_cast<uint4*>(dst + i * plane) = make_uint4(pk[i][0], pk[i][1], pk[i][2], pk[i][3]);
+  for (int i = 0; i < kDigitPlanes; ++i) {
+    if constexpr (kN == 4)
+      *reinterpret_cast<uint32_t*>(planes + i * plane + off) = pk[i][0];
+    else
+      *reinterpret_cast<uint4*>(planes + i * plane + off) =
+          make_uint4(pk[i][0], pk[i][1], pk[i][2], pk[i][3]);
+  }
 }
 
+template <int kColK>
 __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
   const size_t total = a.begin[a.count];
   for (size_t g = size_t(blockIdx.x) * 256 + threadIdx.x; g < total;
@@ -110,29 +117,37 @@ __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
       const int r = int(rem / (K / 4)), k = 4 * int(rem % (K / 4));
       const size_t src = b * size_t(rows) * cols + size_t(r) * cols + k;
       const size_t off = b * size_t(R) * K + kblock_off(size_t(r), k, size_t(R));
+      const size_t sv = view_index(a, j, b, size_t(r), size_t(k), src);
+      const size_t cs = (a.view[j][0] | a.view[j][1] | a.view[j][2]) ? a.view[j][2] : 1;
       uint64_t v[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = split_val(a, j, src + t);
-      write4(a.planes[j], plane, off, v);
+      for (int t = 0; t < 4; ++t) v[t] = split_val(a, j, src + t, sv + t * cs);
+      write_k<4>(a.planes[j], plane, off, v);
       if (a.planes_a0[j]) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) v[t] += a.a0[j][src + t];
-        write4(a.planes_a0[j], plane, off, v);
+        write_k<4>(a.planes_a0[j], plane, off, v);
       }
     } else {
-      const size_t per_batch = size_t(R) * (K / 16);
+      constexpr int kSeg = 32 / kColK;  // lanes per 32-byte plane segment
+      const size_t per_batch = size_t(R) * (K / kColK);
       const size_t b = q / per_batch, rem = q % per_batch;
-      const int h = int(rem & 1), kb = int(rem / (2 * size_t(R)));
-      const int r = int((rem >> 1) % size_t(R));
-      const int k0 = 32 * kb + 16 * h;
+      const int kq = int(rem % kSeg), kb = int(rem / (kSeg * size_t(R)));
+      const int r = int((rem / kSeg) % size_t(R));
+      const int k0 = 32 * kb + kColK * kq;
       const size_t src = b * size_t(rows) * cols + size_t(k0) * cols + r;
       const size_t off = b * size_t(R) * K + kblock_off(size_t(r), k0, size_t(R));
-      write16(a.planes[j] + off, plane, [&](int t) { return split_val(a, j, src + size_t(t) * cols); });
+      const size_t sv = view_index(a, j, b, size_t(k0), size_t(r), src);
+      const size_t rs = (a.view[j][0] | a.view[j][1] | a.view[j][2]) ? a.view[j][1] : size_t(cols);
+      uint64_t v[kColK];
+#pragma unroll
+      for (int t = 0; t < kColK; ++t)
+        v[t] = split_val(a, j, src + size_t(t) * cols, sv + size_t(t) * rs);
+      write_k<kColK>(a.planes[j], plane, off, v);
       if (a.planes_a0[j]) {
-        const uint64_t* a0 = a.a0[j];
-        write16(a.planes_a0[j] + off, plane, [&](int t) {
-          return split_val(a, j, src + size_t(t) * cols) + a0[src + size_t(t) * cols];
-        });
+#pragma unroll
+        for (int t = 0; t < kColK; ++t) v[t] += a.a0[j][src + size_t(t) * cols];
+        write_k<kColK>(a.planes_a0[j], plane, off, v);
       }
     }
   }
@@ -406,17 +421,32 @@ int split_job(SplitArgs& a, int j, int8_t* planes, int batches, int rows, int co
   a.rows[j] = rows;
   a.cols[j] = cols;
   a.k_is_col[j] = k_is_col ? 1 : 0;
-  const size_t n = size_t(batches) * rows * cols;
-  a.begin[j + 1] = a.begin[j] + n / (k_is_col ? 4 : 16);
   return SUFHIP_OK;
 }
 
+// Column-side jobs take 16 k per lane when that still gives two waves per
+// SIMD, else 4 (more lanes, shorter per-lane chains).
 int launch_split(SplitArgs& a, int count, void* stream) {
   a.count = count;
+  int cus = 256;
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  size_t col16 = 0;
+  for (int j = 0; j < count; ++j)
+    if (!a.k_is_col[j]) col16 += size_t(a.batches[j]) * a.rows[j] * a.cols[j] / 16;
+  const int ck = col16 >= size_t(cus) * 4 * 64 * 2 ? 16 : 4;
+  a.begin[0] = 0;
+  for (int j = 0; j < count; ++j)
+    a.begin[j + 1] = a.begin[j] + size_t(a.batches[j]) * a.rows[j] * a.cols[j] /
+                                      size_t(a.k_is_col[j] ? 4 : ck);
   if (a.begin[count] == 0) return SUFHIP_OK;
   size_t g = (a.begin[count] + 255) / 256;
   if (g > 4096) g = 4096;
-  hipLaunchKernelGGL(kb_split_kernel, dim3(unsigned(g)), dim3(256), 0, as_stream(stream), a);
+  if (ck == 16)
+    hipLaunchKernelGGL(kb_split_kernel<16>, dim3(unsigned(g)), dim3(256), 0, as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(kb_split_kernel<4>, dim3(unsigned(g)), dim3(256), 0, as_stream(stream), a);
   return check_launch("kb_split_kernel");
 }
 
@@ -454,10 +484,13 @@ int sufhip_kb_open_split_batch(const sufhip_kb_open_job* jobs, int count, void* 
     SUFHIP_REQUIRE(jb.a[0] && jb.a[1], "sufhip_kb_open_split_batch: null share a[0] or a[1]");
     SUFHIP_REQUIRE((jb.b[0] == nullptr) == (jb.b[1] == nullptr),
                    "sufhip_kb_open_split_batch: give both shares of b or neither");
+    SUFHIP_REQUIRE(jb.a_stride[0] >= 0 && jb.a_stride[1] >= 0 && jb.a_stride[2] >= 0,
+                   "sufhip_kb_open_split_batch: a_stride entries must be >= 0");
     a.src[j] = jb.a[0];
     a.add[j] = jb.a[1];
     a.sub[j][0] = jb.b[0];
     a.sub[j][1] = jb.b[1];
+    for (int t = 0; t < 3; ++t) a.view[j][t] = size_t(jb.a_stride[t]);
     if (int rc = split_job(a, j, jb.planes, jb.batches, jb.rows, jb.cols, jb.k_is_col,
                            jb.planes_a0, jb.a0, "sufhip_kb_open_split_batch"))
       return rc;

@@ -117,19 +117,30 @@ def kb_split(jobs):
 
 def kb_open_split(jobs):
     """Masked opens written straight as digit planes, up to 8 in one launch:
-    jobs of (a, b, planes, batches, rows, cols, k_is_col[, planes_a0, a0])
-    with a and b pairs of share arrays (b may be None); element i is
-    a0 + a1 - b0 - b1, and with the last two also its + a0[i] planes."""
+    jobs of (a, b, planes, batches, rows, cols, k_is_col[, planes_a0, a0[,
+    view]]) with a and b pairs of share arrays (b may be None); element i is
+    a0 + a1 - b0 - b1, and with planes_a0 and a0 (either may be None) also
+    its + a0[i] planes.  view = (offset, batch, row, col strides) in words:
+    element (batch, row, col) of a[p] is a[p][offset + strides . index]."""
     arr = (native.KbOpenJob * len(jobs))()
     for i, jb in enumerate(jobs):
         a, b, planes, nb, r, c, kc = jb[:7]
-        arr[i].a[0], arr[i].a[1] = ptr(a[0]), ptr(a[1])
+        view = jb[9] if len(jb) > 9 else None
+        off = 0
+        if view is not None:
+            off, sb, sr, sc = view
+            last = off + (nb - 1) * sb + (r - 1) * sr + (c - 1) * sc  # the view's last element
+            if min(sb, sr, sc, off) < 0 or min(a[0].numel(), a[1].numel()) <= last:
+                raise ValueError("kb_open_split: the view runs outside a[p]")
+        arr[i].a[0], arr[i].a[1] = ptr(a[0]) + 8 * off, ptr(a[1]) + 8 * off
         if b is not None:
             arr[i].b[0], arr[i].b[1] = ptr(b[0]), ptr(b[1])
         arr[i].planes = ptr(planes)
         arr[i].batches, arr[i].rows, arr[i].cols, arr[i].k_is_col = nb, r, c, int(kc)
-        if len(jb) > 7:
+        if len(jb) > 7 and jb[7] is not None:
             arr[i].planes_a0, arr[i].a0 = ptr(jb[7]), ptr(jb[8])
+        if len(jb) > 9 and jb[9] is not None:
+            arr[i].a_stride[0], arr[i].a_stride[1], arr[i].a_stride[2] = jb[9][1:4]
     native.call("sufhip_kb_open_split_batch", arr, len(jobs), stream_ptr())
 
 
@@ -307,16 +318,20 @@ class AttentionCore:
         # D = open(Q_h - A), E = open(K_h^T - B), and already the second
         # product's E2 = open(V_h - B2), in one launch; then the per-head products.
         hsd = h * seq * dh
-        gq = operand(term(qkv, index=mp["gq"]), term(self.tri_qk.A, neg=True))
-        gk = operand(term(qkv, index=mp["gk"]), term(self.tri_qk.B, neg=True))
-        gv = operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True))
         if self.mfma():
-            # The three opens go straight to the products' digit planes.
-            lin2_batch([(gq, hsd, None, 0, self.tri_qk.d_planes()),
-                        (gk, hsd, None, 0, (self.tri_qk.Ep, h, dh, seq, 0)),
-                        (gv, hsd, None, 0, (self.tri_pv.Ep, h, seq, dh, 0))])
+            # The three opens go straight to the products' digit planes, each
+            # head's Q, K^T and V read through a strided view of the QKV rows
+            # (the index maps gq, gk, gv as strides), whole plane segments
+            # per lane.
+            tq, tp = self.tri_qk, self.tri_pv
+            kb_open_split([(qkv, tq.A, tq.Dp, h, seq, dh, 1, tq.Xp, tq.A[0], (0, dh, 3 * d, 1)),
+                           (qkv, tq.B, tq.Ep, h, dh, seq, 0, None, None, (d, dh, 1, 3 * d)),
+                           (qkv, tp.B, tp.Ep, h, seq, dh, 0, None, None, (2 * d, dh, 3 * d, 1))])
             _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S, split=False)
         else:
+            gq = operand(term(qkv, index=mp["gq"]), term(self.tri_qk.A, neg=True))
+            gk = operand(term(qkv, index=mp["gk"]), term(self.tri_qk.B, neg=True))
+            gv = operand(term(qkv, index=mp["gv"]), term(self.tri_pv.B, neg=True))
             lin2_batch([(gq, hsd, self.D, 0), (gk, hsd, self.E, 0), (gv, hsd, self.E2, 0)])
             _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S)
         prep[0].wait(prep[1])

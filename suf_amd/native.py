@@ -242,7 +242,7 @@ class KbOpenJob(ctypes.Structure):
     """sufhip_kb_open_job (include/suf_hip.h)."""
     _fields_ = [("a", c_vp * 2), ("b", c_vp * 2), ("planes", c_vp), ("batches", c_int),
                 ("rows", c_int), ("cols", c_int), ("k_is_col", c_int), ("planes_a0", c_vp),
-                ("a0", c_vp)]
+                ("a0", c_vp), ("a_stride", ctypes.c_int64 * 3)]
 
 
 class Triple2(ctypes.Structure):

@@ -438,10 +438,13 @@ def test_plane_outputs_reject_bad_layouts():
                     0, None, pm.work.data_ptr(), pm.work_bytes, 0)
 
 
-@pytest.mark.parametrize("shape", [(1, 64, 96, 1), (1, 96, 64, 0), (3, 32, 64, 0)])
+@pytest.mark.parametrize("shape", [(1, 64, 96, 1), (1, 96, 64, 0), (3, 32, 64, 0),
+                                   (1, 1024, 2048, 0)])
 def test_kb_open_split_matches_open_then_split(shape):
     """The open-and-split launch writes the same digit planes as the open
-    a0 + a1 - b0 - b1 in u64 followed by the split, with and without b."""
+    a0 + a1 - b0 - b1 in u64 followed by the split, with and without b.  The
+    last shape is large enough for 16 k per lane on the column side (the
+    others take 4)."""
     nb, r, c, kc = shape
     print("[gpu-case] kb_open_split", shape, flush=True)
     g = np.random.default_rng(7)
@@ -471,6 +474,46 @@ def test_kb_open_split_matches_open_then_split(shape):
         arr[0].batches, arr[0].rows, arr[0].cols, arr[0].k_is_col = nb, r, c, kc
         with pytest.raises(native.SufHipError, match="both shares of b"):
             native.call("sufhip_kb_open_split_batch", arr, 1, 0)
+
+
+@pytest.mark.parametrize("seq,d,heads", [(64, 128, 2), (128, 768, 12)])
+def test_kb_open_split_strided_views_match_gathers(seq, d, heads):
+    """The attention's three opens read through strided views of the QKV rows
+    (Q_h - A with the planes of + A_0, K_h^T - B, V_h - B2) write the same
+    planes as the opens of the index-map gathers (attention_maps) split
+    plainly, in one launch."""
+    print("[gpu-case] kb_open_split strided views", seq, d, heads, flush=True)
+    dh = d // heads
+    g = np.random.default_rng(9)
+    qkv = tuple(dev(g.integers(0, 2**64, seq * 3 * d, dtype=np.uint64)) for _ in range(2))
+    A = tuple(dev(g.integers(0, 2**64, heads * seq * dh, dtype=np.uint64)) for _ in range(2))
+    B = tuple(dev(g.integers(0, 2**64, heads * dh * seq, dtype=np.uint64)) for _ in range(2))
+    B2 = tuple(dev(g.integers(0, 2**64, heads * seq * dh, dtype=np.uint64)) for _ in range(2))
+    mp = layer.attention_maps(seq, d, heads)
+    shapes = [(heads, seq, dh, 1), (heads, dh, seq, 0), (heads, seq, dh, 0)]
+    views = [(0, dh, 3 * d, 1), (d, dh, 1, 3 * d), (2 * d, dh, 3 * d, 1)]
+    subs = [A, B, B2]
+    got = [layer.kb_planes(*s[:3]) for s in shapes] + [layer.kb_planes(heads, seq, dh)]
+    want = [layer.kb_planes(*s[:3]) for s in shapes] + [layer.kb_planes(heads, seq, dh)]
+    for t in got:
+        t.fill_(0x5a5a)  # every planes byte must be written
+    jobs = []
+    for i, (s, v, b) in enumerate(zip(shapes, views, subs)):
+        extra = (got[3], A[0]) if i == 0 else (None, None)
+        jobs.append((qkv, b, got[i], *s, *extra, v))
+    layer.kb_open_split(jobs)
+    for i, (s, key, b) in enumerate(zip(shapes, ("gq", "gk", "gv"), subs)):
+        idx = torch.from_numpy(mp[key].astype(np.int64)).cuda()
+        gathered = tuple(qkv[p][idx].contiguous() for p in (0, 1))
+        extra = (want[3], A[0]) if i == 0 else ()
+        layer.kb_open_split([(gathered, b, want[i], *s, *extra)])
+    torch.cuda.synchronize()
+    for i, (nb, r, c) in enumerate([s[:3] for s in shapes] + [(heads, seq, dh)]):
+        nbytes = native.load().sufhip_kb_planes_bytes(nb, r, c)
+        assert torch.equal(got[i].view(torch.uint8)[:nbytes], want[i].view(torch.uint8)[:nbytes]), i
+    with pytest.raises(ValueError, match="outside"):  # the view's last element past qkv
+        layer.kb_open_split([(qkv, B2, got[2], heads, seq, dh, 0, None, None,
+                              (2 * d + 1, dh, 3 * d, 1))])
 
 
 def test_kb_open_split_two_jobs_mixed():
