@@ -187,25 +187,35 @@ __device__ __forceinline__ void bm2_store(const Bm2Args& a, int p, int l, int m0
 
 // With the truncation epilogue: both parties' tiles are in LDS (both[p]);
 // wave p opens rows r in [8p, 8p + 8) and writes both parties' outputs.
-__device__ __forceinline__ void bm2_trunc_rows(const Bm2Args& a, int p, int l, int m0, int n0,
-                                               size_t b, const uint64_t (*both)[16][64]) {
+// eh: the gate's key headers, read before the kernel's first global store;
+// every table read is issued before the first output store.
+__device__ __forceinline__ void bm2_trunc_rows(const Bm2Args& a, const EpiHdrs& eh, int p, int l,
+                                               int m0, int n0, size_t b,
+                                               const uint64_t (*both)[16][64]) {
   const int M = a.M, N = a.N;
   const int col = n0 + (l & 31);
   const size_t ob = b * size_t(M) * N;
   const size_t ld = size_t(a.batches) * N;
+  uint64_t open[8], w[8][2];
+  size_t o[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     const int r = 8 * p + q;
     const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-    const size_t o = a.merge ? size_t(row) * ld + b * N + col : ob + size_t(row) * N + col;
-    const uint64_t open = both[0][r][l] + both[1][r][l] + a.mask;
-    const uint64_t y0 = trunc_table_eval(a.epi.key[0], a.epi.table[0], a.epi.f, open);
-    const uint64_t y1 = trunc_table_eval(a.epi.key[1], a.epi.table[1], a.epi.f, open);
-    a.epi.y[0][o] = y0;
-    a.epi.y[1][o] = y1;
+    o[q] = a.merge ? size_t(row) * ld + b * N + col : ob + size_t(row) * N + col;
+    open[q] = both[0][r][l] + both[1][r][l] + a.mask;
+    w[q][0] = trunc_table_word(eh.h[0], a.epi.table[0], a.epi.f, open[q]);
+    w[q][1] = trunc_table_word(eh.h[1], a.epi.table[1], a.epi.f, open[q]);
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint64_t y0 = trunc_table_out(eh.h[0], a.epi.f, open[q], w[q][0]);
+    const uint64_t y1 = trunc_table_out(eh.h[1], a.epi.f, open[q], w[q][1]);
+    a.epi.y[0][o[q]] = y0;
+    a.epi.y[1][o[q]] = y1;
     if (a.xp.planes) {
-      put_x_digits(a.xp, size_t(M), o, 0, y0);
-      put_x_digits(a.xp, size_t(M), o, 1, y1);
+      put_x_digits(a.xp, size_t(M), o[q], 0, y0);
+      put_x_digits(a.xp, size_t(M), o[q], 1, y1);
     }
   }
 }
@@ -261,6 +271,7 @@ __global__ void __launch_bounds__(128 * kKWaves) beaver_mfma2_kernel(Bm2Args a) 
       for (int j = 0; i + j < kDigitPlanes; ++j)
         acc[i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x[i], e[j], acc[i + j], 0, 0, 0);
   }
+  const EpiHdrs eh = epi_hdrs(a.epi);
   uint64_t v[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -300,7 +311,7 @@ __global__ void __launch_bounds__(128 * kKWaves) beaver_mfma2_kernel(Bm2Args a) 
     for (int r = 0; r < 16; ++r) both[p][r][l] = v[r];
   }
   __syncthreads();
-  if (kw == 0) bm2_trunc_rows(a, p, l, m0, n0, b, both);
+  if (kw == 0) bm2_trunc_rows(a, eh, p, l, m0, n0, b, both);
 }
 
 // Balanced form (Xp given): wave p computes party p's tile over every
@@ -369,6 +380,7 @@ __global__ void __launch_bounds__(128, 1) beaver_bal_kernel(Bm2Args a) {
       }
     }
   }
+  const EpiHdrs eh = epi_hdrs(a.epi);
   uint64_t v[16];
   const int col = n0 + (l & 31);
   const size_t ob = b * size_t(M) * N;
@@ -387,7 +399,7 @@ __global__ void __launch_bounds__(128, 1) beaver_bal_kernel(Bm2Args a) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) both[p][r][l] = v[r];
   __syncthreads();
-  bm2_trunc_rows(a, p, l, m0, n0, b, both);
+  bm2_trunc_rows(a, eh, p, l, m0, n0, b, both);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }

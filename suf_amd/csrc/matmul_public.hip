@@ -182,6 +182,7 @@ public_mfma_kernel(PubArgs a) {
 #pragma unroll
   for (int h = 0; h < S - 1; ++h)
     if (h < rest) mfmas(h);
+  const EpiHdrs eh = epi_hdrs(a.epi);  // before the first global store
   const int col = n0 + (l & 31);
   uint64_t v[16];
 #pragma unroll
@@ -213,9 +214,17 @@ public_mfma_kernel(PubArgs a) {
     __syncthreads();
     if (p == 0) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-        put_open(a.epi, a.zhat, size_t(row) * N + col, v[r] + other[r][l] + a.mask);
+      for (int h = 0; h < 2; ++h) {
+        size_t ii[8];
+        uint64_t vv[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int r = 8 * h + q;
+          const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+          ii[q] = size_t(row) * N + col;
+          vv[q] = v[r] + other[r][l] + a.mask;
+        }
+        put_open_n<8>(a.epi, eh, a.zhat, ii, vv);
       }
     }
   }
@@ -379,6 +388,7 @@ __global__ void __launch_bounds__(256, 1) public_lds_kernel(PubArgs a) {
     stage = stage + 1 == kPubStages ? 0 : stage + 1;
   }
   __builtin_amdgcn_s_waitcnt(vm_wait_imm<0>());  // no DMA may land after the ring is reused
+  const EpiHdrs eh = epi_hdrs(a.epi);  // before the first global store
   const int col = n0 + 32 * c + (l & 31);
   uint64_t v[16];
 #pragma unroll
@@ -410,12 +420,16 @@ __global__ void __launch_bounds__(256, 1) public_lds_kernel(PubArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) both[c][p][r][l] = v[r];
     __syncthreads();
+    size_t ii[8];
+    uint64_t vv[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int r = 8 * p + q;
       const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-      put_open(a.epi, a.zhat, size_t(row) * N + col, both[c][0][r][l] + both[c][1][r][l] + a.mask);
+      ii[q] = size_t(row) * N + col;
+      vv[q] = both[c][0][r][l] + both[c][1][r][l] + a.mask;
     }
+    put_open_n<8>(a.epi, eh, a.zhat, ii, vv);
   }
 }
 
@@ -435,6 +449,7 @@ size_t public_lds_bytes() {
 __global__ void __launch_bounds__(256)
     public_reduce_kernel(const uint64_t* part, int slices, size_t mn, uint64_t* out0,
                          uint64_t* out1, uint64_t* zhat, uint64_t mask, TruncEpi epi) {
+  const EpiHdrs eh = epi_hdrs(epi);
   for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < mn; i += size_t(gridDim.x) * 256) {
     uint64_t v0 = 0, v1 = 0;
     for (int z = 0; z < slices; ++z) {
@@ -443,7 +458,7 @@ __global__ void __launch_bounds__(256)
     }
     if (out0) out0[i] = v0;
     if (out1) out1[i] = v1;
-    put_open(epi, zhat, i, v0 + v1 + mask);
+    put_open(epi, eh, zhat, i, v0 + v1 + mask);
   }
 }
 

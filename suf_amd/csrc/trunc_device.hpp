@@ -119,21 +119,73 @@ struct TruncEpi {
   int on;
 };
 
-// Writes the open value v of element i: the gate's two output shares (plus
-// the addend) when the epilogue is on, else the open itself (if requested).
-__device__ __forceinline__ void put_open(const TruncEpi& e, uint64_t* hat, size_t i, uint64_t v) {
+// trunc_table_eval_h in two halves, so that a caller can issue several
+// elements' table reads before it uses any: the table's value word at xhat
+// (0 where the gate reads none), then the output from that word.
+__device__ __forceinline__ bool trunc_table_key_ok(const TruncHdr& h, int f) {
+  return h.tag == kTruncTag && h.kind == SUFHIP_TRUNC_GAPARS && int(h.f) == f;
+}
+__device__ __forceinline__ uint64_t trunc_table_word(const TruncHdr& h, const uint4* table, int f,
+                                                     uint64_t xhat) {
+  if (!trunc_table_key_ok(h, f) || !(h.flags & 1)) return 0;
+  const uint4 q = table[2 * (xhat & ((uint64_t(1) << f) - 1)) + 1];
+  return uint64_t(q.x) | uint64_t(q.y) << 32;
+}
+__device__ __forceinline__ uint64_t trunc_table_out(const TruncHdr& h, int f, uint64_t xhat,
+                                                    uint64_t word) {
+  if (!trunc_table_key_ok(h, f)) return 0;
+  const uint64_t carry = (h.flags & 1) ? trunc_carry_from(h, word) : 0;
+  return trunc_postproc<SUFHIP_TRUNC_GAPARS>(h, f, xhat, carry, 0, 0);
+}
+
+// The two parties' key headers of an epilogue, read once before the
+// caller's element loop.  Read inside it, each header load would follow the
+// previous element's output stores, which may alias the keys as far as the
+// compiler knows, so every element would wait for two fresh header loads.
+struct EpiHdrs {
+  TruncHdr h[2];
+};
+__device__ __forceinline__ EpiHdrs epi_hdrs(const TruncEpi& e) {
+  EpiHdrs r{};
   if (e.on) {
-    uint64_t y0 = trunc_table_eval(e.key[0], e.table[0], e.f, v);
-    uint64_t y1 = trunc_table_eval(e.key[1], e.table[1], e.f, v);
-    if (e.add[0]) {
-      y0 += e.add[0][i];
-      y1 += e.add[1][i];
-    }
-    e.y[0][i] = y0;
-    e.y[1][i] = y1;
-  } else if (hat) {
-    hat[i] = v;
+    r.h[0] = read_trunc_hdr(e.key[0]);
+    r.h[1] = read_trunc_hdr(e.key[1]);
   }
+  return r;
+}
+
+// Writes the open values v[t] of elements i[t], t < N: the gate's two
+// output shares (plus the addend) when the epilogue is on, else the opens
+// themselves (if requested).  Every table and addend read is issued before
+// the first output store.
+template <int N>
+__device__ __forceinline__ void put_open_n(const TruncEpi& e, const EpiHdrs& eh, uint64_t* hat,
+                                           const size_t (&i)[N], const uint64_t (&v)[N]) {
+  if (e.on) {
+    uint64_t w[N][2], ad[N][2];
+#pragma unroll
+    for (int t = 0; t < N; ++t) {
+      w[t][0] = trunc_table_word(eh.h[0], e.table[0], e.f, v[t]);
+      w[t][1] = trunc_table_word(eh.h[1], e.table[1], e.f, v[t]);
+      ad[t][0] = e.add[0] ? e.add[0][i[t]] : 0;
+      ad[t][1] = e.add[0] ? e.add[1][i[t]] : 0;
+    }
+#pragma unroll
+    for (int t = 0; t < N; ++t) {
+      e.y[0][i[t]] = trunc_table_out(eh.h[0], e.f, v[t], w[t][0]) + ad[t][0];
+      e.y[1][i[t]] = trunc_table_out(eh.h[1], e.f, v[t], w[t][1]) + ad[t][1];
+    }
+  } else if (hat) {
+#pragma unroll
+    for (int t = 0; t < N; ++t) hat[i[t]] = v[t];
+  }
+}
+
+__device__ __forceinline__ void put_open(const TruncEpi& e, const EpiHdrs& eh, uint64_t* hat,
+                                         size_t i, uint64_t v) {
+  const size_t ii[1] = {i};
+  const uint64_t vv[1] = {v};
+  put_open_n<1>(e, eh, hat, ii, vv);
 }
 
 // Validates an epilogue for n elements and converts it (NULL -> off).

@@ -111,11 +111,12 @@ __global__ void __launch_bounds__(kBlock)
     lin2_kernel(sufhip_operand2 x, size_t n, uint64_t* out0, uint64_t* out1, uint64_t* xhat,
                 uint64_t mask, TruncEpi epi) {
   const size_t stride = size_t(gridDim.x) * kBlock;
+  const EpiHdrs eh = epi_hdrs(epi);
   for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
     const uint64_t x0 = operand_at(x, 0, i), x1 = operand_at(x, 1, i);
     if (out0) out0[i] = x0;
     if (out1) out1[i] = x1;
-    put_open(epi, xhat, i, x0 + x1 + mask);
+    put_open(epi, eh, xhat, i, x0 + x1 + mask);
   }
 }
 
@@ -139,12 +140,13 @@ __global__ void __launch_bounds__(kBlock) lin2_batch_kernel(Lin2Batch b) {
   while (j + 1 < b.count && blockIdx.x >= b.begin[j + 1]) ++j;
   const unsigned groups = b.begin[j + 1] - b.begin[j];
   const size_t stride = size_t(groups) * kBlock;
+  const EpiHdrs eh = epi_hdrs(b.epi[j]);
   for (size_t i = size_t(blockIdx.x - b.begin[j]) * kBlock + threadIdx.x; i < b.n[j];
        i += stride) {
     const uint64_t x0 = operand_at(b.x[j], 0, i), x1 = operand_at(b.x[j], 1, i);
     if (b.out[j][0]) b.out[j][0][i] = x0;
     if (b.out[j][1]) b.out[j][1][i] = x1;
-    put_open(b.epi[j], b.xhat[j], i, x0 + x1 + b.mask[j]);
+    put_open(b.epi[j], eh, b.xhat[j], i, x0 + x1 + b.mask[j]);
     if (b.kb[j].planes) put_kb_digits(b.kb[j], i, x0 + x1 + b.mask[j]);
   }
 }
@@ -164,7 +166,9 @@ __global__ void __launch_bounds__(kBlock) mul2x_kernel(sufhip_mul2x_args a, size
     const uint64_t z0 = c0 + d * b0 + e * a0 + d * e + operand_at(a.z_add, 0, i);
     const uint64_t z1 = c1 + d * b1 + e * a1 + operand_at(a.z_add, 1, i);
     if (open) {
-      put_open(epi, a.zhat, i, z0 + z1 + a.open_mask);
+      // Headers read per element: hoisted, they would join the operands'
+      // wave-uniform registers and spill them.
+      put_open(epi, epi_hdrs(epi), a.zhat, i, z0 + z1 + a.open_mask);
     } else {
       a.z[0][i] = z0;
       a.z[1][i] = z1;
@@ -178,6 +182,7 @@ __global__ void __launch_bounds__(kBlock)
                     uint64_t mul_const, uint64_t* sum0, uint64_t* sum1, uint64_t* hat,
                     uint64_t mask, TruncEpi epi) {
   const int lane = threadIdx.x & 63;
+  const EpiHdrs eh = epi_hdrs(epi);
   for (int r = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6); r < rows;
        r += gridDim.x * (kBlock / 64)) {
     const size_t b = offs ? size_t(offs[r]) : size_t(r) * size_t(cols);
@@ -192,7 +197,7 @@ __global__ void __launch_bounds__(kBlock)
     if (lane == 0) {
       if (sum0) sum0[r] = s0;
       if (sum1) sum1[r] = s1;
-      put_open(epi, hat, size_t(r), s0 + s1 + mask);
+      put_open(epi, eh, hat, size_t(r), s0 + s1 + mask);
     }
   }
 }
