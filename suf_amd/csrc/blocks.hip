@@ -49,7 +49,9 @@ template <int kPer>
 __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
   __shared__ __align__(16) uint32_t tab[256 * kLnCopies];
   __shared__ ChainLds L;
+  constexpr int kRsProds = chain_products<SUFHIP_CHAIN_RSQRT>();
   __shared__ TruncHdr th[4][2];
+  __shared__ TruncHdr rth[kRsProds][2];  // the rsqrt chain's truncation key headers
   __shared__ uint64_t red[2][kLnWaves];
   __shared__ uint64_t bc[2];
   __shared__ ChainPre pre;
@@ -57,6 +59,11 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
   chain_stage(A.rs, 2, L);
   if (threadIdx.x < 8) th[threadIdx.x >> 1][threadIdx.x & 1] =
       read_trunc_hdr(A.tr[threadIdx.x >> 1].key[threadIdx.x & 1]);
+  {
+    TruncHdrStager<kRsProds> hs;
+    hs.load(A.rs, 64);
+    hs.store(rth);
+  }
   __syncthreads();
   chain_compare(A.rs, L);
   __syncthreads();
@@ -133,7 +140,7 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
     if (threadIdx.x < 64) {
       const Two v{{var.v[0] + A.eps, var.v[1]}};
       const Two rs =
-          chain_eval_quad<SUFHIP_CHAIN_RSQRT, LnAes>(A.rs, L, K, aes, size_t(r), v, pre);
+          chain_eval_quad<SUFHIP_CHAIN_RSQRT, LnAes>(A.rs, L, K, aes, size_t(r), v, pre, rth);
       if (threadIdx.x == 0) {
         bc[0] = rs.v[0];
         bc[1] = rs.v[1];

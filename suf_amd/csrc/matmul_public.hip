@@ -321,6 +321,8 @@ __device__ __forceinline__ void rd_frags<4>(v4i (&x)[kPlanes], v4i (&w)[4], uint
 template <int J>
 __global__ void __launch_bounds__(256, 1) public_lds_kernel(PubArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  // The truncation's key headers (scalar loads) in flight during the k-loop.
+  const EpiHdrs eh = epi_hdrs(a.epi);
   constexpr int kBlocks = stage_blocks<J>();
   constexpr int kPerWave = kBlocks / 4;
   constexpr int kStageBytes = kBlocks * 1024;
@@ -388,7 +390,6 @@ __global__ void __launch_bounds__(256, 1) public_lds_kernel(PubArgs a) {
     stage = stage + 1 == kPubStages ? 0 : stage + 1;
   }
   __builtin_amdgcn_s_waitcnt(vm_wait_imm<0>());  // no DMA may land after the ring is reused
-  const EpiHdrs eh = epi_hdrs(a.epi);  // before the first global store
   const int col = n0 + 32 * c + (l & 31);
   uint64_t v[16];
 #pragma unroll
