@@ -281,39 +281,56 @@ constexpr int stage_blocks() {
   "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]), "=&v"(x[6]), \
       "=&v"(x[7])
 
-// x: the 8 X fragments at ax (1 KB apart); w: the J W fragments at aw.
+// x: the 8 X fragments at ax (1 KB apart); w: the J W fragments at aw.  The
+// reads are issued without a wait: wait_frags() completes them.
 template <int J>
 __device__ __forceinline__ void rd_frags(v4i (&x)[kPlanes], v4i (&w)[J], uint32_t ax, uint32_t aw);
 template <>
 __device__ __forceinline__ void rd_frags<1>(v4i (&x)[kPlanes], v4i (&w)[1], uint32_t ax,
                                             uint32_t aw) {
-  asm volatile(SUFHIP_RD_X8(9) SUFHIP_RD(8, 10, 0) "s_waitcnt lgkmcnt(0)"
-               : SUFHIP_XOUT, "=&v"(w[0])
-               : "v"(ax), "v"(aw));
+  asm volatile(SUFHIP_RD_X8(9) SUFHIP_RD(8, 10, 0) : SUFHIP_XOUT, "=&v"(w[0]) : "v"(ax), "v"(aw));
 }
 template <>
 __device__ __forceinline__ void rd_frags<2>(v4i (&x)[kPlanes], v4i (&w)[2], uint32_t ax,
                                             uint32_t aw) {
-  asm volatile(SUFHIP_RD_X8(10) SUFHIP_RD(8, 11, 0) SUFHIP_RD(9, 11, 1024) "s_waitcnt lgkmcnt(0)"
+  asm volatile(SUFHIP_RD_X8(10) SUFHIP_RD(8, 11, 0) SUFHIP_RD(9, 11, 1024)
                : SUFHIP_XOUT, "=&v"(w[0]), "=&v"(w[1])
                : "v"(ax), "v"(aw));
 }
 template <>
 __device__ __forceinline__ void rd_frags<3>(v4i (&x)[kPlanes], v4i (&w)[3], uint32_t ax,
                                             uint32_t aw) {
-  asm volatile(SUFHIP_RD_X8(11) SUFHIP_RD(8, 12, 0) SUFHIP_RD(9, 12, 1024)
-                   SUFHIP_RD(10, 12, 2048) "s_waitcnt lgkmcnt(0)"
+  asm volatile(SUFHIP_RD_X8(11) SUFHIP_RD(8, 12, 0) SUFHIP_RD(9, 12, 1024) SUFHIP_RD(10, 12, 2048)
                : SUFHIP_XOUT, "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2])
                : "v"(ax), "v"(aw));
 }
 template <>
 __device__ __forceinline__ void rd_frags<4>(v4i (&x)[kPlanes], v4i (&w)[4], uint32_t ax,
                                             uint32_t aw) {
-  asm volatile(SUFHIP_RD_X8(12) SUFHIP_RD(8, 13, 0) SUFHIP_RD(9, 13, 1024)
-                   SUFHIP_RD(10, 13, 2048) SUFHIP_RD(11, 13, 3072) "s_waitcnt lgkmcnt(0)"
+  asm volatile(SUFHIP_RD_X8(12) SUFHIP_RD(8, 13, 0) SUFHIP_RD(9, 13, 1024) SUFHIP_RD(10, 13, 2048)
+                   SUFHIP_RD(11, 13, 3072)
                : SUFHIP_XOUT, "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
                : "v"(ax), "v"(aw));
 }
+
+// Waits for rd_frags' reads.  The fragments are in-out operands, so that no
+// use of them can be scheduled above the wait.
+#define SUFHIP_XIO                                                                           \
+  "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), \
+      "+v"(x[7])
+template <int J>
+__device__ __forceinline__ void wait_frags(v4i (&x)[kPlanes], v4i (&w)[J]) {
+  if constexpr (J == 1)
+    asm volatile("s_waitcnt lgkmcnt(0)" : SUFHIP_XIO, "+v"(w[0]));
+  else if constexpr (J == 2)
+    asm volatile("s_waitcnt lgkmcnt(0)" : SUFHIP_XIO, "+v"(w[0]), "+v"(w[1]));
+  else if constexpr (J == 3)
+    asm volatile("s_waitcnt lgkmcnt(0)" : SUFHIP_XIO, "+v"(w[0]), "+v"(w[1]), "+v"(w[2]));
+  else
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : SUFHIP_XIO, "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]));
+}
+#undef SUFHIP_XIO
 #undef SUFHIP_RD
 #undef SUFHIP_RD_X8
 #undef SUFHIP_XOUT
@@ -370,25 +387,58 @@ __global__ void __launch_bounds__(256, 1) public_lds_kernel(PubArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[s][r] = 0;
   const int n = s_end - s_begin;
-#pragma unroll
-  for (int q = 0; q < kPubStages - 1; ++q) dma(q, s_begin + q);
   const uint32_t lane_base = lds_addr(lds) + 16 * uint32_t(l);
   const uint32_t xoff = uint32_t(8 * p) * 1024, woff = uint32_t(16 + c * J) * 1024;
-  int stage = 0;
-  for (int t = 0; t < n; ++t) {
-    __builtin_amdgcn_s_waitcnt(vm_wait_imm<(kPubStages - 2) * kPerWave>());
-    __builtin_amdgcn_s_barrier();
-    dma(stage == 0 ? kPubStages - 1 : stage - 1, s_begin + t + kPubStages - 1);
+  auto frags = [&](int stage, v4i (&x)[kPlanes], v4i (&wf)[J]) {
     const uint32_t sb = lane_base + uint32_t(stage) * kStageBytes;
-    v4i x[kPlanes], wf[J];
     rd_frags<J>(x, wf, sb + xoff, sb + woff);
+    // The MFMAs that follow stay below the reads (issued after the last
+    // MFMA, the reads would wait for the whole step's MFMA issue).
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto mfmas = [&](const v4i (&x)[kPlanes], const v4i (&wf)[J]) {
 #pragma unroll
     for (int j = 0; j < J; ++j)
 #pragma unroll
       for (int i = 0; i + j < kPlanes; ++i)
         acc[i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x[i], wf[j], acc[i + j], 0, 0, 0);
-    stage = stage + 1 == kPubStages ? 0 : stage + 1;
+    // ... and above the wait for the next step's reads.
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Every stage filled (steps 0 .. kPubStages - 1), step 0's fragments read.
+  // Then step t: wait for step t + 1's blocks (this wave's DMAs, then the
+  // barrier for everyone's, which also says that every wave has read step
+  // t's stage), refill step t's stage with step t + kPubStages, read step
+  // t + 1's fragments into the other register set, and run step t's MFMAs
+  // while those reads are in flight.  Reads of a step past the slice see a
+  // stage holding its last step again (never used).
+#pragma unroll
+  for (int q = 0; q < kPubStages; ++q) dma(q, s_begin + q);
+  v4i xa[kPlanes], wa[J], xb[kPlanes], wb[J];
+  __builtin_amdgcn_s_waitcnt(vm_wait_imm<(kPubStages - 1) * kPerWave>());
+  __builtin_amdgcn_s_barrier();
+  frags(0, xa, wa);
+  wait_frags<J>(xa, wa);
+  int stage = 0;  // step t's stage
+  int t = 0;
+  for (; t + 1 < n; t += 2) {  // steps t (in xa) and t + 1 (in xb)
+    const int s1 = stage + 1 == kPubStages ? 0 : stage + 1;
+    const int s2 = s1 + 1 == kPubStages ? 0 : s1 + 1;
+    __builtin_amdgcn_s_waitcnt(vm_wait_imm<(kPubStages - 2) * kPerWave>());
+    __builtin_amdgcn_s_barrier();
+    dma(stage, s_begin + t + kPubStages);
+    frags(s1, xb, wb);
+    mfmas(xa, wa);
+    wait_frags<J>(xb, wb);
+    __builtin_amdgcn_s_waitcnt(vm_wait_imm<(kPubStages - 2) * kPerWave>());
+    __builtin_amdgcn_s_barrier();
+    dma(s1, s_begin + t + 1 + kPubStages);
+    frags(s2, xa, wa);
+    mfmas(xb, wb);
+    wait_frags<J>(xa, wa);
+    stage = s2;
   }
+  if (t < n) mfmas(xa, wa);  // an odd last step, already in xa
   __builtin_amdgcn_s_waitcnt(vm_wait_imm<0>());  // no DMA may land after the ring is reused
   const int col = n0 + 32 * c + (l & 31);
   uint64_t v[16];
