@@ -321,9 +321,11 @@ __global__ void __launch_bounds__(128 * kKWaves) beaver_mfma2_kernel(Bm2Args a) 
 // kStages deep (a pair's planes are loaded kStages - 1 pairs before its
 // MFMAs), which keeps loads in flight while the wave -- the only one on its
 // SIMD -- multiplies.  Bases are wave-uniform (scalar registers) plus each
-// lane's 32-bit fragment offset.
-constexpr int kStages = 4;
-
+// lane's 32-bit fragment offset.  kPrefC (short K, three stages): the
+// wave's 16 C_p words are loaded with the first operand pairs, so the tile
+// needs no memory round trip after the k-loop (four stages leave no
+// registers for them).
+template <int kStages, bool kPrefC>
 __global__ void __launch_bounds__(128, 1) beaver_bal_kernel(Bm2Args a) {
   __shared__ uint64_t both[2][16][64];
   const int l = threadIdx.x & 63;
@@ -341,6 +343,14 @@ __global__ void __launch_bounds__(128, 1) beaver_bal_kernel(Bm2Args a) {
   const int8_t* Ld = a.D + lb0;
   const int8_t* Re = a.E + rb0;
   const int8_t* Rb = (p == 0 ? a.B[0] : a.B[1]) + rb0;
+  const int col = n0 + (l & 31);
+  const size_t ob = b * size_t(M) * N;
+  uint64_t cpre[16];
+  if constexpr (kPrefC) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      cpre[r] = a.C[p][ob + size_t(m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3)) * N + col];
+  }
   v16i acc[kDigitPlanes];
 #pragma unroll
   for (int s = 0; s < kDigitPlanes; ++s)
@@ -382,15 +392,13 @@ __global__ void __launch_bounds__(128, 1) beaver_bal_kernel(Bm2Args a) {
   }
   const EpiHdrs eh = epi_hdrs(a.epi);
   uint64_t v[16];
-  const int col = n0 + (l & 31);
-  const size_t ob = b * size_t(M) * N;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     v[r] = 0;
 #pragma unroll
     for (int s = 0; s < kDigitPlanes; ++s) v[r] += uint64_t(int64_t(acc[s][r])) << (8 * s);
     const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-    v[r] += a.C[p][ob + size_t(row) * N + col];
+    v[r] += kPrefC ? cpre[r] : a.C[p][ob + size_t(row) * N + col];
   }
   if (!a.epi.on) {
     bm2_store(a, p, l, m0, n0, b, v);
@@ -542,7 +550,10 @@ int sufhip_beaver_matmul2_mfma_ex(const sufhip_beaver_mfma2_args* args, void* st
   const uint64_t plane_set = uint64_t(kDigitPlanes) * uint64_t(g.batches) * uint64_t(g.K) *
                              uint64_t(g.M > g.N ? g.M : g.N);
   if (g.Xp && plane_set < (uint64_t(1) << 32)) {
-    hipLaunchKernelGGL(beaver_bal_kernel, grid, dim3(128), 0, as_stream(stream), a);
+    if (g.K <= 128)  // at most 8 operand pairs
+      hipLaunchKernelGGL((beaver_bal_kernel<3, true>), grid, dim3(128), 0, as_stream(stream), a);
+    else
+      hipLaunchKernelGGL((beaver_bal_kernel<4, false>), grid, dim3(128), 0, as_stream(stream), a);
     return check_launch("beaver_bal_kernel");
   }
   const int steps = g.K / 32;
