@@ -80,8 +80,8 @@ __device__ __forceinline__ size_t view_index(const SplitArgs& a, int j, size_t b
 template <int kN>
 __device__ __forceinline__ void write_k(int8_t* planes, size_t plane, size_t off,
                                         const uint64_t (&v)[kN]) {
-  static_assert(kN == 4 || kN == 16, "4 or 16 k per store");
-  uint32_t pk[kDigitPlanes][kN / 4] = {};
+  static_assert(kN == 1 || kN == 2 || kN == 4 || kN == 16, "1, 2, 4 or 16 k per store");
+  uint32_t pk[kDigitPlanes][(kN + 3) / 4] = {};
 #pragma unroll
   for (int t = 0; t < kN; ++t) {
     uint32_t d[kDigitPlanes];
@@ -91,7 +91,11 @@ __device__ __forceinline__ void write_k(int8_t* planes, size_t plane, size_t off
   }
 #pragma unroll
   for (int i = 0; i < kDigitPlanes; ++i) {
-    if constexpr (kN == 4)
+    if constexpr (kN == 1)
+      planes[i * plane + off] = int8_t(pk[i][0]);
+    else if constexpr (kN == 2)
+      *reinterpret_cast<uint16_t*>(planes + i * plane + off) = uint16_t(pk[i][0]);
+    else if constexpr (kN == 4)
       *reinterpret_cast<uint32_t*>(planes + i * plane + off) = pk[i][0];
     else
       *reinterpret_cast<uint4*>(planes + i * plane + off) =
@@ -99,7 +103,7 @@ __device__ __forceinline__ void write_k(int8_t* planes, size_t plane, size_t off
   }
 }
 
-template <int kColK>
+template <int kColK, int kRowK>
 __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
   const size_t total = a.begin[a.count];
   for (size_t g = size_t(blockIdx.x) * 256 + threadIdx.x; g < total;
@@ -112,21 +116,21 @@ __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
     const int K = kc ? cols : rows, R = kc ? rows : cols;
     const size_t plane = size_t(a.batches[j]) * R * K;
     if (kc) {
-      const size_t per_batch = size_t(R) * (K / 4);
+      const size_t per_batch = size_t(R) * (K / kRowK);
       const size_t b = q / per_batch, rem = q % per_batch;
-      const int r = int(rem / (K / 4)), k = 4 * int(rem % (K / 4));
+      const int r = int(rem / (K / kRowK)), k = kRowK * int(rem % (K / kRowK));
       const size_t src = b * size_t(rows) * cols + size_t(r) * cols + k;
       const size_t off = b * size_t(R) * K + kblock_off(size_t(r), k, size_t(R));
       const size_t sv = view_index(a, j, b, size_t(r), size_t(k), src);
       const size_t cs = (a.view[j][0] | a.view[j][1] | a.view[j][2]) ? a.view[j][2] : 1;
-      uint64_t v[4];
+      uint64_t v[kRowK];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = split_val(a, j, src + t, sv + t * cs);
-      write_k<4>(a.planes[j], plane, off, v);
+      for (int t = 0; t < kRowK; ++t) v[t] = split_val(a, j, src + t, sv + t * cs);
+      write_k<kRowK>(a.planes[j], plane, off, v);
       if (a.planes_a0[j]) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) v[t] += a.a0[j][src + t];
-        write_k<4>(a.planes_a0[j], plane, off, v);
+        for (int t = 0; t < kRowK; ++t) v[t] += a.a0[j][src + t];
+        write_k<kRowK>(a.planes_a0[j], plane, off, v);
       }
     } else {
       constexpr int kSeg = 32 / kColK;  // lanes per 32-byte plane segment
@@ -455,18 +459,29 @@ int launch_split(SplitArgs& a, int count, void* stream) {
   size_t col16 = 0;
   for (int j = 0; j < count; ++j)
     if (!a.k_is_col[j]) col16 += size_t(a.batches[j]) * a.rows[j] * a.cols[j] / 16;
-  const int ck = col16 >= size_t(cus) * 4 * 64 * 2 ? 16 : 4;
+  const size_t two_waves = size_t(cus) * 4 * 64 * 2;
+  size_t n4 = 0;  // lanes at 4 k per lane
+  for (int j = 0; j < count; ++j) n4 += size_t(a.batches[j]) * a.rows[j] * a.cols[j] / 4;
+  // Launches of fewer than two waves per SIMD at 4 k per lane take 2 k per
+  // lane on both sides (twice the lanes, half the serial loads per lane).
+  const int ck = col16 >= two_waves ? 16 : (n4 < two_waves ? 1 : 4);
+  const int rk = ck == 1 ? 1 : 4;
   a.begin[0] = 0;
   for (int j = 0; j < count; ++j)
     a.begin[j + 1] = a.begin[j] + size_t(a.batches[j]) * a.rows[j] * a.cols[j] /
-                                      size_t(a.k_is_col[j] ? 4 : ck);
+                                      size_t(a.k_is_col[j] ? rk : ck);
   if (a.begin[count] == 0) return SUFHIP_OK;
   size_t g = (a.begin[count] + 255) / 256;
   if (g > 4096) g = 4096;
   if (ck == 16)
-    hipLaunchKernelGGL(kb_split_kernel<16>, dim3(unsigned(g)), dim3(256), 0, as_stream(stream), a);
+    hipLaunchKernelGGL((kb_split_kernel<16, 4>), dim3(unsigned(g)), dim3(256), 0,
+                       as_stream(stream), a);
+  else if (ck == 4)
+    hipLaunchKernelGGL((kb_split_kernel<4, 4>), dim3(unsigned(g)), dim3(256), 0,
+                       as_stream(stream), a);
   else
-    hipLaunchKernelGGL(kb_split_kernel<4>, dim3(unsigned(g)), dim3(256), 0, as_stream(stream), a);
+    hipLaunchKernelGGL((kb_split_kernel<1, 1>), dim3(unsigned(g)), dim3(256), 0,
+                       as_stream(stream), a);
   return check_launch("kb_split_kernel");
 }
 
