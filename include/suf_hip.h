@@ -812,6 +812,20 @@ typedef struct sufhip_kb_open_job {
   int64_t a_stride[3];
 } sufhip_kb_open_job;
 int sufhip_kb_open_split_batch(const sufhip_kb_open_job* jobs, int count, void* stream);
+/* sufhip_kb_open_split_prepare: sufhip_trunc_prepare_batch(prg_state, tjobs,
+ * tcount) followed by sufhip_kb_open_split_batch(jobs, count), with the same
+ * results, in one launch when every truncation job is a table gate
+ * (frac_bits <= 14) and at most 8 jobs whose walks cover at most three
+ * quarters of one full walk workgroup per CU: the walks' dependent levels then
+ * run beside the split's memory stream.  Other truncation jobs take
+ * sufhip_trunc_prepare_batch's own launches first.  The two calls it replaces
+ * stand for the Beaver matmul's materialize_open (src/nn/matmul_beaver.cpp:
+ * 34-53) and the key-dependent DCF evaluation of the truncation that follows
+ * it (include/gates/composite_fss.hpp:1508-1515); the reference issues them
+ * separately.  tcount = 0 is the open split alone. */
+int sufhip_kb_open_split_prepare(const sufhip_kb_open_job* jobs, int count,
+                                 const uint8_t* prg_state, const sufhip_trunc_job* tjobs,
+                                 int tcount, void* stream);
 int sufhip_beaver_matmul2_mfma_batched(const int8_t* d_Dp, const int8_t* d_Ep,
                                        const int8_t* d_Ap0, const int8_t* d_Ap1,
                                        const int8_t* d_Bp0, const int8_t* d_Bp1,

@@ -26,6 +26,7 @@
 #include "suf_hip.h"
 #include "sufhip_internal.hpp"
 #include "trunc_device.hpp"
+#include "walk_device.hpp"
 
 namespace sufhip {
 namespace {
@@ -103,11 +104,11 @@ __device__ __forceinline__ void write_k(int8_t* planes, size_t plane, size_t off
   }
 }
 
+// Lanes first, first + stride, ... of a split launch over `a`.
 template <int kColK, int kRowK>
-__global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
+__device__ __forceinline__ void split_lanes(const SplitArgs& a, size_t first, size_t stride) {
   const size_t total = a.begin[a.count];
-  for (size_t g = size_t(blockIdx.x) * 256 + threadIdx.x; g < total;
-       g += size_t(gridDim.x) * 256) {
+  for (size_t g = first; g < total; g += stride) {
     int j = 0;
     while (j + 1 < a.count && g >= a.begin[j + 1]) ++j;
     const size_t q = g - a.begin[j];
@@ -155,6 +156,48 @@ __global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
       }
     }
   }
+}
+
+template <int kColK, int kRowK>
+__global__ void __launch_bounds__(256) kb_split_kernel(SplitArgs a) {
+  split_lanes<kColK, kRowK>(a, size_t(blockIdx.x) * 256 + threadIdx.x, size_t(gridDim.x) * 256);
+}
+
+// The opens' digit planes and the key-only walks of truncation gates in one
+// launch: workgroups below walk_groups walk (a 16-copy T table in LDS, every
+// level walked, 8 lanes per walk, as trunc_batch_walk_kernel with no local
+// levels), the others split.  Neither role waits for the other, so the
+// walks' dependent levels run under the split's memory stream.
+constexpr int kFusedWalkJobs = 8;
+constexpr int kFusedCopies = 16;
+using FusedAes = AesLds<kFusedCopies>;
+
+struct SplitWalkArgs {
+  SplitArgs s;
+  WalkJobs<kFusedWalkJobs> w;
+  uint32_t walk_groups;
+};
+
+static_assert(sizeof(SplitWalkArgs) <= 4096, "kernel argument block must fit in 4 KB");
+
+template <int kColK, int kRowK>
+__global__ void __launch_bounds__(256) kb_split_walk_kernel(SplitWalkArgs a) {
+  __shared__ __align__(16) uint32_t tab[FusedAes::kWords];
+  __shared__ uint4 rkl[4 * 11];
+  if (blockIdx.x < a.walk_groups) {
+    fill_ttable<kFusedCopies>(tab, kTDev.v);
+    fill_round_keys(rkl, a.w.prg.rk, 4);
+    __syncthreads();
+    const FusedAes aes{tab, threadIdx.x % kFusedCopies};
+    const uint32_t gl = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t g = gl >> 3;  // walk; whole 8-lane groups leave together
+    if (g >= a.w.begin[a.w.count]) return;
+    const int j = batch_job<kFusedWalkJobs>(a.w.begin, a.w.count, g);
+    walk_leaf_path(aes, rkl, a.w.key[j], a.w.out[j], a.w.geo[j], g - a.w.begin[j], gl);
+    return;
+  }
+  split_lanes<kColK, kRowK>(a.s, size_t(blockIdx.x - a.walk_groups) * 256 + threadIdx.x,
+                            size_t(gridDim.x - a.walk_groups) * 256);
 }
 
 struct Bm2Args {
@@ -448,9 +491,38 @@ int split_job(SplitArgs& a, int j, int8_t* planes, int batches, int rows, int co
   return SUFHIP_OK;
 }
 
+// SplitArgs of sufhip_kb_open_split_batch's jobs.
+int open_split_args(const sufhip_kb_open_job* jobs, int count, SplitArgs& a, const char* what) {
+  auto fail = [&](const char* msg) {
+    set_error(std::string(what) + ": " + msg);
+    return SUFHIP_ERR_INVALID;
+  };
+  if (count < 0 || count > kSplitJobs || (count > 0 && !jobs))
+    return fail("0..SUFHIP_KB_SPLIT_JOBS jobs");
+  for (int j = 0; j < count; ++j) {
+    const sufhip_kb_open_job& jb = jobs[j];
+    if (!jb.a[0] || !jb.a[1]) return fail("null share a[0] or a[1]");
+    if ((jb.b[0] == nullptr) != (jb.b[1] == nullptr)) return fail("give both shares of b or neither");
+    if (jb.a_stride[0] < 0 || jb.a_stride[1] < 0 || jb.a_stride[2] < 0)
+      return fail("a_stride entries must be >= 0");
+    a.src[j] = jb.a[0];
+    a.add[j] = jb.a[1];
+    a.sub[j][0] = jb.b[0];
+    a.sub[j][1] = jb.b[1];
+    for (int t = 0; t < 3; ++t) a.view[j][t] = size_t(jb.a_stride[t]);
+    if (int rc = split_job(a, j, jb.planes, jb.batches, jb.rows, jb.cols, jb.k_is_col,
+                           jb.planes_a0, jb.a0, what))
+      return rc;
+  }
+  return SUFHIP_OK;
+}
+
 // Column-side jobs take 16 k per lane when that still gives two waves per
-// SIMD, else 4 (more lanes, shorter per-lane chains).
-int launch_split(SplitArgs& a, int count, void* stream) {
+// SIMD, else 4 (more lanes, shorter per-lane chains); launches of fewer than
+// two waves per SIMD at 4 k per lane take one k per lane on both sides (the
+// most lanes, no serial loads per lane).  Sets a.count and a.begin; *ck and
+// *rk: k per lane on the column and row side.
+void plan_split(SplitArgs& a, int count, int* ck, int* rk) {
   a.count = count;
   int cus = 256;
   int dev = 0;
@@ -462,14 +534,17 @@ int launch_split(SplitArgs& a, int count, void* stream) {
   const size_t two_waves = size_t(cus) * 4 * 64 * 2;
   size_t n4 = 0;  // lanes at 4 k per lane
   for (int j = 0; j < count; ++j) n4 += size_t(a.batches[j]) * a.rows[j] * a.cols[j] / 4;
-  // Launches of fewer than two waves per SIMD at 4 k per lane take 2 k per
-  // lane on both sides (twice the lanes, half the serial loads per lane).
-  const int ck = col16 >= two_waves ? 16 : (n4 < two_waves ? 1 : 4);
-  const int rk = ck == 1 ? 1 : 4;
+  *ck = col16 >= two_waves ? 16 : (n4 < two_waves ? 1 : 4);
+  *rk = *ck == 1 ? 1 : 4;
   a.begin[0] = 0;
   for (int j = 0; j < count; ++j)
     a.begin[j + 1] = a.begin[j] + size_t(a.batches[j]) * a.rows[j] * a.cols[j] /
-                                      size_t(a.k_is_col[j] ? rk : ck);
+                                      size_t(a.k_is_col[j] ? *rk : *ck);
+}
+
+int launch_split(SplitArgs& a, int count, void* stream) {
+  int ck = 0, rk = 0;
+  plan_split(a, count, &ck, &rk);
   if (a.begin[count] == 0) return SUFHIP_OK;
   size_t g = (a.begin[count] + 255) / 256;
   if (g > 4096) g = 4096;
@@ -483,6 +558,26 @@ int launch_split(SplitArgs& a, int count, void* stream) {
     hipLaunchKernelGGL((kb_split_kernel<1, 1>), dim3(unsigned(g)), dim3(256), 0,
                        as_stream(stream), a);
   return check_launch("kb_split_kernel");
+}
+
+// The split of `a` (count jobs) with the walk of `w` in one launch.
+int launch_split_walk(SplitWalkArgs& f, int count, void* stream) {
+  int ck = 0, rk = 0;
+  plan_split(f.s, count, &ck, &rk);
+  const size_t walk_lanes_n = 8 * size_t(f.w.begin[f.w.count]);
+  const size_t wg = (walk_lanes_n + 255) / 256;
+  size_t g = (f.s.begin[count] + 255) / 256;
+  if (g > 4096) g = 4096;
+  if (wg + g == 0) return SUFHIP_OK;
+  f.walk_groups = uint32_t(wg);
+  const dim3 grid(unsigned(wg + (g > 0 ? g : 0)));
+  if (ck == 16)
+    hipLaunchKernelGGL((kb_split_walk_kernel<16, 4>), grid, dim3(256), 0, as_stream(stream), f);
+  else if (ck == 4)
+    hipLaunchKernelGGL((kb_split_walk_kernel<4, 4>), grid, dim3(256), 0, as_stream(stream), f);
+  else
+    hipLaunchKernelGGL((kb_split_walk_kernel<1, 1>), grid, dim3(256), 0, as_stream(stream), f);
+  return check_launch("kb_split_walk_kernel");
 }
 
 }  // namespace
@@ -511,26 +606,29 @@ int sufhip_kb_split_batch(const sufhip_kb_split_job* jobs, int count, void* stre
 }
 
 int sufhip_kb_open_split_batch(const sufhip_kb_open_job* jobs, int count, void* stream) {
-  SUFHIP_REQUIRE(count >= 0 && count <= kSplitJobs && (count == 0 || jobs),
-                 "sufhip_kb_open_split_batch: 0..SUFHIP_KB_SPLIT_JOBS jobs");
   SplitArgs a{};
-  for (int j = 0; j < count; ++j) {
-    const sufhip_kb_open_job& jb = jobs[j];
-    SUFHIP_REQUIRE(jb.a[0] && jb.a[1], "sufhip_kb_open_split_batch: null share a[0] or a[1]");
-    SUFHIP_REQUIRE((jb.b[0] == nullptr) == (jb.b[1] == nullptr),
-                   "sufhip_kb_open_split_batch: give both shares of b or neither");
-    SUFHIP_REQUIRE(jb.a_stride[0] >= 0 && jb.a_stride[1] >= 0 && jb.a_stride[2] >= 0,
-                   "sufhip_kb_open_split_batch: a_stride entries must be >= 0");
-    a.src[j] = jb.a[0];
-    a.add[j] = jb.a[1];
-    a.sub[j][0] = jb.b[0];
-    a.sub[j][1] = jb.b[1];
-    for (int t = 0; t < 3; ++t) a.view[j][t] = size_t(jb.a_stride[t]);
-    if (int rc = split_job(a, j, jb.planes, jb.batches, jb.rows, jb.cols, jb.k_is_col,
-                           jb.planes_a0, jb.a0, "sufhip_kb_open_split_batch"))
-      return rc;
-  }
+  if (int rc = open_split_args(jobs, count, a, "sufhip_kb_open_split_batch")) return rc;
   return launch_split(a, count, stream);
+}
+
+int sufhip_kb_open_split_prepare(const sufhip_kb_open_job* jobs, int count,
+                                 const uint8_t* prg_state, const sufhip_trunc_job* tjobs,
+                                 int tcount, void* stream) {
+  SplitWalkArgs f{};
+  if (int rc = open_split_args(jobs, count, f.s, "sufhip_kb_open_split_prepare")) return rc;
+  bool one = false;
+  if (int rc = trunc_walk_plan(prg_state, tjobs, tcount, kFusedWalkJobs, f.w.begin, f.w.key,
+                               f.w.out, f.w.geo, &one))
+    return rc;
+  if (!one) {
+    // Jobs that need the prepare's own launches (expansion levels, local
+    // levels, more than kFusedWalkJobs jobs): those first, then the split.
+    if (int rc = sufhip_trunc_prepare_batch(prg_state, tjobs, tcount, stream)) return rc;
+    return launch_split(f.s, count, stream);
+  }
+  fill_prg4(prg_state, &f.w.prg);
+  f.w.count = tcount;
+  return launch_split_walk(f, count, stream);
 }
 
 int sufhip_beaver_matmul2_mfma_ex(const sufhip_beaver_mfma2_args* args, void* stream) {

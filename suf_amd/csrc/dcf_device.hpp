@@ -76,7 +76,7 @@ struct CwFull {
 // Reads 16 bytes at p.  When p + 16 is the end of the key (`more` false) and
 // p is not 4-byte aligned, the last sh bytes come from byte loads so that no
 // word past the key is touched.
-__device__ __forceinline__ void load16(const uint8_t* p, bool more, uint32_t (&w)[4]) {
+__device__ __forceinline__ void load16_bytes(const uint8_t* p, bool more, uint32_t (&w)[4]) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(p);
   const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
   const uint32_t sh = uint32_t(a & 3);
@@ -228,7 +228,7 @@ __device__ __forceinline__ uint32_t walk_bit(const AesLds4& aes, KeySelPtr keys,
                                              const uint8_t* chunk, int in_bits, uint64_t x,
                                              uint32_t party) {
   uint32_t seed[4];
-  load16(chunk, true, seed);
+  load16_bytes(chunk, true, seed);
   uint32_t s[4] = {seed[0], seed[1], seed[2], seed[3] & 0x7fffffffu};
   uint32_t t = party;
   uint32_t v = 0;
@@ -293,7 +293,7 @@ __device__ __forceinline__ uint32_t walk_bit(const AesLds4& aes, KeySelPtr keys,
     t = tn;
   }
   uint32_t np1[4];
-  load16(cw, false, np1);
+  load16_bytes(cw, false, np1);
   return (v ^ s[0] ^ (np1[0] & t)) & 1u;
 }
 
@@ -334,7 +334,7 @@ __device__ __forceinline__ U128 walk_full(const AesLds4& aes, KeySelPtr keys, co
                                           int in_bits, uint64_t x, uint32_t party,
                                           bool more_after) {
   uint32_t seed[4];
-  load16(chunk, true, seed);
+  load16_bytes(chunk, true, seed);
   uint32_t s[4] = {seed[0], seed[1], seed[2], seed[3] & 0x7fffffffu};
   uint32_t t = party;
   U128 v{0, 0};
@@ -403,7 +403,7 @@ __device__ __forceinline__ U128 walk_full(const AesLds4& aes, KeySelPtr keys, co
     t = tn;
   }
   uint32_t np1[4];
-  load16(cw, more_after, np1);
+  load16_bytes(cw, more_after, np1);
   U128 sv = mk(s[0], s[1], s[2], s[3]);
   if (t) sv = gadd<kGroup>(sv, mk(np1[0], np1[1], np1[2], np1[3]));
   if (party) sv = gneg<kGroup>(sv);
@@ -450,7 +450,7 @@ __device__ __forceinline__ CwAdd64 load_cw_add64(const uint8_t* p) {
 // State at the root of one chunk (chunk = key + 8: seed, CWs, cw_np1).
 __device__ __forceinline__ Add64State add64_root(const uint8_t* chunk, uint32_t party) {
   uint32_t seed[4];
-  load16(chunk, true, seed);
+  load16_bytes(chunk, true, seed);
   return Add64State{seed[0], seed[1], seed[2], seed[3] & 0x7fffffffu, party, 0};
 }
 
@@ -496,7 +496,7 @@ __device__ __forceinline__ void add64_walk(const DcfAes& aes, const uint4* rkl,
 __device__ __forceinline__ uint64_t add64_finish(const uint8_t* chunk, int in_bits,
                                                  uint32_t party, const Add64State& st) {
   uint32_t np1[4];
-  load16(chunk + 16 + 33 * in_bits, false, np1);
+  load16_bytes(chunk + 16 + 33 * in_bits, false, np1);
   uint64_t s = uint64_t(st.s0) | uint64_t(st.s1) << 32;
   if (st.t) s += uint64_t(np1[0]) | uint64_t(np1[1]) << 32;
   return st.v + (party ? 0 - s : s);

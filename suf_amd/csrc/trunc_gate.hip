@@ -36,6 +36,7 @@
 #include "dcf_device.hpp"
 #include "suf_hip.h"
 #include "trunc_device.hpp"
+#include "walk_device.hpp"
 
 namespace sufhip {
 namespace {
@@ -270,37 +271,16 @@ __global__ void __launch_bounds__(256) trunc_eval_table_kernel(TruncEvalArgs a) 
 }
 
 // Key-only halves of several gates at once: the walk to depth min(d, 12) of
-// up to kWalkJobs jobs in one launch (lanes [begin[j], begin[j+1]) belong to
-// job j), then per level one launch expanding up to kBatchJobs jobs that go
-// deeper.  Both argument blocks stay under 4 KB.
+// up to kWalkJobs jobs in one launch (walk_device.hpp), then per level one
+// launch expanding up to kBatchJobs jobs that go deeper.  Both argument
+// blocks stay under 4 KB.
 constexpr int kWalkJobs = 96;
 constexpr int kBatchJobs = 32;
-
-// A table job's walks go to depth f - kWalkLocal and expand the last
-// kWalkLocal levels themselves (both children of each node), so a walk writes
-// 2^kWalkLocal entries: 2 (f - kWalkLocal) + 4 (2^kWalkLocal - 1) AES blocks
-// per 2^kWalkLocal entries instead of 2 f per entry.
-#ifndef SUFHIP_WALK_LOCAL
-#define SUFHIP_WALK_LOCAL 4
-#endif
-constexpr int kWalkLocal = SUFHIP_WALK_LOCAL;
-static_assert(kWalkLocal >= 1 && kWalkLocal <= 4, "kWalkLocal: 1..4");
 // Up to 1024 lanes per workgroup: the walk's 8 lanes per node and one
 // workgroup per CU (128 KB of AES tables) must cover a batch in one round.
 constexpr int kWalkBlock = 1024;
-#ifndef SUFHIP_WALK_GROUP
-#define SUFHIP_WALK_GROUP 4
-#endif
-constexpr int kWalkGroup = SUFHIP_WALK_GROUP;  // lockstep width of the expansion
 
-struct WalkArgs {
-  Prg4 prg;
-  int count;
-  uint32_t begin[kWalkJobs + 1];
-  const uint8_t* key[kWalkJobs];
-  uint4* out[kWalkJobs];
-  uint32_t geo[kWalkJobs];  // f | d << 8 | e << 16: bits, depth written, local levels
-};
+using WalkArgs = WalkJobs<kWalkJobs>;
 
 struct BatchLevelArgs {
   Prg4 prg;
@@ -316,135 +296,6 @@ struct BatchLevelArgs {
 static_assert(sizeof(WalkArgs) <= 4096 && sizeof(BatchLevelArgs) <= 4096,
               "kernel argument blocks must fit in 4 KB");
 
-// The job of lane g: the last j < count with begin[j] <= g (jobs with no
-// lanes share their begin with the next job, so the last such j owns g).
-template <int kJobs>
-__device__ __forceinline__ int batch_job(const uint32_t (&begin)[kJobs + 1], int count,
-                                         uint32_t g) {
-  int lo = 0, hi = count - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (begin[mid] <= g)
-      lo = mid;
-    else
-      hi = mid - 1;
-  }
-  return lo;
-}
-
-// One walk per 8 lanes.  Lanes 0-3 of the group compute the next-seed block
-// AES_{K_{2b}}(s) and lanes 4-7 the value block AES_{K_{2b+1}}(s), column-
-// parallel (AesLds4::encrypt_quad): lane q of either half holds word q of the
-// seed.  A level is then about a quarter of the dependent issue time of the
-// one-lane walk (add64_walk), which bounds these latency-bound launches.
-struct Walk8 {
-  uint32_t s;  // seed word q (both halves)
-  uint32_t t;  // control bit (both halves)
-  uint64_t v;  // accumulated value, low 64 bits (value half)
-};
-
-// Little-endian word at byte address p + 4 idx (any alignment; reads the
-// aligned words idx and idx + 1 around it).
-__device__ __forceinline__ uint32_t word_at(const uint8_t* p, int idx) {
-  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-  return __builtin_amdgcn_alignbyte(w[idx + 1], w[idx], uint32_t(a & 3));
-}
-
-__device__ __forceinline__ uint32_t row_shr4(uint32_t v) {
-  return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x114, 0xf, 0xf, false));
-}
-
-struct Walk8Ctx {
-  const DcfAes& aes;
-  const uint4* rkl;
-  const uint8_t* chunk;
-  uint4* nodes;
-  int f;
-  uint32_t party, h, q;
-};
-
-// One level (record cw) of N independent walks in lockstep: walk n goes
-// from state par[(b0 + n) >> 1] towards child bit (b0 + n) & 1 (the walk
-// loop passes N = 1 and its own bit as b0).  add64_walk's level on 8 lanes.
-template <int N>
-__device__ __forceinline__ void walk8_step_n(const Walk8Ctx& c, const uint8_t* cw, uint32_t b0,
-                                             const Walk8* par, Walk8* kid) {
-  const uint32_t csq = word_at(cw, int(c.q));
-  const uint64_t cv = uint64_t(word_at(cw, 4)) | uint64_t(word_at(cw, 5)) << 32;
-  const uint32_t tb = cw[32];
-  uint32_t o[N];
-  const uint32_t* rkq[N];
-#pragma unroll
-  for (int n = 0; n < N; ++n) {
-    const uint32_t b = N == 1 ? b0 : ((b0 + n) & 1u);
-    o[n] = par[N == 1 ? 0 : (b0 + n) >> 1].s;
-    rkq[n] = reinterpret_cast<const uint32_t*>(c.rkl + 11 * (2 * b + c.h)) + c.q;
-  }
-  c.aes.encrypt_quad_n<N>(o, rkq);
-#pragma unroll
-  for (int n = 0; n < N; ++n) {
-    const Walk8& w = par[N == 1 ? 0 : (b0 + n) >> 1];
-    const uint32_t b = N == 1 ? b0 : ((b0 + n) & 1u);
-    uint32_t on = o[n] ^ w.s;
-    // Value half: the low 64 bits of its block; seed half: bit 127 of its block.
-    const uint64_t vd0 = uint64_t(quad_bcast<0>(on)) | uint64_t(quad_bcast<1>(on)) << 32;
-    uint32_t tn = quad_bcast<3>(on) >> 31;
-    if (c.q == 3) on &= 0x7fffffffu;
-    on ^= csq & (0u - w.t);
-    tn ^= ((b ? tb : (tb >> 1)) & 1u) & w.t;
-    const uint64_t vd = vd0 + (w.t ? cv : 0);
-    Walk8 r;
-    r.v = w.v + (c.party ? 0 - vd : vd);
-    // The seed half's next seed and t move to the value half (lane - 4).
-    const uint32_t os = row_shr4(on), ts = row_shr4(tn);
-    r.s = c.h ? os : on;
-    r.t = c.h ? ts : tn;
-    kid[n] = r;
-  }
-}
-
-// Table entry `leaf` from a depth-f state (add64_finish), written by lane 0
-// of the value half, which holds the seed, t and v.
-__device__ __forceinline__ void walk8_leaf(const Walk8Ctx& c, const Walk8& w, uint32_t leaf) {
-  const uint8_t* np1 = c.chunk + 16 + 33 * c.f;
-  const uint64_t s64 = uint64_t(quad_bcast<0>(w.s)) | uint64_t(quad_bcast<1>(w.s)) << 32;
-  const uint64_t n64 = uint64_t(word_at(np1, 0)) | uint64_t(word_at(np1, 1)) << 32;
-  const uint64_t sv = s64 + (w.t ? n64 : 0);
-  const uint64_t out = w.v + (c.party ? 0 - sv : sv);
-  if (c.h == 1 && c.q == 0)
-    c.nodes[2 * leaf + 1] = make_uint4(uint32_t(out), uint32_t(out >> 32), 0, 0);
-}
-
-// Breadth-first expansion of the subtree below a depth-(f - E) node: the
-// 2^(L+1) children of level L in lockstep groups of kWalkGroup, then the
-// table entries (v << E) | i in order.
-template <int L, int E>
-__device__ __forceinline__ void walk8_expand(const Walk8Ctx& c, const uint8_t* cw,
-                                             const Walk8 (&par)[1 << L], uint32_t v) {
-  if constexpr (L == E) {
-    walk8_leaf(c, par[0], v);  // E = 0
-  } else if constexpr (L + 1 == E) {
-    // The last level: each group's children are written as soon as they exist.
-    constexpr int kKids = 2 << L;
-    constexpr int kGroup = kKids < kWalkGroup ? kKids : kWalkGroup;
-#pragma unroll
-    for (int b0 = 0; b0 < kKids; b0 += kGroup) {
-      Walk8 kid[kGroup];
-      walk8_step_n<kGroup>(c, cw, b0, par, kid);
-#pragma unroll
-      for (int i = 0; i < kGroup; ++i) walk8_leaf(c, kid[i], (v << E) | uint32_t(b0 + i));
-    }
-  } else {
-    constexpr int kKids = 2 << L;
-    constexpr int kGroup = kKids < kWalkGroup ? kKids : kWalkGroup;
-    Walk8 kid[kKids];
-#pragma unroll
-    for (int b0 = 0; b0 < kKids; b0 += kGroup) walk8_step_n<kGroup>(c, cw, b0, par, kid + b0);
-    walk8_expand<L + 1, E>(c, cw + 33, kid, v);
-  }
-}
-
 __global__ void __launch_bounds__(kWalkBlock) trunc_batch_walk_kernel(WalkArgs a) {
   SUFHIP_DCF_LDS_SETUP(a.prg);
   const uint32_t gl = blockIdx.x * blockDim.x + threadIdx.x;
@@ -457,7 +308,10 @@ __global__ void __launch_bounds__(kWalkBlock) trunc_batch_walk_kernel(WalkArgs a
   const uint32_t geo = a.geo[j];
   const int f = int(geo & 0xff), d = int((geo >> 8) & 0xff), e = int(geo >> 16);
   const uint8_t* chunk = key + kHdrBytes + 8;
-  const Walk8Ctx c{aes, rkl, chunk, a.out[j], f, uint32_t(key[6] & 1u), (gl >> 2) & 1u, gl & 3u};
+  // The body stays in the kernel: passed through a helper function, the same
+  // steps spill at the 1024-lane register limit.
+  const Walk8Ctx<DcfAes> c{aes, rkl, chunk, a.out[j], f, uint32_t(key[6] & 1u),
+                           (gl >> 2) & 1u, gl & 3u};
   const int dw = d - e;  // depth walked before the local expansion
   const uint64_t x = uint64_t(v) << (f - dw);
   Walk8 w;
@@ -586,7 +440,109 @@ int launch_finish(int kind, const TruncEvalArgs& a, int parties, hipStream_t s) 
   return check_launch("trunc_eval_aes_kernel");
 }
 
+// Shared argument checks of the evaluation entry points.
+int trunc_check(const char* fn, int kind, int frac_bits, const uint8_t* prg_state,
+                const uint8_t* d_key, size_t key_bytes, size_t n, const void* d_work,
+                size_t work_bytes) {
+  SUFHIP_REQUIRE(valid_kind(kind), std::string(fn) + ": unknown kind");
+  SUFHIP_REQUIRE(frac_bits >= 1 && frac_bits <= 62, std::string(fn) + ": frac_bits out of [1, 62]");
+  SUFHIP_REQUIRE(key_bytes == sufhip_trunc_key_bytes(kind, frac_bits),
+                 std::string(fn) + ": key_bytes does not match (kind, frac_bits)");
+  SUFHIP_REQUIRE(n < kMaxElems, std::string(fn) + ": n too large");
+  SUFHIP_REQUIRE(prg_state && d_key, std::string(fn) + ": null pointer");
+  SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_key) & 7) == 0,
+                 std::string(fn) + ": key must be 8-byte aligned");
+  const size_t need = sufhip_trunc_work_bytes(frac_bits, n);
+  SUFHIP_REQUIRE(work_bytes >= need && (need == 0 || d_work),
+                 std::string(fn) + ": workspace smaller than sufhip_trunc_work_bytes()");
+  SUFHIP_REQUIRE(need == 0 || (reinterpret_cast<uintptr_t>(d_work) & 15) == 0,
+                 std::string(fn) + ": workspace must be 16-byte aligned");
+  return SUFHIP_OK;
+}
+
+// The walk launch of m <= kWalkJobs prepare jobs: per job its depth d, walked
+// depth k0 and the two workspace regions, alternated so that depth d ends in
+// the first (as sufhip_trunc_prepare), and the local levels el of the
+// full-domain walks.
+struct WalkPlan {
+  int d[kWalkJobs], k0s[kWalkJobs], cur[kWalkJobs];
+  uint4* lvl[kWalkJobs][2];
+  int maxd, el;
+};
+
+int plan_walk(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int m, const char* what,
+              WalkPlan& p) {
+  p.maxd = 0;
+  for (int i = 0; i < m; ++i) {
+    const sufhip_trunc_job& jb = jobs[i];
+    if (int rc = trunc_check(what, jb.kind, jb.frac_bits, prg_state, jb.d_key, jb.key_bytes,
+                             jb.n, jb.d_work, jb.work_bytes))
+      return rc;
+    p.d[i] = frontier_bits(jb.frac_bits, jb.n);
+    p.k0s[i] = batch_walk_bits(p.d[i], jb.frac_bits);
+    p.lvl[i][0] = static_cast<uint4*>(jb.d_work);
+    p.lvl[i][1] = p.d[i] > 0 ? p.lvl[i][0] + 2 * (size_t(1) << p.d[i]) : nullptr;
+    p.cur[i] = (p.d[i] - p.k0s[i]) & 1;
+    if (p.d[i] > p.maxd) p.maxd = p.d[i];
+  }
+  // Local levels of the full-domain walks: a walk level costs about as
+  // much as one lockstep group of the expansion, so the walks go as deep as
+  // the lanes allow -- the fewest local levels whose walks take less than
+  // three quarters of one full workgroup per CU (at most kWalkLocal; past
+  // that the extra waves per SIMD slow every level more than a local level
+  // costs).
+  int cus = 0;
+  if (int rc = cu_count(&cus)) return rc;
+  p.el = 0;
+  for (; p.el < kWalkLocal; ++p.el) {
+    size_t lanes = 0;
+    for (int i = 0; i < m; ++i) {
+      const int k0 = p.k0s[i];
+      const int e = k0 == jobs[i].frac_bits && k0 >= p.el ? p.el : 0;
+      lanes += p.d[i] > 0 ? 8 * (size_t(1) << (k0 - e)) : 0;
+    }
+    if (4 * lanes < 3 * size_t(cus) * kWalkBlock) break;
+  }
+  return SUFHIP_OK;
+}
+
+// WalkJobs' fields for the plan: walks per job, keys, outputs, geometry.
+void fill_walk(const WalkPlan& p, const sufhip_trunc_job* jobs, int m, uint32_t* begin,
+               const uint8_t** key, uint4** out, uint32_t* geo) {
+  begin[0] = 0;
+  for (int i = 0; i < m; ++i) {
+    const sufhip_trunc_job& jb = jobs[i];
+    const int k0 = p.k0s[i];
+    const int e = k0 == jb.frac_bits && k0 >= p.el ? p.el : 0;
+    key[i] = jb.d_key;
+    out[i] = p.lvl[i][p.cur[i]];
+    geo[i] = uint32_t(jb.frac_bits) | uint32_t(k0) << 8 | uint32_t(e) << 16;
+    begin[i + 1] = begin[i] + (p.d[i] > 0 ? (1u << (k0 - e)) : 0u);
+  }
+}
+
 }  // namespace
+
+int trunc_walk_plan(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int count,
+                    int max_jobs, uint32_t* begin, const uint8_t** key, uint4** out,
+                    uint32_t* geo, bool* one) {
+  *one = false;
+  SUFHIP_REQUIRE(count >= 0 && (count == 0 || jobs), "sufhip_kb_open_split_prepare: bad jobs");
+  SUFHIP_REQUIRE(prg_state, "sufhip_kb_open_split_prepare: null prg_state");
+  if (count > max_jobs || count > kWalkJobs) return SUFHIP_OK;
+  WalkPlan p;
+  if (int rc = plan_walk(prg_state, jobs, count, "sufhip_kb_open_split_prepare", p)) return rc;
+  // Table gates only (every walk ends in a table entry), no local levels and
+  // no expansion launches.
+  bool ok = p.el == 0;
+  for (int i = 0; i < count; ++i)
+    ok = ok && (p.d[i] == 0 || (p.k0s[i] == p.d[i] && p.d[i] == jobs[i].frac_bits));
+  if (!ok) return SUFHIP_OK;
+  fill_walk(p, jobs, count, begin, key, out, geo);
+  *one = true;
+  return SUFHIP_OK;
+}
+
 }  // namespace sufhip
 
 using namespace sufhip;
@@ -713,26 +669,6 @@ size_t sufhip_trunc_work_bytes(int frac_bits, size_t n) {
   return frontier_nodes(frontier_bits(frac_bits, n)) * 32;
 }
 
-// Shared argument checks of the evaluation entry points.
-static int trunc_check(const char* fn, int kind, int frac_bits, const uint8_t* prg_state,
-                       const uint8_t* d_key, size_t key_bytes, size_t n, const void* d_work,
-                       size_t work_bytes) {
-  SUFHIP_REQUIRE(valid_kind(kind), std::string(fn) + ": unknown kind");
-  SUFHIP_REQUIRE(frac_bits >= 1 && frac_bits <= 62, std::string(fn) + ": frac_bits out of [1, 62]");
-  SUFHIP_REQUIRE(key_bytes == sufhip_trunc_key_bytes(kind, frac_bits),
-                 std::string(fn) + ": key_bytes does not match (kind, frac_bits)");
-  SUFHIP_REQUIRE(n < kMaxElems, std::string(fn) + ": n too large");
-  SUFHIP_REQUIRE(prg_state && d_key, std::string(fn) + ": null pointer");
-  SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_key) & 7) == 0,
-                 std::string(fn) + ": key must be 8-byte aligned");
-  const size_t need = sufhip_trunc_work_bytes(frac_bits, n);
-  SUFHIP_REQUIRE(work_bytes >= need && (need == 0 || d_work),
-                 std::string(fn) + ": workspace smaller than sufhip_trunc_work_bytes()");
-  SUFHIP_REQUIRE(need == 0 || (reinterpret_cast<uintptr_t>(d_work) & 15) == 0,
-                 std::string(fn) + ": workspace must be 16-byte aligned");
-  return SUFHIP_OK;
-}
-
 int sufhip_trunc_prepare(int kind, int frac_bits, const uint8_t* prg_state, const uint8_t* d_key,
                          size_t key_bytes, size_t n, void* d_work, size_t work_bytes,
                          void* stream) {
@@ -818,54 +754,16 @@ int sufhip_trunc_prepare_batch(const uint8_t* prg_state, const sufhip_trunc_job*
   fill_prg4(prg_state, &prg);
   for (int base = 0; base < count; base += kWalkJobs) {
     const int m = count - base < kWalkJobs ? count - base : kWalkJobs;
-    // Per job: its depth d, walked depth k0 and the two workspace regions,
-    // alternated so that depth d ends in the first (as sufhip_trunc_prepare).
-    int d[kWalkJobs], k0s[kWalkJobs], cur[kWalkJobs];
-    uint4* lvl[kWalkJobs][2];
-    int maxd = 0;
-    for (int i = 0; i < m; ++i) {
-      const sufhip_trunc_job& jb = jobs[base + i];
-      if (int rc = trunc_check("sufhip_trunc_prepare_batch", jb.kind, jb.frac_bits, prg_state,
-                               jb.d_key, jb.key_bytes, jb.n, jb.d_work, jb.work_bytes))
-        return rc;
-      d[i] = frontier_bits(jb.frac_bits, jb.n);
-      k0s[i] = batch_walk_bits(d[i], jb.frac_bits);
-      const int k0 = k0s[i];
-      lvl[i][0] = static_cast<uint4*>(jb.d_work);
-      lvl[i][1] = d[i] > 0 ? lvl[i][0] + 2 * (size_t(1) << d[i]) : nullptr;
-      cur[i] = (d[i] - k0) & 1;
-      if (d[i] > maxd) maxd = d[i];
-    }
-    // Local levels of the full-domain walks: a walk level costs about as
-    // much as one lockstep group of the expansion, so the walks go as deep as
-    // the lanes allow -- the fewest local levels whose walks take less than
-    // three quarters of one full workgroup per CU (at most kWalkLocal; past
-    // that the extra waves per SIMD slow every level more than a local level
-    // costs).
-    int cus = 0;
-    if (int rc = cu_count(&cus)) return rc;
-    int el = 0;
-    for (; el < kWalkLocal; ++el) {
-      size_t lanes = 0;
-      for (int i = 0; i < m; ++i) {
-        const int k0 = k0s[i];
-        const int e = k0 == jobs[base + i].frac_bits && k0 >= el ? el : 0;
-        lanes += d[i] > 0 ? 8 * (size_t(1) << (k0 - e)) : 0;
-      }
-      if (4 * lanes < 3 * size_t(cus) * kWalkBlock) break;
-    }
+    WalkPlan p;
+    if (int rc = plan_walk(prg_state, jobs + base, m, "sufhip_trunc_prepare_batch", p)) return rc;
+    int(&d)[kWalkJobs] = p.d;
+    int(&k0s)[kWalkJobs] = p.k0s;
+    int(&cur)[kWalkJobs] = p.cur;
+    uint4*(&lvl)[kWalkJobs][2] = p.lvl;
+    const int maxd = p.maxd;
     WalkArgs wa{};
     wa.prg = prg;
-    wa.begin[0] = 0;
-    for (int i = 0; i < m; ++i) {
-      const sufhip_trunc_job& jb = jobs[base + i];
-      const int k0 = k0s[i];
-      const int e = k0 == jb.frac_bits && k0 >= el ? el : 0;
-      wa.key[i] = jb.d_key;
-      wa.out[i] = lvl[i][cur[i]];
-      wa.geo[i] = uint32_t(jb.frac_bits) | uint32_t(k0) << 8 | uint32_t(e) << 16;
-      wa.begin[i + 1] = wa.begin[i] + (d[i] > 0 ? (1u << (k0 - e)) : 0u);
-    }
+    fill_walk(p, jobs + base, m, wa.begin, wa.key, wa.out, wa.geo);
     wa.count = m;
     if (wa.begin[m] > 0) {
       unsigned int g = 0, b = 0;

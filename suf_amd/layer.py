@@ -115,13 +115,16 @@ def kb_split(jobs):
     native.call("sufhip_kb_split_batch", arr, len(jobs), stream_ptr())
 
 
-def kb_open_split(jobs):
+def kb_open_split(jobs, prepare=None):
     """Masked opens written straight as digit planes, up to 8 in one launch:
     jobs of (a, b, planes, batches, rows, cols, k_is_col[, planes_a0, a0[,
     view]]) with a and b pairs of share arrays (b may be None); element i is
     a0 + a1 - b0 - b1, and with planes_a0 and a0 (either may be None) also
     its + a0[i] planes.  view = (offset, batch, row, col strides) in words:
-    element (batch, row, col) of a[p] is a[p][offset + strides . index]."""
+    element (batch, row, col) of a[p] is a[p][offset + strides . index].
+    prepare: optional truncation gates (tasks.Trunc, one PRG state) whose
+    key-only halves run in the same launch when they fit beside the split
+    (sufhip_kb_open_split_prepare), else in their own launches first."""
     arr = (native.KbOpenJob * len(jobs))()
     for i, jb in enumerate(jobs):
         a, b, planes, nb, r, c, kc = jb[:7]
@@ -141,7 +144,16 @@ def kb_open_split(jobs):
             arr[i].planes_a0, arr[i].a0 = ptr(jb[7]), ptr(jb[8])
         if len(jb) > 9 and jb[9] is not None:
             arr[i].a_stride[0], arr[i].a_stride[1], arr[i].a_stride[2] = jb[9][1:4]
-    native.call("sufhip_kb_open_split_batch", arr, len(jobs), stream_ptr())
+    if not prepare:
+        native.call("sufhip_kb_open_split_batch", arr, len(jobs), stream_ptr())
+        return
+    state = prepare[0].prg_state
+    if any(t.prg_state != state for t in prepare):
+        raise ValueError("kb_open_split: gates with different PRG states")
+    tj = [j for t in prepare for j in t.jobs()]
+    tarr = (native.TruncJob * len(tj))(*tj)
+    native.call("sufhip_kb_open_split_prepare", arr, len(jobs), prepare[0]._state, tarr, len(tj),
+                stream_ptr())
 
 
 class BatchedTriples:

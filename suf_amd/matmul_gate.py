@@ -146,7 +146,7 @@ class BeaverMatmulTrunc:
         return out
 
     def _eval2_fused(self, X, W, out, events=None):
-        """The truncation's key-only half, the opens D = X - A and E = W - B
+        """The truncation's key-only half with the opens D = X - A and E = W - B
         written straight as their digit planes (one launch), then both
         parties' products with the truncation of their masked open in one
         launch; all on the current stream."""
@@ -162,11 +162,11 @@ class BeaverMatmulTrunc:
         epi = self.tr.epilogue(out)
         a.trunc = native.ctypes.pointer(epi)
         a.mask = self.tr.mask & M64
-        self.tr.prepare()
         if events:
             events[0].record()
+        # The truncation's key-only walks run in the opens' launch.
         layer.kb_open_split([(X, self.A, self.Dp, 1, M, K, 1, self.Xp, self.A[0]),
-                             (W, self.B, self.Ep, 1, K, N, 0)])
+                             (W, self.B, self.Ep, 1, K, N, 0)], prepare=[self.tr])
         if events and len(events) > 2:
             events[1].record()
         native.call("sufhip_beaver_matmul2_mfma_ex", native.ctypes.byref(a), _stream())

@@ -96,6 +96,7 @@ _SIGS = {
     "sufhip_beaver_matmul2_mfma_ex": (c_int, [c_vp, c_vp]),
     "sufhip_kb_split_batch": (c_int, [c_vp, c_int, c_vp]),
     "sufhip_kb_open_split_batch": (c_int, [c_vp, c_int, c_vp]),
+    "sufhip_kb_open_split_prepare": (c_int, [c_vp, c_int, c_vp, c_vp, c_int, c_vp]),
     "sufhip_beaver_matmul2_mfma_batched": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                                    c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp,
                                                    c_vp]),

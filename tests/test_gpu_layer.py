@@ -541,6 +541,62 @@ def test_kb_open_split_two_jobs_mixed():
         assert torch.equal(job[2].view(torch.uint8)[:nbytes], want.view(torch.uint8)[:nbytes])
 
 
+@pytest.mark.parametrize("gates,f,n", [(1, 12, 4096), (2, 7, 100), (1, 14, 4096), (5, 12, 4096),
+                                       (1, 20, 1 << 16), (1, 20, 4096)])
+def test_kb_open_split_prepare_matches_separate_calls(gates, f, n):
+    """The opens with the truncations' key-only walks in the same launch
+    (sufhip_kb_open_split_prepare) write the same digit planes as the opens
+    alone and the same workspaces as the batched prepare.  One or two table
+    gates run in the one launch; f = 14 (walks past three quarters of a walk
+    workgroup per CU), five gates (ten jobs, above eight), f = 20 with 2^16
+    points (expansion launches) and f = 20 with 4096 points (a depth-12
+    frontier, not a table) take the prepare's own launches first."""
+    from suf_amd.tasks import Trunc, prepare_batch
+    print("[gpu-case] kb_open_split_prepare", gates, f, n, flush=True)
+    g = np.random.default_rng(11)
+    dealer = Dealer(21)
+    trs = [Trunc(dealer, f, n, STATE) for _ in range(gates)]
+    specs = [(1, 64, 96, 1, True), (2, 32, 64, 0, False)]
+    jobs, got_planes, want_planes = [], [], []
+    for nb, r, c, kc, use_b in specs:
+        m = nb * r * c
+        a = tuple(dev(g.integers(0, 2**64, m, dtype=np.uint64)) for _ in range(2))
+        b = tuple(dev(g.integers(0, 2**64, m, dtype=np.uint64)) for _ in range(2)) if use_b else None
+        got_planes.append(layer.kb_planes(nb, r, c))
+        want_planes.append(layer.kb_planes(nb, r, c))
+        got_planes[-1].fill_(0x5a5a)  # every planes byte must be written
+        want_planes[-1].fill_(0)
+        jobs.append((a, b, nb, r, c, kc))
+    for t in trs:
+        for p in (0, 1):
+            t.work[p].fill_(0x3c3c)
+    layer.kb_open_split([(a, b, pl, nb, r, c, kc) for (a, b, nb, r, c, kc), pl
+                         in zip(jobs, got_planes)], prepare=trs)
+    torch.cuda.synchronize()
+    got_work = [t.work[p].clone() for t in trs for p in (0, 1)]
+    for t in trs:
+        for p in (0, 1):
+            t.work[p].fill_(0x3c3c)
+    prepare_batch(trs)
+    layer.kb_open_split([(a, b, pl, nb, r, c, kc) for (a, b, nb, r, c, kc), pl
+                         in zip(jobs, want_planes)])
+    torch.cuda.synchronize()
+    want_work = [t.work[p] for t in trs for p in (0, 1)]
+    for i, (gw, ww) in enumerate(zip(got_work, want_work)):
+        assert torch.equal(gw, ww), ("workspace", i)
+    for (a, b, nb, r, c, kc), gp, wp in zip(jobs, got_planes, want_planes):
+        nbytes = native.load().sufhip_kb_planes_bytes(nb, r, c)
+        assert torch.equal(gp.view(torch.uint8)[:nbytes], wp.view(torch.uint8)[:nbytes])
+    # The tables give the gate's shares: x >> f after the finish (one gate).
+    t = trs[0]
+    x = g.integers(0, 2**40, n, dtype=np.uint64)
+    xh = dev(x + np.uint64(t.mask))
+    out = (torch.empty(n, dtype=torch.int64, device="cuda"),
+           torch.empty(n, dtype=torch.int64, device="cuda"))
+    t.finish(xh, out)
+    assert np.array_equal(u64(out[0] + out[1]), x >> np.uint64(f))
+
+
 @pytest.mark.parametrize("shape", [(1, 64, 96, 1), (2, 96, 64, 0), (3, 32, 64, 0)])
 def test_lin2_batch_planes_match_open_then_split(shape):
     """lin2_batch's digit-plane output of an open (row-side layouts written in
