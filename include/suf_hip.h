@@ -520,6 +520,20 @@ typedef struct sufhip_layernorm2_args {
   sufhip_chain2_args rsqrt;
   uint64_t* out[2];        /* may be NULL when out_planes is given */
   sufhip_x_planes out_planes;
+  /* Optional (in_slices != NULL; x is then ignored): the input is the
+   * truncation of a public-weight product whose k-slices
+   * sufhip_matmul_public2_planes_partial left unreduced,
+   *   x_p[i] = tr_in_p(sum_z in_slices[(2 z) mn + i] + in_slices[(2 z + 1) mn + i]
+   *                    + in_mask) + tr_in.add[p][i]   (mn = rows cols),
+   * written to tr_in.y[p][i] and then normalised: the product's reduction and
+   * its truncation epilogue (the residual r1 = tr(ctx Wout) + x of
+   * transformer_layer_forward, src/nn/transformer_layer.cpp:626-760) run in
+   * this launch instead of their own.  2..8 slices; tr_in a prepared GapARS
+   * table gate with outputs (and optionally an addend). */
+  const uint64_t* in_slices;
+  int in_slice_count;
+  sufhip_trunc_epilogue tr_in;
+  uint64_t in_mask;
 } sufhip_layernorm2_args;
 int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream);
 
@@ -859,6 +873,22 @@ int sufhip_matmul_public2_planes(const int8_t* d_Xp, int M, int K, int N, const 
                                  int digits, uint64_t* d_out0, uint64_t* d_out1, uint64_t* d_zhat,
                                  uint64_t mask, const sufhip_trunc_epilogue* trunc, void* d_work,
                                  size_t work_bytes, void* stream);
+/* The number of k-slices the products above split (M, K, N) into (0 for a
+ * bad shape).  Above 1 each slice's partial shares pass through the
+ * workspace and a reduction launch; sufhip_matmul_public2_planes_partial
+ * stops before that launch and leaves the reduction (with the truncation) to
+ * the consumer, sufhip_layernorm2's in_slices. */
+int sufhip_matmul_public2_slices(int M, int K, int N);
+/* sufhip_matmul_public2_planes without the reduction: on return *d_slices
+ * points at the partial shares inside d_work, [slices][2][M N] u64 (slice z,
+ * party p at (2 z + p) M N), valid once the launch has run and until the
+ * workspace's next use.  Needs sufhip_matmul_public2_slices(M, K, N) > 1.
+ * The product is the reference's public-weight matmul
+ * (src/nn/matmul_publicW.cpp:17-36) before the truncation that follows it. */
+int sufhip_matmul_public2_planes_partial(const int8_t* d_Xp, int M, int K, int N,
+                                         const int8_t* d_planes, int digits, void* d_work,
+                                         size_t work_bytes, const uint64_t** d_slices,
+                                         void* stream);
 int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int K, int N,
                           const int8_t* d_planes, int digits, uint64_t* d_out0, uint64_t* d_out1,
                           uint64_t* d_zhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,

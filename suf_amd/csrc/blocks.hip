@@ -13,6 +13,8 @@
 //                      97-450) with RowMaxDiffTask, nExp, row sum, Recip
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "chain_device.hpp"
 #include "digit_planes.hpp"
 #include "reduce_device.hpp"
@@ -31,34 +33,39 @@ struct LnArgs {
   const uint64_t* x[2];
   int rows, cols;
   uint64_t inv_len, eps;
-  TruncEpi tr[4];  // mean, var0, var1, norm
-  uint64_t mask[4];
+  TruncEpi tr[5];  // mean, var0, var1, norm, and the input's (with in_slices)
+  uint64_t mask[5];
   sufhip_triple2 sq, norm;
   ChainArgs rs;
   uint64_t* out[2];
   sufhip_x_planes xp;
+  const uint64_t* in_slices;  // optional: [slices][2][rows cols] partial products
+  int in_count;
 };
 
-enum { kTrMean = 0, kTrVar0 = 1, kTrVar1 = 2, kTrNorm = 3 };
+enum { kTrMean = 0, kTrVar0 = 1, kTrVar1 = 2, kTrNorm = 3, kTrIn = 4 };
+constexpr int kLnMaxSlices = 8;
+constexpr int kLnMaxInPer = 4;  // in_slices rows of up to 1024 elements
 
 // Every load that does not depend on an open is issued when the row starts:
 // x, both triples' shares, and (lane 0) the rsqrt chain's triples; the key
 // headers of all truncation gates sit in LDS.  What remains serial per row
 // is one table read per truncation gate and the rsqrt LUT's AES.
-template <int kPer>
+template <int kPer, bool kIn>
 __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
   __shared__ __align__(16) uint32_t tab[256 * kLnCopies];
   __shared__ ChainLds L;
   constexpr int kRsProds = chain_products<SUFHIP_CHAIN_RSQRT>();
-  __shared__ TruncHdr th[4][2];
+  __shared__ TruncHdr th[5][2];
   __shared__ TruncHdr rth[kRsProds][2];  // the rsqrt chain's truncation key headers
   __shared__ uint64_t red[2][kLnWaves];
   __shared__ uint64_t bc[2];
   __shared__ ChainPre pre;
   fill_ttable<kLnCopies>(tab, kTDev.v);
   chain_stage(A.rs, 2, L);
-  if (threadIdx.x < 8) th[threadIdx.x >> 1][threadIdx.x & 1] =
-      read_trunc_hdr(A.tr[threadIdx.x >> 1].key[threadIdx.x & 1]);
+  if (threadIdx.x < (kIn ? 10 : 8))
+    th[threadIdx.x >> 1][threadIdx.x & 1] =
+        read_trunc_hdr(A.tr[threadIdx.x >> 1].key[threadIdx.x & 1]);
   {
     TruncHdrStager<kRsProds> hs;
     hs.load(A.rs, 64);
@@ -83,11 +90,80 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
     // each step then waits only for its own words, and the norm triple's
     // arrive while lane 0 runs the rsqrt chain.
     uint64_t d[kPer][2], sa[kPer][2], sb[kPer][2], sc[kPer][2], na[kPer][2], nc[kPer][2];
+    if (kIn) {
+      // x = tr_in(the open of the product's slice sums) + addend, written
+      // out as the product's output.  All slice and addend loads first.
+      const size_t mn = size_t(A.rows) * size_t(cols);
+      const TruncEpi& ti = A.tr[kTrIn];
+      uint64_t ad[kPer][2];
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int c = threadIdx.x + k * kLnBlock;
+      for (int k = 0; k < kPer; ++k) {
+        const int c = threadIdx.x + k * kLnBlock;
 #pragma unroll
-      for (int p = 0; p < 2; ++p) d[k][p] = c < cols ? A.x[p][base + c] : 0;
+        for (int p = 0; p < 2; ++p) {
+          d[k][p] = 0;
+          ad[k][p] = c < cols && ti.add[0] ? ti.add[p][base + c] : 0;
+        }
+      }
+      // Slices in groups of four, then one by one: every load of a group is
+      // unconditional (a lane past the row end reads the row's first
+      // element and drops the sum), so a group is one round trip.  A load
+      // whose value a select or branch might drop would be sunk into the
+      // branch and wait for the loads before it.
+      const int ns = A.in_count;
+      auto add_slices = [&](int z0, auto nz) {
+        constexpr int kN = decltype(nz)::value;
+        uint64_t t[kPer][2][kN];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+          const int c = threadIdx.x + k * kLnBlock;
+          const size_t e = c < cols ? base + c : base;
+#pragma unroll
+          for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int dz = 0; dz < kN; ++dz)
+              t[k][p][dz] = A.in_slices[(size_t(z0 + dz) * 2 + p) * mn + e];
+        }
+        // Every load of the group before any add (the scheduler otherwise
+        // waits for each element's loads before issuing the next one's).
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < kPer; ++k)
+#pragma unroll
+          for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int dz = 0; dz < kN; ++dz) d[k][p] += t[k][p][dz];
+      };
+      int z0 = 0;
+      for (; z0 + 4 <= ns; z0 += 4) add_slices(z0, std::integral_constant<int, 4>{});
+      for (; z0 < ns; ++z0) add_slices(z0, std::integral_constant<int, 1>{});
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        if (threadIdx.x + k * kLnBlock >= cols) d[k][0] = d[k][1] = 0;
+      }
+      uint64_t zh[kPer], w[kPer][2];
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        zh[k] = d[k][0] + d[k][1] + A.mask[kTrIn];
+        w[k][0] = trunc_table_word(th[kTrIn][0], ti.table[0], ti.f, zh[k]);
+        w[k][1] = trunc_table_word(th[kTrIn][1], ti.table[1], ti.f, zh[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int c = threadIdx.x + k * kLnBlock;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          d[k][p] = c < cols ? trunc_table_out(th[kTrIn][p], ti.f, zh[k], w[k][p]) + ad[k][p] : 0;
+          if (c < cols) ti.y[p][base + c] = d[k][p];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int c = threadIdx.x + k * kLnBlock;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) d[k][p] = c < cols ? A.x[p][base + c] : 0;
+      }
     }
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -740,9 +816,14 @@ int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
   SUFHIP_REQUIRE(g.rows >= 0 && g.cols >= 1 && g.cols <= kLnBlock * kLnMaxPer,
                  "sufhip_layernorm2: cols in [1, 2048]");
   if (g.rows == 0) return SUFHIP_OK;
-  SUFHIP_REQUIRE(g.x[0] && g.x[1] && (g.out[0] == nullptr) == (g.out[1] == nullptr) &&
+  SUFHIP_REQUIRE((g.in_slices || (g.x[0] && g.x[1])) &&
+                     (g.out[0] == nullptr) == (g.out[1] == nullptr) &&
                      (g.out[0] || g.out_planes.planes),
                  "sufhip_layernorm2: null input or output");
+  SUFHIP_REQUIRE(!g.in_slices || (g.in_slice_count >= 2 && g.in_slice_count <= kLnMaxSlices),
+                 "sufhip_layernorm2: in_slice_count in [2, 8]");
+  SUFHIP_REQUIRE(!g.in_slices || g.cols <= kLnBlock * kLnMaxInPer,
+                 "sufhip_layernorm2: in_slices need cols <= 1024");
   SUFHIP_REQUIRE(x_planes_ok(g.out_planes, size_t(g.rows) * size_t(g.cols)) &&
                      (!g.out_planes.planes || g.out_planes.cols == g.cols),
                  "sufhip_layernorm2: out_planes needs cols == the row length, rows and cols "
@@ -760,6 +841,12 @@ int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
   if (int rc = table_epi(g.tr_var[1], size_t(g.rows), "sufhip_layernorm2 tr_var", &A.tr[kTrVar1]))
     return rc;
   if (int rc = table_epi(g.tr_norm, n, "sufhip_layernorm2 tr_norm", &A.tr[kTrNorm])) return rc;
+  if (g.in_slices) {
+    if (int rc = make_epi(&g.tr_in, n, "sufhip_layernorm2 tr_in", &A.tr[kTrIn])) return rc;
+    A.in_slices = g.in_slices;
+    A.in_count = g.in_slice_count;
+    A.mask[kTrIn] = g.in_mask;
+  }
   A.x[0] = g.x[0];
   A.x[1] = g.x[1];
   A.rows = g.rows;
@@ -781,14 +868,24 @@ int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
   const int grid = g.rows < cus * 8 ? g.rows : cus * 8;
   const int per = (g.cols + kLnBlock - 1) / kLnBlock;
   hipStream_t s = as_stream(stream);
-  if (per <= 1)
-    hipLaunchKernelGGL(layernorm2_kernel<1>, dim3(grid), dim3(kLnBlock), 0, s, A);
-  else if (per <= 2)
-    hipLaunchKernelGGL(layernorm2_kernel<2>, dim3(grid), dim3(kLnBlock), 0, s, A);
-  else if (per <= 4)
-    hipLaunchKernelGGL(layernorm2_kernel<4>, dim3(grid), dim3(kLnBlock), 0, s, A);
-  else
-    hipLaunchKernelGGL(layernorm2_kernel<kLnMaxPer>, dim3(grid), dim3(kLnBlock), 0, s, A);
+  if (A.in_slices) {
+    if (per <= 1)
+      hipLaunchKernelGGL((layernorm2_kernel<1, true>), dim3(grid), dim3(kLnBlock), 0, s, A);
+    else if (per <= 2)
+      hipLaunchKernelGGL((layernorm2_kernel<2, true>), dim3(grid), dim3(kLnBlock), 0, s, A);
+    else
+      hipLaunchKernelGGL((layernorm2_kernel<kLnMaxInPer, true>), dim3(grid), dim3(kLnBlock), 0,
+                         s, A);
+  } else if (per <= 1) {
+    hipLaunchKernelGGL((layernorm2_kernel<1, false>), dim3(grid), dim3(kLnBlock), 0, s, A);
+  } else if (per <= 2) {
+    hipLaunchKernelGGL((layernorm2_kernel<2, false>), dim3(grid), dim3(kLnBlock), 0, s, A);
+  } else if (per <= 4) {
+    hipLaunchKernelGGL((layernorm2_kernel<4, false>), dim3(grid), dim3(kLnBlock), 0, s, A);
+  } else {
+    hipLaunchKernelGGL((layernorm2_kernel<kLnMaxPer, false>), dim3(grid), dim3(kLnBlock), 0, s,
+                       A);
+  }
   return check_launch("layernorm2_kernel");
 }
 

@@ -594,10 +594,12 @@ namespace {
 
 // The product from X's planes Lp ([8][K/32][2M][32]); work holds the
 // k-slices' partial tiles after the X planes region.
+// partial: stop before the reduction of the k-slices (the caller checked
+// that there are several).
 int launch_public2(const char* what, const int8_t* Lp, int M, int K, int N,
                    const int8_t* d_planes, int digits, uint64_t* d_out0, uint64_t* d_out1,
                    uint64_t* d_zhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,
-                   void* d_work, size_t work_bytes, hipStream_t s) {
+                   void* d_work, size_t work_bytes, hipStream_t s, bool partial = false) {
   TruncEpi epi;
   if (int rc = make_epi(trunc, size_t(M) * N, what, &epi)) return rc;
   if (work_bytes < sufhip_matmul_public2_work_bytes(M, K, N)) {
@@ -635,7 +637,7 @@ int launch_public2(const char* what, const int8_t* Lp, int M, int K, int N,
     }
     if (int rc = check_launch("public_mfma_kernel")) return rc;
   }
-  if (sl == 1) return SUFHIP_OK;
+  if (sl == 1 || partial) return SUFHIP_OK;
   const size_t mn = size_t(M) * N;
   size_t g = (mn + 255) / 256;
   if (g > 4096) g = 4096;
@@ -704,6 +706,33 @@ int sufhip_matmul_public2_planes(const int8_t* d_Xp, int M, int K, int N, const 
                  "sufhip_matmul_public2_planes: X planes null or not 16-byte aligned");
   return launch_public2(what, d_Xp, M, K, N, d_planes, digits, d_out0, d_out1, d_zhat, mask,
                         trunc, d_work, work_bytes, as_stream(stream));
+}
+
+int sufhip_matmul_public2_slices(int M, int K, int N) {
+  return shape_ok(M, K, N) ? pub_slices(M, K, N) : 0;
+}
+
+int sufhip_matmul_public2_planes_partial(const int8_t* d_Xp, int M, int K, int N,
+                                         const int8_t* d_planes, int digits, void* d_work,
+                                         size_t work_bytes, const uint64_t** d_slices,
+                                         void* stream) {
+  const char* what = "sufhip_matmul_public2_planes_partial";
+  SUFHIP_REQUIRE(d_slices, "sufhip_matmul_public2_planes_partial: null d_slices");
+  *d_slices = nullptr;
+  uint64_t dummy = 0;  // check_public2 wants an output; the slices are it
+  if (int rc = check_public2(what, M, K, N, d_planes, digits, nullptr, nullptr, &dummy, nullptr,
+                             d_work))
+    return rc;
+  SUFHIP_REQUIRE(pub_slices(M, K, N) > 1,
+                 "sufhip_matmul_public2_planes_partial: this shape runs as one k-slice");
+  SUFHIP_REQUIRE(d_Xp && (reinterpret_cast<uintptr_t>(d_Xp) & 15) == 0,
+                 "sufhip_matmul_public2_planes_partial: X planes null or not 16-byte aligned");
+  if (int rc = launch_public2(what, d_Xp, M, K, N, d_planes, digits, nullptr, nullptr, nullptr, 0,
+                              nullptr, d_work, work_bytes, as_stream(stream), true))
+    return rc;
+  *d_slices = reinterpret_cast<const uint64_t*>(static_cast<const int8_t*>(d_work) +
+                                                size_t(kPlanes) * 2 * M * K);
+  return SUFHIP_OK;
 }
 
 }  // extern "C"

@@ -81,6 +81,23 @@ class PublicMatmulTrunc:
         eval2(None, ...): the first region of the workspace."""
         return (self.work, self.K)
 
+    def slices(self):
+        """The product's k-slice count (above 1, eval2_slices can leave the
+        reduction and the truncation to the consumer's launch)."""
+        return native.load().sufhip_matmul_public2_slices(self.M, self.K, self.N)
+
+    def eval2_slices(self, out, add=None):
+        """The product of the producer-written X planes with its k-slices
+        left unreduced (sufhip_matmul_public2_planes_partial): returns
+        LayerNormBlock's `pre` for a block that reduces them, applies this
+        product's truncation (prepared) and writes out = trunc_f(X W) (+ add)
+        in its own launch."""
+        sl = native.ctypes.c_void_p()
+        native.call("sufhip_matmul_public2_planes_partial", ptr(self.work), self.M, self.K, self.N,
+                    ptr(self.planes), self.digits, ptr(self.work), self.work_bytes,
+                    native.ctypes.byref(sl), stream_ptr())
+        return (sl.value, self.slices(), self.tr.epilogue(out, add), self.tr.mask)
+
     def eval2(self, X, out, add=None):
         """out = trunc_f(X W) (+ the pair `add`: a residual).  X = None: X's
         digit planes were written to x_planes() by its producer.  The
@@ -476,12 +493,18 @@ class TransformerLayer:
             self.qkv.eval2(self.h1, self.qkvs)
         prep.release()  # the second half's gates, after the QKV product
         mark()
+        pre = None
         if self.attn.mfma():
             self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)), planes=self.proj.x_planes(),
                             sm_marks=sm_marks, sm_spin=sm_spin)
             mark()
             prep.wait(b(2))
-            self.proj.eval2(None, self.r1, add=x)  # r1 = trunc(ctx Wout) + x
+            if fused_ln and self.proj.slices() > 1 and self.proj.tr.has_table():
+                # r1 = trunc(ctx Wout) + x: the k-slices' reduction and the
+                # truncation run in the second LayerNorm's launch.
+                pre = self.proj.eval2_slices(self.r1, add=x)
+            else:
+                self.proj.eval2(None, self.r1, add=x)  # r1 = trunc(ctx Wout) + x
         else:
             self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)), sm_marks=sm_marks,
                             sm_spin=sm_spin)
@@ -491,7 +514,7 @@ class TransformerLayer:
         mark()
         if fused_ln:
             self.ln2.eval2(self.r1, self.h2, prep=(prep, b(2)), planes=self.w1.x_planes(),
-                           write_out=self.keep)
+                           write_out=self.keep, pre=pre)
             mark()
             self.w1.eval2(None, self.u)
         else:

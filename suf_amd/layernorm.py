@@ -108,12 +108,18 @@ class LayerNormBlock:
     def truncs(self):
         return [self.tr_mean] + self.tr_var + self.rsqrt.truncs() + [self.tr_norm]
 
-    def block_args(self, x, out, planes=None, write_out=True):
+    def block_args(self, x, out, planes=None, write_out=True, pre=None):
         """sufhip_layernorm2_args of the one-launch block over x into out
         (planes = (buffer, cols): also as a public-weight product's digit
-        planes; write_out False: only those)."""
+        planes; write_out False: only those).  pre = (slices address, slice
+        count, truncation epilogue, mask) from PublicMatmulTrunc.eval2_slices:
+        x is that product's truncated output, reduced and written (to the
+        epilogue's outputs) in this launch; x itself is not read."""
         a = native.LayerNorm2Args()
-        a.x[0], a.x[1] = x[0].data_ptr(), x[1].data_ptr()
+        if pre is not None:
+            a.in_slices, a.in_slice_count, a.tr_in, a.in_mask = pre[0], pre[1], pre[2], pre[3] & M64
+        else:
+            a.x[0], a.x[1] = x[0].data_ptr(), x[1].data_ptr()
         a.rows, a.cols = self.rows, self.cols
         a.inv_len, a.eps = self.inv_len & M64, self.eps_q & M64
         a.tr_mean = self.tr_mean.epilogue(self.mu)
@@ -137,23 +143,24 @@ class LayerNormBlock:
         return (self.cols <= 2048 and self.rsqrt.iters == 1 and
                 all(t.has_table() for t in self.truncs()))
 
-    def eval2(self, x, out, prep=None, fused=True, planes=None, write_out=True):
+    def eval2(self, x, out, prep=None, fused=True, planes=None, write_out=True, pre=None):
         """x, out: pairs of int64 [rows * cols] device tensors.  prep:
         (tasks.Prepared, batch) holding this block's key-only halves, or None
         to issue them here on the block's side stream.  fused: the whole block
         in one launch (sufhip_layernorm2); else launch by launch.  planes =
         (buffer, cols), fused only: the output also as a public-weight
-        product's digit planes (write_out False: only those)."""
+        product's digit planes (write_out False: only those).  pre, fused
+        only: x comes from a product's unreduced k-slices (block_args)."""
         rows, cols, n = self.rows, self.cols, self.n
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
         prep[0].wait(prep[1])
         if fused and self.fusable():
-            a = self.block_args(x, out, planes, write_out)
+            a = self.block_args(x, out, planes, write_out, pre)
             native.call("sufhip_layernorm2", native.ctypes.byref(a), stream_ptr())
             return out
-        if planes is not None:
-            raise ValueError("LayerNormBlock.eval2: planes need the fused block")
+        if planes is not None or pre is not None:
+            raise ValueError("LayerNormBlock.eval2: planes and pre need the fused block")
         row_sum2(operand(term(x)), rows, cols, mul_const=self.inv_len,
                  into=(self.tr_mean, self.mu))
         diff = operand(term(x), term(self.mu, index=self.row_index, neg=True, length=rows))

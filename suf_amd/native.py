@@ -106,6 +106,9 @@ _SIGS = {
     "sufhip_matmul_public2_work_bytes": (c_sz, [c_int, c_int, c_int]),
     "sufhip_matmul_public2_planes": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_vp,
                                              c_vp, c_u64, c_vp, c_vp, c_sz, c_vp]),
+    "sufhip_matmul_public2_slices": (c_int, [c_int, c_int, c_int]),
+    "sufhip_matmul_public2_planes_partial": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp,
+                                                     c_sz, c_vp, c_vp]),
     "sufhip_matmul_public2": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_vp,
                                       c_vp, c_u64, c_vp, c_vp, c_sz, c_vp]),
     "sufhip_trunc_finish2": (c_int, [c_int, c_int, c_vp, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp,
@@ -257,7 +260,8 @@ class LayerNorm2Args(ctypes.Structure):
                 ("eps", c_u64), ("tr_mean", TruncEpilogue), ("tr_var", TruncEpilogue * 2),
                 ("tr_norm", TruncEpilogue), ("mean_mask", c_u64), ("var_mask", c_u64 * 2),
                 ("norm_mask", c_u64), ("sq", Triple2), ("norm", Triple2), ("rsqrt", Chain2Args),
-                ("out", c_vp * 2), ("out_planes", XPlanes)]
+                ("out", c_vp * 2), ("out_planes", XPlanes), ("in_slices", c_vp),
+                ("in_slice_count", c_int), ("tr_in", TruncEpilogue), ("in_mask", c_u64)]
 
 
 class ReluRoundKey(ctypes.Structure):

@@ -133,6 +133,48 @@ def test_producer_planes_feed_public_matmul(producer):
         assert np.array_equal(u64(ref[p]), u64(got[p]))
 
 
+def test_layernorm_reduces_product_slices():
+    """A LayerNorm block over a public-weight product's unreduced k-slices
+    (sufhip_matmul_public2_planes_partial, then sufhip_layernorm2 with
+    in_slices: the reduction, the truncation and its residual addend in the
+    block's launch) writes the same truncated product + residual and the same
+    normalised shares as the product's own reduction followed by the block
+    (the output projection and second LayerNorm of the layer, 128 x 768)."""
+    M, K, N = 128, 768, 768
+    say("layernorm over product slices %dx%dx%d" % (M, K, N))
+    x = pfss.host_normal_fixed(91, 1.0, 0.0, F, M * K)
+    xin = tuple(dev(v) for v in _pair(x, 92))
+    W = pfss.host_normal_fixed(93, 0.05, 0.0, F, K * N).view(np.int64).reshape(K, N)
+    res = tuple(dev(v) for v in _pair(pfss.host_normal_fixed(94, 1.0, 0.0, F, M * N), 95))
+    pm = layer.PublicMatmulTrunc(M, K, N, W, Dealer(5), STATE, F)
+    assert pm.slices() > 1
+    ln = layer.LayerNormBlock(M, N, STATE, F, seed=33)
+    assert ln.fusable()
+    for t in pm.truncs() + ln.truncs():
+        t.prepare()
+    pair_ = lambda: tuple(torch.empty(M * N, dtype=torch.int64, device="cuda")  # noqa: E731
+                          for _ in range(2))
+    r_want, h_want, r_got, h_got = pair_(), pair_(), pair_(), pair_()
+    pm.eval2(xin, r_want, add=res)  # X's planes stay in the product's workspace
+    ln.eval2(r_want, h_want)
+    for t in r_got + h_got:
+        t.fill_(0x5a5a)
+    pre = pm.eval2_slices(r_got, add=res)
+    ln.eval2(None, h_got, pre=pre)
+    torch.cuda.synchronize()
+    for p in (0, 1):
+        assert np.array_equal(u64(r_got[p]), u64(r_want[p])), ("r", p)
+        assert np.array_equal(u64(h_got[p]), u64(h_want[p])), ("h", p)
+    # Refused on the host: one slice, or a shape the product runs unsliced.
+    a = ln.block_args(None, h_got, pre=(pre[0], 1, pre[2], pre[3]))
+    with pytest.raises(native.SufHipError, match="in_slice_count"):
+        native.call("sufhip_layernorm2", native.ctypes.byref(a), 0)
+    small = layer.PublicMatmulTrunc(32, 64, 64, W[:64, :64], Dealer(6), STATE, F)
+    assert small.slices() == 1
+    with pytest.raises(native.SufHipError, match="one k-slice"):
+        small.eval2_slices(pair_())
+
+
 def test_lin2_batch_matches_single_launches():
     """Four opens of different sizes in one launch equal four sufhip_lin2
     calls; a batch with a bad operand is refused on the host."""
