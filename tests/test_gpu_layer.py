@@ -175,6 +175,49 @@ def test_layernorm_reduces_product_slices():
         small.eval2_slices(pair_())
 
 
+@pytest.mark.parametrize("rows,cols,slices", [(2080, 64, 5), (2080, 320, 3), (96, 1024, 2)])
+def test_layernorm_in_slices_several_rows_per_workgroup(rows, cols, slices):
+    """sufhip_layernorm2 over synthetic k-slices, with more rows than the
+    launch has workgroups (2080 > 8 per CU: some workgroups take two rows)
+    and with 2, 3 and 5 slices (groups of four and single slices): x = the
+    truncation of the slices' open plus a residual, as the gate's own finish
+    computes it, then the block, equal to the block over that x."""
+    from suf_amd.tasks import Trunc
+    say("layernorm in_slices %dx%d, %d slices" % (rows, cols, slices))
+    n = rows * cols
+    g = np.random.default_rng(rows + cols + slices)
+    # Slice sums of a Q(f) value near 1: each party's slices are random but
+    # sum to its share of x (x = x_0 + x_1 + r).
+    x = pfss.host_normal_fixed(96, 1.0, 0.0, F, n).astype(np.uint64)
+    parts = g.integers(0, 2**64, (slices, 2, n), dtype=np.uint64)
+    x0 = g.integers(0, 2**64, n, dtype=np.uint64)
+    parts[-1, 0] = (x0 - parts[:-1, 0].sum(axis=0, dtype=np.uint64)).astype(np.uint64)
+    parts[-1, 1] = (x - x0 - parts[:-1, 1].sum(axis=0, dtype=np.uint64)).astype(np.uint64)
+    dparts = dev(parts.reshape(-1))
+    tr = Trunc(Dealer(40), F, n, STATE)
+    tr.prepare()
+    res = tuple(dev(v) for v in _pair(pfss.host_normal_fixed(97, 0.5, 0.0, F, n), 98))
+    ln = layer.LayerNormBlock(rows, cols, STATE, F, seed=34)
+    assert ln.fusable()
+    for t in ln.truncs():
+        t.prepare()
+    pair_ = lambda: tuple(torch.empty(n, dtype=torch.int64, device="cuda")  # noqa: E731
+                          for _ in range(2))
+    r_want, h_want, r_got, h_got = pair_(), pair_(), pair_(), pair_()
+    xhat = dev((x + np.uint64(tr.mask)).astype(np.uint64))
+    tr.finish(xhat, r_want)
+    for p in (0, 1):
+        r_want[p].add_(res[p])
+    ln.eval2(r_want, h_want)
+    for t in r_got + h_got:
+        t.fill_(0x5a5a)
+    ln.eval2(None, h_got, pre=(dparts.data_ptr(), slices, tr.epilogue(r_got, res), tr.mask))
+    torch.cuda.synchronize()
+    for p in (0, 1):
+        assert np.array_equal(u64(r_got[p]), u64(r_want[p])), ("r", p)
+        assert np.array_equal(u64(h_got[p]), u64(h_want[p])), ("h", p)
+
+
 def test_lin2_batch_matches_single_launches():
     """Four opens of different sizes in one launch equal four sufhip_lin2
     calls; a batch with a bad operand is refused on the host."""
