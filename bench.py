@@ -54,7 +54,7 @@ def parse():
                     help="skip the spline-gate and Beaver matmul pipeline timings")
     ap.add_argument("--no-shared", action="store_true",
                     help="configs 2, 4, 5: skip the shared-keystream timings (profiling runs)")
-    ap.add_argument("--only", choices=["spline", "matmul", "softmax_ln", "layer"],
+    ap.add_argument("--only", choices=["spline", "matmul", "softmax_ln", "layer", "aes"],
                     help="run one gate pipeline alone and print its result object "
                          "(for profiling; not the benchmark line)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -840,6 +840,42 @@ def cpu_baseline_reference(keys0, keys1, xhat, gpu_bits0, gpu_bits1, seconds):
             "mismatches": mism, "host": host_info()}
 
 
+def bench_aes(steps, warmup, blocks=1 << 24):
+    """AES-128-CTR keystream of `blocks` blocks by the LDS T-table kernel and
+    by the bitsliced one (the alternative the DCF's AES was chosen against):
+    launch times by events behind a device-side spin, blocks per second, and
+    the two outputs compared with each other (the GPU tests compare each form
+    with the oracle)."""
+    import numpy as np
+    import torch
+
+    from suf_amd import pfss
+
+    rk = bytes(range(176))
+    outs = {k: torch.empty(blocks * 16, dtype=torch.uint8, device="cuda")
+            for k in ("ttable", "bitsliced")}
+    res = {"blocks": blocks}
+    for name in ("ttable", "bitsliced"):
+        bs = name == "bitsliced"
+        for _ in range(warmup):
+            pfss.aes128_ctr(rk, 5, 7, blocks, bitsliced=bs, out=outs[name])
+        ms = []
+        for _ in range(steps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            spin()
+            e0.record()
+            pfss.aes128_ctr(rk, 5, 7, blocks, bitsliced=bs, out=outs[name])
+            e1.record()
+            torch.cuda.synchronize()
+            ms.append(e0.elapsed_time(e1))
+        res[name + "_ms"] = float(np.median(ms))
+        res[name + "_blocks_per_s"] = blocks / (res[name + "_ms"] / 1e3)
+    res["bitsliced_over_ttable"] = res["bitsliced_ms"] / res["ttable_ms"]
+    same = bool(torch.equal(outs["ttable"], outs["bitsliced"]))
+    res["check"] = "ok" if same else "MISMATCH"
+    return res
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -862,7 +898,8 @@ def main():
                "softmax_ln": lambda: bench_softmax_ln(a.steps, a.warmup, cpu=not a.no_cpu,
                                                       shared=sh),
                "layer": lambda: bench_layer(a.steps, a.warmup, cpu=not a.no_cpu,
-                                            shared=sh)}[a.only]
+                                            shared=sh),
+               "aes": lambda: bench_aes(a.steps, a.warmup)}[a.only]
         res = run()
         print(json.dumps({"only": a.only, **res}), flush=True)
         sys.exit(0 if res["check"] in ("ok", "not run (--no-cpu)") else 1)

@@ -106,6 +106,13 @@ int sufhip_event_synchronize(void* ev);
  * key schedule); d_out: [blocks][16]. */
 int sufhip_aes128_ctr(uint8_t* d_out, const uint8_t* round_keys, uint64_t ctr_lo,
                       uint64_t ctr_hi, size_t blocks, void* stream);
+/* The same keystream (the same reference kernel replaced) computed bitsliced
+ * on the VALU: 32 counter blocks per lane as 128 32-bit slices, the S-box as
+ * tower-field inversion and affine map, no tables; d_out 16-byte aligned.
+ * It is the measured alternative to the LDS T-table AES that every other
+ * kernel uses (the DCF profile compares the two by counters). */
+int sufhip_aes128_ctr_bitsliced(uint8_t* d_out, const uint8_t* round_keys, uint64_t ctr_lo,
+                                uint64_t ctr_hi, size_t blocks, void* stream);
 
 /* myl7 PRG (third_party/myl7_fss/src/prg/aes128_mmo.c:41-52) on n seeds:
  * d_out[i][16 j .. 16 j + 16) = AES_{K_j}(seed_i) xor seed_i, j < out_blocks

@@ -8,6 +8,7 @@
 #include <random>
 #include <string>
 
+#include "aes_bitsliced.hpp"
 #include "aes_lds.hpp"
 #include "sufhip_internal.hpp"
 
@@ -54,6 +55,51 @@ __global__ void __launch_bounds__(256) aes128_ctr_kernel(uint8_t* __restrict__ o
     aes.encrypt(s0, s1, s2, s3, rkl);
     uint4 v = make_uint4(s0, s1, s2, s3);
     *reinterpret_cast<uint4*>(out + 16 * i) = v;
+  }
+}
+
+// The same keystream bitsliced (aes_bitsliced.hpp): lane g encrypts the 32
+// counter blocks 32 g .. 32 g + 31 held as 128 slices, no tables.  Block k's
+// counter is c0 + k, c0 = ctr_lo + 32 g: its low 5 bits, (c0 + k) mod 32,
+// are rotations of fixed patterns (c0 mod 32 = ctr_lo mod 32 for every
+// lane), and its bits above come from c0 - c0 mod 32 for the blocks before
+// the carry out of bit 4 and from 32 more after it.
+__global__ void __launch_bounds__(256) aes128_ctr_bs_kernel(uint8_t* __restrict__ out,
+                                                            RoundKeys rk, uint64_t ctr_lo,
+                                                            uint64_t ctr_hi, size_t blocks) {
+  const size_t groups = (blocks + 31) / 32;
+  const uint32_t low = uint32_t(ctr_lo) & 31u;
+  const uint32_t first = low == 0 ? 0xffffffffu : (1u << (32 - low)) - 1u;  // k < 32 - low
+  constexpr uint32_t kPat[5] = {0xaaaaaaaau, 0xccccccccu, 0xf0f0f0f0u, 0xff00ff00u, 0xffff0000u};
+  for (size_t g = blockIdx.x * size_t(blockDim.x) + threadIdx.x; g < groups;
+       g += size_t(gridDim.x) * blockDim.x) {
+    const uint64_t h0 = (ctr_lo + 32 * uint64_t(g)) & ~uint64_t(31), h1 = h0 + 32;
+    uint32_t s[128];
+#pragma unroll
+    for (int b = 0; b < 5; ++b)
+      s[b] = low == 0 ? kPat[b] : ((kPat[b] >> low) | (kPat[b] << (32 - low)));
+#pragma unroll
+    for (int i = 5; i < 64; ++i)
+      s[i] = (((h0 >> i) & 1u) ? first : 0u) | (((h1 >> i) & 1u) ? ~first : 0u);
+#pragma unroll
+    for (int i = 0; i < 64; ++i) s[64 + i] = 0u - uint32_t((ctr_hi >> i) & 1u);
+    aes_bs::encrypt(s, rk.w);
+    // Quarter w of the slices transposed holds word w of each block.
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t a[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) a[i] = s[32 * w + i];
+      aes_bs::transpose32(a);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) s[32 * w + i] = a[i];
+    }
+    const size_t b0 = 32 * g;
+#pragma unroll
+    for (int k = 0; k < 32; ++k)
+      if (b0 + k < blocks)
+        *reinterpret_cast<uint4*>(out + 16 * (b0 + k)) =
+            make_uint4(s[k], s[32 + k], s[64 + k], s[96 + k]);
   }
 }
 
@@ -238,6 +284,19 @@ int sufhip_aes128_ctr(uint8_t* d_out, const uint8_t* round_keys, uint64_t ctr_lo
   hipLaunchKernelGGL(aes128_ctr_kernel, dim3(capped_grid(blocks, 256)), dim3(256), 0,
                      as_stream(stream), d_out, rk, ctr_lo, ctr_hi, blocks);
   return check_launch("aes128_ctr_kernel");
+}
+
+int sufhip_aes128_ctr_bitsliced(uint8_t* d_out, const uint8_t* round_keys, uint64_t ctr_lo,
+                                uint64_t ctr_hi, size_t blocks, void* stream) {
+  if (blocks == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(d_out && round_keys, "sufhip_aes128_ctr_bitsliced: null pointer");
+  SUFHIP_REQUIRE((reinterpret_cast<uintptr_t>(d_out) & 15) == 0,
+                 "sufhip_aes128_ctr_bitsliced: d_out must be 16-byte aligned");
+  RoundKeys rk;
+  std::memcpy(rk.w, round_keys, 176);
+  hipLaunchKernelGGL(aes128_ctr_bs_kernel, dim3(capped_grid((blocks + 31) / 32, 256)), dim3(256),
+                     0, as_stream(stream), d_out, rk, ctr_lo, ctr_hi, blocks);
+  return check_launch("aes128_ctr_bs_kernel");
 }
 
 int sufhip_prg_mmo(const uint8_t* prg_state, const uint8_t* d_seeds, size_t n, int out_blocks,

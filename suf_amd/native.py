@@ -59,6 +59,7 @@ _SIGS = {
     "sufhip_event_elapsed_ms": (c_int, [c_vp, c_vp, c_vp]),
     "sufhip_event_synchronize": (c_int, [c_vp]),
     "sufhip_aes128_ctr": (c_int, [c_vp, c_vp, c_u64, c_u64, c_sz, c_vp]),
+    "sufhip_aes128_ctr_bitsliced": (c_int, [c_vp, c_vp, c_u64, c_u64, c_sz, c_vp]),
     "sufhip_prg_mmo": (c_int, [c_vp, c_vp, c_sz, c_int, c_vp, c_vp]),
     "sufhip_dcf_key_bytes": (c_sz, [c_int, c_int]),
     "sufhip_dcf_gen": (c_int, [c_int, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_vp, c_sz, c_vp,

@@ -123,10 +123,15 @@ def trunc_eval(kind, frac_bits, prg_state, key, xhat, out=None, work=None):
     return out
 
 
-def aes128_ctr(round_keys, ctr_lo, ctr_hi, blocks, device="cuda"):
-    out = torch.empty(blocks * 16, dtype=torch.uint8, device=device)
+def aes128_ctr(round_keys, ctr_lo, ctr_hi, blocks, device="cuda", bitsliced=False, out=None):
+    """AES-128-CTR keystream blocks (the LDS T-table kernel, or the bitsliced
+    one when bitsliced is true); out: optional uint8 device buffer of
+    blocks * 16 bytes."""
+    if out is None:
+        out = torch.empty(blocks * 16, dtype=torch.uint8, device=device)
     rk = native.ctypes.create_string_buffer(bytes(round_keys), 176)
-    native.call("sufhip_aes128_ctr", _ptr(out), rk, ctr_lo, ctr_hi, blocks, _stream())
+    native.call("sufhip_aes128_ctr_bitsliced" if bitsliced else "sufhip_aes128_ctr", _ptr(out),
+                rk, ctr_lo, ctr_hi, blocks, _stream())
     return out
 
 
