@@ -896,6 +896,32 @@ int sufhip_matmul_public2_planes_partial(const int8_t* d_Xp, int M, int K, int N
                                          const int8_t* d_planes, int digits, void* d_work,
                                          size_t work_bytes, const uint64_t** d_slices,
                                          void* stream);
+/* The attention's opens written by the QKV product's launch.  For the
+ * [seq x 3d] product Y = trunc(X Wqkv) (d = heads dh; M = seq, N = 3d) the
+ * launch writes no Y: element (m, c), head h and column k of the head in
+ * region j = c / d, goes as Y_0 + Y_1 - sub[j][0] - sub[j][1] to the digit
+ * planes out[j] (sufhip_kb_planes).  Every sub[j][p] is indexed
+ * [heads][seq][dh] like the head split of Y: A of QK^T, its B transposed per
+ * head, and B of PV.  The planes:
+ *   j = 0: Q_h - A    (heads, seq, dh, k_is_col 1; planes_a0 with a0 = A_0)
+ *   j = 1: K_h^T - B  (heads, dh, seq, k_is_col 0)
+ *   j = 2: V_h - B2   (heads, seq, dh, k_is_col 0)
+ * the same planes as sufhip_kb_open_split_batch over strided views of Y
+ * after sufhip_matmul_public2_planes with `trunc` (the head split of
+ * attention_block.cpp:1517-1531 and materialize_open of
+ * src/nn/matmul_beaver.cpp:34-53, in the product's epilogue).  trunc is
+ * required (a prepared table gate; its y pointers are not written); dh a
+ * multiple of 32, d of 64; the product unsliced. */
+typedef struct sufhip_qkv_opens {
+  int heads, seq, dh;
+  const uint64_t* sub[3][2];
+  sufhip_kb_planes out[3];
+} sufhip_qkv_opens;
+int sufhip_matmul_public2_planes_qkv(const int8_t* d_Xp, int M, int K, int N,
+                                     const int8_t* d_planes, int digits, uint64_t mask,
+                                     const sufhip_trunc_epilogue* trunc,
+                                     const sufhip_qkv_opens* opens, void* d_work,
+                                     size_t work_bytes, void* stream);
 int sufhip_matmul_public2(const uint64_t* d_X0, const uint64_t* d_X1, int M, int K, int N,
                           const int8_t* d_planes, int digits, uint64_t* d_out0, uint64_t* d_out1,
                           uint64_t* d_zhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,

@@ -84,6 +84,17 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// The QKV product's epilogue writing the attention's opens (on != 0): for
+// output element (m, col) of [seq x 3 d], d = heads dh, region j = col / d
+// (Q, K, V) and head h, column k of the region's head, the truncated value
+// y_0 + y_1 minus sub[j] goes to out[j]'s digit planes (Q_h - A with
+// Q_h - A + A_0, K_h^T - B, V_h - B2).
+struct QkvOpen {
+  int on, seq, dh, d;
+  sufhip_kb_planes out[3];
+  const uint64_t* sub[3][2];
+};
+
 struct PubArgs {
   const int8_t* Lp;  // [8][K/32][2M][32]
   const int8_t* Wp;  // [J][K/32][N][32]
@@ -93,7 +104,76 @@ struct PubArgs {
   uint64_t mask;
   uint64_t* part;    // [slices][2][M][N] when gridDim.z > 1
   TruncEpi epi;      // the open feeds this truncation gate (replaces zhat)
+  QkvOpen qo;        // with epi: its outputs go to the attention's opens instead
 };
+
+// The epilogue's open values v[t] of rows row[t] in column col, as the
+// attention's opens (QkvOpen).  A 64-column block lies in one region (d is a
+// multiple of 64); the subtrahends are indexed [heads][seq][dh] in every
+// region (K^T's B transposed), so a wave's loads run along its columns.
+// Every table, subtrahend and A_0 read is issued before the first plane
+// store.  Rows row[4 g .. 4 g + 3] are consecutive and start at a multiple
+// of 4 (the accumulator layout), so V's planes, whose k is the row, take one
+// 4-byte store per plane for four rows.
+template <int kN>
+__device__ __forceinline__ void qkv_open_n(const TruncEpi& e, const EpiHdrs& eh, const QkvOpen& q,
+                                           const int (&row)[kN], int col,
+                                           const uint64_t (&v)[kN]) {
+  static_assert(kN % 4 == 0, "rows in groups of four");
+  const int j = col / q.d;
+  const int n = col - j * q.d, h = n / q.dh, k = n - h * q.dh;
+  const sufhip_kb_planes& o = q.out[j];
+  const size_t hb = size_t(h) * size_t(q.seq) * size_t(q.dh);
+  uint64_t w[kN][2], sb[kN][2], a0[kN];
+#pragma unroll
+  for (int t = 0; t < kN; ++t) {
+    const size_t idx = hb + size_t(row[t]) * q.dh + k;
+    w[t][0] = trunc_table_word(eh.h[0], e.table[0], e.f, v[t]);
+    w[t][1] = trunc_table_word(eh.h[1], e.table[1], e.f, v[t]);
+    sb[t][0] = q.sub[j][0][idx];
+    sb[t][1] = q.sub[j][1][idx];
+    a0[t] = o.a0 ? o.a0[idx] : 0;
+  }
+  const size_t plane = size_t(o.batches) * size_t(q.seq) * size_t(q.dh);
+  uint64_t x[kN];
+#pragma unroll
+  for (int t = 0; t < kN; ++t)
+    x[t] = trunc_table_out(eh.h[0], e.f, v[t], w[t][0]) +
+           trunc_table_out(eh.h[1], e.f, v[t], w[t][1]) - sb[t][0] - sb[t][1];
+  if (j == 2) {
+    // V_h - B2: k = the sequence index (R = dh); four rows per 4-byte store.
+#pragma unroll
+    for (int g = 0; g < kN / 4; ++g) {
+      uint32_t pk[kDigitPlanes] = {};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        uint32_t dg[kDigitPlanes];
+        digits8(x[4 * g + t], dg);
+#pragma unroll
+        for (int i = 0; i < kDigitPlanes; ++i) pk[i] |= dg[i] << (8 * t);
+      }
+      const size_t off = hb + kblock_off(size_t(k), row[4 * g], size_t(q.dh));
+#pragma unroll
+      for (int i = 0; i < kDigitPlanes; ++i)
+        *reinterpret_cast<uint32_t*>(o.planes + i * plane + off) = pk[i];
+    }
+    return;
+  }
+  // Q_h - A and K_h^T - B: k = column k of the head (R = seq).
+#pragma unroll
+  for (int t = 0; t < kN; ++t) {
+    const size_t off = hb + kblock_off(size_t(row[t]), k, size_t(q.seq));
+    uint32_t dg[kDigitPlanes];
+    digits8(x[t], dg);
+#pragma unroll
+    for (int i = 0; i < kDigitPlanes; ++i) o.planes[i * plane + off] = int8_t(dg[i]);
+    if (o.planes_a0) {
+      digits8(x[t] + a0[t], dg);
+#pragma unroll
+      for (int i = 0; i < kDigitPlanes; ++i) o.planes_a0[i * plane + off] = int8_t(dg[i]);
+    }
+  }
+}
 
 // k-steps in the register pipeline of a wave: step st's fragments are
 // loaded pub_stages - 1 steps before its MFMAs (8 + J fragments a step).
@@ -472,15 +552,19 @@ __global__ void __launch_bounds__(256, 1) public_lds_kernel(PubArgs a) {
     for (int r = 0; r < 16; ++r) both[c][p][r][l] = v[r];
     __syncthreads();
     size_t ii[8];
+    int rr[8];
     uint64_t vv[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int r = 8 * p + q;
-      const int row = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-      ii[q] = size_t(row) * N + col;
+      rr[q] = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+      ii[q] = size_t(rr[q]) * N + col;
       vv[q] = both[c][0][r][l] + both[c][1][r][l] + a.mask;
     }
-    put_open_n<8>(a.epi, eh, a.zhat, ii, vv);
+    if (a.qo.on)
+      qkv_open_n<8>(a.epi, eh, a.qo, rr, col, vv);
+    else
+      put_open_n<8>(a.epi, eh, a.zhat, ii, vv);
   }
 }
 
@@ -599,7 +683,8 @@ namespace {
 int launch_public2(const char* what, const int8_t* Lp, int M, int K, int N,
                    const int8_t* d_planes, int digits, uint64_t* d_out0, uint64_t* d_out1,
                    uint64_t* d_zhat, uint64_t mask, const sufhip_trunc_epilogue* trunc,
-                   void* d_work, size_t work_bytes, hipStream_t s, bool partial = false) {
+                   void* d_work, size_t work_bytes, hipStream_t s, bool partial = false,
+                   const QkvOpen* qo = nullptr) {
   TruncEpi epi;
   if (int rc = make_epi(trunc, size_t(M) * N, what, &epi)) return rc;
   if (work_bytes < sufhip_matmul_public2_work_bytes(M, K, N)) {
@@ -609,7 +694,8 @@ int launch_public2(const char* what, const int8_t* Lp, int M, int K, int N,
   const int sl = pub_slices(M, K, N);
   uint64_t* part =
       reinterpret_cast<uint64_t*>(static_cast<int8_t*>(d_work) + size_t(kPlanes) * 2 * M * K);
-  PubArgs a{Lp, d_planes, M, K, N, {d_out0, d_out1}, d_zhat, mask, part, epi};
+  PubArgs a{Lp, d_planes, M, K, N, {d_out0, d_out1}, d_zhat, mask, part, epi, QkvOpen{}};
+  if (qo) a.qo = *qo;
   if (N % 64 == 0) {
     const dim3 grid(N / 64, M / 32, sl);
     switch (digits) {
@@ -706,6 +792,48 @@ int sufhip_matmul_public2_planes(const int8_t* d_Xp, int M, int K, int N, const 
                  "sufhip_matmul_public2_planes: X planes null or not 16-byte aligned");
   return launch_public2(what, d_Xp, M, K, N, d_planes, digits, d_out0, d_out1, d_zhat, mask,
                         trunc, d_work, work_bytes, as_stream(stream));
+}
+
+int sufhip_matmul_public2_planes_qkv(const int8_t* d_Xp, int M, int K, int N,
+                                     const int8_t* d_planes, int digits, uint64_t mask,
+                                     const sufhip_trunc_epilogue* trunc,
+                                     const sufhip_qkv_opens* opens, void* d_work,
+                                     size_t work_bytes, void* stream) {
+  const char* what = "sufhip_matmul_public2_planes_qkv";
+  SUFHIP_REQUIRE(opens && trunc, "sufhip_matmul_public2_planes_qkv: opens and trunc are required");
+  if (int rc = check_public2(what, M, K, N, d_planes, digits, nullptr, nullptr, nullptr, trunc,
+                             d_work))
+    return rc;
+  SUFHIP_REQUIRE(d_Xp && (reinterpret_cast<uintptr_t>(d_Xp) & 15) == 0,
+                 "sufhip_matmul_public2_planes_qkv: X planes null or not 16-byte aligned");
+  const sufhip_qkv_opens& g = *opens;
+  const long long d = (long long)g.heads * g.dh;
+  SUFHIP_REQUIRE(g.heads >= 1 && g.dh >= 32 && g.dh % 32 == 0 && d % 64 == 0 && g.seq == M &&
+                     3 * d == N && pub_slices(M, K, N) == 1,
+                 "sufhip_matmul_public2_planes_qkv: needs M = seq, N = 3 heads dh, dh a "
+                 "multiple of 32, heads dh of 64, and an unsliced product");
+  const int shape[3][3] = {{g.seq, g.dh, 1}, {g.dh, g.seq, 0}, {g.seq, g.dh, 0}};
+  QkvOpen q{};
+  q.on = 1;
+  q.seq = g.seq;
+  q.dh = g.dh;
+  q.d = int(d);
+  const size_t n = size_t(g.heads) * g.seq * g.dh;
+  for (int j = 0; j < 3; ++j) {
+    const sufhip_kb_planes& o = g.out[j];
+    SUFHIP_REQUIRE(o.planes && kb_planes_ok(o, n) && o.batches == g.heads &&
+                       o.rows == shape[j][0] && o.cols == shape[j][1] &&
+                       (o.k_is_col != 0) == (shape[j][2] != 0) && (j == 0 || !o.planes_a0) &&
+                       g.sub[j][0] && g.sub[j][1],
+                   "sufhip_matmul_public2_planes_qkv: out[j] must be the planes of Q - A "
+                   "(heads, seq, dh, k_is_col 1, optionally + A_0), K^T - B (heads, dh, seq, "
+                   "0) and V - B2 (heads, seq, dh, 0), with both shares of each subtrahend");
+    q.out[j] = o;
+    q.sub[j][0] = g.sub[j][0];
+    q.sub[j][1] = g.sub[j][1];
+  }
+  return launch_public2(what, d_Xp, M, K, N, d_planes, digits, nullptr, nullptr, nullptr, mask,
+                        trunc, d_work, work_bytes, as_stream(stream), false, &q);
 }
 
 int sufhip_matmul_public2_slices(int M, int K, int N) {

@@ -81,6 +81,16 @@ class PublicMatmulTrunc:
         eval2(None, ...): the first region of the workspace."""
         return (self.work, self.K)
 
+    def eval2_qkv(self, opens):
+        """The product of the producer-written X planes with its truncation,
+        written as the attention's opens (AttentionCore.qkv_opens: the
+        planes of Q_h - A, K_h^T - B and V_h - B2) instead of as Y
+        (sufhip_matmul_public2_planes_qkv)."""
+        epi = self.tr.epilogue((self.zhat, self.zhat))  # y is not written
+        native.call("sufhip_matmul_public2_planes_qkv", ptr(self.work), self.M, self.K, self.N,
+                    ptr(self.planes), self.digits, self.tr.mask & M64, native.ctypes.byref(epi),
+                    native.ctypes.byref(opens), ptr(self.work), self.work_bytes, stream_ptr())
+
     def slices(self):
         """The product's k-slice count (above 1, eval2_slices can leave the
         reduction and the truncation to the consumer's launch)."""
@@ -307,6 +317,10 @@ class AttentionCore:
         self.maps = {k: dev_i32(mp[k], device) for k in ("gq", "gk", "gv", "gs", "gp", "gc")}
         self.tri_qk = BatchedTriples(dealer, heads, seq, dh, seq, device)
         self.tri_pv = BatchedTriples(dealer, heads, seq, seq, dh, device)
+        # QK^T's B shares also as [heads][seq][dh] (B transposed per head), for
+        # a QKV product that subtracts them in its epilogue (qkv_opens).
+        self.qk_bt = tuple(b.reshape(heads, dh, seq).transpose(1, 2).contiguous().reshape(-1)
+                           for b in self.tri_qk.B)
         # The scores' truncation by 2f as two f-bit table gates (same floor).
         self.tr_s = [Trunc(dealer, frac_bits, self.n, prg_state, device=device)
                      for _ in range(2)]
@@ -330,6 +344,22 @@ class AttentionCore:
     def truncs(self):
         return self.tr_s + [self.tr_c] + self.softmax.truncs()
 
+    def qkv_opens(self):
+        """sufhip_qkv_opens for a QKV product that writes this core's three
+        opens itself (PublicMatmulTrunc.eval2_qkv; matrix-core products):
+        the planes of Q_h - A (with + A_0), K_h^T - B and V_h - B2."""
+        from .tasks import kb_planes_out
+        tq, tp = self.tri_qk, self.tri_pv
+        h, seq, dh = self.heads, self.seq, self.dh
+        o = native.QkvOpens()
+        o.heads, o.seq, o.dh = h, seq, dh
+        for j, sub in enumerate((tq.A, self.qk_bt, tp.B)):
+            o.sub[j][0], o.sub[j][1] = ptr(sub[0]), ptr(sub[1])
+        o.out[0] = kb_planes_out((tq.Dp, h, seq, dh, 1, tq.Xp, tq.A[0]))
+        o.out[1] = kb_planes_out((tq.Ep, h, dh, seq, 0))
+        o.out[2] = kb_planes_out((tp.Ep, h, seq, dh, 0))
+        return o
+
     def eval2(self, qkv, out, prep=None, fused=True, planes=None, sm_marks=None,
               sm_spin=None):
         """prep: (tasks.Prepared, batch) holding the key-only halves of
@@ -340,22 +370,29 @@ class AttentionCore:
         that receives two timing events around the one-launch softmax block
         (eager profiling); sm_spin: optional callable that queues device work
         before the first of them (a spin that hides the host's staging of the
-        launch, so the events bracket the kernel)."""
+        launch, so the events bracket the kernel).  qkv = None (matrix-core
+        products): the QKV product already wrote the three opens
+        (qkv_opens)."""
         seq, d, h, dh, mp = self.seq, self.d, self.heads, self.dh, self.maps
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
         # D = open(Q_h - A), E = open(K_h^T - B), and already the second
         # product's E2 = open(V_h - B2), in one launch; then the per-head products.
         hsd = h * seq * dh
+        if qkv is None and not self.mfma():
+            raise ValueError("AttentionCore.eval2: qkv = None needs the matrix-core products")
         if self.mfma():
             # The three opens go straight to the products' digit planes, each
             # head's Q, K^T and V read through a strided view of the QKV rows
             # (the index maps gq, gk, gv as strides), whole plane segments
             # per lane.
             tq, tp = self.tri_qk, self.tri_pv
-            kb_open_split([(qkv, tq.A, tq.Dp, h, seq, dh, 1, tq.Xp, tq.A[0], (0, dh, 3 * d, 1)),
-                           (qkv, tq.B, tq.Ep, h, dh, seq, 0, None, None, (d, dh, 1, 3 * d)),
-                           (qkv, tp.B, tp.Ep, h, seq, dh, 0, None, None, (2 * d, dh, 3 * d, 1))])
+            if qkv is not None:
+                kb_open_split([(qkv, tq.A, tq.Dp, h, seq, dh, 1, tq.Xp, tq.A[0],
+                                (0, dh, 3 * d, 1)),
+                               (qkv, tq.B, tq.Ep, h, dh, seq, 0, None, None, (d, dh, 1, 3 * d)),
+                               (qkv, tp.B, tp.Ep, h, seq, dh, 0, None, None,
+                                (2 * d, dh, 3 * d, 1))])
             _beaver_batched(self.D, self.E, self.tri_qk, h, seq, dh, seq, self.S, split=False)
         else:
             gq = operand(term(qkv, index=mp["gq"]), term(self.tri_qk.A, neg=True))
@@ -422,8 +459,9 @@ class TransformerLayer:
 
     def __init__(self, prg_state, weights, seq=128, d=768, heads=12, ffn=3072, frac_bits=12,
                  seed=13, device="cuda", keep_intermediates=False):
-        """keep_intermediates: also write h1, h2 and g as int64 shares (they
-        otherwise go only to the next product's digit planes)."""
+        """keep_intermediates: also write h1, Q K V, h2 and g as int64 shares
+        (they otherwise go only to the next product's digit planes, Q K V to
+        the attention's opens)."""
         self.seq, self.d, self.heads, self.ffn, self.f = seq, d, heads, ffn, frac_bits
         self.keep = keep_intermediates
         self.prg_state = bytes(prg_state)
@@ -482,11 +520,20 @@ class TransformerLayer:
         # they are written as its digit planes when the block runs fused.
         fused_ln = self.ln1.fusable() and self.ln2.fusable()
         mark()
+        # With the matrix-core attention the QKV product writes the attention's
+        # three opens as digit planes instead of Q, K and V (unsliced product,
+        # Q, K and V not kept).
+        qkv_opens = fused_ln and self.attn.mfma() and not self.keep and \
+            self.qkv.slices() == 1 and self.qkv.tr.has_table() and self.attn.dh % 32 == 0 and \
+            self.d % 64 == 0
         if fused_ln:
             self.ln1.eval2(x, self.h1, prep=(prep, b(0)), planes=self.qkv.x_planes(),
                            write_out=self.keep)
             mark()
-            self.qkv.eval2(None, self.qkvs)
+            if qkv_opens:
+                self.qkv.eval2_qkv(self.attn.qkv_opens())
+            else:
+                self.qkv.eval2(None, self.qkvs)
         else:
             self.ln1.eval2(x, self.h1, prep=(prep, b(0)))
             mark()
@@ -495,8 +542,8 @@ class TransformerLayer:
         mark()
         pre = None
         if self.attn.mfma():
-            self.attn.eval2(self.qkvs, self.ctx, prep=(prep, b(1)), planes=self.proj.x_planes(),
-                            sm_marks=sm_marks, sm_spin=sm_spin)
+            self.attn.eval2(None if qkv_opens else self.qkvs, self.ctx, prep=(prep, b(1)),
+                            planes=self.proj.x_planes(), sm_marks=sm_marks, sm_spin=sm_spin)
             mark()
             prep.wait(b(2))
             if fused_ln and self.proj.slices() > 1 and self.proj.tr.has_table():

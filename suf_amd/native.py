@@ -110,6 +110,8 @@ _SIGS = {
     "sufhip_matmul_public2_slices": (c_int, [c_int, c_int, c_int]),
     "sufhip_matmul_public2_planes_partial": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp,
                                                      c_sz, c_vp, c_vp]),
+    "sufhip_matmul_public2_planes_qkv": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_int, c_u64,
+                                                 c_vp, c_vp, c_vp, c_sz, c_vp]),
     "sufhip_matmul_public2": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_vp,
                                       c_vp, c_u64, c_vp, c_vp, c_sz, c_vp]),
     "sufhip_trunc_finish2": (c_int, [c_int, c_int, c_vp, c_vp, c_vp, c_sz, c_vp, c_sz, c_vp, c_vp,
@@ -221,6 +223,12 @@ class KbPlanes(ctypes.Structure):
     """sufhip_kb_planes (include/suf_hip.h)."""
     _fields_ = [("planes", c_vp), ("batches", c_int), ("rows", c_int), ("cols", c_int),
                 ("k_is_col", c_int), ("planes_a0", c_vp), ("a0", c_vp)]
+
+
+class QkvOpens(ctypes.Structure):
+    """sufhip_qkv_opens (include/suf_hip.h)."""
+    _fields_ = [("heads", c_int), ("seq", c_int), ("dh", c_int), ("sub", (c_vp * 2) * 3),
+                ("out", KbPlanes * 3)]
 
 
 class Lin2Job(ctypes.Structure):

@@ -218,6 +218,50 @@ def test_layernorm_in_slices_several_rows_per_workgroup(rows, cols, slices):
         assert np.array_equal(u64(h_got[p]), u64(h_want[p])), ("h", p)
 
 
+@pytest.mark.parametrize("seq,d,heads", [(64, 128, 2), (128, 768, 12)])
+def test_qkv_product_writes_attention_opens(seq, d, heads):
+    """The QKV product writing the attention's three opens in its epilogue
+    (sufhip_matmul_public2_planes_qkv) gives the same digit planes (Q_h - A
+    with + A_0, K_h^T - B, V_h - B2) as the product's truncated output
+    followed by the strided-view open-and-split launch."""
+    say("qkv product -> attention opens seq=%d d=%d heads=%d" % (seq, d, heads))
+    dealer = Dealer(7)
+    x = pfss.host_normal_fixed(101, 1.0, 0.0, F, seq * d)
+    xin = tuple(dev(v) for v in _pair(x, 102))
+    W = pfss.host_normal_fixed(103, 0.05, 0.0, F, d * 3 * d).view(np.int64).reshape(d, 3 * d)
+    pm = layer.PublicMatmulTrunc(seq, d, 3 * d, W, dealer, STATE, F)
+    assert pm.slices() == 1
+    attn = layer.AttentionCore(seq, d, heads, dealer, STATE, F)
+    assert attn.mfma()
+    pm.tr.prepare()
+    qkv = tuple(torch.empty(seq * 3 * d, dtype=torch.int64, device="cuda") for _ in range(2))
+    pm.eval2(xin, qkv)  # X's planes stay in the product's workspace
+    tq, tp = attn.tri_qk, attn.tri_pv
+    dh = d // heads
+    planes = [tq.Dp, tq.Xp, tq.Ep, tp.Ep]
+    layer.kb_open_split([(qkv, tq.A, tq.Dp, heads, seq, dh, 1, tq.Xp, tq.A[0], (0, dh, 3 * d, 1)),
+                         (qkv, tq.B, tq.Ep, heads, dh, seq, 0, None, None, (d, dh, 1, 3 * d)),
+                         (qkv, tp.B, tp.Ep, heads, seq, dh, 0, None, None,
+                          (2 * d, dh, 3 * d, 1))])
+    torch.cuda.synchronize()
+    want = [t.clone() for t in planes]
+    for t in planes:
+        t.fill_(0x5a5a)  # every planes byte must be written
+    pm.eval2_qkv(attn.qkv_opens())
+    torch.cuda.synchronize()
+    nbytes = native.load().sufhip_kb_planes_bytes(heads, seq, dh)
+    for i, (g_, w_) in enumerate(zip(planes, want)):
+        assert torch.equal(g_.view(torch.uint8)[:nbytes], w_.view(torch.uint8)[:nbytes]), i
+    # Refused on the host: K^T's planes with the row-side layout.
+    bad = attn.qkv_opens()
+    bad.out[1].k_is_col = 1
+    with pytest.raises(native.SufHipError, match="out\\[j\\]"):
+        epi = pm.tr.epilogue((pm.zhat, pm.zhat))
+        native.call("sufhip_matmul_public2_planes_qkv", pm.work.data_ptr(), seq, d, 3 * d,
+                    pm.planes.data_ptr(), pm.digits, pm.tr.mask, native.ctypes.byref(epi),
+                    native.ctypes.byref(bad), pm.work.data_ptr(), pm.work_bytes, 0)
+
+
 def test_lin2_batch_matches_single_launches():
     """Four opens of different sizes in one launch equal four sufhip_lin2
     calls; a batch with a bad operand is refused on the host."""
