@@ -176,7 +176,101 @@ struct SplitWalkArgs {
   SplitArgs s;
   WalkJobs<kFusedWalkJobs> w;
   uint32_t walk_groups;
+  // Column-side jobs split by tiles (split_tile): tiles [tbegin[t],
+  // tbegin[t + 1]) belong to job tjob[t]; their workgroups follow the walk's.
+  int tcount;
+  int tjob[kSplitJobs];
+  uint32_t tbegin[kSplitJobs + 1];
+  uint32_t tile_groups;
 };
+
+// Column-side jobs (k runs along the source rows) by 32 (k) x 64 (column)
+// tiles through LDS: each wave reads 64 consecutive columns of one row (512
+// contiguous bytes per source array), the workgroup forms the values in LDS,
+// and lane (column c, quarter q) writes bytes 8 q .. 8 q + 7 of column c's
+// 32-byte plane segment, so four adjacent lanes write a segment whole and a
+// wave 512 contiguous bytes per plane.  The lane form reads 16 rows per lane
+// (two 256-byte runs per wave and load).
+constexpr int kTileK = 32, kTileN = 64;
+using SplitTile = uint64_t[kTileK][kTileN + 1];  // + 1: the column reads spread over banks
+
+__device__ __forceinline__ void split_tile(const SplitArgs& a, int j, uint32_t tile,
+                                           SplitTile& E) {
+  const int K = a.rows[j], N = a.cols[j];
+  const uint32_t tn = uint32_t(N / kTileN), per_b = tn * uint32_t(K / kTileK);
+  const uint32_t b = tile / per_b, rem = tile - b * per_b;
+  const int kb = int(rem / tn), nb = int(rem - (rem / tn) * tn);
+  const size_t bk = size_t(b) * size_t(K) * size_t(N);
+  const size_t base = bk + size_t(kb) * kTileK * N + size_t(nb) * kTileN;
+  uint64_t v[kTileK * kTileN / 256];
+#pragma unroll
+  for (int i = 0; i < kTileK * kTileN / 256; ++i) {
+    const int e = int(threadIdx.x) + 256 * i;
+    const size_t idx = base + size_t(e / kTileN) * N + (e % kTileN);
+    v[i] = split_val(a, j, idx, idx);
+  }
+  __syncthreads();  // the previous tile's column reads are done
+#pragma unroll
+  for (int i = 0; i < kTileK * kTileN / 256; ++i) {
+    const int e = int(threadIdx.x) + 256 * i;
+    E[e / kTileN][e % kTileN] = v[i];
+  }
+  __syncthreads();
+  const int c = int(threadIdx.x >> 2), q = int(threadIdx.x & 3);
+  uint32_t pk[kDigitPlanes][2] = {};
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    uint32_t d[kDigitPlanes];
+    digits8(E[8 * q + t][c], d);
+#pragma unroll
+    for (int i = 0; i < kDigitPlanes; ++i) pk[i][t >> 2] |= d[i] << (8 * (t & 3));
+  }
+  const size_t plane = size_t(a.batches[j]) * size_t(K) * size_t(N);
+  const size_t off = bk + kblock_off(size_t(nb) * kTileN + c, kTileK * kb + 8 * q, size_t(N));
+#pragma unroll
+  for (int i = 0; i < kDigitPlanes; ++i)
+    *reinterpret_cast<uint2*>(a.planes[j] + i * plane + off) = make_uint2(pk[i][0], pk[i][1]);
+}
+
+// Walks (workgroups below walk_groups, with kWalk), tiles (the next
+// tile_groups, one tile each: more tiles per workgroup measured slower), then
+// the other jobs' lanes at 4 k per lane.  Beside the walks the tiles beat the
+// lane form (25.7 against 26.6 us at config 3's shape); alone they do not
+// (22.0 against 20.6 us for the triples' planes), so only the launch with
+// walks uses them.
+template <bool kWalk>
+__global__ void __launch_bounds__(256) kb_split_tiled_kernel(SplitWalkArgs a) {
+  __shared__ SplitTile E;
+  const uint32_t wg = kWalk ? a.walk_groups : 0u;
+  if constexpr (kWalk) {
+    __shared__ __align__(16) uint32_t tab[FusedAes::kWords];
+    __shared__ uint4 rkl[4 * 11];
+    if (blockIdx.x < wg) {
+      fill_ttable<kFusedCopies>(tab, kTDev.v);
+      fill_round_keys(rkl, a.w.prg.rk, 4);
+      __syncthreads();
+      const FusedAes aes{tab, threadIdx.x % kFusedCopies};
+      const uint32_t gl = blockIdx.x * 256 + threadIdx.x;
+      const uint32_t g = gl >> 3;  // walk; whole 8-lane groups leave together
+      if (g >= a.w.begin[a.w.count]) return;
+      const int j = batch_job<kFusedWalkJobs>(a.w.begin, a.w.count, g);
+      walk_leaf_path(aes, rkl, a.w.key[j], a.w.out[j], a.w.geo[j], g - a.w.begin[j], gl);
+      return;
+    }
+  }
+  if (blockIdx.x < wg + a.tile_groups) {
+    const uint32_t total = a.tbegin[a.tcount];
+    for (uint32_t t = blockIdx.x - wg; t < total; t += a.tile_groups) {
+      int u = 0;
+      while (u + 1 < a.tcount && t >= a.tbegin[u + 1]) ++u;
+      split_tile(a.s, a.tjob[u], t - a.tbegin[u], E);
+    }
+    return;
+  }
+  const uint32_t first = wg + a.tile_groups;
+  split_lanes<4, 4>(a.s, size_t(blockIdx.x - first) * 256 + threadIdx.x,
+                    size_t(gridDim.x - first) * 256);
+}
 
 static_assert(sizeof(SplitWalkArgs) <= 4096, "kernel argument block must fit in 4 KB");
 
@@ -542,6 +636,54 @@ void plan_split(SplitArgs& a, int count, int* ck, int* rk) {
                                       size_t(a.k_is_col[j] ? *rk : *ck);
 }
 
+// Column-side jobs go by tiles (split_tile) when the launch is large enough
+// for 16 k per lane and every such job is plain (no view), without the
+// planes of + a0, and has a multiple of 64 columns.  Fills f's tile fields
+// and gives those jobs no lanes in f.s.begin (the other jobs keep theirs at
+// 4 k per lane); false leaves f untouched.
+bool plan_tiles(SplitWalkArgs& f, int count, int ck) {
+  SplitArgs& a = f.s;
+  if (ck != 16) return false;
+  int n = 0;
+  for (int j = 0; j < count; ++j) {
+    if (a.k_is_col[j]) continue;
+    if ((a.view[j][0] | a.view[j][1] | a.view[j][2]) || a.planes_a0[j] || a.cols[j] % kTileN)
+      return false;
+    ++n;
+  }
+  if (n == 0) return false;
+  f.tcount = 0;
+  f.tbegin[0] = 0;
+  a.begin[0] = 0;
+  for (int j = 0; j < count; ++j) {
+    const size_t elems = size_t(a.batches[j]) * a.rows[j] * a.cols[j];
+    if (a.k_is_col[j]) {
+      a.begin[j + 1] = a.begin[j] + elems / 4;
+      continue;
+    }
+    a.begin[j + 1] = a.begin[j];
+    f.tjob[f.tcount] = j;
+    f.tbegin[f.tcount + 1] = f.tbegin[f.tcount] + uint32_t(elems / (kTileK * kTileN));
+    ++f.tcount;
+  }
+  int cus = 256, dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const uint32_t tiles = f.tbegin[f.tcount], cap = uint32_t(cus) * 8;
+  f.tile_groups = tiles < cap ? tiles : cap;
+  return true;
+}
+
+template <bool kWalk>
+int launch_tiled(SplitWalkArgs& f, void* stream) {
+  size_t g = (f.s.begin[f.s.count] + 255) / 256;
+  if (g > 4096) g = 4096;
+  const size_t wg = kWalk ? f.walk_groups : 0;
+  hipLaunchKernelGGL((kb_split_tiled_kernel<kWalk>), dim3(unsigned(wg + f.tile_groups + g)),
+                     dim3(256), 0, as_stream(stream), f);
+  return check_launch("kb_split_tiled_kernel");
+}
+
 int launch_split(SplitArgs& a, int count, void* stream) {
   int ck = 0, rk = 0;
   plan_split(a, count, &ck, &rk);
@@ -566,10 +708,11 @@ int launch_split_walk(SplitWalkArgs& f, int count, void* stream) {
   plan_split(f.s, count, &ck, &rk);
   const size_t walk_lanes_n = 8 * size_t(f.w.begin[f.w.count]);
   const size_t wg = (walk_lanes_n + 255) / 256;
+  f.walk_groups = uint32_t(wg);
+  if (plan_tiles(f, count, ck)) return launch_tiled<true>(f, stream);
   size_t g = (f.s.begin[count] + 255) / 256;
   if (g > 4096) g = 4096;
   if (wg + g == 0) return SUFHIP_OK;
-  f.walk_groups = uint32_t(wg);
   const dim3 grid(unsigned(wg + (g > 0 ? g : 0)));
   if (ck == 16)
     hipLaunchKernelGGL((kb_split_walk_kernel<16, 4>), grid, dim3(256), 0, as_stream(stream), f);

@@ -670,22 +670,27 @@ def test_kb_open_split_two_jobs_mixed():
         assert torch.equal(job[2].view(torch.uint8)[:nbytes], want.view(torch.uint8)[:nbytes])
 
 
-@pytest.mark.parametrize("gates,f,n", [(1, 12, 4096), (2, 7, 100), (1, 14, 4096), (5, 12, 4096),
-                                       (1, 20, 1 << 16), (1, 20, 4096)])
-def test_kb_open_split_prepare_matches_separate_calls(gates, f, n):
+@pytest.mark.parametrize("gates,f,n,big", [(1, 12, 4096, False), (2, 7, 100, False),
+                                           (1, 14, 4096, False), (5, 12, 4096, False),
+                                           (1, 20, 1 << 16, False), (1, 20, 4096, False),
+                                           (1, 12, 128 * 3072, True)])
+def test_kb_open_split_prepare_matches_separate_calls(gates, f, n, big):
     """The opens with the truncations' key-only walks in the same launch
     (sufhip_kb_open_split_prepare) write the same digit planes as the opens
     alone and the same workspaces as the batched prepare.  One or two table
     gates run in the one launch; f = 14 (walks past three quarters of a walk
     workgroup per CU), five gates (ten jobs, above eight), f = 20 with 2^16
     points (expansion launches) and f = 20 with 4096 points (a depth-12
-    frontier, not a table) take the prepare's own launches first."""
+    frontier, not a table) take the prepare's own launches first.  big: the
+    matmul gate's shapes (D 128 x 768 with the planes of + A_0, E 768 x 3072),
+    whose E goes by LDS tiles beside the walks."""
     from suf_amd.tasks import Trunc, prepare_batch
-    print("[gpu-case] kb_open_split_prepare", gates, f, n, flush=True)
+    print("[gpu-case] kb_open_split_prepare", gates, f, n, big, flush=True)
     g = np.random.default_rng(11)
     dealer = Dealer(21)
     trs = [Trunc(dealer, f, n, STATE) for _ in range(gates)]
-    specs = [(1, 64, 96, 1, True), (2, 32, 64, 0, False)]
+    specs = [(1, 128, 768, 1, True), (1, 768, 3072, 0, True)] if big else \
+        [(1, 64, 96, 1, True), (2, 32, 64, 0, False)]
     jobs, got_planes, want_planes = [], [], []
     for nb, r, c, kc, use_b in specs:
         m = nb * r * c
