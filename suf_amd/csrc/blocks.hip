@@ -23,9 +23,14 @@
 namespace sufhip {
 namespace {
 
-constexpr int kLnBlock = 256;
-constexpr int kLnWaves = kLnBlock / 64;
-constexpr int kLnMaxPer = 8;  // elements per thread: cols <= 2048
+// Rows of up to 1024 elements: 512 threads, up to two elements each (half
+// the per-thread element work of 256 threads; the first LayerNorm of the
+// layer 22.6 -> 21.4 us).  Longer rows (up to 2048): 256 threads, up to eight
+// elements each (at 512 threads eight elements spill).
+constexpr int kLnBlock = 512;
+constexpr int kLnWideBlock = 256;
+constexpr int kLnMaxPer = 2;      // elements per thread at kLnBlock: cols <= 1024
+constexpr int kLnWidePer = 8;     // at kLnWideBlock: cols <= 2048
 constexpr int kLnCopies = 4;  // the T table serves one lane per workgroup
 using LnAes = AesLds<kLnCopies>;  // one lane's chain: the small table fills fastest
 
@@ -45,14 +50,15 @@ struct LnArgs {
 
 enum { kTrMean = 0, kTrVar0 = 1, kTrVar1 = 2, kTrNorm = 3, kTrIn = 4 };
 constexpr int kLnMaxSlices = 8;
-constexpr int kLnMaxInPer = 4;  // in_slices rows of up to 1024 elements
+constexpr int kLnMaxInPer = kLnMaxPer;  // in_slices rows of up to 1024 elements
 
 // Every load that does not depend on an open is issued when the row starts:
 // x, both triples' shares, and (lane 0) the rsqrt chain's triples; the key
 // headers of all truncation gates sit in LDS.  What remains serial per row
 // is one table read per truncation gate and the rsqrt LUT's AES.
-template <int kPer, bool kIn>
-__global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
+template <int kPer, bool kIn, int kBlock>
+__global__ void __launch_bounds__(kBlock) layernorm2_kernel(LnArgs A) {
+  constexpr int kLnWaves = kBlock / 64;
   __shared__ __align__(16) uint32_t tab[256 * kLnCopies];
   __shared__ ChainLds L;
   constexpr int kRsProds = chain_products<SUFHIP_CHAIN_RSQRT>();
@@ -98,7 +104,7 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
       uint64_t ad[kPer][2];
 #pragma unroll
       for (int k = 0; k < kPer; ++k) {
-        const int c = threadIdx.x + k * kLnBlock;
+        const int c = threadIdx.x + k * kBlock;
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
           d[k][p] = 0;
@@ -116,7 +122,7 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
         uint64_t t[kPer][2][kN];
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
-          const int c = threadIdx.x + k * kLnBlock;
+          const int c = threadIdx.x + k * kBlock;
           const size_t e = c < cols ? base + c : base;
 #pragma unroll
           for (int p = 0; p < 2; ++p)
@@ -139,7 +145,7 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
       for (; z0 < ns; ++z0) add_slices(z0, std::integral_constant<int, 1>{});
 #pragma unroll
       for (int k = 0; k < kPer; ++k) {
-        if (threadIdx.x + k * kLnBlock >= cols) d[k][0] = d[k][1] = 0;
+        if (threadIdx.x + k * kBlock >= cols) d[k][0] = d[k][1] = 0;
       }
       uint64_t zh[kPer], w[kPer][2];
 #pragma unroll
@@ -150,7 +156,7 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
       }
 #pragma unroll
       for (int k = 0; k < kPer; ++k) {
-        const int c = threadIdx.x + k * kLnBlock;
+        const int c = threadIdx.x + k * kBlock;
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
           d[k][p] = c < cols ? trunc_table_out(th[kTrIn][p], ti.f, zh[k], w[k][p]) + ad[k][p] : 0;
@@ -160,14 +166,14 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
     } else {
 #pragma unroll
       for (int k = 0; k < kPer; ++k) {
-        const int c = threadIdx.x + k * kLnBlock;
+        const int c = threadIdx.x + k * kBlock;
 #pragma unroll
         for (int p = 0; p < 2; ++p) d[k][p] = c < cols ? A.x[p][base + c] : 0;
       }
     }
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const int c = threadIdx.x + k * kLnBlock;
+      const int c = threadIdx.x + k * kBlock;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         sa[k][p] = c < cols ? A.sq.a[p][base + c] : 0;
@@ -177,7 +183,7 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
     }
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const int c = threadIdx.x + k * kLnBlock;
+      const int c = threadIdx.x + k * kBlock;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         na[k][p] = c < cols ? A.norm.a[p][base + c] : 0;
@@ -198,7 +204,7 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
     uint64_t q0 = 0, q1 = 0;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const int c = threadIdx.x + k * kLnBlock;
+      const int c = threadIdx.x + k * kBlock;
       if (c < cols) {
         d[k][0] -= mu.v[0];
         d[k][1] -= mu.v[1];
@@ -227,7 +233,7 @@ __global__ void __launch_bounds__(kLnBlock) layernorm2_kernel(LnArgs A) {
     const uint64_t ee = (bc[0] - nb0) + (bc[1] - nb1);
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const int c = threadIdx.x + k * kLnBlock;
+      const int c = threadIdx.x + k * kBlock;
       if (c < cols) {
         const size_t i = base + c;
         const uint64_t dd = (d[k][0] - na[k][0]) + (d[k][1] - na[k][1]);
@@ -813,7 +819,7 @@ extern "C" {
 int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
   SUFHIP_REQUIRE(args != nullptr, "sufhip_layernorm2: null args");
   const sufhip_layernorm2_args& g = *args;
-  SUFHIP_REQUIRE(g.rows >= 0 && g.cols >= 1 && g.cols <= kLnBlock * kLnMaxPer,
+  SUFHIP_REQUIRE(g.rows >= 0 && g.cols >= 1 && g.cols <= kLnWideBlock * kLnWidePer,
                  "sufhip_layernorm2: cols in [1, 2048]");
   if (g.rows == 0) return SUFHIP_OK;
   SUFHIP_REQUIRE((g.in_slices || (g.x[0] && g.x[1])) &&
@@ -870,21 +876,20 @@ int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
   hipStream_t s = as_stream(stream);
   if (A.in_slices) {
     if (per <= 1)
-      hipLaunchKernelGGL((layernorm2_kernel<1, true>), dim3(grid), dim3(kLnBlock), 0, s, A);
-    else if (per <= 2)
-      hipLaunchKernelGGL((layernorm2_kernel<2, true>), dim3(grid), dim3(kLnBlock), 0, s, A);
+      hipLaunchKernelGGL((layernorm2_kernel<1, true, kLnBlock>), dim3(grid), dim3(kLnBlock), 0, s,
+                         A);
     else
-      hipLaunchKernelGGL((layernorm2_kernel<kLnMaxInPer, true>), dim3(grid), dim3(kLnBlock), 0,
-                         s, A);
+      hipLaunchKernelGGL((layernorm2_kernel<kLnMaxInPer, true, kLnBlock>), dim3(grid),
+                         dim3(kLnBlock), 0, s, A);
   } else if (per <= 1) {
-    hipLaunchKernelGGL((layernorm2_kernel<1, false>), dim3(grid), dim3(kLnBlock), 0, s, A);
-  } else if (per <= 2) {
-    hipLaunchKernelGGL((layernorm2_kernel<2, false>), dim3(grid), dim3(kLnBlock), 0, s, A);
-  } else if (per <= 4) {
-    hipLaunchKernelGGL((layernorm2_kernel<4, false>), dim3(grid), dim3(kLnBlock), 0, s, A);
-  } else {
-    hipLaunchKernelGGL((layernorm2_kernel<kLnMaxPer, false>), dim3(grid), dim3(kLnBlock), 0, s,
+    hipLaunchKernelGGL((layernorm2_kernel<1, false, kLnBlock>), dim3(grid), dim3(kLnBlock), 0, s,
                        A);
+  } else if (per <= kLnMaxPer) {
+    hipLaunchKernelGGL((layernorm2_kernel<kLnMaxPer, false, kLnBlock>), dim3(grid),
+                       dim3(kLnBlock), 0, s, A);
+  } else {
+    hipLaunchKernelGGL((layernorm2_kernel<kLnWidePer, false, kLnWideBlock>), dim3(grid),
+                       dim3(kLnWideBlock), 0, s, A);
   }
   return check_launch("layernorm2_kernel");
 }
