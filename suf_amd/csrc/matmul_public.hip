@@ -586,8 +586,25 @@ __global__ void __launch_bounds__(256)
                          uint64_t* out1, uint64_t* zhat, uint64_t mask, TruncEpi epi) {
   const EpiHdrs eh = epi_hdrs(epi);
   for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < mn; i += size_t(gridDim.x) * 256) {
+    // Slices in groups of four, then one by one, every load of a group
+    // issued before its adds: a loop of single slices waits for each
+    // slice's loads before it issues the next.
     uint64_t v0 = 0, v1 = 0;
-    for (int z = 0; z < slices; ++z) {
+    int z = 0;
+    for (; z + 4 <= slices; z += 4) {
+      uint64_t t[4][2];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        t[u][0] = part[(size_t(z + u) * 2 + 0) * mn + i];
+        t[u][1] = part[(size_t(z + u) * 2 + 1) * mn + i];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v0 += t[u][0];
+        v1 += t[u][1];
+      }
+    }
+    for (; z < slices; ++z) {
       v0 += part[(size_t(z) * 2 + 0) * mn + i];
       v1 += part[(size_t(z) * 2 + 1) * mn + i];
     }
