@@ -638,7 +638,10 @@ __global__ void __launch_bounds__(kSmTeamThreads) softmax2_team_kernel(SmArgs a)
   __shared__ uint64_t invs[kSmWaves][2];           // the row's reciprocal shares
   extern __shared__ uint64_t rowbuf[];
   const int mr = a.max_row;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // Wave-uniform (a scalar register): the row offsets then load through the
+  // scalar cache and the team's branches are scalar branches.
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
   const int slot = wave >> 1, tw = wave & 1;  // row slot in the group, wave in the team
   const int j = lane + 64 * tw;               // this lane's element of the row
   uint64_t* even = rowbuf + size_t(slot) * tree_row_words(mr);
