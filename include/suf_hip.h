@@ -541,6 +541,17 @@ typedef struct sufhip_layernorm2_args {
   int in_slice_count;
   sufhip_trunc_epilogue tr_in;
   uint64_t in_mask;
+  /* Optional (walk_count > 0): the key-only halves of other truncation gates,
+   * as sufhip_trunc_prepare_batch(walk_prg_state, walk_jobs, walk_count)
+   * would write them, for gates that later launches evaluate (the prepare of
+   * transformer_layer_forward's later truncations, src/nn/
+   * transformer_layer.cpp:435-830).  Up to 24 table-gate jobs (f <= 14) run
+   * as extra workgroups of this launch, on the CUs its rows leave free; other
+   * job sets go through sufhip_trunc_prepare_batch on the same stream first.
+   * The results are byte-equal either way. */
+  const sufhip_trunc_job* walk_jobs;
+  int walk_count;
+  const uint8_t* walk_prg_state;
 } sufhip_layernorm2_args;
 int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream);
 

@@ -19,6 +19,7 @@
 #include "digit_planes.hpp"
 #include "reduce_device.hpp"
 #include "relu_tree_device.hpp"
+#include "walk_device.hpp"
 
 namespace sufhip {
 namespace {
@@ -33,6 +34,11 @@ constexpr int kLnMaxPer = 2;      // elements per thread at kLnBlock: cols <= 10
 constexpr int kLnWidePer = 8;     // at kLnWideBlock: cols <= 2048
 constexpr int kLnCopies = 4;  // the T table serves one lane per workgroup
 using LnAes = AesLds<kLnCopies>;  // one lane's chain: the small table fills fastest
+// Key-only walks of later gates' tables, run by the workgroups past the rows'
+// (walk_device.hpp): up to kLnWalkJobs jobs, on their own 16-copy T table.
+constexpr int kLnWalkJobs = 24;
+constexpr int kLnWalkCopies = 16;
+using LnWalkAes = AesLds<kLnWalkCopies>;
 
 struct LnArgs {
   const uint64_t* x[2];
@@ -46,7 +52,24 @@ struct LnArgs {
   sufhip_x_planes xp;
   const uint64_t* in_slices;  // optional: [slices][2][rows cols] partial products
   int in_count;
+  int row_groups;              // workgroups [0, row_groups) run the rows
+  WalkJobs<kLnWalkJobs> w;     // the others walk these jobs' tables
 };
+static_assert(sizeof(LnArgs) <= 4096, "kernel argument blocks must fit in 4 KB");
+
+// Lane gl of the walk role: the node of walk gl / 8 and its table entries.
+__device__ __forceinline__ void ln_walk_role(const WalkJobs<kLnWalkJobs>& w, uint32_t gl) {
+  __shared__ __align__(16) uint32_t wtab[LnWalkAes::kWords];
+  __shared__ uint4 rkl[4 * 11];
+  fill_ttable<kLnWalkCopies>(wtab, kTDev.v);
+  fill_round_keys(rkl, w.prg.rk, 4);
+  __syncthreads();
+  const LnWalkAes aes{wtab, threadIdx.x % kLnWalkCopies};
+  const uint32_t g = gl >> 3;  // whole 8-lane groups leave together
+  if (g >= w.begin[w.count]) return;
+  const int j = batch_job<kLnWalkJobs>(w.begin, w.count, g);
+  walk_table(aes, rkl, w.key[j], w.out[j], w.geo[j], g - w.begin[j], gl);
+}
 
 enum { kTrMean = 0, kTrVar0 = 1, kTrVar1 = 2, kTrNorm = 3, kTrIn = 4 };
 constexpr int kLnMaxSlices = 8;
@@ -59,6 +82,10 @@ constexpr int kLnMaxInPer = kLnMaxPer;  // in_slices rows of up to 1024 elements
 template <int kPer, bool kIn, int kBlock>
 __global__ void __launch_bounds__(kBlock) layernorm2_kernel(LnArgs A) {
   constexpr int kLnWaves = kBlock / 64;
+  if (int(blockIdx.x) >= A.row_groups) {
+    ln_walk_role(A.w, (blockIdx.x - A.row_groups) * kBlock + threadIdx.x);
+    return;
+  }
   __shared__ __align__(16) uint32_t tab[256 * kLnCopies];
   __shared__ ChainLds L;
   constexpr int kRsProds = chain_products<SUFHIP_CHAIN_RSQRT>();
@@ -87,7 +114,7 @@ __global__ void __launch_bounds__(kBlock) layernorm2_kernel(LnArgs A) {
                 trunc_table_eval_h(th[j][1], A.tr[j].table[1], A.tr[j].f, v)}};
   };
   const int cols = A.cols;
-  for (int r = blockIdx.x; r < A.rows; r += gridDim.x) {
+  for (int r = blockIdx.x; r < A.rows; r += A.row_groups) {
     const size_t base = size_t(r) * size_t(cols);
     // The row's rsqrt triples, one word per lane (visible to lane 0 after
     // the row sum's barriers).
@@ -824,7 +851,12 @@ int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
   const sufhip_layernorm2_args& g = *args;
   SUFHIP_REQUIRE(g.rows >= 0 && g.cols >= 1 && g.cols <= kLnWideBlock * kLnWidePer,
                  "sufhip_layernorm2: cols in [1, 2048]");
-  if (g.rows == 0) return SUFHIP_OK;
+  SUFHIP_REQUIRE(g.walk_count >= 0 && (g.walk_count == 0 || (g.walk_jobs && g.walk_prg_state)),
+                 "sufhip_layernorm2: walk_count >= 0, walk jobs and PRG state given");
+  if (g.rows == 0)
+    return g.walk_count > 0
+               ? sufhip_trunc_prepare_batch(g.walk_prg_state, g.walk_jobs, g.walk_count, stream)
+               : SUFHIP_OK;
   SUFHIP_REQUIRE((g.in_slices || (g.x[0] && g.x[1])) &&
                      (g.out[0] == nullptr) == (g.out[1] == nullptr) &&
                      (g.out[0] || g.out_planes.planes),
@@ -876,22 +908,45 @@ int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   const int grid = g.rows < cus * 8 ? g.rows : cus * 8;
   const int per = (g.cols + kLnBlock - 1) / kLnBlock;
+  const int block = per <= kLnMaxPer || A.in_slices ? kLnBlock : kLnWideBlock;
+  A.row_groups = grid;
+  // The walks: one workgroup per CU fits beside the rows' (the kernel's
+  // registers allow one), so the CUs without a row hold one pass of them.
+  size_t walk_groups = 0;
+  if (g.walk_count > 0) {
+    const size_t room = size_t(cus > grid ? cus - grid : 0) * size_t(block);
+    bool one = false;
+    if (int rc = trunc_walk_plan_fit(g.walk_prg_state, g.walk_jobs, g.walk_count, kLnWalkJobs,
+                                     room, A.w.begin, A.w.key, A.w.out, A.w.geo, &one,
+                                     "sufhip_layernorm2 walk"))
+      return rc;
+    if (one) {
+      fill_prg4(g.walk_prg_state, &A.w.prg);
+      A.w.count = g.walk_count;
+      walk_groups = (8 * size_t(A.w.begin[A.w.count]) + block - 1) / size_t(block);
+    } else if (int rc = sufhip_trunc_prepare_batch(g.walk_prg_state, g.walk_jobs, g.walk_count,
+                                                   stream)) {
+      return rc;
+    }
+  }
+  SUFHIP_REQUIRE(size_t(grid) + walk_groups <= 0x7fffffffu, "sufhip_layernorm2: grid too large");
+  const dim3 launch(unsigned(size_t(grid) + walk_groups));
   hipStream_t s = as_stream(stream);
   if (A.in_slices) {
     if (per <= 1)
-      hipLaunchKernelGGL((layernorm2_kernel<1, true, kLnBlock>), dim3(grid), dim3(kLnBlock), 0, s,
+      hipLaunchKernelGGL((layernorm2_kernel<1, true, kLnBlock>), launch, dim3(kLnBlock), 0, s,
                          A);
     else
-      hipLaunchKernelGGL((layernorm2_kernel<kLnMaxInPer, true, kLnBlock>), dim3(grid),
+      hipLaunchKernelGGL((layernorm2_kernel<kLnMaxInPer, true, kLnBlock>), launch,
                          dim3(kLnBlock), 0, s, A);
   } else if (per <= 1) {
-    hipLaunchKernelGGL((layernorm2_kernel<1, false, kLnBlock>), dim3(grid), dim3(kLnBlock), 0, s,
+    hipLaunchKernelGGL((layernorm2_kernel<1, false, kLnBlock>), launch, dim3(kLnBlock), 0, s,
                        A);
   } else if (per <= kLnMaxPer) {
-    hipLaunchKernelGGL((layernorm2_kernel<kLnMaxPer, false, kLnBlock>), dim3(grid),
+    hipLaunchKernelGGL((layernorm2_kernel<kLnMaxPer, false, kLnBlock>), launch,
                        dim3(kLnBlock), 0, s, A);
   } else {
-    hipLaunchKernelGGL((layernorm2_kernel<kLnWidePer, false, kLnWideBlock>), dim3(grid),
+    hipLaunchKernelGGL((layernorm2_kernel<kLnWidePer, false, kLnWideBlock>), launch,
                        dim3(kLnWideBlock), 0, s, A);
   }
   return check_launch("layernorm2_kernel");

@@ -471,7 +471,7 @@ struct WalkPlan {
 };
 
 int plan_walk(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int m, const char* what,
-              WalkPlan& p) {
+              WalkPlan& p, size_t lanes_cap = 0) {
   p.maxd = 0;
   for (int i = 0; i < m; ++i) {
     const sufhip_trunc_job& jb = jobs[i];
@@ -490,9 +490,11 @@ int plan_walk(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int m, con
   // the lanes allow -- the fewest local levels whose walks take less than
   // three quarters of one full workgroup per CU (at most kWalkLocal; past
   // that the extra waves per SIMD slow every level more than a local level
-  // costs).
+  // costs).  A hosted walk (lanes_cap > 0) takes the fewest whose walks fit
+  // in the host's room.
   int cus = 0;
   if (int rc = cu_count(&cus)) return rc;
+  const size_t cap = lanes_cap > 0 ? lanes_cap + 1 : 3 * size_t(cus) * kWalkBlock / 4;
   p.el = 0;
   for (; p.el < kWalkLocal; ++p.el) {
     size_t lanes = 0;
@@ -501,7 +503,7 @@ int plan_walk(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int m, con
       const int e = k0 == jobs[i].frac_bits && k0 >= p.el ? p.el : 0;
       lanes += p.d[i] > 0 ? 8 * (size_t(1) << (k0 - e)) : 0;
     }
-    if (4 * lanes < 3 * size_t(cus) * kWalkBlock) break;
+    if (lanes < cap) break;
   }
   return SUFHIP_OK;
 }
@@ -535,6 +537,27 @@ int trunc_walk_plan(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int 
   // Table gates only (every walk ends in a table entry), no local levels and
   // no expansion launches.
   bool ok = p.el == 0;
+  for (int i = 0; i < count; ++i)
+    ok = ok && (p.d[i] == 0 || (p.k0s[i] == p.d[i] && p.d[i] == jobs[i].frac_bits));
+  if (!ok) return SUFHIP_OK;
+  fill_walk(p, jobs, count, begin, key, out, geo);
+  *one = true;
+  return SUFHIP_OK;
+}
+
+int trunc_walk_plan_fit(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int count,
+                        int max_jobs, size_t lanes_cap, uint32_t* begin, const uint8_t** key,
+                        uint4** out, uint32_t* geo, bool* one, const char* what) {
+  *one = false;
+  SUFHIP_REQUIRE(count >= 0 && (count == 0 || jobs), "trunc walk: bad jobs");
+  SUFHIP_REQUIRE(prg_state, "trunc walk: null prg_state");
+  if (count > max_jobs || count > kWalkJobs) return SUFHIP_OK;
+  WalkPlan p;
+  if (int rc = plan_walk(prg_state, jobs, count, what, p, lanes_cap > 0 ? lanes_cap : 1))
+    return rc;
+  // Table gates only: every walk ends in table entries, nothing is left for
+  // the expansion launches.
+  bool ok = true;
   for (int i = 0; i < count; ++i)
     ok = ok && (p.d[i] == 0 || (p.k0s[i] == p.d[i] && p.d[i] == jobs[i].frac_bits));
   if (!ok) return SUFHIP_OK;

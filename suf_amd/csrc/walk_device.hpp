@@ -26,6 +26,18 @@ int trunc_walk_plan(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int 
                     int max_jobs, uint32_t* begin, const uint8_t** key, uint4** out,
                     uint32_t* geo, bool* one);
 
+// Plans `count` table-gate jobs (at most max_jobs) as the walks of a launch
+// that another kernel hosts, with room for lanes_cap walk lanes at once: the
+// fewest local levels (at most kWalkLocal) whose walks fit in lanes_cap, so
+// that the walks take one pass of the room when they can.  *one is set when
+// every job is a table gate (f <= 14, no expansion launches) and there are at
+// most max_jobs of them; then begin[0..count], key, out and geo hold
+// WalkJobs' fields for walk_table.  Validates every job as
+// sufhip_trunc_prepare_batch does (defined in trunc_gate.hip).
+int trunc_walk_plan_fit(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int count,
+                        int max_jobs, size_t lanes_cap, uint32_t* begin, const uint8_t** key,
+                        uint4** out, uint32_t* geo, bool* one, const char* what);
+
 namespace {
 
 // A table job's walks go to depth f - kWalkLocal and expand the last
@@ -212,6 +224,44 @@ __device__ __forceinline__ void walk_leaf_path(const Aes& aes, const uint4* rkl,
     w = n[0];
   }
   walk8_leaf(c, w, v);
+}
+
+// Lane gl's walk of a table job with e = geo >> 16 local levels (0..4): the
+// depth-(f - e) node v, then its subtree's 2^e table entries (v << e) + i,
+// as trunc_batch_walk_kernel walks table jobs.  For kernels that run these
+// walks as a role beside their own work, at 512 lanes per workgroup or
+// fewer (the expansion's lockstep groups need more than the 128 registers
+// of a 1024-lane workgroup when passed through this function).
+template <class Aes>
+__device__ __forceinline__ void walk_table(const Aes& aes, const uint4* rkl, const uint8_t* key,
+                                           uint4* out, uint32_t geo, uint32_t v, uint32_t gl) {
+  if (!(key[7] & 1)) return;
+  const int f = int(geo & 0xff), e = int(geo >> 16);
+  const uint8_t* chunk = key + kTruncHdrBytes + 8;
+  const Walk8Ctx<Aes> c{aes, rkl, chunk, out, f, uint32_t(key[6] & 1u), (gl >> 2) & 1u, gl & 3u};
+  Walk8 w;
+  w.s = word_at(chunk, int(c.q));
+  if (c.q == 3) w.s &= 0x7fffffffu;
+  w.t = c.party;
+  w.v = 0;
+  const int dw = f - e;
+  const uint8_t* cw = chunk + 16;
+  for (int i = 0; i < dw; ++i, cw += 33) {
+    Walk8 n[1];
+    walk8_step_n<1>(c, cw, (v >> (dw - 1 - i)) & 1u, &w, n);
+    w = n[0];
+  }
+  const Walk8 root[1] = {w};
+  if (e == 0)
+    walk8_leaf(c, w, v);
+  else if (e == 1)
+    walk8_expand<0, 1>(c, cw, root, v);
+  else if (e == 2)
+    walk8_expand<0, 2>(c, cw, root, v);
+  else if (e == 3)
+    walk8_expand<0, 3>(c, cw, root, v);
+  else  // e == 4 = kWalkLocal at most (static_assert above)
+    walk8_expand<0, 4>(c, cw, root, v);
 }
 
 }  // namespace

@@ -482,6 +482,7 @@ class TransformerLayer:
         self.w2 = PublicMatmulTrunc(seq, ffn, d, weights["W2"], dealer, self.prg_state,
                                     frac_bits, device)
         self.side = torch.cuda.Stream(device=device)
+        self.host_walks = True
         n = seq * d
         self.h1, self.qkvs, self.ctx = pair(n), pair(3 * n), pair(n)
         self.r1, self.h2, self.u, self.g = pair(n), pair(n), pair(seq * ffn), pair(seq * ffn)
@@ -495,19 +496,45 @@ class TransformerLayer:
                 self.proj.truncs() + self.ln2.truncs() + self.w1.truncs() + self.gelu.truncs() +
                 self.w2.truncs()]
 
+    def hosted_walks(self):
+        """The gates whose key-only halves the two LayerNorm launches prepare
+        on the CUs their rows leave free: (in the first, in the second).
+        Each takes as many as those CUs walk in one pass at two local levels
+        (one 512-lane workgroup per free CU, 8192 lanes per table, two tables
+        per gate): at 128 rows on 256 CUs, four gates each -- about as long
+        as the LayerNorm's rows take.  More gates per launch need three local
+        levels, whose walks outlast the rows (measured: the layer 0.2666 ms
+        with 4 + 4 hosted gates, 0.2737 with 4 + 5, 0.2882 with 8 + 5, 0.2798
+        with none).  The first takes the second LayerNorm's first gates, the
+        second the MLP's."""
+        cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+        k = max(cus - self.seq, 0) * 512 // (2 * 8192)
+        mlp = self.w1.truncs() + self.gelu.truncs() + self.w2.truncs()
+        first = (self.ln2.truncs() + mlp)[:k]
+        return first, [t for t in mlp if all(t is not u for u in first)][:k]
+
     def eval2(self, x, out, marks=None, overlap_prepare=False, sm_marks=None, sm_spin=None):
         """x, out: pairs of int64 [seq * d] device tensors.  marks: optional
         list of torch events recorded after each stage (profiling).  The
-        key-only halves of all truncation gates run first, in one batched
-        walk on the current stream; with overlap_prepare they run on a side
-        stream instead, in three batches, each ahead of the stage that needs
-        it (a fork or join between streams costs about as much as it
+        key-only halves of the truncation gates run first, in one batched
+        walk on the current stream, except those of hosted_walks(), which the
+        fused LayerNorm launches walk on their spare CUs (host_walks; always
+        before the gates' first use).  With overlap_prepare they all run on a
+        side stream instead, in three batches, each ahead of the stage that
+        needs it (a fork or join between streams costs about as much as it
         hides).  sm_marks, sm_spin: see AttentionCore.eval2."""
+        # LayerNorm and GeLU outputs feed only the next public-weight product:
+        # they are written as its digit planes when the block runs fused.
+        fused_ln = self.ln1.fusable() and self.ln2.fusable()
+        hosted = ([], [])
         if overlap_prepare:
             prep = Prepared(self.side, self.stage_truncs(), upfront=2)
             b = lambda k: k  # noqa: E731
         else:
-            prep = Prepared(None, [sum(self.stage_truncs(), [])])
+            if self.host_walks and fused_ln:
+                hosted = self.hosted_walks()
+            skip = {id(t) for t in hosted[0] + hosted[1]}
+            prep = Prepared(None, [[t for t in sum(self.stage_truncs(), []) if id(t) not in skip]])
             b = lambda k: 0  # noqa: E731
 
         def mark():
@@ -516,9 +543,6 @@ class TransformerLayer:
                 ev.record()
                 marks.append(ev)
 
-        # LayerNorm and GeLU outputs feed only the next public-weight product:
-        # they are written as its digit planes when the block runs fused.
-        fused_ln = self.ln1.fusable() and self.ln2.fusable()
         mark()
         # With the matrix-core attention the QKV product writes the attention's
         # three opens as digit planes instead of Q, K and V (unsliced product,
@@ -528,7 +552,7 @@ class TransformerLayer:
             self.d % 64 == 0
         if fused_ln:
             self.ln1.eval2(x, self.h1, prep=(prep, b(0)), planes=self.qkv.x_planes(),
-                           write_out=self.keep)
+                           write_out=self.keep, walk=hosted[0])
             mark()
             if qkv_opens:
                 self.qkv.eval2_qkv(self.attn.qkv_opens())
@@ -561,7 +585,7 @@ class TransformerLayer:
         mark()
         if fused_ln:
             self.ln2.eval2(self.r1, self.h2, prep=(prep, b(2)), planes=self.w1.x_planes(),
-                           write_out=self.keep, pre=pre)
+                           write_out=self.keep, pre=pre, walk=hosted[1])
             mark()
             self.w1.eval2(None, self.u)
         else:

@@ -25,8 +25,8 @@ import torch
 
 from . import native, tables
 from .tasks import (M64, CoeffLut, Dealer, Prepared, Triples, Trunc, chain2, chain2_args,
-                    dev_i32, lin2, mul2x, operand, pair, row_sum2, stream_ptr, term, triple2,
-                    x_planes)
+                    dev_i32, lin2, mul2x, operand, pair, prepare_batch, row_sum2, stream_ptr,
+                    term, triple2, trunc_jobs, x_planes)
 
 
 class Rsqrt:
@@ -108,14 +108,24 @@ class LayerNormBlock:
     def truncs(self):
         return [self.tr_mean] + self.tr_var + self.rsqrt.truncs() + [self.tr_norm]
 
-    def block_args(self, x, out, planes=None, write_out=True, pre=None):
+    def block_args(self, x, out, planes=None, write_out=True, pre=None, walk=None):
         """sufhip_layernorm2_args of the one-launch block over x into out
         (planes = (buffer, cols): also as a public-weight product's digit
         planes; write_out False: only those).  pre = (slices address, slice
         count, truncation epilogue, mask) from PublicMatmulTrunc.eval2_slices:
         x is that product's truncated output, reduced and written (to the
-        epilogue's outputs) in this launch; x itself is not read."""
+        epilogue's outputs) in this launch; x itself is not read.  walk: other
+        truncation gates whose key-only halves this launch also prepares (as
+        tasks.prepare_batch would), for gates evaluated after the block; the
+        job array is kept in self._walk until the next call."""
         a = native.LayerNorm2Args()
+        self._walk = None
+        if walk:
+            state, arr, count = trunc_jobs(walk)
+            self._walk = (state, arr)
+            a.walk_jobs = native.ctypes.addressof(arr)
+            a.walk_count = count
+            a.walk_prg_state = native.ctypes.addressof(state)
         if pre is not None:
             a.in_slices, a.in_slice_count, a.tr_in, a.in_mask = pre[0], pre[1], pre[2], pre[3] & M64
         else:
@@ -143,24 +153,30 @@ class LayerNormBlock:
         return (self.cols <= 2048 and self.rsqrt.iters == 1 and
                 all(t.has_table() for t in self.truncs()))
 
-    def eval2(self, x, out, prep=None, fused=True, planes=None, write_out=True, pre=None):
+    def eval2(self, x, out, prep=None, fused=True, planes=None, write_out=True, pre=None,
+              walk=None):
         """x, out: pairs of int64 [rows * cols] device tensors.  prep:
         (tasks.Prepared, batch) holding this block's key-only halves, or None
         to issue them here on the block's side stream.  fused: the whole block
         in one launch (sufhip_layernorm2); else launch by launch.  planes =
         (buffer, cols), fused only: the output also as a public-weight
         product's digit planes (write_out False: only those).  pre, fused
-        only: x comes from a product's unreduced k-slices (block_args)."""
+        only: x comes from a product's unreduced k-slices (block_args).
+        walk: later gates whose key-only halves are prepared here too (by the
+        fused launch's spare workgroups; launch by launch, by
+        tasks.prepare_batch on the current stream)."""
         rows, cols, n = self.rows, self.cols, self.n
         if prep is None:
             prep = (Prepared(self.side, [self.truncs()]), 0)
         prep[0].wait(prep[1])
         if fused and self.fusable():
-            a = self.block_args(x, out, planes, write_out, pre)
+            a = self.block_args(x, out, planes, write_out, pre, walk)
             native.call("sufhip_layernorm2", native.ctypes.byref(a), stream_ptr())
             return out
         if planes is not None or pre is not None:
             raise ValueError("LayerNormBlock.eval2: planes and pre need the fused block")
+        if walk:
+            prepare_batch(walk)
         row_sum2(operand(term(x)), rows, cols, mul_const=self.inv_len,
                  into=(self.tr_mean, self.mu))
         diff = operand(term(x), term(self.mu, index=self.row_index, neg=True, length=rows))

@@ -270,7 +270,8 @@ class LayerNorm2Args(ctypes.Structure):
                 ("tr_norm", TruncEpilogue), ("mean_mask", c_u64), ("var_mask", c_u64 * 2),
                 ("norm_mask", c_u64), ("sq", Triple2), ("norm", Triple2), ("rsqrt", Chain2Args),
                 ("out", c_vp * 2), ("out_planes", XPlanes), ("in_slices", c_vp),
-                ("in_slice_count", c_int), ("tr_in", TruncEpilogue), ("in_mask", c_u64)]
+                ("in_slice_count", c_int), ("tr_in", TruncEpilogue), ("in_mask", c_u64),
+                ("walk_jobs", c_vp), ("walk_count", c_int), ("walk_prg_state", c_vp)]
 
 
 class ReluRoundKey(ctypes.Structure):

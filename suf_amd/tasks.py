@@ -270,18 +270,24 @@ class Trunc:
                     stream_ptr())
 
 
+def trunc_jobs(truncs):
+    """(PRG state buffer, sufhip_trunc_job array, count) of the key-only
+    halves of truncation gates that share one PRG state."""
+    state = truncs[0].prg_state
+    if any(t.prg_state != state for t in truncs):
+        raise ValueError("prepare_batch: gates with different PRG states")
+    jobs = [j for t in truncs for j in t.jobs()]
+    return truncs[0]._state, (native.TruncJob * len(jobs))(*jobs), len(jobs)
+
+
 def prepare_batch(truncs, stream=None):
     """The key-only halves of many truncation gates (same PRG state) in one
     batched launch sequence on `stream` (default: current)."""
     if not truncs:
         return
-    state = truncs[0].prg_state
-    if any(t.prg_state != state for t in truncs):
-        raise ValueError("prepare_batch: gates with different PRG states")
-    jobs = [j for t in truncs for j in t.jobs()]
-    arr = (native.TruncJob * len(jobs))(*jobs)
+    state, arr, count = trunc_jobs(truncs)
     s = stream.cuda_stream if stream is not None else stream_ptr()
-    native.call("sufhip_trunc_prepare_batch", truncs[0]._state, arr, len(jobs), s)
+    native.call("sufhip_trunc_prepare_batch", state, arr, count, s)
 
 
 class Prepared:

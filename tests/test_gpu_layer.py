@@ -175,6 +175,63 @@ def test_layernorm_reduces_product_slices():
         small.eval2_slices(pair_())
 
 
+@pytest.mark.parametrize("rows,cols,gates,f,n", [
+    (128, 768, 8, 12, 128 * 768),   # the layer's second LayerNorm gates in the first
+    (128, 768, 5, 12, 128 * 3072),  # the MLP's gates in the second
+    (128, 768, 12, 12, 1000),       # 24 jobs, the most one launch walks
+    (64, 1536, 3, 14, 5000),        # 256-thread rows, f = 14
+    (2080, 64, 2, 12, 4096),        # every CU holds a row: the walks come after
+    (128, 768, 13, 12, 4096),       # 26 jobs: the batched prepare first
+    (128, 768, 1, 20, 1 << 16),     # expansion launches: the batched prepare first
+])
+def test_layernorm_walks_later_gates(rows, cols, gates, f, n):
+    """A fused LayerNorm launch that also walks other gates' key-only halves
+    (sufhip_layernorm2's walk jobs, on the workgroups past the rows') writes
+    the same normalised shares as the block alone and the same workspaces as
+    the batched prepare, and the tables give the gates' shares.  Job sets the
+    launch cannot walk go through the batched prepare first, same results."""
+    from suf_amd.tasks import Trunc, prepare_batch
+    say("layernorm with walks %dx%d, %d gates, f %d, n %d" % (rows, cols, gates, f, n))
+    g = np.random.default_rng(rows + gates + f)
+    m = rows * cols
+    x = pfss.host_normal_fixed(101, 1.0, 0.0, F, m)
+    xin = tuple(dev(v) for v in _pair(x, 102))
+    ln = layer.LayerNormBlock(rows, cols, STATE, F, seed=35)
+    assert ln.fusable()
+    for t in ln.truncs():
+        t.prepare()
+    dealer = Dealer(22)
+    trs = [Trunc(dealer, f, n, STATE) for _ in range(gates)]
+    pair_ = lambda: tuple(torch.empty(m, dtype=torch.int64, device="cuda")  # noqa: E731
+                          for _ in range(2))
+    h_want, h_got = pair_(), pair_()
+    ln.eval2(xin, h_want)
+    for t in trs:
+        for p in (0, 1):
+            t.work[p].fill_(0x3c3c)
+    for t in h_got:
+        t.fill_(0x5a5a)
+    ln.eval2(xin, h_got, walk=trs)
+    torch.cuda.synchronize()
+    got_work = [t.work[p].clone() for t in trs for p in (0, 1)]
+    for t in trs:
+        for p in (0, 1):
+            t.work[p].fill_(0x3c3c)
+    prepare_batch(trs)
+    torch.cuda.synchronize()
+    for p in (0, 1):
+        assert np.array_equal(u64(h_got[p]), u64(h_want[p])), ("h", p)
+    want_work = [t.work[p] for t in trs for p in (0, 1)]
+    for i, (gw, ww) in enumerate(zip(got_work, want_work)):
+        assert torch.equal(gw, ww), ("workspace", i)
+    for t in (trs[0], trs[-1]):
+        xs = g.integers(0, 2**40, n, dtype=np.uint64)
+        out = (torch.empty(n, dtype=torch.int64, device="cuda"),
+               torch.empty(n, dtype=torch.int64, device="cuda"))
+        t.finish(dev(xs + np.uint64(t.mask)), out)
+        assert np.array_equal(u64(out[0] + out[1]), xs >> np.uint64(f))
+
+
 @pytest.mark.parametrize("rows,cols,slices", [(2080, 64, 5), (2080, 320, 3), (96, 1024, 2)])
 def test_layernorm_in_slices_several_rows_per_workgroup(rows, cols, slices):
     """sufhip_layernorm2 over synthetic k-slices, with more rows than the
