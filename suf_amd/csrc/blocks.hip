@@ -35,10 +35,8 @@ constexpr int kLnWidePer = 8;     // at kLnWideBlock: cols <= 2048
 constexpr int kLnCopies = 4;  // the T table serves one lane per workgroup
 using LnAes = AesLds<kLnCopies>;  // one lane's chain: the small table fills fastest
 // Key-only walks of later gates' tables, run by the workgroups past the rows'
-// (walk_device.hpp): up to kLnWalkJobs jobs, on their own 16-copy T table.
+// (hosted_walk_role): up to kLnWalkJobs jobs.
 constexpr int kLnWalkJobs = 24;
-constexpr int kLnWalkCopies = 16;
-using LnWalkAes = AesLds<kLnWalkCopies>;
 
 struct LnArgs {
   const uint64_t* x[2];
@@ -57,20 +55,6 @@ struct LnArgs {
 };
 static_assert(sizeof(LnArgs) <= 4096, "kernel argument blocks must fit in 4 KB");
 
-// Lane gl of the walk role: the node of walk gl / 8 and its table entries.
-__device__ __forceinline__ void ln_walk_role(const WalkJobs<kLnWalkJobs>& w, uint32_t gl) {
-  __shared__ __align__(16) uint32_t wtab[LnWalkAes::kWords];
-  __shared__ uint4 rkl[4 * 11];
-  fill_ttable<kLnWalkCopies>(wtab, kTDev.v);
-  fill_round_keys(rkl, w.prg.rk, 4);
-  __syncthreads();
-  const LnWalkAes aes{wtab, threadIdx.x % kLnWalkCopies};
-  const uint32_t g = gl >> 3;  // whole 8-lane groups leave together
-  if (g >= w.begin[w.count]) return;
-  const int j = batch_job<kLnWalkJobs>(w.begin, w.count, g);
-  walk_table(aes, rkl, w.key[j], w.out[j], w.geo[j], g - w.begin[j], gl);
-}
-
 enum { kTrMean = 0, kTrVar0 = 1, kTrVar1 = 2, kTrNorm = 3, kTrIn = 4 };
 constexpr int kLnMaxSlices = 8;
 constexpr int kLnMaxInPer = kLnMaxPer;  // in_slices rows of up to 1024 elements
@@ -83,7 +67,7 @@ template <int kPer, bool kIn, int kBlock>
 __global__ void __launch_bounds__(kBlock) layernorm2_kernel(LnArgs A) {
   constexpr int kLnWaves = kBlock / 64;
   if (int(blockIdx.x) >= A.row_groups) {
-    ln_walk_role(A.w, (blockIdx.x - A.row_groups) * kBlock + threadIdx.x);
+    hosted_walk_role<kLnWalkJobs, true>(A.w, (blockIdx.x - A.row_groups) * kBlock + threadIdx.x);
     return;
   }
   __shared__ __align__(16) uint32_t tab[256 * kLnCopies];
@@ -912,23 +896,12 @@ int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
   A.row_groups = grid;
   // The walks: one workgroup per CU fits beside the rows' (the kernel's
   // registers allow one), so the CUs without a row hold one pass of them.
-  size_t walk_groups = 0;
-  if (g.walk_count > 0) {
-    const size_t room = size_t(cus > grid ? cus - grid : 0) * size_t(block);
-    bool one = false;
-    if (int rc = trunc_walk_plan_fit(g.walk_prg_state, g.walk_jobs, g.walk_count, kLnWalkJobs,
-                                     room, A.w.begin, A.w.key, A.w.out, A.w.geo, &one,
-                                     "sufhip_layernorm2 walk"))
-      return rc;
-    if (one) {
-      fill_prg4(g.walk_prg_state, &A.w.prg);
-      A.w.count = g.walk_count;
-      walk_groups = (8 * size_t(A.w.begin[A.w.count]) + block - 1) / size_t(block);
-    } else if (int rc = sufhip_trunc_prepare_batch(g.walk_prg_state, g.walk_jobs, g.walk_count,
-                                                   stream)) {
-      return rc;
-    }
-  }
+  size_t walk_lanes = 0;
+  if (int rc = plan_hosted_walk(g.walk_prg_state, g.walk_jobs, g.walk_count,
+                                size_t(cus > grid ? cus - grid : 0) * size_t(block), stream,
+                                "sufhip_layernorm2 walk", A.w, &walk_lanes))
+    return rc;
+  const size_t walk_groups = (walk_lanes + block - 1) / size_t(block);
   SUFHIP_REQUIRE(size_t(grid) + walk_groups <= 0x7fffffffu, "sufhip_layernorm2: grid too large");
   const dim3 launch(unsigned(size_t(grid) + walk_groups));
   hipStream_t s = as_stream(stream);

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "dcf_device.hpp"
 #include "suf_hip.h"
@@ -262,6 +263,62 @@ __device__ __forceinline__ void walk_table(const Aes& aes, const uint4* rkl, con
     walk8_expand<0, 3>(c, cw, root, v);
   else  // e == 4 = kWalkLocal at most (static_assert above)
     walk8_expand<0, 4>(c, cw, root, v);
+}
+
+// The walk role of a host kernel's spare workgroups (table jobs planned by
+// trunc_walk_plan_fit): lane gl of the launch's walk lanes, on the role's own
+// AES tables and round keys in LDS -- the walk launch's four-table span
+// (kFour: 128 KB, for hosts with one workgroup per CU and the LDS to spare)
+// or a 16-copy single table (16 KB).  Called by whole workgroups (it has
+// barriers); whole 8-lane groups leave together.
+constexpr int kHostedWalkCopies = 16;
+
+template <int kJobs, bool kFour>
+__device__ __forceinline__ void hosted_walk_role(const WalkJobs<kJobs>& w, uint32_t gl) {
+  using Aes = std::conditional_t<kFour, DcfAes, AesLds<kHostedWalkCopies>>;
+  __shared__ __align__(16) uint32_t wtab[Aes::kWords];
+  __shared__ uint4 rkl[4 * 11];
+  if constexpr (kFour) {
+    __shared__ uint32_t stage[256];
+    DcfAes::fill(wtab, stage, kTDev.v);
+  } else {
+    fill_ttable<kHostedWalkCopies>(wtab, kTDev.v);
+  }
+  fill_round_keys(rkl, w.prg.rk, 4);
+  __syncthreads();
+  const Aes aes = [&] {
+    if constexpr (kFour)
+      return DcfAes::make(wtab);
+    else
+      return Aes{wtab, uint32_t(threadIdx.x % kHostedWalkCopies)};
+  }();
+  const uint32_t g = gl >> 3;
+  if (g >= w.begin[w.count]) return;
+  const int j = batch_job<kJobs>(w.begin, w.count, g);
+  walk_table(aes, rkl, w.key[j], w.out[j], w.geo[j], g - w.begin[j], gl);
+}
+
+// Host side of a hosted walk: w for `count` jobs walked by a launch with
+// room for lanes_cap walk lanes in one pass, and *lanes = the walk lanes the
+// launch must add (0 for no jobs).  Job sets a hosted walk cannot take (more
+// than kJobs jobs, gates other than table gates) go through
+// sufhip_trunc_prepare_batch on `stream` here instead, with *lanes = 0.
+template <int kJobs>
+int plan_hosted_walk(const uint8_t* prg_state, const sufhip_trunc_job* jobs, int count,
+                     size_t lanes_cap, void* stream, const char* what, WalkJobs<kJobs>& w,
+                     size_t* lanes) {
+  *lanes = 0;
+  w.count = 0;
+  if (count <= 0) return SUFHIP_OK;
+  bool one = false;
+  if (int rc = trunc_walk_plan_fit(prg_state, jobs, count, kJobs, lanes_cap, w.begin, w.key,
+                                   w.out, w.geo, &one, what))
+    return rc;
+  if (!one) return sufhip_trunc_prepare_batch(prg_state, jobs, count, stream);
+  fill_prg4(prg_state, &w.prg);
+  w.count = count;
+  *lanes = 8 * size_t(w.begin[count]);
+  return SUFHIP_OK;
 }
 
 }  // namespace

@@ -498,17 +498,16 @@ class TransformerLayer:
 
     def hosted_walks(self):
         """The gates whose key-only halves the two LayerNorm launches prepare
-        on the CUs their rows leave free: (in the first, in the second).
-        Each takes as many as those CUs walk in one pass at two local levels
-        (one 512-lane workgroup per free CU, 8192 lanes per table, two tables
-        per gate): at 128 rows on 256 CUs, four gates each -- about as long
-        as the LayerNorm's rows take.  More gates per launch need three local
-        levels, whose walks outlast the rows (measured: the layer 0.2666 ms
-        with 4 + 4 hosted gates, 0.2737 with 4 + 5, 0.2882 with 8 + 5, 0.2798
-        with none).  The first takes the second LayerNorm's first gates, the
-        second the MLP's."""
+        on the CUs their rows leave free: (in the first, in the second).  A
+        LayerNorm holds one 512-lane workgroup per CU, and its walks take
+        three local levels (4096 lanes per table, two tables per gate) in one
+        pass of seven eighths of the free CUs: at 128 rows on 256 CUs, seven
+        gates, about as long as the rows take (measured, one LayerNorm of
+        128 x 768 rows, L2-warm: 16.4 us alone, 17.0 / 20.7 / 21.6 / 21.8 /
+        31.0 us walking 4 / 5 / 6 / 7 / 8 gates).  The first takes the second
+        LayerNorm's gates, the second the MLP's."""
         cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
-        k = max(cus - self.seq, 0) * 512 // (2 * 8192)
+        k = max(cus - self.seq, 0) * 7 * 512 // (8 * 2 * 4096)
         mlp = self.w1.truncs() + self.gelu.truncs() + self.w2.truncs()
         first = (self.ln2.truncs() + mlp)[:k]
         return first, [t for t in mlp if all(t is not u for u in first)][:k]
