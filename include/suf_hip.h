@@ -546,8 +546,9 @@ typedef struct sufhip_layernorm2_args {
    * would write them, for gates that later launches evaluate (the prepare of
    * transformer_layer_forward's later truncations, src/nn/
    * transformer_layer.cpp:435-830).  Up to 24 table-gate jobs (f <= 14) run
-   * as extra workgroups of this launch, on the CUs its rows leave free; other
-   * job sets go through sufhip_trunc_prepare_batch on the same stream first.
+   * as extra workgroups of this launch, on the CUs its rows leave free (rows
+   * of up to 1024 elements); other job sets and longer rows go through
+   * sufhip_trunc_prepare_batch on the same stream first.
    * The results are byte-equal either way. */
   const sufhip_trunc_job* walk_jobs;
   int walk_count;

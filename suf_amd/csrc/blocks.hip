@@ -63,12 +63,18 @@ constexpr int kLnMaxInPer = kLnMaxPer;  // in_slices rows of up to 1024 elements
 // x, both triples' shares, and (lane 0) the rsqrt chain's triples; the key
 // headers of all truncation gates sit in LDS.  What remains serial per row
 // is one table read per truncation gate and the rsqrt LUT's AES.
-template <int kPer, bool kIn, int kBlock>
+// kWalk: the workgroups past the rows' walk A.w's jobs (a separate
+// instantiation, so that launches without walks keep the rows' own register
+// allocation and LDS).
+template <int kPer, bool kIn, int kBlock, bool kWalk>
 __global__ void __launch_bounds__(kBlock) layernorm2_kernel(LnArgs A) {
   constexpr int kLnWaves = kBlock / 64;
-  if (int(blockIdx.x) >= A.row_groups) {
-    hosted_walk_role<kLnWalkJobs, true>(A.w, (blockIdx.x - A.row_groups) * kBlock + threadIdx.x);
-    return;
+  if constexpr (kWalk) {
+    if (int(blockIdx.x) >= A.row_groups) {
+      hosted_walk_role<kLnWalkJobs, true>(A.w,
+                                          (blockIdx.x - A.row_groups) * kBlock + threadIdx.x);
+      return;
+    }
   }
   __shared__ __align__(16) uint32_t tab[256 * kLnCopies];
   __shared__ ChainLds L;
@@ -896,30 +902,43 @@ int sufhip_layernorm2(const sufhip_layernorm2_args* args, void* stream) {
   A.row_groups = grid;
   // The walks: one workgroup per CU fits beside the rows' (the kernel's
   // registers allow one), so the CUs without a row hold one pass of them.
+  // The 256-lane form for rows past 1024 elements walks nothing itself.
   size_t walk_lanes = 0;
-  if (int rc = plan_hosted_walk(g.walk_prg_state, g.walk_jobs, g.walk_count,
-                                size_t(cus > grid ? cus - grid : 0) * size_t(block), stream,
-                                "sufhip_layernorm2 walk", A.w, &walk_lanes))
-    return rc;
+  if (block == kLnBlock) {
+    if (int rc = plan_hosted_walk(g.walk_prg_state, g.walk_jobs, g.walk_count,
+                                  size_t(cus > grid ? cus - grid : 0) * size_t(block), stream,
+                                  "sufhip_layernorm2 walk", A.w, &walk_lanes))
+      return rc;
+  } else if (g.walk_count > 0) {
+    if (int rc = sufhip_trunc_prepare_batch(g.walk_prg_state, g.walk_jobs, g.walk_count, stream))
+      return rc;
+  }
   const size_t walk_groups = (walk_lanes + block - 1) / size_t(block);
   SUFHIP_REQUIRE(size_t(grid) + walk_groups <= 0x7fffffffu, "sufhip_layernorm2: grid too large");
   const dim3 launch(unsigned(size_t(grid) + walk_groups));
   hipStream_t s = as_stream(stream);
+  auto rows512 = [&](auto per_c, auto in_c) {
+    constexpr int kP = decltype(per_c)::value;
+    constexpr bool kI = decltype(in_c)::value;
+    if (walk_groups > 0)
+      hipLaunchKernelGGL((layernorm2_kernel<kP, kI, kLnBlock, true>), launch, dim3(kLnBlock), 0,
+                         s, A);
+    else
+      hipLaunchKernelGGL((layernorm2_kernel<kP, kI, kLnBlock, false>), launch, dim3(kLnBlock), 0,
+                         s, A);
+  };
+  using PerOne = std::integral_constant<int, 1>;
   if (A.in_slices) {
     if (per <= 1)
-      hipLaunchKernelGGL((layernorm2_kernel<1, true, kLnBlock>), launch, dim3(kLnBlock), 0, s,
-                         A);
+      rows512(PerOne{}, std::true_type{});
     else
-      hipLaunchKernelGGL((layernorm2_kernel<kLnMaxInPer, true, kLnBlock>), launch,
-                         dim3(kLnBlock), 0, s, A);
+      rows512(std::integral_constant<int, kLnMaxInPer>{}, std::true_type{});
   } else if (per <= 1) {
-    hipLaunchKernelGGL((layernorm2_kernel<1, false, kLnBlock>), launch, dim3(kLnBlock), 0, s,
-                       A);
+    rows512(PerOne{}, std::false_type{});
   } else if (per <= kLnMaxPer) {
-    hipLaunchKernelGGL((layernorm2_kernel<kLnMaxPer, false, kLnBlock>), launch,
-                       dim3(kLnBlock), 0, s, A);
+    rows512(std::integral_constant<int, kLnMaxPer>{}, std::false_type{});
   } else {
-    hipLaunchKernelGGL((layernorm2_kernel<kLnWidePer, false, kLnWideBlock>), launch,
+    hipLaunchKernelGGL((layernorm2_kernel<kLnWidePer, false, kLnWideBlock, false>), launch,
                        dim3(kLnWideBlock), 0, s, A);
   }
   return check_launch("layernorm2_kernel");

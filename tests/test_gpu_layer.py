@@ -179,7 +179,7 @@ def test_layernorm_reduces_product_slices():
     (128, 768, 8, 12, 128 * 768),   # the layer's second LayerNorm gates in the first
     (128, 768, 5, 12, 128 * 3072),  # the MLP's gates in the second
     (128, 768, 12, 12, 1000),       # 24 jobs, the most one launch walks
-    (64, 1536, 3, 14, 5000),        # 256-thread rows, f = 14
+    (64, 1536, 3, 14, 5000),        # 256-thread rows (the batched prepare first), f = 14
     (2080, 64, 2, 12, 4096),        # every CU holds a row: the walks come after
     (128, 768, 13, 12, 4096),       # 26 jobs: the batched prepare first
     (128, 768, 1, 20, 1 << 16),     # expansion launches: the batched prepare first
